@@ -1,0 +1,160 @@
+// Shared device helpers and C-ABI plumbing for the mzoo_amd HIP library (gfx950).
+//
+// Numerics rules every kernel in this library follows (the build passes
+// -ffp-contract=off, so a*b+c is two roundings unless written as fmaf):
+//   * bf16 <-> fp32 conversion is done with integer arithmetic (round to nearest even),
+//   * fp32 division and sqrt are the correctly rounded IEEE operations,
+//   * fp32 denormals are kept (no flush to zero).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdarg.h>
+#include <string>
+
+#include "../../include/mzk.h"
+
+namespace mzk {
+
+// ------------------------------------------------------------------------------------
+// error reporting
+// ------------------------------------------------------------------------------------
+void set_last_error(const char* fmt, ...);
+
+#define MZK_CHECK_ARG(cond, ...)                                                   \
+  do {                                                                              \
+    if (!(cond)) {                                                                  \
+      ::mzk::set_last_error(__VA_ARGS__);                                           \
+      return MZK_EINVAL;                                                            \
+    }                                                                               \
+  } while (0)
+
+#define MZK_LAUNCH_CHECK(name)                                                      \
+  do {                                                                              \
+    hipError_t _e = hipGetLastError();                                              \
+    if (_e != hipSuccess) {                                                         \
+      ::mzk::set_last_error("%s: launch failed: %s", name, hipGetErrorString(_e)); \
+      return MZK_ELAUNCH;                                                           \
+    }                                                                               \
+  } while (0)
+
+static inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ------------------------------------------------------------------------------------
+// scalar conversions
+// ------------------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t b = __float_as_uint(f);
+  if ((b & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((b >> 16) | 0x40);  // quiet NaN
+  b += 0x7fffu + ((b >> 16) & 1u);
+  return static_cast<uint16_t>(b >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));  // round to nearest even
+}
+
+// Load element i of a tensor of the given dtype as fp32.
+template <int DT>
+__device__ __forceinline__ float load_as_f32(const void* p, int64_t i) {
+  if constexpr (DT == MZK_F32) return static_cast<const float*>(p)[i];
+  else if constexpr (DT == MZK_BF16) return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  else return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+// Round fp32 to the dtype and store (the ".to(x.dtype)" of the reference).
+template <int DT>
+__device__ __forceinline__ void store_from_f32(void* p, int64_t i, float v) {
+  if constexpr (DT == MZK_F32) static_cast<float*>(p)[i] = v;
+  else if constexpr (DT == MZK_BF16) static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+  else static_cast<uint16_t*>(p)[i] = f32_to_f16(v);
+}
+
+// fp32 value rounded to the dtype, returned as fp32.
+template <int DT>
+__device__ __forceinline__ float round_to_dtype(float v) {
+  if constexpr (DT == MZK_F32) return v;
+  else if constexpr (DT == MZK_BF16) return bf16_to_f32(f32_to_bf16(v));
+  else return f16_to_f32(f32_to_f16(v));
+}
+
+// 2^k for integer k in [-126, 127] built from the exponent field.
+__device__ __forceinline__ float pow2i(int k) { return __uint_as_float(static_cast<uint32_t>(k + 127) << 23); }
+
+// ue8m0 scale: 2^(E - 127 + (M != 0)) from the fp32 fields of t > 0 (power of two
+// rounded up).  Results below 2^-126 are built exactly as subnormals.
+__device__ __forceinline__ float pow2_ceil(float t) {
+  uint32_t b = __float_as_uint(t);
+  int k = static_cast<int>((b >> 23) & 0xffu) - 127 + ((b & 0x7fffffu) != 0u);
+  if (k >= 128) return __uint_as_float(0x7f800000u);
+  if (k >= -126) return pow2i(k);
+  return __uint_as_float(1u << (k + 149));  // k in [-127, -126) only for t == 0 / subnormal t
+}
+
+// ------------------------------------------------------------------------------------
+// FP8 e4m3 (OCP e4m3fn) encode/decode, integer arithmetic, round to nearest even.
+// |x| >= 480 or NaN -> NaN code 0x7f (with sign); the sign of zero is kept.
+// ------------------------------------------------------------------------------------
+__device__ __forceinline__ uint8_t e4m3_encode(float x) {
+  uint32_t b = __float_as_uint(x);
+  uint32_t sign = (b >> 24) & 0x80u;
+  uint32_t a = b & 0x7fffffffu;
+  uint32_t code;
+  if (a >= 0x43f00000u) {               // >= 480.0f or NaN
+    code = 0x7fu;
+  } else if (a >= 0x3c800000u) {        // >= 2^-6: normal
+    uint32_t r = (a + 0x7ffffu + ((a >> 20) & 1u)) >> 20;  // 8-bit exp : 3-bit mantissa
+    code = r - ((127u - 7u) << 3);
+  } else {                              // subnormal: nearest multiple of 2^-9, ties to even
+    float s = __uint_as_float(a) * 512.0f;                 // exact
+    code = static_cast<uint32_t>(__builtin_rintf(s));      // 0..8 (8 = smallest normal)
+  }
+  return static_cast<uint8_t>(code | sign);
+}
+
+__device__ __forceinline__ float e4m3_decode(uint32_t c) {
+  // place the 7 magnitude bits at the fp32 exponent/mantissa boundary, then rescale by
+  // 2^120: exact for normals and subnormals alike (fp32 denormals are kept).
+  uint32_t mag = (c & 0x7fu) << 20;
+  float v = __uint_as_float(mag) * 1.329227995784916e+36f;  // 2^120
+  if ((c & 0x7fu) == 0x7fu) v = __uint_as_float(0x7fc00000u);
+  return (c & 0x80u) ? -v : v;
+}
+
+// ------------------------------------------------------------------------------------
+// FP4 e2m1 codes.  code = number of thresholds <= |q| (ties at 0.25/1.25/2.5/5 round
+// down, at 0.75/1.75/3.5 round up), sign in bit 3 from the sign bit (-0 -> 8).
+// ------------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t e2m1_code(float q) {
+  float a = fabsf(q);
+  uint32_t c = (a >= 0x1.000002p-2f) + (a >= 0.75f) + (a >= 0x1.400002p+0f) + (a >= 1.75f) +
+               (a >= 0x1.400002p+1f) + (a >= 3.5f) + (a >= 0x1.400002p+2f);
+  return c | ((__float_as_uint(q) >> 28) & 0x8u);
+}
+
+__device__ __forceinline__ float e2m1_value(uint32_t code) {
+  // {0, .5, 1, 1.5, 2, 3, 4, 6}; code 8 decodes to +0.0
+  const uint32_t m = code & 7u;
+  float v = (m < 4u) ? 0.5f * static_cast<float>(m)
+                     : static_cast<float>(1u << (((m - 4u) >> 1) + 1u)) * ((m & 1u) ? 1.5f : 1.0f);
+  return ((code & 8u) && m) ? -v : v;
+}
+
+// ------------------------------------------------------------------------------------
+// wave helpers (wave64)
+// ------------------------------------------------------------------------------------
+__device__ __forceinline__ float wave_max_group(float v, int group) {
+  for (int m = group >> 1; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+}  // namespace mzk

@@ -1,0 +1,353 @@
+// Piece 1: block FP8-e4m3 / FP4-e2m1 quantizers and the packed cache formats.
+//
+// Semantics follow src/mzoo/archs/owlet1/quant.py (the reference's fake quantizers):
+//   fp8:  amax = max(max|x|, 1e-4);  s = pow2ceil(amax * fp32(1/448));
+//         y = e4m3(clamp(x / s, +-448)) * s                                   (:72-86)
+//   fp4:  ue8m0: s = pow2ceil(max(amax, 6*2^-126) * fp32(1/6))
+//         e4m3 : s = e4m3(max(amax, 6*2^-9) / 6)
+//         y = e2m1(clamp(x / s, +-6)) * s                                     (:49-66)
+// Layout: every kernel maps `G = block_size / 4` consecutive lanes to one block of
+// `block_size` contiguous elements (4 per lane); the block amax is a xor-shuffle
+// reduction inside that lane group.  One HBM read and one write per element.
+#include "common.h"
+
+namespace mzk {
+namespace {
+
+constexpr float kInv448 = 1.0f / 448.0f;  // the fp32-rounded reciprocal the reference multiplies by
+constexpr float kInv6 = 1.0f / 6.0f;
+
+__device__ __forceinline__ float fp8_scale_from_amax(float amax) {
+  return pow2_ceil(fmaxf(amax, 1e-4f) * kInv448);
+}
+
+__device__ __forceinline__ float fp4_scale_from_amax(float amax, bool e4m3_scales) {
+  if (e4m3_scales) return e4m3_decode(e4m3_encode(__fdiv_rn(fmaxf(amax, 0x1.8p-7f /* 6*2^-9 */), 6.0f)));
+  return pow2_ceil(fmaxf(amax, 0x1.8p-124f /* 6*2^-126 */) * kInv6);
+}
+
+__device__ __forceinline__ float clampf(float v, float lim) { return fminf(fmaxf(v, -lim), lim); }
+
+// ---- fake quant (value round trips) ------------------------------------------------
+
+template <int DT, bool FP4>
+__global__ void fake_quant_kernel(const void* __restrict__ x, void* __restrict__ y, int64_t nthreads,
+                                  int group, bool e4m3_scales) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= nthreads) return;  // whole lane groups are in or out (nthreads % group == 0)
+  const int64_t base = t * 4;
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = load_as_f32<DT>(x, base + i);
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  amax = wave_max_group(amax, group);
+  if constexpr (FP4) {
+    const float s = fp4_scale_from_amax(amax, e4m3_scales);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = e2m1_code(clampf(__fdiv_rn(v[i], s), 6.0f));
+      store_from_f32<DT>(y, base + i, e2m1_value(c) * s);
+    }
+  } else {
+    const float s = fp8_scale_from_amax(amax);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = e4m3_encode(clampf(__fdiv_rn(v[i], s), 448.0f));
+      store_from_f32<DT>(y, base + i, e4m3_decode(c) * s);
+    }
+  }
+}
+
+// Fallback for block sizes that are not a power of two in [4, 256]: one thread per block.
+template <int DT, bool FP4>
+__global__ void fake_quant_serial_kernel(const void* __restrict__ x, void* __restrict__ y, int64_t nblocks,
+                                         int bs, bool e4m3_scales) {
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (j >= nblocks) return;
+  const int64_t base = j * bs;
+  float amax = 0.0f;
+  for (int i = 0; i < bs; ++i) amax = fmaxf(amax, fabsf(load_as_f32<DT>(x, base + i)));
+  const float s = FP4 ? fp4_scale_from_amax(amax, e4m3_scales) : fp8_scale_from_amax(amax);
+  for (int i = 0; i < bs; ++i) {
+    const float v = load_as_f32<DT>(x, base + i);
+    float r;
+    if constexpr (FP4) r = e2m1_value(e2m1_code(clampf(__fdiv_rn(v, s), 6.0f))) * s;
+    else r = e4m3_decode(e4m3_encode(clampf(__fdiv_rn(v, s), 448.0f))) * s;
+    store_from_f32<DT>(y, base + i, r);
+  }
+}
+
+// ---- packed encoders ---------------------------------------------------------------
+
+template <int DT>
+__global__ void quant_fp8_block_kernel(const void* __restrict__ x, uint8_t* __restrict__ codes,
+                                       float* __restrict__ scales, int64_t nthreads, int group) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= nthreads) return;
+  const int64_t base = t * 4;
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = load_as_f32<DT>(x, base + i);
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  amax = wave_max_group(amax, group);
+  const float s = fp8_scale_from_amax(amax);
+  uint32_t word = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) word |= static_cast<uint32_t>(e4m3_encode(clampf(__fdiv_rn(v[i], s), 448.0f))) << (8 * i);
+  reinterpret_cast<uint32_t*>(codes)[t] = word;
+  if ((t % group) == 0) scales[t / group] = s;
+}
+
+template <int DT>
+__global__ void quant_mxfp4_kernel(const void* __restrict__ x, uint8_t* __restrict__ packed,
+                                   uint8_t* __restrict__ e8m0, int64_t nthreads) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= nthreads) return;
+  const int64_t base = t * 4;
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = load_as_f32<DT>(x, base + i);
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  amax = wave_max_group(amax, 8);
+  const float s = fp4_scale_from_amax(amax, false);
+  uint32_t c[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c[i] = e2m1_code(clampf(__fdiv_rn(v[i], s), 6.0f));
+  const uint16_t two = static_cast<uint16_t>(c[0] | (c[1] << 4) | (c[2] << 8) | (c[3] << 12));
+  reinterpret_cast<uint16_t*>(packed)[t] = two;
+  if ((t & 7) == 0) e8m0[t >> 3] = static_cast<uint8_t>(__float_as_uint(s) >> 23);
+}
+
+template <int DT>
+__global__ void dequant_fp8_block_kernel(const uint8_t* __restrict__ codes, const float* __restrict__ scales,
+                                         int64_t nthreads, int bs, void* __restrict__ y) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= nthreads) return;
+  const uint32_t word = reinterpret_cast<const uint32_t*>(codes)[t];
+  const float s = scales[(t * 4) / bs];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) store_from_f32<DT>(y, t * 4 + i, e4m3_decode((word >> (8 * i)) & 0xffu) * s);
+}
+
+template <int DT>
+__global__ void dequant_mxfp4_kernel(const uint8_t* __restrict__ packed, const uint8_t* __restrict__ e8m0,
+                                     int64_t nthreads, void* __restrict__ y) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= nthreads) return;
+  const uint32_t two = reinterpret_cast<const uint16_t*>(packed)[t];
+  const float s = __uint_as_float(static_cast<uint32_t>(e8m0[t >> 3]) << 23);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) store_from_f32<DT>(y, t * 4 + i, e2m1_value((two >> (4 * i)) & 0xfu) * s);
+}
+
+// ---- FP8-b128 latent entries ---------------------------------------------------------
+// One workgroup per row; thread t < nope/4 quantizes nope channels 4t..4t+3 (32 lanes per
+// 128-channel block), then the rope channels are rounded to bf16.
+
+template <int DT>
+__global__ void pack_latent_kernel(const void* __restrict__ x, int nope, int rope, const int64_t* __restrict__ dst,
+                                   uint8_t* __restrict__ cache) {
+  const int64_t row = blockIdx.x;
+  const int t = threadIdx.x;
+  const int d = nope + rope;
+  const int nb = nope / 128;
+  const int64_t entry_bytes = nope + 4 * nb + 2 * rope;
+  uint8_t* e = cache + (dst ? dst[row] : row) * entry_bytes;
+  const int64_t xrow = row * d;
+  if (t < nope / 4) {
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = load_as_f32<DT>(x, xrow + 4 * t + i);
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    amax = wave_max_group(amax, 32);
+    const float s = fp8_scale_from_amax(amax);
+    uint32_t word = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) word |= static_cast<uint32_t>(e4m3_encode(clampf(__fdiv_rn(v[i], s), 448.0f))) << (8 * i);
+    reinterpret_cast<uint32_t*>(e)[t] = word;
+    if ((t & 31) == 0) reinterpret_cast<float*>(e + nope)[t >> 5] = s;
+  }
+  uint16_t* r = reinterpret_cast<uint16_t*>(e + nope + 4 * nb);
+  for (int i = t; i < rope; i += blockDim.x) r[i] = f32_to_bf16(load_as_f32<DT>(x, xrow + nope + i));
+}
+
+template <int DT>
+__global__ void unpack_latent_kernel(const uint8_t* __restrict__ cache, int nope, int rope, void* __restrict__ y) {
+  const int64_t row = blockIdx.x;
+  const int t = threadIdx.x;
+  const int d = nope + rope;
+  const int nb = nope / 128;
+  const uint8_t* e = cache + row * static_cast<int64_t>(nope + 4 * nb + 2 * rope);
+  const int64_t yrow = row * d;
+  if (t < nope / 4) {
+    const uint32_t word = reinterpret_cast<const uint32_t*>(e)[t];
+    const float s = reinterpret_cast<const float*>(e + nope)[t >> 5];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) store_from_f32<DT>(y, yrow + 4 * t + i, e4m3_decode((word >> (8 * i)) & 0xffu) * s);
+  }
+  const uint16_t* r = reinterpret_cast<const uint16_t*>(e + nope + 4 * nb);
+  for (int i = t; i < rope; i += blockDim.x) store_from_f32<DT>(y, yrow + nope + i, bf16_to_f32(r[i]));
+}
+
+bool pow2_in(int v, int lo, int hi) { return v >= lo && v <= hi && (v & (v - 1)) == 0; }
+
+inline unsigned grid_for(int64_t n, int threads) { return static_cast<unsigned>((n + threads - 1) / threads); }
+
+#define MZK_DISPATCH_DT(dtype, FN, ...)                               \
+  switch (dtype) {                                                    \
+    case MZK_F32: FN<MZK_F32>(__VA_ARGS__); break;                    \
+    case MZK_BF16: FN<MZK_BF16>(__VA_ARGS__); break;                  \
+    case MZK_F16: FN<MZK_F16>(__VA_ARGS__); break;                    \
+    default: set_last_error("unsupported dtype %d", dtype); return MZK_EINVAL; \
+  }
+
+template <int DT>
+void launch_fake(const void* x, void* y, int64_t rows, int64_t n, int bs, bool fp4, bool e4m3, hipStream_t s) {
+  const int64_t total = rows * n;
+  if (pow2_in(bs, 4, 256)) {
+    const int64_t nthreads = total / 4;
+    if (fp4)
+      fake_quant_kernel<DT, true><<<grid_for(nthreads, 256), 256, 0, s>>>(x, y, nthreads, bs / 4, e4m3);
+    else
+      fake_quant_kernel<DT, false><<<grid_for(nthreads, 256), 256, 0, s>>>(x, y, nthreads, bs / 4, e4m3);
+  } else {
+    const int64_t nblocks = total / bs;
+    if (fp4)
+      fake_quant_serial_kernel<DT, true><<<grid_for(nblocks, 256), 256, 0, s>>>(x, y, nblocks, bs, e4m3);
+    else
+      fake_quant_serial_kernel<DT, false><<<grid_for(nblocks, 256), 256, 0, s>>>(x, y, nblocks, bs, e4m3);
+  }
+}
+
+template <int DT>
+void launch_quant_fp8(const void* x, int64_t rows, int64_t n, int bs, uint8_t* codes, float* scales, hipStream_t s) {
+  const int64_t nthreads = rows * n / 4;
+  quant_fp8_block_kernel<DT><<<grid_for(nthreads, 256), 256, 0, s>>>(x, codes, scales, nthreads, bs / 4);
+}
+
+template <int DT>
+void launch_quant_mxfp4(const void* x, int64_t rows, int64_t n, uint8_t* packed, uint8_t* e8m0, hipStream_t s) {
+  const int64_t nthreads = rows * n / 4;
+  quant_mxfp4_kernel<DT><<<grid_for(nthreads, 256), 256, 0, s>>>(x, packed, e8m0, nthreads);
+}
+
+template <int DT>
+void launch_dequant_fp8(const uint8_t* codes, const float* scales, int64_t rows, int64_t n, int bs, void* y, hipStream_t s) {
+  const int64_t nthreads = rows * n / 4;
+  dequant_fp8_block_kernel<DT><<<grid_for(nthreads, 256), 256, 0, s>>>(codes, scales, nthreads, bs, y);
+}
+
+template <int DT>
+void launch_dequant_mxfp4(const uint8_t* packed, const uint8_t* e8m0, int64_t rows, int64_t n, void* y, hipStream_t s) {
+  const int64_t nthreads = rows * n / 4;
+  dequant_mxfp4_kernel<DT><<<grid_for(nthreads, 256), 256, 0, s>>>(packed, e8m0, nthreads, y);
+}
+
+inline int latent_threads(int nope, int rope) {
+  int t = nope / 4;
+  if (t < rope) t = rope;
+  return ((t + 63) / 64) * 64;
+}
+
+template <int DT>
+void launch_pack_latent(const void* x, int64_t rows, int nope, int rope, const int64_t* dst, uint8_t* cache, hipStream_t s) {
+  pack_latent_kernel<DT><<<static_cast<unsigned>(rows), latent_threads(nope, rope), 0, s>>>(x, nope, rope, dst, cache);
+}
+
+template <int DT>
+void launch_unpack_latent(const uint8_t* cache, int64_t rows, int nope, int rope, void* y, hipStream_t s) {
+  unpack_latent_kernel<DT><<<static_cast<unsigned>(rows), latent_threads(nope, rope), 0, s>>>(cache, nope, rope, y);
+}
+
+}  // namespace
+}  // namespace mzk
+
+using namespace mzk;
+
+extern "C" int mzk_fake_quant_fp8_block(const void* x, void* y, int dtype, int64_t rows, int64_t n, int block_size,
+                                        void* stream) {
+  MZK_CHECK_ARG(x && y, "fake_quant_fp8_block: null pointer");
+  MZK_CHECK_ARG(rows >= 0 && n > 0 && block_size > 0 && n % block_size == 0,
+                "fake_quant_fp8_block: need n %% block_size == 0 (n=%lld, block_size=%d)", (long long)n, block_size);
+  if (rows == 0) return MZK_OK;
+  MZK_DISPATCH_DT(dtype, launch_fake, x, y, rows, n, block_size, false, false, as_stream(stream));
+  MZK_LAUNCH_CHECK("fake_quant_fp8_block");
+  return MZK_OK;
+}
+
+extern "C" int mzk_fake_quant_fp4_block(const void* x, void* y, int dtype, int64_t rows, int64_t n, int block_size,
+                                        int e4m3_scales, void* stream) {
+  MZK_CHECK_ARG(x && y, "fake_quant_fp4_block: null pointer");
+  MZK_CHECK_ARG(rows >= 0 && n > 0 && block_size > 0 && n % block_size == 0,
+                "fake_quant_fp4_block: need n %% block_size == 0 (n=%lld, block_size=%d)", (long long)n, block_size);
+  if (rows == 0) return MZK_OK;
+  MZK_DISPATCH_DT(dtype, launch_fake, x, y, rows, n, block_size, true, e4m3_scales != 0, as_stream(stream));
+  MZK_LAUNCH_CHECK("fake_quant_fp4_block");
+  return MZK_OK;
+}
+
+extern "C" int mzk_quant_fp8_block(const void* x, int dtype, int64_t rows, int64_t n, int block_size, uint8_t* codes,
+                                   float* scales, void* stream) {
+  MZK_CHECK_ARG(x && codes && scales, "quant_fp8_block: null pointer");
+  MZK_CHECK_ARG(pow2_in(block_size, 4, 256) && n % block_size == 0 && rows >= 0,
+                "quant_fp8_block: block_size must be a power of two in [4, 256] dividing n (n=%lld, block_size=%d)",
+                (long long)n, block_size);
+  if (rows == 0) return MZK_OK;
+  MZK_DISPATCH_DT(dtype, launch_quant_fp8, x, rows, n, block_size, codes, scales, as_stream(stream));
+  MZK_LAUNCH_CHECK("quant_fp8_block");
+  return MZK_OK;
+}
+
+extern "C" int mzk_quant_mxfp4(const void* x, int dtype, int64_t rows, int64_t n, uint8_t* packed, uint8_t* e8m0,
+                               void* stream) {
+  MZK_CHECK_ARG(x && packed && e8m0, "quant_mxfp4: null pointer");
+  MZK_CHECK_ARG(n % 32 == 0 && rows >= 0, "quant_mxfp4: n must be a multiple of 32 (n=%lld)", (long long)n);
+  if (rows == 0) return MZK_OK;
+  MZK_DISPATCH_DT(dtype, launch_quant_mxfp4, x, rows, n, packed, e8m0, as_stream(stream));
+  MZK_LAUNCH_CHECK("quant_mxfp4");
+  return MZK_OK;
+}
+
+extern "C" int mzk_dequant_fp8_block(const uint8_t* codes, const float* scales, int64_t rows, int64_t n, int block_size,
+                                     void* y, int dtype, void* stream) {
+  MZK_CHECK_ARG(codes && scales && y, "dequant_fp8_block: null pointer");
+  MZK_CHECK_ARG(block_size >= 4 && block_size % 4 == 0 && n % block_size == 0 && rows >= 0,
+                "dequant_fp8_block: need block_size %% 4 == 0 and n %% block_size == 0");
+  if (rows == 0) return MZK_OK;
+  MZK_DISPATCH_DT(dtype, launch_dequant_fp8, codes, scales, rows, n, block_size, y, as_stream(stream));
+  MZK_LAUNCH_CHECK("dequant_fp8_block");
+  return MZK_OK;
+}
+
+extern "C" int mzk_dequant_mxfp4(const uint8_t* packed, const uint8_t* e8m0, int64_t rows, int64_t n, void* y,
+                                 int dtype, void* stream) {
+  MZK_CHECK_ARG(packed && e8m0 && y, "dequant_mxfp4: null pointer");
+  MZK_CHECK_ARG(n % 32 == 0 && rows >= 0, "dequant_mxfp4: n must be a multiple of 32");
+  if (rows == 0) return MZK_OK;
+  MZK_DISPATCH_DT(dtype, launch_dequant_mxfp4, packed, e8m0, rows, n, y, as_stream(stream));
+  MZK_LAUNCH_CHECK("dequant_mxfp4");
+  return MZK_OK;
+}
+
+extern "C" int mzk_pack_latent_fp8_b128(const void* x, int dtype, int64_t rows, int nope, int rope,
+                                        const int64_t* dst_index, uint8_t* cache, void* stream) {
+  MZK_CHECK_ARG(x && cache, "pack_latent_fp8_b128: null pointer");
+  MZK_CHECK_ARG(nope > 0 && nope % 128 == 0 && nope <= 4096 && rope >= 0 && rope % 2 == 0 && rope <= 1024 && rows >= 0,
+                "pack_latent_fp8_b128: nope must be a positive multiple of 128 (<= 4096), rope even (got %d, %d)",
+                nope, rope);
+  if (rows == 0) return MZK_OK;
+  MZK_DISPATCH_DT(dtype, launch_pack_latent, x, rows, nope, rope, dst_index, cache, as_stream(stream));
+  MZK_LAUNCH_CHECK("pack_latent_fp8_b128");
+  return MZK_OK;
+}
+
+extern "C" int mzk_unpack_latent_fp8_b128(const uint8_t* cache, int64_t rows, int nope, int rope, void* y, int dtype,
+                                          void* stream) {
+  MZK_CHECK_ARG(cache && y, "unpack_latent_fp8_b128: null pointer");
+  MZK_CHECK_ARG(nope > 0 && nope % 128 == 0 && nope <= 4096 && rope >= 0 && rope % 2 == 0 && rope <= 1024 && rows >= 0,
+                "unpack_latent_fp8_b128: nope must be a positive multiple of 128, rope even");
+  if (rows == 0) return MZK_OK;
+  MZK_DISPATCH_DT(dtype, launch_unpack_latent, cache, rows, nope, rope, y, as_stream(stream));
+  MZK_LAUNCH_CHECK("unpack_latent_fp8_b128");
+  return MZK_OK;
+}

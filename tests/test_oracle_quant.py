@@ -1,0 +1,171 @@
+"""CPU: pin the quantizer oracle (oracle/quant.py) before trusting it as the checker.
+
+Pins, each chosen so a plausible slip fails one of them:
+* the reference's own known answers (owlet1/quant.md:46-48 tie table, -0 -> code 8,
+  the e2m1 value table quant.py:8-11) from tests/golden/kat.json;
+* ``pow2_ceil_scale`` against the closed form ``2^ceil(log2 t)`` from ``math.frexp``;
+* ``e2m1_codes`` against brute force "nearest grid value, ties to the even code";
+* ``e4m3_encode`` against torch's own ``float8_e4m3fn`` cast (the library the reference
+  calls, quant.py:60,85) on every fp32 of 2^13 mantissa patterns x all exponents in
+  [2^-20, 480) plus all subnormal-fp8 neighbourhoods;
+* invariants of the composed quantizers: the ceil rule never clips, outputs lie on the
+  scaled grid, pass-through when ``n % block_size``, floors, the +0.0 of code 8.
+"""
+
+import json
+import math
+import pathlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import quant as Q
+
+KAT = json.loads((pathlib.Path(__file__).parent / "golden" / "kat.json").read_text())
+
+
+def test_e2m1_tie_table_kat():
+    k = KAT["e2m1_ties"]
+    assert Q.e2m1_codes(np.array(k["q"], np.float32)).tolist() == k["codes"]
+    assert int(Q.e2m1_codes(np.array([-0.0], np.float32))[0]) == k["negative_zero_code"]
+    assert Q.FP4_TABLE.tolist() == KAT["fp4_table"]["values"]
+
+
+def _nearest_even_e2m1(a: float) -> int:
+    grid = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
+    d = [abs(a - g) for g in grid]
+    best = min(d)
+    cands = [i for i, v in enumerate(d) if v == best]
+    return min(cands, key=lambda i: (i % 2, i))  # ties go to the even code
+
+
+def test_e2m1_brute_force_nearest_even():
+    rng = np.random.default_rng(0)
+    vals = [0.0, 6.0] + list(np.linspace(0, 6, 20001))
+    for b in (0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0):   # every tie and its fp32 neighbours
+        x = np.float32(b)
+        for _ in range(8):
+            vals += [float(x)]
+            x = np.nextafter(x, np.float32(7))
+        x = np.float32(b)
+        for _ in range(8):
+            x = np.nextafter(x, np.float32(-1))
+            vals += [float(x)]
+    vals += list(rng.uniform(0, 6, 20000))
+    a = np.array(vals, np.float32)
+    got = Q.e2m1_codes(a)
+    want = np.array([_nearest_even_e2m1(float(v)) for v in a])
+    assert np.array_equal(got, want)
+    assert np.array_equal(Q.e2m1_codes(-a[a > 0]), want[a > 0] | 8)
+
+
+def test_pow2_ceil_closed_form():
+    rng = np.random.default_rng(1)
+    t = np.concatenate([rng.uniform(1e-30, 1e30, 5000).astype(np.float32),
+                        np.exp2(np.arange(-126, 127)).astype(np.float32),
+                        np.float32(2.0) ** np.arange(-20, 20).astype(np.float32) * np.float32(1.0000001)])
+    got = Q.pow2_ceil_scale(t)
+    for v, g in zip(t.tolist(), got.tolist()):
+        m, e = math.frexp(v)           # v = m * 2^e, m in [0.5, 1)
+        want = 2.0 ** (e - 1) if m == 0.5 else 2.0 ** e
+        assert g == want, (v, g, want)
+
+
+def _all_mantissas(exp_lo, exp_hi, step=1 << 10):
+    out = []
+    for e in range(exp_lo, exp_hi):
+        m = np.arange(0, 1 << 23, step, dtype=np.uint32)
+        m = np.concatenate([m, m + 1, m + (step >> 1), m + (step >> 1) - 1, m + (step >> 1) + 1])
+        m = m[m < (1 << 23)]
+        out.append(((np.uint32(e) << 23) | m).view(np.float32))
+    return np.concatenate(out)
+
+
+def test_e4m3_encode_matches_torch_cast():
+    x = _all_mantissas(127 - 20, 127 + 9)
+    x = x[np.abs(x) < 480]
+    x = np.concatenate([x, -x, np.array([0.0, -0.0, 1e-45, -1e-45], np.float32)])
+    ref = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(Q.e4m3_encode(x), ref)
+    dec = torch.from_numpy(np.arange(256, dtype=np.uint8)).view(torch.float8_e4m3fn).float().numpy()
+    mine = Q.e4m3_decode(np.arange(256, dtype=np.uint8))
+    assert np.array_equal(np.isnan(dec), np.isnan(mine))
+    ok = ~np.isnan(dec)
+    assert np.array_equal(dec[ok].view(np.uint32), mine[ok].view(np.uint32))
+
+
+def test_round_bf16_matches_torch():
+    rng = np.random.default_rng(2)
+    x = np.concatenate([rng.standard_normal(100000).astype(np.float32),
+                        _all_mantissas(120, 125, step=1 << 12)])
+    ref = torch.from_numpy(x).bfloat16().float().numpy()
+    assert np.array_equal(Q.round_bf16(x).view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("bs", [16, 32, 128])
+def test_fp8_fake_quant_invariants(bs):
+    rng = np.random.default_rng(bs)
+    x = (rng.standard_normal((64, 256)) * np.exp(rng.uniform(-8, 8, (64, 1)))).astype(np.float32)
+    codes, scale = Q.fp8_block_codes(x, bs)
+    blocks = np.abs(x.reshape(64, -1, bs))
+    amax = np.maximum(blocks.max(-1), np.float32(1e-4))
+    assert np.all(amax / scale <= 448.0)                     # ceil rule: clamp never clips
+    assert np.all(amax / scale > 224.0 - 1e-3)               # ... and the scale is the smallest such pow2
+    assert np.all(np.log2(scale) == np.round(np.log2(scale)))
+    y = Q.fake_quant_fp8_block(x, bs)
+    assert np.all(np.abs(y - x) <= np.repeat(scale, bs, -1) * 16)   # half an e4m3 ulp at the top binade
+    assert np.array_equal(Q.fake_quant_fp8_block(y, bs), y)         # idempotent
+    assert Q.fake_quant_fp8_block(x[:, :250], bs) is not None
+    z = x[:, :250]
+    assert Q.fake_quant_fp8_block(z, bs) is z or 250 % bs == 0      # pass-through object
+
+
+def test_fp8_floor_and_zero_sign():
+    x = np.zeros((1, 32), np.float32)
+    x[0, 0] = -0.0
+    x[0, 1] = 1e-6
+    codes, s = Q.fp8_block_codes(x, 32)
+    assert s[0, 0] == Q.pow2_ceil_scale(np.float32(1e-4) * np.float32(1 / 448))
+    assert codes[0, 0] == 0x80                                   # -0.0 keeps its sign in fp8
+    y = Q.fake_quant_fp8_block(x, 32)
+    assert np.signbit(y[0, 0])
+
+
+@pytest.mark.parametrize("e4m3", [False, True])
+@pytest.mark.parametrize("bs", [16, 32])
+def test_fp4_fake_quant_invariants(bs, e4m3):
+    rng = np.random.default_rng(7 + bs)
+    x = (rng.standard_normal((32, 128)) * np.exp(rng.uniform(-4, 4, (32, 1)))).astype(np.float32)
+    codes, scale = Q.fp4_block_codes(x, bs, e4m3)
+    y = Q.fake_quant_fp4_block(x, bs, e4m3)
+    grid = Q.FP4_TABLE[codes.astype(int)] * np.repeat(scale, bs, -1)
+    assert np.array_equal(grid, y)
+    if not e4m3:
+        amax = np.abs(x.reshape(32, -1, bs)).max(-1)
+        assert np.all(amax / scale <= 6.0)
+    # a negative value that rounds to zero decodes to +0.0 (code 8 -> +0.0)
+    tiny = np.zeros((1, bs), np.float32)
+    tiny[0, 0], tiny[0, 1] = 1.0, -1e-3
+    assert not np.signbit(Q.fake_quant_fp4_block(tiny, bs, e4m3)[0, 1])
+
+
+def test_fp4_scale_floors():
+    z = np.zeros((1, 32), np.float32)
+    assert Q.fp4_block_scales(z, 32)[0, 0] == Q.pow2_ceil_scale(np.float32(6 * 2.0 ** -126) * np.float32(1 / 6))
+    assert Q.fp4_block_scales(z, 32, True)[0, 0] == np.float32(2.0 ** -9)
+
+
+def test_packed_formats_roundtrip():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((10, 576)).astype(np.float32)
+    e = Q.pack_latent_fp8_b128(x)
+    assert e.shape == (10, 656) and e.dtype == np.uint8
+    back = Q.unpack_latent_fp8_b128(e)
+    assert np.array_equal(back[:, :512], Q.fake_quant_fp8_block(x[:, :512], 128))
+    assert np.array_equal(back[:, 512:], Q.round_bf16(x[:, 512:]))
+    p, s = Q.quant_mxfp4(x[:, :128])
+    assert p.shape == (10, 64) and s.shape == (10, 4)
+    assert np.array_equal(Q.dequant_mxfp4(p, s), Q.fake_quant_fp4_block(x[:, :128], 32))
+    c, sc = Q.fp8_block_codes(x[:, :128], 128)
+    assert np.array_equal(Q.dequant_fp8_block(c, sc, 128), Q.fake_quant_fp8_block(x[:, :128], 128))
