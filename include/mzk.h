@@ -79,6 +79,83 @@ int mzk_pack_latent_fp8_b128(const void* x, int dtype, int64_t rows, int nope, i
 int mzk_unpack_latent_fp8_b128(const uint8_t* cache, int64_t rows, int nope, int rope, void* y,
                                int dtype, void* stream);
 
+/* ---------------------------------------------------------------------------------
+ * Piece 3: lightning-indexer scores (MFMA)
+ *   score[row, g] = Di^-0.5 * sum_h w[row,h] * relu(q[row,h] . k[b,g])  for g < vis,
+ *   -inf otherwise, vis = min(G, (positions[row] + 1) / ratio)
+ * -- owlet1/indexer.py:124-143, layers/attn/golden_ref.py:213-227,
+ *    layers/attn/indexer/fwd.py:112-132.  rows = B*S, row = b*S + s; `w` [rows, Hi] is
+ * already multiplied by Hi^-0.5; positions [rows] int64 may be NULL (position = s).
+ * Keys: batch b starts at key b*k_batch_stride.  scores: [rows, score_stride] fp32.
+ * Hi <= 64. Di: multiple of 64 (fp8 / mxfp4), 32/64/96/128/256 (bf16).
+ * --------------------------------------------------------------------------------- */
+
+/* FP8 (SGLang/DeepSeek V3.2 indexer layout): q_codes [rows, Hi, Di] e4m3 + q_scales
+ * [rows, Hi] fp32; k_codes [B, G, Di] e4m3 + k_scales [B, G] fp32 (one pow2 scale per row,
+ * i.e. mzk_quant_fp8_block with block_size = Di). */
+int mzk_indexer_scores_fp8(const uint8_t* q_codes, const float* q_scales, const float* w,
+                           const uint8_t* k_codes, const float* k_scales, int64_t B, int64_t S,
+                           int Hi, int Di, int64_t G, int64_t k_batch_stride,
+                           const int64_t* positions, int ratio, float* scores,
+                           int64_t score_stride, void* stream);
+
+/* MXFP4 (the model's own indexer quantizer, owlet1/indexer.py:106,129): packed e2m1
+ * [rows, Hi, Di/2] / [B, G, Di/2] + e8m0 [rows, Hi, Di/32] / [B, G, Di/32]
+ * (mzk_quant_mxfp4 output). */
+int mzk_indexer_scores_mxfp4(const uint8_t* q_packed, const uint8_t* q_e8m0, const float* w,
+                             const uint8_t* k_packed, const uint8_t* k_e8m0, int64_t B, int64_t S,
+                             int Hi, int Di, int64_t G, int64_t k_batch_stride,
+                             const int64_t* positions, int ratio, float* scores,
+                             int64_t score_stride, void* stream);
+
+/* bf16 q [rows, Hi, Di] and k [B, G, Di] -- the contract of layers/attn/indexer/fwd.py:112. */
+int mzk_indexer_scores_bf16(const void* q, const float* w, const void* k, int64_t B, int64_t S,
+                            int Hi, int Di, int64_t G, int64_t k_batch_stride,
+                            const int64_t* positions, int ratio, float* scores,
+                            int64_t score_stride, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * Piece 4: top-k selection
+ * --------------------------------------------------------------------------------- */
+
+/* Per-row top-k of fp32 scores -- replaces `index_scores.topk(min(k, G), sorted=False)`
+ * and the -inf -> dummy-slot mapping of owlet1/indexer.py:158-165,
+ * layers/attn/golden_ref.py:230-243 and layers/attn/indexer/attn.py:67-81.
+ * scores [rows, cols] (row stride `row_stride` floats) -> out [rows, topk] int32
+ * (row stride `out_stride`): the selected column indices in ascending order, then -1.
+ * -inf entries are never selected; among equal scores the lower index wins. */
+int mzk_topk_rows(const float* scores, int64_t rows, int64_t cols, int64_t row_stride, int topk,
+                  int32_t* out, int64_t out_stride, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * Piece 5: sparse shared-latent MQA attention
+ * --------------------------------------------------------------------------------- */
+
+/* One softmax per (row, head) over [window ; dense ; gathered top-k] entries + sink,
+ * K == V, scale D^-0.5 -- replaces eager_attention_forward over the concatenated KV
+ * (owlet1/attention.py:42-71, :199-229), golden(level="sparse"/"compressed")
+ * (layers/attn/golden_ref.py:103-168) and csa2_attn.fwd (layers/attn/csa2_attn/fwd.py:238-286).
+ *   q          [B*S rows, H, D] bf16; row = b*S + s; positions [rows] int64 (absolute)
+ *   fmt        0: entries are bf16 [D]; 1: FP8-b128 latent entries (nope = 512 or 128)
+ *   window src win: row sees tokens max(0, pos-window+1)..pos of batch b at entry
+ *              b*win_batch_entries + (win_cap ? tok % win_cap : tok)          (required)
+ *   dense src  entries 0..min(dense_cap, (pos+1)/dense_ratio)-1 at b*dense_batch_entries
+ *              (dense may be NULL)
+ *   sparse src main_kv entries idx[row*idx_row_stride + j], j < topk; idx < 0 or >= G is
+ *              empty (main_kv may be NULL)
+ *   sinks      [H] fp32 natural-log logit or NULL
+ *   nsplit     splits of the entry axis per row; > 1 needs a workspace of
+ *              rows*nsplit*H*(D+2)*4 bytes (partials, merged by a second kernel)
+ *   out        [rows, H, D] bf16;  lse [B, H, S] fp32 (natural log, sink included). */
+int mzk_sparse_mqa(const void* q, int64_t B, int64_t S, int H, int D, int fmt, int nope,
+                   const int64_t* positions, const void* win, int64_t win_batch_entries,
+                   int win_cap, int window, const void* dense, int64_t dense_batch_entries,
+                   int dense_cap, int dense_ratio, const void* main_kv,
+                   int64_t main_batch_entries, int64_t G, const int32_t* idx,
+                   int64_t idx_row_stride, int topk, const float* sinks, int nsplit,
+                   float* workspace, int64_t workspace_bytes, void* out, float* lse,
+                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -37,6 +37,12 @@ _SIGS = {
     "mzk_dequant_mxfp4": [_P, _P, _I64, _I64, _P, _I32, _P],
     "mzk_pack_latent_fp8_b128": [_P, _I32, _I64, _I32, _I32, _P, _P, _P],
     "mzk_unpack_latent_fp8_b128": [_P, _I64, _I32, _I32, _P, _I32, _P],
+    "mzk_topk_rows": [_P, _I64, _I64, _I64, _I32, _P, _I64, _P],
+    "mzk_indexer_scores_fp8": [_P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P, _I64, _P],
+    "mzk_indexer_scores_mxfp4": [_P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P, _I64, _P],
+    "mzk_indexer_scores_bf16": [_P, _P, _P, _I64, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P, _I64, _P],
+    "mzk_sparse_mqa": [_P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _I64, _I32, _I32, _P, _I64, _I32, _I32, _P,
+                       _I64, _I64, _P, _I64, _I32, _P, _I32, _P, _I64, _P, _P, _P],
 }
 _RESTYPE = {"mzk_last_error": ctypes.c_char_p}
 

@@ -1,0 +1,106 @@
+"""Sparse shared-latent MQA attention on the GPU (piece 5).
+
+Kernel-level drop-ins with the reference's signatures
+(``src/mzoo/layers/attn/csa2_attn/{fwd,attn}.py``):
+
+* ``fwd(q, kv, main_kv, indices, *, window, compress_ratio, causal=True, sinks=None)``
+  -> ``(o bf16 [B,S,H,D], lse fp32 [B,H,S])``   (csa2_attn/fwd.py:238-286)
+* ``attn(...)`` -> ``o``                          (csa2_attn/attn.py:40-55, forward only)
+
+``q`` bf16 [B,S,H,D], ``kv`` bf16 [B,S,1,D] (raw latent, K == V), ``main_kv`` bf16
+[B,G,1,D], ``indices`` int32/int64 [B,S,topk] (``-1`` = empty).  Window ``W`` counts the
+query itself (tokens ``t-W+1..t``); ``compress_ratio`` is documentation only: the
+group-causal rule is baked into ``indices`` by the indexer, as in the reference.
+
+Decode form over the packed caches (used by ``mzoo_amd.decode``):
+
+* ``sparse_mqa_decode(q, positions, win_cache, window, ...)`` -- FP8-b128 (656 B) ring
+  window cache, optional dense compressed cache and gathered top-k cache, split-KV.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+FMT_BF16, FMT_FP8 = 0, 1
+
+
+def workspace_bytes(rows: int, heads: int, dim: int, nsplit: int) -> int:
+    return 0 if nsplit <= 1 else rows * nsplit * heads * (dim + 2) * 4
+
+
+def fwd(q: torch.Tensor, kv: torch.Tensor, main_kv: torch.Tensor, indices: torch.Tensor, *, window: int,
+        compress_ratio: int, causal: bool = True, sinks: torch.Tensor | None = None):
+    """Sliding-window + top-k gathered compressed shared-latent MQA forward."""
+    assert causal, "csa2_attn is causal-only: a non-causal sliding window is not a model shape"
+    assert isinstance(window, int) and window >= 1, f"window must be a positive int, got {window!r}"
+    assert isinstance(compress_ratio, int) and compress_ratio >= 1, (
+        f"compress_ratio must be a positive int, got {compress_ratio!r}")
+    assert q.dtype == torch.bfloat16, f"expected bf16, got {q.dtype}"
+    batch, seq_len, heads, dim = q.shape
+    assert kv.shape == (batch, seq_len, 1, dim), f"kv must be [B, S, 1, D]={(batch, seq_len, 1, dim)}, got {tuple(kv.shape)}"
+    groups = main_kv.shape[1]
+    assert main_kv.shape == (batch, groups, 1, dim), f"main_kv must be [B, G, 1, D], got {tuple(main_kv.shape)}"
+    assert indices.dtype in (torch.int32, torch.int64), f"indices must be int32/int64, got {indices.dtype}"
+    assert indices.dim() == 3 and indices.shape[:2] == (batch, seq_len), (
+        f"indices must be [B, S, topk]=[{batch}, {seq_len}, *], got {tuple(indices.shape)}")
+    if sinks is not None:
+        assert sinks.shape == (heads,), f"sinks must be [H]={heads}, got {tuple(sinks.shape)}"
+    _lib.require_gpu(q, kv, main_kv, indices)
+    topk = indices.shape[2]
+    o = torch.empty_like(q)
+    lse = torch.empty(batch, heads, seq_len, dtype=torch.float32, device=q.device)
+    if batch * seq_len == 0:
+        return o, lse
+    qc = q.contiguous()
+    kvc = kv.contiguous().view(batch, seq_len, dim)
+    has_main = groups > 0 and topk > 0
+    main = main_kv.contiguous().view(batch, groups, dim) if has_main else None
+    idx = indices.to(torch.int32).contiguous() if has_main else None
+    pos = torch.arange(seq_len, device=q.device, dtype=torch.int64).repeat(batch)
+    sk = sinks.detach().float().contiguous() if sinks is not None else None
+    _lib.call("mzk_sparse_mqa", qc.data_ptr(), batch, seq_len, heads, dim, FMT_BF16, dim, pos.data_ptr(),
+              kvc.data_ptr(), seq_len, 0, min(window, seq_len), None, 0, 0, 1,
+              _lib.ptr(main), groups, groups, _lib.ptr(idx), topk, topk if has_main else 0, _lib.ptr(sk), 1, None, 0,
+              o.data_ptr(), lse.data_ptr(), _lib.stream_of(q))
+    return o, lse
+
+
+def attn(q, kv, main_kv, indices, *, window: int, compress_ratio: int, causal: bool = True, sinks=None):
+    """Forward of ``csa2_attn.attn`` (no autograd: this build is inference-only)."""
+    return fwd(q, kv, main_kv, indices, window=window, compress_ratio=compress_ratio, causal=causal, sinks=sinks)[0]
+
+
+def sparse_mqa_decode(q: torch.Tensor, positions: torch.Tensor, win_cache: torch.Tensor, window: int, *,
+                      main_cache: torch.Tensor | None = None, groups: int = 0, indices: torch.Tensor | None = None,
+                      dense_cache: torch.Tensor | None = None, dense_ratio: int = 1,
+                      sinks: torch.Tensor | None = None, nsplit: int = 1, nope: int = 512,
+                      workspace: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                      lse: torch.Tensor | None = None):
+    """One decode token per batch row over FP8-b128 caches.
+
+    q bf16 [B,H,D]; positions int64 [B] (absolute position of the new token, whose own
+    entry is already in the window ring); win_cache uint8 [B,Wcap,EB] ring (token t at slot
+    t % Wcap); main_cache uint8 [B,Gcap,EB] with int32 ``indices`` [B,topk] over its first
+    ``groups`` entries; dense_cache uint8 [B,Dcap,EB] scanned over its first
+    ``(pos+1)//dense_ratio`` entries.  Returns (o bf16 [B,H,D], lse fp32 [B,H])."""
+    b, h, d = q.shape
+    _lib.require_gpu(q, positions, win_cache)
+    if out is None:
+        out = torch.empty_like(q)
+    if lse is None:
+        lse = torch.empty(b, h, dtype=torch.float32, device=q.device)
+    need = workspace_bytes(b, h, d, nsplit)
+    if nsplit > 1 and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need // 4, dtype=torch.float32, device=q.device)
+    topk = 0 if indices is None else indices.shape[-1]
+    _lib.call("mzk_sparse_mqa", q.data_ptr(), b, 1, h, d, FMT_FP8, nope, positions.data_ptr(),
+              win_cache.data_ptr(), win_cache.shape[1], win_cache.shape[1], window,
+              _lib.ptr(dense_cache), 0 if dense_cache is None else dense_cache.shape[1],
+              0 if dense_cache is None else dense_cache.shape[1], dense_ratio,
+              _lib.ptr(main_cache), 0 if main_cache is None else main_cache.shape[1], groups,
+              _lib.ptr(indices), topk, topk, _lib.ptr(sinks), nsplit, _lib.ptr(workspace), need,
+              out.data_ptr(), lse.data_ptr(), _lib.stream_of(q))
+    return out, lse

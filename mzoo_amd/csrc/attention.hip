@@ -1,0 +1,557 @@
+// Piece 5: sparse shared-latent MQA attention (window + dense + top-k gathered sources,
+// per-head sink), split over the entry axis with an LSE combine.
+//
+// Semantics -- one softmax per (row, head) over the concatenation
+//     [window entries ; dense compressed entries ; gathered top-k entries] + sink column,
+// K == V (the single shared latent head), scale D^-0.5, sink only in the denominator:
+//   src/mzoo/archs/owlet1/attention.py:42-71 (eager_attention_forward), :199-214;
+//   src/mzoo/layers/attn/golden_ref.py:83-168 (levels window/compressed/sparse);
+//   src/mzoo/layers/attn/csa2_attn/fwd.py:70-219 (index < 0 or >= G contributes nothing,
+//   lse in natural log including the sink).
+// A row is one query token (a decode row, or token t of a prefill), H heads, D channels.
+//   window : tokens max(0, pos-W+1) .. pos of the row's batch (ring slot tok % cap, or a
+//            linear [B, S] array when cap == 0)
+//   dense  : entries 0 .. min(cap, (pos+1)/ratio)-1 of a compressed cache
+//   sparse : main[idx[row, s]] for s < topk (idx < 0 or >= G skipped)
+// Entry formats: bf16 [D] rows, or the 656 B FP8-b128 latent entry (512 e4m3 + 4 fp32
+// scales + 64 bf16 rope), dequantized on load.
+//
+// Tiling (MI355X): one workgroup = one (row, split, group of <= 64 heads); HG x DS waves,
+// HG = head groups of 32 (the MFMA N axis), DS = number of D-parts (2 when D > 256, so a
+// wave's q fragments + O^T accumulators fit one SIMD's registers).  Per 32-entry tile:
+//   1. the tile is loaded from HBM, dequantized to bf16 and written to LDS twice:
+//      Kt[entry][d] (QK operand) and Vt[d][entry'] (PV operand, entries permuted into the
+//      order the MFMA result registers hold them, so P never leaves VGPRs);
+//   2. S^T[32 entries x 32 heads] = Kt . Q^T on v_mfma_f32_32x32x16_bf16, each wave over its
+//      D-part, partial sums exchanged through LDS (fixed order: part 0 + part 1);
+//   3. online softmax in the exp2 domain, lane-local per head (lane l holds head l%32);
+//   4. O^T[d x 32 heads] += Vt . P^T on MFMA, each wave owning its D-part of O.
+// The workgroup writes either the final bf16 output + lse (one split) or fp32 partials
+// (unnormalized O, running max m, sum l) that mzk combine kernel merges with the sink.
+#include "common.h"
+
+namespace mzk {
+namespace {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+enum { kFmtBf16 = 0, kFmtFp8 = 1 };
+
+constexpr int kTile = 32;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+struct AttnParams {
+  const uint16_t* q;  // [rows, H, D] bf16
+  int64_t S;          // rows per batch: row = b * S + s
+  const int64_t* positions;  // [rows] absolute position of each row
+  // window source
+  const uint8_t* win;
+  int64_t win_batch_entries;
+  int win_cap;  // ring capacity; 0 = linear (token t at entry t)
+  int window;
+  // dense source
+  const uint8_t* dense;
+  int64_t dense_batch_entries;
+  int dense_cap;
+  int dense_ratio;
+  // sparse source
+  const uint8_t* main;
+  int64_t main_batch_entries;
+  int64_t G;
+  const int32_t* idx;
+  int64_t idx_row_stride;
+  int topk;
+  // heads / sink
+  int H;
+  const float* sinks;  // [H] or null
+  float scale_log2;    // D^-0.5 * log2(e)
+  int nsplit;
+  // outputs
+  uint16_t* out;  // [rows, H, D] bf16 (nsplit == 1)
+  float* lse;     // [B, H, S]       (nsplit == 1)
+  float* part_o;  // [rows, nsplit, H, D]
+  float* part_ml; // [rows, nsplit, H, 2]
+};
+
+template <int FMT, int D, int NOPE>
+struct Layout {
+  static constexpr int kEntryBytes = FMT == kFmtFp8 ? NOPE + 4 * (NOPE / 128) + 2 * (D - NOPE) : 2 * D;
+  static constexpr int kChunks = D / 8;  // 8-channel chunks per entry
+};
+
+// Permuted position (within a 32-entry tile) at which entry n is stored in a Vt row, so
+// that lane half `h` of PV step `ks` reads its 8 k-slots as one 16-byte load.  The MFMA
+// result (S^T) holds in register j of lane l the entry 8*(j/4) + 4*(l/32) + j%4; PV step
+// ks consumes registers 8ks..8ks+7.
+__device__ __forceinline__ int vt_pos(int n) {
+  const int blk = n >> 4, r = n & 15;
+  return blk * 16 + ((r >> 2) & 1) * 8 + (r >> 3) * 4 + (r & 3);
+}
+
+__device__ __forceinline__ int c_entry(int j, int lane) { return 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3); }
+
+// 8 consecutive channels of one entry -> 8 bf16 (as 4 dwords).
+template <int FMT, int D, int NOPE>
+__device__ __forceinline__ uint4 load_chunk(const uint8_t* e, int c) {
+  if constexpr (FMT == kFmtBf16) {
+    return *reinterpret_cast<const uint4*>(e + 16 * c);
+  } else {
+    constexpr int NB = NOPE / 128;
+    if (c < NOPE / 8) {
+      const uint2 raw = *reinterpret_cast<const uint2*>(e + 8 * c);
+      const float s = reinterpret_cast<const float*>(e + NOPE)[c >> 4];
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t word = i < 2 ? raw.x : raw.y;
+        const uint32_t c0 = (word >> (16 * (i & 1))) & 0xffu;
+        const uint32_t c1 = (word >> (16 * (i & 1) + 8)) & 0xffu;
+        // exact: e4m3 (4 significant bits) * pow2 scale has 16 zero low bits in fp32
+        const float f0 = __uint_as_float((c0 & 0x7fu) << 20) * 1.329227995784916e+36f * s;
+        const float f1 = __uint_as_float((c1 & 0x7fu) << 20) * 1.329227995784916e+36f * s;
+        const uint32_t b0 = (__float_as_uint(f0) >> 16) | ((c0 & 0x80u) << 8);
+        const uint32_t b1 = (__float_as_uint(f1) >> 16) | ((c1 & 0x80u) << 8);
+        w[i] = b0 | (b1 << 16);
+      }
+      return uint4{w[0], w[1], w[2], w[3]};
+    } else {
+      return *reinterpret_cast<const uint4*>(e + NOPE + 4 * NB + 16 * (c - NOPE / 8));
+    }
+  }
+}
+
+template <int FMT, int D, int NOPE, int HG, int DS>
+__global__ void __launch_bounds__(HG * DS * 64) sparse_mqa_kernel(const AttnParams p) {
+  using L = Layout<FMT, D, NOPE>;
+  constexpr int NT = HG * DS * 64;
+  constexpr int DPART = D / DS;          // channels per D-part
+  constexpr int QSTEPS = DPART / 16;     // QK MFMA steps per wave
+  constexpr int NDB = DPART / 32;        // 32-channel blocks of O per wave
+  constexpr int KT_PITCH = 2 * D + 16;   // bytes per Kt row
+  constexpr int VT_PITCH = 2 * kTile + 16;  // bytes per Vt row
+  static_assert(DPART % 32 == 0, "D-part must be a multiple of 32 channels");
+
+  extern __shared__ __align__(16) uint8_t smem[];
+  uint8_t* kt = smem;                                   // [32][KT_PITCH]
+  uint8_t* vt = kt + kTile * KT_PITCH;                  // [D][VT_PITCH]
+  float* sx = reinterpret_cast<float*>(vt + D * VT_PITCH);  // [waves][64][16] (DS > 1)
+  __shared__ const uint8_t* tab_ptr[kTile];
+  __shared__ int tab_valid[kTile];
+  __shared__ uint32_t tab_mask;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int hg = wave / DS;
+  const int ds = wave % DS;
+  const int half = lane >> 5;
+  const int64_t row = blockIdx.y;
+  const int split = blockIdx.x;
+  const int64_t b = row / p.S;
+  const int64_t pos = p.positions[row];
+
+  // ---- the row's virtual entry list and this split's share of it
+  const int64_t nw = pos + 1 < p.window ? pos + 1 : p.window;
+  int64_t nd = 0;
+  if (p.dense) {
+    nd = (pos + 1) / p.dense_ratio;
+    if (nd > p.dense_cap) nd = p.dense_cap;
+  }
+  const int64_t ns = p.main ? p.topk : 0;
+  const int64_t total = nw + nd + ns;
+  int64_t chunk = (total + p.nsplit - 1) / p.nsplit;
+  chunk = (chunk + kTile - 1) / kTile * kTile;
+  const int64_t v_begin = split * chunk;
+  const int64_t v_end = v_begin + chunk < total ? v_begin + chunk : total;
+
+  // ---- q fragments (B operand of S^T = K Q^T): head hg*32 + lane%32, channels of this
+  // wave's D-part, 8 per lane per step
+  const int head = blockIdx.z * (HG * 32) + hg * 32 + (lane & 31);
+  const bool head_ok = head < p.H;
+  v8bf qf[QSTEPS];
+  {
+    const uint16_t* qrow = p.q + (row * p.H + (head_ok ? head : 0)) * D + ds * DPART + half * 8;
+#pragma unroll
+    for (int st = 0; st < QSTEPS; ++st) {
+      uint4 v = head_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * st) : uint4{0, 0, 0, 0};
+      qf[st] = __builtin_bit_cast(v8bf, v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w});
+    }
+  }
+
+  v16f acc_o[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i) acc_o[i] = v16f{};
+  float m_run = -__builtin_huge_valf();
+  float l_run = 0.0f;
+
+  const uint8_t* win_b = p.win ? p.win + b * p.win_batch_entries * L::kEntryBytes : nullptr;
+  const uint8_t* dense_b = p.dense ? p.dense + b * p.dense_batch_entries * L::kEntryBytes : nullptr;
+  const uint8_t* main_b = p.main ? p.main + b * p.main_batch_entries * L::kEntryBytes : nullptr;
+  const int32_t* idx_row = p.idx ? p.idx + row * p.idx_row_stride : nullptr;
+
+#pragma unroll 1
+  for (int64_t t0 = v_begin; t0 < v_end; t0 += kTile) {
+    // 1a. entry table
+    if (tid < kTile) {
+      const int64_t v = t0 + tid;
+      const uint8_t* ptr = nullptr;
+      int valid = 0;
+      if (v < v_end) {
+        if (v < nw) {
+          const int64_t tok = pos - nw + 1 + v;
+          const int64_t slot = p.win_cap ? tok % p.win_cap : tok;
+          ptr = win_b + slot * L::kEntryBytes;
+          valid = 1;
+        } else if (v < nw + nd) {
+          ptr = dense_b + (v - nw) * L::kEntryBytes;
+          valid = 1;
+        } else {
+          const int64_t g = idx_row[v - nw - nd];
+          if (g >= 0 && g < p.G) {
+            ptr = main_b + g * L::kEntryBytes;
+            valid = 1;
+          }
+        }
+      }
+      tab_ptr[tid] = ptr;
+      tab_valid[tid] = valid;
+      const uint64_t bal = __ballot(valid);
+      if (tid == 0) tab_mask = static_cast<uint32_t>(bal);
+    }
+    __syncthreads();
+
+    // 1b. load + dequantize: item = (entry pair, 8-channel chunk)
+    for (int item = tid; item < (kTile / 2) * L::kChunks; item += NT) {
+      const int pr = item / L::kChunks;
+      const int c = item - pr * L::kChunks;
+      const int n0 = 2 * pr;
+      uint4 v0 = uint4{0, 0, 0, 0}, v1 = uint4{0, 0, 0, 0};
+      if (tab_valid[n0]) v0 = load_chunk<FMT, D, NOPE>(tab_ptr[n0], c);
+      if (tab_valid[n0 + 1]) v1 = load_chunk<FMT, D, NOPE>(tab_ptr[n0 + 1], c);
+      *reinterpret_cast<uint4*>(kt + n0 * KT_PITCH + 16 * c) = v0;
+      *reinterpret_cast<uint4*>(kt + (n0 + 1) * KT_PITCH + 16 * c) = v1;
+      // Vt: entries n0, n0+1 sit at adjacent positions (same group of 4) -> one dword
+      const int vp = vt_pos(n0);
+      const uint32_t a0[4] = {v0.x, v0.y, v0.z, v0.w};
+      const uint32_t a1[4] = {v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = (a0[i] & 0xffffu) | (a1[i] << 16);
+        const uint32_t hi = (a0[i] >> 16) | (a1[i] & 0xffff0000u);
+        *reinterpret_cast<uint32_t*>(vt + (8 * c + 2 * i) * VT_PITCH + 2 * vp) = lo;
+        *reinterpret_cast<uint32_t*>(vt + (8 * c + 2 * i + 1) * VT_PITCH + 2 * vp) = hi;
+      }
+    }
+    __syncthreads();
+
+    // 2. S^T partial over this wave's D-part
+    v16f s = v16f{};
+    {
+      const uint8_t* krow = kt + (lane & 31) * KT_PITCH + 2 * (ds * DPART + half * 8);
+      if constexpr (DS == 1) {
+        // two independent accumulation chains (even / odd K-steps), summed in that order
+        v16f s1 = v16f{};
+#pragma unroll
+        for (int st = 0; st < QSTEPS; ++st) {
+          const uint4 kv = *reinterpret_cast<const uint4*>(krow + 32 * st);
+          const v8bf ka = __builtin_bit_cast(v8bf, v4i{(int)kv.x, (int)kv.y, (int)kv.z, (int)kv.w});
+          if (st & 1) s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[st], s1, 0, 0, 0);
+          else s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[st], s, 0, 0, 0);
+        }
+        s = s + s1;
+      } else {
+#pragma unroll
+        for (int st = 0; st < QSTEPS; ++st) {
+          const uint4 kv = *reinterpret_cast<const uint4*>(krow + 32 * st);
+          const v8bf ka = __builtin_bit_cast(v8bf, v4i{(int)kv.x, (int)kv.y, (int)kv.z, (int)kv.w});
+          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[st], s, 0, 0, 0);
+        }
+        // partial S of each D-part through LDS, summed in D-part order by every wave
+        float* mine = sx + (wave * 64 + lane) * 16;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) mine[j] = s[j];
+        __syncthreads();
+        const float* p0 = sx + ((hg * DS) * 64 + lane) * 16;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s[j] = p0[j];
+#pragma unroll
+        for (int part = 1; part < DS; ++part) {
+          const float* pp = sx + ((hg * DS + part) * 64 + lane) * 16;
+#pragma unroll
+          for (int j = 0; j < 16; ++j) s[j] = s[j] + pp[j];
+        }
+      }
+    }
+
+    // 3. online softmax (exp2 domain), lane-local per head
+    const uint32_t vmask = tab_mask;
+    float tmax = -__builtin_huge_valf();
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      s[j] = ((vmask >> c_entry(j, lane)) & 1u) ? s[j] * p.scale_log2 : -__builtin_huge_valf();
+      tmax = fmaxf(tmax, s[j]);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run, tmax);
+    float alpha = 1.0f;
+    float psum = 0.0f;
+    uint32_t pk[8];
+    if (m_new == -__builtin_huge_valf()) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pk[i] = 0u;
+    } else {
+      alpha = exp2f(m_run - m_new);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float p0 = exp2f(s[2 * i] - m_new);
+        const float p1 = exp2f(s[2 * i + 1] - m_new);
+        psum = psum + p0 + p1;
+        pk[i] = static_cast<uint32_t>(f32_to_bf16(p0)) | (static_cast<uint32_t>(f32_to_bf16(p1)) << 16);
+      }
+    }
+    psum = psum + __shfl_xor(psum, 32, 64);
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) acc_o[i] = acc_o[i] * alpha;
+
+    // 4. O^T += Vt . P^T
+    const v8bf pf0 = __builtin_bit_cast(v8bf, v4i{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]});
+    const v8bf pf1 = __builtin_bit_cast(v8bf, v4i{(int)pk[4], (int)pk[5], (int)pk[6], (int)pk[7]});
+    {
+      const uint8_t* vrow = vt + (ds * DPART + (lane & 31)) * VT_PITCH + 2 * (half * 8);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const uint4 a0 = *reinterpret_cast<const uint4*>(vrow + db * 32 * VT_PITCH);
+        const uint4 a1 = *reinterpret_cast<const uint4*>(vrow + db * 32 * VT_PITCH + 32);
+        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(v8bf, v4i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w}), pf0, acc_o[db], 0, 0, 0);
+        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(v8bf, v4i{(int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w}), pf1, acc_o[db], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue.  acc_o[db][j] holds O^T[d][head], d = ds*DPART + db*32 + c_entry(j, lane)
+  if (!head_ok) return;
+  if (p.nsplit == 1) {
+    float m_fin = m_run, l_fin = l_run, o_scale;
+    if (p.sinks) {
+      const float sk = p.sinks[head] * kLog2e;
+      const float mm = fmaxf(m_run, sk);
+      const float a = m_run == -__builtin_huge_valf() ? 0.0f : exp2f(m_run - mm);
+      l_fin = l_run * a + exp2f(sk - mm);
+      m_fin = mm;
+      o_scale = a / l_fin;
+    } else {
+      o_scale = 1.0f / l_fin;
+    }
+    uint16_t* orow = p.out + (row * p.H + head) * D + ds * DPART;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d0 = db * 32 + 8 * g4 + 4 * half;
+        const uint32_t w0 = f32_to_bf16(acc_o[db][4 * g4 + 0] * o_scale) |
+                            (static_cast<uint32_t>(f32_to_bf16(acc_o[db][4 * g4 + 1] * o_scale)) << 16);
+        const uint32_t w1 = f32_to_bf16(acc_o[db][4 * g4 + 2] * o_scale) |
+                            (static_cast<uint32_t>(f32_to_bf16(acc_o[db][4 * g4 + 3] * o_scale)) << 16);
+        *reinterpret_cast<uint2*>(orow + d0) = uint2{w0, w1};
+      }
+    }
+    if (ds == 0 && half == 0) {
+      const int64_t s_idx = row % p.S;
+      p.lse[(b * p.H + head) * p.S + s_idx] = (m_fin + __log2f(l_fin)) * kLn2;
+    }
+  } else {
+    float* prow = p.part_o + ((row * p.nsplit + split) * p.H + head) * static_cast<int64_t>(D) + ds * DPART;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d0 = db * 32 + 8 * g4 + 4 * half;
+        *reinterpret_cast<float4*>(prow + d0) =
+            float4{acc_o[db][4 * g4], acc_o[db][4 * g4 + 1], acc_o[db][4 * g4 + 2], acc_o[db][4 * g4 + 3]};
+      }
+    }
+    if (ds == 0 && half == 0) {
+      float* ml = p.part_ml + ((row * p.nsplit + split) * p.H + head) * 2;
+      ml[0] = m_run;
+      ml[1] = l_run;
+    }
+  }
+}
+
+// Merge the split partials of one (row, head) with the sink: one workgroup per (row, head).
+template <int D>
+__global__ void __launch_bounds__(64) combine_kernel(const float* __restrict__ part_o, const float* __restrict__ part_ml,
+                                                     int nsplit, int H, int64_t S, const float* __restrict__ sinks,
+                                                     uint16_t* __restrict__ out, float* __restrict__ lse) {
+  const int64_t row = blockIdx.x;
+  const int head = blockIdx.y;
+  const int lane = threadIdx.x;
+  float M = -__builtin_huge_valf();
+  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, part_ml[((row * nsplit + s) * H + head) * 2]);
+  const float sk = sinks ? sinks[head] * kLog2e : -__builtin_huge_valf();
+  M = fmaxf(M, sk);
+  float L = sinks ? exp2f(sk - M) : 0.0f;
+  for (int s = 0; s < nsplit; ++s) {
+    const float m = part_ml[((row * nsplit + s) * H + head) * 2];
+    const float l = part_ml[((row * nsplit + s) * H + head) * 2 + 1];
+    if (m != -__builtin_huge_valf()) L = L + l * exp2f(m - M);
+  }
+  const float inv = 1.0f / L;
+  for (int d = 4 * lane; d < D; d += 4 * 64) {
+    float4 acc = float4{0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < nsplit; ++s) {
+      const float m = part_ml[((row * nsplit + s) * H + head) * 2];
+      if (m == -__builtin_huge_valf()) continue;
+      const float wgt = exp2f(m - M);
+      const float4 o = *reinterpret_cast<const float4*>(part_o + ((row * nsplit + s) * H + head) * static_cast<int64_t>(D) + d);
+      acc.x = acc.x + o.x * wgt;
+      acc.y = acc.y + o.y * wgt;
+      acc.z = acc.z + o.z * wgt;
+      acc.w = acc.w + o.w * wgt;
+    }
+    const uint32_t w0 = f32_to_bf16(acc.x * inv) | (static_cast<uint32_t>(f32_to_bf16(acc.y * inv)) << 16);
+    const uint32_t w1 = f32_to_bf16(acc.z * inv) | (static_cast<uint32_t>(f32_to_bf16(acc.w * inv)) << 16);
+    *reinterpret_cast<uint2*>(out + (row * H + head) * static_cast<int64_t>(D) + d) = uint2{w0, w1};
+  }
+  if (lane == 0) {
+    const int64_t b = row / S, s_idx = row % S;
+    lse[(b * H + head) * S + s_idx] = (M + __log2f(L)) * kLn2;
+  }
+}
+
+template <int FMT, int D, int NOPE, int HG, int DS>
+int launch_attn(const AttnParams& p, int64_t rows, hipStream_t s) {
+  constexpr int NT = HG * DS * 64;
+  constexpr size_t lds = static_cast<size_t>(kTile) * (2 * D + 16) + static_cast<size_t>(D) * (2 * kTile + 16) +
+                         (DS > 1 ? static_cast<size_t>(HG * DS) * 64 * 16 * 4 : 0);
+  static_assert(lds <= 150 * 1024, "LDS budget");
+  auto kern = sparse_mqa_kernel<FMT, D, NOPE, HG, DS>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                        static_cast<int>(lds));
+    attr_set = true;
+  }
+  // heads beyond HG*32 go to further workgroups along z (each re-reads the KV tiles)
+  dim3 grid(static_cast<unsigned>(p.nsplit), static_cast<unsigned>(rows), static_cast<unsigned>((p.H + HG * 32 - 1) / (HG * 32)));
+  kern<<<grid, NT, lds, s>>>(p);
+  return MZK_OK;
+}
+
+template <int FMT, int D, int NOPE>
+int dispatch_heads(const AttnParams& p, int64_t rows, hipStream_t s) {
+  // D > 256: two waves per 32 heads, each owning half of D (keeps q + O^T within 256 VGPRs)
+  constexpr int DS = D > 256 ? 2 : 1;
+  // at most 64 heads per workgroup: q fragments + O^T accumulators of 64 heads x D fill the
+  // register file of one CU at one wave per SIMD; more heads use several workgroups.
+  if (p.H <= 32) return launch_attn<FMT, D, NOPE, 1, DS>(p, rows, s);
+  if (p.H <= 128) return launch_attn<FMT, D, NOPE, 2, DS>(p, rows, s);
+  set_last_error("sparse_mqa: at most 128 heads (got %d)", p.H);
+  return MZK_EUNSUPPORTED;
+}
+
+int dispatch(int fmt, int D, int nope, const AttnParams& p, int64_t rows, hipStream_t s) {
+  if (fmt == kFmtFp8) {
+    if (D == 576 && nope == 512) return dispatch_heads<kFmtFp8, 576, 512>(p, rows, s);
+    if (D == 160 && nope == 128) return dispatch_heads<kFmtFp8, 160, 128>(p, rows, s);
+    set_last_error("sparse_mqa fp8: unsupported latent %d+%d (have 512+64, 128+32)", nope, D - nope);
+    return MZK_EUNSUPPORTED;
+  }
+  switch (D) {
+    case 64: return dispatch_heads<kFmtBf16, 64, 64>(p, rows, s);
+    case 96: return dispatch_heads<kFmtBf16, 96, 96>(p, rows, s);
+    case 128: return dispatch_heads<kFmtBf16, 128, 128>(p, rows, s);
+    case 160: return dispatch_heads<kFmtBf16, 160, 160>(p, rows, s);
+    case 256: return dispatch_heads<kFmtBf16, 256, 256>(p, rows, s);
+    case 576: return dispatch_heads<kFmtBf16, 576, 576>(p, rows, s);
+    default:
+      set_last_error("sparse_mqa bf16: unsupported head dim %d (have 64, 96, 128, 160, 256, 576)", D);
+      return MZK_EUNSUPPORTED;
+  }
+}
+
+template <int D>
+void launch_combine(const float* po, const float* pml, int nsplit, int H, int64_t S, const float* sinks, uint16_t* out,
+                    float* lse, int64_t rows, hipStream_t s) {
+  combine_kernel<D><<<dim3(static_cast<unsigned>(rows), static_cast<unsigned>(H)), 64, 0, s>>>(po, pml, nsplit, H, S,
+                                                                                               sinks, out, lse);
+}
+
+}  // namespace
+}  // namespace mzk
+
+using namespace mzk;
+
+extern "C" int mzk_sparse_mqa(const void* q, int64_t B, int64_t S, int H, int D, int fmt, int nope,
+                              const int64_t* positions, const void* win, int64_t win_batch_entries, int win_cap,
+                              int window, const void* dense, int64_t dense_batch_entries, int dense_cap,
+                              int dense_ratio, const void* main_kv, int64_t main_batch_entries, int64_t G,
+                              const int32_t* idx, int64_t idx_row_stride, int topk, const float* sinks, int nsplit,
+                              float* workspace, int64_t workspace_bytes, void* out, float* lse, void* stream) {
+  MZK_CHECK_ARG(B >= 0 && S >= 0 && H >= 1 && D > 0, "sparse_mqa: bad sizes");
+  MZK_CHECK_ARG(fmt == 0 || fmt == 1, "sparse_mqa: fmt must be 0 (bf16) or 1 (fp8-b128)");
+  MZK_CHECK_ARG(nsplit >= 1 && nsplit <= 65535, "sparse_mqa: nsplit must be in [1, 65535]");
+  MZK_CHECK_ARG(window >= 1 && win != nullptr, "sparse_mqa: a window source (window >= 1) is required");
+  MZK_CHECK_ARG(win_cap == 0 || win_cap >= window, "sparse_mqa: ring capacity smaller than the window");
+  MZK_CHECK_ARG(!dense || (dense_ratio >= 1 && dense_cap >= 0), "sparse_mqa: dense source needs ratio >= 1");
+  MZK_CHECK_ARG(!main_kv || (idx && topk >= 0 && G >= 0 && idx_row_stride >= topk && main_batch_entries >= G),
+                "sparse_mqa: sparse source needs idx [rows, >= topk] and main_batch_entries >= G");
+  const int64_t rows = B * S;
+  if (rows == 0) return MZK_OK;
+  MZK_CHECK_ARG(q && positions && out && lse, "sparse_mqa: null pointer");
+  MZK_CHECK_ARG(rows <= 0x7fffffff, "sparse_mqa: too many rows");
+  if (nsplit > 1) {
+    const int64_t need = rows * nsplit * static_cast<int64_t>(H) * (D + 2) * 4;
+    MZK_CHECK_ARG(workspace && workspace_bytes >= need, "sparse_mqa: workspace needs %lld bytes", (long long)need);
+  }
+  AttnParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.S = S;
+  p.positions = positions;
+  p.win = static_cast<const uint8_t*>(win);
+  p.win_batch_entries = win_batch_entries;
+  p.win_cap = win_cap;
+  p.window = window;
+  p.dense = static_cast<const uint8_t*>(dense);
+  p.dense_batch_entries = dense_batch_entries;
+  p.dense_cap = dense_cap;
+  p.dense_ratio = dense_ratio < 1 ? 1 : dense_ratio;
+  p.main = static_cast<const uint8_t*>(main_kv);
+  p.main_batch_entries = main_batch_entries;
+  p.G = G;
+  p.idx = idx;
+  p.idx_row_stride = idx_row_stride;
+  p.topk = main_kv ? topk : 0;
+  p.H = H;
+  p.sinks = sinks;
+  p.scale_log2 = (1.0f / __builtin_sqrtf(static_cast<float>(D))) * kLog2e;
+  p.nsplit = nsplit;
+  p.out = static_cast<uint16_t*>(out);
+  p.lse = lse;
+  p.part_o = workspace;
+  p.part_ml = workspace ? workspace + rows * nsplit * static_cast<int64_t>(H) * D : nullptr;
+  hipStream_t s = as_stream(stream);
+  int rc = dispatch(fmt, D, nope, p, rows, s);
+  if (rc) return rc;
+  MZK_LAUNCH_CHECK("sparse_mqa");
+  if (nsplit > 1) {
+    switch (D) {
+      case 64: launch_combine<64>(p.part_o, p.part_ml, nsplit, H, S, sinks, p.out, lse, rows, s); break;
+      case 96: launch_combine<96>(p.part_o, p.part_ml, nsplit, H, S, sinks, p.out, lse, rows, s); break;
+      case 128: launch_combine<128>(p.part_o, p.part_ml, nsplit, H, S, sinks, p.out, lse, rows, s); break;
+      case 160: launch_combine<160>(p.part_o, p.part_ml, nsplit, H, S, sinks, p.out, lse, rows, s); break;
+      case 256: launch_combine<256>(p.part_o, p.part_ml, nsplit, H, S, sinks, p.out, lse, rows, s); break;
+      default: launch_combine<576>(p.part_o, p.part_ml, nsplit, H, S, sinks, p.out, lse, rows, s); break;
+    }
+    MZK_LAUNCH_CHECK("sparse_mqa combine");
+  }
+  return MZK_OK;
+}

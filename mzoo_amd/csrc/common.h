@@ -59,8 +59,19 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }
 
+// fp32 -> fp16, round to nearest even, in integer arithmetic.  (A plain conversion lets
+// the compiler fold a preceding multiply into v_fma_mix*_f16 with a +0 addend, which
+// turns a -0.0 product into +0.0.)
 __device__ __forceinline__ uint16_t f32_to_f16(float f) {
-  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));  // round to nearest even
+  const uint32_t b = __float_as_uint(f);
+  const uint32_t sign = (b >> 16) & 0x8000u;
+  const uint32_t a = b & 0x7fffffffu;
+  uint32_t h;
+  if (a > 0x7f800000u) h = 0x7e00u;                         // NaN
+  else if (a >= 0x477ff000u) h = 0x7c00u;                   // rounds to +-inf
+  else if (a >= 0x38800000u) h = ((a + 0xfffu + ((a >> 13) & 1u)) >> 13) - (112u << 10);  // normal
+  else h = static_cast<uint32_t>(__builtin_rintf(__uint_as_float(a) * 16777216.0f));      // 2^-24 steps
+  return static_cast<uint16_t>(h | sign);
 }
 
 // Load element i of a tensor of the given dtype as fp32.

@@ -1,0 +1,136 @@
+"""Lightning indexer on the GPU (pieces 3 and 4): scores on MFMA, radix top-k.
+
+Kernel-level drop-ins with the reference's signatures and output contracts:
+
+* ``fwd(q, k, w, *, compress_ratio)``        -- ``layers/attn/indexer/fwd.py:112-132``
+  bf16 ``q [B,S,Hi,Di]``, ``k [B,T,Di]``, fp32 ``w [B,S,Hi]`` (already x ``Hi**-0.5``)
+  -> fp32 ``[B,S,T]``, ``-inf`` where ``t >= (s+1)//compress_ratio``.
+* ``attn(q, k, w, *, compress_ratio, topk)`` -- ``layers/attn/indexer/attn.py:67-81``
+  -> int32 ``[B,S,topk]``, ``-1`` = empty slot.
+
+Quantized paths used by the decode step (same math on packed operands):
+
+* ``scores_fp8``   -- FP8-e4m3 q/k with one pow2 fp32 scale per row (V3.2 layout)
+* ``scores_mxfp4`` -- MXFP4 q/k (e2m1 + e8m0 per 32), the model's own indexer quantizer
+* ``topk``         -- per-row top-k, lowest index wins ties, ascending output, ``-1`` pad
+
+``positions`` (int64 ``[B,S]``) gives absolute query positions for the group-causal
+rule; omitted, query ``s`` sits at position ``s`` (a prefill from position 0).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _positions(positions, b, s, device):
+    if positions is None:
+        return None
+    p = torch.as_tensor(positions, device=device).to(torch.int64).expand(b, s).contiguous()
+    return p
+
+
+def topk(scores: torch.Tensor, k: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """scores fp32 [..., G] -> int32 [..., k]: the ``min(k, G)`` best columns (lower index
+    first among equal scores), never a ``-inf`` one, ascending, then ``-1``."""
+    _lib.require_gpu(scores)
+    if scores.dtype != torch.float32:
+        raise TypeError(f"topk: scores must be float32, got {scores.dtype}")
+    g = scores.shape[-1]
+    sc = scores if scores.stride(-1) == 1 else scores.contiguous()
+    flat = sc.reshape(-1, g) if sc.dim() != 2 else sc
+    rows = flat.shape[0]
+    if out is None:
+        out = torch.empty(*scores.shape[:-1], k, dtype=torch.int32, device=scores.device)
+    of = out.view(-1, k)
+    _lib.call("mzk_topk_rows", flat.data_ptr(), rows, g, flat.stride(0) if rows else g, k, of.data_ptr(), k,
+              _lib.stream_of(scores))
+    return out
+
+
+_topk_rows = topk
+
+
+def _check_scores_out(b, s, g, device, out):
+    if out is None:
+        return torch.empty(b, s, g, dtype=torch.float32, device=device)
+    if out.shape != (b, s, g) or out.dtype != torch.float32 or out.stride(-1) != 1 or out.stride(0) != s * out.stride(1):
+        raise ValueError("scores out must be fp32 [B, S, G] with unit column stride")
+    return out
+
+
+def fwd(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor, *, compress_ratio: int, positions=None) -> torch.Tensor:
+    """Lightning-indexer score matrix (reference ``indexer.fwd``)."""
+    assert q.dtype == k.dtype == torch.bfloat16, f"q/k must be bf16, got {q.dtype}/{k.dtype}"
+    batch, seq_len, heads, dim = q.shape
+    assert k.shape[0] == batch and k.shape[2] == dim, f"k must be [B, T, {dim}], got {tuple(k.shape)}"
+    assert w.shape == (batch, seq_len, heads), f"w must be [B, S, Hi]={(batch, seq_len, heads)}, got {tuple(w.shape)}"
+    assert compress_ratio >= 1, f"compress_ratio must be >= 1, got {compress_ratio}"
+    _lib.require_gpu(q, k, w)
+    seq_kv = k.shape[1]
+    out = torch.empty(batch, seq_len, seq_kv, dtype=torch.float32, device=q.device)
+    if seq_kv == 0 or batch * seq_len == 0:
+        return out
+    qc, kc, wc = q.contiguous(), k.contiguous(), w.float().contiguous()
+    pos = _positions(positions, batch, seq_len, q.device)
+    _lib.call("mzk_indexer_scores_bf16", qc.data_ptr(), wc.data_ptr(), kc.data_ptr(), batch, seq_len, heads, dim, seq_kv,
+              seq_kv, _lib.ptr(pos), compress_ratio, out.data_ptr(), seq_kv, _lib.stream_of(q))
+    return out
+
+
+def attn(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor, *, compress_ratio: int, topk: int,
+         positions=None) -> torch.Tensor:
+    """Indices int32 [B, S, topk] (``-1`` = empty slot) -- reference ``indexer.attn``."""
+    batch, seq_len = q.shape[0], q.shape[1]
+    assert topk >= 0, f"topk must be >= 0, got {topk}"
+    idx = torch.full((batch, seq_len, topk), -1, dtype=torch.int32, device=q.device)
+    if topk == 0 or k.shape[1] == 0:
+        return idx
+    scores = fwd(q, k, w, compress_ratio=compress_ratio, positions=positions)
+    return _topk_rows(scores, topk, out=idx)
+
+
+def scores_fp8(q_codes: torch.Tensor, q_scales: torch.Tensor, w: torch.Tensor, k_codes: torch.Tensor,
+               k_scales: torch.Tensor, *, compress_ratio: int, positions=None, groups: int | None = None,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """FP8 indexer scores.  q_codes uint8 [B,S,Hi,Di], q_scales fp32 [B,S,Hi], w fp32
+    [B,S,Hi], k_codes uint8 [B,Gcap,Di], k_scales fp32 [B,Gcap]; ``groups`` (default Gcap)
+    keys of each batch row are scored -> fp32 [B,S,groups]."""
+    b, s, hi, di = q_codes.shape
+    gcap = k_codes.shape[1]
+    g = gcap if groups is None else groups
+    if k_codes.shape != (b, gcap, di) or k_scales.shape != (b, gcap) or q_scales.shape != (b, s, hi) \
+            or w.shape != (b, s, hi) or q_codes.dtype != torch.uint8 or k_codes.dtype != torch.uint8:
+        raise ValueError("scores_fp8: shape/dtype mismatch")
+    _lib.require_gpu(q_codes, k_codes)
+    out = _check_scores_out(b, s, g, q_codes.device, out)
+    pos = _positions(positions, b, s, q_codes.device)
+    _lib.call("mzk_indexer_scores_fp8", q_codes.contiguous().data_ptr(), q_scales.float().contiguous().data_ptr(),
+              w.float().contiguous().data_ptr(), k_codes.contiguous().data_ptr(),
+              k_scales.float().contiguous().data_ptr(), b, s, hi, di, g, gcap, _lib.ptr(pos), compress_ratio,
+              out.data_ptr(), out.stride(1), _lib.stream_of(q_codes))
+    return out
+
+
+def scores_mxfp4(q_packed: torch.Tensor, q_e8m0: torch.Tensor, w: torch.Tensor, k_packed: torch.Tensor,
+                 k_e8m0: torch.Tensor, *, compress_ratio: int, positions=None, groups: int | None = None,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """MXFP4 indexer scores.  q_packed uint8 [B,S,Hi,Di/2], q_e8m0 uint8 [B,S,Hi,Di/32],
+    k_packed uint8 [B,Gcap,Di/2], k_e8m0 uint8 [B,Gcap,Di/32] -> fp32 [B,S,groups]."""
+    b, s, hi, half = q_packed.shape
+    di = half * 2
+    gcap = k_packed.shape[1]
+    g = gcap if groups is None else groups
+    if k_packed.shape != (b, gcap, half) or k_e8m0.shape != (b, gcap, di // 32) \
+            or q_e8m0.shape != (b, s, hi, di // 32) or w.shape != (b, s, hi):
+        raise ValueError("scores_mxfp4: shape mismatch")
+    _lib.require_gpu(q_packed, k_packed)
+    out = _check_scores_out(b, s, g, q_packed.device, out)
+    pos = _positions(positions, b, s, q_packed.device)
+    _lib.call("mzk_indexer_scores_mxfp4", q_packed.contiguous().data_ptr(), q_e8m0.contiguous().data_ptr(),
+              w.float().contiguous().data_ptr(), k_packed.contiguous().data_ptr(), k_e8m0.contiguous().data_ptr(),
+              b, s, hi, di, g, gcap, _lib.ptr(pos), compress_ratio, out.data_ptr(), out.stride(1),
+              _lib.stream_of(q_packed))
+    return out

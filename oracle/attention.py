@@ -90,9 +90,14 @@ def indexer_scores(q, k, w, compress_ratio, positions=None):
 
 
 def indexer_abs_scores(q, k, w, compress_ratio, positions=None):
-    """``sum_h |w[b,s,h]| * relu(q·k) * Di^-0.5`` -- the magnitude the fp32 accumulation error
-    of ``indexer_scores`` scales with (used to state the relative tolerance)."""
-    return indexer_scores(q, k, torch.as_tensor(w).float().abs(), compress_ratio, positions)
+    """``Di^-0.5 * sum_h |w[b,s,h]| * sum_d |q[b,s,h,d] * k[b,g,d]|`` -- the magnitude the
+    rounding error of any fp32 accumulation order of ``indexer_scores`` scales with (the
+    scale the relative tolerance is stated against).  Masked entries are ``-inf``."""
+    q, k, w = (torch.as_tensor(t).float() for t in (q, k, w))
+    mag = torch.einsum("bshd,bgd->bshg", q.abs(), k.abs()) * q.shape[-1] ** -0.5
+    out = (mag * w.abs().unsqueeze(-1)).sum(dim=2)
+    ref = indexer_scores(q[..., :1] * 0, k[..., :1] * 0, w, compress_ratio, positions)
+    return out.masked_fill(torch.isinf(ref), float("-inf"))
 
 
 def topk_indices(scores, topk: int) -> np.ndarray:
@@ -105,6 +110,8 @@ def topk_indices(scores, topk: int) -> np.ndarray:
                     np.float32)
     lead = sc.shape[:-1]
     g = sc.shape[-1]
+    if g == 0 or sc.size == 0:
+        return np.full((*lead, topk), -1, np.int64)
     flat = sc.reshape(-1, g)
     out = np.full((flat.shape[0], topk), -1, np.int64)
     kk = min(topk, g)

@@ -1,0 +1,199 @@
+"""GPU parity of the sparse latent-MQA kernel (piece 5).
+
+Bar (north_star tier 4): bf16 output cosine >= 0.9999 and max-abs <= 2e-2 against the
+fp32 CPU oracle on identical inputs; lse (fp32 throughout) within atol=rtol=2e-3
+(``layers/attn/csa2_attn/fwd_test.py:26``).  Structural checks from the reference's own
+test matrix (``csa2_attn/fwd_test.py:80-195``): non-power-of-two topk and G, topk beyond
+the visible groups, sinks, all-empty indices and G == 0 (equal to each other bit for bit,
+and to the window-only oracle), plus the FP8-b128 decode form at the BASELINE shapes
+with split-KV.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from mzoo_amd import csa2_attn as MA
+from mzoo_amd import quant as MQ
+from oracle import attention as OA
+from oracle import quant as Q
+from tests.helpers import assert_attn_close
+
+pytestmark = pytest.mark.gpu
+LSE_TOL = dict(atol=2e-3, rtol=2e-3)
+WINDOW = 128
+
+
+def _inputs(b, h, s, d, g, seed=0):
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, s, h, d, generator=gen).bfloat16()
+    kv = torch.randn(b, s, 1, d, generator=gen).bfloat16()
+    main = torch.randn(b, g, 1, d, generator=gen).bfloat16()
+    return q, kv, main
+
+
+def _indices(b, s, g, ratio, topk, seed=1):
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, s, 4, 64, generator=gen)
+    k = torch.randn(b, g, 64, generator=gen)
+    w = torch.randn(b, s, 4, generator=gen) * 0.5
+    return torch.from_numpy(OA.topk_indices(OA.indexer_scores(q, k, w, ratio), topk)).int()
+
+
+def _check(dev, q, kv, main, idx, window=WINDOW, sinks=None):
+    o, lse = MA.fwd(q.to(dev), kv.to(dev), main.to(dev), idx.to(dev), window=window, compress_ratio=2,
+                    sinks=None if sinks is None else sinks.to(dev))
+    assert o.shape == q.shape and o.dtype == torch.bfloat16 and lse.shape == (q.shape[0], q.shape[2], q.shape[1])
+    ref, ref_lse = OA.golden(q.float(), kv.float(), level="sparse", window=window, main_kv=main.float(),
+                             compress_ratio=2, indices=idx.long(), sinks=sinks)
+    assert_attn_close(o, ref)
+    torch.testing.assert_close(lse.cpu(), ref_lse, **LSE_TOL)
+    return o, lse
+
+
+@pytest.mark.parametrize("heads", [4, 16, 64])
+@pytest.mark.parametrize("dim", [64, 96, 128])
+def test_fwd_matches_oracle(dev, dim, heads):
+    q, kv, main = _inputs(2, heads, 512, dim, 256)
+    _check(dev, q, kv, main, _indices(2, 512, 256, 2, 64))
+
+
+@pytest.mark.parametrize("heads", [4, 64])
+def test_fwd_dim256(dev, heads):
+    q, kv, main = _inputs(1, heads, 512, 256, 128)
+    _check(dev, q, kv, main, _indices(1, 512, 128, 4, 64))
+
+
+@pytest.mark.parametrize("topk", [64, 100, 512])
+def test_fwd_topk(dev, topk):
+    q, kv, main = _inputs(1, 64, 512, 128, 256)
+    _check(dev, q, kv, main, _indices(1, 512, 256, 2, topk))
+
+
+def test_fwd_groups_not_power_of_two(dev):
+    idx = _indices(2, 512, 100, 2, 512)
+    assert (idx < 0).any() and idx.max() == 99
+    q, kv, main = _inputs(2, 16, 512, 128, 100)
+    _check(dev, q, kv, main, idx)
+
+
+def test_fwd_sinks(dev):
+    sinks = torch.randn(16, generator=torch.Generator().manual_seed(7))
+    q, kv, main = _inputs(2, 16, 512, 128, 256)
+    _check(dev, q, kv, main, _indices(2, 512, 256, 2, 100), sinks=sinks)
+
+
+def test_fwd_latent_576_128_heads(dev):
+    """The BASELINE latent (512+64) and head count in the prefill form."""
+    q, kv, main = _inputs(1, 128, 256, 576, 64, seed=3)
+    sinks = torch.randn(128, generator=torch.Generator().manual_seed(8))
+    _check(dev, q, kv, main, _indices(1, 256, 64, 4, 32), sinks=sinks)
+
+
+def test_fwd_config1_dims(dev):
+    """Config-1 geometry: 8 heads over a 128+32 latent, window 64."""
+    q, kv, main = _inputs(1, 8, 1024, 160, 256, seed=4)
+    _check(dev, q, kv, main, _indices(1, 1024, 256, 4, 128), window=64)
+
+
+@pytest.mark.parametrize("use_sinks", [False, True])
+def test_all_empty_equals_no_groups_bitwise(dev, use_sinks):
+    q, kv, main = _inputs(2, 16, 512, 128, 256, seed=5)
+    sinks = torch.randn(16).to(dev) if use_sinks else None
+    idx = torch.full((2, 512, 64), -1, dtype=torch.int32)
+    o1, l1 = MA.fwd(q.to(dev), kv.to(dev), main.to(dev), idx.to(dev), window=WINDOW, compress_ratio=2, sinks=sinks)
+    o2, l2 = MA.fwd(q.to(dev), kv.to(dev), main[:, :0].to(dev), idx.to(dev), window=WINDOW, compress_ratio=2,
+                    sinks=sinks)
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    ref, ref_lse = OA.golden(q.float(), kv.float(), level="window", window=WINDOW,
+                             sinks=None if sinks is None else sinks.cpu())
+    assert_attn_close(o1, ref)
+    torch.testing.assert_close(l1.cpu(), ref_lse, **LSE_TOL)
+
+
+def test_all_visible_indices_equal_compressed_oracle(dev):
+    b, s, h, d, g = 1, 256, 16, 128, 128
+    q, kv, main = _inputs(b, h, s, d, g, seed=6)
+    t = torch.arange(s).view(-1, 1)
+    gi = torch.arange(g).view(1, -1)
+    vis = gi < (t + 1) // 2
+    idx = torch.where(vis, gi.expand_as(vis), torch.full_like(gi.expand_as(vis), -1)).unsqueeze(0).int()
+    o, lse = MA.fwd(q.to(dev), kv.to(dev), main.to(dev), idx.to(dev), window=WINDOW, compress_ratio=2)
+    ref, ref_lse = OA.golden(q.float(), kv.float(), level="compressed", window=WINDOW, main_kv=main.float(),
+                             compress_ratio=2)
+    assert_attn_close(o, ref)
+    torch.testing.assert_close(lse.cpu(), ref_lse, **LSE_TOL)
+
+
+def test_rejects_non_causal(dev):
+    q, kv, main = _inputs(1, 16, 64, 128, 32)
+    idx = torch.full((1, 64, 8), -1, dtype=torch.int32)
+    with pytest.raises(AssertionError, match="causal-only"):
+        MA.fwd(q.to(dev), kv.to(dev), main.to(dev), idx.to(dev), window=WINDOW, compress_ratio=2, causal=False)
+
+
+# ---- decode form over FP8-b128 caches ----------------------------------------------------
+
+def _decode_case(dev, b, h, gcap, topk, pos, wcap=128, window=128, dense=0, dense_ratio=128, seed=0):
+    gen = torch.Generator().manual_seed(seed)
+    d = 576
+    q = torch.randn(b, h, d, generator=gen).bfloat16()
+    win_x = torch.randn(b, wcap, d, generator=gen).bfloat16()
+    main_x = torch.randn(b, gcap, d, generator=gen).bfloat16()
+    win_c = MQ.pack_latent_fp8_b128(win_x.to(dev))
+    main_c = MQ.pack_latent_fp8_b128(main_x.to(dev))
+    dense_c = MQ.pack_latent_fp8_b128(torch.randn(b, dense, d, generator=gen).bfloat16().to(dev)) if dense else None
+    g = (pos + 1) // 4
+    idx = torch.stack([torch.randperm(min(g, gcap), generator=gen)[:topk] for _ in range(b)]).int()
+    if idx.shape[1] < topk:
+        idx = torch.cat([idx, torch.full((b, topk - idx.shape[1]), -1, dtype=torch.int32)], 1)
+    idx[0, :7] = -1                                                  # empty slots
+    sinks = torch.randn(h, generator=gen)
+    return q, win_c, main_c, dense_c, idx, sinks, min(g, gcap)
+
+
+def _decode_oracle(q, win_c, main_c, dense_c, idx, sinks, pos, window, dense_ratio, gvalid):
+    win = torch.from_numpy(Q.unpack_latent_fp8_b128(win_c.cpu().numpy()))
+    main = torch.from_numpy(Q.unpack_latent_fp8_b128(main_c.cpu().numpy()))
+    dense = torch.from_numpy(Q.unpack_latent_fp8_b128(dense_c.cpu().numpy())) if dense_c is not None else None
+    wcap = win.shape[1]
+    outs, lses = [], []
+    for r in range(q.shape[0]):
+        nw = min(window, pos + 1)
+        toks = [(pos - nw + 1 + i) % wcap for i in range(nw)]
+        ents = [win[r, toks]]
+        if dense is not None:
+            nd = min(dense.shape[1], (pos + 1) // dense_ratio)
+            ents.append(dense[r, :nd])
+        sel = idx[r][(idx[r] >= 0) & (idx[r] < gvalid)].long()
+        ents.append(main[r, sel])
+        o, l = OA.attend_entries(q[r].float(), torch.cat(ents), sinks)
+        outs.append(o)
+        lses.append(l)
+    return torch.stack(outs), torch.stack(lses)
+
+
+@pytest.mark.parametrize("nsplit", [1, 4, 16])
+def test_decode_fp8_config2_shape(dev, nsplit):
+    b, h, gcap, topk, pos = 32, 128, 8192, 2048, 32767
+    q, win_c, main_c, _, idx, sinks, g = _decode_case(dev, b, h, gcap, topk, pos)
+    positions = torch.full((b,), pos, dtype=torch.int64, device=dev)
+    o, lse = MA.sparse_mqa_decode(q.to(dev), positions, win_c, 128, main_cache=main_c, groups=g,
+                                  indices=idx.to(dev), sinks=sinks.to(dev), nsplit=nsplit)
+    ref, ref_lse = _decode_oracle(q, win_c, main_c, None, idx, sinks, pos, 128, 1, g)
+    assert_attn_close(o, ref)
+    torch.testing.assert_close(lse.cpu(), ref_lse, **LSE_TOL)
+
+
+def test_decode_fp8_early_position_and_dense(dev):
+    """Short history (window not yet full, fewer groups than topk) plus a dense coarse source."""
+    b, h, pos = 4, 128, 300
+    q, win_c, main_c, dense_c, idx, sinks, g = _decode_case(dev, b, h, 256, 128, pos, dense=8, dense_ratio=64,
+                                                            seed=2)
+    positions = torch.full((b,), pos, dtype=torch.int64, device=dev)
+    o, lse = MA.sparse_mqa_decode(q.to(dev), positions, win_c, 128, main_cache=main_c, groups=g,
+                                  indices=idx.to(dev), dense_cache=dense_c, dense_ratio=64, sinks=sinks.to(dev),
+                                  nsplit=3)
+    ref, ref_lse = _decode_oracle(q, win_c, main_c, dense_c, idx, sinks, pos, 128, 64, g)
+    assert_attn_close(o, ref)
+    torch.testing.assert_close(lse.cpu(), ref_lse, **LSE_TOL)

@@ -1,0 +1,157 @@
+"""GPU parity of the indexer score kernels (piece 3) and the top-k kernel (piece 4).
+
+Scores: against ``oracle.attention.indexer_scores`` (fp32 einsum on the dequantized
+operands) within ``SCORE_RTOL`` (1e-5) relative to ``sum_h |w_h| relu(q.k) Di^-0.5``;
+the group-causal ``-inf`` mask must be identical.  Top-k: bit-exact index lists against
+``oracle.attention.topk_indices`` (same scores in, deliberate ties included); end to end
+(scores + top-k) the sets must equal the oracle's except at near-ties of the k-th score.
+Shapes follow the reference tests (``layers/attn/indexer/fwd_test.py:52-83``,
+``attn_test.py:126-139``) plus the BASELINE decode shapes.
+"""
+
+import json
+import pathlib
+
+import numpy as np
+import pytest
+import torch
+
+from mzoo_amd import indexer as MI
+from mzoo_amd import quant as MQ
+from oracle import attention as OA
+from oracle import quant as Q
+from tests.helpers import assert_scores_close, assert_topk_sets_match
+
+pytestmark = pytest.mark.gpu
+KAT = json.loads((pathlib.Path(__file__).parent / "golden" / "kat.json").read_text())
+
+
+def _inputs(b, s, hi, di, g, seed=0):
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, s, hi, di, generator=gen).bfloat16()
+    k = torch.randn(b, g, di, generator=gen).bfloat16()
+    w = torch.randn(b, s, hi, generator=gen) * hi ** -0.5
+    return q, k, w
+
+
+# ---- top-k ------------------------------------------------------------------------------
+
+def test_topk_kat_dummy_slot(dev):
+    k = KAT["topk_dummy_slot"]
+    sc = torch.tensor([[[1.0, 2.0, float("-inf"), float("-inf")]]], device=dev)
+    idx = MI.topk(sc, k["topk"])
+    assert sorted(idx[0, 0, :2].tolist()) == k["first_set"] and idx[0, 0, 2:].tolist() == k["tail"]
+    idx = MI.topk(sc[..., :k["padded_scores_cols"]], k["padded_topk"])
+    assert sorted(idx[0, 0, :2].tolist()) == k["first_set"] and idx[0, 0, 2:].tolist() == k["padded_tail"]
+
+
+@pytest.mark.parametrize("rows,g,k", [(32, 8192, 2048), (8, 32768, 2048), (4, 131072, 2048), (7, 1000, 128),
+                                      (3, 100, 135), (5, 4097, 4096), (2, 0, 16), (64, 256, 1)])
+def test_topk_exact_with_ties(dev, rows, g, k):
+    gen = torch.Generator().manual_seed(rows * 7 + g)
+    sc = torch.randn(rows, g, generator=gen)
+    sc = torch.round(sc * 64) / 64                     # heavy ties
+    if g:
+        sc[:, ::7] = float("-inf")                     # invisible entries
+        sc[0, :] = float("-inf")                       # a row with nothing visible
+        sc[-1, g // 2:] = float("-inf")                # a row with fewer visible than k
+        if rows > 2:
+            sc[1, :] = 0.25                             # a row of all-equal scores
+    got = MI.topk(sc.to(dev), k).cpu().numpy()
+    want = OA.topk_indices(sc.numpy(), k)
+    assert np.array_equal(got, want)
+
+
+# ---- scores -----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("hi", [4, 32, 64])
+@pytest.mark.parametrize("di", [64, 96, 128, 256])
+def test_bf16_scores_match_oracle(dev, hi, di):
+    q, k, w = _inputs(2, 256, hi, di, 128)
+    got = MI.fwd(q.to(dev), k.to(dev), w.to(dev), compress_ratio=2)
+    ref = OA.indexer_scores(q.float(), k.float(), w, 2)
+    assert_scores_close(got, ref, OA.indexer_abs_scores(q.float(), k.float(), w, 2))
+
+
+@pytest.mark.parametrize("ratio,g", [(1, 256), (4, 64), (2, 400), (2, 7)])
+def test_bf16_ratios_and_lengths(dev, ratio, g):
+    q, k, w = _inputs(1, 256, 32, 128, g, seed=ratio)
+    got = MI.fwd(q.to(dev), k.to(dev), w.to(dev), compress_ratio=ratio)
+    ref = OA.indexer_scores(q.float(), k.float(), w, ratio)
+    assert_scores_close(got, ref, OA.indexer_abs_scores(q.float(), k.float(), w, ratio))
+
+
+def test_bf16_empty_kv(dev):
+    q, k, w = _inputs(1, 16, 32, 128, 0)
+    assert MI.fwd(q.to(dev), k.to(dev), w.to(dev), compress_ratio=2).shape == (1, 16, 0)
+    idx = MI.attn(q.to(dev), k.to(dev), w.to(dev), compress_ratio=2, topk=64)
+    assert idx.shape == (1, 16, 64) and bool((idx == -1).all())
+
+
+@pytest.mark.parametrize("topk", [64, 135])
+@pytest.mark.parametrize("ratio", [1, 2, 4])
+def test_attn_indices_match_oracle(dev, ratio, topk):
+    q, k, w = _inputs(2, 256, 32, 128, 128, seed=10 + ratio)
+    got = MI.attn(q.to(dev), k.to(dev), w.to(dev), compress_ratio=ratio, topk=topk)
+    assert got.dtype == torch.int32 and got.shape == (2, 256, topk)
+    ref = OA.indexer_scores(q.float(), k.float(), w, ratio)
+    assert_topk_sets_match(got, ref, OA.indexer_abs_scores(q.float(), k.float(), w, ratio), topk)
+
+
+def _fp8_operands(q, k):
+    di = q.shape[-1]
+    qc, qs = Q.fp8_block_codes(q.float().numpy(), di)
+    kc, ks = Q.fp8_block_codes(k.float().numpy(), di)
+    qd = torch.from_numpy(Q.dequant_fp8_block(qc, qs, di))
+    kd = torch.from_numpy(Q.dequant_fp8_block(kc, ks, di))
+    return (torch.from_numpy(qc), torch.from_numpy(qs[..., 0]), torch.from_numpy(kc), torch.from_numpy(ks[..., 0]),
+            qd, kd)
+
+
+@pytest.mark.parametrize("b,s,g,ratio,pos", [(32, 1, 8192, 4, 32767), (2, 64, 512, 2, None), (3, 1, 1000, 4, 2000)])
+def test_fp8_scores_match_oracle(dev, b, s, g, ratio, pos):
+    q, k, w = _inputs(b, s, 64, 128, g, seed=g)
+    qc, qs, kc, ks, qd, kd = _fp8_operands(q, k)
+    positions = None if pos is None else torch.full((b, s), pos, dtype=torch.int64)
+    got = MI.scores_fp8(qc.to(dev), qs.to(dev), w.to(dev), kc.to(dev), ks.to(dev), compress_ratio=ratio,
+                        positions=None if positions is None else positions.to(dev))
+    ref = OA.indexer_scores(qd, kd, w, ratio, positions)
+    assert_scores_close(got, ref, OA.indexer_abs_scores(qd, kd, w, ratio, positions))
+
+
+def test_fp8_quantizer_feeds_scores(dev):
+    """GPU quantizer -> GPU scores equals oracle quantizer -> oracle scores."""
+    q, k, w = _inputs(4, 1, 64, 128, 2048, seed=3)
+    qc, qs = MQ.quant_fp8_block(q.to(dev), 128)
+    kc, ks = MQ.quant_fp8_block(k.to(dev), 128)
+    pos = torch.full((4, 1), 8191, dtype=torch.int64, device=dev)
+    got = MI.scores_fp8(qc, qs[..., 0], w.to(dev), kc, ks[..., 0], compress_ratio=4, positions=pos)
+    _, _, _, _, qd, kd = _fp8_operands(q, k)
+    ref = OA.indexer_scores(qd, kd, w, 4, pos.cpu())
+    assert_scores_close(got, ref, OA.indexer_abs_scores(qd, kd, w, 4, pos.cpu()))
+
+
+@pytest.mark.parametrize("b,s,g,ratio,pos", [(8, 1, 4096, 4, 16383), (2, 32, 256, 2, None), (1, 1, 300, 1, 150)])
+def test_mxfp4_scores_match_oracle(dev, b, s, g, ratio, pos):
+    q, k, w = _inputs(b, s, 64, 128, g, seed=g + 1)
+    qp, qe = Q.quant_mxfp4(q.float().numpy())
+    kp, ke = Q.quant_mxfp4(k.float().numpy())
+    qd, kd = torch.from_numpy(Q.dequant_mxfp4(qp, qe)), torch.from_numpy(Q.dequant_mxfp4(kp, ke))
+    positions = None if pos is None else torch.full((b, s), pos, dtype=torch.int64)
+    got = MI.scores_mxfp4(torch.from_numpy(qp).to(dev), torch.from_numpy(qe).to(dev), w.to(dev),
+                          torch.from_numpy(kp).to(dev), torch.from_numpy(ke).to(dev), compress_ratio=ratio,
+                          positions=None if positions is None else positions.to(dev))
+    ref = OA.indexer_scores(qd, kd, w, ratio, positions)
+    assert_scores_close(got, ref, OA.indexer_abs_scores(qd, kd, w, ratio, positions))
+
+
+def test_fp8_decode_topk_end_to_end(dev):
+    """BASELINE config-2 indexer: B=32 rows at position 32767, 8192 FP8 keys, top-2048."""
+    q, k, w = _inputs(32, 1, 64, 128, 8192, seed=2)
+    qc, qs, kc, ks, qd, kd = _fp8_operands(q, k)
+    pos = torch.full((32, 1), 32767, dtype=torch.int64)
+    sc = MI.scores_fp8(qc.to(dev), qs.to(dev), w.to(dev), kc.to(dev), ks.to(dev), compress_ratio=4,
+                       positions=pos.to(dev))
+    idx = MI.topk(sc, 2048)
+    ref = OA.indexer_scores(qd, kd, w, 4, pos)
+    assert_topk_sets_match(idx, ref, OA.indexer_abs_scores(qd, kd, w, 4, pos), 2048)
