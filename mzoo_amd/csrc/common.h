@@ -39,6 +39,15 @@ void set_last_error(const char* fmt, ...);
     }                                                                               \
   } while (0)
 
+// Call FN<DT>(args...) for a runtime dtype code (inside a function returning int).
+#define MZK_DISPATCH_DT(dtype, FN, ...)                               \
+  switch (dtype) {                                                    \
+    case MZK_F32: FN<MZK_F32>(__VA_ARGS__); break;                    \
+    case MZK_BF16: FN<MZK_BF16>(__VA_ARGS__); break;                  \
+    case MZK_F16: FN<MZK_F16>(__VA_ARGS__); break;                    \
+    default: set_last_error("unsupported dtype %d", dtype); return MZK_EINVAL; \
+  }
+
 static inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 // ------------------------------------------------------------------------------------

@@ -193,14 +193,6 @@ bool pow2_in(int v, int lo, int hi) { return v >= lo && v <= hi && (v & (v - 1))
 
 inline unsigned grid_for(int64_t n, int threads) { return static_cast<unsigned>((n + threads - 1) / threads); }
 
-#define MZK_DISPATCH_DT(dtype, FN, ...)                               \
-  switch (dtype) {                                                    \
-    case MZK_F32: FN<MZK_F32>(__VA_ARGS__); break;                    \
-    case MZK_BF16: FN<MZK_BF16>(__VA_ARGS__); break;                  \
-    case MZK_F16: FN<MZK_F16>(__VA_ARGS__); break;                    \
-    default: set_last_error("unsupported dtype %d", dtype); return MZK_EINVAL; \
-  }
-
 template <int DT>
 void launch_fake(const void* x, void* y, int64_t rows, int64_t n, int bs, bool fp4, bool e4m3, hipStream_t s) {
   const int64_t total = rows * n;
