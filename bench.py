@@ -1,0 +1,253 @@
+"""Decode throughput of the sparse-attention hot path on one MI355X.
+
+Workload: one CSA2 attention layer decoding one token per row for
+B=32 rows at context 32768: bf16 queries, 128 heads over the shared 512+64 latent stored
+as FP8-b128 (656 B/entry), FP8 lightning indexer 64x128 over the 8192 compressed entries
+(ratio 4), top-2048, sliding window 128, per-head sink.  A "step" is one graph replay of
+``SparseDecodeLayer.step``: window append, indexer-query quantization, indexer scores,
+top-k, sparse MQA (split-KV) and the split merge.  Inputs are synthetic (seed 1) and
+resident in HBM before timing starts.
+
+Prints one JSON line (metric, value = decode tokens/s on this GPU, roofline of the
+dominant kernel measured with HIP events on its stream, cpu_baseline = the CPU oracle's
+decode step on this host's cores over the same workload).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import re
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP8_PEAK_TFLOPS = 5000.0
+
+# Algorithmic work per decoded row
+ENTRY_BYTES = 656                 # FP8-b128 latent entry
+QO_BYTES = 2 * 128 * 576 * 2      # q read + out written, bf16
+IDX_KEY_BYTES = 132               # FP8 indexer key (128 codes + fp32 scale)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--nsplit", type=int, default=4)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline time budget")
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+def build_layer(torch, dev, nsplit):
+    from mzoo_amd.decode import DecodeConfig, SparseDecodeLayer
+    cfg = DecodeConfig(batch=32, heads=128, nope=512, rope=64, index_heads=64, index_dim=128, ratio=4, window=128,
+                       topk=2048, max_groups=8192, index_format="fp8", nsplit=nsplit)
+    ctx = 32768
+    gen = torch.Generator(device=dev).manual_seed(1)
+    sinks = torch.randn(cfg.heads, generator=gen, device=dev)
+    layer = SparseDecodeLayer(cfg, dev, sinks=sinks)
+    b, d = cfg.batch, cfg.dim
+    layer.fill_window(torch.randn(b, cfg.window, d, generator=gen, device=dev).bfloat16(), ctx - 2)
+    layer.append_groups(0, torch.randn(b, cfg.max_groups, d, generator=gen, device=dev).bfloat16(),
+                        torch.randn(b, cfg.max_groups, cfg.index_dim, generator=gen, device=dev).bfloat16())
+    layer.set_positions(ctx - 1)
+    q = torch.randn(b, cfg.heads, d, generator=gen, device=dev).bfloat16()
+    kv = torch.randn(b, d, generator=gen, device=dev).bfloat16()
+    q_idx = torch.randn(b, cfg.index_heads, cfg.index_dim, generator=gen, device=dev).bfloat16()
+    w = torch.randn(b, cfg.index_heads, generator=gen, device=dev) * cfg.index_heads ** -0.5
+    return layer, (q, kv, q_idx, w), sinks
+
+
+def time_launches(torch, fn, iters):
+    """Average duration of `fn` (its kernels on the current stream), HIP events."""
+    st = torch.cuda.current_stream()
+    fn()
+    st.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(iters):
+        fn()
+    e1.record(st)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / iters * 1e3  # microseconds
+
+
+def stage_times(torch, layer, inputs, iters):
+    """Each kernel of the step alone, same inputs, same stream."""
+    from mzoo_amd import _lib, csa2_attn, indexer, quant
+    cfg = layer.cfg
+    b = cfg.batch
+    q, kv, q_idx, w = inputs
+    codes, scales = quant.quant_fp8_block(q_idx.view(b, 1, cfg.index_heads, cfg.index_dim), 128)
+    pos = layer.positions.view(b, 1)
+    slots = layer._slot_base + layer.positions % cfg.window
+    ws = layer.workspace
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+
+    def attn_partial():
+        _lib.call("mzk_sparse_mqa", q.data_ptr(), b, 1, cfg.heads, cfg.dim, 1, cfg.nope, layer.positions.data_ptr(),
+                  layer.win.data_ptr(), cfg.window, cfg.window, cfg.window, None, 0, 0, 1, layer.main.data_ptr(),
+                  cfg.max_groups, cfg.max_groups, layer.idx.data_ptr(), cfg.topk, cfg.topk,
+                  layer.sinks.data_ptr(), cfg.nsplit, ws.data_ptr(), ws.numel() * 4, None, None, st())
+
+    def attn_combine():
+        _lib.call("mzk_sparse_mqa_combine", ws.data_ptr(), b, 1, cfg.heads, cfg.dim, cfg.nsplit,
+                  layer.sinks.data_ptr(), layer.out.data_ptr(), layer.lse.data_ptr(), st())
+
+    stages = {
+        "window_append": lambda: quant.pack_latent_fp8_b128(kv, out=layer.win.view(-1, layer.win.shape[-1]),
+                                                            dst_index=slots),
+        "index_q_quant": lambda: quant.quant_fp8_block(q_idx.view(b, 1, cfg.index_heads, cfg.index_dim), 128),
+        "indexer_scores_fp8": lambda: indexer.scores_fp8(codes, scales[..., 0], w.view(b, 1, -1), layer.k_codes,
+                                                         layer.k_scales, compress_ratio=cfg.ratio, positions=pos,
+                                                         out=layer.scores),
+        "topk": lambda: indexer.topk(layer.scores.view(b, cfg.max_groups), cfg.topk, out=layer.idx),
+        "sparse_mqa": attn_partial,
+        "sparse_mqa_combine": attn_combine,
+    }
+    return {k: time_launches(torch, f, iters) for k, f in stages.items()}
+
+
+def cpu_baseline(torch, layer, inputs, budget_s):
+    """The CPU oracle's decode step (indexer scores -> top-k -> attention) in fp32 on the
+    dequantized caches, all 32 rows, on this host's cores; median of repeated steps."""
+    from mzoo_amd import quant
+    from oracle import attention as OA
+    from oracle import quant as OQ
+    cfg = layer.cfg
+    q, kv, q_idx, w = (t.float().cpu() for t in inputs)
+    win = quant.unpack_latent_fp8_b128(layer.win, dtype=torch.float32).cpu()
+    main = quant.unpack_latent_fp8_b128(layer.main, dtype=torch.float32).cpu()
+    kd = (layer.k_codes.cpu().view(torch.float8_e4m3fn).float() * layer.k_scales.cpu().unsqueeze(-1))
+    sinks = layer.sinks.cpu()
+    pos = int(layer.positions[0])
+    positions = torch.full((cfg.batch, 1), pos, dtype=torch.int64)
+    threads = torch.get_num_threads()
+
+    def step():
+        qd = torch.from_numpy(OQ.fake_quant_fp8_block(q_idx.numpy(), cfg.index_dim))
+        sc = OA.indexer_scores(qd.unsqueeze(1), kd, w.unsqueeze(1), cfg.ratio, positions)
+        idx = torch.from_numpy(OA.topk_indices(sc[:, 0], cfg.topk))
+        toks = torch.arange(pos - cfg.window + 1, pos + 1) % cfg.window
+        for r in range(cfg.batch):
+            ents = torch.cat([win[r, toks], main[r, idx[r][idx[r] >= 0]]])
+            OA.attend_entries(q[r], ents, sinks)
+
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 and (time.perf_counter() - t_start < budget_s or len(times) < 2):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": cfg.batch / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"full config-2 decode step (32 rows: FP8 indexer over 8192 keys, top-2048, "
+                      f"attention over 2176 entries x 128 heads), fp32 torch on dequantized caches, "
+                      f"median of {len(times)} steps"}
+
+
+def traffic_from_profiles(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed PMC summary, if one exists."""
+    f = ROOT / "profiles" / "sparse_mqa_decode_c2_pmc.md"
+    if not f.exists():
+        return None
+    m = re.search(rf"{kernel}\s+traffic_bytes_per_launch\s*=\s*([0-9.eE+]+)", f.read_text())
+    return float(m.group(1)) if m else None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only; multi-GPU runs are not part of it "
+              f"(got --gpus {args.gpus})", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    layer, inputs, _ = build_layer(torch, dev, args.nsplit)
+    cfg = layer.cfg
+    layer.capture(*inputs, advance=False)
+    for _ in range(args.warmup):
+        layer.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        layer.replay()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed / args.steps * 1e3
+    tokens_per_s = cfg.batch / (ms / 1e3)
+
+    stages = stage_times(torch, layer, inputs, max(args.steps, 50))
+    # algorithmic work per launch
+    rows = cfg.batch
+    entries = cfg.window + cfg.topk
+    attn_bytes = rows * (entries * ENTRY_BYTES + QO_BYTES)
+    attn_flops = rows * 4.0 * cfg.dim * cfg.heads * entries
+    idx_bytes = rows * cfg.max_groups * IDX_KEY_BYTES
+    idx_flops = rows * 2.0 * cfg.index_heads * cfg.index_dim * cfg.max_groups
+    dominant = max(("sparse_mqa", "indexer_scores_fp8", "topk"), key=lambda k: stages[k])
+    if dominant == "sparse_mqa":
+        t = stages["sparse_mqa"] * 1e-6
+        mfma_bound = attn_flops / (BF16_PEAK_TFLOPS * 1e12) > attn_bytes / (HBM_PEAK_GBS * 1e9)
+        if mfma_bound:
+            roof = {"bound": "mfma", "achieved": attn_flops / t / 1e12, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s"}
+        else:
+            roof = {"bound": "hbm", "achieved": attn_bytes / t / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s"}
+    elif dominant == "indexer_scores_fp8":
+        t = stages[dominant] * 1e-6
+        roof = {"bound": "hbm", "achieved": idx_bytes / t / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s"}
+    else:
+        t = stages[dominant] * 1e-6
+        sb = rows * cfg.max_groups * 4 + rows * cfg.topk * 4
+        roof = {"bound": "hbm", "achieved": sb / t / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s"}
+    roof["frac"] = roof["achieved"] / roof["peak"]
+    roof["traffic"] = traffic_from_profiles(dominant)
+    roof["kernel"] = dominant
+    roof["kernel_us"] = stages[dominant]
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(torch, layer, inputs, args.cpu_seconds)
+
+    out = {
+        "metric": "decode tokens/s/GPU at 32k ctx (sparse MQA + indexer); % HBM/MFMA roofline",
+        "value": tokens_per_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seed 1), caches resident in HBM",
+        "config": {"workload": "config2: decode B=32 ctx=32768, 128 heads x (512+64) FP8-b128 latent cache, "
+                               "FP8 indexer 64x128 over 8192 groups (ratio 4), top-2048, window 128, sink",
+                   "batch": cfg.batch, "context": 32768, "heads": cfg.heads, "latent": "512+64",
+                   "index": "64x128 fp8", "topk": cfg.topk, "window": cfg.window, "nsplit": cfg.nsplit},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "stages_us": stages,
+        "step_roofline": {
+            "hbm_bytes_alg": attn_bytes + idx_bytes,
+            "ideal_us_hbm": (attn_bytes + idx_bytes) / (HBM_PEAK_GBS * 1e9) * 1e6,
+            "frac_hbm": (attn_bytes + idx_bytes) / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9),
+        },
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

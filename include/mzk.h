@@ -80,6 +80,28 @@ int mzk_unpack_latent_fp8_b128(const uint8_t* cache, int64_t rows, int nope, int
                                int dtype, void* stream);
 
 /* ---------------------------------------------------------------------------------
+ * Piece 2: KV compressor and RoPE
+ * --------------------------------------------------------------------------------- */
+
+/* DeepseekV41Compressor.forward after its two fp32 projections (owlet1/cache.py:157-172)
+ * plus its RMSNorm (owlet1/norm_rope.py:25-30):
+ *   out[b, g] = w * dtype( h * rsqrt(mean(h^2) + eps) ),
+ *   h = dtype( sum_r kv[b, g*ratio + r] * softmax_r(gate[b, g*ratio + r]) )   (ratio > 1)
+ *   h = dtype( kv[b, g] )                                                      (ratio == 1)
+ * kv, gate: fp32 [B, tokens_per_batch, D] (gate unused at ratio 1); norm_weight [D] of
+ * weight_dtype; out [B, n_groups, D] of out_dtype.  D <= 1024.  Evaluation order is fixed
+ * (see compressor.hip), so results are reproducible bit for bit. */
+int mzk_compress(const float* kv, const float* gate, int64_t B, int64_t n_groups, int ratio,
+                 int D, int64_t tokens_per_batch, const void* norm_weight, int weight_dtype,
+                 float eps, void* out, int out_dtype, void* stream);
+
+/* apply_rotary_pos_emb (owlet1/norm_rope.py:126-145): x [rows, D] of `dtype`; the trailing
+ * rope_dim channels are rotated as (even, odd) pairs with cos/sin [rows/heads, rope_dim/2]
+ * fp32 (one table row per `heads` consecutive x rows); inverse != 0 conjugates. */
+int mzk_rope(const void* x, int dtype, const float* cos_t, const float* sin_t, int64_t rows,
+             int D, int rope_dim, int heads, int inverse, void* y, void* stream);
+
+/* ---------------------------------------------------------------------------------
  * Piece 3: lightning-indexer scores (MFMA)
  *   score[row, g] = Di^-0.5 * sum_h w[row,h] * relu(q[row,h] . k[b,g])  for g < vis,
  *   -inf otherwise, vis = min(G, (positions[row] + 1) / ratio)
@@ -146,7 +168,9 @@ int mzk_topk_rows(const float* scores, int64_t rows, int64_t cols, int64_t row_s
  *   sinks      [H] fp32 natural-log logit or NULL
  *   nsplit     splits of the entry axis per row; > 1 needs a workspace of
  *              rows*nsplit*H*(D+2)*4 bytes (partials, merged by a second kernel)
- *   out        [rows, H, D] bf16;  lse [B, H, S] fp32 (natural log, sink included). */
+ *   out        [rows, H, D] bf16;  lse [B, H, S] fp32 (natural log, sink included).
+ *              With nsplit > 1, out == lse == NULL writes only the partials (the merge is
+ *              then mzk_sparse_mqa_combine). */
 int mzk_sparse_mqa(const void* q, int64_t B, int64_t S, int H, int D, int fmt, int nope,
                    const int64_t* positions, const void* win, int64_t win_batch_entries,
                    int win_cap, int window, const void* dense, int64_t dense_batch_entries,
@@ -155,6 +179,12 @@ int mzk_sparse_mqa(const void* q, int64_t B, int64_t S, int H, int D, int fmt, i
                    int64_t idx_row_stride, int topk, const float* sinks, int nsplit,
                    float* workspace, int64_t workspace_bytes, void* out, float* lse,
                    void* stream);
+
+/* Merge the nsplit partials a previous mzk_sparse_mqa call left in `workspace` with the
+ * sink: the log-sum-exp combination of the split softmaxes (equal to the one softmax of
+ * owlet1/attention.py:64-70 over all entries). */
+int mzk_sparse_mqa_combine(const float* workspace, int64_t B, int64_t S, int H, int D,
+                           int nsplit, const float* sinks, void* out, float* lse, void* stream);
 
 #ifdef __cplusplus
 }

@@ -506,7 +506,8 @@ extern "C" int mzk_sparse_mqa(const void* q, int64_t B, int64_t S, int H, int D,
                 "sparse_mqa: sparse source needs idx [rows, >= topk] and main_batch_entries >= G");
   const int64_t rows = B * S;
   if (rows == 0) return MZK_OK;
-  MZK_CHECK_ARG(q && positions && out && lse, "sparse_mqa: null pointer");
+  MZK_CHECK_ARG(q && positions && (nsplit > 1 || (out && lse)), "sparse_mqa: null pointer");
+  MZK_CHECK_ARG((out == nullptr) == (lse == nullptr), "sparse_mqa: out and lse go together");
   MZK_CHECK_ARG(rows <= 0x7fffffff, "sparse_mqa: too many rows");
   if (nsplit > 1) {
     const int64_t need = rows * nsplit * static_cast<int64_t>(H) * (D + 2) * 4;
@@ -542,16 +543,29 @@ extern "C" int mzk_sparse_mqa(const void* q, int64_t B, int64_t S, int H, int D,
   int rc = dispatch(fmt, D, nope, p, rows, s);
   if (rc) return rc;
   MZK_LAUNCH_CHECK("sparse_mqa");
-  if (nsplit > 1) {
-    switch (D) {
-      case 64: launch_combine<64>(p.part_o, p.part_ml, nsplit, H, S, sinks, p.out, lse, rows, s); break;
-      case 96: launch_combine<96>(p.part_o, p.part_ml, nsplit, H, S, sinks, p.out, lse, rows, s); break;
-      case 128: launch_combine<128>(p.part_o, p.part_ml, nsplit, H, S, sinks, p.out, lse, rows, s); break;
-      case 160: launch_combine<160>(p.part_o, p.part_ml, nsplit, H, S, sinks, p.out, lse, rows, s); break;
-      case 256: launch_combine<256>(p.part_o, p.part_ml, nsplit, H, S, sinks, p.out, lse, rows, s); break;
-      default: launch_combine<576>(p.part_o, p.part_ml, nsplit, H, S, sinks, p.out, lse, rows, s); break;
-    }
-    MZK_LAUNCH_CHECK("sparse_mqa combine");
+  if (nsplit > 1 && out != nullptr) return mzk_sparse_mqa_combine(workspace, B, S, H, D, nsplit, sinks, out, lse, stream);
+  return MZK_OK;
+}
+
+extern "C" int mzk_sparse_mqa_combine(const float* workspace, int64_t B, int64_t S, int H, int D, int nsplit,
+                                      const float* sinks, void* out, float* lse, void* stream) {
+  MZK_CHECK_ARG(B >= 0 && S >= 0 && H >= 1 && nsplit >= 1, "sparse_mqa_combine: bad sizes");
+  const int64_t rows = B * S;
+  if (rows == 0) return MZK_OK;
+  MZK_CHECK_ARG(workspace && out && lse, "sparse_mqa_combine: null pointer");
+  const float* po = workspace;
+  const float* pml = workspace + rows * nsplit * static_cast<int64_t>(H) * D;
+  uint16_t* o = static_cast<uint16_t*>(out);
+  hipStream_t s = as_stream(stream);
+  switch (D) {
+    case 64: launch_combine<64>(po, pml, nsplit, H, S, sinks, o, lse, rows, s); break;
+    case 96: launch_combine<96>(po, pml, nsplit, H, S, sinks, o, lse, rows, s); break;
+    case 128: launch_combine<128>(po, pml, nsplit, H, S, sinks, o, lse, rows, s); break;
+    case 160: launch_combine<160>(po, pml, nsplit, H, S, sinks, o, lse, rows, s); break;
+    case 256: launch_combine<256>(po, pml, nsplit, H, S, sinks, o, lse, rows, s); break;
+    case 576: launch_combine<576>(po, pml, nsplit, H, S, sinks, o, lse, rows, s); break;
+    default: set_last_error("sparse_mqa_combine: unsupported head dim %d", D); return MZK_EUNSUPPORTED;
   }
+  MZK_LAUNCH_CHECK("sparse_mqa_combine");
   return MZK_OK;
 }

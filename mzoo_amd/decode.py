@@ -1,0 +1,182 @@
+"""Graph-captured decode step of one CSA2 attention layer (piece 6).
+
+Replaces the per-step work of ``DeepseekV41Attention.forward`` with a cache
+(``owlet1/attention.py:145-229``; cache state ``owlet1/cache.py:84-124``; indexer
+``owlet1/indexer.py:78-165``) for one new token per batch row, with every piece of state
+preallocated on the device so the whole step records into one HIP graph:
+
+* window ring  ``win``   uint8 [B, W, 656]  -- FP8-b128 latent of the last W tokens,
+  token t at slot t % W (the reference keeps the last W-1 and concatenates the new one,
+  ``cache.py:84-94``; the ring holds the same W entries without a ``torch.cat``);
+* compressed   ``main``  uint8 [B, Gcap, 656] -- one entry per emitted group;
+* indexer keys ``k_*``   FP8 (codes [B,Gcap,Di] + fp32 scale [B,Gcap]) or MXFP4
+  (nibbles [B,Gcap,Di/2] + e8m0 [B,Gcap,Di/32]);
+* optional dense coarse branch ``coarse`` uint8 [B, Gc, 656] (hierarchical config);
+* ``positions`` int64 [B] on the device: the position of the token being decoded.  The
+  reference keeps Python ints (``entry_count``, ``cache.py:46``) and grows tensors with
+  ``torch.cat``; here visibility is derived on the device from ``positions``
+  (``(pos+1) // ratio`` visible groups, ``indexer.py:141-143``), so nothing on the host
+  changes between steps.
+
+``step(q, kv, q_idx, w)`` for one token per row:
+  1. pack the new token's latent into its ring slot,
+  2. quantize the indexer query (FP8 b128 per head, or MXFP4),
+  3. indexer scores over all keys (group-causal ``-inf`` beyond ``(pos+1)//ratio``),
+  4. top-k (lowest index wins ties),
+  5. sparse MQA over window + [coarse] + top-k entries with the sink, split-KV + merge,
+  6. ``positions += 1`` when ``advance``.
+Group emission (the compressor, one entry per ``ratio`` steps) is ``append_groups``.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import csa2_attn, indexer, quant
+
+
+@dataclass
+class DecodeConfig:
+    batch: int
+    heads: int = 128
+    nope: int = 512
+    rope: int = 64
+    index_heads: int = 64
+    index_dim: int = 128
+    ratio: int = 4
+    window: int = 128
+    topk: int = 2048
+    max_groups: int = 8192
+    index_format: str = "fp8"       # "fp8" or "mxfp4"
+    coarse_ratio: int = 0            # > 0: dense coarse branch (hierarchical config)
+    coarse_groups: int = 0
+    nsplit: int = 4
+
+    @property
+    def dim(self) -> int:
+        return self.nope + self.rope
+
+
+class SparseDecodeLayer:
+    def __init__(self, cfg: DecodeConfig, device, sinks: torch.Tensor | None = None):
+        if cfg.index_format not in ("fp8", "mxfp4"):
+            raise ValueError(f"index_format must be 'fp8' or 'mxfp4', got {cfg.index_format!r}")
+        self.cfg = cfg
+        self.device = torch.device(device)
+        b, eb = cfg.batch, quant.entry_bytes(cfg.nope, cfg.rope)
+        u8 = dict(dtype=torch.uint8, device=self.device)
+        self.win = torch.zeros(b, cfg.window, eb, **u8)
+        self.main = torch.zeros(b, cfg.max_groups, eb, **u8)
+        self.coarse = torch.zeros(b, cfg.coarse_groups, eb, **u8) if cfg.coarse_ratio else None
+        di = cfg.index_dim
+        if cfg.index_format == "fp8":
+            self.k_codes = torch.zeros(b, cfg.max_groups, di, **u8)
+            self.k_scales = torch.ones(b, cfg.max_groups, dtype=torch.float32, device=self.device)
+        else:
+            self.k_packed = torch.zeros(b, cfg.max_groups, di // 2, **u8)
+            self.k_e8m0 = torch.full((b, cfg.max_groups, di // 32), 127, **u8)
+        self.positions = torch.zeros(b, dtype=torch.int64, device=self.device)
+        self.sinks = None if sinks is None else sinks.float().to(self.device).contiguous()
+        # per-step buffers (fixed addresses, so a captured graph can replay them)
+        self.scores = torch.empty(b, 1, cfg.max_groups, dtype=torch.float32, device=self.device)
+        self.idx = torch.empty(b, cfg.topk, dtype=torch.int32, device=self.device)
+        self.out = torch.empty(b, cfg.heads, cfg.dim, dtype=torch.bfloat16, device=self.device)
+        self.lse = torch.empty(b, cfg.heads, dtype=torch.float32, device=self.device)
+        nbytes = csa2_attn.workspace_bytes(b, cfg.heads, cfg.dim, cfg.nsplit)
+        self.workspace = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=self.device)
+        self._slot_base = torch.arange(b, device=self.device, dtype=torch.int64) * cfg.window
+        self._graph = None
+        self._static = None
+
+    # ---- state ---------------------------------------------------------------------------
+    def set_positions(self, pos) -> None:
+        self.positions.copy_(torch.as_tensor(pos, dtype=torch.int64).expand(self.cfg.batch))
+
+    def fill_window(self, latents: torch.Tensor, last_position: int) -> None:
+        """latents [B, W, D] for tokens last_position-W+1 .. last_position."""
+        w = self.cfg.window
+        toks = torch.arange(last_position - w + 1, last_position + 1, device=self.device)
+        slots = (self._slot_base.view(-1, 1) + (toks % w).view(1, -1)).reshape(-1)
+        quant.pack_latent_fp8_b128(latents.reshape(-1, self.cfg.dim), rope=self.cfg.rope,
+                                   out=self.win.view(-1, self.win.shape[-1]), dst_index=slots)
+
+    def append_groups(self, start: int, latents: torch.Tensor, index_keys: torch.Tensor) -> None:
+        """Write groups start..start+n-1: rotated latents [B,n,D] into the main cache and
+        their indexer keys [B,n,Di] (quantized here) -- update_compressor_states."""
+        n = latents.shape[1]
+        rows = (torch.arange(self.cfg.batch, device=self.device).view(-1, 1) * self.cfg.max_groups
+                + torch.arange(start, start + n, device=self.device).view(1, -1)).reshape(-1)
+        quant.pack_latent_fp8_b128(latents.reshape(-1, self.cfg.dim), rope=self.cfg.rope,
+                                   out=self.main.view(-1, self.main.shape[-1]), dst_index=rows)
+        if self.cfg.index_format == "fp8":
+            codes, scales = quant.quant_fp8_block(index_keys, self.cfg.index_dim)
+            self.k_codes[:, start:start + n] = codes
+            self.k_scales[:, start:start + n] = scales[..., 0]
+        else:
+            packed, e8 = quant.quant_mxfp4(index_keys)
+            self.k_packed[:, start:start + n] = packed
+            self.k_e8m0[:, start:start + n] = e8
+
+    def fill_coarse(self, latents: torch.Tensor) -> None:
+        """latents [B, n, D] -> coarse entries 0..n-1 of every row."""
+        n = latents.shape[1]
+        rows = (torch.arange(self.cfg.batch, device=self.device).view(-1, 1) * self.cfg.coarse_groups
+                + torch.arange(n, device=self.device).view(1, -1)).reshape(-1)
+        quant.pack_latent_fp8_b128(latents.reshape(-1, self.cfg.dim), rope=self.cfg.rope,
+                                   out=self.coarse.view(-1, self.coarse.shape[-1]), dst_index=rows)
+
+    # ---- the step ------------------------------------------------------------------------
+    def step(self, q: torch.Tensor, kv: torch.Tensor | None, q_idx: torch.Tensor, w: torch.Tensor,
+             advance: bool = False) -> torch.Tensor:
+        """q bf16 [B,H,D] (rotated), kv bf16 [B,D] (the new token's rotated latent, or None
+        if already in the ring), q_idx bf16 [B,Hi,Di] (rotated), w fp32 [B,Hi] (x Hi^-0.5)."""
+        cfg = self.cfg
+        b = cfg.batch
+        if kv is not None:
+            slots = self._slot_base + self.positions % cfg.window
+            quant.pack_latent_fp8_b128(kv, rope=cfg.rope, out=self.win.view(-1, self.win.shape[-1]), dst_index=slots)
+        pos = self.positions.view(b, 1)
+        if cfg.index_format == "fp8":
+            codes, scales = quant.quant_fp8_block(q_idx.view(b, 1, cfg.index_heads, cfg.index_dim), cfg.index_dim)
+            indexer.scores_fp8(codes, scales[..., 0], w.view(b, 1, -1), self.k_codes, self.k_scales,
+                               compress_ratio=cfg.ratio, positions=pos, out=self.scores)
+        else:
+            packed, e8 = quant.quant_mxfp4(q_idx.view(b, 1, cfg.index_heads, cfg.index_dim))
+            indexer.scores_mxfp4(packed, e8, w.view(b, 1, -1), self.k_packed, self.k_e8m0,
+                                 compress_ratio=cfg.ratio, positions=pos, out=self.scores)
+        indexer.topk(self.scores.view(b, cfg.max_groups), cfg.topk, out=self.idx)
+        csa2_attn.sparse_mqa_decode(q, self.positions, self.win, cfg.window, main_cache=self.main,
+                                    groups=cfg.max_groups, indices=self.idx, dense_cache=self.coarse,
+                                    dense_ratio=max(cfg.coarse_ratio, 1), sinks=self.sinks, nsplit=cfg.nsplit,
+                                    nope=cfg.nope, workspace=self.workspace, out=self.out, lse=self.lse)
+        if advance:
+            self.positions.add_(1)
+        return self.out
+
+    def capture(self, q, kv, q_idx, w, advance: bool = False, warmup: int = 2) -> torch.cuda.CUDAGraph:
+        """Record ``step`` into a HIP graph over static copies of the inputs; ``replay``
+        then reruns it after the caller writes new inputs into ``static_inputs``."""
+        self._static = tuple(None if t is None else t.clone() for t in (q, kv, q_idx, w))
+        s = torch.cuda.Stream(device=self.device)
+        s.wait_stream(torch.cuda.current_stream(self.device))
+        saved = self.positions.clone()
+        with torch.cuda.stream(s):
+            for _ in range(warmup):
+                self.step(*self._static, advance=False)
+        torch.cuda.current_stream(self.device).wait_stream(s)
+        self.positions.copy_(saved)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.step(*self._static, advance=advance)
+        self._graph = g
+        return g
+
+    @property
+    def static_inputs(self):
+        return self._static
+
+    def replay(self) -> torch.Tensor:
+        self._graph.replay()
+        return self.out

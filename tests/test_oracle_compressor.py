@@ -1,0 +1,113 @@
+"""CPU: pin the compressor / RMSNorm / RoPE oracle (oracle/compressor.py).
+
+The oracle fixes the float32 evaluation order that torch leaves implementation-defined;
+these checks show it still computes the reference's functions:
+* ``exp_f32`` within 2 ulp of float64 ``exp`` over the softmax range (and exact at 0);
+* ``softmax_pool`` within a few ulp of the reference expression evaluated by torch's own
+  ``softmax`` (``owlet1/cache.py:171``), plus closed forms: a one-hot gate returns that
+  token's kv exactly, a constant gate returns the mean;
+* ``rms_norm`` within a few ulp of torch's ``x * rsqrt(mean(x^2) + eps)``; a constant
+  vector normalises to +-weight;
+* ``rope``: position 0 is the identity, inverse after forward restores x, and the
+  rotation preserves each pair's norm;
+* ``split_groups``: the carry invariant of ``store_compression_weights``.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import compressor as C
+from oracle import quant as Q
+
+
+def _ulps(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return np.abs(a - b) / np.spacing(np.abs(b).astype(np.float32)).astype(np.float64)
+
+
+def test_exp_accuracy():
+    x = np.concatenate([-np.random.default_rng(0).exponential(6, 2_000_000),
+                        np.linspace(-103, 0, 100001), [0.0, -0.0]]).astype(np.float32)
+    got = C.exp_f32(x)
+    ref = np.exp(x.astype(np.float64))
+    normal = ref >= 2.0 ** -126
+    assert _ulps(got[normal], ref[normal]).max() <= 2.0
+    assert np.all(np.abs(got[~normal] - ref[~normal]) <= 2.0 ** -149)
+    assert C.exp_f32(np.float32(0.0)) == 1.0
+    assert C.exp_f32(np.float32(-np.inf)) == 0.0
+
+
+def test_softmax_pool_matches_torch_softmax():
+    rng = np.random.default_rng(1)
+    kv = rng.standard_normal((4, 64, 4, 576)).astype(np.float32)
+    gate = (rng.standard_normal((4, 64, 4, 576)) * 3).astype(np.float32)
+    got = C.softmax_pool(kv, gate)
+    t_kv, t_g = torch.from_numpy(kv), torch.from_numpy(gate)
+    ref = (t_kv * t_g.softmax(dim=2, dtype=torch.float32)).sum(dim=2).numpy()   # cache.py:171
+    err = np.abs(got.astype(np.float64) - ref)
+    scale = np.abs(kv).max(axis=2)
+    assert (err / scale).max() < 4 * 2.0 ** -23
+
+
+def test_softmax_pool_closed_forms():
+    rng = np.random.default_rng(2)
+    kv = rng.standard_normal((3, 5, 4, 32)).astype(np.float32)
+    onehot = np.full((3, 5, 4, 32), -200.0, np.float32)
+    onehot[:, :, 2, :] = 0.0
+    assert np.array_equal(C.softmax_pool(kv, onehot), kv[:, :, 2, :])
+    const = np.zeros((3, 5, 4, 32), np.float32)
+    mean = ((kv[:, :, 0] + kv[:, :, 1]) + kv[:, :, 2] + kv[:, :, 3]) * np.float32(0.25)
+    assert np.allclose(C.softmax_pool(kv, const), mean, rtol=0, atol=4e-7 * np.abs(kv).max())
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_rms_norm_matches_torch(dtype):
+    rng = np.random.default_rng(3)
+    x = Q.round_to(rng.standard_normal((256, 576)).astype(np.float32) * 3, dtype)
+    w = Q.round_to(rng.uniform(0.5, 1.5, 576).astype(np.float32), dtype)
+    got = C.rms_norm(x, w, 1e-20, dtype)
+    tdt = torch.float32 if dtype == "float32" else torch.bfloat16
+    h = torch.from_numpy(x).float()
+    ref = (torch.from_numpy(w).to(tdt) * (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + 1e-20)).to(tdt)).float()
+    ulp = 2.0 ** -23 if dtype == "float32" else 2.0 ** -8
+    assert np.max(np.abs(got - ref.numpy()) / np.maximum(np.abs(ref.numpy()), 1e-30)) <= 4 * ulp
+
+
+def test_rms_norm_constant_vector():
+    x = np.full((2, 160), -3.0, np.float32)
+    w = np.linspace(0.5, 2, 160).astype(np.float32)
+    got = C.rms_norm(x, w, 1e-20, "float32")
+    assert np.allclose(got, -w, rtol=2e-7, atol=0)
+
+
+def test_compress_ratio1_is_plain_norm():
+    rng = np.random.default_rng(4)
+    kv = rng.standard_normal((2, 8, 160)).astype(np.float32)
+    w = np.ones(160, np.float32)
+    assert np.array_equal(C.compress(kv, None, 1, w, 1e-6, "float32"), C.rms_norm(kv, w, 1e-6, "float32"))
+
+
+def test_rope_identities():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((2, 7, 4, 160)).astype(np.float32)
+    cos0, sin0 = C.rope_tables(np.zeros((2, 7)), 32, 160000.0)
+    assert np.array_equal(C.rope(x, cos0[:, :, None], sin0[:, :, None]), x)
+    cos, sin = C.rope_tables(rng.integers(0, 100000, (2, 7)), 32, 160000.0)
+    y = C.rope(x, cos[:, :, None], sin[:, :, None])
+    back = C.rope(y, cos[:, :, None], sin[:, :, None], inverse=True)
+    assert np.allclose(back, x, atol=1e-5)
+    assert np.array_equal(y[..., :128], x[..., :128])
+    n_in = x[..., 128::2] ** 2 + x[..., 129::2] ** 2
+    n_out = y[..., 128::2] ** 2 + y[..., 129::2] ** 2
+    assert np.allclose(n_in, n_out, rtol=1e-5)
+
+
+def test_split_groups_carry():
+    buffered, emitted, ratio = 0, 0, 4
+    for new in [5, 1, 1, 1, 9, 0, 3]:
+        usable, buffered = C.split_groups(buffered, new, ratio)
+        assert usable % ratio == 0 and 0 <= buffered < ratio
+        emitted += usable // ratio
+    assert emitted == (5 + 1 + 1 + 1 + 9 + 0 + 3) // ratio
