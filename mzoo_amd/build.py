@@ -6,6 +6,8 @@ library.  Flags:
 * ``--offload-arch=gfx950``: MI355X only, no other targets.
 * ``-ffp-contract=off``: no implicit fused multiply-adds, so the kernels evaluate
   exactly the float32 operation sequence they spell out (fused steps use ``fmaf``).
+* ``-fhip-fp32-correctly-rounded-divide-sqrt``: fp32 ``/`` and ``sqrt`` are the
+  correctly rounded IEEE operations (the compressor's bit-exact RMSNorm relies on it).
 * ``-Xclang -target-feature -Xclang -packed-fp32-ops`` disables the packed fp32
   instructions (v_pk_*_f32), keeping every float32 op scalar.
 * ``-fgpu-flush-denormals-to-zero`` is NOT given: fp32 denormals are kept.
@@ -30,6 +32,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 COMMON = [
     "-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950", "-ffp-contract=off",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result", "-I", str(ROOT.parent / "include"),
 ]

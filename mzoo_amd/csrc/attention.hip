@@ -19,13 +19,14 @@
 // Tiling (MI355X): one workgroup = one (row, split, group of <= 64 heads); HG x DS waves,
 // HG = head groups of 32 (the MFMA N axis), DS = number of D-parts (2 when D > 256, so a
 // wave's q fragments + O^T accumulators fit one SIMD's registers).  Per 32-entry tile:
-//   1. the tile is loaded from HBM, dequantized to bf16 and written to LDS twice:
-//      Kt[entry][d] (QK operand) and Vt[d][entry'] (PV operand, entries permuted into the
-//      order the MFMA result registers hold them, so P never leaves VGPRs);
+//   1. the tile (fetched from HBM into registers while the previous tile computed) is
+//      dequantized to bf16 into LDS, Kt[entry][d];
 //   2. S^T[32 entries x 32 heads] = Kt . Q^T on v_mfma_f32_32x32x16_bf16, each wave over its
 //      D-part, partial sums exchanged through LDS (fixed order: part 0 + part 1);
 //   3. online softmax in the exp2 domain, lane-local per head (lane l holds head l%32);
-//   4. O^T[d x 32 heads] += Vt . P^T on MFMA, each wave owning its D-part of O.
+//   4. O^T[d x 32 heads] += V^T . P^T on MFMA, each wave owning its D-part of O: P^T stays
+//      in the registers the S^T result left it in, and the V^T operand is gathered from
+//      Kt columns in the matching entry order.
 // The workgroup writes either the final bf16 output + lse (one split) or fp32 partials
 // (unnormalized O, running max m, sum l) that mzk combine kernel merges with the sink.
 #include "common.h"
@@ -82,44 +83,56 @@ struct Layout {
   static constexpr int kChunks = D / 8;  // 8-channel chunks per entry
 };
 
-// Permuted position (within a 32-entry tile) at which entry n is stored in a Vt row, so
-// that lane half `h` of PV step `ks` reads its 8 k-slots as one 16-byte load.  The MFMA
-// result (S^T) holds in register j of lane l the entry 8*(j/4) + 4*(l/32) + j%4; PV step
-// ks consumes registers 8ks..8ks+7.
-__device__ __forceinline__ int vt_pos(int n) {
-  const int blk = n >> 4, r = n & 15;
-  return blk * 16 + ((r >> 2) & 1) * 8 + (r >> 3) * 4 + (r & 3);
-}
-
+// Entry held by register j of lane l in a 32x32 MFMA result: 8*(j/4) + 4*(l/32) + j%4.
 __device__ __forceinline__ int c_entry(int j, int lane) { return 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3); }
 
-// 8 consecutive channels of one entry -> 8 bf16 (as 4 dwords).
+// Raw bytes of one 8-channel chunk of an entry, fetched from HBM ahead of use.
+struct RawChunk {
+  uint4 v;   // bf16: 8 channels; fp8 nope: .x/.y = 8 codes; fp8 rope: 8 bf16
+  float s;   // fp8 nope: the chunk's 128-channel block scale
+};
+
 template <int FMT, int D, int NOPE>
-__device__ __forceinline__ uint4 load_chunk(const uint8_t* e, int c) {
+__device__ __forceinline__ RawChunk fetch_chunk(const uint8_t* e, int c) {
+  RawChunk r;
+  r.s = 1.0f;
   if constexpr (FMT == kFmtBf16) {
-    return *reinterpret_cast<const uint4*>(e + 16 * c);
+    r.v = *reinterpret_cast<const uint4*>(e + 16 * c);
   } else {
     constexpr int NB = NOPE / 128;
     if (c < NOPE / 8) {
       const uint2 raw = *reinterpret_cast<const uint2*>(e + 8 * c);
-      const float s = reinterpret_cast<const float*>(e + NOPE)[c >> 4];
-      uint32_t w[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t word = i < 2 ? raw.x : raw.y;
-        const uint32_t c0 = (word >> (16 * (i & 1))) & 0xffu;
-        const uint32_t c1 = (word >> (16 * (i & 1) + 8)) & 0xffu;
-        // exact: e4m3 (4 significant bits) * pow2 scale has 16 zero low bits in fp32
-        const float f0 = __uint_as_float((c0 & 0x7fu) << 20) * 1.329227995784916e+36f * s;
-        const float f1 = __uint_as_float((c1 & 0x7fu) << 20) * 1.329227995784916e+36f * s;
-        const uint32_t b0 = (__float_as_uint(f0) >> 16) | ((c0 & 0x80u) << 8);
-        const uint32_t b1 = (__float_as_uint(f1) >> 16) | ((c1 & 0x80u) << 8);
-        w[i] = b0 | (b1 << 16);
-      }
-      return uint4{w[0], w[1], w[2], w[3]};
+      r.v = uint4{raw.x, raw.y, 0u, 0u};
+      r.s = reinterpret_cast<const float*>(e + NOPE)[c >> 4];
     } else {
-      return *reinterpret_cast<const uint4*>(e + NOPE + 4 * NB + 16 * (c - NOPE / 8));
+      r.v = *reinterpret_cast<const uint4*>(e + NOPE + 4 * NB + 16 * (c - NOPE / 8));
     }
+  }
+  return r;
+}
+
+// 8 bf16 (as 4 dwords) of a fetched chunk.  e4m3 * pow2 scale is exact in bf16: the
+// 7 magnitude bits are placed at the fp32 exponent/mantissa boundary, rescaled by 2^120
+// (exact for normals and subnormals) and by the block scale.
+template <int FMT, int NOPE>
+__device__ __forceinline__ uint4 decode_chunk(const RawChunk& r, int c) {
+  if constexpr (FMT == kFmtBf16) {
+    return r.v;
+  } else {
+    if (c >= NOPE / 8) return r.v;
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t word = i < 2 ? r.v.x : r.v.y;
+      const uint32_t c0 = (word >> (16 * (i & 1))) & 0xffu;
+      const uint32_t c1 = (word >> (16 * (i & 1) + 8)) & 0xffu;
+      const float f0 = __uint_as_float((c0 & 0x7fu) << 20) * 1.329227995784916e+36f * r.s;
+      const float f1 = __uint_as_float((c1 & 0x7fu) << 20) * 1.329227995784916e+36f * r.s;
+      const uint32_t b0 = (__float_as_uint(f0) >> 16) | ((c0 & 0x80u) << 8);
+      const uint32_t b1 = (__float_as_uint(f1) >> 16) | ((c1 & 0x80u) << 8);
+      w[i] = b0 | (b1 << 16);
+    }
+    return uint4{w[0], w[1], w[2], w[3]};
   }
 }
 
@@ -127,20 +140,20 @@ template <int FMT, int D, int NOPE, int HG, int DS>
 __global__ void __launch_bounds__(HG * DS * 64) sparse_mqa_kernel(const AttnParams p) {
   using L = Layout<FMT, D, NOPE>;
   constexpr int NT = HG * DS * 64;
-  constexpr int DPART = D / DS;          // channels per D-part
-  constexpr int QSTEPS = DPART / 16;     // QK MFMA steps per wave
-  constexpr int NDB = DPART / 32;        // 32-channel blocks of O per wave
-  constexpr int KT_PITCH = 2 * D + 16;   // bytes per Kt row
-  constexpr int VT_PITCH = 2 * kTile + 16;  // bytes per Vt row
+  constexpr int DPART = D / DS;           // channels per D-part
+  constexpr int QSTEPS = DPART / 16;      // QK MFMA steps per wave
+  constexpr int NDB = DPART / 32;         // 32-channel blocks of O per wave
+  constexpr int KT_PITCH = 2 * D + 16;    // bytes per Kt row (16 B pad spreads LDS banks)
+  constexpr int TPE = NT / kTile;         // threads per entry in the load/dequant phase
+  constexpr int CPT = (L::kChunks + TPE - 1) / TPE;  // chunks per thread
   static_assert(DPART % 32 == 0, "D-part must be a multiple of 32 channels");
+  static_assert(NT % kTile == 0, "whole threads per entry");
 
   extern __shared__ __align__(16) uint8_t smem[];
-  uint8_t* kt = smem;                                   // [32][KT_PITCH]
-  uint8_t* vt = kt + kTile * KT_PITCH;                  // [D][VT_PITCH]
-  float* sx = reinterpret_cast<float*>(vt + D * VT_PITCH);  // [waves][64][16] (DS > 1)
-  __shared__ const uint8_t* tab_ptr[kTile];
-  __shared__ int tab_valid[kTile];
-  __shared__ uint32_t tab_mask;
+  uint8_t* kt = smem;                                         // [32][KT_PITCH] bf16 tile
+  float* sx = reinterpret_cast<float*>(kt + kTile * KT_PITCH);  // [waves][16][64] partial S
+  __shared__ const uint8_t* tab_ptr[2][kTile];
+  __shared__ uint32_t tab_mask[2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -167,8 +180,48 @@ __global__ void __launch_bounds__(HG * DS * 64) sparse_mqa_kernel(const AttnPara
   const int64_t v_begin = split * chunk;
   const int64_t v_end = v_begin + chunk < total ? v_begin + chunk : total;
 
-  // ---- q fragments (B operand of S^T = K Q^T): head hg*32 + lane%32, channels of this
-  // wave's D-part, 8 per lane per step
+  const uint8_t* win_b = p.win ? p.win + b * p.win_batch_entries * L::kEntryBytes : nullptr;
+  const uint8_t* dense_b = p.dense ? p.dense + b * p.dense_batch_entries * L::kEntryBytes : nullptr;
+  const uint8_t* main_b = p.main ? p.main + b * p.main_batch_entries * L::kEntryBytes : nullptr;
+  const int32_t* idx_row = p.idx ? p.idx + row * p.idx_row_stride : nullptr;
+
+  // entry table of the tile starting at virtual index t0 (threads 0..31)
+  auto build_table = [&](int64_t t0, int buf) {
+    if (tid < kTile) {
+      const int64_t v = t0 + tid;
+      const uint8_t* ptr = nullptr;
+      if (v < v_end) {
+        if (v < nw) {
+          const int64_t tok = pos - nw + 1 + v;
+          ptr = win_b + (p.win_cap ? tok % p.win_cap : tok) * L::kEntryBytes;
+        } else if (v < nw + nd) {
+          ptr = dense_b + (v - nw) * L::kEntryBytes;
+        } else {
+          const int64_t g = idx_row[v - nw - nd];
+          if (g >= 0 && g < p.G) ptr = main_b + g * L::kEntryBytes;
+        }
+      }
+      tab_ptr[buf][tid] = ptr;
+      const uint64_t bal = __ballot(ptr != nullptr);
+      if (tid == 0) tab_mask[buf] = static_cast<uint32_t>(bal);
+    }
+  };
+  // load phase: thread owns entry tid / TPE, chunks (tid % TPE) + TPE*k
+  const int my_entry = tid / TPE;
+  const int my_c0 = tid % TPE;
+  RawChunk raw[CPT];
+  auto fetch_tile = [&](int buf) {
+    const uint8_t* e = tab_ptr[buf][my_entry];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int c = my_c0 + TPE * k;
+      raw[k].v = uint4{0u, 0u, 0u, 0u};
+      raw[k].s = 1.0f;
+      if (e != nullptr && c < L::kChunks) raw[k] = fetch_chunk<FMT, D, NOPE>(e, c);
+    }
+  };
+
+  // ---- q fragments (B operand of S^T = K Q^T): head, channels of this wave's D-part
   const int head = blockIdx.z * (HG * 32) + hg * 32 + (lane & 31);
   const bool head_ok = head < p.H;
   v8bf qf[QSTEPS];
@@ -187,73 +240,34 @@ __global__ void __launch_bounds__(HG * DS * 64) sparse_mqa_kernel(const AttnPara
   float m_run = -__builtin_huge_valf();
   float l_run = 0.0f;
 
-  const uint8_t* win_b = p.win ? p.win + b * p.win_batch_entries * L::kEntryBytes : nullptr;
-  const uint8_t* dense_b = p.dense ? p.dense + b * p.dense_batch_entries * L::kEntryBytes : nullptr;
-  const uint8_t* main_b = p.main ? p.main + b * p.main_batch_entries * L::kEntryBytes : nullptr;
-  const int32_t* idx_row = p.idx ? p.idx + row * p.idx_row_stride : nullptr;
+  int buf = 0;
+  if (v_begin < v_end) {
+    build_table(v_begin, 0);
+    __syncthreads();
+    fetch_tile(0);
+  }
 
 #pragma unroll 1
   for (int64_t t0 = v_begin; t0 < v_end; t0 += kTile) {
-    // 1a. entry table
-    if (tid < kTile) {
-      const int64_t v = t0 + tid;
-      const uint8_t* ptr = nullptr;
-      int valid = 0;
-      if (v < v_end) {
-        if (v < nw) {
-          const int64_t tok = pos - nw + 1 + v;
-          const int64_t slot = p.win_cap ? tok % p.win_cap : tok;
-          ptr = win_b + slot * L::kEntryBytes;
-          valid = 1;
-        } else if (v < nw + nd) {
-          ptr = dense_b + (v - nw) * L::kEntryBytes;
-          valid = 1;
-        } else {
-          const int64_t g = idx_row[v - nw - nd];
-          if (g >= 0 && g < p.G) {
-            ptr = main_b + g * L::kEntryBytes;
-            valid = 1;
-          }
-        }
-      }
-      tab_ptr[tid] = ptr;
-      tab_valid[tid] = valid;
-      const uint64_t bal = __ballot(valid);
-      if (tid == 0) tab_mask = static_cast<uint32_t>(bal);
-    }
-    __syncthreads();
-
-    // 1b. load + dequantize: item = (entry pair, 8-channel chunk)
-    for (int item = tid; item < (kTile / 2) * L::kChunks; item += NT) {
-      const int pr = item / L::kChunks;
-      const int c = item - pr * L::kChunks;
-      const int n0 = 2 * pr;
-      uint4 v0 = uint4{0, 0, 0, 0}, v1 = uint4{0, 0, 0, 0};
-      if (tab_valid[n0]) v0 = load_chunk<FMT, D, NOPE>(tab_ptr[n0], c);
-      if (tab_valid[n0 + 1]) v1 = load_chunk<FMT, D, NOPE>(tab_ptr[n0 + 1], c);
-      *reinterpret_cast<uint4*>(kt + n0 * KT_PITCH + 16 * c) = v0;
-      *reinterpret_cast<uint4*>(kt + (n0 + 1) * KT_PITCH + 16 * c) = v1;
-      // Vt: entries n0, n0+1 sit at adjacent positions (same group of 4) -> one dword
-      const int vp = vt_pos(n0);
-      const uint32_t a0[4] = {v0.x, v0.y, v0.z, v0.w};
-      const uint32_t a1[4] = {v1.x, v1.y, v1.z, v1.w};
+    // 1. dequantize the fetched tile into Kt; publish the next tile's entry table
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t lo = (a0[i] & 0xffffu) | (a1[i] << 16);
-        const uint32_t hi = (a0[i] >> 16) | (a1[i] & 0xffff0000u);
-        *reinterpret_cast<uint32_t*>(vt + (8 * c + 2 * i) * VT_PITCH + 2 * vp) = lo;
-        *reinterpret_cast<uint32_t*>(vt + (8 * c + 2 * i + 1) * VT_PITCH + 2 * vp) = hi;
-      }
+    for (int k = 0; k < CPT; ++k) {
+      const int c = my_c0 + TPE * k;
+      if (c < L::kChunks)
+        *reinterpret_cast<uint4*>(kt + my_entry * KT_PITCH + 16 * c) = decode_chunk<FMT, NOPE>(raw[k], c);
     }
+    const bool has_next = t0 + kTile < v_end;
+    if (has_next) build_table(t0 + kTile, buf ^ 1);
     __syncthreads();
+    // 2. next tile's HBM reads overlap this tile's MFMA work
+    if (has_next) fetch_tile(buf ^ 1);
 
-    // 2. S^T partial over this wave's D-part
+    // 3. S^T partial over this wave's D-part
     v16f s = v16f{};
     {
       const uint8_t* krow = kt + (lane & 31) * KT_PITCH + 2 * (ds * DPART + half * 8);
       if constexpr (DS == 1) {
-        // two independent accumulation chains (even / odd K-steps), summed in that order
-        v16f s1 = v16f{};
+        v16f s1 = v16f{};  // two independent chains (even / odd K-steps), summed in that order
 #pragma unroll
         for (int st = 0; st < QSTEPS; ++st) {
           const uint4 kv = *reinterpret_cast<const uint4*>(krow + 32 * st);
@@ -269,25 +283,23 @@ __global__ void __launch_bounds__(HG * DS * 64) sparse_mqa_kernel(const AttnPara
           const v8bf ka = __builtin_bit_cast(v8bf, v4i{(int)kv.x, (int)kv.y, (int)kv.z, (int)kv.w});
           s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[st], s, 0, 0, 0);
         }
-        // partial S of each D-part through LDS, summed in D-part order by every wave
-        float* mine = sx + (wave * 64 + lane) * 16;
+        // partial S of each D-part through LDS ([wave][j][lane], conflict-free), summed in
+        // D-part order by every wave of the head group
 #pragma unroll
-        for (int j = 0; j < 16; ++j) mine[j] = s[j];
+        for (int j = 0; j < 16; ++j) sx[(wave * 16 + j) * 64 + lane] = s[j];
         __syncthreads();
-        const float* p0 = sx + ((hg * DS) * 64 + lane) * 16;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) s[j] = p0[j];
+        for (int j = 0; j < 16; ++j) s[j] = sx[((hg * DS) * 16 + j) * 64 + lane];
 #pragma unroll
         for (int part = 1; part < DS; ++part) {
-          const float* pp = sx + ((hg * DS + part) * 64 + lane) * 16;
 #pragma unroll
-          for (int j = 0; j < 16; ++j) s[j] = s[j] + pp[j];
+          for (int j = 0; j < 16; ++j) s[j] = s[j] + sx[((hg * DS + part) * 16 + j) * 64 + lane];
         }
       }
     }
 
-    // 3. online softmax (exp2 domain), lane-local per head
-    const uint32_t vmask = tab_mask;
+    // 4. online softmax (exp2 domain), lane-local per head
+    const uint32_t vmask = tab_mask[buf];
     float tmax = -__builtin_huge_valf();
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
@@ -318,27 +330,40 @@ __global__ void __launch_bounds__(HG * DS * 64) sparse_mqa_kernel(const AttnPara
 #pragma unroll
     for (int i = 0; i < NDB; ++i) acc_o[i] = acc_o[i] * alpha;
 
-    // 4. O^T += Vt . P^T
+    // 5. O^T += V^T . P^T.  P^T is the S^T result in registers: PV step ks consumes
+    // registers 8ks..8ks+7 = entries 16ks + {0..3, 8..11} + 4*half.  The matching V^T
+    // k-slots are gathered from Kt column d with 16-bit LDS reads (lanes 0-31 and 32-63
+    // read rows 4 apart: disjoint banks).
     const v8bf pf0 = __builtin_bit_cast(v8bf, v4i{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]});
     const v8bf pf1 = __builtin_bit_cast(v8bf, v4i{(int)pk[4], (int)pk[5], (int)pk[6], (int)pk[7]});
     {
-      const uint8_t* vrow = vt + (ds * DPART + (lane & 31)) * VT_PITCH + 2 * (half * 8);
+      const uint16_t* vcol = reinterpret_cast<const uint16_t*>(kt + (4 * half) * KT_PITCH) +
+                             (ds * DPART + (lane & 31));
+      constexpr int RP = KT_PITCH / 2;  // row pitch in bf16 elements
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        const uint4 a0 = *reinterpret_cast<const uint4*>(vrow + db * 32 * VT_PITCH);
-        const uint4 a1 = *reinterpret_cast<const uint4*>(vrow + db * 32 * VT_PITCH + 32);
+        const uint16_t* vc = vcol + db * 32;
+        uint32_t a[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // ks = 0: entries {0,1,2,3} + 8*(i/2) ... packed two per dword
+          const int n0 = (2 * i < 4 ? 2 * i : 2 * i + 4);
+          a[i] = static_cast<uint32_t>(vc[n0 * RP]) | (static_cast<uint32_t>(vc[(n0 + 1) * RP]) << 16);
+          a[4 + i] = static_cast<uint32_t>(vc[(16 + n0) * RP]) | (static_cast<uint32_t>(vc[(17 + n0) * RP]) << 16);
+        }
         acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            __builtin_bit_cast(v8bf, v4i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w}), pf0, acc_o[db], 0, 0, 0);
+            __builtin_bit_cast(v8bf, v4i{(int)a[0], (int)a[1], (int)a[2], (int)a[3]}), pf0, acc_o[db], 0, 0, 0);
         acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            __builtin_bit_cast(v8bf, v4i{(int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w}), pf1, acc_o[db], 0, 0, 0);
+            __builtin_bit_cast(v8bf, v4i{(int)a[4], (int)a[5], (int)a[6], (int)a[7]}), pf1, acc_o[db], 0, 0, 0);
       }
     }
+    buf ^= 1;
     __syncthreads();
   }
 
   // ---- epilogue.  acc_o[db][j] holds O^T[d][head], d = ds*DPART + db*32 + c_entry(j, lane)
   if (!head_ok) return;
-  if (p.nsplit == 1) {
+  if (p.out != nullptr && p.nsplit == 1) {
     float m_fin = m_run, l_fin = l_run, o_scale;
     if (p.sinks) {
       const float sk = p.sinks[head] * kLog2e;
@@ -430,7 +455,7 @@ __global__ void __launch_bounds__(64) combine_kernel(const float* __restrict__ p
 template <int FMT, int D, int NOPE, int HG, int DS>
 int launch_attn(const AttnParams& p, int64_t rows, hipStream_t s) {
   constexpr int NT = HG * DS * 64;
-  constexpr size_t lds = static_cast<size_t>(kTile) * (2 * D + 16) + static_cast<size_t>(D) * (2 * kTile + 16) +
+  constexpr size_t lds = static_cast<size_t>(kTile) * (2 * D + 16) +
                          (DS > 1 ? static_cast<size_t>(HG * DS) * 64 * 16 * 4 : 0);
   static_assert(lds <= 150 * 1024, "LDS budget");
   auto kern = sparse_mqa_kernel<FMT, D, NOPE, HG, DS>;

@@ -83,6 +83,13 @@ __device__ __forceinline__ uint16_t f32_to_f16(float f) {
   return static_cast<uint16_t>(h | sign);
 }
 
+// Correctly rounded fp32 square root and division.  (HIP's __fsqrt_rn is the ~1 ulp
+// hardware v_sqrt_f32 unless OCML_BASIC_ROUNDED_OPERATIONS is defined; the plain
+// operators are correctly rounded under -fhip-fp32-correctly-rounded-divide-sqrt,
+// which the build passes explicitly.)
+__device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
+__device__ __forceinline__ float div_rn(float a, float b) { return a / b; }
+
 // Load element i of a tensor of the given dtype as fp32.
 template <int DT>
 __device__ __forceinline__ float load_as_f32(const void* p, int64_t i) {

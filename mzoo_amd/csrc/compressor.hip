@@ -80,7 +80,7 @@ __global__ void __launch_bounds__(256) compress_kernel(const float* __restrict__
         float acc = 0.0f;
         for (int r = 0; r < ratio; ++r) {
           const float e = exp_pinned(gtb[static_cast<int64_t>(r) * D + d] - m);
-          acc = acc + kvb[static_cast<int64_t>(r) * D + d] * __fdiv_rn(e, s);
+          acc = acc + kvb[static_cast<int64_t>(r) * D + d] * div_rn(e, s);
         }
         v = acc;
       }
@@ -92,10 +92,8 @@ __global__ void __launch_bounds__(256) compress_kernel(const float* __restrict__
   // xor butterfly: every lane ends with the same total
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) ss = ss + __shfl_xor(ss, m, 64);
-  const float var = __fdiv_rn(ss, static_cast<float>(D));
-  const float inv = __fdiv_rn(1.0f, __fsqrt_rn(var + eps));
-  float* of = nullptr;
-  (void)of;
+  const float var = div_rn(ss, static_cast<float>(D));
+  const float inv = div_rn(1.0f, sqrt_rn(var + eps));
 #pragma unroll
   for (int i = 0; i < kMaxPerLane; ++i) {
     const int d = lane + 64 * i;

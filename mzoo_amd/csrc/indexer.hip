@@ -111,7 +111,7 @@ indexer_scores_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q
   int64_t vis = (pos + 1) / ratio;
   if (vis > G) vis = G;
   if (vis < 0) vis = 0;
-  const float inv_sqrt_di = 1.0f / __fsqrt_rn(static_cast<float>(DI));
+  const float inv_sqrt_di = 1.0f / sqrt_rn(static_cast<float>(DI));
 
   // A fragments (queries) and per-head coefficients, resident for the whole workgroup
   Frag a[MB][NST];

@@ -22,7 +22,7 @@ __device__ __forceinline__ float fp8_scale_from_amax(float amax) {
 }
 
 __device__ __forceinline__ float fp4_scale_from_amax(float amax, bool e4m3_scales) {
-  if (e4m3_scales) return e4m3_decode(e4m3_encode(__fdiv_rn(fmaxf(amax, 0x1.8p-7f /* 6*2^-9 */), 6.0f)));
+  if (e4m3_scales) return e4m3_decode(e4m3_encode(div_rn(fmaxf(amax, 0x1.8p-7f /* 6*2^-9 */), 6.0f)));
   return pow2_ceil(fmaxf(amax, 0x1.8p-124f /* 6*2^-126 */) * kInv6);
 }
 
@@ -45,14 +45,14 @@ __global__ void fake_quant_kernel(const void* __restrict__ x, void* __restrict__
     const float s = fp4_scale_from_amax(amax, e4m3_scales);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t c = e2m1_code(clampf(__fdiv_rn(v[i], s), 6.0f));
+      const uint32_t c = e2m1_code(clampf(div_rn(v[i], s), 6.0f));
       store_from_f32<DT>(y, base + i, e2m1_value(c) * s);
     }
   } else {
     const float s = fp8_scale_from_amax(amax);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t c = e4m3_encode(clampf(__fdiv_rn(v[i], s), 448.0f));
+      const uint32_t c = e4m3_encode(clampf(div_rn(v[i], s), 448.0f));
       store_from_f32<DT>(y, base + i, e4m3_decode(c) * s);
     }
   }
@@ -71,8 +71,8 @@ __global__ void fake_quant_serial_kernel(const void* __restrict__ x, void* __res
   for (int i = 0; i < bs; ++i) {
     const float v = load_as_f32<DT>(x, base + i);
     float r;
-    if constexpr (FP4) r = e2m1_value(e2m1_code(clampf(__fdiv_rn(v, s), 6.0f))) * s;
-    else r = e4m3_decode(e4m3_encode(clampf(__fdiv_rn(v, s), 448.0f))) * s;
+    if constexpr (FP4) r = e2m1_value(e2m1_code(clampf(div_rn(v, s), 6.0f))) * s;
+    else r = e4m3_decode(e4m3_encode(clampf(div_rn(v, s), 448.0f))) * s;
     store_from_f32<DT>(y, base + i, r);
   }
 }
@@ -93,7 +93,7 @@ __global__ void quant_fp8_block_kernel(const void* __restrict__ x, uint8_t* __re
   const float s = fp8_scale_from_amax(amax);
   uint32_t word = 0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) word |= static_cast<uint32_t>(e4m3_encode(clampf(__fdiv_rn(v[i], s), 448.0f))) << (8 * i);
+  for (int i = 0; i < 4; ++i) word |= static_cast<uint32_t>(e4m3_encode(clampf(div_rn(v[i], s), 448.0f))) << (8 * i);
   reinterpret_cast<uint32_t*>(codes)[t] = word;
   if ((t % group) == 0) scales[t / group] = s;
 }
@@ -112,7 +112,7 @@ __global__ void quant_mxfp4_kernel(const void* __restrict__ x, uint8_t* __restri
   const float s = fp4_scale_from_amax(amax, false);
   uint32_t c[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) c[i] = e2m1_code(clampf(__fdiv_rn(v[i], s), 6.0f));
+  for (int i = 0; i < 4; ++i) c[i] = e2m1_code(clampf(div_rn(v[i], s), 6.0f));
   const uint16_t two = static_cast<uint16_t>(c[0] | (c[1] << 4) | (c[2] << 8) | (c[3] << 12));
   reinterpret_cast<uint16_t*>(packed)[t] = two;
   if ((t & 7) == 0) e8m0[t >> 3] = static_cast<uint8_t>(__float_as_uint(s) >> 23);
@@ -163,7 +163,7 @@ __global__ void pack_latent_kernel(const void* __restrict__ x, int nope, int rop
     const float s = fp8_scale_from_amax(amax);
     uint32_t word = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) word |= static_cast<uint32_t>(e4m3_encode(clampf(__fdiv_rn(v[i], s), 448.0f))) << (8 * i);
+    for (int i = 0; i < 4; ++i) word |= static_cast<uint32_t>(e4m3_encode(clampf(div_rn(v[i], s), 448.0f))) << (8 * i);
     reinterpret_cast<uint32_t*>(e)[t] = word;
     if ((t & 31) == 0) reinterpret_cast<float*>(e + nope)[t >> 5] = s;
   }
