@@ -111,28 +111,15 @@ __device__ __forceinline__ RawChunk fetch_chunk(const uint8_t* e, int c) {
   return r;
 }
 
-// 8 bf16 (as 4 dwords) of a fetched chunk.  e4m3 * pow2 scale is exact in bf16: the
-// 7 magnitude bits are placed at the fp32 exponent/mantissa boundary, rescaled by 2^120
-// (exact for normals and subnormals) and by the block scale.
+// 8 bf16 (as 4 dwords) of a fetched chunk: e4m3 codes times the pow2 block scale through
+// the hardware conversion (exact in bf16), rope / bf16 chunks as they are.
 template <int FMT, int NOPE>
 __device__ __forceinline__ uint4 decode_chunk(const RawChunk& r, int c) {
   if constexpr (FMT == kFmtBf16) {
     return r.v;
   } else {
     if (c >= NOPE / 8) return r.v;
-    uint32_t w[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t word = i < 2 ? r.v.x : r.v.y;
-      const uint32_t c0 = (word >> (16 * (i & 1))) & 0xffu;
-      const uint32_t c1 = (word >> (16 * (i & 1) + 8)) & 0xffu;
-      const float f0 = __uint_as_float((c0 & 0x7fu) << 20) * 1.329227995784916e+36f * r.s;
-      const float f1 = __uint_as_float((c1 & 0x7fu) << 20) * 1.329227995784916e+36f * r.s;
-      const uint32_t b0 = (__float_as_uint(f0) >> 16) | ((c0 & 0x80u) << 8);
-      const uint32_t b1 = (__float_as_uint(f1) >> 16) | ((c1 & 0x80u) << 8);
-      w[i] = b0 | (b1 << 16);
-    }
-    return uint4{w[0], w[1], w[2], w[3]};
+    return dequant_fp8x8_bf16(uint2{r.v.x, r.v.y}, r.s);
   }
 }
 
@@ -298,7 +285,10 @@ __global__ void __launch_bounds__(HG * DS * 64) sparse_mqa_kernel(const AttnPara
       }
     }
 
-    // 4. online softmax (exp2 domain), lane-local per head
+    // 4. online softmax (exp2 domain), lane-local per head.  The running max is only
+    // raised when a head's tile max exceeds it by more than kLazy (log2 units): until then
+    // exp2(s - m) <= 2^kLazy stays exact enough in fp32/bf16 and O needs no rescale.  The
+    // decision is wave-uniform, so most tiles skip the O^T *= alpha pass.
     const uint32_t vmask = tab_mask[buf];
     float tmax = -__builtin_huge_valf();
 #pragma unroll
@@ -307,28 +297,27 @@ __global__ void __launch_bounds__(HG * DS * 64) sparse_mqa_kernel(const AttnPara
       tmax = fmaxf(tmax, s[j]);
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);
-    float alpha = 1.0f;
+    constexpr float kLazy = 8.0f;
+    const bool raise = tmax > m_run + kLazy;
+    if (__any(raise)) {
+      const float m_new = raise ? tmax : m_run;
+      const float alpha = (m_run == -__builtin_huge_valf()) ? 0.0f : exp2f(m_run - m_new);
+      l_run = l_run * alpha;
+#pragma unroll
+      for (int i = 0; i < NDB; ++i) acc_o[i] = acc_o[i] * alpha;
+      m_run = m_new;
+    }
     float psum = 0.0f;
     uint32_t pk[8];
-    if (m_new == -__builtin_huge_valf()) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) pk[i] = 0u;
-    } else {
-      alpha = exp2f(m_run - m_new);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float p0 = exp2f(s[2 * i] - m_new);
-        const float p1 = exp2f(s[2 * i + 1] - m_new);
-        psum = psum + p0 + p1;
-        pk[i] = static_cast<uint32_t>(f32_to_bf16(p0)) | (static_cast<uint32_t>(f32_to_bf16(p1)) << 16);
-      }
+    for (int i = 0; i < 8; ++i) {
+      const float p0 = s[2 * i] == -__builtin_huge_valf() ? 0.0f : exp2f(s[2 * i] - m_run);
+      const float p1 = s[2 * i + 1] == -__builtin_huge_valf() ? 0.0f : exp2f(s[2 * i + 1] - m_run);
+      psum = psum + p0 + p1;
+      pk[i] = pack_bf16x2(p0, p1);
     }
     psum = psum + __shfl_xor(psum, 32, 64);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int i = 0; i < NDB; ++i) acc_o[i] = acc_o[i] * alpha;
+    l_run = l_run + psum;
 
     // 5. O^T += V^T . P^T.  P^T is the S^T result in registers: PV step ks consumes
     // registers 8ks..8ks+7 = entries 16ks + {0..3, 8..11} + 4*half.  The matching V^T

@@ -177,6 +177,29 @@ __device__ __forceinline__ float e2m1_value(uint32_t code) {
 }
 
 // ------------------------------------------------------------------------------------
+// gfx950 hardware conversions
+// ------------------------------------------------------------------------------------
+typedef __bf16 mzk_v2bf __attribute__((ext_vector_type(2)));
+
+// 8 e4m3 codes (little-endian in `raw`) times a power-of-two `scale` -> 8 bf16 (as 4
+// dwords, element 2i in the low half of dword i), with v_cvt_scalef32_pk_bf16_fp8.  Exact:
+// an e4m3 value has 4 significant bits, so code * 2^k is representable in bf16.
+__device__ __forceinline__ uint4 dequant_fp8x8_bf16(uint2 raw, float scale) {
+  const mzk_v2bf a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(static_cast<int>(raw.x), scale, false);
+  const mzk_v2bf b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(static_cast<int>(raw.x), scale, true);
+  const mzk_v2bf c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(static_cast<int>(raw.y), scale, false);
+  const mzk_v2bf d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(static_cast<int>(raw.y), scale, true);
+  return uint4{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b), __builtin_bit_cast(uint32_t, c),
+               __builtin_bit_cast(uint32_t, d)};
+}
+
+// Two fp32 -> packed bf16x2 (round to nearest even) with v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const mzk_v2bf v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// ------------------------------------------------------------------------------------
 // wave helpers (wave64)
 // ------------------------------------------------------------------------------------
 __device__ __forceinline__ float wave_max_group(float v, int group) {

@@ -179,11 +179,28 @@ __global__ void unpack_latent_kernel(const uint8_t* __restrict__ cache, int nope
   const int nb = nope / 128;
   const uint8_t* e = cache + row * static_cast<int64_t>(nope + 4 * nb + 2 * rope);
   const int64_t yrow = row * d;
-  if (t < nope / 4) {
-    const uint32_t word = reinterpret_cast<const uint32_t*>(e)[t];
-    const float s = reinterpret_cast<const float*>(e + nope)[t >> 5];
+  if constexpr (DT == MZK_BF16) {
+    // 8 channels per thread through the hardware e4m3 -> bf16 conversion (the same
+    // routine the attention kernel dequantizes its tiles with)
+    if (t < nope / 8) {
+      const uint2 raw = reinterpret_cast<const uint2*>(e)[t];
+      const float s = reinterpret_cast<const float*>(e + nope)[t >> 4];
+      const uint4 v = dequant_fp8x8_bf16(raw, s);
+      uint16_t* yy = static_cast<uint16_t*>(y) + yrow + 8 * t;
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) store_from_f32<DT>(y, yrow + 4 * t + i, e4m3_decode((word >> (8 * i)) & 0xffu) * s);
+      for (int i = 0; i < 4; ++i) {
+        yy[2 * i] = static_cast<uint16_t>(w[i] & 0xffffu);
+        yy[2 * i + 1] = static_cast<uint16_t>(w[i] >> 16);
+      }
+    }
+  } else {
+    if (t < nope / 4) {
+      const uint32_t word = reinterpret_cast<const uint32_t*>(e)[t];
+      const float s = reinterpret_cast<const float*>(e + nope)[t >> 5];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) store_from_f32<DT>(y, yrow + 4 * t + i, e4m3_decode((word >> (8 * i)) & 0xffu) * s);
+    }
   }
   const uint16_t* r = reinterpret_cast<const uint16_t*>(e + nope + 4 * nb);
   for (int i = t; i < rope; i += blockDim.x) store_from_f32<DT>(y, yrow + nope + i, bf16_to_f32(r[i]));

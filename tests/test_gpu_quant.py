@@ -103,3 +103,22 @@ def test_small_model_dims(dev):
     e = MQ.pack_latent_fp8_b128(x.to(dev), rope=32)
     assert e.shape == (64, 128 + 4 + 64)
     assert np.array_equal(e.cpu().numpy(), Q.pack_latent_fp8_b128(x.numpy(), nope=128))
+
+
+def test_unpack_bf16_all_codes_and_scales(dev):
+    """The bf16 unpack runs the hardware e4m3 -> bf16 conversion the attention kernel
+    dequantizes with: every code (0..255) under scales 2^-40 .. 2^20 must decode to the
+    oracle's value exactly (NaN codes to NaN)."""
+    rows = 16
+    rng = np.random.default_rng(0)
+    e = np.zeros((rows, 656), np.uint8)
+    for r in range(rows):
+        e[r, :512] = (np.arange(512) + 37 * r) % 256
+        sc = np.array([2.0 ** (-40 + 4 * r), 2.0 ** -7, 1.0, 2.0 ** (r % 21)], np.float32)
+        e[r, 512:528] = sc.view(np.uint8)
+        e[r, 528:] = Q.bf16_bits(rng.standard_normal(64).astype(np.float32)).view(np.uint8)
+    got = MQ.unpack_latent_fp8_b128(torch.from_numpy(e).to(dev), dtype=torch.bfloat16).cpu()
+    want = torch.from_numpy(Q.unpack_latent_fp8_b128(e)).bfloat16()
+    gnan, wnan = torch.isnan(got.float()), torch.isnan(want.float())
+    assert torch.equal(gnan, wnan)
+    assert torch.equal(got[~gnan].view(torch.int16), want[~wnan].view(torch.int16))
