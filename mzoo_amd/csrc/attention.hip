@@ -37,8 +37,14 @@ namespace {
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef short v8s __attribute__((ext_vector_type(8)));
 
 enum { kFmtBf16 = 0, kFmtFp8 = 1 };
+
+__device__ __forceinline__ __attribute__((address_space(3))) v4s* lds_v4s(const uint8_t* p) {
+  return (__attribute__((address_space(3))) v4s*)(p);
+}
 
 constexpr int kTile = 32;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -86,26 +92,44 @@ struct Layout {
 // Entry held by register j of lane l in a 32x32 MFMA result: 8*(j/4) + 4*(l/32) + j%4.
 __device__ __forceinline__ int c_entry(int j, int lane) { return 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3); }
 
-// Raw bytes of one 8-channel chunk of an entry, fetched from HBM ahead of use.
+// Workgroup barrier that waits only for this wave's LDS operations (not for vector
+// memory: the tile DMA stays in flight across it).  The "memory" clobber keeps the
+// compiler from moving memory accesses across.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory"); }
+
+constexpr int kIdxCap = 4096;  // sparse indices of one split staged in LDS
+
+typedef const uint8_t __attribute__((address_space(1)))* gptr_t;  // global (not flat) loads
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+template <typename T>
+__device__ __forceinline__ T gload(gptr_t p) {
+  return *(const __attribute__((address_space(1))) T*)(p);
+}
+
+// Raw bytes of one 8-channel chunk of an entry, fetched from HBM a tile ahead of use.
 struct RawChunk {
   uint4 v;   // bf16: 8 channels; fp8 nope: .x/.y = 8 codes; fp8 rope: 8 bf16
   float s;   // fp8 nope: the chunk's 128-channel block scale
 };
 
 template <int FMT, int D, int NOPE>
-__device__ __forceinline__ RawChunk fetch_chunk(const uint8_t* e, int c) {
+__device__ __forceinline__ RawChunk fetch_chunk(gptr_t e, int c) {
   RawChunk r;
   r.s = 1.0f;
   if constexpr (FMT == kFmtBf16) {
-    r.v = *reinterpret_cast<const uint4*>(e + 16 * c);
+    const u32x4 v = gload<u32x4>(e + 16 * c);
+    r.v = uint4{v.x, v.y, v.z, v.w};
   } else {
     constexpr int NB = NOPE / 128;
     if (c < NOPE / 8) {
-      const uint2 raw = *reinterpret_cast<const uint2*>(e + 8 * c);
+      const u32x2 raw = gload<u32x2>(e + 8 * c);
       r.v = uint4{raw.x, raw.y, 0u, 0u};
-      r.s = reinterpret_cast<const float*>(e + NOPE)[c >> 4];
+      r.s = gload<float>(e + NOPE + 4 * (c >> 4));
     } else {
-      r.v = *reinterpret_cast<const uint4*>(e + NOPE + 4 * NB + 16 * (c - NOPE / 8));
+      const u32x4 v = gload<u32x4>(e + NOPE + 4 * NB + 16 * (c - NOPE / 8));
+      r.v = uint4{v.x, v.y, v.z, v.w};
     }
   }
   return r;
@@ -124,23 +148,32 @@ __device__ __forceinline__ uint4 decode_chunk(const RawChunk& r, int c) {
 }
 
 template <int FMT, int D, int NOPE, int HG, int DS>
+struct Smem {
+  static constexpr int KT = kTile * (2 * D + 16);
+  static constexpr int SX = DS > 1 ? HG * DS * 16 * 64 * 4 : 0;
+  static constexpr int LDS = KT + SX;
+};
+
+template <int FMT, int D, int NOPE, int HG, int DS>
 __global__ void __launch_bounds__(HG * DS * 64) sparse_mqa_kernel(const AttnParams p) {
   using L = Layout<FMT, D, NOPE>;
+  using M = Smem<FMT, D, NOPE, HG, DS>;
   constexpr int NT = HG * DS * 64;
   constexpr int DPART = D / DS;           // channels per D-part
   constexpr int QSTEPS = DPART / 16;      // QK MFMA steps per wave
   constexpr int NDB = DPART / 32;         // 32-channel blocks of O per wave
   constexpr int KT_PITCH = 2 * D + 16;    // bytes per Kt row (16 B pad spreads LDS banks)
+  constexpr int NTAB = 2;                 // entry tables: current and next tile
   constexpr int TPE = NT / kTile;         // threads per entry in the load/dequant phase
   constexpr int CPT = (L::kChunks + TPE - 1) / TPE;  // chunks per thread
   static_assert(DPART % 32 == 0, "D-part must be a multiple of 32 channels");
-  static_assert(NT % kTile == 0, "whole threads per entry");
 
   extern __shared__ __align__(16) uint8_t smem[];
-  uint8_t* kt = smem;                                         // [32][KT_PITCH] bf16 tile
-  float* sx = reinterpret_cast<float*>(kt + kTile * KT_PITCH);  // [waves][16][64] partial S
-  __shared__ const uint8_t* tab_ptr[2][kTile];
-  __shared__ uint32_t tab_mask[2];
+  uint8_t* kt = smem;                                           // [32][KT_PITCH] bf16 tile
+  float* sx = reinterpret_cast<float*>(kt + M::KT);             // [waves][16][64] partial S
+  __shared__ const uint8_t* tab_ptr[NTAB][kTile];
+  __shared__ uint32_t tab_mask[NTAB];
+  __shared__ int32_t sidx[kIdxCap];  // this split's sparse indices
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -166,16 +199,26 @@ __global__ void __launch_bounds__(HG * DS * 64) sparse_mqa_kernel(const AttnPara
   chunk = (chunk + kTile - 1) / kTile * kTile;
   const int64_t v_begin = split * chunk;
   const int64_t v_end = v_begin + chunk < total ? v_begin + chunk : total;
+  const int ntiles = v_end > v_begin ? static_cast<int>((v_end - v_begin + kTile - 1) / kTile) : 0;
 
-  const uint8_t* win_b = p.win ? p.win + b * p.win_batch_entries * L::kEntryBytes : nullptr;
+  const uint8_t* win_b = p.win + b * p.win_batch_entries * L::kEntryBytes;
   const uint8_t* dense_b = p.dense ? p.dense + b * p.dense_batch_entries * L::kEntryBytes : nullptr;
   const uint8_t* main_b = p.main ? p.main + b * p.main_batch_entries * L::kEntryBytes : nullptr;
   const int32_t* idx_row = p.idx ? p.idx + row * p.idx_row_stride : nullptr;
 
-  // entry table of the tile starting at virtual index t0 (threads 0..31)
-  auto build_table = [&](int64_t t0, int buf) {
+  // this split's slice of the sparse index list, staged in LDS once (the host guarantees
+  // it fits kIdxCap), so the tile loop issues no vector-memory reads besides the tile DMA
+  const int64_t sp_begin = v_begin > nw + nd ? v_begin - nw - nd : 0;
+  const int64_t sp_end = v_end > nw + nd ? v_end - nw - nd : 0;
+  for (int64_t s = sp_begin + tid; s < sp_end; s += NT) sidx[s - sp_begin] = idx_row[s];
+  __syncthreads();  // the slice is read by other threads below
+  auto load_slot = [&](int64_t v) -> int64_t {
+    return (v >= nw + nd && v < v_end) ? static_cast<int64_t>(sidx[v - nw - nd - sp_begin]) : -1;
+  };
+  // entry table of tile `t` (threads 0..31); `g` = this thread's prefetched sparse index
+  auto build_table = [&](int t, int64_t g) {
     if (tid < kTile) {
-      const int64_t v = t0 + tid;
+      const int64_t v = v_begin + static_cast<int64_t>(t) * kTile + tid;
       const uint8_t* ptr = nullptr;
       if (v < v_end) {
         if (v < nw) {
@@ -183,22 +226,22 @@ __global__ void __launch_bounds__(HG * DS * 64) sparse_mqa_kernel(const AttnPara
           ptr = win_b + (p.win_cap ? tok % p.win_cap : tok) * L::kEntryBytes;
         } else if (v < nw + nd) {
           ptr = dense_b + (v - nw) * L::kEntryBytes;
-        } else {
-          const int64_t g = idx_row[v - nw - nd];
-          if (g >= 0 && g < p.G) ptr = main_b + g * L::kEntryBytes;
+        } else if (g >= 0 && g < p.G) {
+          ptr = main_b + g * L::kEntryBytes;
         }
       }
-      tab_ptr[buf][tid] = ptr;
+      tab_ptr[t % NTAB][tid] = ptr;
       const uint64_t bal = __ballot(ptr != nullptr);
-      if (tid == 0) tab_mask[buf] = static_cast<uint32_t>(bal);
+      if (tid == 0) tab_mask[t % NTAB] = static_cast<uint32_t>(bal);
     }
   };
-  // load phase: thread owns entry tid / TPE, chunks (tid % TPE) + TPE*k
+  // load phase: thread owns entry tid / TPE, 8-channel chunks (tid % TPE) + TPE*k; the
+  // next tile's chunks are fetched into registers while the current tile computes
   const int my_entry = tid / TPE;
   const int my_c0 = tid % TPE;
   RawChunk raw[CPT];
-  auto fetch_tile = [&](int buf) {
-    const uint8_t* e = tab_ptr[buf][my_entry];
+  auto fetch_tile = [&](int t) {
+    const gptr_t e = (gptr_t)(tab_ptr[t % NTAB][my_entry]);
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int c = my_c0 + TPE * k;
@@ -227,27 +270,33 @@ __global__ void __launch_bounds__(HG * DS * 64) sparse_mqa_kernel(const AttnPara
   float m_run = -__builtin_huge_valf();
   float l_run = 0.0f;
 
-  int buf = 0;
-  if (v_begin < v_end) {
-    build_table(v_begin, 0);
+  int64_t g_pref = -1;  // prefetched sparse index for table t+2 (threads 0..31)
+  if (ntiles > 0) {
+    build_table(0, tid < kTile ? load_slot(v_begin + tid) : -1);
+    build_table(1, tid < kTile ? load_slot(v_begin + kTile + tid) : -1);
+    if (tid < kTile) g_pref = load_slot(v_begin + 2 * kTile + tid);
     __syncthreads();
     fetch_tile(0);
   }
 
 #pragma unroll 1
-  for (int64_t t0 = v_begin; t0 < v_end; t0 += kTile) {
-    // 1. dequantize the fetched tile into Kt; publish the next tile's entry table
+  for (int t = 0; t < ntiles; ++t) {
+    const int tb = t % NTAB;
+    // 1. dequantize the fetched tile into Kt (empty slots are zero); the table of tile
+    //    t+2 replaces tile t's (no longer read: the softmax below uses its mask copy)
+    const uint32_t vmask = tab_mask[tb];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int c = my_c0 + TPE * k;
       if (c < L::kChunks)
         *reinterpret_cast<uint4*>(kt + my_entry * KT_PITCH + 16 * c) = decode_chunk<FMT, NOPE>(raw[k], c);
     }
-    const bool has_next = t0 + kTile < v_end;
-    if (has_next) build_table(t0 + kTile, buf ^ 1);
-    __syncthreads();
-    // 2. next tile's HBM reads overlap this tile's MFMA work
-    if (has_next) fetch_tile(buf ^ 1);
+    lds_barrier();  // Kt complete; every wave has read tile t's table
+    build_table(t + 2, g_pref);
+    if (tid < kTile) g_pref = load_slot(v_begin + static_cast<int64_t>(t + 3) * kTile + tid);
+    // 2. the next tile's HBM reads overlap this tile's MFMA work (stays in flight across
+    //    the LDS-only barriers below)
+    if (t + 1 < ntiles) fetch_tile(t + 1);
 
     // 3. S^T partial over this wave's D-part
     v16f s = v16f{};
@@ -274,7 +323,7 @@ __global__ void __launch_bounds__(HG * DS * 64) sparse_mqa_kernel(const AttnPara
         // D-part order by every wave of the head group
 #pragma unroll
         for (int j = 0; j < 16; ++j) sx[(wave * 16 + j) * 64 + lane] = s[j];
-        __syncthreads();
+        lds_barrier();
 #pragma unroll
         for (int j = 0; j < 16; ++j) s[j] = sx[((hg * DS) * 16 + j) * 64 + lane];
 #pragma unroll
@@ -289,7 +338,6 @@ __global__ void __launch_bounds__(HG * DS * 64) sparse_mqa_kernel(const AttnPara
     // raised when a head's tile max exceeds it by more than kLazy (log2 units): until then
     // exp2(s - m) <= 2^kLazy stays exact enough in fp32/bf16 and O needs no rescale.  The
     // decision is wave-uniform, so most tiles skip the O^T *= alpha pass.
-    const uint32_t vmask = tab_mask[buf];
     float tmax = -__builtin_huge_valf();
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
@@ -301,7 +349,7 @@ __global__ void __launch_bounds__(HG * DS * 64) sparse_mqa_kernel(const AttnPara
     const bool raise = tmax > m_run + kLazy;
     if (__any(raise)) {
       const float m_new = raise ? tmax : m_run;
-      const float alpha = (m_run == -__builtin_huge_valf()) ? 0.0f : exp2f(m_run - m_new);
+      const float alpha = (m_run == -__builtin_huge_valf()) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
       l_run = l_run * alpha;
 #pragma unroll
       for (int i = 0; i < NDB; ++i) acc_o[i] = acc_o[i] * alpha;
@@ -311,8 +359,9 @@ __global__ void __launch_bounds__(HG * DS * 64) sparse_mqa_kernel(const AttnPara
     uint32_t pk[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float p0 = s[2 * i] == -__builtin_huge_valf() ? 0.0f : exp2f(s[2 * i] - m_run);
-      const float p1 = s[2 * i + 1] == -__builtin_huge_valf() ? 0.0f : exp2f(s[2 * i + 1] - m_run);
+      // v_exp_f32 directly: arguments are <= kLazy, results below 2^-126 may flush to 0
+      const float p0 = s[2 * i] == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f(s[2 * i] - m_run);
+      const float p1 = s[2 * i + 1] == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f(s[2 * i + 1] - m_run);
       psum = psum + p0 + p1;
       pk[i] = pack_bf16x2(p0, p1);
     }
@@ -321,33 +370,33 @@ __global__ void __launch_bounds__(HG * DS * 64) sparse_mqa_kernel(const AttnPara
 
     // 5. O^T += V^T . P^T.  P^T is the S^T result in registers: PV step ks consumes
     // registers 8ks..8ks+7 = entries 16ks + {0..3, 8..11} + 4*half.  The matching V^T
-    // k-slots are gathered from Kt column d with 16-bit LDS reads (lanes 0-31 and 32-63
-    // read rows 4 apart: disjoint banks).
+    // operand (32 channels x 8 entries) comes from Kt with ds_read_b64_tr_b16: inside a
+    // 16-lane group, lane i receives element i%4 of the 4-element rows the lanes
+    // 4k + i/4 (k = 0..3) point at.  Lane j therefore points at
+    // Kt[e0 + j/4][d0 + 4*(j%4)] and receives Kt[e0 + k][d0 + i] for k = 0..3:
+    // four consecutive entries of its own channel, two reads per fragment.
     const v8bf pf0 = __builtin_bit_cast(v8bf, v4i{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]});
     const v8bf pf1 = __builtin_bit_cast(v8bf, v4i{(int)pk[4], (int)pk[5], (int)pk[6], (int)pk[7]});
     {
-      const uint16_t* vcol = reinterpret_cast<const uint16_t*>(kt + (4 * half) * KT_PITCH) +
-                             (ds * DPART + (lane & 31));
-      constexpr int RP = KT_PITCH / 2;  // row pitch in bf16 elements
+      const int grp = lane >> 4;  // 16-lane group: channel half (grp & 1), entry half (grp >> 1)
+      const int j = lane & 15;
+      const int e0 = 4 * (grp >> 1) + (j >> 2);
+      const int dcol = ds * DPART + 16 * (grp & 1) + 4 * (j & 3);
+      const uint8_t* tr0 = kt + e0 * KT_PITCH + 2 * dcol;
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        const uint16_t* vc = vcol + db * 32;
-        uint32_t a[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          // ks = 0: entries {0,1,2,3} + 8*(i/2) ... packed two per dword
-          const int n0 = (2 * i < 4 ? 2 * i : 2 * i + 4);
-          a[i] = static_cast<uint32_t>(vc[n0 * RP]) | (static_cast<uint32_t>(vc[(n0 + 1) * RP]) << 16);
-          a[4 + i] = static_cast<uint32_t>(vc[(16 + n0) * RP]) | (static_cast<uint32_t>(vc[(17 + n0) * RP]) << 16);
-        }
-        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            __builtin_bit_cast(v8bf, v4i{(int)a[0], (int)a[1], (int)a[2], (int)a[3]}), pf0, acc_o[db], 0, 0, 0);
-        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            __builtin_bit_cast(v8bf, v4i{(int)a[4], (int)a[5], (int)a[6], (int)a[7]}), pf1, acc_o[db], 0, 0, 0);
+        const uint8_t* tp = tr0 + 64 * db;
+        const v4s r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4s(tp));                     // entries 0-3 (+4h)
+        const v4s r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4s(tp + 8 * KT_PITCH));      // entries 8-11
+        const v4s r2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4s(tp + 16 * KT_PITCH));     // entries 16-19
+        const v4s r3 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4s(tp + 24 * KT_PITCH));     // entries 24-27
+        const v8bf a0 = __builtin_bit_cast(v8bf, v8s{r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]});
+        const v8bf a1 = __builtin_bit_cast(v8bf, v8s{r2[0], r2[1], r2[2], r2[3], r3[0], r3[1], r3[2], r3[3]});
+        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, pf0, acc_o[db], 0, 0, 0);
+        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, pf1, acc_o[db], 0, 0, 0);
       }
     }
-    buf ^= 1;
-    __syncthreads();
+    lds_barrier();  // Kt and the S exchange buffer are free for the next tile
   }
 
   // ---- epilogue.  acc_o[db][j] holds O^T[d][head], d = ds*DPART + db*32 + c_entry(j, lane)
@@ -444,8 +493,7 @@ __global__ void __launch_bounds__(64) combine_kernel(const float* __restrict__ p
 template <int FMT, int D, int NOPE, int HG, int DS>
 int launch_attn(const AttnParams& p, int64_t rows, hipStream_t s) {
   constexpr int NT = HG * DS * 64;
-  constexpr size_t lds = static_cast<size_t>(kTile) * (2 * D + 16) +
-                         (DS > 1 ? static_cast<size_t>(HG * DS) * 64 * 16 * 4 : 0);
+  constexpr size_t lds = Smem<FMT, D, NOPE, HG, DS>::LDS;
   static_assert(lds <= 150 * 1024, "LDS budget");
   auto kern = sparse_mqa_kernel<FMT, D, NOPE, HG, DS>;
   static bool attr_set = false;
@@ -523,6 +571,12 @@ extern "C" int mzk_sparse_mqa(const void* q, int64_t B, int64_t S, int H, int D,
   MZK_CHECK_ARG(q && positions && (nsplit > 1 || (out && lse)), "sparse_mqa: null pointer");
   MZK_CHECK_ARG((out == nullptr) == (lse == nullptr), "sparse_mqa: out and lse go together");
   MZK_CHECK_ARG(rows <= 0x7fffffff, "sparse_mqa: too many rows");
+  {
+    const int64_t total_max = static_cast<int64_t>(window) + (dense ? dense_cap : 0) + (main_kv ? topk : 0);
+    const int64_t chunk = ((total_max + nsplit - 1) / nsplit + 31) / 32 * 32;
+    MZK_CHECK_ARG(chunk <= kIdxCap, "sparse_mqa: %lld entries per split exceed %d; use nsplit >= %lld",
+                  (long long)chunk, kIdxCap, (long long)((total_max + kIdxCap - 33) / (kIdxCap - 32)));
+  }
   if (nsplit > 1) {
     const int64_t need = rows * nsplit * static_cast<int64_t>(H) * (D + 2) * 4;
     MZK_CHECK_ARG(workspace && workspace_bytes >= need, "sparse_mqa: workspace needs %lld bytes", (long long)need);
