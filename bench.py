@@ -44,6 +44,10 @@ def parse():
     ap.add_argument("--nsplit", type=int, default=4)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline time budget")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--stage-iters", type=int, default=0, help="launches per stage timing (0: max(steps, 50))")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (3 launches): the reference kernel "
+                         "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
     return ap.parse_args()
 
 
@@ -158,7 +162,7 @@ def cpu_baseline(torch, layer, inputs, budget_s):
 
 def traffic_from_profiles(kernel: str):
     """HBM bytes per launch of `kernel` from the committed PMC summary, if one exists."""
-    f = ROOT / "profiles" / "sparse_mqa_decode_c2_pmc.md"
+    f = ROOT / "profiles" / "decode_step_c2_hbm_traffic.md"
     if not f.exists():
         return None
     m = re.search(rf"{kernel}\s+traffic_bytes_per_launch\s*=\s*([0-9.eE+]+)", f.read_text())
@@ -174,6 +178,14 @@ def main():
     import torch
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_mib:
+        src = torch.ones(args.copy_mib << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4}))
+        return
     layer, inputs, _ = build_layer(torch, dev, args.nsplit)
     cfg = layer.cfg
     layer.capture(*inputs, advance=False)
@@ -188,7 +200,7 @@ def main():
     ms = elapsed / args.steps * 1e3
     tokens_per_s = cfg.batch / (ms / 1e3)
 
-    stages = stage_times(torch, layer, inputs, max(args.steps, 50))
+    stages = stage_times(torch, layer, inputs, args.stage_iters or max(args.steps, 50))
     # algorithmic work per launch
     rows = cfg.batch
     entries = cfg.window + cfg.topk
