@@ -97,15 +97,13 @@ def stage_times(torch, layer, inputs, iters):
     ws = layer.workspace
     st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
 
-    def attn_partial():
+    def attn():
+        # split-KV attention and the split merge, as in the step
         _lib.call("mzk_sparse_mqa", q.data_ptr(), b, 1, cfg.heads, cfg.dim, 1, cfg.nope, layer.positions.data_ptr(),
                   layer.win.data_ptr(), cfg.window, cfg.window, cfg.window, None, 0, 0, 1, layer.main.data_ptr(),
                   cfg.max_groups, cfg.max_groups, layer.idx.data_ptr(), cfg.topk, cfg.topk,
-                  layer.sinks.data_ptr(), cfg.nsplit, ws.data_ptr(), ws.numel() * 4, None, None, st())
-
-    def attn_combine():
-        _lib.call("mzk_sparse_mqa_combine", ws.data_ptr(), b, 1, cfg.heads, cfg.dim, cfg.nsplit,
-                  layer.sinks.data_ptr(), layer.out.data_ptr(), layer.lse.data_ptr(), st())
+                  layer.sinks.data_ptr(), cfg.nsplit, ws.data_ptr(), ws.numel() * 4, layer.out.data_ptr(),
+                  layer.lse.data_ptr(), st())
 
     stages = {
         "window_append": lambda: quant.pack_latent_fp8_b128(kv, out=layer.win.view(-1, layer.win.shape[-1]),
@@ -115,8 +113,7 @@ def stage_times(torch, layer, inputs, iters):
                                                          layer.k_scales, compress_ratio=cfg.ratio, positions=pos,
                                                          out=layer.scores),
         "topk": lambda: indexer.topk(layer.scores.view(b, cfg.max_groups), cfg.topk, out=layer.idx),
-        "sparse_mqa": attn_partial,
-        "sparse_mqa_combine": attn_combine,
+        "sparse_mqa": attn,
     }
     return {k: time_launches(torch, f, iters) for k, f in stages.items()}
 

@@ -28,7 +28,13 @@ FMT_BF16, FMT_FP8 = 0, 1
 
 
 def workspace_bytes(rows: int, heads: int, dim: int, nsplit: int) -> int:
+    """Split-KV workspace: the fp32 partials (O, m, l) of every split."""
     return 0 if nsplit <= 1 else rows * nsplit * heads * (dim + 2) * 4
+
+
+def new_workspace(rows: int, heads: int, dim: int, nsplit: int, device) -> torch.Tensor:
+    """A split-KV workspace for ``sparse_mqa_decode`` (zero-filled)."""
+    return torch.zeros(max(workspace_bytes(rows, heads, dim, nsplit) // 4, 1), dtype=torch.float32, device=device)
 
 
 def fwd(q: torch.Tensor, kv: torch.Tensor, main_kv: torch.Tensor, indices: torch.Tensor, *, window: int,
@@ -94,7 +100,7 @@ def sparse_mqa_decode(q: torch.Tensor, positions: torch.Tensor, win_cache: torch
         lse = torch.empty(b, h, dtype=torch.float32, device=q.device)
     need = workspace_bytes(b, h, d, nsplit)
     if nsplit > 1 and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = torch.empty(need // 4, dtype=torch.float32, device=q.device)
+        workspace = new_workspace(b, h, d, nsplit, q.device)
     topk = 0 if indices is None else indices.shape[-1]
     _lib.call("mzk_sparse_mqa", q.data_ptr(), b, 1, h, d, FMT_FP8, nope, positions.data_ptr(),
               win_cache.data_ptr(), win_cache.shape[1], win_cache.shape[1], window,

@@ -35,6 +35,7 @@ namespace mzk {
 namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef short v4s __attribute__((ext_vector_type(4)));
@@ -52,6 +53,7 @@ constexpr float kLn2 = 0.6931471805599453f;
 
 struct AttnParams {
   const uint16_t* q;  // [rows, H, D] bf16
+  int64_t rows;       // B * S
   int64_t S;          // rows per batch: row = b * S + s
   const int64_t* positions;  // [rows] absolute position of each row
   // window source
@@ -86,322 +88,245 @@ struct AttnParams {
 template <int FMT, int D, int NOPE>
 struct Layout {
   static constexpr int kEntryBytes = FMT == kFmtFp8 ? NOPE + 4 * (NOPE / 128) + 2 * (D - NOPE) : 2 * D;
-  static constexpr int kChunks = D / 8;  // 8-channel chunks per entry
+  // An entry is fetched as 16-byte pieces: fp8 = NOPE/16 code pieces (16 e4m3 codes each)
+  // followed by (D-NOPE)/8 rope pieces (8 bf16 each); bf16 = D/8 pieces of 8 channels.
+  static constexpr int kCodePieces = FMT == kFmtFp8 ? NOPE / 16 : 0;
+  static constexpr int kPieces = FMT == kFmtFp8 ? NOPE / 16 + (D - NOPE) / 8 : D / 8;
 };
 
 // Entry held by register j of lane l in a 32x32 MFMA result: 8*(j/4) + 4*(l/32) + j%4.
 __device__ __forceinline__ int c_entry(int j, int lane) { return 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3); }
 
 // Workgroup barrier that waits only for this wave's LDS operations (not for vector
-// memory: the tile DMA stays in flight across it).  The "memory" clobber keeps the
-// compiler from moving memory accesses across.
+// memory: the next tile's loads stay in flight across it).  The "memory" clobber keeps
+// the compiler from moving memory accesses across.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory"); }
 
 constexpr int kIdxCap = 4096;  // sparse indices of one split staged in LDS
 
 typedef const uint8_t __attribute__((address_space(1)))* gptr_t;  // global (not flat) loads
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 template <typename T>
 __device__ __forceinline__ T gload(gptr_t p) {
   return *(const __attribute__((address_space(1))) T*)(p);
 }
 
-// Raw bytes of one 8-channel chunk of an entry, fetched from HBM a tile ahead of use.
-struct RawChunk {
-  uint4 v;   // bf16: 8 channels; fp8 nope: .x/.y = 8 codes; fp8 rope: 8 bf16
-  float s;   // fp8 nope: the chunk's 128-channel block scale
+// One fetched 16-byte piece of an entry (held in registers a tile ahead of use).
+struct Piece {
+  u32x4 v;  // fp8 code piece: 16 codes; rope / bf16 piece: 8 bf16
+  float s;  // fp8 code piece: its 128-channel block scale
 };
 
 template <int FMT, int D, int NOPE>
-__device__ __forceinline__ RawChunk fetch_chunk(gptr_t e, int c) {
-  RawChunk r;
+__device__ __forceinline__ Piece fetch_piece(gptr_t e, int q) {
+  using L = Layout<FMT, D, NOPE>;
+  Piece r;
   r.s = 1.0f;
-  if constexpr (FMT == kFmtBf16) {
-    const u32x4 v = gload<u32x4>(e + 16 * c);
-    r.v = uint4{v.x, v.y, v.z, v.w};
-  } else {
+  if constexpr (FMT == kFmtFp8) {
     constexpr int NB = NOPE / 128;
-    if (c < NOPE / 8) {
-      const u32x2 raw = gload<u32x2>(e + 8 * c);
-      r.v = uint4{raw.x, raw.y, 0u, 0u};
-      r.s = gload<float>(e + NOPE + 4 * (c >> 4));
+    if (q < L::kCodePieces) {
+      r.v = gload<u32x4>(e + 16 * q);
+      r.s = gload<float>(e + NOPE + 4 * (q >> 3));
     } else {
-      const u32x4 v = gload<u32x4>(e + NOPE + 4 * NB + 16 * (c - NOPE / 8));
-      r.v = uint4{v.x, v.y, v.z, v.w};
+      r.v = gload<u32x4>(e + NOPE + 4 * NB + 16 * (q - L::kCodePieces));
     }
+  } else {
+    r.v = gload<u32x4>(e + 16 * q);
   }
   return r;
 }
 
-// 8 bf16 (as 4 dwords) of a fetched chunk: e4m3 codes times the pow2 block scale through
-// the hardware conversion (exact in bf16), rope / bf16 chunks as they are.
-template <int FMT, int NOPE>
-__device__ __forceinline__ uint4 decode_chunk(const RawChunk& r, int c) {
-  if constexpr (FMT == kFmtBf16) {
-    return r.v;
+// Writes piece q of an entry to its bf16 row in LDS: e4m3 codes times the pow2 block scale
+// through the hardware conversion (exact in bf16); rope / bf16 pieces as they are.
+template <int FMT, int D, int NOPE>
+__device__ __forceinline__ void store_piece(uint8_t* krow, const Piece& r, int q) {
+  using L = Layout<FMT, D, NOPE>;
+  if constexpr (FMT == kFmtFp8) {
+    if (q < L::kCodePieces) {
+      *reinterpret_cast<uint4*>(krow + 32 * q) = dequant_fp8x8_bf16(uint2{r.v.x, r.v.y}, r.s);
+      *reinterpret_cast<uint4*>(krow + 32 * q + 16) = dequant_fp8x8_bf16(uint2{r.v.z, r.v.w}, r.s);
+    } else {
+      *reinterpret_cast<uint4*>(krow + 2 * NOPE + 16 * (q - L::kCodePieces)) = uint4{r.v.x, r.v.y, r.v.z, r.v.w};
+    }
   } else {
-    if (c >= NOPE / 8) return r.v;
-    return dequant_fp8x8_bf16(uint2{r.v.x, r.v.y}, r.s);
+    *reinterpret_cast<uint4*>(krow + 16 * q) = uint4{r.v.x, r.v.y, r.v.z, r.v.w};
   }
 }
 
-template <int FMT, int D, int NOPE, int HG, int DS>
-struct Smem {
-  static constexpr int KT = kTile * (2 * D + 16);
-  static constexpr int SX = DS > 1 ? HG * DS * 16 * 64 * 4 : 0;
-  static constexpr int LDS = KT + SX;
-};
-
-template <int FMT, int D, int NOPE, int HG, int DS>
-__global__ void __launch_bounds__(HG * DS * 64) sparse_mqa_kernel(const AttnParams p) {
+// One (row, split, head group)'s share of the row's virtual entry list
+// [window nw | dense nd | sparse ns], the entry tables of its tiles, and the register
+// prefetch of a tile.  Shared by both kernels.
+template <int FMT, int D, int NOPE, int NT, int NSLOT = 2>
+struct RowPlan {
   using L = Layout<FMT, D, NOPE>;
-  using M = Smem<FMT, D, NOPE, HG, DS>;
-  constexpr int NT = HG * DS * 64;
-  constexpr int DPART = D / DS;           // channels per D-part
-  constexpr int QSTEPS = DPART / 16;      // QK MFMA steps per wave
-  constexpr int NDB = DPART / 32;         // 32-channel blocks of O per wave
-  constexpr int KT_PITCH = 2 * D + 16;    // bytes per Kt row (16 B pad spreads LDS banks)
-  constexpr int NTAB = 2;                 // entry tables: current and next tile
-  constexpr int TPE = NT / kTile;         // threads per entry in the load/dequant phase
-  constexpr int CPT = (L::kChunks + TPE - 1) / TPE;  // chunks per thread
-  static_assert(DPART % 32 == 0, "D-part must be a multiple of 32 channels");
+  static constexpr int TPE = NT / kTile;                          // threads per entry
+  static constexpr int PPT = (L::kPieces + TPE - 1) / TPE;        // pieces per thread
 
-  extern __shared__ __align__(16) uint8_t smem[];
-  uint8_t* kt = smem;                                           // [32][KT_PITCH] bf16 tile
-  float* sx = reinterpret_cast<float*>(kt + M::KT);             // [waves][16][64] partial S
-  __shared__ const uint8_t* tab_ptr[NTAB][kTile];
-  __shared__ uint32_t tab_mask[NTAB];
-  __shared__ int32_t sidx[kIdxCap];  // this split's sparse indices
+  int64_t row, b, pos;
+  int split, hgrp;
+  int nw, nwd, v_begin, v_end, ntiles, sp_begin, win_first;
+  int64_t g_lim;
+  const uint8_t* win_b;
+  const uint8_t* dense_b;
+  const uint8_t* main_b;
+  const uint8_t** tab_ptr;   // [NSLOT][kTile] in LDS: tile t uses slot t % NSLOT
+  uint32_t* tab_mask;        // [NSLOT] in LDS
+  const int32_t* sidx;       // this split's sparse indices (the first sidx_cap), in LDS
+  const int32_t* idx_row;    // the row's sparse indices in global memory
+  int sidx_cap;
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int hg = wave / DS;
-  const int ds = wave % DS;
-  const int half = lane >> 5;
-  const int64_t row = blockIdx.y;
-  const int split = blockIdx.x;
-  const int64_t b = row / p.S;
-  const int64_t pos = p.positions[row];
+  // Workgroup -> (row, split, head group).  The head groups of one (row, split) read the
+  // same entries: they get consecutive slots of one XCD (workgroups are dealt to the 8
+  // XCDs round-robin), so the second and later reads of an entry hit that XCD's L2.
+  // 32-bit arithmetic: the host keeps the grid below 2^31 workgroups and the list
+  // lengths (window + dense_cap + topk) below 2^31.
+  __device__ void init(const AttnParams& p, int heads_per_wg) {
+    const uint32_t nhg = static_cast<uint32_t>((p.H + heads_per_wg - 1) / heads_per_wg);
+    const uint32_t units = static_cast<uint32_t>(p.rows) * static_cast<uint32_t>(p.nsplit);
+    const uint32_t L0 = blockIdx.x;
+    uint32_t unit;
+    if ((units & 7u) == 0) {
+      const uint32_t w = L0 >> 3;
+      hgrp = static_cast<int>(w % nhg);
+      unit = (w / nhg) * 8 + (L0 & 7u);
+    } else {
+      hgrp = static_cast<int>(L0 % nhg);
+      unit = L0 / nhg;
+    }
+    const uint32_t row32 = unit / static_cast<uint32_t>(p.nsplit);
+    split = static_cast<int>(unit - row32 * static_cast<uint32_t>(p.nsplit));
+    row = row32;
+    b = row32 / static_cast<uint32_t>(p.S);
+    pos = p.positions[row];
 
-  // ---- the row's virtual entry list and this split's share of it
-  const int64_t nw = pos + 1 < p.window ? pos + 1 : p.window;
-  int64_t nd = 0;
-  if (p.dense) {
-    nd = (pos + 1) / p.dense_ratio;
-    if (nd > p.dense_cap) nd = p.dense_cap;
+    nw = static_cast<int>(pos + 1 < p.window ? pos + 1 : p.window);
+    int nd = 0;
+    if (p.dense) {
+      const int64_t n = (pos + 1) / p.dense_ratio;
+      nd = static_cast<int>(n < p.dense_cap ? n : p.dense_cap);
+    }
+    const int ns = p.main ? p.topk : 0;
+    nwd = nw + nd;
+    const int total = nwd + ns;
+    int chunk = (total + p.nsplit - 1) / p.nsplit;
+    chunk = (chunk + kTile - 1) / kTile * kTile;
+    v_begin = split * chunk;
+    v_end = v_begin + chunk < total ? v_begin + chunk : total;
+    ntiles = v_end > v_begin ? (v_end - v_begin + kTile - 1) / kTile : 0;
+    sp_begin = v_begin > nwd ? v_begin - nwd : 0;
+
+    win_b = p.win + b * p.win_batch_entries * L::kEntryBytes;
+    dense_b = p.dense ? p.dense + b * p.dense_batch_entries * L::kEntryBytes : nullptr;
+    main_b = p.main ? p.main + b * p.main_batch_entries * L::kEntryBytes : nullptr;
+    // ring slot of window entry 0 (token pos - nw + 1); entry v sits v slots later
+    win_first = static_cast<int>(p.win_cap ? (pos - nw + 1) % p.win_cap : pos - nw + 1);
+    g_lim = p.G < 0x7fffffff ? p.G : 0x7fffffff;
   }
-  const int64_t ns = p.main ? p.topk : 0;
-  const int64_t total = nw + nd + ns;
-  int64_t chunk = (total + p.nsplit - 1) / p.nsplit;
-  chunk = (chunk + kTile - 1) / kTile * kTile;
-  const int64_t v_begin = split * chunk;
-  const int64_t v_end = v_begin + chunk < total ? v_begin + chunk : total;
-  const int ntiles = v_end > v_begin ? static_cast<int>((v_end - v_begin + kTile - 1) / kTile) : 0;
 
-  const uint8_t* win_b = p.win + b * p.win_batch_entries * L::kEntryBytes;
-  const uint8_t* dense_b = p.dense ? p.dense + b * p.dense_batch_entries * L::kEntryBytes : nullptr;
-  const uint8_t* main_b = p.main ? p.main + b * p.main_batch_entries * L::kEntryBytes : nullptr;
-  const int32_t* idx_row = p.idx ? p.idx + row * p.idx_row_stride : nullptr;
+  // Stage this split's slice of the sparse index list in LDS (the host guarantees it fits
+  // kIdxCap), so the tile loop issues no vector-memory reads besides the tiles.
+  // The caller synchronises before the slice is read.
+  // Stage up to `cap` indices of this split's slice of the sparse list in LDS, so the tile
+  // loop reads them from there; positions beyond the cap are read from global memory.
+  // The caller synchronises before the slice is read.
+  __device__ void stage_indices(const AttnParams& p, int32_t* sidx_lds, int cap, int tid) {
+    const int sp_end = v_end > nwd ? v_end - nwd : 0;
+    idx_row = p.idx ? p.idx + row * p.idx_row_stride : nullptr;
+    const int lim = sp_end < sp_begin + cap ? sp_end : sp_begin + cap;
+    for (int s = sp_begin + tid; s < lim; s += NT) sidx_lds[s - sp_begin] = idx_row[s];
+    sidx = sidx_lds;
+    sidx_cap = cap;
+  }
 
-  // this split's slice of the sparse index list, staged in LDS once (the host guarantees
-  // it fits kIdxCap), so the tile loop issues no vector-memory reads besides the tile DMA
-  const int64_t sp_begin = v_begin > nw + nd ? v_begin - nw - nd : 0;
-  const int64_t sp_end = v_end > nw + nd ? v_end - nw - nd : 0;
-  for (int64_t s = sp_begin + tid; s < sp_end; s += NT) sidx[s - sp_begin] = idx_row[s];
-  __syncthreads();  // the slice is read by other threads below
-  auto load_slot = [&](int64_t v) -> int64_t {
-    return (v >= nw + nd && v < v_end) ? static_cast<int64_t>(sidx[v - nw - nd - sp_begin]) : -1;
-  };
-  // entry table of tile `t` (threads 0..31); `g` = this thread's prefetched sparse index
-  auto build_table = [&](int t, int64_t g) {
+  // sparse index of list position v (-1 outside the sparse part of this split)
+  __device__ int slot(int v) const {
+    if (v < nwd || v >= v_end) return -1;
+    const int s = v - nwd - sp_begin;
+    return s < sidx_cap ? sidx[s] : idx_row[sp_begin + s];
+  }
+
+  // entry table of tile t (threads 0..31); g = this thread's prefetched sparse index
+  __device__ void build_table(const AttnParams& p, int t, int g, int tid) {
     if (tid < kTile) {
-      const int64_t v = v_begin + static_cast<int64_t>(t) * kTile + tid;
+      const int v = v_begin + t * kTile + tid;
       const uint8_t* ptr = nullptr;
       if (v < v_end) {
         if (v < nw) {
-          const int64_t tok = pos - nw + 1 + v;
-          ptr = win_b + (p.win_cap ? tok % p.win_cap : tok) * L::kEntryBytes;
-        } else if (v < nw + nd) {
-          ptr = dense_b + (v - nw) * L::kEntryBytes;
-        } else if (g >= 0 && g < p.G) {
-          ptr = main_b + g * L::kEntryBytes;
+          int slot_w = win_first + v;
+          if (p.win_cap && slot_w >= p.win_cap) slot_w -= p.win_cap;
+          ptr = win_b + static_cast<int64_t>(slot_w) * L::kEntryBytes;
+        } else if (v < nwd) {
+          ptr = dense_b + static_cast<int64_t>(v - nw) * L::kEntryBytes;
+        } else if (g >= 0 && g < g_lim) {
+          ptr = main_b + static_cast<int64_t>(g) * L::kEntryBytes;
         }
       }
-      tab_ptr[t % NTAB][tid] = ptr;
+      tab_ptr[(t % NSLOT) * kTile + tid] = ptr;
       const uint64_t bal = __ballot(ptr != nullptr);
-      if (tid == 0) tab_mask[t % NTAB] = static_cast<uint32_t>(bal);
+      if (tid == 0) tab_mask[t % NSLOT] = static_cast<uint32_t>(bal);
     }
-  };
-  // load phase: thread owns entry tid / TPE, 8-channel chunks (tid % TPE) + TPE*k; the
-  // next tile's chunks are fetched into registers while the current tile computes
-  const int my_entry = tid / TPE;
-  const int my_c0 = tid % TPE;
-  RawChunk raw[CPT];
-  auto fetch_tile = [&](int t) {
-    const gptr_t e = (gptr_t)(tab_ptr[t % NTAB][my_entry]);
+  }
+
+  // The tile's pieces for this thread: entry tid / TPE, pieces (tid % TPE) + TPE*k, so the
+  // TPE threads of an entry read TPE consecutive 16-byte pieces per load instruction.
+  // Empty slots load zeros.
+  __device__ void fetch(int t, int tid, Piece (&raw)[PPT]) const {
+    const gptr_t e = (gptr_t)(tab_ptr[(t % NSLOT) * kTile + tid / TPE]);
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-      const int c = my_c0 + TPE * k;
-      raw[k].v = uint4{0u, 0u, 0u, 0u};
+    for (int k = 0; k < PPT; ++k) {
+      const int q = tid % TPE + TPE * k;
+      raw[k].v = u32x4{0u, 0u, 0u, 0u};
       raw[k].s = 1.0f;
-      if (e != nullptr && c < L::kChunks) raw[k] = fetch_chunk<FMT, D, NOPE>(e, c);
-    }
-  };
-
-  // ---- q fragments (B operand of S^T = K Q^T): head, channels of this wave's D-part
-  const int head = blockIdx.z * (HG * 32) + hg * 32 + (lane & 31);
-  const bool head_ok = head < p.H;
-  v8bf qf[QSTEPS];
-  {
-    const uint16_t* qrow = p.q + (row * p.H + (head_ok ? head : 0)) * D + ds * DPART + half * 8;
-#pragma unroll
-    for (int st = 0; st < QSTEPS; ++st) {
-      uint4 v = head_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * st) : uint4{0, 0, 0, 0};
-      qf[st] = __builtin_bit_cast(v8bf, v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w});
+      if (e != nullptr && q < L::kPieces) raw[k] = fetch_piece<FMT, D, NOPE>(e, q);
     }
   }
 
-  v16f acc_o[NDB];
+  // Dequantize the fetched pieces into this thread's entry row of a bf16 tile in LDS.
+  __device__ void store(uint8_t* kt, int kt_pitch, int tid, const Piece (&raw)[PPT]) const {
+    uint8_t* krow = kt + (tid / TPE) * kt_pitch;
 #pragma unroll
-  for (int i = 0; i < NDB; ++i) acc_o[i] = v16f{};
-  float m_run = -__builtin_huge_valf();
-  float l_run = 0.0f;
-
-  int64_t g_pref = -1;  // prefetched sparse index for table t+2 (threads 0..31)
-  if (ntiles > 0) {
-    build_table(0, tid < kTile ? load_slot(v_begin + tid) : -1);
-    build_table(1, tid < kTile ? load_slot(v_begin + kTile + tid) : -1);
-    if (tid < kTile) g_pref = load_slot(v_begin + 2 * kTile + tid);
-    __syncthreads();
-    fetch_tile(0);
+    for (int k = 0; k < PPT; ++k) {
+      const int q = tid % TPE + TPE * k;
+      if (q < L::kPieces) store_piece<FMT, D, NOPE>(krow, raw[k], q);
+    }
   }
+};
 
-#pragma unroll 1
-  for (int t = 0; t < ntiles; ++t) {
-    const int tb = t % NTAB;
-    // 1. dequantize the fetched tile into Kt (empty slots are zero); the table of tile
-    //    t+2 replaces tile t's (no longer read: the softmax below uses its mask copy)
-    const uint32_t vmask = tab_mask[tb];
-#pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-      const int c = my_c0 + TPE * k;
-      if (c < L::kChunks)
-        *reinterpret_cast<uint4*>(kt + my_entry * KT_PITCH + 16 * c) = decode_chunk<FMT, NOPE>(raw[k], c);
-    }
-    lds_barrier();  // Kt complete; every wave has read tile t's table
-    build_table(t + 2, g_pref);
-    if (tid < kTile) g_pref = load_slot(v_begin + static_cast<int64_t>(t + 3) * kTile + tid);
-    // 2. the next tile's HBM reads overlap this tile's MFMA work (stays in flight across
-    //    the LDS-only barriers below)
-    if (t + 1 < ntiles) fetch_tile(t + 1);
+// V^T operand of O^T += V^T . P^T for one 32-channel block and the two 16-entry K-steps,
+// read from a bf16 tile with ds_read_b64_tr_b16: inside a 16-lane group, lane i receives
+// element i%4 of the 4-element rows the lanes 4k + i/4 (k = 0..3) point at.  Lane j
+// therefore points at Kt[e0 + j/4][d0 + 4*(j%4)] and receives Kt[e0 + k][d0 + i] for
+// k = 0..3: four consecutive entries of its own channel, two reads per fragment.
+// K-step ks covers entries 16ks + {0..3, 8..11} + 4*half (the S^T register order).
+template <int KT_PITCH>
+__device__ __forceinline__ void pv_block(const uint8_t* tp, const v8bf& pf0, const v8bf& pf1, v16f& acc) {
+  const v4s r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4s(tp));                  // entries 0-3 (+4h)
+  const v4s r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4s(tp + 8 * KT_PITCH));   // entries 8-11
+  const v4s r2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4s(tp + 16 * KT_PITCH));  // entries 16-19
+  const v4s r3 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4s(tp + 24 * KT_PITCH));  // entries 24-27
+  const v8bf a0 = __builtin_bit_cast(v8bf, v8s{r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]});
+  const v8bf a1 = __builtin_bit_cast(v8bf, v8s{r2[0], r2[1], r2[2], r2[3], r3[0], r3[1], r3[2], r3[3]});
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, pf0, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, pf1, acc, 0, 0, 0);
+}
 
-    // 3. S^T partial over this wave's D-part
-    v16f s = v16f{};
-    {
-      const uint8_t* krow = kt + (lane & 31) * KT_PITCH + 2 * (ds * DPART + half * 8);
-      if constexpr (DS == 1) {
-        v16f s1 = v16f{};  // two independent chains (even / odd K-steps), summed in that order
-#pragma unroll
-        for (int st = 0; st < QSTEPS; ++st) {
-          const uint4 kv = *reinterpret_cast<const uint4*>(krow + 32 * st);
-          const v8bf ka = __builtin_bit_cast(v8bf, v4i{(int)kv.x, (int)kv.y, (int)kv.z, (int)kv.w});
-          if (st & 1) s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[st], s1, 0, 0, 0);
-          else s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[st], s, 0, 0, 0);
-        }
-        s = s + s1;
-      } else {
-#pragma unroll
-        for (int st = 0; st < QSTEPS; ++st) {
-          const uint4 kv = *reinterpret_cast<const uint4*>(krow + 32 * st);
-          const v8bf ka = __builtin_bit_cast(v8bf, v4i{(int)kv.x, (int)kv.y, (int)kv.z, (int)kv.w});
-          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[st], s, 0, 0, 0);
-        }
-        // partial S of each D-part through LDS ([wave][j][lane], conflict-free), summed in
-        // D-part order by every wave of the head group
-#pragma unroll
-        for (int j = 0; j < 16; ++j) sx[(wave * 16 + j) * 64 + lane] = s[j];
-        lds_barrier();
-#pragma unroll
-        for (int j = 0; j < 16; ++j) s[j] = sx[((hg * DS) * 16 + j) * 64 + lane];
-#pragma unroll
-        for (int part = 1; part < DS; ++part) {
-#pragma unroll
-          for (int j = 0; j < 16; ++j) s[j] = s[j] + sx[((hg * DS + part) * 16 + j) * 64 + lane];
-        }
-      }
-    }
+// Lane offset of the V^T read pattern above inside a tile, for channel block base d_base.
+template <int KT_PITCH>
+__device__ __forceinline__ int pv_lane_offset(int lane, int d_base) {
+  const int grp = lane >> 4;  // 16-lane group: channel half (grp & 1), entry half (grp >> 1)
+  const int j = lane & 15;
+  const int e0 = 4 * (grp >> 1) + (j >> 2);
+  return e0 * KT_PITCH + 2 * (d_base + 16 * (grp & 1) + 4 * (j & 3));
+}
 
-    // 4. online softmax (exp2 domain), lane-local per head.  The running max is only
-    // raised when a head's tile max exceeds it by more than kLazy (log2 units): until then
-    // exp2(s - m) <= 2^kLazy stays exact enough in fp32/bf16 and O needs no rescale.  The
-    // decision is wave-uniform, so most tiles skip the O^T *= alpha pass.
-    float tmax = -__builtin_huge_valf();
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      s[j] = ((vmask >> c_entry(j, lane)) & 1u) ? s[j] * p.scale_log2 : -__builtin_huge_valf();
-      tmax = fmaxf(tmax, s[j]);
-    }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    constexpr float kLazy = 8.0f;
-    const bool raise = tmax > m_run + kLazy;
-    if (__any(raise)) {
-      const float m_new = raise ? tmax : m_run;
-      const float alpha = (m_run == -__builtin_huge_valf()) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-      l_run = l_run * alpha;
-#pragma unroll
-      for (int i = 0; i < NDB; ++i) acc_o[i] = acc_o[i] * alpha;
-      m_run = m_new;
-    }
-    float psum = 0.0f;
-    uint32_t pk[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      // v_exp_f32 directly: arguments are <= kLazy, results below 2^-126 may flush to 0
-      const float p0 = s[2 * i] == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f(s[2 * i] - m_run);
-      const float p1 = s[2 * i + 1] == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f(s[2 * i + 1] - m_run);
-      psum = psum + p0 + p1;
-      pk[i] = pack_bf16x2(p0, p1);
-    }
-    psum = psum + __shfl_xor(psum, 32, 64);
-    l_run = l_run + psum;
-
-    // 5. O^T += V^T . P^T.  P^T is the S^T result in registers: PV step ks consumes
-    // registers 8ks..8ks+7 = entries 16ks + {0..3, 8..11} + 4*half.  The matching V^T
-    // operand (32 channels x 8 entries) comes from Kt with ds_read_b64_tr_b16: inside a
-    // 16-lane group, lane i receives element i%4 of the 4-element rows the lanes
-    // 4k + i/4 (k = 0..3) point at.  Lane j therefore points at
-    // Kt[e0 + j/4][d0 + 4*(j%4)] and receives Kt[e0 + k][d0 + i] for k = 0..3:
-    // four consecutive entries of its own channel, two reads per fragment.
-    const v8bf pf0 = __builtin_bit_cast(v8bf, v4i{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]});
-    const v8bf pf1 = __builtin_bit_cast(v8bf, v4i{(int)pk[4], (int)pk[5], (int)pk[6], (int)pk[7]});
-    {
-      const int grp = lane >> 4;  // 16-lane group: channel half (grp & 1), entry half (grp >> 1)
-      const int j = lane & 15;
-      const int e0 = 4 * (grp >> 1) + (j >> 2);
-      const int dcol = ds * DPART + 16 * (grp & 1) + 4 * (j & 3);
-      const uint8_t* tr0 = kt + e0 * KT_PITCH + 2 * dcol;
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const uint8_t* tp = tr0 + 64 * db;
-        const v4s r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4s(tp));                     // entries 0-3 (+4h)
-        const v4s r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4s(tp + 8 * KT_PITCH));      // entries 8-11
-        const v4s r2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4s(tp + 16 * KT_PITCH));     // entries 16-19
-        const v4s r3 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4s(tp + 24 * KT_PITCH));     // entries 24-27
-        const v8bf a0 = __builtin_bit_cast(v8bf, v8s{r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]});
-        const v8bf a1 = __builtin_bit_cast(v8bf, v8s{r2[0], r2[1], r2[2], r2[3], r3[0], r3[1], r3[2], r3[3]});
-        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, pf0, acc_o[db], 0, 0, 0);
-        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, pf1, acc_o[db], 0, 0, 0);
-      }
-    }
-    lds_barrier();  // Kt and the S exchange buffer are free for the next tile
-  }
-
-  // ---- epilogue.  acc_o[db][j] holds O^T[d][head], d = ds*DPART + db*32 + c_entry(j, lane)
-  if (!head_ok) return;
-  if (p.out != nullptr && p.nsplit == 1) {
+// Final bf16 output + lse (one split) or fp32 partials (several) for one lane's head and
+// O^T blocks [b_lo, b_lo + nb): acc[db][j] holds O^T[d][head], d = (b_lo+db)*32 + c_entry(j).
+template <int D, int NDBM>
+__device__ __forceinline__ void write_result(const AttnParams& p, int64_t row, int64_t b, int split, int head, int half,
+                                             bool lse_lane, int b_lo, int nb, float m_run, float l_run,
+                                             const v16f (&acc)[NDBM]) {
+  if (p.nsplit == 1) {
     float m_fin = m_run, l_fin = l_run, o_scale;
     if (p.sinks) {
       const float sk = p.sinks[head] * kLog2e;
@@ -413,40 +338,387 @@ __global__ void __launch_bounds__(HG * DS * 64) sparse_mqa_kernel(const AttnPara
     } else {
       o_scale = 1.0f / l_fin;
     }
-    uint16_t* orow = p.out + (row * p.H + head) * D + ds * DPART;
+    uint16_t* orow = p.out + (row * p.H + head) * D + b_lo * 32;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) {
+    for (int db = 0; db < NDBM; ++db) {
+      if (db < nb) {
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int d0 = db * 32 + 8 * g4 + 4 * half;
-        const uint32_t w0 = f32_to_bf16(acc_o[db][4 * g4 + 0] * o_scale) |
-                            (static_cast<uint32_t>(f32_to_bf16(acc_o[db][4 * g4 + 1] * o_scale)) << 16);
-        const uint32_t w1 = f32_to_bf16(acc_o[db][4 * g4 + 2] * o_scale) |
-                            (static_cast<uint32_t>(f32_to_bf16(acc_o[db][4 * g4 + 3] * o_scale)) << 16);
-        *reinterpret_cast<uint2*>(orow + d0) = uint2{w0, w1};
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int d0 = db * 32 + 8 * g4 + 4 * half;
+          const uint32_t w0 = f32_to_bf16(acc[db][4 * g4 + 0] * o_scale) |
+                              (static_cast<uint32_t>(f32_to_bf16(acc[db][4 * g4 + 1] * o_scale)) << 16);
+          const uint32_t w1 = f32_to_bf16(acc[db][4 * g4 + 2] * o_scale) |
+                              (static_cast<uint32_t>(f32_to_bf16(acc[db][4 * g4 + 3] * o_scale)) << 16);
+          *reinterpret_cast<uint2*>(orow + d0) = uint2{w0, w1};
+        }
       }
     }
-    if (ds == 0 && half == 0) {
+    if (lse_lane) {
       const int64_t s_idx = row % p.S;
       p.lse[(b * p.H + head) * p.S + s_idx] = (m_fin + __log2f(l_fin)) * kLn2;
     }
   } else {
-    float* prow = p.part_o + ((row * p.nsplit + split) * p.H + head) * static_cast<int64_t>(D) + ds * DPART;
+    float* prow = p.part_o + ((row * p.nsplit + split) * p.H + head) * static_cast<int64_t>(D) + b_lo * 32;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) {
+    for (int db = 0; db < NDBM; ++db) {
+      if (db < nb) {
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int d0 = db * 32 + 8 * g4 + 4 * half;
-        *reinterpret_cast<float4*>(prow + d0) =
-            float4{acc_o[db][4 * g4], acc_o[db][4 * g4 + 1], acc_o[db][4 * g4 + 2], acc_o[db][4 * g4 + 3]};
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int d0 = db * 32 + 8 * g4 + 4 * half;
+          *reinterpret_cast<float4*>(prow + d0) =
+              float4{acc[db][4 * g4], acc[db][4 * g4 + 1], acc[db][4 * g4 + 2], acc[db][4 * g4 + 3]};
+        }
       }
     }
-    if (ds == 0 && half == 0) {
+    if (lse_lane) {
       float* ml = p.part_ml + ((row * p.nsplit + split) * p.H + head) * 2;
       ml[0] = m_run;
       ml[1] = l_run;
     }
   }
+}
+
+constexpr float kLazy = 8.0f;  // log2 headroom before the running max must be raised
+
+// ------------------------------------------------------------------------------------
+// D <= 256: one wave per 32 heads over the whole of D.  HG waves per workgroup.
+// Per tile: dequantize into Kt, S^T = K.Q^T (two MFMA chains), lane-local online
+// softmax, O^T += V^T.P^T with P^T straight from the S^T registers.
+// ------------------------------------------------------------------------------------
+template <int FMT, int D, int NOPE, int HG>
+__global__ void __launch_bounds__(HG * 64) sparse_mqa_kernel(const AttnParams p) {
+  constexpr int NT = HG * 64;
+  constexpr int KS = D / 16;
+  constexpr int NB = D / 32;
+  constexpr int KT_PITCH = 2 * D + 16;  // bytes per Kt row (16 B pad spreads LDS banks)
+  using RP = RowPlan<FMT, D, NOPE, NT>;
+  static_assert(D % 32 == 0, "D must be a multiple of 32");
+
+  __shared__ __align__(16) uint8_t kt[kTile * KT_PITCH];
+  __shared__ const uint8_t* tab_ptr[2 * kTile];
+  __shared__ uint32_t tab_mask[2];
+  __shared__ int32_t sidx[kIdxCap];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int hg = tid >> 6;
+  const int half = lane >> 5;
+  RP rp;
+  rp.tab_ptr = tab_ptr;
+  rp.tab_mask = tab_mask;
+  rp.init(p, HG * 32);
+  rp.stage_indices(p, sidx, kIdxCap, tid);
+  __syncthreads();
+
+  const int head = rp.hgrp * (HG * 32) + hg * 32 + (lane & 31);
+  const bool head_ok = head < p.H;
+  v8bf qf[KS];
+  {
+    const uint16_t* qrow = p.q + (rp.row * p.H + (head_ok ? head : 0)) * D + half * 8;
+#pragma unroll
+    for (int st = 0; st < KS; ++st) {
+      uint4 v = head_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * st) : uint4{0, 0, 0, 0};
+      qf[st] = __builtin_bit_cast(v8bf, v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w});
+    }
+  }
+  v16f acc_o[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) acc_o[i] = v16f{};
+  float m_run = -__builtin_huge_valf();
+  float l_run = 0.0f;
+
+  Piece raw[RP::PPT];
+  int g_pref = -1;
+  if (rp.ntiles > 0) {
+    rp.build_table(p, 0, tid < kTile ? rp.slot(rp.v_begin + tid) : -1, tid);
+    rp.build_table(p, 1, tid < kTile ? rp.slot(rp.v_begin + kTile + tid) : -1, tid);
+    if (tid < kTile) g_pref = rp.slot(rp.v_begin + 2 * kTile + tid);
+    __syncthreads();
+    rp.fetch(0, tid, raw);
+  }
+
+#pragma unroll 1
+  for (int t = 0; t < rp.ntiles; ++t) {
+    const uint32_t vmask = tab_mask[t & 1];
+    rp.store(kt, KT_PITCH, tid, raw);
+    lds_barrier();  // Kt complete; every wave has read tile t's table
+    rp.build_table(p, t + 2, g_pref, tid);
+    if (tid < kTile) g_pref = rp.slot(rp.v_begin + (t + 3) * kTile + tid);
+    if (t + 1 < rp.ntiles) rp.fetch(t + 1, tid, raw);  // in flight across the LDS-only barriers
+
+    v16f s = v16f{}, s1 = v16f{};  // even / odd K-steps, summed in that order
+    {
+      const uint8_t* krow = kt + (lane & 31) * KT_PITCH + 2 * (half * 8);
+#pragma unroll
+      for (int st = 0; st < KS; ++st) {
+        const uint4 kv = *reinterpret_cast<const uint4*>(krow + 32 * st);
+        const v8bf ka = __builtin_bit_cast(v8bf, v4i{(int)kv.x, (int)kv.y, (int)kv.z, (int)kv.w});
+        if (st & 1) s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[st], s1, 0, 0, 0);
+        else s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[st], s, 0, 0, 0);
+      }
+      s = s + s1;
+    }
+    // online softmax (exp2 domain), lane-local per head over its 16 entries plus the other
+    // half's 16.  The running max is raised only when a head's tile max exceeds it by more
+    // than kLazy; the decision is wave-uniform, so most tiles skip the O^T *= alpha pass.
+    float tmax = -__builtin_huge_valf();
+    if (vmask == 0xffffffffu) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        s[j] = s[j] * p.scale_log2;
+        tmax = fmaxf(tmax, s[j]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        s[j] = ((vmask >> c_entry(j, lane)) & 1u) ? s[j] * p.scale_log2 : -__builtin_huge_valf();
+        tmax = fmaxf(tmax, s[j]);
+      }
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const bool raise = tmax > m_run + kLazy;
+    if (__any(raise)) {
+      const float m_new = raise ? tmax : m_run;
+      const float alpha = (m_run == -__builtin_huge_valf()) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run = l_run * alpha;
+#pragma unroll
+      for (int i = 0; i < NB; ++i) acc_o[i] = acc_o[i] * alpha;
+      m_run = m_new;
+    }
+    // masked entries are -inf and v_exp_f32(-inf) = 0; before any finite entry the
+    // reference point is 0 instead of -inf (which would give NaN)
+    const float m_use = m_run == -__builtin_huge_valf() ? 0.0f : m_run;
+    float psum = 0.0f;
+    uint32_t pk[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      // v_exp_f32 directly: arguments are <= kLazy, results below 2^-126 may flush to 0
+      const float p0 = __builtin_amdgcn_exp2f(s[2 * i] - m_use);
+      const float p1 = __builtin_amdgcn_exp2f(s[2 * i + 1] - m_use);
+      psum = psum + p0 + p1;
+      pk[i] = pack_bf16x2(p0, p1);
+    }
+    psum = psum + __shfl_xor(psum, 32, 64);
+    l_run = l_run + psum;
+    const v8bf pf0 = __builtin_bit_cast(v8bf, v4i{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]});
+    const v8bf pf1 = __builtin_bit_cast(v8bf, v4i{(int)pk[4], (int)pk[5], (int)pk[6], (int)pk[7]});
+    const uint8_t* tr0 = kt + pv_lane_offset<KT_PITCH>(lane, 0);
+#pragma unroll
+    for (int db = 0; db < NB; ++db) pv_block<KT_PITCH>(tr0 + 64 * db, pf0, pf1, acc_o[db]);
+    lds_barrier();  // Kt is free for the next tile
+  }
+
+  if (!head_ok) return;
+  write_result<D, NB>(p, rp.row, rp.b, rp.split, head, half, half == 0, 0, NB, m_run, l_run, acc_o);
+}
+
+// ------------------------------------------------------------------------------------
+// D > 256 (the 512+64 latent): 64 heads per workgroup, each 32-head group split over 4
+// waves by D (8 waves, two per SIMD).  A wave holds its D-quarter of q (9 K-steps) and at
+// most 5 O^T blocks.  The loop is software-pipelined: iteration t starts with tile t's
+// S^T partials already published (computed in iteration t-1, or the prologue).
+//   barrier A.  Wave ds finishes entries 8ds..8ds+7 of tile t (S^T registers 4ds..4ds+3):
+//      sums the four partials in D-part order and bounds the tile max by the sum of the
+//      partial maxima (an upper bound, so exp2(s - m) <= 2^kLazy still holds; the online
+//      softmax is exact for any reference point); its P^T quarter goes to LDS.  Meanwhile
+//      the workgroup dequantizes tile t+1 into Kt[(t+1)%2] and builds table t+2.
+//   barrier B.  O^T += V^T.P^T of tile t from Kt[t%2] and the S^T partial of tile t+1 from
+//      Kt[(t+1)%2], in one block so the two MFMA streams interleave; the partial and its
+//      per-head maximum are published; the pieces of tile t+2 are fetched.
+// Two barriers per tile.
+// ------------------------------------------------------------------------------------
+template <int FMT, int D, int NOPE>
+struct SplitSmem {
+  static constexpr int HG = 2, DS = 4;
+  static constexpr int KT_PITCH = 2 * D + 16;
+  static constexpr int KT = kTile * KT_PITCH;             // one bf16 tile
+  static constexpr int SX = HG * DS * 4 * 64 * 16;        // [wave][4][64] float4 partial S^T
+  static constexpr int PM = HG * 32 * 2 * DS * 4;         // [64 heads][8] partial maxima / row sums
+  static constexpr int PB = HG * 2 * 64 * 16;             // [hg][2 K-steps][64] P^T
+  static constexpr int LDS = 2 * KT + SX + PM + PB;
+};
+
+template <int FMT, int D, int NOPE>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+sparse_mqa_dsplit_kernel(const AttnParams p) {
+  using M = SplitSmem<FMT, D, NOPE>;
+  constexpr int HG = M::HG, DS = M::DS;
+  constexpr int NT = HG * DS * 64;
+  constexpr int KT_PITCH = M::KT_PITCH;
+  constexpr int QST = D / 16 / DS;            // QK K-steps per wave
+  constexpr int NB = D / 32;                  // 32-channel blocks of O
+  constexpr int NDBM = (NB + DS - 1) / DS;    // most O blocks one wave owns
+  using RP = RowPlan<FMT, D, NOPE, NT>;
+  static_assert((D / 16) % DS == 0 && D % 32 == 0, "D must split into 4 parts of 16-channel steps");
+
+  extern __shared__ __align__(16) uint8_t smem[];
+  uint8_t* kt0 = smem;                                                   // 2 x [32][KT_PITCH]
+  float4* sx = reinterpret_cast<float4*>(smem + 2 * M::KT);
+  float* pm = reinterpret_cast<float*>(smem + 2 * M::KT + M::SX);
+  uint4* pb = reinterpret_cast<uint4*>(smem + 2 * M::KT + M::SX + M::PM);
+  __shared__ const uint8_t* tab_ptr[2 * kTile];
+  __shared__ uint32_t tab_mask[2];
+  __shared__ int32_t sidx[kIdxCap];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int hg = wave / DS;
+  const int ds = wave % DS;
+  const int half = lane >> 5;
+  RP rp;
+  rp.tab_ptr = tab_ptr;
+  rp.tab_mask = tab_mask;
+  rp.init(p, HG * 32);
+  rp.stage_indices(p, sidx, kIdxCap, tid);
+  __syncthreads();
+
+  const int hl = hg * 32 + (lane & 31);  // head within the workgroup
+  const int head = rp.hgrp * (HG * 32) + hl;
+  const bool head_ok = head < p.H;
+  const int qc0 = ds * QST * 16;  // first QK channel of this wave
+  v8bf qf[QST];
+  {
+    const uint16_t* qrow = p.q + (rp.row * p.H + (head_ok ? head : 0)) * D + qc0 + half * 8;
+#pragma unroll
+    for (int st = 0; st < QST; ++st) {
+      uint4 v = head_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * st) : uint4{0, 0, 0, 0};
+      qf[st] = __builtin_bit_cast(v8bf, v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w});
+    }
+  }
+  const int b_lo = ds * NB / DS;
+  const int nb_mine = (ds + 1) * NB / DS - b_lo;
+  v16f acc_o[NDBM];
+#pragma unroll
+  for (int i = 0; i < NDBM; ++i) acc_o[i] = v16f{};
+  float m_run = -__builtin_huge_valf();  // identical in the 8 lanes x waves of a head
+  float l_run = 0.0f;                    // this lane's share of the head's row sum
+
+  Piece raw[RP::PPT];
+  int g_pref = -1;
+  const int pv_off = pv_lane_offset<KT_PITCH>(lane, b_lo * 32);
+  // S^T partial over this wave's D-quarter of the tile in `kt`; all K fragments are read
+  // before the MFMA chain
+  auto qk = [&](const uint8_t* kt) -> v16f {
+    const uint8_t* krow = kt + (lane & 31) * KT_PITCH + 2 * (qc0 + half * 8);
+    v8bf kf[QST];
+#pragma unroll
+    for (int st = 0; st < QST; ++st) {
+      const uint4 kv = *reinterpret_cast<const uint4*>(krow + 32 * st);
+      kf[st] = __builtin_bit_cast(v8bf, v4i{(int)kv.x, (int)kv.y, (int)kv.z, (int)kv.w});
+    }
+    v16f s = v16f{};
+#pragma unroll
+    for (int st = 0; st < QST; ++st) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[st], qf[st], s, 0, 0, 0);
+    return s;
+  };
+  // the partial ([wave][j/4][lane] float4: consecutive lanes at consecutive 16 B,
+  // conflict-free) and its per-head maximum over this lane's 16 entries go to LDS
+  auto publish = [&](const v16f& s) {
+    float mx = s[0];
+#pragma unroll
+    for (int j = 1; j < 16; ++j) mx = fmaxf(mx, s[j]);
+    pm[hl * 8 + 2 * ds + half] = mx;
+#pragma unroll
+    for (int j4 = 0; j4 < 4; ++j4)
+      sx[(wave * 4 + j4) * 64 + lane] = float4{s[4 * j4], s[4 * j4 + 1], s[4 * j4 + 2], s[4 * j4 + 3]};
+  };
+  if (rp.ntiles > 0) {
+    rp.build_table(p, 0, tid < kTile ? rp.slot(rp.v_begin + tid) : -1, tid);
+    rp.build_table(p, 1, tid < kTile ? rp.slot(rp.v_begin + kTile + tid) : -1, tid);
+    if (tid < kTile) g_pref = rp.slot(rp.v_begin + 2 * kTile + tid);
+    __syncthreads();
+    rp.fetch(0, tid, raw);
+    rp.store(kt0, KT_PITCH, tid, raw);
+    if (rp.ntiles > 1) rp.fetch(1, tid, raw);
+    lds_barrier();  // Kt[0] complete
+    publish(qk(kt0));
+  }
+
+#pragma unroll 1
+  for (int t = 0; t < rp.ntiles; ++t) {
+    const uint8_t* kt = kt0 + (t & 1) * M::KT;
+    uint8_t* kt_next = kt0 + ((t + 1) & 1) * M::KT;
+    const uint32_t vmask = tab_mask[t & 1];  // read before barrier A; table t+2 replaces it after
+    lds_barrier();  // A: tile t's partials published; every wave is done with PV(t-1)
+
+    // dequantize tile t+1 into the buffer PV(t-1) has released
+    if (t + 1 < rp.ntiles) rp.store(kt_next, KT_PITCH, tid, raw);
+    rp.build_table(p, t + 2, g_pref, tid);
+    if (tid < kTile) g_pref = rp.slot(rp.v_begin + (t + 3) * kTile + tid);
+
+    // entries 8ds..8ds+7 of tile t for this lane's head
+    float4 a = sx[((hg * DS) * 4 + ds) * 64 + lane];
+#pragma unroll
+    for (int part = 1; part < DS; ++part) {
+      const float4 c = sx[((hg * DS + part) * 4 + ds) * 64 + lane];
+      a.x = a.x + c.x;
+      a.y = a.y + c.y;
+      a.z = a.z + c.z;
+      a.w = a.w + c.w;
+    }
+    float v4[4] = {a.x * p.scale_log2, a.y * p.scale_log2, a.z * p.scale_log2, a.w * p.scale_log2};
+    if (vmask != 0xffffffffu) {
+      const uint32_t bits = vmask >> (8 * ds + 4 * half);  // entries 8ds + 4half + i
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (!((bits >> i) & 1u)) v4[i] = -__builtin_huge_valf();
+    }
+    float bound;
+    {
+      const float4 t0 = *reinterpret_cast<const float4*>(pm + hl * 8);
+      const float4 t1 = *reinterpret_cast<const float4*>(pm + hl * 8 + 4);
+      bound = (((fmaxf(t0.x, t0.y) + fmaxf(t0.z, t0.w)) + fmaxf(t1.x, t1.y)) + fmaxf(t1.z, t1.w)) * p.scale_log2;
+    }
+    const bool raise = bound > m_run + kLazy;
+    if (__any(raise)) {  // identical in every wave of the head group
+      const float m_new = raise ? bound : m_run;
+      const float alpha = (m_run == -__builtin_huge_valf()) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run = l_run * alpha;
+#pragma unroll
+      for (int i = 0; i < NDBM; ++i) acc_o[i] = acc_o[i] * alpha;
+      m_run = m_new;
+    }
+    {
+      const float p0 = __builtin_amdgcn_exp2f(v4[0] - m_run);
+      const float p1 = __builtin_amdgcn_exp2f(v4[1] - m_run);
+      const float p2 = __builtin_amdgcn_exp2f(v4[2] - m_run);
+      const float p3 = __builtin_amdgcn_exp2f(v4[3] - m_run);
+      l_run = l_run + ((p0 + p1) + (p2 + p3));
+      // PV K-step ks = ds/2 takes registers 8ks..8ks+7 = D-parts 2ks (slots 0-3), 2ks+1 (4-7)
+      uint2* dst = reinterpret_cast<uint2*>(pb + (hg * 2 + (ds >> 1)) * 64 + lane) + (ds & 1);
+      *dst = uint2{pack_bf16x2(p0, p1), pack_bf16x2(p2, p3)};
+    }
+    lds_barrier();  // B: P^T of tile t and Kt of tile t+1 complete, table t+2 visible
+
+    if (t + 2 < rp.ntiles) rp.fetch(t + 2, tid, raw);
+    const uint4 w0 = pb[(hg * 2 + 0) * 64 + lane];
+    const uint4 w1 = pb[(hg * 2 + 1) * 64 + lane];
+    const v8bf pf0 = __builtin_bit_cast(v8bf, v4i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w});
+    const v8bf pf1 = __builtin_bit_cast(v8bf, v4i{(int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w});
+    // PV(t) and QK(t+1) in one block, so the two MFMA streams interleave.  After the last
+    // tile QK runs on the stale buffer; its result is published but never read.
+    const uint8_t* tr0 = kt + pv_off;
+#pragma unroll
+    for (int db = 0; db < NDBM - 1; ++db) pv_block<KT_PITCH>(tr0 + 64 * db, pf0, pf1, acc_o[db]);
+    const v16f s_next = qk(kt_next);
+    if (nb_mine == NDBM) pv_block<KT_PITCH>(tr0 + 64 * (NDBM - 1), pf0, pf1, acc_o[NDBM - 1]);
+    publish(s_next);
+  }
+
+  // row sum: each lane holds the share of its entries (all scaled to the same running max);
+  // the 8 shares of a head are reduced in a fixed order
+  __syncthreads();  // every wave is done reading pm
+  pm[hl * 8 + 2 * ds + half] = l_run;
+  __syncthreads();
+  {
+    const float4 t0 = *reinterpret_cast<const float4*>(pm + hl * 8);
+    const float4 t1 = *reinterpret_cast<const float4*>(pm + hl * 8 + 4);
+    l_run = (((t0.x + t0.y) + (t0.z + t0.w)) + ((t1.x + t1.y) + (t1.z + t1.w)));
+  }
+  if (head_ok)
+    write_result<D, NDBM>(p, rp.row, rp.b, rp.split, head, half, ds == 0 && half == 0, b_lo, nb_mine, m_run, l_run,
+                          acc_o);
 }
 
 // Merge the split partials of one (row, head) with the sink: one workgroup per (row, head).
@@ -490,34 +762,39 @@ __global__ void __launch_bounds__(64) combine_kernel(const float* __restrict__ p
   }
 }
 
-template <int FMT, int D, int NOPE, int HG, int DS>
-int launch_attn(const AttnParams& p, int64_t rows, hipStream_t s) {
-  constexpr int NT = HG * DS * 64;
-  constexpr size_t lds = Smem<FMT, D, NOPE, HG, DS>::LDS;
-  static_assert(lds <= 150 * 1024, "LDS budget");
-  auto kern = sparse_mqa_kernel<FMT, D, NOPE, HG, DS>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                        static_cast<int>(lds));
-    attr_set = true;
+template <typename K>
+int launch_kernel(K kern, size_t dyn_lds, int threads, int heads_per_wg, const AttnParams& p, int64_t rows, hipStream_t s) {
+  const int64_t nhg = (p.H + heads_per_wg - 1) / heads_per_wg;
+  const int64_t nblocks = rows * p.nsplit * nhg;
+  if (nblocks > 0x7fffffff) {
+    set_last_error("sparse_mqa: %lld workgroups exceed the grid limit", (long long)nblocks);
+    return MZK_EINVAL;
   }
-  // heads beyond HG*32 go to further workgroups along z (each re-reads the KV tiles)
-  dim3 grid(static_cast<unsigned>(p.nsplit), static_cast<unsigned>(rows), static_cast<unsigned>((p.H + HG * 32 - 1) / (HG * 32)));
-  kern<<<grid, NT, lds, s>>>(p);
+  kern<<<dim3(static_cast<unsigned>(nblocks)), threads, dyn_lds, s>>>(p);
   return MZK_OK;
 }
 
 template <int FMT, int D, int NOPE>
 int dispatch_heads(const AttnParams& p, int64_t rows, hipStream_t s) {
-  // D > 256: two waves per 32 heads, each owning half of D (keeps q + O^T within 256 VGPRs)
-  constexpr int DS = D > 256 ? 2 : 1;
-  // at most 64 heads per workgroup: q fragments + O^T accumulators of 64 heads x D fill the
-  // register file of one CU at one wave per SIMD; more heads use several workgroups.
-  if (p.H <= 32) return launch_attn<FMT, D, NOPE, 1, DS>(p, rows, s);
-  if (p.H <= 128) return launch_attn<FMT, D, NOPE, 2, DS>(p, rows, s);
-  set_last_error("sparse_mqa: at most 128 heads (got %d)", p.H);
-  return MZK_EUNSUPPORTED;
+  if (p.H > 128) {
+    set_last_error("sparse_mqa: at most 128 heads (got %d)", p.H);
+    return MZK_EUNSUPPORTED;
+  }
+  if constexpr (D > 256) {
+    // 64 heads per workgroup, each 32-head group split by D over 4 waves
+    using M = SplitSmem<FMT, D, NOPE>;
+    static_assert(M::LDS <= 120 * 1024, "LDS budget");
+    auto kern = sparse_mqa_dsplit_kernel<FMT, D, NOPE>;
+    static bool attr_set = false;
+    if (!attr_set) {
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, M::LDS);
+      attr_set = true;
+    }
+    return launch_kernel(kern, M::LDS, 512, 64, p, rows, s);
+  } else {
+    if (p.H <= 32) return launch_kernel(sparse_mqa_kernel<FMT, D, NOPE, 1>, 0, 64, 32, p, rows, s);
+    return launch_kernel(sparse_mqa_kernel<FMT, D, NOPE, 2>, 0, 128, 64, p, rows, s);
+  }
 }
 
 int dispatch(int fmt, int D, int nope, const AttnParams& p, int64_t rows, hipStream_t s) {
@@ -573,6 +850,7 @@ extern "C" int mzk_sparse_mqa(const void* q, int64_t B, int64_t S, int H, int D,
   MZK_CHECK_ARG(rows <= 0x7fffffff, "sparse_mqa: too many rows");
   {
     const int64_t total_max = static_cast<int64_t>(window) + (dense ? dense_cap : 0) + (main_kv ? topk : 0);
+    MZK_CHECK_ARG(total_max < 0x7fffffff, "sparse_mqa: window + dense_cap + topk must stay below 2^31");
     const int64_t chunk = ((total_max + nsplit - 1) / nsplit + 31) / 32 * 32;
     MZK_CHECK_ARG(chunk <= kIdxCap, "sparse_mqa: %lld entries per split exceed %d; use nsplit >= %lld",
                   (long long)chunk, kIdxCap, (long long)((total_max + kIdxCap - 33) / (kIdxCap - 32)));
@@ -583,6 +861,7 @@ extern "C" int mzk_sparse_mqa(const void* q, int64_t B, int64_t S, int H, int D,
   }
   AttnParams p{};
   p.q = static_cast<const uint16_t*>(q);
+  p.rows = rows;
   p.S = S;
   p.positions = positions;
   p.win = static_cast<const uint8_t*>(win);

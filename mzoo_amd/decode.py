@@ -84,8 +84,7 @@ class SparseDecodeLayer:
         self.idx = torch.empty(b, cfg.topk, dtype=torch.int32, device=self.device)
         self.out = torch.empty(b, cfg.heads, cfg.dim, dtype=torch.bfloat16, device=self.device)
         self.lse = torch.empty(b, cfg.heads, dtype=torch.float32, device=self.device)
-        nbytes = csa2_attn.workspace_bytes(b, cfg.heads, cfg.dim, cfg.nsplit)
-        self.workspace = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=self.device)
+        self.workspace = csa2_attn.new_workspace(b, cfg.heads, cfg.dim, cfg.nsplit, self.device)
         self._slot_base = torch.arange(b, device=self.device, dtype=torch.int64) * cfg.window
         self._graph = None
         self._static = None

@@ -197,3 +197,20 @@ def test_decode_fp8_early_position_and_dense(dev):
     ref, ref_lse = _decode_oracle(q, win_c, main_c, dense_c, idx, sinks, pos, 128, 64, g)
     assert_attn_close(o, ref)
     torch.testing.assert_close(lse.cpu(), ref_lse, **LSE_TOL)
+
+
+def test_decode_workspace_reuse(dev):
+    """One workspace reused across calls gives identical results call after call, equal to
+    the oracle."""
+    b, h, gcap, topk, pos = 8, 128, 2048, 512, 8191
+    q, win_c, main_c, _, idx, sinks, g = _decode_case(dev, b, h, gcap, topk, pos, seed=5)
+    positions = torch.full((b,), pos, dtype=torch.int64, device=dev)
+    ns = 4
+    ws = MA.new_workspace(b, h, 576, ns, dev)
+    args = dict(main_cache=main_c, groups=g, indices=idx.to(dev), sinks=sinks.to(dev), nsplit=ns, workspace=ws)
+    o1, l1 = MA.sparse_mqa_decode(q.to(dev), positions, win_c, 128, **args)
+    o2, l2 = MA.sparse_mqa_decode(q.to(dev), positions, win_c, 128, **args)
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    ref, ref_lse = _decode_oracle(q, win_c, main_c, None, idx, sinks, pos, 128, 1, g)
+    assert_attn_close(o1, ref)
+    torch.testing.assert_close(l1.cpu(), ref_lse, **LSE_TOL)
