@@ -87,15 +87,18 @@ def time_launches(torch, fn, iters):
 
 def stage_times(torch, layer, inputs, iters):
     """Each kernel of the step alone, same inputs, same stream."""
-    from mzoo_amd import _lib, csa2_attn, indexer, quant
+    from mzoo_amd import _lib, indexer
     cfg = layer.cfg
     b = cfg.batch
     q, kv, q_idx, w = inputs
-    codes, scales = quant.quant_fp8_block(q_idx.view(b, 1, cfg.index_heads, cfg.index_dim), 128)
     pos = layer.positions.view(b, 1)
-    slots = layer._slot_base + layer.positions % cfg.window
     ws = layer.workspace
     st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+
+    def prologue():
+        _lib.call("mzk_decode_prologue", kv.data_ptr(), 1, b, cfg.nope, cfg.rope, layer.positions.data_ptr(),
+                  layer.win.data_ptr(), cfg.window, cfg.window, q_idx.data_ptr(), 1, b * cfg.index_heads,
+                  cfg.index_dim, 0, layer.q_codes.data_ptr(), layer.q_scales.data_ptr(), None, st())
 
     def attn():
         # split-KV attention and the split merge, as in the step
@@ -106,12 +109,10 @@ def stage_times(torch, layer, inputs, iters):
                   layer.lse.data_ptr(), st())
 
     stages = {
-        "window_append": lambda: quant.pack_latent_fp8_b128(kv, out=layer.win.view(-1, layer.win.shape[-1]),
-                                                            dst_index=slots),
-        "index_q_quant": lambda: quant.quant_fp8_block(q_idx.view(b, 1, cfg.index_heads, cfg.index_dim), 128),
-        "indexer_scores_fp8": lambda: indexer.scores_fp8(codes, scales[..., 0], w.view(b, 1, -1), layer.k_codes,
-                                                         layer.k_scales, compress_ratio=cfg.ratio, positions=pos,
-                                                         out=layer.scores),
+        "decode_prologue": prologue,
+        "indexer_scores_fp8": lambda: indexer.scores_fp8(layer.q_codes, layer.q_scales[..., 0], w.view(b, 1, -1),
+                                                         layer.k_codes, layer.k_scales, compress_ratio=cfg.ratio,
+                                                         positions=pos, out=layer.scores),
         "topk": lambda: indexer.topk(layer.scores.view(b, cfg.max_groups), cfg.topk, out=layer.idx),
         "sparse_mqa": attn,
     }

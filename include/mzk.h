@@ -79,6 +79,21 @@ int mzk_pack_latent_fp8_b128(const void* x, int dtype, int64_t rows, int nope, i
 int mzk_unpack_latent_fp8_b128(const uint8_t* cache, int64_t rows, int nope, int rope, void* y,
                                int dtype, void* stream);
 
+/* Decode-step prologue in one launch, for one new token per batch row:
+ *  (1) the token's latent kv [B, nope+rope] (kv_dtype) into its window-ring slot, entry
+ *      b*win_batch_entries + positions[b] % win_cap of win_cache (FP8-b128 entries as
+ *      mzk_pack_latent_fp8_b128) -- the window write of DeepseekV41CSACache.update
+ *      (owlet1/cache.py:84-94), with the ring slot derived on the device;
+ *  (2) the indexer query quantization (owlet1/indexer.py:129): q_idx [q_rows, q_dim]
+ *      (q_dtype) to FP8 b128 (q_format 0: q_codes [q_rows, q_dim] e4m3 + q_scales
+ *      [q_rows, q_dim/128] fp32, as mzk_quant_fp8_block) or MXFP4 (q_format 1: q_codes =
+ *      packed [q_rows, q_dim/2] + q_e8m0 [q_rows, q_dim/32], as mzk_quant_mxfp4). */
+int mzk_decode_prologue(const void* kv, int kv_dtype, int64_t B, int nope, int rope,
+                        const int64_t* positions, uint8_t* win_cache, int64_t win_batch_entries,
+                        int win_cap, const void* q_idx, int q_dtype, int64_t q_rows, int q_dim,
+                        int q_format, uint8_t* q_codes, float* q_scales, uint8_t* q_e8m0,
+                        void* stream);
+
 /* ---------------------------------------------------------------------------------
  * Piece 2: KV compressor and RoPE
  * --------------------------------------------------------------------------------- */

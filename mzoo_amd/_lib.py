@@ -36,6 +36,8 @@ _SIGS = {
     "mzk_dequant_fp8_block": [_P, _P, _I64, _I64, _I32, _P, _I32, _P],
     "mzk_dequant_mxfp4": [_P, _P, _I64, _I64, _P, _I32, _P],
     "mzk_pack_latent_fp8_b128": [_P, _I32, _I64, _I32, _I32, _P, _P, _P],
+    "mzk_decode_prologue": [_P, _I32, _I64, _I32, _I32, _P, _P, _I64, _I32, _P, _I32, _I64, _I32, _I32, _P, _P, _P,
+                            _P],
     "mzk_unpack_latent_fp8_b128": [_P, _I64, _I32, _I32, _P, _I32, _P],
     "mzk_topk_rows": [_P, _I64, _I64, _I64, _I32, _P, _I64, _P],
     "mzk_indexer_scores_fp8": [_P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P, _I64, _P],

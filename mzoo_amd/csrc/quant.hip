@@ -79,11 +79,11 @@ __global__ void fake_quant_serial_kernel(const void* __restrict__ x, void* __res
 
 // ---- packed encoders ---------------------------------------------------------------
 
+// Thread t encodes elements 4t..4t+3; the `group` consecutive threads of a block share
+// one amax (lane shuffles), so groups must not straddle a wave.
 template <int DT>
-__global__ void quant_fp8_block_kernel(const void* __restrict__ x, uint8_t* __restrict__ codes,
-                                       float* __restrict__ scales, int64_t nthreads, int group) {
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (t >= nthreads) return;
+__device__ __forceinline__ void quant_fp8_4(const void* __restrict__ x, uint8_t* __restrict__ codes,
+                                            float* __restrict__ scales, int64_t t, int group) {
   const int64_t base = t * 4;
   float v[4];
 #pragma unroll
@@ -99,10 +99,8 @@ __global__ void quant_fp8_block_kernel(const void* __restrict__ x, uint8_t* __re
 }
 
 template <int DT>
-__global__ void quant_mxfp4_kernel(const void* __restrict__ x, uint8_t* __restrict__ packed,
-                                   uint8_t* __restrict__ e8m0, int64_t nthreads) {
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (t >= nthreads) return;
+__device__ __forceinline__ void quant_mxfp4_4(const void* __restrict__ x, uint8_t* __restrict__ packed,
+                                              uint8_t* __restrict__ e8m0, int64_t t) {
   const int64_t base = t * 4;
   float v[4];
 #pragma unroll
@@ -116,6 +114,20 @@ __global__ void quant_mxfp4_kernel(const void* __restrict__ x, uint8_t* __restri
   const uint16_t two = static_cast<uint16_t>(c[0] | (c[1] << 4) | (c[2] << 8) | (c[3] << 12));
   reinterpret_cast<uint16_t*>(packed)[t] = two;
   if ((t & 7) == 0) e8m0[t >> 3] = static_cast<uint8_t>(__float_as_uint(s) >> 23);
+}
+
+template <int DT>
+__global__ void quant_fp8_block_kernel(const void* __restrict__ x, uint8_t* __restrict__ codes,
+                                       float* __restrict__ scales, int64_t nthreads, int group) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t < nthreads) quant_fp8_4<DT>(x, codes, scales, t, group);
+}
+
+template <int DT>
+__global__ void quant_mxfp4_kernel(const void* __restrict__ x, uint8_t* __restrict__ packed,
+                                   uint8_t* __restrict__ e8m0, int64_t nthreads) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t < nthreads) quant_mxfp4_4<DT>(x, packed, e8m0, t);
 }
 
 template <int DT>
@@ -145,14 +157,10 @@ __global__ void dequant_mxfp4_kernel(const uint8_t* __restrict__ packed, const u
 // 128-channel block), then the rope channels are rounded to bf16.
 
 template <int DT>
-__global__ void pack_latent_kernel(const void* __restrict__ x, int nope, int rope, const int64_t* __restrict__ dst,
-                                   uint8_t* __restrict__ cache) {
-  const int64_t row = blockIdx.x;
-  const int t = threadIdx.x;
+__device__ __forceinline__ void pack_latent_row(const void* __restrict__ x, int nope, int rope, int64_t row,
+                                                uint8_t* __restrict__ e, int t) {
   const int d = nope + rope;
   const int nb = nope / 128;
-  const int64_t entry_bytes = nope + 4 * nb + 2 * rope;
-  uint8_t* e = cache + (dst ? dst[row] : row) * entry_bytes;
   const int64_t xrow = row * d;
   if (t < nope / 4) {
     float v[4];
@@ -169,6 +177,36 @@ __global__ void pack_latent_kernel(const void* __restrict__ x, int nope, int rop
   }
   uint16_t* r = reinterpret_cast<uint16_t*>(e + nope + 4 * nb);
   for (int i = t; i < rope; i += blockDim.x) r[i] = f32_to_bf16(load_as_f32<DT>(x, xrow + nope + i));
+}
+
+template <int DT>
+__global__ void pack_latent_kernel(const void* __restrict__ x, int nope, int rope, const int64_t* __restrict__ dst,
+                                   uint8_t* __restrict__ cache) {
+  const int64_t row = blockIdx.x;
+  const int64_t entry_bytes = nope + 4 * (nope / 128) + 2 * rope;
+  pack_latent_row<DT>(x, nope, rope, row, cache + (dst ? dst[row] : row) * entry_bytes, threadIdx.x);
+}
+
+// Decode-step prologue: blocks 0..B-1 write the new token of row b into its window-ring
+// slot (b * win_batch_entries + positions[b] % win_cap); the remaining blocks quantize the
+// indexer queries (FP8 b128 or MXFP4), 256 threads x 4 elements each.
+template <int DT, int QDT, bool MX>
+__global__ void __launch_bounds__(256) decode_prologue_kernel(
+    const void* __restrict__ kv, int64_t B, int nope, int rope, const int64_t* __restrict__ positions,
+    uint8_t* __restrict__ win, int64_t win_batch_entries, int win_cap, const void* __restrict__ q, int64_t qthreads,
+    int qgroup, uint8_t* __restrict__ qcodes, float* __restrict__ qscales, uint8_t* __restrict__ qe8m0) {
+  const int64_t blk = blockIdx.x;
+  if (blk < B) {
+    const int64_t entry_bytes = nope + 4 * (nope / 128) + 2 * rope;
+    const int64_t slot = blk * win_batch_entries + positions[blk] % win_cap;
+    pack_latent_row<DT>(kv, nope, rope, blk, win + slot * entry_bytes, threadIdx.x);
+  } else {
+    const int64_t t = (blk - B) * 256 + threadIdx.x;
+    if (t < qthreads) {
+      if constexpr (MX) quant_mxfp4_4<QDT>(q, qcodes, qe8m0, t);
+      else quant_fp8_4<QDT>(q, qcodes, qscales, t, qgroup);
+    }
+  }
 }
 
 template <int DT>
@@ -268,10 +306,65 @@ void launch_unpack_latent(const uint8_t* cache, int64_t rows, int nope, int rope
   unpack_latent_kernel<DT><<<static_cast<unsigned>(rows), latent_threads(nope, rope), 0, s>>>(cache, nope, rope, y);
 }
 
+template <int DT, int QDT>
+int launch_prologue(const void* kv, int64_t B, int nope, int rope, const int64_t* positions, uint8_t* win,
+                    int64_t wbe, int wcap, const void* q, int64_t qrows, int qdim, int qfmt, uint8_t* qcodes,
+                    float* qscales, uint8_t* qe8m0, hipStream_t s) {
+  const int64_t qthreads = qrows * qdim / 4;
+  const unsigned grid = static_cast<unsigned>(B + (qthreads + 255) / 256);
+  if (qfmt == 0)
+    decode_prologue_kernel<DT, QDT, false><<<grid, 256, 0, s>>>(kv, B, nope, rope, positions, win, wbe, wcap, q,
+                                                                 qthreads, 32, qcodes, qscales, qe8m0);
+  else
+    decode_prologue_kernel<DT, QDT, true><<<grid, 256, 0, s>>>(kv, B, nope, rope, positions, win, wbe, wcap, q,
+                                                                qthreads, 8, qcodes, qscales, qe8m0);
+  return MZK_OK;
+}
+
+template <int DT>
+int launch_prologue_q(int qdt, const void* kv, int64_t B, int nope, int rope, const int64_t* positions, uint8_t* win,
+                      int64_t wbe, int wcap, const void* q, int64_t qrows, int qdim, int qfmt, uint8_t* qcodes,
+                      float* qscales, uint8_t* qe8m0, hipStream_t s) {
+  switch (qdt) {
+    case MZK_F32: return launch_prologue<DT, MZK_F32>(kv, B, nope, rope, positions, win, wbe, wcap, q, qrows, qdim, qfmt, qcodes, qscales, qe8m0, s);
+    case MZK_BF16: return launch_prologue<DT, MZK_BF16>(kv, B, nope, rope, positions, win, wbe, wcap, q, qrows, qdim, qfmt, qcodes, qscales, qe8m0, s);
+    case MZK_F16: return launch_prologue<DT, MZK_F16>(kv, B, nope, rope, positions, win, wbe, wcap, q, qrows, qdim, qfmt, qcodes, qscales, qe8m0, s);
+    default: set_last_error("decode_prologue: unsupported query dtype %d", qdt); return MZK_EINVAL;
+  }
+}
+
 }  // namespace
 }  // namespace mzk
 
 using namespace mzk;
+
+extern "C" int mzk_decode_prologue(const void* kv, int kv_dtype, int64_t B, int nope, int rope,
+                                   const int64_t* positions, uint8_t* win_cache, int64_t win_batch_entries,
+                                   int win_cap, const void* q_idx, int q_dtype, int64_t q_rows, int q_dim,
+                                   int q_format, uint8_t* q_codes, float* q_scales, uint8_t* q_e8m0, void* stream) {
+  MZK_CHECK_ARG(B >= 0 && q_rows >= 0, "decode_prologue: bad sizes");
+  MZK_CHECK_ARG(nope > 0 && nope % 128 == 0 && nope <= 1024 && rope >= 0 && rope % 2 == 0 && rope <= 256,
+                "decode_prologue: nope must be a multiple of 128 (<= 1024), rope even (<= 256)");
+  MZK_CHECK_ARG(win_cap >= 1 && win_batch_entries >= win_cap, "decode_prologue: bad window ring (cap %d)", win_cap);
+  MZK_CHECK_ARG(q_format == 0 || q_format == 1, "decode_prologue: q_format must be 0 (FP8 b128) or 1 (MXFP4)");
+  MZK_CHECK_ARG(q_format == 0 ? q_dim % 128 == 0 : q_dim % 32 == 0,
+                "decode_prologue: q_dim must be a multiple of %d", q_format == 0 ? 128 : 32);
+  if (B + q_rows == 0) return MZK_OK;
+  MZK_CHECK_ARG(!B || (kv && positions && win_cache), "decode_prologue: null kv / positions / window");
+  MZK_CHECK_ARG(!q_rows || (q_idx && q_codes && (q_format == 0 ? q_scales != nullptr : q_e8m0 != nullptr)),
+                "decode_prologue: null query buffers");
+  int rc;
+  hipStream_t s = as_stream(stream);
+  switch (kv_dtype) {
+    case MZK_F32: rc = launch_prologue_q<MZK_F32>(q_dtype, kv, B, nope, rope, positions, win_cache, win_batch_entries, win_cap, q_idx, q_rows, q_dim, q_format, q_codes, q_scales, q_e8m0, s); break;
+    case MZK_BF16: rc = launch_prologue_q<MZK_BF16>(q_dtype, kv, B, nope, rope, positions, win_cache, win_batch_entries, win_cap, q_idx, q_rows, q_dim, q_format, q_codes, q_scales, q_e8m0, s); break;
+    case MZK_F16: rc = launch_prologue_q<MZK_F16>(q_dtype, kv, B, nope, rope, positions, win_cache, win_batch_entries, win_cap, q_idx, q_rows, q_dim, q_format, q_codes, q_scales, q_e8m0, s); break;
+    default: set_last_error("decode_prologue: unsupported kv dtype %d", kv_dtype); return MZK_EINVAL;
+  }
+  if (rc) return rc;
+  MZK_LAUNCH_CHECK("decode_prologue");
+  return MZK_OK;
+}
 
 extern "C" int mzk_fake_quant_fp8_block(const void* x, void* y, int dtype, int64_t rows, int64_t n, int block_size,
                                         void* stream) {

@@ -19,8 +19,8 @@ preallocated on the device so the whole step records into one HIP graph:
   changes between steps.
 
 ``step(q, kv, q_idx, w)`` for one token per row:
-  1. pack the new token's latent into its ring slot,
-  2. quantize the indexer query (FP8 b128 per head, or MXFP4),
+  1+2. one launch: pack the new token's latent into its ring slot (derived on the device
+     from ``positions``) and quantize the indexer query (FP8 b128 per head, or MXFP4),
   3. indexer scores over all keys (group-causal ``-inf`` beyond ``(pos+1)//ratio``),
   4. top-k (lowest index wins ties),
   5. sparse MQA over window + [coarse] + top-k entries with the sink, split-KV + merge,
@@ -34,7 +34,7 @@ from dataclasses import dataclass
 
 import torch
 
-from . import csa2_attn, indexer, quant
+from . import _lib, csa2_attn, indexer, quant
 
 
 @dataclass
@@ -86,6 +86,13 @@ class SparseDecodeLayer:
         self.lse = torch.empty(b, cfg.heads, dtype=torch.float32, device=self.device)
         self.workspace = csa2_attn.new_workspace(b, cfg.heads, cfg.dim, cfg.nsplit, self.device)
         self._slot_base = torch.arange(b, device=self.device, dtype=torch.int64) * cfg.window
+        hi = cfg.index_heads
+        if cfg.index_format == "fp8":
+            self.q_codes = torch.empty(b, 1, hi, di, **u8)
+            self.q_scales = torch.empty(b, 1, hi, di // 128, dtype=torch.float32, device=self.device)
+        else:
+            self.q_codes = torch.empty(b, 1, hi, di // 2, **u8)
+            self.q_e8m0 = torch.empty(b, 1, hi, di // 32, **u8)
         self._graph = None
         self._static = None
 
@@ -133,17 +140,22 @@ class SparseDecodeLayer:
         if already in the ring), q_idx bf16 [B,Hi,Di] (rotated), w fp32 [B,Hi] (x Hi^-0.5)."""
         cfg = self.cfg
         b = cfg.batch
-        if kv is not None:
-            slots = self._slot_base + self.positions % cfg.window
-            quant.pack_latent_fp8_b128(kv, rope=cfg.rope, out=self.win.view(-1, self.win.shape[-1]), dst_index=slots)
+        fp8 = cfg.index_format == "fp8"
+        # window append + indexer-query quantization, one launch
+        kvc = None if kv is None else kv.contiguous()
+        qc = q_idx.contiguous()
+        _lib.require_gpu(qc, *(() if kvc is None else (kvc,)))
+        _lib.call("mzk_decode_prologue", _lib.ptr(kvc), _lib.dtype_code((qc if kvc is None else kvc).dtype),
+                  0 if kvc is None else b, cfg.nope, cfg.rope, self.positions.data_ptr(), self.win.data_ptr(),
+                  cfg.window, cfg.window, qc.data_ptr(), _lib.dtype_code(qc.dtype), b * cfg.index_heads,
+                  cfg.index_dim, 0 if fp8 else 1, self.q_codes.data_ptr(), self.q_scales.data_ptr() if fp8 else None,
+                  None if fp8 else self.q_e8m0.data_ptr(), _lib.stream_of(qc))
         pos = self.positions.view(b, 1)
-        if cfg.index_format == "fp8":
-            codes, scales = quant.quant_fp8_block(q_idx.view(b, 1, cfg.index_heads, cfg.index_dim), cfg.index_dim)
-            indexer.scores_fp8(codes, scales[..., 0], w.view(b, 1, -1), self.k_codes, self.k_scales,
+        if fp8:
+            indexer.scores_fp8(self.q_codes, self.q_scales[..., 0], w.view(b, 1, -1), self.k_codes, self.k_scales,
                                compress_ratio=cfg.ratio, positions=pos, out=self.scores)
         else:
-            packed, e8 = quant.quant_mxfp4(q_idx.view(b, 1, cfg.index_heads, cfg.index_dim))
-            indexer.scores_mxfp4(packed, e8, w.view(b, 1, -1), self.k_packed, self.k_e8m0,
+            indexer.scores_mxfp4(self.q_codes, self.q_e8m0, w.view(b, 1, -1), self.k_packed, self.k_e8m0,
                                  compress_ratio=cfg.ratio, positions=pos, out=self.scores)
         indexer.topk(self.scores.view(b, cfg.max_groups), cfg.topk, out=self.idx)
         csa2_attn.sparse_mqa_decode(q, self.positions, self.win, cfg.window, main_cache=self.main,

@@ -122,3 +122,40 @@ def test_unpack_bf16_all_codes_and_scales(dev):
     gnan, wnan = torch.isnan(got.float()), torch.isnan(want.float())
     assert torch.equal(gnan, wnan)
     assert torch.equal(got[~gnan].view(torch.int16), want[~wnan].view(torch.int16))
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp4"])
+def test_decode_prologue_bit_exact(dev, fmt):
+    """mzk_decode_prologue = the window-ring write of each row's new token (slot
+    positions[b] % W of row b) + the indexer-query quantization, bit-exact against the
+    oracle's packer and block quantizers."""
+    from mzoo_amd import _lib
+    b, w, hi, di = 5, 16, 8, 128
+    kv = _inputs(b, 576, 21, torch.bfloat16)
+    q = _inputs(b * hi, di, 22, torch.bfloat16)
+    pos = torch.tensor([0, 15, 16, 1000, 31], dtype=torch.int64)
+    win = torch.zeros(b, w, 656, dtype=torch.uint8, device=dev)
+    if fmt == "fp8":
+        codes = torch.empty(b * hi, di, dtype=torch.uint8, device=dev)
+        scales = torch.empty(b * hi, 1, dtype=torch.float32, device=dev)
+        e8 = None
+    else:
+        codes = torch.empty(b * hi, di // 2, dtype=torch.uint8, device=dev)
+        scales = None
+        e8 = torch.empty(b * hi, di // 32, dtype=torch.uint8, device=dev)
+    kvd, qd, posd = kv.to(dev), q.to(dev), pos.to(dev)
+    _lib.call("mzk_decode_prologue", kvd.data_ptr(), 1, b, 512, 64, posd.data_ptr(), win.data_ptr(), w, w,
+              qd.data_ptr(), 1, b * hi, di, 0 if fmt == "fp8" else 1, codes.data_ptr(), _lib.ptr(scales),
+              _lib.ptr(e8), torch.cuda.current_stream().cuda_stream)
+    want = Q.pack_latent_fp8_b128(kv.float().numpy())
+    wc = win.cpu().numpy()
+    for r in range(b):
+        assert np.array_equal(wc[r, int(pos[r]) % w], want[r])
+    if fmt == "fp8":
+        c_ref, s_ref = Q.fp8_block_codes(q.float().numpy(), 128)
+        assert np.array_equal(codes.cpu().numpy(), c_ref)
+        assert np.array_equal(scales.cpu().numpy().reshape(s_ref.shape).view(np.int32), s_ref.view(np.int32))
+    else:
+        p_ref, e_ref = Q.quant_mxfp4(q.float().numpy())
+        assert np.array_equal(codes.cpu().numpy(), p_ref)
+        assert np.array_equal(e8.cpu().numpy(), e_ref)
