@@ -28,8 +28,8 @@ FMT_BF16, FMT_FP8 = 0, 1
 
 
 def workspace_bytes(rows: int, heads: int, dim: int, nsplit: int) -> int:
-    """Split-KV workspace: the fp32 partials (O, m, l) of every split."""
-    return 0 if nsplit <= 1 else rows * nsplit * heads * (dim + 2) * 4
+    """Split-KV workspace: each split's output O/l in bf16, then its (m, l) in fp32."""
+    return 0 if nsplit <= 1 else rows * nsplit * heads * (2 * dim + 8)
 
 
 def new_workspace(rows: int, heads: int, dim: int, nsplit: int, device) -> torch.Tensor:

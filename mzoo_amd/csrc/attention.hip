@@ -81,8 +81,8 @@ struct AttnParams {
   // outputs
   uint16_t* out;  // [rows, H, D] bf16 (nsplit == 1)
   float* lse;     // [B, H, S]       (nsplit == 1)
-  float* part_o;  // [rows, nsplit, H, D]
-  float* part_ml; // [rows, nsplit, H, 2]
+  uint16_t* part_o;  // [rows, nsplit, H, D] bf16: the split's output O / l
+  float* part_ml;    // [rows, nsplit, H, 2]: the split's running max m (log2 units) and sum l
 };
 
 template <int FMT, int D, int NOPE>
@@ -358,15 +358,18 @@ __device__ __forceinline__ void write_result(const AttnParams& p, int64_t row, i
       p.lse[(b * p.H + head) * p.S + s_idx] = (m_fin + __log2f(l_fin)) * kLn2;
     }
   } else {
-    float* prow = p.part_o + ((row * p.nsplit + split) * p.H + head) * static_cast<int64_t>(D) + b_lo * 32;
+    // the split's own normalized output in bf16 (a split that saw no entry writes zeros)
+    const float inv_l = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    uint16_t* prow = p.part_o + ((row * p.nsplit + split) * p.H + head) * static_cast<int64_t>(D) + b_lo * 32;
 #pragma unroll
     for (int db = 0; db < NDBM; ++db) {
       if (db < nb) {
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
           const int d0 = db * 32 + 8 * g4 + 4 * half;
-          *reinterpret_cast<float4*>(prow + d0) =
-              float4{acc[db][4 * g4], acc[db][4 * g4 + 1], acc[db][4 * g4 + 2], acc[db][4 * g4 + 3]};
+          *reinterpret_cast<uint2*>(prow + d0) =
+              uint2{pack_bf16x2(acc[db][4 * g4] * inv_l, acc[db][4 * g4 + 1] * inv_l),
+                    pack_bf16x2(acc[db][4 * g4 + 2] * inv_l, acc[db][4 * g4 + 3] * inv_l)};
         }
       }
     }
@@ -721,45 +724,47 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
                           acc_o);
 }
 
-// Merge the split partials of one (row, head) with the sink: one workgroup per (row, head).
+// Merge the split partials with the sink: split s contributes its normalized output O_s
+// with weight l_s exp2(m_s - M) / L, where M = max(m_s, sink) and
+// L = sum_s l_s exp2(m_s - M) + exp2(sink - M).  One thread per 8 channels of a (row, head).
 template <int D>
-__global__ void __launch_bounds__(64) combine_kernel(const float* __restrict__ part_o, const float* __restrict__ part_ml,
-                                                     int nsplit, int H, int64_t S, const float* __restrict__ sinks,
-                                                     uint16_t* __restrict__ out, float* __restrict__ lse) {
-  const int64_t row = blockIdx.x;
-  const int head = blockIdx.y;
-  const int lane = threadIdx.x;
+__global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict__ part_o,
+                                                      const float* __restrict__ part_ml, int nsplit, int H, int64_t S,
+                                                      int64_t rows, const float* __restrict__ sinks,
+                                                      uint16_t* __restrict__ out, float* __restrict__ lse) {
+  constexpr int C8 = D / 8;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= rows * H * C8) return;
+  const int c = static_cast<int>(t % C8);
+  const int64_t rh = t / C8;
+  const int head = static_cast<int>(rh % H);
+  const int64_t row = rh / H;
+  const float* ml = part_ml + (row * nsplit * H + head) * 2;  // split s at + 2 s H
   float M = -__builtin_huge_valf();
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, part_ml[((row * nsplit + s) * H + head) * 2]);
+  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, ml[2 * s * H]);
   const float sk = sinks ? sinks[head] * kLog2e : -__builtin_huge_valf();
   M = fmaxf(M, sk);
   float L = sinks ? exp2f(sk - M) : 0.0f;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const uint16_t* po = part_o + (row * nsplit * H + head) * static_cast<int64_t>(D) + 8 * c;
   for (int s = 0; s < nsplit; ++s) {
-    const float m = part_ml[((row * nsplit + s) * H + head) * 2];
-    const float l = part_ml[((row * nsplit + s) * H + head) * 2 + 1];
-    if (m != -__builtin_huge_valf()) L = L + l * exp2f(m - M);
+    const float l = ml[2 * s * H + 1];
+    if (!(l > 0.0f)) continue;
+    const float wgt = l * exp2f(ml[2 * s * H] - M);
+    L = L + wgt;
+    const uint4 v = *reinterpret_cast<const uint4*>(po + static_cast<int64_t>(s) * H * D);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[2 * i] = acc[2 * i] + bf16_to_f32(static_cast<uint16_t>(w[i] & 0xffffu)) * wgt;
+      acc[2 * i + 1] = acc[2 * i + 1] + bf16_to_f32(static_cast<uint16_t>(w[i] >> 16)) * wgt;
+    }
   }
   const float inv = 1.0f / L;
-  for (int d = 4 * lane; d < D; d += 4 * 64) {
-    float4 acc = float4{0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < nsplit; ++s) {
-      const float m = part_ml[((row * nsplit + s) * H + head) * 2];
-      if (m == -__builtin_huge_valf()) continue;
-      const float wgt = exp2f(m - M);
-      const float4 o = *reinterpret_cast<const float4*>(part_o + ((row * nsplit + s) * H + head) * static_cast<int64_t>(D) + d);
-      acc.x = acc.x + o.x * wgt;
-      acc.y = acc.y + o.y * wgt;
-      acc.z = acc.z + o.z * wgt;
-      acc.w = acc.w + o.w * wgt;
-    }
-    const uint32_t w0 = f32_to_bf16(acc.x * inv) | (static_cast<uint32_t>(f32_to_bf16(acc.y * inv)) << 16);
-    const uint32_t w1 = f32_to_bf16(acc.z * inv) | (static_cast<uint32_t>(f32_to_bf16(acc.w * inv)) << 16);
-    *reinterpret_cast<uint2*>(out + (row * H + head) * static_cast<int64_t>(D) + d) = uint2{w0, w1};
-  }
-  if (lane == 0) {
-    const int64_t b = row / S, s_idx = row % S;
-    lse[(b * H + head) * S + s_idx] = (M + __log2f(L)) * kLn2;
-  }
+  *reinterpret_cast<uint4*>(out + rh * static_cast<int64_t>(D) + 8 * c) =
+      uint4{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv),
+            pack_bf16x2(acc[4] * inv, acc[5] * inv), pack_bf16x2(acc[6] * inv, acc[7] * inv)};
+  if (c == 0) lse[((row / S) * H + head) * S + row % S] = (M + __log2f(L)) * kLn2;
 }
 
 template <typename K>
@@ -818,10 +823,11 @@ int dispatch(int fmt, int D, int nope, const AttnParams& p, int64_t rows, hipStr
 }
 
 template <int D>
-void launch_combine(const float* po, const float* pml, int nsplit, int H, int64_t S, const float* sinks, uint16_t* out,
-                    float* lse, int64_t rows, hipStream_t s) {
-  combine_kernel<D><<<dim3(static_cast<unsigned>(rows), static_cast<unsigned>(H)), 64, 0, s>>>(po, pml, nsplit, H, S,
-                                                                                               sinks, out, lse);
+void launch_combine(const uint16_t* po, const float* pml, int nsplit, int H, int64_t S, const float* sinks,
+                    uint16_t* out, float* lse, int64_t rows, hipStream_t s) {
+  const int64_t n = rows * H * (D / 8);
+  combine_kernel<D><<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(po, pml, nsplit, H, S, rows, sinks, out,
+                                                                           lse);
 }
 
 }  // namespace
@@ -856,7 +862,7 @@ extern "C" int mzk_sparse_mqa(const void* q, int64_t B, int64_t S, int H, int D,
                   (long long)chunk, kIdxCap, (long long)((total_max + kIdxCap - 33) / (kIdxCap - 32)));
   }
   if (nsplit > 1) {
-    const int64_t need = rows * nsplit * static_cast<int64_t>(H) * (D + 2) * 4;
+    const int64_t need = rows * nsplit * static_cast<int64_t>(H) * (2 * D + 8);
     MZK_CHECK_ARG(workspace && workspace_bytes >= need, "sparse_mqa: workspace needs %lld bytes", (long long)need);
   }
   AttnParams p{};
@@ -884,8 +890,8 @@ extern "C" int mzk_sparse_mqa(const void* q, int64_t B, int64_t S, int H, int D,
   p.nsplit = nsplit;
   p.out = static_cast<uint16_t*>(out);
   p.lse = lse;
-  p.part_o = workspace;
-  p.part_ml = workspace ? workspace + rows * nsplit * static_cast<int64_t>(H) * D : nullptr;
+  p.part_o = reinterpret_cast<uint16_t*>(workspace);
+  p.part_ml = workspace ? reinterpret_cast<float*>(p.part_o + rows * nsplit * static_cast<int64_t>(H) * D) : nullptr;
   hipStream_t s = as_stream(stream);
   int rc = dispatch(fmt, D, nope, p, rows, s);
   if (rc) return rc;
@@ -900,8 +906,8 @@ extern "C" int mzk_sparse_mqa_combine(const float* workspace, int64_t B, int64_t
   const int64_t rows = B * S;
   if (rows == 0) return MZK_OK;
   MZK_CHECK_ARG(workspace && out && lse, "sparse_mqa_combine: null pointer");
-  const float* po = workspace;
-  const float* pml = workspace + rows * nsplit * static_cast<int64_t>(H) * D;
+  const uint16_t* po = reinterpret_cast<const uint16_t*>(workspace);
+  const float* pml = reinterpret_cast<const float*>(po + rows * nsplit * static_cast<int64_t>(H) * D);
   uint16_t* o = static_cast<uint16_t*>(out);
   hipStream_t s = as_stream(stream);
   switch (D) {
