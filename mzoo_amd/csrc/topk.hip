@@ -16,8 +16,8 @@
 //      are still to be taken.
 //   3. compaction in index order: take key > T, and the first `need_eq` entries with
 //      key == T; two block-wide exclusive scans per 4096-entry chunk give the ranks.
-// When the row fits (G <= kLdsKeys) the keys are staged once in LDS; otherwise every pass
-// re-reads the row (L2-resident after the first pass).
+// Rows up to 32 * 1024 keys keep them in registers (topk_rows_reg_kernel); longer rows
+// re-read the row every pass (L2-resident after the first pass).
 #include "common.h"
 
 namespace mzk {
@@ -62,6 +62,26 @@ __device__ __forceinline__ int block_excl_scan(int v, int* wsum, int& total) {
   return out;
 }
 
+// hist[bin] += 1 for every active lane.  The first radix pass sees few distinct digits
+// (scores share a handful of exponents), where per-lane LDS atomics would serialize on
+// the same addresses: two rounds aggregate the lanes of the lowest pending lane's bin with
+// a ballot (one atomic per round), the remaining lanes (spread digits) add individually.
+__device__ __forceinline__ void hist_add(int* hist, uint32_t bin, bool active) {
+  uint64_t pending = __ballot(active);
+#pragma unroll
+  for (int round = 0; round < 2; ++round) {
+    if (pending == 0) return;
+    const int leader = __builtin_ctzll(pending);
+    const uint32_t lb = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(bin), leader));
+    const bool mine = active && bin == lb;
+    const uint64_t same = __ballot(mine);
+    if ((threadIdx.x & 63) == leader) atomicAdd(&hist[lb], __popcll(same));
+    active = active && !mine;
+    pending &= ~same;
+  }
+  if (active) atomicAdd(&hist[bin], 1);
+}
+
 template <bool STAGE>
 __global__ void __launch_bounds__(kThreads) topk_rows_kernel(const float* __restrict__ scores, int64_t row_stride,
                                                              int G, int k, int32_t* __restrict__ out,
@@ -96,9 +116,11 @@ __global__ void __launch_bounds__(kThreads) topk_rows_kernel(const float* __rest
     for (int shift = 24; shift >= 0; shift -= 8) {
       for (int i = tid; i < 256; i += kThreads) hist[i] = 0;
       __syncthreads();
-      for (int i = tid; i < G; i += kThreads) {
-        const uint32_t kk = key_at(i);
-        if ((kk & mask) == prefix) atomicAdd(&hist[(kk >> shift) & 255u], 1);
+      // wave-uniform trip count, so every lane takes part in the ballots
+      for (int i0 = 0; i0 < G; i0 += kThreads) {
+        const int i = i0 + tid;
+        const uint32_t kk = i < G ? key_at(i) : 0u;
+        hist_add(hist, (kk >> shift) & 255u, i < G && (kk & mask) == prefix);
       }
       __syncthreads();
       if (tid < 64) {
@@ -171,6 +193,107 @@ __global__ void __launch_bounds__(kThreads) topk_rows_kernel(const float* __rest
   for (int i = written + tid; i < k; i += kThreads) dst[i] = -1;
 }
 
+// Rows of G <= KPT * kThreads: thread t holds keys t*KPT .. t*KPT+KPT-1 in registers.
+// Same selection as above with fewer workgroup barriers: the histogram is double-buffered
+// (the next pass clears the other copy), and the compaction needs one scan: the output
+// slot of an entry is (#key > T before it) + min(#key == T before it, need_eq), so a
+// single exclusive scan of the packed pair (n_gt << 16 | n_eq) gives every position.
+template <int KPT>
+__global__ void __launch_bounds__(kThreads) topk_rows_reg_kernel(const float* __restrict__ scores, int64_t row_stride,
+                                                                 int G, int k, int32_t* __restrict__ out,
+                                                                 int64_t out_stride) {
+  __shared__ int hist[2][256];
+  __shared__ int wsum[2 * kWaves + 1];
+  __shared__ uint32_t sel_digit[2];
+  __shared__ int sel_rem[2];
+
+  const int64_t row = blockIdx.x;
+  const float* src = scores + row * row_stride;
+  int32_t* dst = out + row * out_stride;
+  const int tid = threadIdx.x;
+  const int i0 = tid * KPT;
+
+  uint32_t key[KPT];
+  int nfin = 0;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    key[j] = (i0 + j < G) ? order_key(src[i0 + j]) : 0u;  // 0 sorts below -inf: never taken
+    nfin += key[j] > kNegInfKey;
+  }
+  if (tid < 256) hist[0][tid] = 0;
+  int total_fin;
+  block_excl_scan(nfin, wsum, total_fin);  // also publishes the cleared hist[0]
+
+  uint32_t T = kNegInfKey;
+  int need_eq = 0;
+  if (total_fin > k) {
+    uint32_t prefix = 0, mask = 0;
+    int rem = k;
+#pragma unroll 1
+    for (int pass = 0; pass < 4; ++pass) {
+      const int shift = 24 - 8 * pass;
+      const int cur = pass & 1;
+      if (tid < 256) hist[cur ^ 1][tid] = 0;  // the next pass's copy (last read two passes ago)
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) hist_add(hist[cur], (key[j] >> shift) & 255u, (key[j] & mask) == prefix);
+      __syncthreads();
+      if (tid < 64) {
+        const int lane = tid;
+        int h[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) h[j] = hist[cur][4 * lane + j];
+        const int s = h[0] + h[1] + h[2] + h[3];
+        int suf = s;  // inclusive suffix sum over lanes (higher lanes hold larger digits)
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const int o = __shfl_down(suf, off, 64);
+          if (lane + off < 64) suf += o;
+        }
+        int above = suf - s;
+#pragma unroll
+        for (int j = 3; j >= 0; --j) {
+          if (above < rem && rem <= above + h[j]) {
+            sel_digit[cur] = static_cast<uint32_t>(4 * lane + j);
+            sel_rem[cur] = rem - above;
+          }
+          above += h[j];
+        }
+      }
+      __syncthreads();
+      prefix |= sel_digit[cur] << shift;
+      mask |= 255u << shift;
+      rem = sel_rem[cur];
+    }
+    T = prefix;
+    need_eq = rem;
+  }
+
+  // compaction in index order
+  int n_gt = 0, n_eq = 0;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    n_gt += key[j] > T;
+    n_eq += (key[j] == T) && (T != kNegInfKey);
+  }
+  // packed as unsigned: n_gt <= G <= 32768 fills bit 31 at most, n_eq stays below 2^16
+  int tot_i;
+  const uint32_t pre = static_cast<uint32_t>(block_excl_scan((n_gt << 16) | n_eq, wsum, tot_i));
+  const uint32_t tot = static_cast<uint32_t>(tot_i);
+  int gt_before = static_cast<int>(pre >> 16), eq_before = static_cast<int>(pre & 0xffffu);
+  const int written = static_cast<int>(tot >> 16) + min(static_cast<int>(tot & 0xffffu), need_eq);
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    if (key[j] > T) {
+      dst[gt_before + min(eq_before, need_eq)] = i0 + j;
+      ++gt_before;
+    } else if (key[j] == T && T != kNegInfKey) {
+      if (eq_before < need_eq) dst[gt_before + eq_before] = i0 + j;
+      ++eq_before;
+    }
+  }
+  for (int i = written + tid; i < k; i += kThreads) dst[i] = -1;
+}
+
 }  // namespace
 }  // namespace mzk
 
@@ -186,12 +309,18 @@ extern "C" int mzk_topk_rows(const float* scores, int64_t rows, int64_t cols, in
   MZK_CHECK_ARG(rows <= 0x7fffffff, "topk_rows: too many rows");
   hipStream_t s = as_stream(stream);
   const int G = static_cast<int>(cols);
-  if (G <= kLdsKeys)
-    topk_rows_kernel<true><<<static_cast<unsigned>(rows), kThreads, static_cast<size_t>(G) * 4, s>>>(
-        scores, row_stride, G, topk, out, out_stride);
+  const unsigned nr = static_cast<unsigned>(rows);
+  if (G <= 8 * kThreads)
+    topk_rows_reg_kernel<8><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
+  else if (G <= 16 * kThreads)
+    topk_rows_reg_kernel<16><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
+  else if (G <= 32 * kThreads)
+    topk_rows_reg_kernel<32><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
+  else if (G <= kLdsKeys)
+    topk_rows_kernel<true><<<nr, kThreads, static_cast<size_t>(G) * 4, s>>>(scores, row_stride, G, topk, out,
+                                                                           out_stride);
   else
-    topk_rows_kernel<false><<<static_cast<unsigned>(rows), kThreads, 0, s>>>(scores, row_stride, G, topk, out,
-                                                                             out_stride);
+    topk_rows_kernel<false><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
   MZK_LAUNCH_CHECK("topk_rows");
   return MZK_OK;
 }
