@@ -113,9 +113,42 @@ indexer_scores_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q
   if (vis < 0) vis = 0;
   const float inv_sqrt_di = 1.0f / sqrt_rn(static_cast<float>(DI));
 
-  // A fragments (queries) and per-head coefficients, resident for the whole workgroup
+  const uint8_t* kb_base = k + b * k_batch_stride * RB;
+  const float* ks_base = FMT == kFp8 ? k_scale + b * k_batch_stride : nullptr;
+  const uint8_t* ke_base = FMT == kMxfp4 ? k_e8m0 + b * k_batch_stride * (DI / 32) : nullptr;
+  float* out = scores + row * score_stride;
+
+  const int64_t wave_key0 = static_cast<int64_t>(blockIdx.x) * kKeysPerWg + wave * (kNkb * 32);
+  // all key fragments of the wave's tiles are requested first -- before the query rows and
+  // head weights, and without waiting for the row's position -- so the workgroup pays one
+  // HBM round trip instead of three dependent ones (keys below G are always readable;
+  // invisible ones are masked at the end)
+  Frag bf[kNkb][NST];
+  float ksv[kNkb];  // FP8: the per-key scales
+#pragma unroll
+  for (int t = 0; t < kNkb; ++t) {
+    const int64_t g0 = wave_key0 + t * 32;
+    const int64_t g = g0 + (lane & 31);
+    const bool kv = g < G;
+    const uint8_t* krow = kb_base + (kv ? g : 0) * RB;
+    const uint8_t* kerow = FMT == kMxfp4 ? ke_base + (kv ? g : 0) * (DI / 32) : nullptr;
+#pragma unroll
+    for (int st = 0; st < NST; ++st) bf[t][st] = load_frag<FMT, DI>(krow, kerow, st, hi, kv);
+    ksv[t] = (FMT == kFp8 && kv) ? ks_base[g] : 1.0f;
+  }
+  // per-head coefficients w (x the FP8 query scale): one lane per head, through LDS, so
+  // a lane issues one load instead of one per accumulator row it needs
+  __shared__ float coef_s[64];
+  if (wave == 0) {
+    float c = 0.0f;
+    if (lane < Hi) {
+      c = w[row * Hi + lane];
+      if constexpr (FMT == kFp8) c = c * q_scale[row * Hi + lane];
+    }
+    coef_s[lane] = c;
+  }
+  // A fragments (queries), resident for the whole workgroup
   Frag a[MB][NST];
-  float coef[MB][16];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int h = mb * 32 + (lane & 31);
@@ -124,52 +157,36 @@ indexer_scores_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q
     const uint8_t* erow = FMT == kMxfp4 ? q_e8m0 + (row * Hi + (hv ? h : 0)) * (DI / 32) : nullptr;
 #pragma unroll
     for (int st = 0; st < NST; ++st) a[mb][st] = load_frag<FMT, DI>(qrow, erow, st, hi, hv);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int hr = mb * 32 + acc_row(j, lane);
-      float c = 0.0f;
-      if (hr < Hi) {
-        c = w[row * Hi + hr];
-        if constexpr (FMT == kFp8) c = c * q_scale[row * Hi + hr];
-      }
-      coef[mb][j] = c;
-    }
   }
+  __syncthreads();
+  float coef[MB][16];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) coef[mb][j] = coef_s[mb * 32 + acc_row(j, lane)];
 
-  const uint8_t* kb_base = k + b * k_batch_stride * RB;
-  const float* ks_base = FMT == kFp8 ? k_scale + b * k_batch_stride : nullptr;
-  const uint8_t* ke_base = FMT == kMxfp4 ? k_e8m0 + b * k_batch_stride * (DI / 32) : nullptr;
-  float* out = scores + row * score_stride;
-
-  const int64_t wave_key0 = static_cast<int64_t>(blockIdx.x) * kKeysPerWg + wave * (kNkb * 32);
-#pragma unroll 1
+#pragma unroll
   for (int t = 0; t < kNkb; ++t) {
     const int64_t g0 = wave_key0 + t * 32;
-    if (g0 >= G) break;
     const int64_t g = g0 + (lane & 31);
+    if (g0 >= G) break;
     if (g0 >= vis) {  // nothing in this tile is visible to the row
       if (lane < 32 && g < G) out[g] = -__builtin_huge_valf();
       continue;
     }
-    const bool kv = g < G;
-    const uint8_t* krow = kb_base + (kv ? g : 0) * RB;
-    const uint8_t* kerow = FMT == kMxfp4 ? ke_base + (kv ? g : 0) * (DI / 32) : nullptr;
-    Frag bf[NST];
-#pragma unroll
-    for (int st = 0; st < NST; ++st) bf[st] = load_frag<FMT, DI>(krow, kerow, st, hi, kv);
     float part = 0.0f;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
       v16f acc = {};
 #pragma unroll
-      for (int st = 0; st < NST; ++st) acc = mma<FMT>(a[mb][st], bf[st], acc);
+      for (int st = 0; st < NST; ++st) acc = mma<FMT>(a[mb][st], bf[t][st], acc);
 #pragma unroll
       for (int j = 0; j < 16; ++j) part = part + coef[mb][j] * fmaxf(acc[j], 0.0f);
     }
     const float total = part + __shfl_xor(part, 32, 64);
-    if (lane < 32 && kv) {
+    if (lane < 32 && g < G) {
       float s = total * inv_sqrt_di;
-      if constexpr (FMT == kFp8) s = s * ks_base[g];
+      if constexpr (FMT == kFp8) s = s * ksv[t];
       out[g] = (g < vis) ? s : -__builtin_huge_valf();
     }
   }
