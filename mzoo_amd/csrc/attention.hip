@@ -29,6 +29,8 @@
 //      Kt columns in the matching entry order.
 // The workgroup writes either the final bf16 output + lse (one split) or fp32 partials
 // (unnormalized O, running max m, sum l) that mzk combine kernel merges with the sink.
+#include <type_traits>
+
 #include "common.h"
 
 namespace mzk {
@@ -523,12 +525,14 @@ __global__ void __launch_bounds__(HG * 64) sparse_mqa_kernel(const AttnParams p)
 //   barrier A.  Wave ds finishes entries 8ds..8ds+7 of tile t (S^T registers 4ds..4ds+3):
 //      sums the four partials in D-part order and bounds the tile max by the sum of the
 //      partial maxima (an upper bound, so exp2(s - m) <= 2^kLazy still holds; the online
-//      softmax is exact for any reference point); its P^T quarter goes to LDS.  Meanwhile
-//      the workgroup dequantizes tile t+1 into Kt[(t+1)%2] and builds table t+2.
+//      softmax is exact for any reference point as long as no significant term underflows,
+//      which the pass checks at its end); its P^T quarter goes to LDS.  Meanwhile the
+//      workgroup dequantizes tile t+1 into Kt[(t+1)%2] and builds table t+3.
 //   barrier B.  O^T += V^T.P^T of tile t from Kt[t%2] and the S^T partial of tile t+1 from
 //      Kt[(t+1)%2], in one block so the two MFMA streams interleave; the partial and its
-//      per-head maximum are published; the pieces of tile t+2 are fetched.
-// Two barriers per tile.
+//      per-head maximum are published; the pieces of tile t+3 are fetched.
+// Two barriers per tile (three in the exact pass, which replaces the bound by the true
+// tile max).
 // ------------------------------------------------------------------------------------
 template <int FMT, int D, int NOPE>
 struct SplitSmem {
@@ -538,7 +542,8 @@ struct SplitSmem {
   static constexpr int SX = HG * DS * 4 * 64 * 16;        // [wave][4][64] float4 partial S^T
   static constexpr int PM = HG * 32 * 2 * DS * 4;         // [64 heads][8] partial maxima / row sums
   static constexpr int PB = HG * 2 * 64 * 16;             // [hg][2 K-steps][64] P^T
-  static constexpr int LDS = 2 * KT + SX + PM + PB;
+  static constexpr int PE = HG * 32 * 2 * DS * 4;         // [64 heads][8] true lane maxima
+  static constexpr int LDS = 2 * KT + SX + PM + PB + PE;
 };
 
 template <int FMT, int D, int NOPE>
@@ -551,7 +556,8 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
   constexpr int QST = D / 16 / DS;            // QK K-steps per wave
   constexpr int NB = D / 32;                  // 32-channel blocks of O
   constexpr int NDBM = (NB + DS - 1) / DS;    // most O blocks one wave owns
-  using RP = RowPlan<FMT, D, NOPE, NT>;
+  constexpr int NSLOT = 4;  // entry tables: t (mask), t+1, t+2 (fetched), t+3 (built, then fetched)
+  using RP = RowPlan<FMT, D, NOPE, NT, NSLOT>;
   static_assert((D / 16) % DS == 0 && D % 32 == 0, "D must split into 4 parts of 16-channel steps");
 
   extern __shared__ __align__(16) uint8_t smem[];
@@ -559,14 +565,17 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
   float4* sx = reinterpret_cast<float4*>(smem + 2 * M::KT);
   float* pm = reinterpret_cast<float*>(smem + 2 * M::KT + M::SX);
   uint4* pb = reinterpret_cast<uint4*>(smem + 2 * M::KT + M::SX + M::PM);
-  __shared__ const uint8_t* tab_ptr[2 * kTile];
-  __shared__ uint32_t tab_mask[2];
+  float* pe = reinterpret_cast<float*>(smem + 2 * M::KT + M::SX + M::PM + M::PB);
+  __shared__ const uint8_t* tab_ptr[NSLOT * kTile];
+  __shared__ uint32_t tab_mask[NSLOT];
   __shared__ int32_t sidx[kIdxCap];
+  __shared__ int redo;  // set when the fast pass's running max drifted too far above the truth
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int hg = wave / DS;
+  if (tid == 0) redo = 0;  // published by the barrier after the indices are staged
   const int ds = wave % DS;
   const int half = lane >> 5;
   RP rp;
@@ -591,14 +600,6 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
   }
   const int b_lo = ds * NB / DS;
   const int nb_mine = (ds + 1) * NB / DS - b_lo;
-  v16f acc_o[NDBM];
-#pragma unroll
-  for (int i = 0; i < NDBM; ++i) acc_o[i] = v16f{};
-  float m_run = -__builtin_huge_valf();  // identical in the 8 lanes x waves of a head
-  float l_run = 0.0f;                    // this lane's share of the head's row sum
-
-  Piece raw[RP::PPT];
-  int g_pref = -1;
   const int pv_off = pv_lane_offset<KT_PITCH>(lane, b_lo * 32);
   // S^T partial over this wave's D-quarter of the tile in `kt`; all K fragments are read
   // before the MFMA chain
@@ -626,102 +627,161 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
     for (int j4 = 0; j4 < 4; ++j4)
       sx[(wave * 4 + j4) * 64 + lane] = float4{s[4 * j4], s[4 * j4 + 1], s[4 * j4 + 2], s[4 * j4 + 3]};
   };
-  if (rp.ntiles > 0) {
-    rp.build_table(p, 0, tid < kTile ? rp.slot(rp.v_begin + tid) : -1, tid);
-    rp.build_table(p, 1, tid < kTile ? rp.slot(rp.v_begin + kTile + tid) : -1, tid);
-    if (tid < kTile) g_pref = rp.slot(rp.v_begin + 2 * kTile + tid);
-    __syncthreads();
-    rp.fetch(0, tid, raw);
-    rp.store(kt0, KT_PITCH, tid, raw);
-    if (rp.ntiles > 1) rp.fetch(1, tid, raw);
-    lds_barrier();  // Kt[0] complete
-    publish(qk(kt0));
-  }
 
+  // One pass over the split.  The fast pass raises the running max to the partial-maxima
+  // bound, which may exceed the true maximum; it tracks each head's true maximum on the
+  // side and gives up (returns false, writes nothing) if the final running max lies more
+  // than kBoundSlack above it.  Below that every entry that v_exp_f32 flushes to zero
+  // (argument < -126) weighs less than 2^-62 of the largest entry, so the result is exact
+  // to fp32 resolution.  The exact pass (only run after a fast pass gave up) exchanges
+  // the true tile max through LDS with one more barrier per tile.
+  constexpr float kBoundSlack = 64.0f;
+  auto pass = [&](auto exact_tag) -> bool {
+    constexpr bool kExact = decltype(exact_tag)::value;
+    v16f acc_o[NDBM];
+#pragma unroll
+    for (int i = 0; i < NDBM; ++i) acc_o[i] = v16f{};
+    float m_run = -__builtin_huge_valf();  // identical in the 8 lanes x waves of a head
+    float l_run = 0.0f;                    // this lane's share of the head's row sum
+    float m_seen = -__builtin_huge_valf(); // true max of this lane's (unmasked) entries
+
+    // the pieces of the next two tiles are in flight in registers (tile t+1 in one set, t+2
+    // in the other), so a tile's loads have two tile periods to arrive before dequantization
+    Piece raw_a[RP::PPT], raw_b[RP::PPT];
+    int g_pref = -1;
+    // One tile: enters with tile t's S^T partials published and `raw` holding tile t+1's
+    // pieces; leaves with tile t+1's partials published and `raw` holding tile t+3's.
+    auto tile_step = [&](int t, Piece (&raw)[RP::PPT]) {
+      const uint8_t* kt = kt0 + (t & 1) * M::KT;
+      uint8_t* kt_next = kt0 + ((t + 1) & 1) * M::KT;
+      const uint32_t vmask = tab_mask[t % NSLOT];  // read before barrier A; table t+4 replaces it later
+      lds_barrier();  // A: tile t's partials published; every wave is done with PV(t-1)
+
+      // dequantize tile t+1 into the buffer PV(t-1) has released
+      if (t + 1 < rp.ntiles) rp.store(kt_next, KT_PITCH, tid, raw);
+      rp.build_table(p, t + 3, g_pref, tid);
+      if (tid < kTile) g_pref = rp.slot(rp.v_begin + (t + 4) * kTile + tid);
+
+      // entries 8ds..8ds+7 of tile t for this lane's head
+      float4 a = sx[((hg * DS) * 4 + ds) * 64 + lane];
+#pragma unroll
+      for (int part = 1; part < DS; ++part) {
+        const float4 c = sx[((hg * DS + part) * 4 + ds) * 64 + lane];
+        a.x = a.x + c.x;
+        a.y = a.y + c.y;
+        a.z = a.z + c.z;
+        a.w = a.w + c.w;
+      }
+      float v4[4] = {a.x * p.scale_log2, a.y * p.scale_log2, a.z * p.scale_log2, a.w * p.scale_log2};
+      if (vmask != 0xffffffffu) {
+        const uint32_t bits = vmask >> (8 * ds + 4 * half);  // entries 8ds + 4half + i
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (!((bits >> i) & 1u)) v4[i] = -__builtin_huge_valf();
+      }
+      const float lane_max = fmaxf(fmaxf(v4[0], v4[1]), fmaxf(v4[2], v4[3]));
+      float bound;
+      if constexpr (kExact) {
+        // the head's true tile max: its 8 lanes' maxima through LDS (read back before
+        // barrier B; the next tile writes them after its barrier A)
+        pe[hl * 8 + 2 * ds + half] = lane_max;
+        lds_barrier();
+        const float4 t0 = *reinterpret_cast<const float4*>(pe + hl * 8);
+        const float4 t1 = *reinterpret_cast<const float4*>(pe + hl * 8 + 4);
+        bound = fmaxf(fmaxf(fmaxf(t0.x, t0.y), fmaxf(t0.z, t0.w)), fmaxf(fmaxf(t1.x, t1.y), fmaxf(t1.z, t1.w)));
+      } else {
+        m_seen = fmaxf(m_seen, lane_max);
+        const float4 t0 = *reinterpret_cast<const float4*>(pm + hl * 8);
+        const float4 t1 = *reinterpret_cast<const float4*>(pm + hl * 8 + 4);
+        bound = (((fmaxf(t0.x, t0.y) + fmaxf(t0.z, t0.w)) + fmaxf(t1.x, t1.y)) + fmaxf(t1.z, t1.w)) * p.scale_log2;
+      }
+      const bool raise = bound > m_run + kLazy;
+      if (__any(raise)) {  // identical in every wave of the head group
+        const float m_new = raise ? bound : m_run;
+        const float alpha = (m_run == -__builtin_huge_valf()) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run = l_run * alpha;
+#pragma unroll
+        for (int i = 0; i < NDBM; ++i) acc_o[i] = acc_o[i] * alpha;
+        m_run = m_new;
+      }
+      {
+        // the exact pass may see a head with no finite entry yet (m_run = -inf): then every
+        // entry is -inf and the reference point 0 gives exp2(-inf) = 0 instead of NaN
+        const float m_use = (kExact && m_run == -__builtin_huge_valf()) ? 0.0f : m_run;
+        const float p0 = __builtin_amdgcn_exp2f(v4[0] - m_use);
+        const float p1 = __builtin_amdgcn_exp2f(v4[1] - m_use);
+        const float p2 = __builtin_amdgcn_exp2f(v4[2] - m_use);
+        const float p3 = __builtin_amdgcn_exp2f(v4[3] - m_use);
+        l_run = l_run + ((p0 + p1) + (p2 + p3));
+        // PV K-step ks = ds/2 takes registers 8ks..8ks+7 = D-parts 2ks (slots 0-3), 2ks+1 (4-7)
+        uint2* dst = reinterpret_cast<uint2*>(pb + (hg * 2 + (ds >> 1)) * 64 + lane) + (ds & 1);
+        *dst = uint2{pack_bf16x2(p0, p1), pack_bf16x2(p2, p3)};
+      }
+      lds_barrier();  // B: P^T of tile t and Kt of tile t+1 complete, table t+3 visible
+
+      const uint4 w0 = pb[(hg * 2 + 0) * 64 + lane];
+      const uint4 w1 = pb[(hg * 2 + 1) * 64 + lane];
+      const v8bf pf0 = __builtin_bit_cast(v8bf, v4i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w});
+      const v8bf pf1 = __builtin_bit_cast(v8bf, v4i{(int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w});
+      // PV(t) and QK(t+1) in one block, so the two MFMA streams interleave; the fetch of
+      // tile t+3 is issued behind them.  After the last tile QK runs on the stale buffer; its
+      // result is published but never read.
+      const uint8_t* tr0 = kt + pv_off;
+#pragma unroll
+      for (int db = 0; db < NDBM - 1; ++db) pv_block<KT_PITCH>(tr0 + 64 * db, pf0, pf1, acc_o[db]);
+      const v16f s_next = qk(kt_next);
+      if (nb_mine == NDBM) pv_block<KT_PITCH>(tr0 + 64 * (NDBM - 1), pf0, pf1, acc_o[NDBM - 1]);
+      if (t + 3 < rp.ntiles) rp.fetch(t + 3, tid, raw);
+      publish(s_next);
+    };
+
+    if (rp.ntiles > 0) {
+#pragma unroll
+      for (int t = 0; t < 3; ++t) rp.build_table(p, t, tid < kTile ? rp.slot(rp.v_begin + t * kTile + tid) : -1, tid);
+      if (tid < kTile) g_pref = rp.slot(rp.v_begin + 3 * kTile + tid);
+      __syncthreads();
+      rp.fetch(0, tid, raw_a);
+      if (rp.ntiles > 1) rp.fetch(1, tid, raw_b);
+      rp.store(kt0, KT_PITCH, tid, raw_a);
+      if (rp.ntiles > 2) rp.fetch(2, tid, raw_a);
+      lds_barrier();  // Kt[0] complete
+      publish(qk(kt0));
+    }
+    // tile t dequantizes tile t+1 from the set that tile t-1 refilled: sets alternate
 #pragma unroll 1
-  for (int t = 0; t < rp.ntiles; ++t) {
-    const uint8_t* kt = kt0 + (t & 1) * M::KT;
-    uint8_t* kt_next = kt0 + ((t + 1) & 1) * M::KT;
-    const uint32_t vmask = tab_mask[t & 1];  // read before barrier A; table t+2 replaces it after
-    lds_barrier();  // A: tile t's partials published; every wave is done with PV(t-1)
-
-    // dequantize tile t+1 into the buffer PV(t-1) has released
-    if (t + 1 < rp.ntiles) rp.store(kt_next, KT_PITCH, tid, raw);
-    rp.build_table(p, t + 2, g_pref, tid);
-    if (tid < kTile) g_pref = rp.slot(rp.v_begin + (t + 3) * kTile + tid);
-
-    // entries 8ds..8ds+7 of tile t for this lane's head
-    float4 a = sx[((hg * DS) * 4 + ds) * 64 + lane];
-#pragma unroll
-    for (int part = 1; part < DS; ++part) {
-      const float4 c = sx[((hg * DS + part) * 4 + ds) * 64 + lane];
-      a.x = a.x + c.x;
-      a.y = a.y + c.y;
-      a.z = a.z + c.z;
-      a.w = a.w + c.w;
+    for (int t = 0; t < rp.ntiles; t += 2) {
+      tile_step(t, raw_b);
+      if (t + 1 < rp.ntiles) tile_step(t + 1, raw_a);
     }
-    float v4[4] = {a.x * p.scale_log2, a.y * p.scale_log2, a.z * p.scale_log2, a.w * p.scale_log2};
-    if (vmask != 0xffffffffu) {
-      const uint32_t bits = vmask >> (8 * ds + 4 * half);  // entries 8ds + 4half + i
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (!((bits >> i) & 1u)) v4[i] = -__builtin_huge_valf();
-    }
-    float bound;
+
+    // row sum: each lane holds the share of its entries (all scaled to the same running
+    // max); the 8 shares of a head are reduced in a fixed order
+    __syncthreads();  // every wave is done reading pm and pe
+    pm[hl * 8 + 2 * ds + half] = l_run;
+    if (!kExact) pe[hl * 8 + 2 * ds + half] = m_seen;
+    __syncthreads();
     {
       const float4 t0 = *reinterpret_cast<const float4*>(pm + hl * 8);
       const float4 t1 = *reinterpret_cast<const float4*>(pm + hl * 8 + 4);
-      bound = (((fmaxf(t0.x, t0.y) + fmaxf(t0.z, t0.w)) + fmaxf(t1.x, t1.y)) + fmaxf(t1.z, t1.w)) * p.scale_log2;
+      l_run = (((t0.x + t0.y) + (t0.z + t0.w)) + ((t1.x + t1.y) + (t1.z + t1.w)));
     }
-    const bool raise = bound > m_run + kLazy;
-    if (__any(raise)) {  // identical in every wave of the head group
-      const float m_new = raise ? bound : m_run;
-      const float alpha = (m_run == -__builtin_huge_valf()) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-      l_run = l_run * alpha;
-#pragma unroll
-      for (int i = 0; i < NDBM; ++i) acc_o[i] = acc_o[i] * alpha;
-      m_run = m_new;
+    if constexpr (!kExact) {
+      const float4 t0 = *reinterpret_cast<const float4*>(pe + hl * 8);
+      const float4 t1 = *reinterpret_cast<const float4*>(pe + hl * 8 + 4);
+      const float m_true =
+          fmaxf(fmaxf(fmaxf(t0.x, t0.y), fmaxf(t0.z, t0.w)), fmaxf(fmaxf(t1.x, t1.y), fmaxf(t1.z, t1.w)));
+      // a head with no unmasked entry (m_true = -inf) contributes nothing and is exact
+      if (head_ok && m_true > -__builtin_huge_valf() && m_run - m_true > kBoundSlack) redo = 1;
+      __syncthreads();
+      if (redo) return false;  // uniform: every wave reads the flag after the same barrier
     }
-    {
-      const float p0 = __builtin_amdgcn_exp2f(v4[0] - m_run);
-      const float p1 = __builtin_amdgcn_exp2f(v4[1] - m_run);
-      const float p2 = __builtin_amdgcn_exp2f(v4[2] - m_run);
-      const float p3 = __builtin_amdgcn_exp2f(v4[3] - m_run);
-      l_run = l_run + ((p0 + p1) + (p2 + p3));
-      // PV K-step ks = ds/2 takes registers 8ks..8ks+7 = D-parts 2ks (slots 0-3), 2ks+1 (4-7)
-      uint2* dst = reinterpret_cast<uint2*>(pb + (hg * 2 + (ds >> 1)) * 64 + lane) + (ds & 1);
-      *dst = uint2{pack_bf16x2(p0, p1), pack_bf16x2(p2, p3)};
-    }
-    lds_barrier();  // B: P^T of tile t and Kt of tile t+1 complete, table t+2 visible
+    if (head_ok)
+      write_result<D, NDBM>(p, rp.row, rp.b, rp.split, head, half, ds == 0 && half == 0, b_lo, nb_mine, m_run, l_run,
+                            acc_o);
+    return true;
+  };
 
-    if (t + 2 < rp.ntiles) rp.fetch(t + 2, tid, raw);
-    const uint4 w0 = pb[(hg * 2 + 0) * 64 + lane];
-    const uint4 w1 = pb[(hg * 2 + 1) * 64 + lane];
-    const v8bf pf0 = __builtin_bit_cast(v8bf, v4i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w});
-    const v8bf pf1 = __builtin_bit_cast(v8bf, v4i{(int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w});
-    // PV(t) and QK(t+1) in one block, so the two MFMA streams interleave.  After the last
-    // tile QK runs on the stale buffer; its result is published but never read.
-    const uint8_t* tr0 = kt + pv_off;
-#pragma unroll
-    for (int db = 0; db < NDBM - 1; ++db) pv_block<KT_PITCH>(tr0 + 64 * db, pf0, pf1, acc_o[db]);
-    const v16f s_next = qk(kt_next);
-    if (nb_mine == NDBM) pv_block<KT_PITCH>(tr0 + 64 * (NDBM - 1), pf0, pf1, acc_o[NDBM - 1]);
-    publish(s_next);
-  }
-
-  // row sum: each lane holds the share of its entries (all scaled to the same running max);
-  // the 8 shares of a head are reduced in a fixed order
-  __syncthreads();  // every wave is done reading pm
-  pm[hl * 8 + 2 * ds + half] = l_run;
-  __syncthreads();
-  {
-    const float4 t0 = *reinterpret_cast<const float4*>(pm + hl * 8);
-    const float4 t1 = *reinterpret_cast<const float4*>(pm + hl * 8 + 4);
-    l_run = (((t0.x + t0.y) + (t0.z + t0.w)) + ((t1.x + t1.y) + (t1.z + t1.w)));
-  }
-  if (head_ok)
-    write_result<D, NDBM>(p, rp.row, rp.b, rp.split, head, half, ds == 0 && half == 0, b_lo, nb_mine, m_run, l_run,
-                          acc_o);
+  if (!pass(std::false_type{})) pass(std::true_type{});
 }
 
 // Merge the split partials with the sink: split s contributes its normalized output O_s

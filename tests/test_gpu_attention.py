@@ -214,3 +214,19 @@ def test_decode_workspace_reuse(dev):
     ref, ref_lse = _decode_oracle(q, win_c, main_c, None, idx, sinks, pos, 128, 1, g)
     assert_attn_close(o1, ref)
     torch.testing.assert_close(l1.cpu(), ref_lse, **LSE_TOL)
+
+
+@pytest.mark.parametrize("nsplit", [1, 4])
+def test_decode_large_logit_range(dev, nsplit):
+    """Logits spread over hundreds of log2 units, so a later tile's max lies far above the
+    first tile's: the kernel's fixed-reference softmax must hand over to the rescaling one
+    and still match the oracle."""
+    b, h, gcap, topk, pos = 4, 128, 2048, 1024, 8191
+    q, win_c, main_c, _, idx, sinks, g = _decode_case(dev, b, h, gcap, topk, pos, seed=7)
+    q = (q.float() * 80.0).bfloat16()
+    positions = torch.full((b,), pos, dtype=torch.int64, device=dev)
+    o, lse = MA.sparse_mqa_decode(q.to(dev), positions, win_c, 128, main_cache=main_c, groups=g,
+                                  indices=idx.to(dev), sinks=sinks.to(dev), nsplit=nsplit)
+    ref, ref_lse = _decode_oracle(q, win_c, main_c, None, idx, sinks, pos, 128, 1, g)
+    assert_attn_close(o, ref)
+    torch.testing.assert_close(lse.cpu(), ref_lse, **LSE_TOL)
