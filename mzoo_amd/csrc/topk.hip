@@ -193,36 +193,154 @@ __global__ void __launch_bounds__(kThreads) topk_rows_kernel(const float* __rest
   for (int i = written + tid; i < k; i += kThreads) dst[i] = -1;
 }
 
-// Rows of G <= KPT * kThreads: thread t holds keys t*KPT .. t*KPT+KPT-1 in registers.
-// Same selection as above with fewer workgroup barriers: the histogram is double-buffered
-// (the next pass clears the other copy), and the compaction needs one scan: the output
-// slot of an entry is (#key > T before it) + min(#key == T before it, need_eq), so a
-// single exclusive scan of the packed pair (n_gt << 16 | n_eq) gives every position.
+// ---- rows of G <= KPT * kThreads, keys held in registers -----------------------------
+
+// Inclusive prefix sum over the 64 lanes with DPP: Kogge-Stone inside each row of 16
+// lanes (row_shr 1, 2, 4, 8), then row_bcast:15 adds row r's total to row r+1 (rows 1, 3)
+// and row_bcast:31 adds the total of rows 0-1 to rows 2-3.  Lanes a DPP source does not
+// reach, and rows the row mask leaves out, add 0.
+__device__ __forceinline__ int wave_incl_scan_dpp(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false); // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false); // row_bcast:31
+  return v;
+}
+
+// Every bin of the radix histogram has kSub counters, lane l adding to counter l % kSub:
+// lanes whose keys share a digit (the leading digits of similar scores) then collide on
+// at most 64 / kSub addresses per LDS atomic instead of all 64.
+constexpr int kSub = 16;
+constexpr int kHist = 256 * kSub;
+
+// Digit selection by one wave over a histogram.  The 16 KiB of counters are read with
+// consecutive lanes on consecutive 16 B (conflict-free): read r gives lane l the four
+// counters 4(l%4).. of bin 16r + l/4, a quad reduction completes each bin, and the 256 bin
+// totals go through `tot` so that lane l then owns bins 255-4l .. 252-4l in descending
+// order: an inclusive prefix over lanes counts the entries in higher bins.  Finds the bin
+// holding the rem-th largest key; returns its digit, the rank left inside it, and whether
+// the whole bin is taken (rank == count).
+struct DigitSel {
+  int digit, rem, whole;
+};
+__device__ __forceinline__ DigitSel select_digit(const int* hist, int* tot, int rem, int lane) {
+  static_assert(kSub == 16, "one int4 per lane covers a quarter of a bin");
+  const int4* h4 = reinterpret_cast<const int4*>(hist);
+  int part[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int4 v = h4[r * 64 + lane];
+    part[r] = (v.x + v.y) + (v.z + v.w);
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    // quad butterfly: lanes 4m..4m+3 all end with bin 16r + m's total
+    part[r] += __builtin_amdgcn_update_dpp(0, part[r], 0xb1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+    part[r] += __builtin_amdgcn_update_dpp(0, part[r], 0x4e, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+  }
+  // lane l stores bins 16r + l/4 for r = l%4, l%4+4, l%4+8, l%4+12
+#pragma unroll
+  for (int r4 = 0; r4 < 4; ++r4) {
+    int v = part[r4 * 4];
+#pragma unroll
+    for (int e = 1; e < 4; ++e)
+      if ((lane & 3) == e) v = part[r4 * 4 + e];
+    tot[16 * (r4 * 4 + (lane & 3)) + (lane >> 2)] = v;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int4 t4 = reinterpret_cast<const int4*>(tot)[63 - lane];  // bins 252-4l .. 255-4l
+  const int h[4] = {t4.w, t4.z, t4.y, t4.x};                      // h[j] = bin 255-4l-j
+  const int s = (h[0] + h[1]) + (h[2] + h[3]);
+  int above = wave_incl_scan_dpp(s) - s;
+  DigitSel res{0, 0, 0};
+  bool hit = false;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (above < rem && rem <= above + h[j]) {
+      res.digit = 255 - 4 * lane - j;
+      res.rem = rem - above;
+      res.whole = (rem - above) == h[j];
+      hit = true;
+    }
+    above += h[j];
+  }
+  // exactly one lane hits (the counts above the k-th key are < rem <= counts down to it)
+  const uint64_t m = __ballot(hit);
+  const int src_lane = m ? __builtin_ctzll(m) : 0;
+  res.digit = __builtin_amdgcn_readlane(res.digit, src_lane);
+  res.rem = __builtin_amdgcn_readlane(res.rem, src_lane);
+  res.whole = __builtin_amdgcn_readlane(res.whole, src_lane);
+  return res;
+}
+
+// Thread t holds keys t*KPT .. t*KPT+KPT-1.  The first digit's histogram is built while
+// the finite entries are counted, and a pass stops the search early when the bin of the
+// k-th largest key is taken whole (threshold: every key >= the bin's lowest key), which
+// for distinct scores usually happens after two or three of the four 8-bit digits.
+// Compaction: the output slot of an entry is (#key > T before it) +
+// min(#key == T before it, need_eq), so one exclusive scan of the packed pair
+// (n_gt << 16 | n_eq) gives every position.
 template <int KPT>
 __global__ void __launch_bounds__(kThreads) topk_rows_reg_kernel(const float* __restrict__ scores, int64_t row_stride,
                                                                  int G, int k, int32_t* __restrict__ out,
                                                                  int64_t out_stride) {
-  __shared__ int hist[2][256];
-  __shared__ int wsum[2 * kWaves + 1];
-  __shared__ uint32_t sel_digit[2];
-  __shared__ int sel_rem[2];
+  __shared__ __align__(16) int hist[2][kHist];
+  __shared__ __align__(16) int wsum[kWaves];
+  __shared__ int sel[2][3];  // digit, rem, whole of the pass using hist[p & 1]
+  __shared__ __align__(16) int bin_tot[256];
 
   const int64_t row = blockIdx.x;
   const float* src = scores + row * row_stride;
   int32_t* dst = out + row * out_stride;
   const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int i0 = tid * KPT;
 
+  float x[KPT];
+  if ((reinterpret_cast<uintptr_t>(src) & 15) == 0 && i0 + KPT <= G) {
+#pragma unroll
+    for (int j = 0; j < KPT; j += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(src + i0 + j);
+      x[j] = v.x;
+      x[j + 1] = v.y;
+      x[j + 2] = v.z;
+      x[j + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) x[j] = (i0 + j < G) ? src[i0 + j] : 0.0f;
+  }
+  {
+    int4* h4 = reinterpret_cast<int4*>(&hist[0][0]);
+    for (int i = tid; i < 2 * kHist / 4; i += kThreads) h4[i] = int4{0, 0, 0, 0};
+  }
+  __syncthreads();  // histograms cleared (while the scores are in flight)
+
   uint32_t key[KPT];
-  int nfin = 0;
+  int nfin = 0;  // wave-uniform
+  int* h0 = &hist[0][lane % kSub];
 #pragma unroll
   for (int j = 0; j < KPT; ++j) {
-    key[j] = (i0 + j < G) ? order_key(src[i0 + j]) : 0u;  // 0 sorts below -inf: never taken
-    nfin += key[j] > kNegInfKey;
+    key[j] = (i0 + j < G) ? order_key(x[j]) : 0u;  // 0 sorts below -inf: never taken
+    nfin += __popcll(__ballot(key[j] > kNegInfKey));
+    atomicAdd(h0 + (key[j] >> 24) * kSub, 1);
   }
-  if (tid < 256) hist[0][tid] = 0;
-  int total_fin;
-  block_excl_scan(nfin, wsum, total_fin);  // also publishes the cleared hist[0]
+  if (lane == 0) wsum[wave] = nfin;
+  __syncthreads();  // first histogram and the finite counts complete
+  int total_fin = 0;
+  {
+    const int4* w4 = reinterpret_cast<const int4*>(wsum);
+#pragma unroll
+    for (int q = 0; q < kWaves / 4; ++q) {
+      const int4 v = w4[q];
+      total_fin += (v.x + v.y) + (v.z + v.w);
+    }
+  }
 
   uint32_t T = kNegInfKey;
   int need_eq = 0;
@@ -233,39 +351,41 @@ __global__ void __launch_bounds__(kThreads) topk_rows_reg_kernel(const float* __
     for (int pass = 0; pass < 4; ++pass) {
       const int shift = 24 - 8 * pass;
       const int cur = pass & 1;
-      if (tid < 256) hist[cur ^ 1][tid] = 0;  // the next pass's copy (last read two passes ago)
-#pragma unroll
-      for (int j = 0; j < KPT; ++j) hist_add(hist[cur], (key[j] >> shift) & 255u, (key[j] & mask) == prefix);
-      __syncthreads();
-      if (tid < 64) {
-        const int lane = tid;
-        int h[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) h[j] = hist[cur][4 * lane + j];
-        const int s = h[0] + h[1] + h[2] + h[3];
-        int suf = s;  // inclusive suffix sum over lanes (higher lanes hold larger digits)
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-          const int o = __shfl_down(suf, off, 64);
-          if (lane + off < 64) suf += o;
+      if (wave == 0) {
+        const DigitSel r = select_digit(hist[cur], bin_tot, rem, lane);
+        if (lane == 0) {
+          sel[cur][0] = r.digit;
+          sel[cur][1] = r.rem;
+          sel[cur][2] = r.whole;
         }
-        int above = suf - s;
-#pragma unroll
-        for (int j = 3; j >= 0; --j) {
-          if (above < rem && rem <= above + h[j]) {
-            sel_digit[cur] = static_cast<uint32_t>(4 * lane + j);
-            sel_rem[cur] = rem - above;
-          }
-          above += h[j];
-        }
+      } else if (pass > 0) {
+        // the next pass's copy (its last reader, the selection two passes ago, is done);
+        // hist[1] is still clear for the second pass
+        int4* h4 = reinterpret_cast<int4*>(&hist[cur ^ 1][0]);
+        for (int i = tid - 64; i < kHist / 4; i += kThreads - 64) h4[i] = int4{0, 0, 0, 0};
       }
-      __syncthreads();
-      prefix |= sel_digit[cur] << shift;
+      __syncthreads();  // selection published, next copy cleared
+      const uint32_t digit = static_cast<uint32_t>(sel[cur][0]);
+      rem = sel[cur][1];
+      const uint32_t low = prefix | (digit << shift);
+      if (sel[cur][2] && low != 0u) {  // bin taken whole: every key >= low
+        T = low - 1u;
+        need_eq = 0;
+        break;
+      }
+      prefix = low;
       mask |= 255u << shift;
-      rem = sel_rem[cur];
+      if (shift == 0) {
+        T = prefix;
+        need_eq = rem;
+        break;
+      }
+      int* hn = &hist[cur ^ 1][lane % kSub];
+#pragma unroll
+      for (int j = 0; j < KPT; ++j)
+        if ((key[j] & mask) == prefix) atomicAdd(hn + ((key[j] >> (shift - 8)) & 255u) * kSub, 1);
+      __syncthreads();  // next histogram complete
     }
-    T = prefix;
-    need_eq = rem;
   }
 
   // compaction in index order
@@ -276,10 +396,26 @@ __global__ void __launch_bounds__(kThreads) topk_rows_reg_kernel(const float* __
     n_eq += (key[j] == T) && (T != kNegInfKey);
   }
   // packed as unsigned: n_gt <= G <= 32768 fills bit 31 at most, n_eq stays below 2^16
-  int tot_i;
-  const uint32_t pre = static_cast<uint32_t>(block_excl_scan((n_gt << 16) | n_eq, wsum, tot_i));
-  const uint32_t tot = static_cast<uint32_t>(tot_i);
-  int gt_before = static_cast<int>(pre >> 16), eq_before = static_cast<int>(pre & 0xffffu);
+  const int packed = (n_gt << 16) | n_eq;
+  const int incl = wave_incl_scan_dpp(packed);
+  __syncthreads();  // every wave is done reading wsum (finite counts)
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  uint32_t before = static_cast<uint32_t>(incl - packed), tot = 0;
+  {
+    const int4* w4 = reinterpret_cast<const int4*>(wsum);
+#pragma unroll
+    for (int q = 0; q < kWaves / 4; ++q) {
+      const int4 v = w4[q];
+      const int w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (4 * q + e < wave) before += static_cast<uint32_t>(w[e]);
+        tot += static_cast<uint32_t>(w[e]);
+      }
+    }
+  }
+  int gt_before = static_cast<int>(before >> 16), eq_before = static_cast<int>(before & 0xffffu);
   const int written = static_cast<int>(tot >> 16) + min(static_cast<int>(tot & 0xffffu), need_eq);
 #pragma unroll
   for (int j = 0; j < KPT; ++j) {

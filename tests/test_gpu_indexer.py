@@ -62,6 +62,26 @@ def test_topk_exact_with_ties(dev, rows, g, k):
     assert np.array_equal(got, want)
 
 
+
+@pytest.mark.parametrize("case", ["distinct", "near_lowest_float", "mixed_sign_few_exponents"])
+def test_topk_exact_distinct_and_extreme(dev, case):
+    """Distinct scores (the radix search usually stops once the k-th key's bin is taken
+    whole), finite scores next to -FLT_MAX (the k-th key's leading byte is 0), and scores
+    sharing a handful of exponents."""
+    gen = torch.Generator().manual_seed(11)
+    rows, g, k = 16, 8192, 2048
+    if case == "distinct":
+        sc = torch.randn(rows, g, generator=gen)
+    elif case == "near_lowest_float":
+        sc = -3.4e38 * (0.55 + 0.45 * torch.rand(rows, g, generator=gen))
+        sc[:, ::5] = float("-inf")
+    else:
+        sc = torch.sign(torch.randn(rows, g, generator=gen)) * torch.exp2(torch.randint(-2, 3, (rows, g), generator=gen).float())
+        sc = sc * (1 + torch.rand(rows, g, generator=gen) * 2 ** -20)
+    got = MI.topk(sc.to(dev), k).cpu().numpy()
+    want = OA.topk_indices(sc.numpy(), k)
+    assert np.array_equal(got, want)
+
 # ---- scores -----------------------------------------------------------------------------
 
 @pytest.mark.parametrize("hi", [4, 32, 64])
