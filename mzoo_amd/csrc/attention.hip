@@ -787,6 +787,8 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
 // Merge the split partials with the sink: split s contributes its normalized output O_s
 // with weight l_s exp2(m_s - M) / L, where M = max(m_s, sink) and
 // L = sum_s l_s exp2(m_s - M) + exp2(sink - M).  One thread per 8 channels of a (row, head).
+constexpr int kCombineRegSplits = 8;  // splits merged from registers in one round trip
+
 template <int D>
 __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict__ part_o,
                                                       const float* __restrict__ part_ml, int nsplit, int H, int64_t S,
@@ -800,25 +802,49 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
   const int head = static_cast<int>(rh % H);
   const int64_t row = rh / H;
   const float* ml = part_ml + (row * nsplit * H + head) * 2;  // split s at + 2 s H
-  float M = -__builtin_huge_valf();
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, ml[2 * s * H]);
-  const float sk = sinks ? sinks[head] * kLog2e : -__builtin_huge_valf();
-  M = fmaxf(M, sk);
-  float L = sinks ? exp2f(sk - M) : 0.0f;
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   const uint16_t* po = part_o + (row * nsplit * H + head) * static_cast<int64_t>(D) + 8 * c;
-  for (int s = 0; s < nsplit; ++s) {
-    const float l = ml[2 * s * H + 1];
-    if (!(l > 0.0f)) continue;
-    const float wgt = l * exp2f(ml[2 * s * H] - M);
+  const float sk = sinks ? sinks[head] * kLog2e : -__builtin_huge_valf();
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float M = sk, L;
+  // accumulate splits with weight l_s exp2(m_s - M); a split that saw no entry (l = 0)
+  // contributes nothing (its output is zeros, its m may be -inf)
+  auto add_split = [&](const float2 ms, const uint4 v) {
+    const float wgt = ms.y > 0.0f ? ms.y * exp2f(ms.x - M) : 0.0f;
     L = L + wgt;
-    const uint4 v = *reinterpret_cast<const uint4*>(po + static_cast<int64_t>(s) * H * D);
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       acc[2 * i] = acc[2 * i] + bf16_to_f32(static_cast<uint16_t>(w[i] & 0xffffu)) * wgt;
       acc[2 * i + 1] = acc[2 * i + 1] + bf16_to_f32(static_cast<uint16_t>(w[i] >> 16)) * wgt;
     }
+  };
+  if (nsplit <= kCombineRegSplits) {
+    // every split's (m, l) and output chunk requested at once: one memory round trip
+    float2 ms[kCombineRegSplits];
+    uint4 v[kCombineRegSplits];
+#pragma unroll
+    for (int s = 0; s < kCombineRegSplits; ++s) {
+      if (s < nsplit) {
+        ms[s] = *reinterpret_cast<const float2*>(ml + 2 * s * H);
+        v[s] = *reinterpret_cast<const uint4*>(po + static_cast<int64_t>(s) * H * D);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < kCombineRegSplits; ++s)
+      if (s < nsplit && ms[s].y > 0.0f) M = fmaxf(M, ms[s].x);
+    L = sinks ? exp2f(sk - M) : 0.0f;
+#pragma unroll
+    for (int s = 0; s < kCombineRegSplits; ++s)
+      if (s < nsplit) add_split(ms[s], v[s]);
+  } else {
+    for (int s = 0; s < nsplit; ++s) {
+      const float2 m = *reinterpret_cast<const float2*>(ml + 2 * s * H);
+      if (m.y > 0.0f) M = fmaxf(M, m.x);
+    }
+    L = sinks ? exp2f(sk - M) : 0.0f;
+    for (int s = 0; s < nsplit; ++s)
+      add_split(*reinterpret_cast<const float2*>(ml + 2 * s * H),
+                *reinterpret_cast<const uint4*>(po + static_cast<int64_t>(s) * H * D));
   }
   const float inv = 1.0f / L;
   *reinterpret_cast<uint4*>(out + rh * static_cast<int64_t>(D) + 8 * c) =
@@ -925,6 +951,9 @@ extern "C" int mzk_sparse_mqa(const void* q, int64_t B, int64_t S, int H, int D,
     const int64_t need = rows * nsplit * static_cast<int64_t>(H) * (2 * D + 8);
     MZK_CHECK_ARG(workspace && workspace_bytes >= need, "sparse_mqa: workspace needs %lld bytes", (long long)need);
   }
+  MZK_CHECK_ARG(aligned16(q) && aligned16(win) && aligned16(dense) && aligned16(main_kv) && aligned16(workspace) &&
+                    aligned16(out),
+                "sparse_mqa: q, caches, workspace and out must be 16-byte aligned");
   AttnParams p{};
   p.q = static_cast<const uint16_t*>(q);
   p.rows = rows;
@@ -966,6 +995,7 @@ extern "C" int mzk_sparse_mqa_combine(const float* workspace, int64_t B, int64_t
   const int64_t rows = B * S;
   if (rows == 0) return MZK_OK;
   MZK_CHECK_ARG(workspace && out && lse, "sparse_mqa_combine: null pointer");
+  MZK_CHECK_ARG(aligned16(workspace) && aligned16(out), "sparse_mqa_combine: workspace and out must be 16-byte aligned");
   const uint16_t* po = reinterpret_cast<const uint16_t*>(workspace);
   const float* pml = reinterpret_cast<const float*>(po + rows * nsplit * static_cast<int64_t>(H) * D);
   uint16_t* o = static_cast<uint16_t*>(out);

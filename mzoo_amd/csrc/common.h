@@ -30,6 +30,9 @@ void set_last_error(const char* fmt, ...);
     }                                                                               \
   } while (0)
 
+// Vector loads and stores of 16 bytes need 16-byte aligned base pointers (null passes).
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 #define MZK_LAUNCH_CHECK(name)                                                      \
   do {                                                                              \
     hipError_t _e = hipGetLastError();                                              \

@@ -230,3 +230,17 @@ def test_decode_large_logit_range(dev, nsplit):
     ref, ref_lse = _decode_oracle(q, win_c, main_c, None, idx, sinks, pos, 128, 1, g)
     assert_attn_close(o, ref)
     torch.testing.assert_close(lse.cpu(), ref_lse, **LSE_TOL)
+
+
+def test_decode_rejects_misaligned_query(dev):
+    """16-byte vector loads need aligned bases: a query view offset by one element is an
+    argument error, raised before any launch."""
+    b, h, gcap, topk, pos = 2, 128, 256, 64, 1023
+    q, win_c, main_c, _, idx, sinks, g = _decode_case(dev, b, h, gcap, topk, pos, seed=3)
+    positions = torch.full((b,), pos, dtype=torch.int64, device=dev)
+    flat = torch.empty(q.numel() + 1, dtype=q.dtype, device=dev)
+    q_off = flat[1:].view_as(q)
+    q_off.copy_(q.to(dev))
+    with pytest.raises(Exception, match="16-byte aligned"):
+        MA.sparse_mqa_decode(q_off, positions, win_c, 128, main_cache=main_c, groups=g, indices=idx.to(dev),
+                             sinks=sinks.to(dev), nsplit=2)
