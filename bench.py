@@ -91,30 +91,33 @@ def stage_times(torch, layer, inputs, iters):
     cfg = layer.cfg
     b = cfg.batch
     q, kv, q_idx, w = inputs
-    pos = layer.positions.view(b, 1)
     ws = layer.workspace
     st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
 
-    def prologue():
-        _lib.call("mzk_decode_prologue", kv.data_ptr(), 1, b, cfg.nope, cfg.rope, layer.positions.data_ptr(),
-                  layer.win.data_ptr(), cfg.window, cfg.window, q_idx.data_ptr(), 1, b * cfg.index_heads,
-                  cfg.index_dim, 0, layer.q_codes.data_ptr(), layer.q_scales.data_ptr(), None, st())
+    def indexer_decode():
+        # window append + indexer-query quantization + FP8 scores: the step's first launch
+        _lib.call("mzk_indexer_decode_fp8", q_idx.data_ptr(), w.data_ptr(), layer.k_codes.data_ptr(),
+                  layer.k_scales.data_ptr(), b, cfg.index_heads, cfg.index_dim, cfg.max_groups, cfg.max_groups,
+                  layer.positions.data_ptr(), cfg.ratio, layer.scores.data_ptr(), cfg.max_groups, None, None,
+                  kv.data_ptr(), cfg.nope, cfg.rope, layer.win.data_ptr(), cfg.window, cfg.window, st())
 
     def attn():
-        # split-KV attention and the split merge, as in the step
+        # the split-KV attention kernel alone: with no `out` the entry point writes the
+        # split partials into the workspace and launches nothing else
         _lib.call("mzk_sparse_mqa", q.data_ptr(), b, 1, cfg.heads, cfg.dim, 1, cfg.nope, layer.positions.data_ptr(),
                   layer.win.data_ptr(), cfg.window, cfg.window, cfg.window, None, 0, 0, 1, layer.main.data_ptr(),
                   cfg.max_groups, cfg.max_groups, layer.idx.data_ptr(), cfg.topk, cfg.topk,
-                  layer.sinks.data_ptr(), cfg.nsplit, ws.data_ptr(), ws.numel() * 4, layer.out.data_ptr(),
-                  layer.lse.data_ptr(), st())
+                  layer.sinks.data_ptr(), cfg.nsplit, ws.data_ptr(), ws.numel() * ws.element_size(), None, None, st())
+
+    def combine():
+        _lib.call("mzk_sparse_mqa_combine", ws.data_ptr(), b, 1, cfg.heads, cfg.dim, cfg.nsplit,
+                  layer.sinks.data_ptr(), layer.out.data_ptr(), layer.lse.data_ptr(), st())
 
     stages = {
-        "decode_prologue": prologue,
-        "indexer_scores_fp8": lambda: indexer.scores_fp8(layer.q_codes, layer.q_scales[..., 0], w.view(b, 1, -1),
-                                                         layer.k_codes, layer.k_scales, compress_ratio=cfg.ratio,
-                                                         positions=pos, out=layer.scores),
+        "indexer_decode_fp8": indexer_decode,
         "topk": lambda: indexer.topk(layer.scores.view(b, cfg.max_groups), cfg.topk, out=layer.idx),
         "sparse_mqa": attn,
+        "sparse_mqa_combine": combine,
     }
     return {k: time_launches(torch, f, iters) for k, f in stages.items()}
 
@@ -206,7 +209,7 @@ def main():
     attn_flops = rows * 4.0 * cfg.dim * cfg.heads * entries
     idx_bytes = rows * cfg.max_groups * IDX_KEY_BYTES
     idx_flops = rows * 2.0 * cfg.index_heads * cfg.index_dim * cfg.max_groups
-    dominant = max(("sparse_mqa", "indexer_scores_fp8", "topk"), key=lambda k: stages[k])
+    dominant = max(("sparse_mqa", "indexer_decode_fp8", "topk"), key=lambda k: stages[k])
     if dominant == "sparse_mqa":
         t = stages["sparse_mqa"] * 1e-6
         mfma_bound = attn_flops / (BF16_PEAK_TFLOPS * 1e12) > attn_bytes / (HBM_PEAK_GBS * 1e9)
@@ -214,7 +217,7 @@ def main():
             roof = {"bound": "mfma", "achieved": attn_flops / t / 1e12, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s"}
         else:
             roof = {"bound": "hbm", "achieved": attn_bytes / t / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s"}
-    elif dominant == "indexer_scores_fp8":
+    elif dominant == "indexer_decode_fp8":
         t = stages[dominant] * 1e-6
         roof = {"bound": "hbm", "achieved": idx_bytes / t / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s"}
     else:

@@ -145,6 +145,28 @@ int mzk_indexer_scores_mxfp4(const uint8_t* q_packed, const uint8_t* q_e8m0, con
                              const int64_t* positions, int ratio, float* scores,
                              int64_t score_stride, void* stream);
 
+/* Decode form of the FP8 indexer with the step's prologue fused in, one new token per
+ * batch row (S = 1): the bf16 indexer query q_idx [B, Hi, 128] is quantized in the kernel
+ * (FP8 b128, identical to mzk_quant_fp8_block with block_size 128 -- owlet1/indexer.py:129
+ * with owlet1/quant.py:72-86) and scored against k_codes / k_scales exactly as
+ * mzk_indexer_scores_fp8 would score the quantized query.  Optional extras, each written
+ * once per row:
+ *   q_codes [B, Hi, 128] e4m3 + q_scales [B, Hi] fp32 -- the quantized query (both or
+ *     neither);
+ *   kv [B, nope + rope] bf16 -- the new token's latent, appended to the window ring as
+ *     mzk_decode_prologue does (entry b*win_batch_entries + positions[b] % win_cap of
+ *     win_cache; owlet1/cache.py:84-94); NULL skips the append.
+ * Replaces mzk_decode_prologue + mzk_indexer_scores_fp8 in the decode step (one launch
+ * instead of two).  Di must be 128; nope a multiple of 128 up to 1024, rope even up to
+ * 256; positions required. */
+int mzk_indexer_decode_fp8(const void* q_idx, const float* w, const uint8_t* k_codes,
+                           const float* k_scales, int64_t B, int Hi, int Di, int64_t G,
+                           int64_t k_batch_stride, const int64_t* positions, int ratio,
+                           float* scores, int64_t score_stride, uint8_t* q_codes,
+                           float* q_scales, const void* kv, int nope, int rope,
+                           uint8_t* win_cache, int64_t win_batch_entries, int win_cap,
+                           void* stream);
+
 /* bf16 q [rows, Hi, Di] and k [B, G, Di] -- the contract of layers/attn/indexer/fwd.py:112. */
 int mzk_indexer_scores_bf16(const void* q, const float* w, const void* k, int64_t B, int64_t S,
                             int Hi, int Di, int64_t G, int64_t k_batch_stride,

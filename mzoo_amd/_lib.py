@@ -41,6 +41,8 @@ _SIGS = {
     "mzk_unpack_latent_fp8_b128": [_P, _I64, _I32, _I32, _P, _I32, _P],
     "mzk_topk_rows": [_P, _I64, _I64, _I64, _I32, _P, _I64, _P],
     "mzk_indexer_scores_fp8": [_P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P, _I64, _P],
+    "mzk_indexer_decode_fp8": [_P, _P, _P, _P, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P, _I64, _P, _P, _P, _I32, _I32,
+                               _P, _I64, _I32, _P],
     "mzk_indexer_scores_mxfp4": [_P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P, _I64, _P],
     "mzk_indexer_scores_bf16": [_P, _P, _P, _I64, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P, _I64, _P],
     "mzk_compress": [_P, _P, _I64, _I64, _I32, _I32, _I64, _P, _I32, _F32, _P, _I32, _P],

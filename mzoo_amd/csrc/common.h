@@ -160,6 +160,16 @@ __device__ __forceinline__ float e4m3_decode(uint32_t c) {
   return (c & 0x80u) ? -v : v;
 }
 
+// FP8 block scale of the reference's fake quantizer (owlet1/quant.py:72-86):
+// s = pow2ceil(max(amax, 1e-4) * fp32(1/448)); codes are e4m3(clamp(x / s, +-448)).
+constexpr float kInv448 = 1.0f / 448.0f;  // the fp32-rounded reciprocal the reference multiplies by
+
+__device__ __forceinline__ float fp8_scale_from_amax(float amax) {
+  return pow2_ceil(fmaxf(amax, 1e-4f) * kInv448);
+}
+
+__device__ __forceinline__ float clampf(float v, float lim) { return fminf(fmaxf(v, -lim), lim); }
+
 // ------------------------------------------------------------------------------------
 // FP4 e2m1 codes.  code = number of thresholds <= |q| (ties at 0.25/1.25/2.5/5 round
 // down, at 0.75/1.75/3.5 round up), sign in bit 3 from the sign bit (-0 -> 8).

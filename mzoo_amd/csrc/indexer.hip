@@ -54,15 +54,15 @@ struct Frag {
   int scale;  // e8m0 byte (kMxfp4 only)
 };
 
-// Load the operand fragment of step `st` for a row `r` of length Di.  Lane half `hi`
-// (lane / 32) selects which half of the step's channels the lane carries.
+// Load the operand fragment of step `st` from a (valid) row of length Di.  Lane half `hi`
+// (lane / 32) selects which half of the step's channels the lane carries.  No branch: the
+// callers clamp out-of-range rows to a readable one, so every load is issued on every lane
+// and the in-order wait counts stay exact.
 template <int FMT, int DI>
 __device__ __forceinline__ Frag load_frag(const uint8_t* __restrict__ rowp, const uint8_t* __restrict__ e8m0row,
-                                          int st, int hi, bool valid) {
+                                          int st, int hi) {
   Frag f;
-  f.v = v8i{0, 0, 0, 0, 0, 0, 0, 0};
   f.scale = 127;
-  if (!valid) return f;
   if constexpr (FMT == kFp8) {
     const uint4* p = reinterpret_cast<const uint4*>(rowp + st * 64 + hi * 32);
     const uint4 a = p[0], b = p[1];
@@ -75,6 +75,14 @@ __device__ __forceinline__ Frag load_frag(const uint8_t* __restrict__ rowp, cons
     const uint4 a = *reinterpret_cast<const uint4*>(rowp + st * 32 + hi * 16);
     f.v = v8i{(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};
   }
+  return f;
+}
+
+// The zero fragment in place of `f` where `keep` is false (rows beyond the operand).
+__device__ __forceinline__ Frag keep_or_zero(Frag f, bool keep) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) f.v[i] = keep ? f.v[i] : 0;
+  f.scale = keep ? f.scale : 127;
   return f;
 }
 
@@ -94,76 +102,175 @@ __device__ __forceinline__ v16f mma(const Frag& a, const Frag& b, v16f c) {
 // head row held by value j of a 32x32 f32 accumulator in lane l (of m-block mb)
 __device__ __forceinline__ int acc_row(int j, int lane) { return 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3); }
 
-template <int FMT, int DI, int MB>
-__global__ void __launch_bounds__(kWaves * 64)
-indexer_scores_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_scale, const uint8_t* __restrict__ q_e8m0,
-                      const float* __restrict__ w, const uint8_t* __restrict__ k, const float* __restrict__ k_scale,
-                      const uint8_t* __restrict__ k_e8m0, int64_t S, int Hi, int64_t G, int64_t k_batch_stride,
-                      const int64_t* __restrict__ positions, int ratio, float* __restrict__ scores, int64_t score_stride) {
+struct IdxParams {
+  const uint8_t* q;  // quantized / bf16 query operand [rows, Hi, row_bytes]
+  const float* q_scale;
+  const uint8_t* q_e8m0;
+  const float* w;
+  const uint8_t* k;
+  const float* k_scale;
+  const uint8_t* k_e8m0;
+  int64_t S;
+  int Hi;
+  int64_t G, kbs;
+  const int64_t* positions;
+  int ratio;
+  float* scores;
+  int64_t sstride;
+  // fused decode prologue (FP8, Di = 128): the bf16 query is quantized in the kernel, and
+  // workgroup 0 of each row stores the codes / scales and appends the new latent
+  const uint16_t* q_raw;  // [rows, Hi, 128] bf16
+  uint8_t* q_codes_out;   // [rows, Hi, 128] e4m3, or null
+  float* q_scales_out;    // [rows, Hi], or null
+  const uint16_t* kv;     // [rows, nope + rope] bf16 (APPEND)
+  int nope, rope;
+  uint8_t* win;
+  int64_t win_batch_entries;
+  int win_cap;
+};
+
+constexpr int kQPitch = 128 + 16;  // LDS bytes per quantized head row (padding spreads banks)
+
+// One workgroup = 4 waves = one query row x kKeysPerWg keys (see the tiling note above).
+// QRAW: the query arrives as bf16 [Hi, 128] and each workgroup quantizes it (FP8 b128 of
+// owlet1/quant.py:72-86: one power-of-two scale per head) into LDS -- thread t owns head
+// t/4, channels 32(t%4)..+31 -- with v_cvt_pk_fp8_f32, which equals the e4m3 encoder of
+// the quantizer (round to nearest even, subnormals kept) for every |x| <= 448.
+// APPEND: workgroup 0 of the row also writes the new token's FP8-b128 latent into its
+// window-ring slot (b * win_batch_entries + pos % win_cap).
+template <int FMT, int DI, int MB, bool QRAW, bool APPEND>
+__global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxParams p) {
+  static_assert(!QRAW || (FMT == kFp8 && DI == 128), "in-kernel quantization: FP8 b128 queries only");
   constexpr int NST = DI / Step<FMT>::K;
   constexpr int RB = row_bytes<FMT>(DI);
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int hi = lane >> 5;
   const int64_t row = blockIdx.y;
-  const int64_t b = row / S;
-  const int64_t pos = positions ? positions[row] : row % S;
-  int64_t vis = (pos + 1) / ratio;
-  if (vis > G) vis = G;
-  if (vis < 0) vis = 0;
+  const int64_t b = row / p.S;
+  const int Hi = p.Hi;
+  const int64_t G = p.G;
   const float inv_sqrt_di = 1.0f / sqrt_rn(static_cast<float>(DI));
 
-  const uint8_t* kb_base = k + b * k_batch_stride * RB;
-  const float* ks_base = FMT == kFp8 ? k_scale + b * k_batch_stride : nullptr;
-  const uint8_t* ke_base = FMT == kMxfp4 ? k_e8m0 + b * k_batch_stride * (DI / 32) : nullptr;
-  float* out = scores + row * score_stride;
+  const uint8_t* kb_base = p.k + b * p.kbs * RB;
+  const float* ks_base = FMT == kFp8 ? p.k_scale + b * p.kbs : nullptr;
+  const uint8_t* ke_base = FMT == kMxfp4 ? p.k_e8m0 + b * p.kbs * (DI / 32) : nullptr;
+  float* out = p.scores + row * p.sstride;
 
   const int64_t wave_key0 = static_cast<int64_t>(blockIdx.x) * kKeysPerWg + wave * (kNkb * 32);
-  // all key fragments of the wave's tiles are requested first -- before the query rows and
-  // head weights, and without waiting for the row's position -- so the workgroup pays one
-  // HBM round trip instead of three dependent ones (keys below G are always readable;
-  // invisible ones are masked at the end)
+  // Load order.  Vector-memory loads complete in issue order, so the small operands every
+  // tile needs -- the query (fragments, or the bf16 rows to quantize) and the head
+  // weights -- go first; then all key fragments of the wave's tiles, so tile 0's MFMAs
+  // start while the later tiles are still arriving.  No load waits for the row's position
+  // and none sits behind a branch (out-of-range rows are clamped to readable ones), so the
+  // compiler's in-order wait counts stay exact.
+  Frag a[MB][NST];
+  uint4 qr[4];  // QRAW: 32 bf16 channels of head tid/4
+  const int qh = tid >> 2, qc = tid & 3;
+  if constexpr (QRAW) {
+    const int hq = qh < Hi ? qh : Hi - 1;
+    const uint4* src = reinterpret_cast<const uint4*>(p.q_raw + (row * Hi + hq) * 128 + 32 * qc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qr[i] = src[i];
+  } else {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int h = mb * 32 + (lane & 31);
+      const bool hv = h < Hi;
+      const uint8_t* qrow = p.q + (row * Hi + (hv ? h : 0)) * static_cast<int64_t>(RB);
+      const uint8_t* erow = FMT == kMxfp4 ? p.q_e8m0 + (row * Hi + (hv ? h : 0)) * (DI / 32) : nullptr;
+#pragma unroll
+      for (int st = 0; st < NST; ++st) a[mb][st] = keep_or_zero(load_frag<FMT, DI>(qrow, erow, st, hi), hv);
+    }
+  }
+  // per-head coefficients w (x the FP8 query scale): lane h loads head h's, and every lane
+  // then gathers the 16 rows of its accumulators with cross-lane reads
+  const int hl = lane < Hi ? lane : Hi - 1;
+  float cw = p.w[row * Hi + hl];
+  float cq = 1.0f;
+  if constexpr (FMT == kFp8 && !QRAW) cq = p.q_scale[row * Hi + hl];
+  cw = lane < Hi ? cw : 0.0f;
   Frag bf[kNkb][NST];
   float ksv[kNkb];  // FP8: the per-key scales
 #pragma unroll
   for (int t = 0; t < kNkb; ++t) {
-    const int64_t g0 = wave_key0 + t * 32;
-    const int64_t g = g0 + (lane & 31);
-    const bool kv = g < G;
-    const uint8_t* krow = kb_base + (kv ? g : 0) * RB;
-    const uint8_t* kerow = FMT == kMxfp4 ? ke_base + (kv ? g : 0) * (DI / 32) : nullptr;
+    // keys at or beyond G read row G-1 instead: their score columns are never written
+    const int64_t g = wave_key0 + t * 32 + (lane & 31);
+    const int64_t gc = g < G ? g : G - 1;
+    const uint8_t* krow = kb_base + gc * RB;
+    const uint8_t* kerow = FMT == kMxfp4 ? ke_base + gc * (DI / 32) : nullptr;
 #pragma unroll
-    for (int st = 0; st < NST; ++st) bf[t][st] = load_frag<FMT, DI>(krow, kerow, st, hi, kv);
-    ksv[t] = (FMT == kFp8 && kv) ? ks_base[g] : 1.0f;
+    for (int st = 0; st < NST; ++st) bf[t][st] = load_frag<FMT, DI>(krow, kerow, st, hi);
+    ksv[t] = FMT == kFp8 ? ks_base[gc] : 1.0f;
   }
-  // per-head coefficients w (x the FP8 query scale): one lane per head, through LDS, so
-  // a lane issues one load instead of one per accumulator row it needs
-  __shared__ float coef_s[64];
-  if (wave == 0) {
-    float c = 0.0f;
-    if (lane < Hi) {
-      c = w[row * Hi + lane];
-      if constexpr (FMT == kFp8) c = c * q_scale[row * Hi + lane];
+  // APPEND: thread t's share of the new latent (nope channels 4t..4t+3, rope channel t),
+  // loaded by every workgroup (clamped), packed by workgroup 0 at the end
+  uint2 kv_nope = uint2{0u, 0u};
+  uint16_t kv_rope = 0;
+  if constexpr (APPEND) {
+    const uint16_t* kvrow = p.kv + row * (p.nope + p.rope);
+    const int tn = tid < p.nope / 4 ? tid : p.nope / 4 - 1;
+    const int tr = tid < p.rope ? tid : p.rope - 1;
+    kv_nope = *reinterpret_cast<const uint2*>(kvrow + 4 * tn);
+    kv_rope = kvrow[p.nope + tr];
+  }
+  const int64_t pos = p.positions ? p.positions[row] : row % p.S;
+  int64_t vis = (pos + 1) / p.ratio;
+  if (vis > G) vis = G;
+  if (vis < 0) vis = 0;
+
+  __shared__ __align__(16) uint8_t q_lds[QRAW ? 64 * kQPitch : 16];
+  __shared__ float qs_lds[QRAW ? 64 : 1];
+  if constexpr (QRAW) {
+    float x[32];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t wv[4] = {qr[i].x, qr[i].y, qr[i].z, qr[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        x[8 * i + 2 * j] = qh < Hi ? bf16_to_f32(static_cast<uint16_t>(wv[j] & 0xffffu)) : 0.0f;
+        x[8 * i + 2 * j + 1] = qh < Hi ? bf16_to_f32(static_cast<uint16_t>(wv[j] >> 16)) : 0.0f;
+      }
     }
-    coef_s[lane] = c;
-  }
-  // A fragments (queries), resident for the whole workgroup
-  Frag a[MB][NST];
+    float amax = 0.0f;
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    const int h = mb * 32 + (lane & 31);
-    const bool hv = h < Hi;
-    const uint8_t* qrow = q + (row * Hi + (hv ? h : 0)) * static_cast<int64_t>(RB);
-    const uint8_t* erow = FMT == kMxfp4 ? q_e8m0 + (row * Hi + (hv ? h : 0)) * (DI / 32) : nullptr;
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
+    amax = wave_max_group(amax, 4);  // the 4 threads of a head are consecutive lanes
+    const float sc = fp8_scale_from_amax(amax);
+    // x / sc == x * (1 / sc) exactly: sc is a power of two in [2^-22, 2^127]
+    const float inv = 1.0f / sc;
+    uint32_t wd[8];
 #pragma unroll
-    for (int st = 0; st < NST; ++st) a[mb][st] = load_frag<FMT, DI>(qrow, erow, st, hi, hv);
+    for (int i = 0; i < 8; ++i) {
+      const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(clampf(x[4 * i] * inv, 448.0f), clampf(x[4 * i + 1] * inv, 448.0f),
+                                                     0, false);
+      wd[i] = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(clampf(x[4 * i + 2] * inv, 448.0f),
+                                                                    clampf(x[4 * i + 3] * inv, 448.0f), lo, true));
+    }
+    uint4* dst = reinterpret_cast<uint4*>(q_lds + qh * kQPitch + 32 * qc);
+    dst[0] = uint4{wd[0], wd[1], wd[2], wd[3]};
+    dst[1] = uint4{wd[4], wd[5], wd[6], wd[7]};
+    if (qc == 0) qs_lds[qh] = sc;
+    __syncthreads();
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const uint4* src = reinterpret_cast<const uint4*>(q_lds + (mb * 32 + (lane & 31)) * kQPitch);
+#pragma unroll
+      for (int st = 0; st < NST; ++st) {
+        const uint4 u = src[4 * st + 2 * hi], v = src[4 * st + 2 * hi + 1];
+        a[mb][st].v = v8i{(int)u.x, (int)u.y, (int)u.z, (int)u.w, (int)v.x, (int)v.y, (int)v.z, (int)v.w};
+        a[mb][st].scale = 127;
+      }
+    }
+    cq = qs_lds[hl];
   }
-  __syncthreads();
+  const float cwq = cw * cq;
   float coef[MB][16];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-    for (int j = 0; j < 16; ++j) coef[mb][j] = coef_s[mb * 32 + acc_row(j, lane)];
+    for (int j = 0; j < 16; ++j) coef[mb][j] = __shfl(cwq, mb * 32 + acc_row(j, lane), 64);
 
 #pragma unroll
   for (int t = 0; t < kNkb; ++t) {
@@ -190,39 +297,86 @@ indexer_scores_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q
       out[g] = (g < vis) ? s : -__builtin_huge_valf();
     }
   }
+
+  if constexpr (QRAW) {
+    if (blockIdx.x == 0) {
+      // the quantized query, for callers that keep it (the codes are still in LDS)
+      if (p.q_codes_out && qh < Hi) {
+        const uint4* src = reinterpret_cast<const uint4*>(q_lds + qh * kQPitch + 32 * qc);
+        uint4* dst = reinterpret_cast<uint4*>(p.q_codes_out + (row * Hi + qh) * 128 + 32 * qc);
+        dst[0] = src[0];
+        dst[1] = src[1];
+        if (qc == 0) p.q_scales_out[row * Hi + qh] = qs_lds[qh];
+      }
+      if constexpr (APPEND) {
+        // FP8-b128 latent entry (as pack_latent_row): threads t < nope/4 hold 4 nope
+        // channels each (32 lanes per 128-channel block), threads t < rope one rope channel
+        const int64_t entry_bytes = p.nope + 4 * (p.nope / 128) + 2 * p.rope;
+        uint8_t* e = p.win + (b * p.win_batch_entries + pos % p.win_cap) * entry_bytes;
+        if (tid < p.nope / 4) {
+          const float v[4] = {bf16_to_f32(static_cast<uint16_t>(kv_nope.x & 0xffffu)),
+                              bf16_to_f32(static_cast<uint16_t>(kv_nope.x >> 16)),
+                              bf16_to_f32(static_cast<uint16_t>(kv_nope.y & 0xffffu)),
+                              bf16_to_f32(static_cast<uint16_t>(kv_nope.y >> 16))};
+          float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+          am = wave_max_group(am, 32);
+          const float sc = fp8_scale_from_amax(am);
+          uint32_t word = 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) word |= static_cast<uint32_t>(e4m3_encode(clampf(div_rn(v[i], sc), 448.0f))) << (8 * i);
+          reinterpret_cast<uint32_t*>(e)[tid] = word;
+          if ((tid & 31) == 0) reinterpret_cast<float*>(e + p.nope)[tid >> 5] = sc;
+        }
+        if (tid < p.rope) reinterpret_cast<uint16_t*>(e + p.nope + 4 * (p.nope / 128))[tid] = kv_rope;
+      }
+    }
+  }
 }
 
 template <int FMT, int DI>
-int launch_di(const uint8_t* q, const float* qs, const uint8_t* qe, const float* w, const uint8_t* k, const float* ks,
-              const uint8_t* ke, int64_t rows, int64_t S, int Hi, int64_t G, int64_t kbs, const int64_t* pos, int ratio,
-              float* scores, int64_t sstride, hipStream_t s) {
-  dim3 grid(static_cast<unsigned>((G + kKeysPerWg - 1) / kKeysPerWg), static_cast<unsigned>(rows));
-  if (Hi <= 32)
-    indexer_scores_kernel<FMT, DI, 1><<<grid, kWaves * 64, 0, s>>>(q, qs, qe, w, k, ks, ke, S, Hi, G, kbs, pos, ratio,
-                                                                  scores, sstride);
-  else
-    indexer_scores_kernel<FMT, DI, 2><<<grid, kWaves * 64, 0, s>>>(q, qs, qe, w, k, ks, ke, S, Hi, G, kbs, pos, ratio,
-                                                                  scores, sstride);
+int launch_di(const IdxParams& p, int64_t rows, hipStream_t s) {
+  dim3 grid(static_cast<unsigned>((p.G + kKeysPerWg - 1) / kKeysPerWg), static_cast<unsigned>(rows));
+  if (p.Hi <= 32) indexer_scores_kernel<FMT, DI, 1, false, false><<<grid, kWaves * 64, 0, s>>>(p);
+  else indexer_scores_kernel<FMT, DI, 2, false, false><<<grid, kWaves * 64, 0, s>>>(p);
   return MZK_OK;
 }
 
 template <int FMT>
-int launch(const uint8_t* q, const float* qs, const uint8_t* qe, const float* w, const uint8_t* k, const float* ks,
-           const uint8_t* ke, int64_t B, int64_t S, int Hi, int Di, int64_t G, int64_t kbs, const int64_t* pos, int ratio,
-           float* scores, int64_t sstride, hipStream_t s) {
-  const int64_t rows = B * S;
+int launch(const IdxParams& p, int64_t rows, int Di, hipStream_t s) {
   switch (Di) {
-    case 64: return launch_di<FMT, 64>(q, qs, qe, w, k, ks, ke, rows, S, Hi, G, kbs, pos, ratio, scores, sstride, s);
-    case 128: return launch_di<FMT, 128>(q, qs, qe, w, k, ks, ke, rows, S, Hi, G, kbs, pos, ratio, scores, sstride, s);
-    case 256: return launch_di<FMT, 256>(q, qs, qe, w, k, ks, ke, rows, S, Hi, G, kbs, pos, ratio, scores, sstride, s);
+    case 64: return launch_di<FMT, 64>(p, rows, s);
+    case 128: return launch_di<FMT, 128>(p, rows, s);
+    case 256: return launch_di<FMT, 256>(p, rows, s);
     default:
       if constexpr (FMT == kBf16) {
-        if (Di == 96) return launch_di<FMT, 96>(q, qs, qe, w, k, ks, ke, rows, S, Hi, G, kbs, pos, ratio, scores, sstride, s);
-        if (Di == 32) return launch_di<FMT, 32>(q, qs, qe, w, k, ks, ke, rows, S, Hi, G, kbs, pos, ratio, scores, sstride, s);
+        if (Di == 96) return launch_di<FMT, 96>(p, rows, s);
+        if (Di == 32) return launch_di<FMT, 32>(p, rows, s);
       }
       set_last_error("indexer_scores: unsupported index head dim %d", Di);
       return MZK_EUNSUPPORTED;
   }
+}
+
+IdxParams make_params(const uint8_t* q, const float* qs, const uint8_t* qe, const float* w, const uint8_t* k,
+                      const float* ks, const uint8_t* ke, int64_t S, int Hi, int64_t G, int64_t kbs, const int64_t* pos,
+                      int ratio, float* scores, int64_t sstride) {
+  IdxParams p{};
+  p.q = q;
+  p.q_scale = qs;
+  p.q_e8m0 = qe;
+  p.w = w;
+  p.k = k;
+  p.k_scale = ks;
+  p.k_e8m0 = ke;
+  p.S = S;
+  p.Hi = Hi;
+  p.G = G;
+  p.kbs = kbs;
+  p.positions = pos;
+  p.ratio = ratio;
+  p.scores = scores;
+  p.sstride = sstride;
+  return p;
 }
 
 int check_common(int64_t B, int64_t S, int Hi, int Di, int64_t G, int64_t kbs, int ratio, int64_t sstride) {
@@ -249,8 +403,9 @@ extern "C" int mzk_indexer_scores_fp8(const uint8_t* q_codes, const float* q_sca
   if (B * S == 0 || G == 0) return MZK_OK;
   MZK_CHECK_ARG(q_codes && q_scales && w && k_codes && k_scales && scores, "indexer_scores_fp8: null pointer");
   MZK_CHECK_ARG(Di % 64 == 0, "indexer_scores_fp8: Di must be a multiple of 64 (got %d)", Di);
-  rc = launch<kFp8>(q_codes, q_scales, nullptr, w, k_codes, k_scales, nullptr, B, S, Hi, Di, G, k_batch_stride, positions,
-                    ratio, scores, score_stride, as_stream(stream));
+  rc = launch<kFp8>(make_params(q_codes, q_scales, nullptr, w, k_codes, k_scales, nullptr, S, Hi, G, k_batch_stride,
+                                positions, ratio, scores, score_stride),
+                    B * S, Di, as_stream(stream));
   if (rc) return rc;
   MZK_LAUNCH_CHECK("indexer_scores_fp8");
   return MZK_OK;
@@ -265,8 +420,9 @@ extern "C" int mzk_indexer_scores_mxfp4(const uint8_t* q_packed, const uint8_t* 
   if (B * S == 0 || G == 0) return MZK_OK;
   MZK_CHECK_ARG(q_packed && q_e8m0 && w && k_packed && k_e8m0 && scores, "indexer_scores_mxfp4: null pointer");
   MZK_CHECK_ARG(Di % 64 == 0, "indexer_scores_mxfp4: Di must be a multiple of 64 (got %d)", Di);
-  rc = launch<kMxfp4>(q_packed, nullptr, q_e8m0, w, k_packed, nullptr, k_e8m0, B, S, Hi, Di, G, k_batch_stride,
-                      positions, ratio, scores, score_stride, as_stream(stream));
+  rc = launch<kMxfp4>(make_params(q_packed, nullptr, q_e8m0, w, k_packed, nullptr, k_e8m0, S, Hi, G, k_batch_stride,
+                                  positions, ratio, scores, score_stride),
+                      B * S, Di, as_stream(stream));
   if (rc) return rc;
   MZK_LAUNCH_CHECK("indexer_scores_mxfp4");
   return MZK_OK;
@@ -279,9 +435,56 @@ extern "C" int mzk_indexer_scores_bf16(const void* q, const float* w, const void
   if (rc) return rc;
   if (B * S == 0 || G == 0) return MZK_OK;
   MZK_CHECK_ARG(q && w && k && scores, "indexer_scores_bf16: null pointer");
-  rc = launch<kBf16>(static_cast<const uint8_t*>(q), nullptr, nullptr, w, static_cast<const uint8_t*>(k), nullptr, nullptr,
-                     B, S, Hi, Di, G, k_batch_stride, positions, ratio, scores, score_stride, as_stream(stream));
+  rc = launch<kBf16>(make_params(static_cast<const uint8_t*>(q), nullptr, nullptr, w, static_cast<const uint8_t*>(k),
+                                 nullptr, nullptr, S, Hi, G, k_batch_stride, positions, ratio, scores, score_stride),
+                     B * S, Di, as_stream(stream));
   if (rc) return rc;
   MZK_LAUNCH_CHECK("indexer_scores_bf16");
+  return MZK_OK;
+}
+
+extern "C" int mzk_indexer_decode_fp8(const void* q_idx, const float* w, const uint8_t* k_codes, const float* k_scales,
+                                      int64_t B, int Hi, int Di, int64_t G, int64_t k_batch_stride,
+                                      const int64_t* positions, int ratio, float* scores, int64_t score_stride,
+                                      uint8_t* q_codes, float* q_scales, const void* kv, int nope, int rope,
+                                      uint8_t* win_cache, int64_t win_batch_entries, int win_cap, void* stream) {
+  int rc = check_common(B, 1, Hi, Di, G, k_batch_stride, ratio, score_stride);
+  if (rc) return rc;
+  MZK_CHECK_ARG(Di == 128, "indexer_decode_fp8: the fused decode form needs Di = 128 (got %d)", Di);
+  MZK_CHECK_ARG(positions != nullptr, "indexer_decode_fp8: positions are required");
+  MZK_CHECK_ARG((q_codes == nullptr) == (q_scales == nullptr), "indexer_decode_fp8: q_codes and q_scales go together");
+  if (kv) {
+    MZK_CHECK_ARG(win_cache && win_cap >= 1 && win_batch_entries >= win_cap, "indexer_decode_fp8: bad window ring");
+    MZK_CHECK_ARG(nope >= 128 && nope % 128 == 0 && nope <= 4 * kWaves * 64 && rope >= 1 && rope <= kWaves * 64 &&
+                      rope % 2 == 0,
+                  "indexer_decode_fp8: latent %d+%d unsupported (nope a multiple of 128 up to 1024, rope even up to 256)",
+                  nope, rope);
+  }
+  if (B == 0) return MZK_OK;
+  MZK_CHECK_ARG(G >= 1, "indexer_decode_fp8: at least one key group is required");
+  MZK_CHECK_ARG(q_idx && w && k_codes && k_scales && scores, "indexer_decode_fp8: null pointer");
+  MZK_CHECK_ARG(aligned16(q_idx) && aligned16(k_codes) && aligned16(q_codes) && aligned16(kv) && aligned16(win_cache),
+                "indexer_decode_fp8: q_idx, k_codes, q_codes, kv and the window cache must be 16-byte aligned");
+  IdxParams p = make_params(nullptr, nullptr, nullptr, w, k_codes, k_scales, nullptr, 1, Hi, G, k_batch_stride,
+                            positions, ratio, scores, score_stride);
+  p.q_raw = static_cast<const uint16_t*>(q_idx);
+  p.q_codes_out = q_codes;
+  p.q_scales_out = q_scales;
+  p.kv = static_cast<const uint16_t*>(kv);
+  p.nope = nope;
+  p.rope = rope;
+  p.win = win_cache;
+  p.win_batch_entries = win_batch_entries;
+  p.win_cap = win_cap;
+  dim3 grid(static_cast<unsigned>((G + kKeysPerWg - 1) / kKeysPerWg), static_cast<unsigned>(B));
+  hipStream_t s = as_stream(stream);
+  if (Hi <= 32) {
+    if (kv) indexer_scores_kernel<kFp8, 128, 1, true, true><<<grid, kWaves * 64, 0, s>>>(p);
+    else indexer_scores_kernel<kFp8, 128, 1, true, false><<<grid, kWaves * 64, 0, s>>>(p);
+  } else {
+    if (kv) indexer_scores_kernel<kFp8, 128, 2, true, true><<<grid, kWaves * 64, 0, s>>>(p);
+    else indexer_scores_kernel<kFp8, 128, 2, true, false><<<grid, kWaves * 64, 0, s>>>(p);
+  }
+  MZK_LAUNCH_CHECK("indexer_decode_fp8");
   return MZK_OK;
 }

@@ -19,9 +19,10 @@ preallocated on the device so the whole step records into one HIP graph:
   changes between steps.
 
 ``step(q, kv, q_idx, w)`` for one token per row:
-  1+2. one launch: pack the new token's latent into its ring slot (derived on the device
-     from ``positions``) and quantize the indexer query (FP8 b128 per head, or MXFP4),
-  3. indexer scores over all keys (group-causal ``-inf`` beyond ``(pos+1)//ratio``),
+  1-3. FP8 index: one launch packs the new token's latent into its ring slot (derived on
+     the device from ``positions``), quantizes the indexer query (FP8 b128 per head) and
+     scores all keys (group-causal ``-inf`` beyond ``(pos+1)//ratio``); MXFP4 index: the
+     append + quantization launch, then the scores launch,
   4. top-k (lowest index wins ties),
   5. sparse MQA over window + [coarse] + top-k entries with the sink, split-KV + merge,
   6. ``positions += 1`` when ``advance``.
@@ -63,6 +64,8 @@ class SparseDecodeLayer:
     def __init__(self, cfg: DecodeConfig, device, sinks: torch.Tensor | None = None):
         if cfg.index_format not in ("fp8", "mxfp4"):
             raise ValueError(f"index_format must be 'fp8' or 'mxfp4', got {cfg.index_format!r}")
+        if cfg.index_format == "fp8" and cfg.index_dim != 128:
+            raise ValueError(f"the FP8 index (one b128 block per head) needs index_dim 128, got {cfg.index_dim}")
         self.cfg = cfg
         self.device = torch.device(device)
         b, eb = cfg.batch, quant.entry_bytes(cfg.nope, cfg.rope)
@@ -87,10 +90,7 @@ class SparseDecodeLayer:
         self.workspace = csa2_attn.new_workspace(b, cfg.heads, cfg.dim, cfg.nsplit, self.device)
         self._slot_base = torch.arange(b, device=self.device, dtype=torch.int64) * cfg.window
         hi = cfg.index_heads
-        if cfg.index_format == "fp8":
-            self.q_codes = torch.empty(b, 1, hi, di, **u8)
-            self.q_scales = torch.empty(b, 1, hi, di // 128, dtype=torch.float32, device=self.device)
-        else:
+        if cfg.index_format == "mxfp4":  # the FP8 step quantizes the query inside its indexer launch
             self.q_codes = torch.empty(b, 1, hi, di // 2, **u8)
             self.q_e8m0 = torch.empty(b, 1, hi, di // 32, **u8)
         self._graph = None
@@ -141,20 +141,21 @@ class SparseDecodeLayer:
         cfg = self.cfg
         b = cfg.batch
         fp8 = cfg.index_format == "fp8"
-        # window append + indexer-query quantization, one launch
         kvc = None if kv is None else kv.contiguous()
-        qc = q_idx.contiguous()
-        _lib.require_gpu(qc, *(() if kvc is None else (kvc,)))
-        _lib.call("mzk_decode_prologue", _lib.ptr(kvc), _lib.dtype_code((qc if kvc is None else kvc).dtype),
-                  0 if kvc is None else b, cfg.nope, cfg.rope, self.positions.data_ptr(), self.win.data_ptr(),
-                  cfg.window, cfg.window, qc.data_ptr(), _lib.dtype_code(qc.dtype), b * cfg.index_heads,
-                  cfg.index_dim, 0 if fp8 else 1, self.q_codes.data_ptr(), self.q_scales.data_ptr() if fp8 else None,
-                  None if fp8 else self.q_e8m0.data_ptr(), _lib.stream_of(qc))
         pos = self.positions.view(b, 1)
         if fp8:
-            indexer.scores_fp8(self.q_codes, self.q_scales[..., 0], w.view(b, 1, -1), self.k_codes, self.k_scales,
-                               compress_ratio=cfg.ratio, positions=pos, out=self.scores)
+            # window append + indexer-query quantization + scores, one launch
+            indexer.decode_fp8(q_idx, w.view(b, -1), self.k_codes, self.k_scales, compress_ratio=cfg.ratio,
+                               positions=pos, out=self.scores, kv=kvc, win_cache=self.win, nope=cfg.nope,
+                               rope=cfg.rope)
         else:
+            # window append + indexer-query quantization (one launch), then scores
+            qc = q_idx.contiguous()
+            _lib.require_gpu(qc, *(() if kvc is None else (kvc,)))
+            _lib.call("mzk_decode_prologue", _lib.ptr(kvc), _lib.dtype_code((qc if kvc is None else kvc).dtype),
+                      0 if kvc is None else b, cfg.nope, cfg.rope, self.positions.data_ptr(), self.win.data_ptr(),
+                      cfg.window, cfg.window, qc.data_ptr(), _lib.dtype_code(qc.dtype), b * cfg.index_heads,
+                      cfg.index_dim, 1, self.q_codes.data_ptr(), None, self.q_e8m0.data_ptr(), _lib.stream_of(qc))
             indexer.scores_mxfp4(self.q_codes, self.q_e8m0, w.view(b, 1, -1), self.k_packed, self.k_e8m0,
                                  compress_ratio=cfg.ratio, positions=pos, out=self.scores)
         indexer.topk(self.scores.view(b, cfg.max_groups), cfg.topk, out=self.idx)

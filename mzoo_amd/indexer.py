@@ -114,6 +114,42 @@ def scores_fp8(q_codes: torch.Tensor, q_scales: torch.Tensor, w: torch.Tensor, k
     return out
 
 
+def decode_fp8(q_idx: torch.Tensor, w: torch.Tensor, k_codes: torch.Tensor, k_scales: torch.Tensor, *,
+               compress_ratio: int, positions: torch.Tensor, out: torch.Tensor | None = None,
+               q_codes: torch.Tensor | None = None, q_scales: torch.Tensor | None = None,
+               kv: torch.Tensor | None = None, win_cache: torch.Tensor | None = None, nope: int = 512,
+               rope: int = 64) -> torch.Tensor:
+    """Decode-step FP8 indexer with the step's prologue fused in (one launch): q_idx bf16
+    [B,Hi,128] is quantized in the kernel (FP8 b128) and scored against k_codes uint8
+    [B,Gcap,128] / k_scales fp32 [B,Gcap] -> fp32 [B,1,Gcap].  Optionally also writes the
+    quantized query (q_codes uint8 [B,Hi,128] + q_scales fp32 [B,Hi]) and appends the new
+    latent kv bf16 [B, nope+rope] to the window ring win_cache uint8 [B,W,entry] at slot
+    positions[b] % W -- what ``quant_fp8_block`` + the window write of the step would do."""
+    b, hi, di = q_idx.shape
+    gcap = k_codes.shape[1]
+    if q_idx.dtype != torch.bfloat16 or k_codes.shape != (b, gcap, di) or k_scales.shape != (b, gcap) \
+            or w.shape[-1] != hi or w.numel() != b * hi:
+        raise ValueError("decode_fp8: shape/dtype mismatch")
+    if (q_codes is None) != (q_scales is None):
+        raise ValueError("decode_fp8: q_codes and q_scales go together")
+    if kv is not None and (kv.dtype != torch.bfloat16 or kv.shape != (b, nope + rope) or win_cache is None):
+        raise ValueError("decode_fp8: kv must be bf16 [B, nope+rope] with a window cache")
+    _lib.require_gpu(q_idx, k_codes, positions)
+    out = _check_scores_out(b, 1, gcap, q_idx.device, out)
+    pos = torch.as_tensor(positions, device=q_idx.device).to(torch.int64).reshape(b).contiguous()  # [B] or [B,1]
+    for t in (q_codes, q_scales, win_cache):
+        if t is not None and not t.is_contiguous():
+            raise ValueError("decode_fp8: q_codes, q_scales and win_cache must be contiguous")
+    qc = q_idx.contiguous()
+    kvc = None if kv is None else kv.contiguous()
+    wcap = 0 if win_cache is None else win_cache.shape[1]
+    _lib.call("mzk_indexer_decode_fp8", qc.data_ptr(), w.float().contiguous().data_ptr(), k_codes.contiguous().data_ptr(),
+              k_scales.float().contiguous().data_ptr(), b, hi, di, gcap, gcap, pos.data_ptr(), compress_ratio,
+              out.data_ptr(), out.stride(1), _lib.ptr(q_codes), _lib.ptr(q_scales), _lib.ptr(kvc), nope, rope,
+              _lib.ptr(win_cache), wcap, wcap, _lib.stream_of(qc))
+    return out
+
+
 def scores_mxfp4(q_packed: torch.Tensor, q_e8m0: torch.Tensor, w: torch.Tensor, k_packed: torch.Tensor,
                  k_e8m0: torch.Tensor, *, compress_ratio: int, positions=None, groups: int | None = None,
                  out: torch.Tensor | None = None) -> torch.Tensor:

@@ -175,3 +175,44 @@ def test_fp8_decode_topk_end_to_end(dev):
     idx = MI.topk(sc, 2048)
     ref = OA.indexer_scores(qd, kd, w, 4, pos)
     assert_topk_sets_match(idx, ref, OA.indexer_abs_scores(qd, kd, w, 4, pos), 2048)
+
+
+@pytest.mark.parametrize("b,hi,g,append", [(5, 64, 1000, True), (3, 20, 512, True), (4, 64, 2048, False)])
+def test_fused_decode_indexer_fp8(dev, b, hi, g, append):
+    """mzk_indexer_decode_fp8 = query quantization + window append + FP8 scores in one
+    launch: the quantized query and the appended window entry are bit-exact against the
+    oracle's quantizer / packer, and the scores are bit-identical to the two-launch path
+    (mzk_indexer_scores_fp8 on the oracle-quantized query), within tolerance of the
+    oracle's fp32 scores, with the group-causal mask."""
+    q, k, w = _inputs(b, 1, hi, 128, g, seed=hi + g)
+    q = q[:, 0]                                                     # [B, Hi, 128]
+    q[0, 0, :5] = torch.tensor([0.0, -0.0, 1e-30, 3e-3, -6.0])     # zeros, underflow, the block max
+    q[1 % b, hi - 1] = 0                                             # an all-zero head (scale floor)
+    qc_ref, qs_ref = Q.fp8_block_codes(q.float().numpy(), 128)
+    _, _, kc, ks, qd, kd = _fp8_operands(q[:, None], k)
+    pos = torch.tensor([4 * g - 1, 37, 4 * g + 9, 0, 1000][:b], dtype=torch.int64)
+    wcap = 16
+    kv = torch.randn(b, 576, generator=torch.Generator().manual_seed(b)).bfloat16()
+    win = torch.zeros(b, wcap, 656, dtype=torch.uint8, device=dev)
+    q_codes = torch.zeros(b, hi, 128, dtype=torch.uint8, device=dev)
+    q_scales = torch.zeros(b, hi, dtype=torch.float32, device=dev)
+    got = MI.decode_fp8(q.to(dev), w[:, 0].to(dev), kc.to(dev), ks.to(dev), compress_ratio=4,
+                        positions=pos.to(dev), q_codes=q_codes, q_scales=q_scales,
+                        kv=kv.to(dev) if append else None, win_cache=win if append else None)
+    assert np.array_equal(q_codes.cpu().numpy().reshape(qc_ref.shape), qc_ref)
+    assert np.array_equal(q_scales.cpu().numpy().reshape(qs_ref.shape).view(np.int32), qs_ref.view(np.int32))
+    wc = win.cpu().numpy()
+    if append:
+        want = Q.pack_latent_fp8_b128(kv.float().numpy())
+        for r in range(b):
+            assert np.array_equal(wc[r, int(pos[r]) % wcap], want[r])
+            others = [i for i in range(wcap) if i != int(pos[r]) % wcap]
+            assert not wc[r, others].any()
+    else:
+        assert not wc.any()
+    two = MI.scores_fp8(torch.from_numpy(qc_ref).reshape(b, 1, hi, 128).to(dev),
+                        torch.from_numpy(qs_ref).reshape(b, 1, hi).to(dev), w.to(dev), kc.to(dev), ks.to(dev),
+                        compress_ratio=4, positions=pos.view(b, 1).to(dev))
+    assert torch.equal(got, two)
+    ref = OA.indexer_scores(qd, kd, w, 4, pos.view(b, 1))
+    assert_scores_close(got, ref, OA.indexer_abs_scores(qd, kd, w, 4, pos.view(b, 1)))
