@@ -104,7 +104,9 @@ __device__ __forceinline__ int c_entry(int j, int lane) { return 8 * (j >> 2) + 
 // the compiler from moving memory accesses across.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory"); }
 
-constexpr int kIdxCap = 4096;  // sparse indices of one split staged in LDS
+constexpr int kIdxCap = 4096;       // sparse indices of one split staged in LDS (D <= 256 kernel)
+constexpr int kSplitIdxCap = 1024;
+constexpr int kMaxDevices = 64;   // per-device one-time launch attributes  // the same for the D-split kernel (its LDS holds three tiles)
 
 typedef const uint8_t __attribute__((address_space(1)))* gptr_t;  // global (not flat) loads
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -174,8 +176,10 @@ struct RowPlan {
   const uint8_t* main_b;
   const uint8_t** tab_ptr;   // [NSLOT][kTile] in LDS: tile t uses slot t % NSLOT
   uint32_t* tab_mask;        // [NSLOT] in LDS
-  const int32_t* sidx;       // this split's sparse indices (the first sidx_cap), in LDS
-  const int32_t* idx_row;    // the row's sparse indices in global memory
+  // typed address spaces: a generic pointer would make these FLAT loads, which count
+  // against the LDS wait counter too and force every later LDS wait to drain completely
+  const __attribute__((address_space(3))) int32_t* sidx;     // this split's sparse indices (the first sidx_cap), in LDS
+  const __attribute__((address_space(1))) int32_t* idx_row;  // the row's sparse indices in global memory
   int sidx_cap;
 
   // Workgroup -> (row, split, head group).  The head groups of one (row, split) read the
@@ -226,18 +230,15 @@ struct RowPlan {
     g_lim = p.G < 0x7fffffff ? p.G : 0x7fffffff;
   }
 
-  // Stage this split's slice of the sparse index list in LDS (the host guarantees it fits
-  // kIdxCap), so the tile loop issues no vector-memory reads besides the tiles.
-  // The caller synchronises before the slice is read.
   // Stage up to `cap` indices of this split's slice of the sparse list in LDS, so the tile
   // loop reads them from there; positions beyond the cap are read from global memory.
   // The caller synchronises before the slice is read.
   __device__ void stage_indices(const AttnParams& p, int32_t* sidx_lds, int cap, int tid) {
     const int sp_end = v_end > nwd ? v_end - nwd : 0;
-    idx_row = p.idx ? p.idx + row * p.idx_row_stride : nullptr;
+    idx_row = p.idx ? (const __attribute__((address_space(1))) int32_t*)(p.idx + row * p.idx_row_stride) : nullptr;
     const int lim = sp_end < sp_begin + cap ? sp_end : sp_begin + cap;
     for (int s = sp_begin + tid; s < lim; s += NT) sidx_lds[s - sp_begin] = idx_row[s];
-    sidx = sidx_lds;
+    sidx = (const __attribute__((address_space(3))) int32_t*)(sidx_lds);
     sidx_cap = cap;
   }
 
@@ -245,7 +246,8 @@ struct RowPlan {
   __device__ int slot(int v) const {
     if (v < nwd || v >= v_end) return -1;
     const int s = v - nwd - sp_begin;
-    return s < sidx_cap ? sidx[s] : idx_row[sp_begin + s];
+    if (s < sidx_cap) return sidx[s];
+    return idx_row[sp_begin + s];
   }
 
   // entry table of tile t (threads 0..31); g = this thread's prefetched sparse index
@@ -519,20 +521,18 @@ __global__ void __launch_bounds__(HG * 64) sparse_mqa_kernel(const AttnParams p)
 
 // ------------------------------------------------------------------------------------
 // D > 256 (the 512+64 latent): 64 heads per workgroup, each 32-head group split over 4
-// waves by D (8 waves, two per SIMD).  A wave holds its D-quarter of q (9 K-steps) and at
-// most 5 O^T blocks.  The loop is software-pipelined: iteration t starts with tile t's
-// S^T partials already published (computed in iteration t-1, or the prologue).
-//   barrier A.  Wave ds finishes entries 8ds..8ds+7 of tile t (S^T registers 4ds..4ds+3):
-//      sums the four partials in D-part order and bounds the tile max by the sum of the
-//      partial maxima (an upper bound, so exp2(s - m) <= 2^kLazy still holds; the online
-//      softmax is exact for any reference point as long as no significant term underflows,
-//      which the pass checks at its end); its P^T quarter goes to LDS.  Meanwhile the
-//      workgroup dequantizes tile t+1 into Kt[(t+1)%2] and builds table t+3.
-//   barrier B.  O^T += V^T.P^T of tile t from Kt[t%2] and the S^T partial of tile t+1 from
-//      Kt[(t+1)%2], in one block so the two MFMA streams interleave; the partial and its
-//      per-head maximum are published; the pieces of tile t+3 are fetched.
-// Two barriers per tile (three in the exact pass, which replaces the bound by the true
-// tile max).
+// waves by D (8 waves, two per SIMD: one of each group).  A wave holds its D-quarter of q
+// (9 K-steps) and at most 5 O^T blocks; the four partial S^T of a head group are summed
+// through LDS.  The two groups run half a tile apart (ping-pong), so on every SIMD one
+// wave does MFMA work (PV of one tile interleaved with QK of the next, operands read a
+// block ahead) while the other does the softmax, its half of the next tile's
+// dequantization into LDS, and the tile fetches; the schedule is spelled out at the
+// tile loop.  Softmax: the running max is raised lazily to an upper bound of the tile
+// max (the sum of the four partial maxima), so exp2(s - m) <= 2^kLazy always holds; the
+// online softmax is exact for any reference point as long as no significant term
+// underflows, which the pass checks at its end (else an exact pass redoes the split).
+// One barrier per half-tile (one more per half-tile in the exact pass, which exchanges
+// the true tile max).
 // ------------------------------------------------------------------------------------
 template <int FMT, int D, int NOPE>
 struct SplitSmem {
@@ -543,7 +543,8 @@ struct SplitSmem {
   static constexpr int PM = HG * 32 * 2 * DS * 4;         // [64 heads][8] partial maxima / row sums
   static constexpr int PB = HG * 2 * 64 * 16;             // [hg][2 K-steps][64] P^T
   static constexpr int PE = HG * 32 * 2 * DS * 4;         // [64 heads][8] true lane maxima
-  static constexpr int LDS = 2 * KT + SX + PM + PB + PE;
+  static constexpr int NKT = 3;                            // bf16 tiles in flight: PV, QK, dequantized
+  static constexpr int LDS = NKT * KT + SX + PM + PB + PE;
 };
 
 template <int FMT, int D, int NOPE>
@@ -556,24 +557,25 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
   constexpr int QST = D / 16 / DS;            // QK K-steps per wave
   constexpr int NB = D / 32;                  // 32-channel blocks of O
   constexpr int NDBM = (NB + DS - 1) / DS;    // most O blocks one wave owns
-  constexpr int NSLOT = 4;  // entry tables: t (mask), t+1, t+2 (fetched), t+3 (built, then fetched)
+  // entry tables in flight: t (its mask), t+1 .. t+3 (fetched), t+4 (built this tile)
+  constexpr int NSLOT = 8;
   using RP = RowPlan<FMT, D, NOPE, NT, NSLOT>;
   static_assert((D / 16) % DS == 0 && D % 32 == 0, "D must split into 4 parts of 16-channel steps");
 
   extern __shared__ __align__(16) uint8_t smem[];
-  uint8_t* kt0 = smem;                                                   // 2 x [32][KT_PITCH]
-  float4* sx = reinterpret_cast<float4*>(smem + 2 * M::KT);
-  float* pm = reinterpret_cast<float*>(smem + 2 * M::KT + M::SX);
-  uint4* pb = reinterpret_cast<uint4*>(smem + 2 * M::KT + M::SX + M::PM);
-  float* pe = reinterpret_cast<float*>(smem + 2 * M::KT + M::SX + M::PM + M::PB);
+  uint8_t* kt0 = smem;                                                   // 3 x [32][KT_PITCH]
+  float4* sx = reinterpret_cast<float4*>(smem + M::NKT * M::KT);
+  float* pm = reinterpret_cast<float*>(smem + M::NKT * M::KT + M::SX);
+  uint4* pb = reinterpret_cast<uint4*>(smem + M::NKT * M::KT + M::SX + M::PM);
+  float* pe = reinterpret_cast<float*>(smem + M::NKT * M::KT + M::SX + M::PM + M::PB);
   __shared__ const uint8_t* tab_ptr[NSLOT * kTile];
   __shared__ uint32_t tab_mask[NSLOT];
-  __shared__ int32_t sidx[kIdxCap];
+  __shared__ int32_t sidx[kSplitIdxCap];
   __shared__ int redo;  // set when the fast pass's running max drifted too far above the truth
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) branches on the group
   const int hg = wave / DS;
   if (tid == 0) redo = 0;  // published by the barrier after the indices are staged
   const int ds = wave % DS;
@@ -582,7 +584,7 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
   rp.tab_ptr = tab_ptr;
   rp.tab_mask = tab_mask;
   rp.init(p, HG * 32);
-  rp.stage_indices(p, sidx, kIdxCap, tid);
+  rp.stage_indices(p, sidx, kSplitIdxCap, tid);
   __syncthreads();
 
   const int hl = hg * 32 + (lane & 31);  // head within the workgroup
@@ -601,24 +603,27 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
   const int b_lo = ds * NB / DS;
   const int nb_mine = (ds + 1) * NB / DS - b_lo;
   const int pv_off = pv_lane_offset<KT_PITCH>(lane, b_lo * 32);
-  // S^T partial over this wave's D-quarter of the tile in `kt`; all K fragments are read
-  // before the MFMA chain
-  auto qk = [&](const uint8_t* kt) -> v16f {
+  // S^T partial over this wave's D-quarter of the tile in `kt`; K fragments are read
+  // three K-steps ahead of their MFMA (a rolling window keeps register pressure low)
+  auto qk = [&](const uint8_t* kt) __attribute__((always_inline)) -> v16f {
+    constexpr int AH = 3;
     const uint8_t* krow = kt + (lane & 31) * KT_PITCH + 2 * (qc0 + half * 8);
-    v8bf kf[QST];
+    uint4 kv[AH];
 #pragma unroll
-    for (int st = 0; st < QST; ++st) {
-      const uint4 kv = *reinterpret_cast<const uint4*>(krow + 32 * st);
-      kf[st] = __builtin_bit_cast(v8bf, v4i{(int)kv.x, (int)kv.y, (int)kv.z, (int)kv.w});
-    }
+    for (int i = 0; i < AH; ++i) kv[i] = *reinterpret_cast<const uint4*>(krow + 32 * i);
     v16f s = v16f{};
 #pragma unroll
-    for (int st = 0; st < QST; ++st) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[st], qf[st], s, 0, 0, 0);
+    for (int st = 0; st < QST; ++st) {
+      const uint4 cur = kv[st % AH];
+      if (st + AH < QST) kv[st % AH] = *reinterpret_cast<const uint4*>(krow + 32 * (st + AH));
+      const v8bf kf = __builtin_bit_cast(v8bf, v4i{(int)cur.x, (int)cur.y, (int)cur.z, (int)cur.w});
+      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s, 0, 0, 0);
+    }
     return s;
   };
   // the partial ([wave][j/4][lane] float4: consecutive lanes at consecutive 16 B,
   // conflict-free) and its per-head maximum over this lane's 16 entries go to LDS
-  auto publish = [&](const v16f& s) {
+  auto publish = [&](const v16f& s) __attribute__((always_inline)) {
     float mx = s[0];
 #pragma unroll
     for (int j = 1; j < 16; ++j) mx = fmaxf(mx, s[j]);
@@ -645,24 +650,31 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
     float l_run = 0.0f;                    // this lane's share of the head's row sum
     float m_seen = -__builtin_huge_valf(); // true max of this lane's (unmasked) entries
 
-    // the pieces of the next two tiles are in flight in registers (tile t+1 in one set, t+2
-    // in the other), so a tile's loads have two tile periods to arrive before dequantization
-    Piece raw_a[RP::PPT], raw_b[RP::PPT];
+    // Ping-pong schedule.  The two head groups run half a tile apart, so on every SIMD
+    // (which holds one wave of each group) one wave does MFMA work while the other does
+    // the softmax and the tile traffic.  Half-step 2u (even) and 2u+1 (odd), each opened by
+    // a workgroup barrier:
+    //   even(u): group 0 softmax(u) -> P^T(u); stores its half (entries 16..31) of tile u+1,
+    //            fetches its half of tile u+3, builds the entry table of tile u+4;
+    //            group 1 PV(u-1) + QK(u) -> publishes S^T(u).
+    //   odd(u):  group 0 PV(u) + QK(u+1) -> publishes S^T(u+1);
+    //            group 1 softmax(u) -> P^T(u); stores its half (entries 0..15) of tile
+    //            u+2, fetches its half of tile u+4.
+    // Tile u lives in LDS tile u%3: it is read by QK at half-steps 2u-1 and 2u and by PV
+    // at 2u+1 and 2u+2, and its halves are written at 2u-3 (group 1) and 2u-2 (group 0),
+    // when the tile that used the buffer before (u-3) is no longer read.  A group's raw
+    // register set holds its half of two tiles in flight (even tiles in one set, odd in
+    // the other), so a load has two tiles' time to arrive.  Group g dequantizes / fetches
+    // as thread tid ^ 256, which maps group 0 to entries 16..31 and group 1 to 0..15.
+    Piece raw[RP::PPT];
     int g_pref = -1;
-    // One tile: enters with tile t's S^T partials published and `raw` holding tile t+1's
-    // pieces; leaves with tile t+1's partials published and `raw` holding tile t+3's.
-    auto tile_step = [&](int t, Piece (&raw)[RP::PPT]) {
-      const uint8_t* kt = kt0 + (t & 1) * M::KT;
-      uint8_t* kt_next = kt0 + ((t + 1) & 1) * M::KT;
-      const uint32_t vmask = tab_mask[t % NSLOT];  // read before barrier A; table t+4 replaces it later
-      lds_barrier();  // A: tile t's partials published; every wave is done with PV(t-1)
+    const int ptid = tid ^ 256;
+    auto ktile = [&](int u) __attribute__((always_inline)) -> uint8_t* { return kt0 + (u % 3) * M::KT; };
 
-      // dequantize tile t+1 into the buffer PV(t-1) has released
-      if (t + 1 < rp.ntiles) rp.store(kt_next, KT_PITCH, tid, raw);
-      rp.build_table(p, t + 3, g_pref, tid);
-      if (tid < kTile) g_pref = rp.slot(rp.v_begin + (t + 4) * kTile + tid);
-
-      // entries 8ds..8ds+7 of tile t for this lane's head
+    // softmax of tile u for this wave's heads: S^T partials -> running max / sum -> P^T
+    auto softmax = [&](int u) __attribute__((always_inline)) {
+      const uint32_t vmask = tab_mask[u % NSLOT];
+      // entries 8ds..8ds+7 of tile u for this lane's head
       float4 a = sx[((hg * DS) * 4 + ds) * 64 + lane];
 #pragma unroll
       for (int part = 1; part < DS; ++part) {
@@ -682,8 +694,8 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
       const float lane_max = fmaxf(fmaxf(v4[0], v4[1]), fmaxf(v4[2], v4[3]));
       float bound;
       if constexpr (kExact) {
-        // the head's true tile max: its 8 lanes' maxima through LDS (read back before
-        // barrier B; the next tile writes them after its barrier A)
+        // the head's true tile max: its 8 lanes' maxima through LDS (the other group
+        // passes the matching barrier at the start of its MFMA half-step)
         pe[hl * 8 + 2 * ds + half] = lane_max;
         lds_barrier();
         const float4 t0 = *reinterpret_cast<const float4*>(pe + hl * 8);
@@ -704,54 +716,143 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
         for (int i = 0; i < NDBM; ++i) acc_o[i] = acc_o[i] * alpha;
         m_run = m_new;
       }
-      {
-        // the exact pass may see a head with no finite entry yet (m_run = -inf): then every
-        // entry is -inf and the reference point 0 gives exp2(-inf) = 0 instead of NaN
-        const float m_use = (kExact && m_run == -__builtin_huge_valf()) ? 0.0f : m_run;
-        const float p0 = __builtin_amdgcn_exp2f(v4[0] - m_use);
-        const float p1 = __builtin_amdgcn_exp2f(v4[1] - m_use);
-        const float p2 = __builtin_amdgcn_exp2f(v4[2] - m_use);
-        const float p3 = __builtin_amdgcn_exp2f(v4[3] - m_use);
-        l_run = l_run + ((p0 + p1) + (p2 + p3));
-        // PV K-step ks = ds/2 takes registers 8ks..8ks+7 = D-parts 2ks (slots 0-3), 2ks+1 (4-7)
-        uint2* dst = reinterpret_cast<uint2*>(pb + (hg * 2 + (ds >> 1)) * 64 + lane) + (ds & 1);
-        *dst = uint2{pack_bf16x2(p0, p1), pack_bf16x2(p2, p3)};
-      }
-      lds_barrier();  // B: P^T of tile t and Kt of tile t+1 complete, table t+3 visible
-
-      const uint4 w0 = pb[(hg * 2 + 0) * 64 + lane];
-      const uint4 w1 = pb[(hg * 2 + 1) * 64 + lane];
-      const v8bf pf0 = __builtin_bit_cast(v8bf, v4i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w});
-      const v8bf pf1 = __builtin_bit_cast(v8bf, v4i{(int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w});
-      // PV(t) and QK(t+1) in one block, so the two MFMA streams interleave; the fetch of
-      // tile t+3 is issued behind them.  After the last tile QK runs on the stale buffer; its
-      // result is published but never read.
-      const uint8_t* tr0 = kt + pv_off;
-#pragma unroll
-      for (int db = 0; db < NDBM - 1; ++db) pv_block<KT_PITCH>(tr0 + 64 * db, pf0, pf1, acc_o[db]);
-      const v16f s_next = qk(kt_next);
-      if (nb_mine == NDBM) pv_block<KT_PITCH>(tr0 + 64 * (NDBM - 1), pf0, pf1, acc_o[NDBM - 1]);
-      if (t + 3 < rp.ntiles) rp.fetch(t + 3, tid, raw);
-      publish(s_next);
+      // the exact pass may see a head with no finite entry yet (m_run = -inf): then every
+      // entry is -inf and the reference point 0 gives exp2(-inf) = 0 instead of NaN
+      const float m_use = (kExact && m_run == -__builtin_huge_valf()) ? 0.0f : m_run;
+      const float p0 = __builtin_amdgcn_exp2f(v4[0] - m_use);
+      const float p1 = __builtin_amdgcn_exp2f(v4[1] - m_use);
+      const float p2 = __builtin_amdgcn_exp2f(v4[2] - m_use);
+      const float p3 = __builtin_amdgcn_exp2f(v4[3] - m_use);
+      l_run = l_run + ((p0 + p1) + (p2 + p3));
+      // PV K-step ks = ds/2 takes registers 8ks..8ks+7 = D-parts 2ks (slots 0-3), 2ks+1 (4-7)
+      uint2* dst = reinterpret_cast<uint2*>(pb + (hg * 2 + (ds >> 1)) * 64 + lane) + (ds & 1);
+      *dst = uint2{pack_bf16x2(p0, p1), pack_bf16x2(p2, p3)};
     };
-
+    // O^T += V^T.P^T of tile `u` (if pv) and the S^T partial of tile u+1 (if qk), in one
+    // block so the two MFMA streams interleave.  Near the end QK runs on a stale buffer;
+    // its partial is published but never read.
+    auto mfma_step = [&](int u, bool pv, bool qk_next) __attribute__((always_inline)) {
+      if constexpr (kExact) lds_barrier();  // pairs with the exact softmax's barrier
+      // Software pipeline for a lone MFMA wave: every operand is read from LDS a step
+      // ahead of the MFMA that consumes it (V^T one 32-channel block ahead, K two K-steps
+      // ahead), and scheduling fences keep the compiler from collapsing the pipeline.
+      const uint8_t* kt_q = ktile(u + 1) + (lane & 31) * KT_PITCH + 2 * (qc0 + half * 8);
+      constexpr int NB_MIN = NB / DS;  // O^T blocks every wave owns (the last one may own one more)
+      uint4 kv[QST];
+      v16f s_acc = v16f{};
+      // one QK K-step; K fragments are read two steps ahead (compile-time indices only)
+      auto qk_step = [&](int st) __attribute__((always_inline)) {
+        if (st + 2 < QST) kv[st + 2] = *reinterpret_cast<const uint4*>(kt_q + 32 * (st + 2));
+        s_acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(v8bf, v4i{(int)kv[st].x, (int)kv[st].y, (int)kv[st].z, (int)kv[st].w}), qf[st], s_acc,
+            0, 0, 0);
+      };
+      if (qk_next) {
+        kv[0] = *reinterpret_cast<const uint4*>(kt_q);
+        if (QST > 1) kv[1] = *reinterpret_cast<const uint4*>(kt_q + 32);
+      }
+      if (pv) {
+        const uint4 w0 = pb[(hg * 2 + 0) * 64 + lane];
+        const uint4 w1 = pb[(hg * 2 + 1) * 64 + lane];
+        const v8bf pf0 = __builtin_bit_cast(v8bf, v4i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w});
+        const v8bf pf1 = __builtin_bit_cast(v8bf, v4i{(int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w});
+        const uint8_t* tr0 = ktile(u) + pv_off;
+        // V^T operands double-buffered by block parity, so block db+1's reads are in flight
+        // while block db's MFMAs run
+        v4s rv[2][4];
+        auto read_v = [&](int db) __attribute__((always_inline)) {
+          const uint8_t* tp = tr0 + 64 * db;
+          v4s (&r)[4] = rv[db & 1];
+          r[0] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4s(tp));
+          r[1] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4s(tp + 8 * KT_PITCH));
+          r[2] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4s(tp + 16 * KT_PITCH));
+          r[3] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4s(tp + 24 * KT_PITCH));
+        };
+        // PV of block db; with_qk interleaves K-steps 2db and 2db+1 of QK (compile time)
+        auto pv_mfma = [&](int db, bool more, bool with_qk) __attribute__((always_inline)) {
+          if (more) read_v(db + 1);
+          const v4s (&r)[4] = rv[db & 1];
+          const v8bf a0 = __builtin_bit_cast(v8bf, v8s{r[0][0], r[0][1], r[0][2], r[0][3], r[1][0], r[1][1], r[1][2], r[1][3]});
+          const v8bf a1 = __builtin_bit_cast(v8bf, v8s{r[2][0], r[2][1], r[2][2], r[2][3], r[3][0], r[3][1], r[3][2], r[3][3]});
+          acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, pf0, acc_o[db], 0, 0, 0);
+          if (with_qk && qk_next && 2 * db < QST) qk_step(2 * db);
+          acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, pf1, acc_o[db], 0, 0, 0);
+          if (with_qk && qk_next && 2 * db + 1 < QST) qk_step(2 * db + 1);
+          __builtin_amdgcn_sched_barrier(0);
+        };
+        read_v(0);
+#pragma unroll
+        for (int db = 0; db < NB_MIN; ++db) pv_mfma(db, db + 1 < NB_MIN || nb_mine > NB_MIN, true);
+        static_assert(2 * NB_MIN <= QST, "every interleaved K-step index must exist");
+#pragma unroll
+        for (int st = 2 * NB_MIN; st < QST; ++st)
+          if (qk_next) qk_step(st);
+        if (nb_mine > NB_MIN) {  // the wave's extra block: the K-steps above are all issued
+#pragma unroll
+          for (int db = NB_MIN; db < NDBM; ++db) pv_mfma(db, false, false);
+        }
+      } else if (qk_next) {
+#pragma unroll
+        for (int st = 0; st < QST; ++st) qk_step(st);
+      }
+      if (qk_next) publish(s_acc);
+    };
+    // group 0: even(u) softmax + traffic, odd(u) PV(u) + QK(u+1)
+    auto group0_pair = [&](int u, Piece (&r0)[RP::PPT]) {
+      lds_barrier();
+      softmax(u);
+      rp.store(ktile(u + 1), KT_PITCH, ptid, r0);
+      rp.fetch(u + 2, ptid, r0);
+      rp.build_table(p, u + 4, g_pref, tid);
+      if (tid < kTile) g_pref = rp.slot(rp.v_begin + (u + 5) * kTile + tid);
+      lds_barrier();
+      mfma_step(u, true, true);
+    };
+    // group 1: even(u) PV(u-1) + QK(u), odd(u) softmax + traffic
+    auto group1_pair = [&](int u, Piece (&r1)[RP::PPT]) {
+      lds_barrier();
+      mfma_step(u - 1, true, true);
+      lds_barrier();
+      softmax(u);
+      rp.store(ktile(u + 2), KT_PITCH, ptid, r1);
+      rp.fetch(u + 3, ptid, r1);
+    };
     if (rp.ntiles > 0) {
 #pragma unroll
-      for (int t = 0; t < 3; ++t) rp.build_table(p, t, tid < kTile ? rp.slot(rp.v_begin + t * kTile + tid) : -1, tid);
-      if (tid < kTile) g_pref = rp.slot(rp.v_begin + 3 * kTile + tid);
+      for (int t = 0; t < 4; ++t) rp.build_table(p, t, tid < kTile ? rp.slot(rp.v_begin + t * kTile + tid) : -1, tid);
+      if (tid < kTile) g_pref = rp.slot(rp.v_begin + 4 * kTile + tid);
       __syncthreads();
-      rp.fetch(0, tid, raw_a);
-      if (rp.ntiles > 1) rp.fetch(1, tid, raw_b);
-      rp.store(kt0, KT_PITCH, tid, raw_a);
-      if (rp.ntiles > 2) rp.fetch(2, tid, raw_a);
-      lds_barrier();  // Kt[0] complete
-      publish(qk(kt0));
+      rp.fetch(0, ptid, raw);
+      rp.store(ktile(0), KT_PITCH, ptid, raw);
+      rp.fetch(1, ptid, raw);
+      if (hg == 1) {  // group 1 also writes its half of tile 1 and holds tile 2
+        rp.store(ktile(1), KT_PITCH, ptid, raw);
+        rp.fetch(2, ptid, raw);
+      }
+      lds_barrier();  // tile 0 and half of tile 1 complete
+      if (hg == 0) publish(qk(ktile(0)));
     }
-    // tile t dequantizes tile t+1 from the set that tile t-1 refilled: sets alternate
+    // group 0 dequantizes tile u+1 from set (u+1)&1, group 1 tile u+2 from set u&1
+    // the loops execute the same barriers in the same order (two per tile, three in the
+    // exact pass)
+    if (hg == 0) {
 #pragma unroll 1
-    for (int t = 0; t < rp.ntiles; t += 2) {
-      tile_step(t, raw_b);
-      if (t + 1 < rp.ntiles) tile_step(t + 1, raw_a);
+      for (int u = 0; u < rp.ntiles; ++u) group0_pair(u, raw);
+    } else if (rp.ntiles > 0) {
+      // u = 0: no PV yet, QK(0) only
+      lds_barrier();
+      mfma_step(-1, false, true);
+      lds_barrier();
+      softmax(0);
+      rp.store(ktile(2), KT_PITCH, ptid, raw);
+      rp.fetch(3, ptid, raw);
+#pragma unroll 1
+      for (int u = 1; u < rp.ntiles; ++u) group1_pair(u, raw);
+    }
+    if (rp.ntiles > 0) {
+      lds_barrier();  // even(nt): the last P^T of group 1 complete
+      if (hg == 1) mfma_step(rp.ntiles - 1, true, false);
+      else if constexpr (kExact) lds_barrier();
     }
 
     // row sum: each lane holds the share of its entries (all scaled to the same running
@@ -874,12 +975,22 @@ int dispatch_heads(const AttnParams& p, int64_t rows, hipStream_t s) {
   if constexpr (D > 256) {
     // 64 heads per workgroup, each 32-head group split by D over 4 waves
     using M = SplitSmem<FMT, D, NOPE>;
-    static_assert(M::LDS <= 120 * 1024, "LDS budget");
+    static_assert(M::LDS + 4 * kSplitIdxCap + 8 * kTile * 8 + 64 <= 160 * 1024, "LDS budget");
     auto kern = sparse_mqa_dsplit_kernel<FMT, D, NOPE>;
-    static bool attr_set = false;
-    if (!attr_set) {
-      hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, M::LDS);
-      attr_set = true;
+    // the dynamic-LDS limit is a per-device function attribute: set once per device
+    static bool attr_set[kMaxDevices] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+      set_last_error("sparse_mqa: no usable current device");
+      return MZK_ELAUNCH;
+    }
+    if (!attr_set[dev]) {
+      if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              M::LDS) != hipSuccess) {
+        set_last_error("sparse_mqa: cannot raise the kernel's LDS limit to %d bytes", M::LDS);
+        return MZK_ELAUNCH;
+      }
+      attr_set[dev] = true;
     }
     return launch_kernel(kern, M::LDS, 512, 64, p, rows, s);
   } else {
