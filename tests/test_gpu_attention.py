@@ -244,3 +244,19 @@ def test_decode_rejects_misaligned_query(dev):
     with pytest.raises(Exception, match="16-byte aligned"):
         MA.sparse_mqa_decode(q_off, positions, win_c, 128, main_cache=main_c, groups=g, indices=idx.to(dev),
                              sinks=sinks.to(dev), nsplit=2)
+
+
+@pytest.mark.parametrize("h,pos,nsplit", [(96, 40, 4), (72, 40, 8), (128, 9, 16), (64, 700, 1), (20, 3000, 5)])
+def test_decode_short_and_partial_head_groups(dev, h, pos, nsplit):
+    """The 576-wide kernel's edge cases: head counts that leave a head group partly empty,
+    splits of one tile, splits with no entry at all (more splits than tiles), and a single
+    split of many tiles."""
+    b, gcap = 3, 512
+    topk = min(64, (pos + 1) // 4) or 1
+    q, win_c, main_c, _, idx, sinks, g = _decode_case(dev, b, h, gcap, topk, pos, seed=h + pos)
+    positions = torch.full((b,), pos, dtype=torch.int64, device=dev)
+    o, lse = MA.sparse_mqa_decode(q.to(dev), positions, win_c, 128, main_cache=main_c, groups=g,
+                                  indices=idx.to(dev), sinks=sinks.to(dev), nsplit=nsplit)
+    ref, ref_lse = _decode_oracle(q, win_c, main_c, None, idx, sinks, pos, 128, 1, g)
+    assert_attn_close(o, ref)
+    torch.testing.assert_close(lse.cpu(), ref_lse, **LSE_TOL)
