@@ -215,43 +215,31 @@ __device__ __forceinline__ int wave_incl_scan_dpp(int v) {
 constexpr int kSub = 16;
 constexpr int kHist = 256 * kSub;
 
-// Digit selection by one wave over a histogram.  The 16 KiB of counters are read with
-// consecutive lanes on consecutive 16 B (conflict-free): read r gives lane l the four
-// counters 4(l%4).. of bin 16r + l/4, a quad reduction completes each bin, and the 256 bin
-// totals go through `tot` so that lane l then owns bins 255-4l .. 252-4l in descending
-// order: an inclusive prefix over lanes counts the entries in higher bins.  Finds the bin
-// holding the rem-th largest key; returns its digit, the rank left inside it, and whether
-// the whole bin is taken (rank == count).
+// Digit selection in two steps.  (1) Every wave folds the sub-counters of its 256 / NW
+// bins into bin totals: consecutive lanes read consecutive 16 B (conflict-free), each
+// int4 being the four counters 4(l%4).. of one bin, and a quad reduction completes the
+// bin.  (2) After a barrier, one wave owns bins 255-4l .. 252-4l in lane l (descending),
+// so an inclusive prefix over lanes counts the entries in higher bins; it finds the bin
+// holding the rem-th largest key and returns its digit, the rank left inside it, and
+// whether the whole bin is taken (rank == count).
 struct DigitSel {
   int digit, rem, whole;
 };
-__device__ __forceinline__ DigitSel select_digit(const int* hist, int* tot, int rem, int lane) {
+template <int NW>
+__device__ __forceinline__ void reduce_bins(const int* hist, int* tot, int wave, int lane) {
   static_assert(kSub == 16, "one int4 per lane covers a quarter of a bin");
-  const int4* h4 = reinterpret_cast<const int4*>(hist);
-  int part[16];
+  constexpr int R = 1024 / NW / 64;  // int4 reads per lane (each wave folds 1024/NW int4)
+  const int4* h4 = reinterpret_cast<const int4*>(hist) + wave * (1024 / NW);
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int4 v = h4[r * 64 + lane];
-    part[r] = (v.x + v.y) + (v.z + v.w);
+  for (int r = 0; r < R; ++r) {
+    const int4 v = h4[r * 64 + lane];  // bin (wave * 1024/NW + 64 r + lane) / 4
+    int c = (v.x + v.y) + (v.z + v.w);
+    c += __builtin_amdgcn_update_dpp(0, c, 0xb1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+    c += __builtin_amdgcn_update_dpp(0, c, 0x4e, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+    if ((lane & 3) == 0) tot[(wave * (1024 / NW) + r * 64 + lane) >> 2] = c;
   }
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    // quad butterfly: lanes 4m..4m+3 all end with bin 16r + m's total
-    part[r] += __builtin_amdgcn_update_dpp(0, part[r], 0xb1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
-    part[r] += __builtin_amdgcn_update_dpp(0, part[r], 0x4e, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
-  }
-  // lane l stores bins 16r + l/4 for r = l%4, l%4+4, l%4+8, l%4+12
-#pragma unroll
-  for (int r4 = 0; r4 < 4; ++r4) {
-    int v = part[r4 * 4];
-#pragma unroll
-    for (int e = 1; e < 4; ++e)
-      if ((lane & 3) == e) v = part[r4 * 4 + e];
-    tot[16 * (r4 * 4 + (lane & 3)) + (lane >> 2)] = v;
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+__device__ __forceinline__ DigitSel select_digit(const int* tot, int rem, int lane) {
   const int4 t4 = reinterpret_cast<const int4*>(tot)[63 - lane];  // bins 252-4l .. 255-4l
   const int h[4] = {t4.w, t4.z, t4.y, t4.x};                      // h[j] = bin 255-4l-j
   const int s = (h[0] + h[1]) + (h[2] + h[3]);
@@ -284,12 +272,14 @@ __device__ __forceinline__ DigitSel select_digit(const int* hist, int* tot, int 
 // Compaction: the output slot of an entry is (#key > T before it) +
 // min(#key == T before it, need_eq), so one exclusive scan of the packed pair
 // (n_gt << 16 | n_eq) gives every position.
-template <int KPT>
-__global__ void __launch_bounds__(kThreads) topk_rows_reg_kernel(const float* __restrict__ scores, int64_t row_stride,
+template <int KPT, int NT>
+__global__ void __launch_bounds__(NT) topk_rows_reg_kernel(const float* __restrict__ scores, int64_t row_stride,
                                                                  int G, int k, int32_t* __restrict__ out,
                                                                  int64_t out_stride) {
   __shared__ __align__(16) int hist[2][kHist];
-  __shared__ __align__(16) int wsum[kWaves];
+  constexpr int NW = NT / 64;
+  static_assert(NW % 4 == 0, "wave sums are read as int4");
+  __shared__ __align__(16) int wsum[NW];
   __shared__ int sel[2][3];  // digit, rem, whole of the pass using hist[p & 1]
   __shared__ __align__(16) int bin_tot[256];
 
@@ -317,7 +307,7 @@ __global__ void __launch_bounds__(kThreads) topk_rows_reg_kernel(const float* __
   }
   {
     int4* h4 = reinterpret_cast<int4*>(&hist[0][0]);
-    for (int i = tid; i < 2 * kHist / 4; i += kThreads) h4[i] = int4{0, 0, 0, 0};
+    for (int i = tid; i < 2 * kHist / 4; i += NT) h4[i] = int4{0, 0, 0, 0};
   }
   __syncthreads();  // histograms cleared (while the scores are in flight)
 
@@ -336,7 +326,7 @@ __global__ void __launch_bounds__(kThreads) topk_rows_reg_kernel(const float* __
   {
     const int4* w4 = reinterpret_cast<const int4*>(wsum);
 #pragma unroll
-    for (int q = 0; q < kWaves / 4; ++q) {
+    for (int q = 0; q < NW / 4; ++q) {
       const int4 v = w4[q];
       total_fin += (v.x + v.y) + (v.z + v.w);
     }
@@ -351,18 +341,21 @@ __global__ void __launch_bounds__(kThreads) topk_rows_reg_kernel(const float* __
     for (int pass = 0; pass < 4; ++pass) {
       const int shift = 24 - 8 * pass;
       const int cur = pass & 1;
+      reduce_bins<NW>(hist[cur], bin_tot, wave, lane);
+      if (pass > 0) {
+        // the next pass's copy (its last reader, the reduction two passes ago, is done);
+        // hist[1] is still clear for the second pass
+        int4* h4 = reinterpret_cast<int4*>(&hist[cur ^ 1][0]);
+        for (int i = tid; i < kHist / 4; i += NT) h4[i] = int4{0, 0, 0, 0};
+      }
+      __syncthreads();  // bin totals complete
       if (wave == 0) {
-        const DigitSel r = select_digit(hist[cur], bin_tot, rem, lane);
+        const DigitSel r = select_digit(bin_tot, rem, lane);
         if (lane == 0) {
           sel[cur][0] = r.digit;
           sel[cur][1] = r.rem;
           sel[cur][2] = r.whole;
         }
-      } else if (pass > 0) {
-        // the next pass's copy (its last reader, the selection two passes ago, is done);
-        // hist[1] is still clear for the second pass
-        int4* h4 = reinterpret_cast<int4*>(&hist[cur ^ 1][0]);
-        for (int i = tid - 64; i < kHist / 4; i += kThreads - 64) h4[i] = int4{0, 0, 0, 0};
       }
       __syncthreads();  // selection published, next copy cleared
       const uint32_t digit = static_cast<uint32_t>(sel[cur][0]);
@@ -405,7 +398,7 @@ __global__ void __launch_bounds__(kThreads) topk_rows_reg_kernel(const float* __
   {
     const int4* w4 = reinterpret_cast<const int4*>(wsum);
 #pragma unroll
-    for (int q = 0; q < kWaves / 4; ++q) {
+    for (int q = 0; q < NW / 4; ++q) {
       const int4 v = w4[q];
       const int w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -427,7 +420,7 @@ __global__ void __launch_bounds__(kThreads) topk_rows_reg_kernel(const float* __
       ++eq_before;
     }
   }
-  for (int i = written + tid; i < k; i += kThreads) dst[i] = -1;
+  for (int i = written + tid; i < k; i += NT) dst[i] = -1;
 }
 
 }  // namespace
@@ -447,11 +440,11 @@ extern "C" int mzk_topk_rows(const float* scores, int64_t rows, int64_t cols, in
   const int G = static_cast<int>(cols);
   const unsigned nr = static_cast<unsigned>(rows);
   if (G <= 8 * kThreads)
-    topk_rows_reg_kernel<8><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
+    topk_rows_reg_kernel<8, kThreads><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
   else if (G <= 16 * kThreads)
-    topk_rows_reg_kernel<16><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
+    topk_rows_reg_kernel<16, kThreads><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
   else if (G <= 32 * kThreads)
-    topk_rows_reg_kernel<32><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
+    topk_rows_reg_kernel<32, kThreads><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
   else if (G <= kLdsKeys)
     topk_rows_kernel<true><<<nr, kThreads, static_cast<size_t>(G) * 4, s>>>(scores, row_stride, G, topk, out,
                                                                            out_stride);
