@@ -260,3 +260,32 @@ def test_decode_short_and_partial_head_groups(dev, h, pos, nsplit):
     ref, ref_lse = _decode_oracle(q, win_c, main_c, None, idx, sinks, pos, 128, 1, g)
     assert_attn_close(o, ref)
     torch.testing.assert_close(lse.cpu(), ref_lse, **LSE_TOL)
+
+
+@pytest.mark.parametrize("nsplit", [2, 4, 16])
+def test_decode_split_merge_paths_agree(dev, nsplit):
+    """One call with an output (attention + merge) equals writing only the partials and
+    merging them with mzk_sparse_mqa_combine, bit for bit, call after call on one
+    workspace."""
+    from mzoo_amd import _lib
+    b, h, gcap, topk, pos = 8, 128, 2048, 512, 8191
+    q, win_c, main_c, _, idx, sinks, g = _decode_case(dev, b, h, gcap, topk, pos, seed=31 + nsplit)
+    qd, idxd, sk = q.to(dev), idx.to(dev), sinks.to(dev)
+    positions = torch.full((b,), pos, dtype=torch.int64, device=dev)
+    ws = MA.new_workspace(b, h, 576, nsplit, dev)
+    args = dict(main_cache=main_c, groups=g, indices=idxd, sinks=sk, nsplit=nsplit, workspace=ws)
+    outs = [MA.sparse_mqa_decode(qd, positions, win_c, 128, **args) for _ in range(3)]
+    for o, l in outs[1:]:
+        assert torch.equal(o, outs[0][0]) and torch.equal(l, outs[0][1])
+    # partials only (no out), then the combine kernel
+    st = torch.cuda.current_stream().cuda_stream
+    _lib.call("mzk_sparse_mqa", qd.data_ptr(), b, 1, h, 576, 1, 512, positions.data_ptr(), win_c.data_ptr(),
+              128, 128, 128, None, 0, 0, 1, main_c.data_ptr(), gcap, g, idxd.data_ptr(), topk, topk,
+              sk.data_ptr(), nsplit, ws.data_ptr(), ws.numel() * ws.element_size(), None, None, st)
+    o2 = torch.empty_like(qd)
+    l2 = torch.empty(b, h, dtype=torch.float32, device=dev)
+    _lib.call("mzk_sparse_mqa_combine", ws.data_ptr(), b, 1, h, 576, nsplit, sk.data_ptr(), o2.data_ptr(),
+              l2.data_ptr(), st)
+    assert torch.equal(o2, outs[0][0]) and torch.equal(l2, outs[0][1])
+    ref, ref_lse = _decode_oracle(q, win_c, main_c, None, idx, sinks, pos, 128, 1, g)
+    assert_attn_close(outs[0][0], ref)
