@@ -188,6 +188,12 @@ struct RowPlan {
   // 32-bit arithmetic: the host keeps the grid below 2^31 workgroups and the list
   // lengths (window + dense_cap + topk) below 2^31.
   __device__ void init(const AttnParams& p, int heads_per_wg) {
+    locate(p, heads_per_wg);
+    plan(p, p.positions[row]);
+  }
+
+  // The workgroup's (row, split, head group); no memory access.
+  __device__ void locate(const AttnParams& p, int heads_per_wg) {
     const uint32_t nhg = static_cast<uint32_t>((p.H + heads_per_wg - 1) / heads_per_wg);
     const uint32_t units = static_cast<uint32_t>(p.rows) * static_cast<uint32_t>(p.nsplit);
     const uint32_t L0 = blockIdx.x;
@@ -204,8 +210,11 @@ struct RowPlan {
     split = static_cast<int>(unit - row32 * static_cast<uint32_t>(p.nsplit));
     row = row32;
     b = row32 / static_cast<uint32_t>(p.S);
-    pos = p.positions[row];
+  }
 
+  // The row's entry list split, given its absolute position.
+  __device__ void plan(const AttnParams& p, int64_t row_pos) {
+    pos = row_pos;
     nw = static_cast<int>(pos + 1 < p.window ? pos + 1 : p.window);
     int nd = 0;
     if (p.dense) {
@@ -242,6 +251,39 @@ struct RowPlan {
     sidx_cap = cap;
   }
 
+  // Request the row's first 4*NT sparse indices, one 16-byte load per thread, before the
+  // row's position (which fixes this split's slice) is known, so the two loads overlap.
+  // Returns false (and loads nothing) unless the whole list fits and its row is 16-byte
+  // aligned; then stage_indices reads it after the position.
+  __device__ bool prefetch_indices(const AttnParams& p, int tid, v4i& pre) {
+    idx_row = p.idx ? (const __attribute__((address_space(1))) int32_t*)(p.idx + row * p.idx_row_stride) : nullptr;
+    const bool ok = idx_row != nullptr && p.topk > 0 && p.topk <= 4 * NT && (p.topk & 3) == 0 &&
+                    (reinterpret_cast<uintptr_t>(idx_row) & 15u) == 0;
+    // branch-free: every thread loads from a valid address (the query, 16-byte aligned, when
+    // the list is not used), so the compiler's in-order wait counts stay exact
+    const int at = 4 * tid < p.topk ? 4 * tid : p.topk - 4;
+    const __attribute__((address_space(1))) v4i* src =
+        ok ? reinterpret_cast<const __attribute__((address_space(1))) v4i*>(idx_row + at)
+           : (const __attribute__((address_space(1))) v4i*)(p.q);
+    pre = *src;
+    if (!ok || 4 * tid >= p.topk) pre = v4i{-1, -1, -1, -1};
+    return ok;
+  }
+
+  // stage_indices from the prefetched list (prefetch_indices returned true): the thread
+  // holding list positions 4tid..4tid+3 writes those inside the slice.
+  __device__ void stage_prefetched(int32_t* sidx_lds, int cap, int tid, const v4i& pre) {
+    const int sp_end = v_end > nwd ? v_end - nwd : 0;
+    const int lim = sp_end < sp_begin + cap ? sp_end : sp_begin + cap;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int s = 4 * tid + j;
+      if (s >= sp_begin && s < lim) sidx_lds[s - sp_begin] = pre[j];
+    }
+    sidx = (const __attribute__((address_space(3))) int32_t*)(sidx_lds);
+    sidx_cap = cap;
+  }
+
   // sparse index of list position v (-1 outside the sparse part of this split)
   __device__ int slot(int v) const {
     if (v < nwd || v >= v_end) return -1;
@@ -250,25 +292,44 @@ struct RowPlan {
     return idx_row[sp_begin + s];
   }
 
+  // address of entry e of tile t (null if empty); g = its sparse index (slot of the entry)
+  __device__ const uint8_t* entry_ptr(const AttnParams& p, int t, int e, int g) const {
+    const int v = v_begin + t * kTile + e;
+    const uint8_t* ptr = nullptr;
+    if (v < v_end) {
+      if (v < nw) {
+        int slot_w = win_first + v;
+        if (p.win_cap && slot_w >= p.win_cap) slot_w -= p.win_cap;
+        ptr = win_b + static_cast<int64_t>(slot_w) * L::kEntryBytes;
+      } else if (v < nwd) {
+        ptr = dense_b + static_cast<int64_t>(v - nw) * L::kEntryBytes;
+      } else if (g >= 0 && g < g_lim) {
+        ptr = main_b + static_cast<int64_t>(g) * L::kEntryBytes;
+      }
+    }
+    return ptr;
+  }
+
   // entry table of tile t (threads 0..31); g = this thread's prefetched sparse index
   __device__ void build_table(const AttnParams& p, int t, int g, int tid) {
     if (tid < kTile) {
-      const int v = v_begin + t * kTile + tid;
-      const uint8_t* ptr = nullptr;
-      if (v < v_end) {
-        if (v < nw) {
-          int slot_w = win_first + v;
-          if (p.win_cap && slot_w >= p.win_cap) slot_w -= p.win_cap;
-          ptr = win_b + static_cast<int64_t>(slot_w) * L::kEntryBytes;
-        } else if (v < nwd) {
-          ptr = dense_b + static_cast<int64_t>(v - nw) * L::kEntryBytes;
-        } else if (g >= 0 && g < g_lim) {
-          ptr = main_b + static_cast<int64_t>(g) * L::kEntryBytes;
-        }
-      }
+      const uint8_t* ptr = entry_ptr(p, t, tid, g);
       tab_ptr[(t % NSLOT) * kTile + tid] = ptr;
       const uint64_t bal = __ballot(ptr != nullptr);
       if (tid == 0) tab_mask[t % NSLOT] = static_cast<uint32_t>(bal);
+    }
+  }
+
+  // entry tables of tiles 0..3 at once (after the indices are staged): thread tid < 4*kTile
+  // fills entry tid % kTile of tile tid / kTile, two tiles per wave
+  __device__ void build_first_tables(const AttnParams& p, int tid) {
+    static_assert(NSLOT >= 4 && NT >= 4 * kTile, "four tables in flight");
+    if (tid < 4 * kTile) {
+      const int t = tid / kTile, e = tid % kTile;
+      const uint8_t* ptr = entry_ptr(p, t, e, slot(v_begin + t * kTile + e));
+      tab_ptr[t * kTile + e] = ptr;
+      const uint64_t bal = __ballot(ptr != nullptr);
+      if (e == 0) tab_mask[t] = static_cast<uint32_t>(bal >> (32 * (t & 1)));
     }
   }
 
@@ -342,7 +403,7 @@ __device__ __forceinline__ void write_result(const AttnParams& p, int64_t row, i
     } else {
       o_scale = 1.0f / l_fin;
     }
-    uint16_t* orow = p.out + (row * p.H + head) * D + b_lo * 32;
+    uint16_t* orow = p.out + row * p.H * D + static_cast<uint32_t>(head * D + b_lo * 32);
 #pragma unroll
     for (int db = 0; db < NDBM; ++db) {
       if (db < nb) {
@@ -364,7 +425,8 @@ __device__ __forceinline__ void write_result(const AttnParams& p, int64_t row, i
   } else {
     // the split's own normalized output in bf16 (a split that saw no entry writes zeros)
     const float inv_l = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-    uint16_t* prow = p.part_o + ((row * p.nsplit + split) * p.H + head) * static_cast<int64_t>(D) + b_lo * 32;
+    uint16_t* prow = p.part_o + (row * p.nsplit + split) * p.H * static_cast<int64_t>(D) +
+                     static_cast<uint32_t>(head * D + b_lo * 32);
 #pragma unroll
     for (int db = 0; db < NDBM; ++db) {
       if (db < nb) {
@@ -378,7 +440,7 @@ __device__ __forceinline__ void write_result(const AttnParams& p, int64_t row, i
       }
     }
     if (lse_lane) {
-      float* ml = p.part_ml + ((row * p.nsplit + split) * p.H + head) * 2;
+      float* ml = p.part_ml + (row * p.nsplit + split) * p.H * 2 + static_cast<uint32_t>(head * 2);
       ml[0] = m_run;
       ml[1] = l_run;
     }
@@ -583,9 +645,12 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
   RP rp;
   rp.tab_ptr = tab_ptr;
   rp.tab_mask = tab_mask;
-  rp.init(p, HG * 32);
-  rp.stage_indices(p, sidx, kSplitIdxCap, tid);
-  __syncthreads();
+  rp.locate(p, HG * 32);
+  // The row's index list, its position and this lane's query fragment are requested
+  // together: one memory round trip at the start instead of three dependent ones.
+  v4i pre;
+  const bool pre_ok = rp.prefetch_indices(p, tid, pre);
+  const int64_t row_pos = p.positions[rp.row];
 
   const int hl = hg * 32 + (lane & 31);  // head within the workgroup
   const int head = rp.hgrp * (HG * 32) + hl;
@@ -593,13 +658,21 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
   const int qc0 = ds * QST * 16;  // first QK channel of this wave
   v8bf qf[QST];
   {
-    const uint16_t* qrow = p.q + (rp.row * p.H + (head_ok ? head : 0)) * D + qc0 + half * 8;
+    // branch-free loads (a missing head reads head 0 and is zeroed); uniform row base plus a
+    // 32-bit lane offset (H <= 128) keeps no 64-bit per-lane address alive
+    const uint16_t* qbase = p.q + rp.row * p.H * D;
+    const uint32_t qoff = static_cast<uint32_t>((head_ok ? head : 0) * D + qc0 + half * 8);
 #pragma unroll
     for (int st = 0; st < QST; ++st) {
-      uint4 v = head_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * st) : uint4{0, 0, 0, 0};
-      qf[st] = __builtin_bit_cast(v8bf, v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w});
+      v4i v = *reinterpret_cast<const v4i*>(qbase + qoff + 16 * st);
+      if (!head_ok) v = v4i{0, 0, 0, 0};
+      qf[st] = __builtin_bit_cast(v8bf, v);
     }
   }
+  rp.plan(p, row_pos);
+  if (pre_ok) rp.stage_prefetched(sidx, kSplitIdxCap, tid, pre);
+  else rp.stage_indices(p, sidx, kSplitIdxCap, tid);
+  __syncthreads();
   const int b_lo = ds * NB / DS;
   const int nb_mine = (ds + 1) * NB / DS - b_lo;
   const int pv_off = pv_lane_offset<KT_PITCH>(lane, b_lo * 32);
@@ -802,9 +875,12 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
       lds_barrier();
       softmax(u);
       rp.store(ktile(u + 1), KT_PITCH, ptid, r0);
+      // the index of tile u+5 is read before the fetch is issued: the wait on that read
+      // (the compiler's counters are in order) then covers no fetch load
+      const int g_next = tid < kTile ? rp.slot(rp.v_begin + (u + 5) * kTile + tid) : -1;
       rp.fetch(u + 2, ptid, r0);
       rp.build_table(p, u + 4, g_pref, tid);
-      if (tid < kTile) g_pref = rp.slot(rp.v_begin + (u + 5) * kTile + tid);
+      g_pref = g_next;
       lds_barrier();
       mfma_step(u, true, true);
     };
@@ -818,8 +894,7 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
       rp.fetch(u + 3, ptid, r1);
     };
     if (rp.ntiles > 0) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) rp.build_table(p, t, tid < kTile ? rp.slot(rp.v_begin + t * kTile + tid) : -1, tid);
+      rp.build_first_tables(p, tid);
       if (tid < kTile) g_pref = rp.slot(rp.v_begin + 4 * kTile + tid);
       __syncthreads();
       rp.fetch(0, ptid, raw);
