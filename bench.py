@@ -3,10 +3,14 @@
 Workload: one CSA2 attention layer decoding one token per row for
 B=32 rows at context 32768: bf16 queries, 128 heads over the shared 512+64 latent stored
 as FP8-b128 (656 B/entry), FP8 lightning indexer 64x128 over the 8192 compressed entries
-(ratio 4), top-2048, sliding window 128, per-head sink.  A "step" is one graph replay of
-``SparseDecodeLayer.step``: window append, indexer-query quantization, indexer scores,
-top-k, sparse MQA (split-KV) and the split merge.  Inputs are synthetic (seed 1) and
-resident in HBM before timing starts.
+(ratio 4), top-2048, sliding window 128, per-head sink.  A "step" is one replay of a HIP
+graph holding ``SparseDecodeLayer.step`` of --layers (default 8) consecutive layers, each
+with its own caches and inputs, as a model's decode graph holds its layers: per layer the
+window append, indexer-query quantization, indexer scores, top-k, sparse MQA (split-KV) and
+the split merge.  Distinct layers keep one layer's working set (about 90 MB) from being
+served out of the last-level cache on the next step.  value = B x layers / replay time
+(token-rows through one attention layer per second); ms_per_step is per layer.  Inputs are
+synthetic (seeds 1..layers) and resident in HBM before timing starts.
 
 Prints one JSON line (metric, value = decode tokens/s on this GPU, roofline of the
 dominant kernel measured with HIP events on its stream, cpu_baseline = the CPU oracle's
@@ -42,6 +46,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--nsplit", type=int, default=4)
+    ap.add_argument("--layers", type=int, default=8, help="distinct attention layers in the replayed graph")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline time budget")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--stage-iters", type=int, default=0, help="launches per stage timing (0: max(steps, 50))")
@@ -51,12 +56,12 @@ def parse():
     return ap.parse_args()
 
 
-def build_layer(torch, dev, nsplit):
+def build_layer(torch, dev, nsplit, seed=1):
     from mzoo_amd.decode import DecodeConfig, SparseDecodeLayer
     cfg = DecodeConfig(batch=32, heads=128, nope=512, rope=64, index_heads=64, index_dim=128, ratio=4, window=128,
                        topk=2048, max_groups=8192, index_format="fp8", nsplit=nsplit)
     ctx = 32768
-    gen = torch.Generator(device=dev).manual_seed(1)
+    gen = torch.Generator(device=dev).manual_seed(seed)
     sinks = torch.randn(cfg.heads, generator=gen, device=dev)
     layer = SparseDecodeLayer(cfg, dev, sinks=sinks)
     b, d = cfg.batch, cfg.dim
@@ -85,8 +90,54 @@ def time_launches(torch, fn, iters):
     return e0.elapsed_time(e1) / iters * 1e3  # microseconds
 
 
-def stage_times(torch, layer, inputs, iters):
-    """Each kernel of the step alone, same inputs, same stream."""
+def capture_layers(torch, layers, inputs):
+    """One HIP graph over the decode steps of several layers (static copies of the inputs);
+    warm-up on a side stream first, as ``SparseDecodeLayer.capture`` does for one layer."""
+    statics = [tuple(t.clone() for t in inp) for inp in inputs]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            for layer, st in zip(layers, statics):
+                layer.step(*st)
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for layer, st in zip(layers, statics):
+            layer.step(*st)
+    return g, statics
+
+
+def stage_times(torch, layers, inputs, iters):
+    """Average duration of each kernel of the step alone: a HIP graph of back-to-back
+    launches of that kernel cycling through the layers (consecutive launches read different
+    caches, as in the decode graph), replayed and timed with HIP events on the stream the
+    kernels run on.  Inside a graph the launches follow each other with no host gap, so the
+    figure is the kernel's own duration."""
+    per_layer = [stage_fns(torch, layer, inp) for layer, inp in zip(layers, inputs)]
+    nl = len(per_layer)
+    reps = max(1, (32 + nl - 1) // nl)  # at least 32 launches per replay (amortizes the replay launch)
+    replays = max(1, iters // (reps * nl))
+    out = {}
+    for name in per_layer[0]:
+        fns = [d[name] for d in per_layer]
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for f in fns:
+                f()
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                for f in fns:
+                    f()
+        out[name] = time_launches(torch, g.replay, replays) / (reps * nl)
+    return out
+
+
+def stage_fns(torch, layer, inputs):
+    """The step's launches for one layer, each callable alone."""
     from mzoo_amd import _lib, indexer
     cfg = layer.cfg
     b = cfg.batch
@@ -113,13 +164,12 @@ def stage_times(torch, layer, inputs, iters):
         _lib.call("mzk_sparse_mqa_combine", ws.data_ptr(), b, 1, cfg.heads, cfg.dim, cfg.nsplit,
                   layer.sinks.data_ptr(), layer.out.data_ptr(), layer.lse.data_ptr(), st())
 
-    stages = {
+    return {
         "indexer_decode_fp8": indexer_decode,
         "topk": lambda: indexer.topk(layer.scores.view(b, cfg.max_groups), cfg.topk, out=layer.idx),
         "sparse_mqa": attn,
         "sparse_mqa_combine": combine,
     }
-    return {k: time_launches(torch, f, iters) for k, f in stages.items()}
 
 
 def cpu_baseline(torch, layer, inputs, budget_s):
@@ -187,21 +237,25 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4}))
         return
-    layer, inputs, _ = build_layer(torch, dev, args.nsplit)
+    nl = max(1, args.layers)
+    built = [build_layer(torch, dev, args.nsplit, seed=1 + i) for i in range(nl)]
+    layers = [b_[0] for b_ in built]
+    inputs_all = [b_[1] for b_ in built]
+    layer, inputs = layers[0], inputs_all[0]
     cfg = layer.cfg
-    layer.capture(*inputs, advance=False)
+    graph, _ = capture_layers(torch, layers, inputs_all)
     for _ in range(args.warmup):
-        layer.replay()
+        graph.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        layer.replay()
+        graph.replay()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    ms = elapsed / args.steps * 1e3
+    ms = elapsed / (args.steps * nl) * 1e3  # per layer
     tokens_per_s = cfg.batch / (ms / 1e3)
 
-    stages = stage_times(torch, layer, inputs, args.stage_iters or max(args.steps, 50))
+    stages = stage_times(torch, layers, inputs_all, args.stage_iters or max(args.steps, 50))
     # algorithmic work per launch
     rows = cfg.batch
     entries = cfg.window + cfg.topk
@@ -245,11 +299,12 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seed 1), caches resident in HBM",
+        "data": f"synthetic (seeds 1..{nl}, one per layer), caches resident in HBM",
         "config": {"workload": "config2: decode B=32 ctx=32768, 128 heads x (512+64) FP8-b128 latent cache, "
                                "FP8 indexer 64x128 over 8192 groups (ratio 4), top-2048, window 128, sink",
                    "batch": cfg.batch, "context": 32768, "heads": cfg.heads, "latent": "512+64",
-                   "index": "64x128 fp8", "topk": cfg.topk, "window": cfg.window, "nsplit": cfg.nsplit},
+                   "index": "64x128 fp8", "topk": cfg.topk, "window": cfg.window, "nsplit": cfg.nsplit,
+                   "graph_layers": nl, "step": "per attention layer, inside a graph replay of graph_layers layers"},
         "roofline": roof,
         "cpu_baseline": cpu,
         "stages_us": stages,
