@@ -1,20 +1,25 @@
 """Decode throughput of the sparse-attention hot path on one MI355X.
 
-Workload: one CSA2 attention layer decoding one token per row for
-B=32 rows at context 32768: bf16 queries, 128 heads over the shared 512+64 latent stored
-as FP8-b128 (656 B/entry), FP8 lightning indexer 64x128 over the 8192 compressed entries
-(ratio 4), top-2048, sliding window 128, per-head sink.  A "step" is one replay of a HIP
-graph holding ``SparseDecodeLayer.step`` of --layers (default 8) consecutive layers, each
-with its own caches and inputs, as a model's decode graph holds its layers: per layer the
-window append, indexer-query quantization, indexer scores, top-k, sparse MQA (split-KV) and
-the split merge.  Distinct layers keep one layer's working set (about 90 MB) from being
-served out of the last-level cache on the next step.  value = B x layers / replay time
-(token-rows through one attention layer per second); ms_per_step is per layer.  Inputs are
-synthetic (seeds 1..layers) and resident in HBM before timing starts.
+Default workload (the headline metric): one CSA2 attention layer decoding
+one token per row for B=32 rows at context 32768: bf16 queries, 128 heads over the shared
+512+64 latent stored as FP8-b128 (656 B/entry), FP8 lightning indexer 64x128 over the 8192
+compressed entries (ratio 4), top-2048, sliding window 128, per-head sink.  A "step" is one
+replay of a HIP graph holding ``SparseDecodeLayer.step`` of --layers (default 8)
+consecutive layers, each with its own caches and inputs, as a model's decode graph holds its
+layers: per layer the window append, indexer-query quantization, indexer scores, top-k,
+sparse MQA (split-KV) and the split merge.  Distinct layers keep one layer's working set
+(about 90 MB) from being served out of the last-level cache on the next step.  value =
+B x layers / replay time (token-rows through one attention layer per second); ms_per_step
+is per layer.  Inputs are synthetic and resident in HBM before timing starts.
 
-Prints one JSON line (metric, value = decode tokens/s on this GPU, roofline of the
-dominant kernel measured with HIP events on its stream, cpu_baseline = the CPU oracle's
-decode step on this host's cores over the same workload).
+--config 4 / 5 run the MXFP4-index decode (B=8, 32768 groups) and the hierarchical decode
+(B=4: dense coarse branch of 4096 entries + MXFP4 fine index over 131072 groups) the same
+way; --config 3 times the causal prefill (B=1, S=8192: FP8 indexer over 2048 groups ->
+top-2048 -> sparse MQA with window 128 on every query row), value = query tokens/s.
+
+Prints one JSON line (metric, value, roofline of the dominant kernel measured with HIP
+events on its stream, cpu_baseline = the CPU oracle on this host's cores over a bounded
+sample of the same workload).
 """
 
 from __future__ import annotations
@@ -34,18 +39,33 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 FP8_PEAK_TFLOPS = 5000.0
 
-# Algorithmic work per decoded row
+# Algorithmic work (bytes a perfect kernel moves)
 ENTRY_BYTES = 656                 # FP8-b128 latent entry
-QO_BYTES = 2 * 128 * 576 * 2      # q read + out written, bf16
-IDX_KEY_BYTES = 132               # FP8 indexer key (128 codes + fp32 scale)
+QO_BYTES = 2 * 128 * 576 * 2      # q read + out written per decoded row, bf16
+KEY_BYTES = {"fp8": 132, "mxfp4": 68}  # indexer key: codes + scale(s)
+
+METRIC = "decode tokens/s/GPU at 32k ctx (sparse MQA + indexer); % HBM/MFMA roofline"
+
+DECODE = {
+    2: dict(batch=32, ctx=32768, groups=8192, index_format="fp8", coarse_ratio=0, coarse_groups=0, nsplit=4, seed=1,
+            text="config2: decode B=32 ctx=32768, 128 heads x (512+64) FP8-b128 latent cache, FP8 indexer 64x128 "
+                 "over 8192 groups (ratio 4), top-2048, window 128, sink"),
+    4: dict(batch=8, ctx=131072, groups=32768, index_format="mxfp4", coarse_ratio=0, coarse_groups=0, nsplit=16,
+            seed=2, text="config4: decode B=8 ctx=131072, 128 heads x (512+64) FP8-b128 latent cache, MXFP4 indexer "
+                         "64x128 over 32768 groups (ratio 4), top-2048, window 128, sink"),
+    5: dict(batch=4, ctx=524288, groups=131072, index_format="mxfp4", coarse_ratio=128, coarse_groups=4096, nsplit=32,
+            seed=4, text="config5: hierarchical decode B=4 ctx=524288, dense coarse branch of 4096 entries (ratio 128) "
+                         "+ MXFP4 fine indexer 64x128 over 131072 groups, top-2048, window 128, merged by log-sum-exp"),
+}
 
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5], help="BASELINE configuration")
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--nsplit", type=int, default=4)
+    ap.add_argument("--nsplit", type=int, default=0, help="attention splits per row (0: the config's default)")
     ap.add_argument("--layers", type=int, default=8, help="distinct attention layers in the replayed graph")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline time budget")
     ap.add_argument("--no-cpu", action="store_true")
@@ -56,23 +76,34 @@ def parse():
     return ap.parse_args()
 
 
-def build_layer(torch, dev, nsplit, seed=1):
+def build_layer(torch, dev, nsplit=0, seed=None, config=2):
+    """A decode layer of BASELINE config `config` (2, 4 or 5) with synthetic history: the
+    window ring holds tokens ctx-129 .. ctx-2, every compressed group is published, and the
+    step decodes the token at position ctx-1 (every group visible)."""
     from mzoo_amd.decode import DecodeConfig, SparseDecodeLayer
-    cfg = DecodeConfig(batch=32, heads=128, nope=512, rope=64, index_heads=64, index_dim=128, ratio=4, window=128,
-                       topk=2048, max_groups=8192, index_format="fp8", nsplit=nsplit)
-    ctx = 32768
-    gen = torch.Generator(device=dev).manual_seed(seed)
-    sinks = torch.randn(cfg.heads, generator=gen, device=dev)
+    c = DECODE[config]
+    cfg = DecodeConfig(batch=c["batch"], heads=128, nope=512, rope=64, index_heads=64, index_dim=128, ratio=4,
+                       window=128, topk=2048, max_groups=c["groups"], index_format=c["index_format"],
+                       coarse_ratio=c["coarse_ratio"], coarse_groups=c["coarse_groups"], nsplit=nsplit or c["nsplit"])
+    ctx = c["ctx"]
+    gen = torch.Generator(device=dev).manual_seed(c["seed"] if seed is None else seed)
+    rnd = lambda *shape: torch.randn(*shape, generator=gen, device=dev)  # noqa: E731
+    sinks = rnd(cfg.heads)
     layer = SparseDecodeLayer(cfg, dev, sinks=sinks)
     b, d = cfg.batch, cfg.dim
-    layer.fill_window(torch.randn(b, cfg.window, d, generator=gen, device=dev).bfloat16(), ctx - 2)
-    layer.append_groups(0, torch.randn(b, cfg.max_groups, d, generator=gen, device=dev).bfloat16(),
-                        torch.randn(b, cfg.max_groups, cfg.index_dim, generator=gen, device=dev).bfloat16())
+    layer.fill_window(rnd(b, cfg.window, d).bfloat16(), ctx - 2)
+    # groups in chunks (bounds the staging buffers of the larger configs)
+    step = max(1, (1 << 27) // (b * d))
+    for g0 in range(0, cfg.max_groups, step):
+        n = min(step, cfg.max_groups - g0)
+        layer.append_groups(g0, rnd(b, n, d).bfloat16(), rnd(b, n, cfg.index_dim).bfloat16())
+    if cfg.coarse_ratio:
+        layer.fill_coarse(rnd(b, cfg.coarse_groups, d).bfloat16())
     layer.set_positions(ctx - 1)
-    q = torch.randn(b, cfg.heads, d, generator=gen, device=dev).bfloat16()
-    kv = torch.randn(b, d, generator=gen, device=dev).bfloat16()
-    q_idx = torch.randn(b, cfg.index_heads, cfg.index_dim, generator=gen, device=dev).bfloat16()
-    w = torch.randn(b, cfg.index_heads, generator=gen, device=dev) * cfg.index_heads ** -0.5
+    q = rnd(b, cfg.heads, d).bfloat16()
+    kv = rnd(b, d).bfloat16()
+    q_idx = rnd(b, cfg.index_heads, cfg.index_dim).bfloat16()
+    w = rnd(b, cfg.index_heads) * cfg.index_heads ** -0.5
     return layer, (q, kv, q_idx, w), sinks
 
 
@@ -108,32 +139,33 @@ def capture_layers(torch, layers, inputs):
     return g, statics
 
 
-def stage_times(torch, layers, inputs, iters):
-    """Average duration of each kernel of the step alone: a HIP graph of back-to-back
-    launches of that kernel cycling through the layers (consecutive launches read different
-    caches, as in the decode graph), replayed and timed with HIP events on the stream the
-    kernels run on.  Inside a graph the launches follow each other with no host gap, so the
-    figure is the kernel's own duration."""
-    per_layer = [stage_fns(torch, layer, inp) for layer, inp in zip(layers, inputs)]
-    nl = len(per_layer)
-    reps = max(1, (32 + nl - 1) // nl)  # at least 32 launches per replay (amortizes the replay launch)
-    replays = max(1, iters // (reps * nl))
-    out = {}
-    for name in per_layer[0]:
-        fns = [d[name] for d in per_layer]
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
+def graph_time(torch, fns, iters):
+    """Average duration of one launch among `fns` (called in turn): a HIP graph of at least
+    32 back-to-back launches, replayed and timed with HIP events on the stream the kernels
+    run on.  Inside a graph the launches follow each other with no host gap, so the figure
+    is the kernels' own duration."""
+    n = len(fns)
+    reps = max(1, (32 + n - 1) // n)
+    replays = max(1, iters // (reps * n))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for f in fns:
+            f()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
             for f in fns:
                 f()
-        torch.cuda.current_stream().wait_stream(side)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for _ in range(reps):
-                for f in fns:
-                    f()
-        out[name] = time_launches(torch, g.replay, replays) / (reps * nl)
-    return out
+    return time_launches(torch, g.replay, replays) / (reps * n)
+
+
+def stage_times(torch, layers, inputs, iters):
+    """Average duration of each kernel of the step alone, launch after launch cycling
+    through the layers (consecutive launches read different caches, as in the decode graph)."""
+    per_layer = [stage_fns(torch, layer, inp) for layer, inp in zip(layers, inputs)]
+    return {name: graph_time(torch, [d[name] for d in per_layer], iters) for name in per_layer[0]}
 
 
 def stage_fns(torch, layer, inputs):
@@ -144,58 +176,83 @@ def stage_fns(torch, layer, inputs):
     q, kv, q_idx, w = inputs
     ws = layer.workspace
     st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
-
-    def indexer_decode():
-        # window append + indexer-query quantization + FP8 scores: the step's first launch
-        _lib.call("mzk_indexer_decode_fp8", q_idx.data_ptr(), w.data_ptr(), layer.k_codes.data_ptr(),
-                  layer.k_scales.data_ptr(), b, cfg.index_heads, cfg.index_dim, cfg.max_groups, cfg.max_groups,
-                  layer.positions.data_ptr(), cfg.ratio, layer.scores.data_ptr(), cfg.max_groups, None, None,
-                  kv.data_ptr(), cfg.nope, cfg.rope, layer.win.data_ptr(), cfg.window, cfg.window, st())
+    fns = {}
+    if cfg.index_format == "fp8":
+        def indexer_decode():
+            # window append + indexer-query quantization + FP8 scores: the step's first launch
+            _lib.call("mzk_indexer_decode_fp8", q_idx.data_ptr(), w.data_ptr(), layer.k_codes.data_ptr(),
+                      layer.k_scales.data_ptr(), b, cfg.index_heads, cfg.index_dim, cfg.max_groups, cfg.max_groups,
+                      layer.positions.data_ptr(), cfg.ratio, layer.scores.data_ptr(), cfg.max_groups, None, None,
+                      kv.data_ptr(), cfg.nope, cfg.rope, layer.win.data_ptr(), cfg.window, cfg.window, st())
+        fns["indexer_decode_fp8"] = indexer_decode
+    else:
+        def prologue():
+            # window append + indexer-query MXFP4 quantization (one launch)
+            _lib.call("mzk_decode_prologue", kv.data_ptr(), _lib.dtype_code(kv.dtype), b, cfg.nope, cfg.rope,
+                      layer.positions.data_ptr(), layer.win.data_ptr(), cfg.window, cfg.window, q_idx.data_ptr(),
+                      _lib.dtype_code(q_idx.dtype), b * cfg.index_heads, cfg.index_dim, 1, layer.q_codes.data_ptr(),
+                      None, layer.q_e8m0.data_ptr(), st())
+        fns["decode_prologue"] = prologue
+        fns["indexer_mxfp4"] = lambda: indexer.scores_mxfp4(
+            layer.q_codes, layer.q_e8m0, w.view(b, 1, -1), layer.k_packed, layer.k_e8m0, compress_ratio=cfg.ratio,
+            positions=layer.positions.view(b, 1), out=layer.scores)
+    fns["topk"] = lambda: indexer.topk(layer.scores.view(b, cfg.max_groups), cfg.topk, out=layer.idx,
+                                       workspace=layer.topk_ws)
+    coarse = layer.coarse
 
     def attn():
         # the split-KV attention kernel alone: with no `out` the entry point writes the
         # split partials into the workspace and launches nothing else
         _lib.call("mzk_sparse_mqa", q.data_ptr(), b, 1, cfg.heads, cfg.dim, 1, cfg.nope, layer.positions.data_ptr(),
-                  layer.win.data_ptr(), cfg.window, cfg.window, cfg.window, None, 0, 0, 1, layer.main.data_ptr(),
-                  cfg.max_groups, cfg.max_groups, layer.idx.data_ptr(), cfg.topk, cfg.topk,
-                  layer.sinks.data_ptr(), cfg.nsplit, ws.data_ptr(), ws.numel() * ws.element_size(), None, None, st())
-
-    def combine():
-        _lib.call("mzk_sparse_mqa_combine", ws.data_ptr(), b, 1, cfg.heads, cfg.dim, cfg.nsplit,
-                  layer.sinks.data_ptr(), layer.out.data_ptr(), layer.lse.data_ptr(), st())
-
-    return {
-        "indexer_decode_fp8": indexer_decode,
-        "topk": lambda: indexer.topk(layer.scores.view(b, cfg.max_groups), cfg.topk, out=layer.idx),
-        "sparse_mqa": attn,
-        "sparse_mqa_combine": combine,
-    }
+                  layer.win.data_ptr(), cfg.window, cfg.window, cfg.window,
+                  None if coarse is None else coarse.data_ptr(), cfg.coarse_groups, cfg.coarse_groups,
+                  max(cfg.coarse_ratio, 1), layer.main.data_ptr(), cfg.max_groups, cfg.max_groups,
+                  layer.idx.data_ptr(), cfg.topk, cfg.topk, layer.sinks.data_ptr(), cfg.nsplit, ws.data_ptr(),
+                  ws.numel() * ws.element_size(), None, None, st())
+    fns["sparse_mqa"] = attn
+    fns["sparse_mqa_combine"] = lambda: _lib.call(
+        "mzk_sparse_mqa_combine", ws.data_ptr(), b, 1, cfg.heads, cfg.dim, cfg.nsplit, layer.sinks.data_ptr(),
+        layer.out.data_ptr(), layer.lse.data_ptr(), st())
+    return fns
 
 
-def cpu_baseline(torch, layer, inputs, budget_s):
-    """The CPU oracle's decode step (indexer scores -> top-k -> attention) in fp32 on the
-    dequantized caches, all 32 rows, on this host's cores; median of repeated steps."""
+def cpu_baseline(torch, layer, inputs, budget_s, rows=None):
+    """The CPU oracle's decode step (indexer scores -> top-k -> attention over window
+    [+ coarse] + selected entries) in fp32 on the dequantized caches, for `rows` (default
+    all) of the batch, on this host's cores; median of repeated steps."""
     from mzoo_amd import quant
     from oracle import attention as OA
     from oracle import quant as OQ
     cfg = layer.cfg
-    q, kv, q_idx, w = (t.float().cpu() for t in inputs)
-    win = quant.unpack_latent_fp8_b128(layer.win, dtype=torch.float32).cpu()
-    main = quant.unpack_latent_fp8_b128(layer.main, dtype=torch.float32).cpu()
-    kd = (layer.k_codes.cpu().view(torch.float8_e4m3fn).float() * layer.k_scales.cpu().unsqueeze(-1))
+    rows = list(range(cfg.batch)) if rows is None else rows
+    q, kv, q_idx, w = (t.float().cpu()[rows] for t in inputs)
+    win = quant.unpack_latent_fp8_b128(layer.win[rows], dtype=torch.float32).cpu()
+    main = quant.unpack_latent_fp8_b128(layer.main[rows], dtype=torch.float32).cpu()
+    coarse = None
+    if layer.coarse is not None:
+        coarse = quant.unpack_latent_fp8_b128(layer.coarse[rows], dtype=torch.float32).cpu()
+    if cfg.index_format == "fp8":
+        kd = layer.k_codes[rows].cpu().view(torch.float8_e4m3fn).float() * layer.k_scales[rows].cpu().unsqueeze(-1)
+    else:
+        kd = quant.dequant_mxfp4(layer.k_packed[rows], layer.k_e8m0[rows]).cpu()
     sinks = layer.sinks.cpu()
     pos = int(layer.positions[0])
-    positions = torch.full((cfg.batch, 1), pos, dtype=torch.int64)
+    positions = torch.full((len(rows), 1), pos, dtype=torch.int64)
+    nc = 0 if coarse is None else min(cfg.coarse_groups, (pos + 1) // cfg.coarse_ratio)
     threads = torch.get_num_threads()
 
     def step():
-        qd = torch.from_numpy(OQ.fake_quant_fp8_block(q_idx.numpy(), cfg.index_dim))
+        if cfg.index_format == "fp8":
+            qd = torch.from_numpy(OQ.fake_quant_fp8_block(q_idx.numpy(), cfg.index_dim))
+        else:
+            qd = torch.from_numpy(OQ.fake_quant_fp4_block(q_idx.numpy(), 32))
         sc = OA.indexer_scores(qd.unsqueeze(1), kd, w.unsqueeze(1), cfg.ratio, positions)
         idx = torch.from_numpy(OA.topk_indices(sc[:, 0], cfg.topk))
         toks = torch.arange(pos - cfg.window + 1, pos + 1) % cfg.window
-        for r in range(cfg.batch):
-            ents = torch.cat([win[r, toks], main[r, idx[r][idx[r] >= 0]]])
-            OA.attend_entries(q[r], ents, sinks)
+        for i in range(len(rows)):
+            parts = [win[i, toks]] + ([coarse[i, :nc]] if coarse is not None else [])
+            ents = torch.cat(parts + [main[i, idx[i][idx[i] >= 0]]])
+            OA.attend_entries(q[i], ents, sinks)
 
     times = []
     t_start = time.perf_counter()
@@ -205,40 +262,38 @@ def cpu_baseline(torch, layer, inputs, budget_s):
         times.append(time.perf_counter() - t0)
     times.sort()
     med = times[len(times) // 2]
-    return {"value": cfg.batch / med, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"full config-2 decode step (32 rows: FP8 indexer over 8192 keys, top-2048, "
-                      f"attention over 2176 entries x 128 heads), fp32 torch on dequantized caches, "
-                      f"median of {len(times)} steps"}
+    entries = cfg.window + nc + cfg.topk
+    return {"value": len(rows) / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"decode step of {len(rows)} of {cfg.batch} rows ({cfg.index_format} indexer over "
+                      f"{cfg.max_groups} keys, top-{cfg.topk}, attention over {entries} entries x {cfg.heads} heads), "
+                      f"fp32 torch on dequantized caches, median of {len(times)} steps"}
 
 
-def traffic_from_profiles(kernel: str):
+def traffic_from_profiles(kernel: str, config: int):
     """HBM bytes per launch of `kernel` from the committed PMC summary, if one exists."""
-    f = ROOT / "profiles" / "decode_step_c2_hbm_traffic.md"
+    f = ROOT / "profiles" / f"decode_step_c{config}_hbm_traffic.md"
     if not f.exists():
         return None
     m = re.search(rf"{kernel}\s+traffic_bytes_per_launch\s*=\s*([0-9.eE+]+)", f.read_text())
     return float(m.group(1)) if m else None
 
 
-def main():
-    args = parse()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU only; multi-GPU runs are not part of it "
-              f"(got --gpus {args.gpus})", file=sys.stderr)
-        sys.exit(2)
-    import torch
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    if args.copy_mib:
-        src = torch.ones(args.copy_mib << 18, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4}))
-        return
+def roofline(kind, flops, nbytes, t_us, peak_tflops=BF16_PEAK_TFLOPS):
+    """The binding roof of one kernel: MFMA if its ideal compute time exceeds its ideal
+    HBM time (or kind == "mfma"), else HBM; achieved = algorithmic work / measured duration."""
+    t = t_us * 1e-6
+    if kind == "mfma" or (kind is None and flops / (peak_tflops * 1e12) > nbytes / (HBM_PEAK_GBS * 1e9)):
+        r = {"bound": "mfma", "achieved": flops / t / 1e12, "peak": peak_tflops, "unit": "TFLOP/s"}
+    else:
+        r = {"bound": "hbm", "achieved": nbytes / t / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s"}
+    r["frac"] = r["achieved"] / r["peak"]
+    return r
+
+
+def run_decode(torch, dev, args):
+    c = DECODE[args.config]
     nl = max(1, args.layers)
-    built = [build_layer(torch, dev, args.nsplit, seed=1 + i) for i in range(nl)]
+    built = [build_layer(torch, dev, args.nsplit, seed=c["seed"] + i, config=args.config) for i in range(nl)]
     layers = [b_[0] for b_ in built]
     inputs_all = [b_[1] for b_ in built]
     layer, inputs = layers[0], inputs_all[0]
@@ -258,37 +313,33 @@ def main():
     stages = stage_times(torch, layers, inputs_all, args.stage_iters or max(args.steps, 50))
     # algorithmic work per launch
     rows = cfg.batch
-    entries = cfg.window + cfg.topk
+    pos = c["ctx"] - 1
+    nc = min(cfg.coarse_groups, (pos + 1) // cfg.coarse_ratio) if cfg.coarse_ratio else 0
+    entries = cfg.window + nc + cfg.topk
     attn_bytes = rows * (entries * ENTRY_BYTES + QO_BYTES)
     attn_flops = rows * 4.0 * cfg.dim * cfg.heads * entries
-    idx_bytes = rows * cfg.max_groups * IDX_KEY_BYTES
+    idx_bytes = rows * cfg.max_groups * KEY_BYTES[cfg.index_format]
     idx_flops = rows * 2.0 * cfg.index_heads * cfg.index_dim * cfg.max_groups
-    dominant = max(("sparse_mqa", "indexer_decode_fp8", "topk"), key=lambda k: stages[k])
+    idx_stage = "indexer_decode_fp8" if cfg.index_format == "fp8" else "indexer_mxfp4"
+    dominant = max(("sparse_mqa", idx_stage, "topk"), key=lambda k: stages[k])
     if dominant == "sparse_mqa":
-        t = stages["sparse_mqa"] * 1e-6
-        mfma_bound = attn_flops / (BF16_PEAK_TFLOPS * 1e12) > attn_bytes / (HBM_PEAK_GBS * 1e9)
-        if mfma_bound:
-            roof = {"bound": "mfma", "achieved": attn_flops / t / 1e12, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s"}
-        else:
-            roof = {"bound": "hbm", "achieved": attn_bytes / t / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s"}
-    elif dominant == "indexer_decode_fp8":
-        t = stages[dominant] * 1e-6
-        roof = {"bound": "hbm", "achieved": idx_bytes / t / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s"}
+        roof = roofline(None, attn_flops, attn_bytes, stages[dominant])
+    elif dominant == idx_stage:
+        roof = roofline("hbm", idx_flops, idx_bytes, stages[dominant])
     else:
-        t = stages[dominant] * 1e-6
-        sb = rows * cfg.max_groups * 4 + rows * cfg.topk * 4
-        roof = {"bound": "hbm", "achieved": sb / t / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s"}
-    roof["frac"] = roof["achieved"] / roof["peak"]
-    roof["traffic"] = traffic_from_profiles(dominant)
+        roof = roofline("hbm", 0.0, rows * cfg.max_groups * 4 + rows * cfg.topk * 4, stages[dominant])
+    roof["traffic"] = traffic_from_profiles(dominant, args.config)
     roof["kernel"] = dominant
     roof["kernel_us"] = stages[dominant]
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(torch, layer, inputs, args.cpu_seconds)
+        # at most 2^18 (row, key) pairs of indexer work on the CPU: all 32 rows of config 2
+        cpu_rows = None if rows * cfg.max_groups <= (1 << 18) else list(range(max(1, (1 << 18) // cfg.max_groups)))
+        cpu = cpu_baseline(torch, layer, inputs, args.cpu_seconds, rows=cpu_rows)
 
-    out = {
-        "metric": "decode tokens/s/GPU at 32k ctx (sparse MQA + indexer); % HBM/MFMA roofline",
+    return {
+        "metric": METRIC,
         "value": tokens_per_s,
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -299,12 +350,11 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": f"synthetic (seeds 1..{nl}, one per layer), caches resident in HBM",
-        "config": {"workload": "config2: decode B=32 ctx=32768, 128 heads x (512+64) FP8-b128 latent cache, "
-                               "FP8 indexer 64x128 over 8192 groups (ratio 4), top-2048, window 128, sink",
-                   "batch": cfg.batch, "context": 32768, "heads": cfg.heads, "latent": "512+64",
-                   "index": "64x128 fp8", "topk": cfg.topk, "window": cfg.window, "nsplit": cfg.nsplit,
-                   "graph_layers": nl, "step": "per attention layer, inside a graph replay of graph_layers layers"},
+        "data": f"synthetic (seeds {c['seed']}..{c['seed'] + nl - 1}, one per layer), caches resident in HBM",
+        "config": {"workload": c["text"], "batch": cfg.batch, "context": c["ctx"], "heads": cfg.heads,
+                   "latent": "512+64", "index": f"64x128 {cfg.index_format}", "topk": cfg.topk,
+                   "window": cfg.window, "coarse": nc, "nsplit": cfg.nsplit, "graph_layers": nl,
+                   "step": "per attention layer, inside a graph replay of graph_layers layers"},
         "roofline": roof,
         "cpu_baseline": cpu,
         "stages_us": stages,
@@ -314,6 +364,154 @@ def main():
             "frac_hbm": (attn_bytes + idx_bytes) / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9),
         },
     }
+
+
+def run_prefill(torch, dev, args):
+    """causal prefill B=1, S=8192, 128 heads over 512+64 (bf16 latent),
+    FP8 indexer 64x128 over 2048 groups (ratio 4), top-2048, window 128, sink.  One step =
+    indexer-query quantization -> FP8 scores -> top-k -> sparse MQA over all query rows."""
+    from mzoo_amd import csa2_attn, indexer, quant
+    b, s, h, d, g, k, win, ratio, hi, di = 1, 8192, 128, 576, 2048, 2048, 128, 4, 64, 128
+    gen = torch.Generator(device=dev).manual_seed(3)
+    rnd = lambda *shape: torch.randn(*shape, generator=gen, device=dev)  # noqa: E731
+    q = rnd(b, s, h, d).bfloat16()
+    kv = rnd(b, s, 1, d).bfloat16()
+    main = rnd(b, g, 1, d).bfloat16()
+    q_idx = rnd(b, s, hi, di).bfloat16()
+    k_idx = rnd(b, g, di).bfloat16()
+    w = rnd(b, s, hi) * hi ** -0.5
+    sinks = rnd(h)
+    kc, ks = quant.quant_fp8_block(k_idx, 128)  # the published key cache
+    ks = ks[..., 0].contiguous()
+    scores = torch.empty(b, s, g, dtype=torch.float32, device=dev)
+    idx = torch.empty(b, s, k, dtype=torch.int32, device=dev)
+    state = {}
+
+    def quant_q():
+        state["q"] = quant.quant_fp8_block(q_idx, 128)
+
+    def scores_fp8():
+        qc, qs = state["q"]
+        indexer.scores_fp8(qc, qs[..., 0], w, kc, ks, compress_ratio=ratio, out=scores)
+
+    def topk():
+        indexer.topk(scores, k, out=idx)
+
+    def attn():
+        state["o"] = csa2_attn.fwd(q, kv, main, idx, window=win, compress_ratio=ratio, sinks=sinks)
+
+    def step():
+        quant_q()
+        scores_fp8()
+        topk()
+        attn()
+
+    steps = min(args.steps, 20)
+    warm = min(args.warmup, 3) + 1
+    for _ in range(warm):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    stages = {"quant_q": time_launches(torch, quant_q, 5), "indexer_fp8": time_launches(torch, scores_fp8, 5),
+              "topk": time_launches(torch, topk, 5), "sparse_mqa": time_launches(torch, attn, 5)}
+    t = torch.arange(s, dtype=torch.float64)
+    pairs = float((torch.clamp((t + 1) // ratio, max=k) + torch.clamp(t + 1, max=win)).sum())
+    attn_flops = 4.0 * d * h * pairs
+    attn_bytes = 2.0 * s * h * d * 2 + (s * d + g * d) * 2 + s * k * 4
+    vis = float(torch.clamp((t + 1) // ratio, max=g).sum())
+    idx_flops = 2.0 * hi * di * vis
+    dominant = max(("sparse_mqa", "indexer_fp8", "topk"), key=lambda x: stages[x])
+    if dominant == "sparse_mqa":
+        roof = roofline("mfma", attn_flops, attn_bytes, stages[dominant])
+    elif dominant == "indexer_fp8":
+        roof = roofline("mfma", idx_flops, s * hi * di + g * 132, stages[dominant], FP8_PEAK_TFLOPS)
+    else:
+        roof = roofline("hbm", 0.0, s * g * 4 + s * k * 4, stages[dominant])
+    roof["traffic"] = None
+    roof["kernel"] = dominant
+    roof["kernel_us"] = stages[dominant]
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = prefill_cpu_baseline(torch, q, kv, main, q_idx, k_idx, w, sinks, win, ratio, k, args.cpu_seconds)
+    return {
+        "metric": METRIC,
+        "value": s / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warm,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seed 3), resident in HBM",
+        "config": {"workload": "config3: causal prefill B=1 S=8192, 128 heads x (512+64) bf16 latent, FP8 indexer "
+                               "64x128 over 2048 groups (ratio 4), top-2048, window 128, sink",
+                   "batch": b, "seq_len": s, "heads": h, "topk": k, "window": win,
+                   "step": "whole prefill (query quantization, FP8 scores, top-k, sparse MQA)"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "stages_us": stages,
+    }
+
+
+def prefill_cpu_baseline(torch, q, kv, main, q_idx, k_idx, w, sinks, win, ratio, k, budget_s):
+    """The oracle's prefill on 16 query rows spread evenly over the sequence."""
+    from oracle import attention as OA
+    from oracle import quant as OQ
+    s = q.shape[1]
+    rows = list(range(s - 1, -1, -(s // 16)))[:16]
+    qd = torch.from_numpy(OQ.fake_quant_fp8_block(q_idx[:, rows].float().cpu().numpy(), 128))
+    kd = torch.from_numpy(OQ.fake_quant_fp8_block(k_idx.float().cpu().numpy(), 128))
+    wr = w[:, rows].cpu()
+    qr = q[0, rows].float().cpu()
+    kvc, mainc, sk = kv[0, :, 0].float().cpu(), main[0, :, 0].float().cpu(), sinks.cpu()
+    pos = torch.tensor(rows, dtype=torch.int64).view(1, -1)
+
+    def step():
+        sc = OA.indexer_scores(qd, kd, wr, ratio, pos)
+        idx = OA.topk_indices(sc[0], k)
+        for i, t in enumerate(rows):
+            sel = torch.from_numpy(idx[i][idx[i] >= 0])
+            OA.attend_entries(qr[i], torch.cat([kvc[max(0, t - win + 1):t + 1], mainc[sel]]), sk)
+
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 and (time.perf_counter() - t_start < budget_s or len(times) < 2):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": len(rows) / med, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{len(rows)} query rows of the 8192-row prefill (FP8 indexer over 2048 keys, top-2048, "
+                      f"attention over window + selected entries x 128 heads), fp32 torch, median of {len(times)} runs"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only; multi-GPU runs are not part of it "
+              f"(got --gpus {args.gpus})", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if args.copy_mib:
+        src = torch.ones(args.copy_mib << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4}))
+        return
+    out = run_prefill(torch, dev, args) if args.config == 3 else run_decode(torch, dev, args)
     print(json.dumps(out))
 
 

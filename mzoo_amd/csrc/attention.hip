@@ -963,7 +963,7 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
 // Merge the split partials with the sink: split s contributes its normalized output O_s
 // with weight l_s exp2(m_s - M) / L, where M = max(m_s, sink) and
 // L = sum_s l_s exp2(m_s - M) + exp2(sink - M).  One thread per 8 channels of a (row, head).
-constexpr int kCombineRegSplits = 8;  // splits merged from registers in one round trip
+constexpr int kCombineRegSplits = 8;  // splits merged per memory round trip
 
 template <int D>
 __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict__ part_o,
@@ -980,47 +980,47 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
   const float* ml = part_ml + (row * nsplit * H + head) * 2;  // split s at + 2 s H
   const uint16_t* po = part_o + (row * nsplit * H + head) * static_cast<int64_t>(D) + 8 * c;
   const float sk = sinks ? sinks[head] * kLog2e : -__builtin_huge_valf();
+  // Splits are merged kCombineRegSplits at a time: a chunk's (m, l) pairs and output pieces
+  // are all requested before any is used (one memory round trip per chunk), then folded
+  // into a running (M, L, acc) -- the sink first, as a split of weight 1 at sk.  A split
+  // that saw no entry (l = 0) contributes nothing (its output is zeros, its m may be -inf).
+  // With at most kCombineRegSplits splits this is a single pass with the global maximum.
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float M = sk, L;
-  // accumulate splits with weight l_s exp2(m_s - M); a split that saw no entry (l = 0)
-  // contributes nothing (its output is zeros, its m may be -inf)
-  auto add_split = [&](const float2 ms, const uint4 v) {
-    const float wgt = ms.y > 0.0f ? ms.y * exp2f(ms.x - M) : 0.0f;
-    L = L + wgt;
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      acc[2 * i] = acc[2 * i] + bf16_to_f32(static_cast<uint16_t>(w[i] & 0xffffu)) * wgt;
-      acc[2 * i + 1] = acc[2 * i + 1] + bf16_to_f32(static_cast<uint16_t>(w[i] >> 16)) * wgt;
-    }
-  };
-  if (nsplit <= kCombineRegSplits) {
-    // every split's (m, l) and output chunk requested at once: one memory round trip
+  float M = sk, L = sinks ? 1.0f : 0.0f;
+  for (int s0 = 0; s0 < nsplit; s0 += kCombineRegSplits) {
     float2 ms[kCombineRegSplits];
     uint4 v[kCombineRegSplits];
 #pragma unroll
-    for (int s = 0; s < kCombineRegSplits; ++s) {
-      if (s < nsplit) {
-        ms[s] = *reinterpret_cast<const float2*>(ml + 2 * s * H);
-        v[s] = *reinterpret_cast<const uint4*>(po + static_cast<int64_t>(s) * H * D);
+    for (int j = 0; j < kCombineRegSplits; ++j) {
+      if (s0 + j < nsplit) {
+        ms[j] = *reinterpret_cast<const float2*>(ml + 2 * (s0 + j) * H);
+        v[j] = *reinterpret_cast<const uint4*>(po + static_cast<int64_t>(s0 + j) * H * D);
       }
     }
+    float M_new = M;
 #pragma unroll
-    for (int s = 0; s < kCombineRegSplits; ++s)
-      if (s < nsplit && ms[s].y > 0.0f) M = fmaxf(M, ms[s].x);
-    L = sinks ? exp2f(sk - M) : 0.0f;
+    for (int j = 0; j < kCombineRegSplits; ++j)
+      if (s0 + j < nsplit && ms[j].y > 0.0f) M_new = fmaxf(M_new, ms[j].x);
+    if (M_new != M) {  // rescale what is merged so far (nothing yet when M = -inf)
+      const float a = M == -__builtin_huge_valf() ? 0.0f : exp2f(M - M_new);
+      L = L * a;
 #pragma unroll
-    for (int s = 0; s < kCombineRegSplits; ++s)
-      if (s < nsplit) add_split(ms[s], v[s]);
-  } else {
-    for (int s = 0; s < nsplit; ++s) {
-      const float2 m = *reinterpret_cast<const float2*>(ml + 2 * s * H);
-      if (m.y > 0.0f) M = fmaxf(M, m.x);
+      for (int i = 0; i < 8; ++i) acc[i] = acc[i] * a;
+      M = M_new;
     }
-    L = sinks ? exp2f(sk - M) : 0.0f;
-    for (int s = 0; s < nsplit; ++s)
-      add_split(*reinterpret_cast<const float2*>(ml + 2 * s * H),
-                *reinterpret_cast<const uint4*>(po + static_cast<int64_t>(s) * H * D));
+#pragma unroll
+    for (int j = 0; j < kCombineRegSplits; ++j) {
+      if (s0 + j < nsplit) {
+        const float wgt = ms[j].y > 0.0f ? ms[j].y * exp2f(ms[j].x - M) : 0.0f;
+        L = L + wgt;
+        const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[2 * i] = acc[2 * i] + bf16_to_f32(static_cast<uint16_t>(w[i] & 0xffffu)) * wgt;
+          acc[2 * i + 1] = acc[2 * i + 1] + bf16_to_f32(static_cast<uint16_t>(w[i] >> 16)) * wgt;
+        }
+      }
+    }
   }
   const float inv = 1.0f / L;
   *reinterpret_cast<uint4*>(out + rh * static_cast<int64_t>(D) + 8 * c) =

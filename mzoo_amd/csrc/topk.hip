@@ -17,7 +17,8 @@
 //   3. compaction in index order: take key > T, and the first `need_eq` entries with
 //      key == T; two block-wide exclusive scans per 4096-entry chunk give the ranks.
 // Rows up to 32 * 1024 keys keep them in registers (topk_rows_reg_kernel); longer rows
-// re-read the row every pass (L2-resident after the first pass).
+// re-read the row every pass (L2-resident after the first pass).  mzk_topk_rows_ws splits
+// rows of 8193 .. 64 x 8192 keys over chunk workgroups (three launches, see below).
 #include "common.h"
 
 namespace mzk {
@@ -423,6 +424,368 @@ __global__ void __launch_bounds__(NT) topk_rows_reg_kernel(const float* __restri
   for (int i = written + tid; i < k; i += NT) dst[i] = -1;
 }
 
+
+// ---- long rows, few of them: the row split over chunk workgroups ---------------------
+//
+// A row of G > kMultiMinG keys is cut into chunks of kChunk keys (thread t of a chunk
+// holds keys 8t .. 8t+7 in registers).  Three launches:
+//   A  one workgroup per (chunk, row): histogram of the top kBinBits of every finite key;
+//   B  one workgroup per row: merge the chunk histograms, find the bin b1 holding the k-th
+//      largest key; the keys of b1 (few, for any spread of scores) are gathered into LDS
+//      and a 3 x 7-bit radix select over their low 21 bits gives the threshold T and the
+//      number need_eq of keys equal to T to take (lowest indices first).  If b1 holds more
+//      than kCandCap keys the same passes stream the row from global memory instead.
+//      Then per chunk: #taken = #(key > T) + its share of the need_eq equal keys, and the
+//      exclusive prefix over chunks gives each chunk's first output slot;
+//   C  one workgroup per (chunk, row): the index-ordered compaction of the register kernel
+//      with the chunk's offset and share of equal keys.
+// Same contract and results as the single-workgroup kernels.
+constexpr int kChunk = 8 * kThreads;           // keys per chunk workgroup
+constexpr int kBinBits = 11;
+constexpr int kBins = 1 << kBinBits;           // 2048 first-level bins
+constexpr int kLowBits = 32 - kBinBits;        // 21 bits resolved in B
+constexpr int kCandCap = 12288;                // keys of bin b1 held in LDS
+constexpr int kMaxChunks = 64;                 // rows up to 64 x 8192 keys
+constexpr int64_t kMultiMinG = 8 * kThreads;   // shorter rows stay on one workgroup
+
+struct ChunkInfo {
+  int offset;   // first output slot of the chunk
+  int eq_take;  // keys equal to T the chunk takes (its lowest-index ones)
+};
+
+// Workspace: hist [rows][nch][kBins] int32 | info [rows][nch] ChunkInfo | T [rows] uint32
+__host__ __device__ inline int64_t multi_hist_bytes(int64_t rows, int64_t nch) { return rows * nch * kBins * 4; }
+__host__ __device__ inline int64_t multi_info_bytes(int64_t rows, int64_t nch) { return rows * nch * 8; }
+__host__ inline int64_t multi_ws_bytes(int64_t rows, int64_t nch) {
+  return multi_hist_bytes(rows, nch) + multi_info_bytes(rows, nch) + rows * 4;
+}
+
+// The 8 keys of thread t of chunk c (0 beyond G: below -inf, never counted or taken).
+__device__ __forceinline__ void load_chunk_keys(const float* __restrict__ src, int G, int base, int t,
+                                                uint32_t (&key)[8]) {
+  const int i0 = base + 8 * t;
+  float x[8];
+  if ((reinterpret_cast<uintptr_t>(src) & 15) == 0 && i0 + 8 <= G) {
+    const float4 a = *reinterpret_cast<const float4*>(src + i0);
+    const float4 b = *reinterpret_cast<const float4*>(src + i0 + 4);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = (i0 + j < G) ? src[i0 + j] : 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) key[j] = (i0 + j < G) ? order_key(x[j]) : 0u;
+}
+
+__global__ void __launch_bounds__(kThreads) topk_chunk_hist_kernel(const float* __restrict__ scores,
+                                                                     int64_t row_stride, int G, int nch,
+                                                                     int* __restrict__ hist_out) {
+  constexpr int kSubA = 4;  // sub-counters per bin (lane % 4): equal digits spread over 4 addresses
+  __shared__ __align__(16) int hist[kBins * kSubA];
+  const int row = blockIdx.y, c = blockIdx.x;
+  const float* src = scores + static_cast<int64_t>(row) * row_stride;
+  const int tid = threadIdx.x;
+  uint32_t key[8];
+  load_chunk_keys(src, G, c * kChunk, tid, key);
+  int4* h4 = reinterpret_cast<int4*>(hist);
+  for (int i = tid; i < kBins * kSubA / 4; i += kThreads) h4[i] = int4{0, 0, 0, 0};
+  __syncthreads();
+  int* hs = hist + (tid & (kSubA - 1));
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (key[j] > kNegInfKey) atomicAdd(hs + (key[j] >> kLowBits) * kSubA, 1);
+  __syncthreads();
+  // bins 2t, 2t+1: sum their sub-counters, one 8-byte store per thread
+  const int4 a = h4[2 * tid], b = h4[2 * tid + 1];
+  int* dst = hist_out + (static_cast<int64_t>(row) * nch + c) * kBins;
+  *reinterpret_cast<int2*>(dst + 2 * tid) = int2{(a.x + a.y) + (a.z + a.w), (b.x + b.y) + (b.z + b.w)};
+}
+
+// Every key of the row, 8 per thread per chunk step (keys beyond G read as 0, which lies
+// in no bin a selection looks at); the loads of kScanBatch steps are issued together, one
+// memory round trip per batch (a batch inside an aligned row takes one workgroup-uniform
+// branch to its vector loads); f(key[8], index of key[0]) runs in wave-uniform control flow.
+constexpr int kScanBatch = 4;
+template <class F>
+__device__ __forceinline__ void for_row_keys(const float* __restrict__ src, int G, F&& f) {
+  const int tid = threadIdx.x;
+  const bool vec = (reinterpret_cast<uintptr_t>(src) & 15) == 0;
+  for (int base = 0; base < G; base += kScanBatch * kChunk) {
+    uint32_t key[kScanBatch][8];
+    if (vec && base + kScanBatch * kChunk <= G) {
+      float4 v[kScanBatch][2];
+#pragma unroll
+      for (int b = 0; b < kScanBatch; ++b) {
+        const float* p = src + base + b * kChunk + 8 * tid;
+        v[b][0] = *reinterpret_cast<const float4*>(p);
+        v[b][1] = *reinterpret_cast<const float4*>(p + 4);
+      }
+#pragma unroll
+      for (int b = 0; b < kScanBatch; ++b) {
+        const float x[8] = {v[b][0].x, v[b][0].y, v[b][0].z, v[b][0].w, v[b][1].x, v[b][1].y, v[b][1].z, v[b][1].w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) key[b][j] = order_key(x[j]);
+      }
+    } else {
+#pragma unroll
+      for (int b = 0; b < kScanBatch; ++b) load_chunk_keys(src, G, base + b * kChunk, tid, key[b]);
+    }
+#pragma unroll
+    for (int b = 0; b < kScanBatch; ++b)
+      if (base + b * kChunk < G) f(key[b], base + b * kChunk + 8 * tid);
+  }
+}
+
+__global__ void __launch_bounds__(kThreads) topk_select_kernel(const float* __restrict__ scores, int64_t row_stride,
+                                                                 int G, int k, int nch, const int* __restrict__ hist_in,
+                                                                 ChunkInfo* __restrict__ info_out,
+                                                                 uint32_t* __restrict__ t_out, int32_t* __restrict__ out,
+                                                                 int64_t out_stride) {
+  __shared__ uint32_t cand_key[kCandCap];
+  __shared__ int cand_idx[kCandCap];
+  __shared__ int hist7[128];
+  __shared__ int chunk_gt[kMaxChunks], chunk_eq[kMaxChunks];
+  __shared__ int wsum[kWaves];
+  __shared__ int sh_b1, sh_rem, sh_cnt, sh_ncand, sh_digit;
+
+  const int row = blockIdx.x;
+  const float* src = scores + static_cast<int64_t>(row) * row_stride;
+  const int* hrow = hist_in + static_cast<int64_t>(row) * nch * kBins;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  // 1. bin totals over the chunks (thread t: bins 2t, 2t+1; 16 chunks per round trip)
+  int t0 = 0, t1 = 0;
+  for (int c0 = 0; c0 < nch; c0 += 16) {
+    int2 v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      v[j] = c0 + j < nch ? *reinterpret_cast<const int2*>(hrow + static_cast<int64_t>(c0 + j) * kBins + 2 * tid)
+                          : int2{0, 0};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      t0 += v[j].x;
+      t1 += v[j].y;
+    }
+  }
+  if (tid < kMaxChunks) {
+    chunk_gt[tid] = 0;
+    chunk_eq[tid] = 0;
+  }
+  // inclusive prefix of the pair totals over threads (= over bins, ascending)
+  const int pair = t0 + t1;
+  int incl = wave_incl_scan_dpp(pair);
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  int total_fin = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    total_fin += wsum[w];
+    incl += w < wave ? wsum[w] : 0;
+  }
+
+  // 2. the bin b1 holding the k-th largest key: keys in bins above thread t's pair number
+  //    total - incl; exactly one (thread, bin) sees the k-th key
+  uint32_t T = kNegInfKey;
+  int need_eq = 0, b_lo = 0;  // chunks take every key in bins >= b_lo (plus b1's selection)
+  bool partial = false;
+  int b1 = 0;
+  if (total_fin > k) {
+    const int above_hi = total_fin - incl;  // keys in bins > 2t+1
+    const int above_lo = above_hi + t1;     // keys in bins > 2t
+    if (above_hi < k && k <= above_hi + t1) {
+      sh_b1 = 2 * tid + 1;
+      sh_rem = k - above_hi;
+      sh_cnt = t1;
+    } else if (above_lo < k && k <= above_lo + t0) {
+      sh_b1 = 2 * tid;
+      sh_rem = k - above_lo;
+      sh_cnt = t0;
+    }
+    __syncthreads();
+    b1 = sh_b1;
+    if (sh_rem == sh_cnt) {  // the bin is taken whole
+      T = (static_cast<uint32_t>(b1) << kLowBits) - 1u;  // b1 >= 4: finite keys sit in bins >= 4
+      b_lo = b1;
+    } else {
+      partial = true;
+      b_lo = b1 + 1;
+    }
+  }
+
+  if (partial) {
+    // 3. select among the keys of bin b1: LDS candidates if they fit, else stream the row
+    //    (b1 >= 4, so the 0 keys past the row end never match)
+    const bool in_lds = sh_cnt <= kCandCap;
+    if (tid == 0) sh_ncand = 0;
+    __syncthreads();
+    if (in_lds) {
+      // one LDS atomic per wave and step reserves the wave's slots
+      for_row_keys(src, G, [&](const uint32_t (&key)[8], int i0) {
+        int nm = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) nm += static_cast<int>(key[j] >> kLowBits) == b1;
+        const int incl = wave_incl_scan_dpp(nm);
+        int wb = 0;
+        if (lane == 63 && incl > 0) wb = atomicAdd(&sh_ncand, incl);
+        int slot = __builtin_amdgcn_readlane(wb, 63) + incl - nm;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (static_cast<int>(key[j] >> kLowBits) == b1) {
+            if (slot < kCandCap) {
+              cand_key[slot] = key[j];
+              cand_idx[slot] = i0 + j;
+            }
+            ++slot;
+          }
+        }
+      });
+      __syncthreads();
+    }
+    const int ncand = in_lds ? min(sh_ncand, kCandCap) : 0;
+    // f(key, index, active) over the keys of bin b1, in wave-uniform control flow
+    auto for_cands = [&](auto&& f) {
+      if (in_lds) {
+        for (int m0 = 0; m0 < ncand; m0 += kThreads) {
+          const int m = m0 + tid;
+          const bool a = m < ncand;
+          f(a ? cand_key[m] : 0u, a ? cand_idx[m] : 0, a);
+        }
+      } else {
+        for_row_keys(src, G, [&](const uint32_t (&key)[8], int i0) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) f(key[j], i0 + j, static_cast<int>(key[j] >> kLowBits) == b1);
+        });
+      }
+    };
+    uint32_t prefix = static_cast<uint32_t>(b1) << kLowBits, mask = ~((1u << kLowBits) - 1u);
+    int rem = sh_rem;
+    for (int shift = kLowBits - 7; shift >= 0; shift -= 7) {
+      if (tid < 128) hist7[tid] = 0;
+      __syncthreads();
+      for_cands([&](uint32_t key, int, bool a) { hist_add(hist7, (key >> shift) & 127u, a && (key & mask) == prefix); });
+      __syncthreads();
+      if (wave == 0) {
+        const int h0 = hist7[127 - 2 * lane], h1 = hist7[126 - 2 * lane];
+        const int hs = h0 + h1;
+        int above = wave_incl_scan_dpp(hs) - hs;
+        int d = -1, r = 0;
+        if (above < rem && rem <= above + h0) {
+          d = 127 - 2 * lane;
+          r = rem - above;
+        } else if (above + h0 < rem && rem <= above + hs) {
+          d = 126 - 2 * lane;
+          r = rem - above - h0;
+        }
+        const uint64_t m = __ballot(d >= 0);
+        const int srcl = m ? __builtin_ctzll(m) : 0;
+        if (lane == srcl) {
+          sh_digit = d < 0 ? 0 : d;
+          sh_rem = r;
+        }
+      }
+      __syncthreads();
+      prefix |= static_cast<uint32_t>(sh_digit) << shift;
+      mask |= 127u << shift;
+      rem = sh_rem;
+      __syncthreads();  // sh_digit / sh_rem read by every thread before the next pass
+    }
+    T = prefix;
+    need_eq = rem;
+    // keys of bin b1 above / equal to T, per chunk
+    for_cands([&](uint32_t key, int i, bool a) {
+      const uint32_t c = static_cast<uint32_t>(i / kChunk);
+      hist_add(chunk_gt, c, a && key > T);
+      hist_add(chunk_eq, c, a && key == T);
+    });
+  }
+
+  // 4. per chunk: keys in bins >= b_lo (wave w: chunks w, w + 16, ...)
+  for (int c = wave; c < nch; c += kWaves) {
+    const int* hc = hrow + static_cast<int64_t>(c) * kBins;
+    int v[kBins / 64];
+#pragma unroll
+    for (int r = 0; r < kBins / 64; ++r) v[r] = hc[64 * r + lane];
+    int n = 0;
+#pragma unroll
+    for (int r = 0; r < kBins / 64; ++r) n += 64 * r + lane >= b_lo ? v[r] : 0;
+    n += __shfl_xor(n, 1, 64);
+    n += __shfl_xor(n, 2, 64);
+    n += __shfl_xor(n, 4, 64);
+    n += __shfl_xor(n, 8, 64);
+    n += __shfl_xor(n, 16, 64);
+    n += __shfl_xor(n, 32, 64);
+    if (lane == 0) atomicAdd(&chunk_gt[c], n);
+  }
+  __syncthreads();
+  // 5. chunk offsets (index order): equal keys go to the lowest indices first
+  if (tid == 0) {
+    int off = 0, eq_left = need_eq;
+    for (int c = 0; c < nch; ++c) {
+      const int take = min(eq_left, chunk_eq[c]);
+      info_out[static_cast<int64_t>(row) * nch + c] = ChunkInfo{off, take};
+      off += chunk_gt[c] + take;
+      eq_left -= take;
+    }
+    t_out[row] = T;
+    sh_ncand = off;  // entries written by the chunks
+  }
+  __syncthreads();
+  int32_t* dst = out + static_cast<int64_t>(row) * out_stride;
+  for (int i = sh_ncand + tid; i < k; i += kThreads) dst[i] = -1;
+}
+
+__global__ void __launch_bounds__(kThreads) topk_chunk_write_kernel(const float* __restrict__ scores, int64_t row_stride,
+                                                                      int G, int k, int nch,
+                                                                      const ChunkInfo* __restrict__ info,
+                                                                      const uint32_t* __restrict__ t_in,
+                                                                      int32_t* __restrict__ out, int64_t out_stride) {
+  __shared__ __align__(16) int wsum[kWaves];
+  const int row = blockIdx.y, c = blockIdx.x;
+  const float* src = scores + static_cast<int64_t>(row) * row_stride;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t key[8];
+  load_chunk_keys(src, G, c * kChunk, tid, key);
+  const uint32_t T = t_in[row];
+  const ChunkInfo ci = info[static_cast<int64_t>(row) * nch + c];
+  int n_gt = 0, n_eq = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    n_gt += key[j] > T;
+    n_eq += (key[j] == T) && (T != kNegInfKey);
+  }
+  // packed exclusive scan over the chunk (both counts < 2^13 per chunk)
+  const int packed = (n_gt << 16) | n_eq;
+  const int incl = wave_incl_scan_dpp(packed);
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  int before = incl - packed;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) before += w < wave ? wsum[w] : 0;
+  int gt_before = before >> 16, eq_before = before & 0xffff;
+  int32_t* dst = out + static_cast<int64_t>(row) * out_stride;
+  const int i0 = c * kChunk + 8 * tid;
+  // slots stay below k by construction; the bound also holds if the scores were changed
+  // between the launches
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (key[j] > T) {
+      const int slot = ci.offset + gt_before + min(eq_before, ci.eq_take);
+      if (slot < k) dst[slot] = i0 + j;
+      ++gt_before;
+    } else if (key[j] == T && T != kNegInfKey) {
+      const int slot = ci.offset + gt_before + eq_before;
+      if (eq_before < ci.eq_take && slot < k) dst[slot] = i0 + j;
+      ++eq_before;
+    }
+  }
+}
+
+int topk_multi_chunks(int64_t rows, int64_t cols) {
+  if (cols <= kMultiMinG || cols > static_cast<int64_t>(kChunk) * kMaxChunks || rows > 65535) return 0;
+  return static_cast<int>((cols + kChunk - 1) / kChunk);
+}
+
 }  // namespace
 }  // namespace mzk
 
@@ -451,5 +814,40 @@ extern "C" int mzk_topk_rows(const float* scores, int64_t rows, int64_t cols, in
   else
     topk_rows_kernel<false><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
   MZK_LAUNCH_CHECK("topk_rows");
+  return MZK_OK;
+}
+
+extern "C" int mzk_topk_workspace_bytes(int64_t rows, int64_t cols, int64_t* bytes) {
+  MZK_CHECK_ARG(rows >= 0 && cols >= 0 && bytes != nullptr, "topk_workspace_bytes: bad arguments");
+  const int nch = topk_multi_chunks(rows, cols);
+  *bytes = nch ? multi_ws_bytes(rows, nch) : 0;
+  return MZK_OK;
+}
+
+extern "C" int mzk_topk_rows_ws(const float* scores, int64_t rows, int64_t cols, int64_t row_stride, int topk,
+                                int32_t* out, int64_t out_stride, void* workspace, int64_t workspace_bytes,
+                                void* stream) {
+  const int nch = topk_multi_chunks(rows, cols);
+  if (nch == 0 || rows == 0 || topk == 0)
+    return mzk_topk_rows(scores, rows, cols, row_stride, topk, out, out_stride, stream);
+  MZK_CHECK_ARG(topk > 0 && cols <= (int64_t(1) << 30) && topk <= (1 << 30), "topk_rows: bad sizes");
+  MZK_CHECK_ARG(row_stride >= cols && out_stride >= topk, "topk_rows: strides smaller than the row");
+  MZK_CHECK_ARG(out != nullptr && scores != nullptr, "topk_rows: null pointer");
+  const int64_t need = multi_ws_bytes(rows, nch);
+  MZK_CHECK_ARG(workspace != nullptr && workspace_bytes >= need && aligned16(workspace),
+                "topk_rows: rows of %lld keys need a 16-byte aligned workspace of %lld bytes", (long long)cols,
+                (long long)need);
+  hipStream_t s = as_stream(stream);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  int* hist = reinterpret_cast<int*>(ws);
+  ChunkInfo* info = reinterpret_cast<ChunkInfo*>(ws + multi_hist_bytes(rows, nch));
+  uint32_t* tv = reinterpret_cast<uint32_t*>(ws + multi_hist_bytes(rows, nch) + multi_info_bytes(rows, nch));
+  const int G = static_cast<int>(cols);
+  const dim3 grid(static_cast<unsigned>(nch), static_cast<unsigned>(rows));
+  topk_chunk_hist_kernel<<<grid, kThreads, 0, s>>>(scores, row_stride, G, nch, hist);
+  topk_select_kernel<<<static_cast<unsigned>(rows), kThreads, 0, s>>>(scores, row_stride, G, topk, nch, hist, info,
+                                                                       tv, out, out_stride);
+  topk_chunk_write_kernel<<<grid, kThreads, 0, s>>>(scores, row_stride, G, topk, nch, info, tv, out, out_stride);
+  MZK_LAUNCH_CHECK("topk_rows_ws");
   return MZK_OK;
 }

@@ -85,6 +85,8 @@ class SparseDecodeLayer:
         # per-step buffers (fixed addresses, so a captured graph can replay them)
         self.scores = torch.empty(b, 1, cfg.max_groups, dtype=torch.float32, device=self.device)
         self.idx = torch.empty(b, cfg.topk, dtype=torch.int32, device=self.device)
+        self.topk_ws = torch.empty(max(indexer.topk_workspace_bytes(b, cfg.max_groups), 16), dtype=torch.uint8,
+                                   device=self.device)
         self.out = torch.empty(b, cfg.heads, cfg.dim, dtype=torch.bfloat16, device=self.device)
         self.lse = torch.empty(b, cfg.heads, dtype=torch.float32, device=self.device)
         self.workspace = csa2_attn.new_workspace(b, cfg.heads, cfg.dim, cfg.nsplit, self.device)
@@ -158,7 +160,7 @@ class SparseDecodeLayer:
                       cfg.index_dim, 1, self.q_codes.data_ptr(), None, self.q_e8m0.data_ptr(), _lib.stream_of(qc))
             indexer.scores_mxfp4(self.q_codes, self.q_e8m0, w.view(b, 1, -1), self.k_packed, self.k_e8m0,
                                  compress_ratio=cfg.ratio, positions=pos, out=self.scores)
-        indexer.topk(self.scores.view(b, cfg.max_groups), cfg.topk, out=self.idx)
+        indexer.topk(self.scores.view(b, cfg.max_groups), cfg.topk, out=self.idx, workspace=self.topk_ws)
         csa2_attn.sparse_mqa_decode(q, self.positions, self.win, cfg.window, main_cache=self.main,
                                     groups=cfg.max_groups, indices=self.idx, dense_cache=self.coarse,
                                     dense_ratio=max(cfg.coarse_ratio, 1), sinks=self.sinks, nsplit=cfg.nsplit,

@@ -20,6 +20,8 @@ rule; omitted, query ``s`` sits at position ``s`` (a prefill from position 0).
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -32,9 +34,20 @@ def _positions(positions, b, s, device):
     return p
 
 
-def topk(scores: torch.Tensor, k: int, out: torch.Tensor | None = None) -> torch.Tensor:
+def topk_workspace_bytes(rows: int, g: int) -> int:
+    """Workspace bytes ``topk`` needs for ``rows`` rows of ``g`` scores (0: none): long rows
+    are split over several workgroups, which exchange partial counts through it."""
+    n = ctypes.c_int64(0)
+    _lib.call("mzk_topk_workspace_bytes", rows, g, ctypes.byref(n))
+    return n.value
+
+
+def topk(scores: torch.Tensor, k: int, out: torch.Tensor | None = None,
+         workspace: torch.Tensor | None = None) -> torch.Tensor:
     """scores fp32 [..., G] -> int32 [..., k]: the ``min(k, G)`` best columns (lower index
-    first among equal scores), never a ``-inf`` one, ascending, then ``-1``."""
+    first among equal scores), never a ``-inf`` one, ascending, then ``-1``.  Rows longer
+    than 8192 use a workspace of ``topk_workspace_bytes`` bytes: the caller's (kept at a
+    fixed address for graph capture) or, if none is given, one allocated here."""
     _lib.require_gpu(scores)
     if scores.dtype != torch.float32:
         raise TypeError(f"topk: scores must be float32, got {scores.dtype}")
@@ -45,8 +58,18 @@ def topk(scores: torch.Tensor, k: int, out: torch.Tensor | None = None) -> torch
     if out is None:
         out = torch.empty(*scores.shape[:-1], k, dtype=torch.int32, device=scores.device)
     of = out.view(-1, k)
-    _lib.call("mzk_topk_rows", flat.data_ptr(), rows, g, flat.stride(0) if rows else g, k, of.data_ptr(), k,
-              _lib.stream_of(scores))
+    need = topk_workspace_bytes(rows, g) if rows and k else 0
+    if need == 0:
+        _lib.call("mzk_topk_rows", flat.data_ptr(), rows, g, flat.stride(0) if rows else g, k, of.data_ptr(), k,
+                  _lib.stream_of(scores))
+        return out
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        if workspace is not None:
+            raise ValueError(f"topk: the workspace holds {workspace.numel() * workspace.element_size()} bytes, "
+                             f"{need} are needed")
+        workspace = torch.empty(need, dtype=torch.uint8, device=scores.device)
+    _lib.call("mzk_topk_rows_ws", flat.data_ptr(), rows, g, flat.stride(0), k, of.data_ptr(), k,
+              workspace.data_ptr(), workspace.numel() * workspace.element_size(), _lib.stream_of(scores))
     return out
 
 

@@ -62,6 +62,39 @@ def test_topk_exact_with_ties(dev, rows, g, k):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("rows,g,k,kind", [(4, 131072, 2048, "distinct"), (3, 40003, 2048, "distinct"),
+                                           (2, 524288, 2048, "distinct"), (5, 16384, 16384, "ties"),
+                                           (6, 9000, 100, "ties"), (4, 65536, 4096, "three_values"),
+                                           (3, 20000, 2048, "negative")])
+def test_topk_long_rows_split_over_workgroups(dev, rows, g, k, kind):
+    """Rows of 8193 .. 524288 scores go through mzk_topk_rows_ws (chunk histograms ->
+    per-row selection -> index-ordered write): exact against the oracle and equal to the
+    single-workgroup kernel.  'distinct' keeps the k-th key's bin small (its keys are
+    selected in LDS); 'three_values' puts tens of thousands of equal keys in that bin (the
+    selection streams the row instead); partial last chunks, k = G, -inf entries and rows
+    with fewer visible entries than k are covered too."""
+    from mzoo_amd import _lib
+    gen = torch.Generator().manual_seed(rows * 13 + g)
+    if kind == "distinct":
+        sc = torch.randn(rows, g, generator=gen)
+    elif kind == "ties":
+        sc = torch.round(torch.randn(rows, g, generator=gen) * 16) / 16
+        sc[:, ::5] = float("-inf")
+        sc[-1, g // 3:] = float("-inf")
+    elif kind == "three_values":
+        sc = torch.randint(0, 3, (rows, g), generator=gen).float()
+    else:
+        sc = -torch.rand(rows, g, generator=gen) - 1.0
+        sc[0, :] = float("-inf")
+    assert MI.topk_workspace_bytes(rows, g) > 0
+    got = MI.topk(sc.to(dev), k).cpu().numpy()
+    want = OA.topk_indices(sc.numpy(), k)
+    assert np.array_equal(got, want)
+    single = torch.empty(rows, k, dtype=torch.int32, device=dev)
+    scd = sc.to(dev)
+    _lib.call("mzk_topk_rows", scd.data_ptr(), rows, g, g, k, single.data_ptr(), k, _lib.stream_of(scd))
+    assert np.array_equal(single.cpu().numpy(), want)
+
 
 @pytest.mark.parametrize("case", ["distinct", "near_lowest_float", "mixed_sign_few_exponents"])
 def test_topk_exact_distinct_and_extreme(dev, case):
