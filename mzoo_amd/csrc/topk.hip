@@ -428,36 +428,42 @@ __global__ void __launch_bounds__(NT) topk_rows_reg_kernel(const float* __restri
 // ---- long rows, few of them: the row split over chunk workgroups ---------------------
 //
 // A row of G > kMultiMinG keys is cut into chunks of kChunk keys (thread t of a chunk
-// holds keys 8t .. 8t+7 in registers).  Three launches:
-//   A  one workgroup per (chunk, row): histogram of the top kBinBits of every finite key;
-//   B  one workgroup per row: merge the chunk histograms, find the bin b1 holding the k-th
-//      largest key; the keys of b1 (few, for any spread of scores) are gathered into LDS
-//      and a 3 x 7-bit radix select over their low 21 bits gives the threshold T and the
-//      number need_eq of keys equal to T to take (lowest indices first).  If b1 holds more
-//      than kCandCap keys the same passes stream the row from global memory instead.
-//      Then per chunk: #taken = #(key > T) + its share of the need_eq equal keys, and the
-//      exclusive prefix over chunks gives each chunk's first output slot;
-//   C  one workgroup per (chunk, row): the index-ordered compaction of the register kernel
-//      with the chunk's offset and share of equal keys.
+// holds keys 8t .. 8t+7 in registers).  Three launches, each spread over every (chunk,
+// row) workgroup, so no step streams a whole row through one CU:
+//   A  histogram of the top kBinBits of the chunk's finite keys;
+//   B  every chunk workgroup merges its row's histograms and finds the bin b1 of the k-th
+//      largest key (all chunks of a row reach the same b1), counts its keys in the bins
+//      above b1 and writes its keys of b1 (a few thousand per row for any spread of
+//      scores) to its own candidate region, in index order;
+//   C  every chunk workgroup loads its row's candidates into LDS and runs the same 3 x
+//      7-bit radix select over their low 21 bits (threshold T, and need_eq keys equal to
+//      T taken, lowest indices first), derives its first output slot from the counts of
+//      the chunks before it and writes its selected indices in index order.  If b1 holds
+//      more than kCandCap keys the selection streams the row instead (slow, but exact).
 // Same contract and results as the single-workgroup kernels.
 constexpr int kChunk = 8 * kThreads;           // keys per chunk workgroup
 constexpr int kBinBits = 11;
 constexpr int kBins = 1 << kBinBits;           // 2048 first-level bins
-constexpr int kLowBits = 32 - kBinBits;        // 21 bits resolved in B
+constexpr int kLowBits = 32 - kBinBits;        // 21 bits resolved in C
 constexpr int kCandCap = 12288;                // keys of bin b1 held in LDS
 constexpr int kMaxChunks = 64;                 // rows up to 64 x 8192 keys
 constexpr int64_t kMultiMinG = 8 * kThreads;   // shorter rows stay on one workgroup
 
-struct ChunkInfo {
-  int offset;   // first output slot of the chunk
-  int eq_take;  // keys equal to T the chunk takes (its lowest-index ones)
+// Workspace: hist [rows][nch][kBins] int32 | above [rows][nch] int32 | sel [rows] int4
+// (mode, b1, rem, finite total) | cand [rows][nch][kChunk] (key, index): chunk c of a row
+// writes its keys of bin b1 to the first hist[row][c][b1] slots of its own region
+struct MultiWs {
+  int64_t hist, above, sel, cand, total;
 };
-
-// Workspace: hist [rows][nch][kBins] int32 | info [rows][nch] ChunkInfo | T [rows] uint32
-__host__ __device__ inline int64_t multi_hist_bytes(int64_t rows, int64_t nch) { return rows * nch * kBins * 4; }
-__host__ __device__ inline int64_t multi_info_bytes(int64_t rows, int64_t nch) { return rows * nch * 8; }
-__host__ inline int64_t multi_ws_bytes(int64_t rows, int64_t nch) {
-  return multi_hist_bytes(rows, nch) + multi_info_bytes(rows, nch) + rows * 4;
+__host__ __device__ inline int64_t round16(int64_t x) { return (x + 15) / 16 * 16; }
+__host__ __device__ inline MultiWs multi_ws(int64_t rows, int64_t nch) {
+  MultiWs w;
+  w.hist = 0;
+  w.above = rows * nch * kBins * 4;
+  w.sel = w.above + round16(rows * nch * 4);
+  w.cand = w.sel + rows * 16;
+  w.total = w.cand + rows * nch * kChunk * 8;
+  return w;
 }
 
 // The 8 keys of thread t of chunk c (0 beyond G: below -inf, never counted or taken).
@@ -537,112 +543,180 @@ __device__ __forceinline__ void for_row_keys(const float* __restrict__ src, int 
   }
 }
 
-__global__ void __launch_bounds__(kThreads) topk_select_kernel(const float* __restrict__ scores, int64_t row_stride,
-                                                                 int G, int k, int nch, const int* __restrict__ hist_in,
-                                                                 ChunkInfo* __restrict__ info_out,
-                                                                 uint32_t* __restrict__ t_out, int32_t* __restrict__ out,
-                                                                 int64_t out_stride) {
-  __shared__ uint32_t cand_key[kCandCap];
-  __shared__ int cand_idx[kCandCap];
-  __shared__ int hist7[128];
-  __shared__ int chunk_gt[kMaxChunks], chunk_eq[kMaxChunks];
-  __shared__ int wsum[kWaves];
-  __shared__ int sh_b1, sh_rem, sh_cnt, sh_ncand, sh_digit;
+// How the row's selection splits at the bin level.  mode 0: at most k finite keys, take
+// them all; 1: the keys of bins >= b1 are exactly the k largest; 2: the keys of bins > b1
+// plus the rem largest of bin b1 (lowest indices first among equals).
+struct RowSel {
+  int mode, b1, rem, total;
+};
 
-  const int row = blockIdx.x;
-  const float* src = scores + static_cast<int64_t>(row) * row_stride;
-  const int* hrow = hist_in + static_cast<int64_t>(row) * nch * kBins;
+// Merge the row's chunk histograms (thread t: bins 2t, 2t+1; 16 chunks per memory round
+// trip) and locate the bin of the k-th largest finite key with one block-wide scan.  Every
+// thread returns the same.  wsum [kWaves] and sh [3] are LDS scratch.
+__device__ RowSel row_threshold_bin(const int* __restrict__ hrow, int nch, int k, int* wsum, int* sh) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-
-  // 1. bin totals over the chunks (thread t: bins 2t, 2t+1; 16 chunks per round trip)
   int t0 = 0, t1 = 0;
   for (int c0 = 0; c0 < nch; c0 += 16) {
     int2 v[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j)
-      v[j] = c0 + j < nch ? *reinterpret_cast<const int2*>(hrow + static_cast<int64_t>(c0 + j) * kBins + 2 * tid)
-                          : int2{0, 0};
+    for (int j = 0; j < 16; ++j) {  // branch-free: chunks past the end re-read the last one
+      const int cj = c0 + j < nch ? c0 + j : nch - 1;
+      v[j] = *reinterpret_cast<const int2*>(hrow + static_cast<int64_t>(cj) * kBins + 2 * tid);
+    }
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      t0 += v[j].x;
-      t1 += v[j].y;
+      const int keep = c0 + j < nch;
+      t0 += keep * v[j].x;
+      t1 += keep * v[j].y;
     }
-  }
-  if (tid < kMaxChunks) {
-    chunk_gt[tid] = 0;
-    chunk_eq[tid] = 0;
   }
   // inclusive prefix of the pair totals over threads (= over bins, ascending)
   const int pair = t0 + t1;
   int incl = wave_incl_scan_dpp(pair);
   if (lane == 63) wsum[wave] = incl;
   __syncthreads();
-  int total_fin = 0;
+  int total = 0;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
-    total_fin += wsum[w];
+    total += wsum[w];
     incl += w < wave ? wsum[w] : 0;
   }
-
-  // 2. the bin b1 holding the k-th largest key: keys in bins above thread t's pair number
-  //    total - incl; exactly one (thread, bin) sees the k-th key
-  uint32_t T = kNegInfKey;
-  int need_eq = 0, b_lo = 0;  // chunks take every key in bins >= b_lo (plus b1's selection)
-  bool partial = false;
-  int b1 = 0;
-  if (total_fin > k) {
-    const int above_hi = total_fin - incl;  // keys in bins > 2t+1
-    const int above_lo = above_hi + t1;     // keys in bins > 2t
+  RowSel r{0, 0, 0, total};
+  if (total > k) {
+    // keys in bins above thread t's pair: total - incl; exactly one (thread, bin) holds
+    // the k-th largest key
+    const int above_hi = total - incl;  // keys in bins > 2t+1
+    const int above_lo = above_hi + t1; // keys in bins > 2t
     if (above_hi < k && k <= above_hi + t1) {
-      sh_b1 = 2 * tid + 1;
-      sh_rem = k - above_hi;
-      sh_cnt = t1;
+      sh[0] = 2 * tid + 1;
+      sh[1] = k - above_hi;
+      sh[2] = t1;
     } else if (above_lo < k && k <= above_lo + t0) {
-      sh_b1 = 2 * tid;
-      sh_rem = k - above_lo;
-      sh_cnt = t0;
+      sh[0] = 2 * tid;
+      sh[1] = k - above_lo;
+      sh[2] = t0;
     }
     __syncthreads();
-    b1 = sh_b1;
-    if (sh_rem == sh_cnt) {  // the bin is taken whole
-      T = (static_cast<uint32_t>(b1) << kLowBits) - 1u;  // b1 >= 4: finite keys sit in bins >= 4
-      b_lo = b1;
-    } else {
-      partial = true;
-      b_lo = b1 + 1;
+    r.b1 = sh[0];
+    r.rem = sh[1];
+    r.mode = sh[1] == sh[2] ? 1 : 2;
+  }
+  return r;
+}
+
+__global__ void __launch_bounds__(kThreads) topk_chunk_gather_kernel(const float* __restrict__ scores,
+                                                                       int64_t row_stride, int G, int k, int nch,
+                                                                       const int* __restrict__ hist_in,
+                                                                       int* __restrict__ above_out,
+                                                                       int4* __restrict__ sel_out,
+                                                                       uint2* __restrict__ cand_out) {
+  __shared__ int wsum[kWaves];
+  __shared__ int red[kWaves];
+  __shared__ int msum[kWaves];
+  __shared__ int sh[3];
+  const int row = blockIdx.y, c = blockIdx.x;
+  const float* src = scores + static_cast<int64_t>(row) * row_stride;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t key[8];
+  load_chunk_keys(src, G, c * kChunk, tid, key);  // in flight during the histogram merge
+  const RowSel rs = row_threshold_bin(hist_in + static_cast<int64_t>(row) * nch * kBins, nch, k, wsum, sh);
+  const int b_lo = rs.mode == 0 ? 0 : (rs.mode == 1 ? rs.b1 : rs.b1 + 1);
+  // this chunk's finite keys in bins >= b_lo (finite keys sit in bins >= 4)
+  int n = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) n += key[j] > kNegInfKey && static_cast<int>(key[j] >> kLowBits) >= b_lo;
+  n += __shfl_xor(n, 1, 64);
+  n += __shfl_xor(n, 2, 64);
+  n += __shfl_xor(n, 4, 64);
+  n += __shfl_xor(n, 8, 64);
+  n += __shfl_xor(n, 16, 64);
+  n += __shfl_xor(n, 32, 64);
+  if (lane == 0) red[wave] = n;
+  // this chunk's keys of bin b1, in index order, to the chunk's own candidate region
+  // (slots from a workgroup scan: no atomics)
+  int nm = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) nm += rs.mode == 2 && static_cast<int>(key[j] >> kLowBits) == rs.b1;
+  const int mincl = wave_incl_scan_dpp(nm);
+  if (lane == 63) msum[wave] = mincl;
+  __syncthreads();
+  if (rs.mode == 2) {
+    int slot = mincl - nm;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) slot += w < wave ? msum[w] : 0;
+    uint2* dst = cand_out + (static_cast<int64_t>(row) * nch + c) * kChunk;
+    const int i0 = c * kChunk + 8 * tid;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (static_cast<int>(key[j] >> kLowBits) == rs.b1) {
+        dst[slot] = uint2{key[j], static_cast<uint32_t>(i0 + j)};
+        ++slot;
+      }
     }
   }
+  if (tid == 0) {
+    int tot = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) tot += red[w];
+    above_out[static_cast<int64_t>(row) * nch + c] = tot;
+    if (c == 0) sel_out[row] = int4{rs.mode, rs.b1, rs.rem, rs.total};
+  }
+}
 
-  if (partial) {
-    // 3. select among the keys of bin b1: LDS candidates if they fit, else stream the row
-    //    (b1 >= 4, so the 0 keys past the row end never match)
-    const bool in_lds = sh_cnt <= kCandCap;
-    if (tid == 0) sh_ncand = 0;
-    __syncthreads();
-    if (in_lds) {
-      // one LDS atomic per wave and step reserves the wave's slots
-      for_row_keys(src, G, [&](const uint32_t (&key)[8], int i0) {
-        int nm = 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) nm += static_cast<int>(key[j] >> kLowBits) == b1;
-        const int incl = wave_incl_scan_dpp(nm);
-        int wb = 0;
-        if (lane == 63 && incl > 0) wb = atomicAdd(&sh_ncand, incl);
-        int slot = __builtin_amdgcn_readlane(wb, 63) + incl - nm;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          if (static_cast<int>(key[j] >> kLowBits) == b1) {
-            if (slot < kCandCap) {
-              cand_key[slot] = key[j];
-              cand_idx[slot] = i0 + j;
-            }
-            ++slot;
-          }
-        }
-      });
-      __syncthreads();
+__global__ void __launch_bounds__(kThreads) topk_chunk_select_write_kernel(
+    const float* __restrict__ scores, int64_t row_stride, int G, int k, int nch, const int* __restrict__ hist_in,
+    const int* __restrict__ above_in, const int4* __restrict__ sel_in, const uint2* __restrict__ cand_in,
+    int32_t* __restrict__ out, int64_t out_stride) {
+  __shared__ uint32_t cand_key[kCandCap];
+  __shared__ int cand_idx[kCandCap];
+  __shared__ int hist7[128];
+  __shared__ int chunk_gt[kMaxChunks], chunk_eq[kMaxChunks], chunk_above[kMaxChunks], cand_start[kMaxChunks + 1];
+  __shared__ __align__(16) int wsum[kWaves];
+  __shared__ int sh_rem, sh_digit, sh_off, sh_take, sh_total;
+
+  const int row = blockIdx.y, c = blockIdx.x;
+  const float* src = scores + static_cast<int64_t>(row) * row_stride;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t key[8];
+  load_chunk_keys(src, G, c * kChunk, tid, key);
+  const int4 rs = sel_in[row];
+  const int mode = rs.x, b1 = rs.y;
+  // per chunk: keys above b1 and keys in b1 (the candidates, from the chunk histograms)
+  int cnt_b1 = 0;
+  if (tid < kMaxChunks) {
+    const int ct = tid < nch ? tid : nch - 1;
+    chunk_gt[tid] = 0;
+    chunk_eq[tid] = 0;
+    chunk_above[tid] = tid < nch ? above_in[static_cast<int64_t>(row) * nch + ct] : 0;
+    cnt_b1 = tid < nch ? hist_in[(static_cast<int64_t>(row) * nch + ct) * kBins + b1] : 0;
+  }
+  if (wave == 0) {  // candidate start of every chunk (exclusive prefix over the 64 lanes)
+    const int ci = wave_incl_scan_dpp(cnt_b1);
+    cand_start[lane + 1] = ci;
+    if (lane == 0) cand_start[0] = 0;
+  }
+  __syncthreads();
+  const int ncand_all = cand_start[kMaxChunks];
+  uint32_t T = kNegInfKey;
+  int need_eq = 0;
+  if (mode == 1) T = (static_cast<uint32_t>(b1) << kLowBits) - 1u;  // b1 >= 4
+  if (mode == 2) {
+    const bool in_lds = ncand_all <= kCandCap;
+    const int ncand = in_lds ? ncand_all : 0;
+    const uint2* cr = cand_in + static_cast<int64_t>(row) * nch * kChunk;
+    for (int m = tid; m < ncand; m += kThreads) {
+      // chunk holding candidate m: the last start <= m (binary search over the starts)
+      int lo = 0, hi = nch - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (cand_start[mid] <= m) lo = mid;
+        else hi = mid - 1;
+      }
+      const uint2 v = cr[static_cast<int64_t>(lo) * kChunk + (m - cand_start[lo])];
+      cand_key[m] = v.x;
+      cand_idx[m] = static_cast<int>(v.y);
     }
-    const int ncand = in_lds ? min(sh_ncand, kCandCap) : 0;
+    __syncthreads();
     // f(key, index, active) over the keys of bin b1, in wave-uniform control flow
     auto for_cands = [&](auto&& f) {
       if (in_lds) {
@@ -652,23 +726,23 @@ __global__ void __launch_bounds__(kThreads) topk_select_kernel(const float* __re
           f(a ? cand_key[m] : 0u, a ? cand_idx[m] : 0, a);
         }
       } else {
-        for_row_keys(src, G, [&](const uint32_t (&key)[8], int i0) {
+        for_row_keys(src, G, [&](const uint32_t (&kk)[8], int i0) {
 #pragma unroll
-          for (int j = 0; j < 8; ++j) f(key[j], i0 + j, static_cast<int>(key[j] >> kLowBits) == b1);
+          for (int j = 0; j < 8; ++j) f(kk[j], i0 + j, static_cast<int>(kk[j] >> kLowBits) == b1);
         });
       }
     };
     uint32_t prefix = static_cast<uint32_t>(b1) << kLowBits, mask = ~((1u << kLowBits) - 1u);
-    int rem = sh_rem;
+    int rem = rs.z;
     for (int shift = kLowBits - 7; shift >= 0; shift -= 7) {
       if (tid < 128) hist7[tid] = 0;
       __syncthreads();
-      for_cands([&](uint32_t key, int, bool a) { hist_add(hist7, (key >> shift) & 127u, a && (key & mask) == prefix); });
+      for_cands([&](uint32_t kk, int, bool a) { hist_add(hist7, (kk >> shift) & 127u, a && (kk & mask) == prefix); });
       __syncthreads();
       if (wave == 0) {
         const int h0 = hist7[127 - 2 * lane], h1 = hist7[126 - 2 * lane];
         const int hs = h0 + h1;
-        int above = wave_incl_scan_dpp(hs) - hs;
+        const int above = wave_incl_scan_dpp(hs) - hs;
         int d = -1, r = 0;
         if (above < rem && rem <= above + h0) {
           d = 127 - 2 * lane;
@@ -693,68 +767,36 @@ __global__ void __launch_bounds__(kThreads) topk_select_kernel(const float* __re
     T = prefix;
     need_eq = rem;
     // keys of bin b1 above / equal to T, per chunk
-    for_cands([&](uint32_t key, int i, bool a) {
-      const uint32_t c = static_cast<uint32_t>(i / kChunk);
-      hist_add(chunk_gt, c, a && key > T);
-      hist_add(chunk_eq, c, a && key == T);
+    for_cands([&](uint32_t kk, int i, bool a) {
+      const uint32_t cc = static_cast<uint32_t>(i / kChunk);
+      hist_add(chunk_gt, cc, a && kk > T);
+      hist_add(chunk_eq, cc, a && kk == T);
     });
   }
-
-  // 4. per chunk: keys in bins >= b_lo (wave w: chunks w, w + 16, ...)
-  for (int c = wave; c < nch; c += kWaves) {
-    const int* hc = hrow + static_cast<int64_t>(c) * kBins;
-    int v[kBins / 64];
-#pragma unroll
-    for (int r = 0; r < kBins / 64; ++r) v[r] = hc[64 * r + lane];
-    int n = 0;
-#pragma unroll
-    for (int r = 0; r < kBins / 64; ++r) n += 64 * r + lane >= b_lo ? v[r] : 0;
-    n += __shfl_xor(n, 1, 64);
-    n += __shfl_xor(n, 2, 64);
-    n += __shfl_xor(n, 4, 64);
-    n += __shfl_xor(n, 8, 64);
-    n += __shfl_xor(n, 16, 64);
-    n += __shfl_xor(n, 32, 64);
-    if (lane == 0) atomicAdd(&chunk_gt[c], n);
-  }
   __syncthreads();
-  // 5. chunk offsets (index order): equal keys go to the lowest indices first
+  // this chunk's first output slot and share of the equal keys (index order), the row total
   if (tid == 0) {
-    int off = 0, eq_left = need_eq;
-    for (int c = 0; c < nch; ++c) {
-      const int take = min(eq_left, chunk_eq[c]);
-      info_out[static_cast<int64_t>(row) * nch + c] = ChunkInfo{off, take};
-      off += chunk_gt[c] + take;
+    int off = 0, eq_left = need_eq, my_off = 0, my_take = 0;
+    for (int cc = 0; cc < nch; ++cc) {
+      const int take = min(eq_left, chunk_eq[cc]);
+      if (cc == c) {
+        my_off = off;
+        my_take = take;
+      }
+      off += chunk_above[cc] + chunk_gt[cc] + take;
       eq_left -= take;
     }
-    t_out[row] = T;
-    sh_ncand = off;  // entries written by the chunks
+    sh_off = my_off;
+    sh_take = my_take;
+    sh_total = off;
   }
-  __syncthreads();
-  int32_t* dst = out + static_cast<int64_t>(row) * out_stride;
-  for (int i = sh_ncand + tid; i < k; i += kThreads) dst[i] = -1;
-}
-
-__global__ void __launch_bounds__(kThreads) topk_chunk_write_kernel(const float* __restrict__ scores, int64_t row_stride,
-                                                                      int G, int k, int nch,
-                                                                      const ChunkInfo* __restrict__ info,
-                                                                      const uint32_t* __restrict__ t_in,
-                                                                      int32_t* __restrict__ out, int64_t out_stride) {
-  __shared__ __align__(16) int wsum[kWaves];
-  const int row = blockIdx.y, c = blockIdx.x;
-  const float* src = scores + static_cast<int64_t>(row) * row_stride;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  uint32_t key[8];
-  load_chunk_keys(src, G, c * kChunk, tid, key);
-  const uint32_t T = t_in[row];
-  const ChunkInfo ci = info[static_cast<int64_t>(row) * nch + c];
+  // packed exclusive scan over the chunk (both counts < 2^13 per chunk)
   int n_gt = 0, n_eq = 0;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     n_gt += key[j] > T;
     n_eq += (key[j] == T) && (T != kNegInfKey);
   }
-  // packed exclusive scan over the chunk (both counts < 2^13 per chunk)
   const int packed = (n_gt << 16) | n_eq;
   const int incl = wave_incl_scan_dpp(packed);
   if (lane == 63) wsum[wave] = incl;
@@ -763,6 +805,7 @@ __global__ void __launch_bounds__(kThreads) topk_chunk_write_kernel(const float*
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) before += w < wave ? wsum[w] : 0;
   int gt_before = before >> 16, eq_before = before & 0xffff;
+  const int off = sh_off, eq_take = sh_take;
   int32_t* dst = out + static_cast<int64_t>(row) * out_stride;
   const int i0 = c * kChunk + 8 * tid;
   // slots stay below k by construction; the bound also holds if the scores were changed
@@ -770,15 +813,17 @@ __global__ void __launch_bounds__(kThreads) topk_chunk_write_kernel(const float*
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     if (key[j] > T) {
-      const int slot = ci.offset + gt_before + min(eq_before, ci.eq_take);
+      const int slot = off + gt_before + min(eq_before, eq_take);
       if (slot < k) dst[slot] = i0 + j;
       ++gt_before;
     } else if (key[j] == T && T != kNegInfKey) {
-      const int slot = ci.offset + gt_before + eq_before;
-      if (eq_before < ci.eq_take && slot < k) dst[slot] = i0 + j;
+      const int slot = off + gt_before + eq_before;
+      if (eq_before < eq_take && slot < k) dst[slot] = i0 + j;
       ++eq_before;
     }
   }
+  if (c == nch - 1)
+    for (int i = sh_total + tid; i < k; i += kThreads) dst[i] = -1;
 }
 
 int topk_multi_chunks(int64_t rows, int64_t cols) {
@@ -820,7 +865,7 @@ extern "C" int mzk_topk_rows(const float* scores, int64_t rows, int64_t cols, in
 extern "C" int mzk_topk_workspace_bytes(int64_t rows, int64_t cols, int64_t* bytes) {
   MZK_CHECK_ARG(rows >= 0 && cols >= 0 && bytes != nullptr, "topk_workspace_bytes: bad arguments");
   const int nch = topk_multi_chunks(rows, cols);
-  *bytes = nch ? multi_ws_bytes(rows, nch) : 0;
+  *bytes = nch ? multi_ws(rows, nch).total : 0;
   return MZK_OK;
 }
 
@@ -833,21 +878,22 @@ extern "C" int mzk_topk_rows_ws(const float* scores, int64_t rows, int64_t cols,
   MZK_CHECK_ARG(topk > 0 && cols <= (int64_t(1) << 30) && topk <= (1 << 30), "topk_rows: bad sizes");
   MZK_CHECK_ARG(row_stride >= cols && out_stride >= topk, "topk_rows: strides smaller than the row");
   MZK_CHECK_ARG(out != nullptr && scores != nullptr, "topk_rows: null pointer");
-  const int64_t need = multi_ws_bytes(rows, nch);
-  MZK_CHECK_ARG(workspace != nullptr && workspace_bytes >= need && aligned16(workspace),
+  const MultiWs w = multi_ws(rows, nch);
+  MZK_CHECK_ARG(workspace != nullptr && workspace_bytes >= w.total && aligned16(workspace),
                 "topk_rows: rows of %lld keys need a 16-byte aligned workspace of %lld bytes", (long long)cols,
-                (long long)need);
+                (long long)w.total);
   hipStream_t s = as_stream(stream);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
-  int* hist = reinterpret_cast<int*>(ws);
-  ChunkInfo* info = reinterpret_cast<ChunkInfo*>(ws + multi_hist_bytes(rows, nch));
-  uint32_t* tv = reinterpret_cast<uint32_t*>(ws + multi_hist_bytes(rows, nch) + multi_info_bytes(rows, nch));
+  int* hist = reinterpret_cast<int*>(ws + w.hist);
+  int* above = reinterpret_cast<int*>(ws + w.above);
+  int4* sel = reinterpret_cast<int4*>(ws + w.sel);
+  uint2* cand = reinterpret_cast<uint2*>(ws + w.cand);
   const int G = static_cast<int>(cols);
   const dim3 grid(static_cast<unsigned>(nch), static_cast<unsigned>(rows));
   topk_chunk_hist_kernel<<<grid, kThreads, 0, s>>>(scores, row_stride, G, nch, hist);
-  topk_select_kernel<<<static_cast<unsigned>(rows), kThreads, 0, s>>>(scores, row_stride, G, topk, nch, hist, info,
-                                                                       tv, out, out_stride);
-  topk_chunk_write_kernel<<<grid, kThreads, 0, s>>>(scores, row_stride, G, topk, nch, info, tv, out, out_stride);
+  topk_chunk_gather_kernel<<<grid, kThreads, 0, s>>>(scores, row_stride, G, topk, nch, hist, above, sel, cand);
+  topk_chunk_select_write_kernel<<<grid, kThreads, 0, s>>>(scores, row_stride, G, topk, nch, hist, above, sel, cand,
+                                                            out, out_stride);
   MZK_LAUNCH_CHECK("topk_rows_ws");
   return MZK_OK;
 }
