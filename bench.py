@@ -186,16 +186,13 @@ def stage_fns(torch, layer, inputs):
                       kv.data_ptr(), cfg.nope, cfg.rope, layer.win.data_ptr(), cfg.window, cfg.window, st())
         fns["indexer_decode_fp8"] = indexer_decode
     else:
-        def prologue():
-            # window append + indexer-query MXFP4 quantization (one launch)
-            _lib.call("mzk_decode_prologue", kv.data_ptr(), _lib.dtype_code(kv.dtype), b, cfg.nope, cfg.rope,
-                      layer.positions.data_ptr(), layer.win.data_ptr(), cfg.window, cfg.window, q_idx.data_ptr(),
-                      _lib.dtype_code(q_idx.dtype), b * cfg.index_heads, cfg.index_dim, 1, layer.q_codes.data_ptr(),
-                      None, layer.q_e8m0.data_ptr(), st())
-        fns["decode_prologue"] = prologue
-        fns["indexer_mxfp4"] = lambda: indexer.scores_mxfp4(
-            layer.q_codes, layer.q_e8m0, w.view(b, 1, -1), layer.k_packed, layer.k_e8m0, compress_ratio=cfg.ratio,
-            positions=layer.positions.view(b, 1), out=layer.scores)
+        def indexer_decode():
+            # window append + indexer-query MXFP4 quantization + scores: one launch
+            _lib.call("mzk_indexer_decode_mxfp4", q_idx.data_ptr(), w.data_ptr(), layer.k_packed.data_ptr(),
+                      layer.k_e8m0.data_ptr(), b, cfg.index_heads, cfg.index_dim, cfg.max_groups, cfg.max_groups,
+                      layer.positions.data_ptr(), cfg.ratio, layer.scores.data_ptr(), cfg.max_groups, None, None,
+                      kv.data_ptr(), cfg.nope, cfg.rope, layer.win.data_ptr(), cfg.window, cfg.window, st())
+        fns["indexer_decode_mxfp4"] = indexer_decode
     fns["topk"] = lambda: indexer.topk(layer.scores.view(b, cfg.max_groups), cfg.topk, out=layer.idx,
                                        workspace=layer.topk_ws)
     coarse = layer.coarse
@@ -320,7 +317,7 @@ def run_decode(torch, dev, args):
     attn_flops = rows * 4.0 * cfg.dim * cfg.heads * entries
     idx_bytes = rows * cfg.max_groups * KEY_BYTES[cfg.index_format]
     idx_flops = rows * 2.0 * cfg.index_heads * cfg.index_dim * cfg.max_groups
-    idx_stage = "indexer_decode_fp8" if cfg.index_format == "fp8" else "indexer_mxfp4"
+    idx_stage = "indexer_decode_fp8" if cfg.index_format == "fp8" else "indexer_decode_mxfp4"
     dominant = max(("sparse_mqa", idx_stage, "topk"), key=lambda k: stages[k])
     if dominant == "sparse_mqa":
         roof = roofline(None, attn_flops, attn_bytes, stages[dominant])

@@ -167,6 +167,19 @@ int mzk_indexer_decode_fp8(const void* q_idx, const float* w, const uint8_t* k_c
                            uint8_t* win_cache, int64_t win_batch_entries, int win_cap,
                            void* stream);
 
+/* The same for the MXFP4 indexer: q_idx [B, Hi, 128] bf16 is quantized in the kernel to
+ * MXFP4 (identical to mzk_quant_mxfp4: block 32, ue8m0 scales -- owlet1/indexer.py:129
+ * with owlet1/quant.py:49-66) and scored against k_packed / k_e8m0 exactly as
+ * mzk_indexer_scores_mxfp4 would score the quantized query.  Optional extras: q_packed
+ * [B, Hi, 64] + q_e8m0 [B, Hi, 4] (both or neither), and the window append of kv as in
+ * mzk_indexer_decode_fp8.  Replaces mzk_decode_prologue + mzk_indexer_scores_mxfp4 in the
+ * decode step. */
+int mzk_indexer_decode_mxfp4(const void* q_idx, const float* w, const uint8_t* k_packed, const uint8_t* k_e8m0,
+                             int64_t B, int Hi, int Di, int64_t G, int64_t k_batch_stride, const int64_t* positions,
+                             int ratio, float* scores, int64_t score_stride, uint8_t* q_packed, uint8_t* q_e8m0,
+                             const void* kv, int nope, int rope, uint8_t* win_cache, int64_t win_batch_entries,
+                             int win_cap, void* stream);
+
 /* bf16 q [rows, Hi, Di] and k [B, G, Di] -- the contract of layers/attn/indexer/fwd.py:112. */
 int mzk_indexer_scores_bf16(const void* q, const float* w, const void* k, int64_t B, int64_t S,
                             int Hi, int Di, int64_t G, int64_t k_batch_stride,

@@ -45,6 +45,8 @@ _SIGS = {
     "mzk_indexer_scores_fp8": [_P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P, _I64, _P],
     "mzk_indexer_decode_fp8": [_P, _P, _P, _P, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P, _I64, _P, _P, _P, _I32, _I32,
                                _P, _I64, _I32, _P],
+    "mzk_indexer_decode_mxfp4": [_P, _P, _P, _P, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P, _I64, _P, _P, _P, _I32,
+                                 _I32, _P, _I64, _I32, _P],
     "mzk_indexer_scores_mxfp4": [_P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P, _I64, _P],
     "mzk_indexer_scores_bf16": [_P, _P, _P, _I64, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P, _I64, _P],
     "mzk_compress": [_P, _P, _I64, _I64, _I32, _I32, _I64, _P, _I32, _F32, _P, _I32, _P],

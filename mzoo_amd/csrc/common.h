@@ -170,6 +170,15 @@ __device__ __forceinline__ float fp8_scale_from_amax(float amax) {
 
 __device__ __forceinline__ float clampf(float v, float lim) { return fminf(fmaxf(v, -lim), lim); }
 
+// FP4 block scale of the reference's fake quantizer (owlet1/quant.py:49-66): ue8m0
+// pow2ceil(max(amax, 6*2^-126) * fp32(1/6)), or with e4m3 scales e4m3(max(amax, 6*2^-9) / 6).
+constexpr float kInv6 = 1.0f / 6.0f;  // the fp32-rounded reciprocal the reference multiplies by
+
+__device__ __forceinline__ float fp4_scale_from_amax(float amax, bool e4m3_scales) {
+  if (e4m3_scales) return e4m3_decode(e4m3_encode(div_rn(fmaxf(amax, 0x1.8p-7f /* 6*2^-9 */), 6.0f)));
+  return pow2_ceil(fmaxf(amax, 0x1.8p-124f /* 6*2^-126 */) * kInv6);
+}
+
 // ------------------------------------------------------------------------------------
 // FP4 e2m1 codes.  code = number of thresholds <= |q| (ties at 0.25/1.25/2.5/5 round
 // down, at 0.75/1.75/3.5 round up), sign in bit 3 from the sign bit (-0 -> 8).

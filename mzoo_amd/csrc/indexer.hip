@@ -117,11 +117,13 @@ struct IdxParams {
   int ratio;
   float* scores;
   int64_t sstride;
-  // fused decode prologue (FP8, Di = 128): the bf16 query is quantized in the kernel, and
-  // workgroup 0 of each row stores the codes / scales and appends the new latent
+  // fused decode prologue (Di = 128): the bf16 query is quantized in the kernel (FP8 b128
+  // or MXFP4), and workgroup 0 of each row stores the codes / scales and appends the new
+  // latent
   const uint16_t* q_raw;  // [rows, Hi, 128] bf16
-  uint8_t* q_codes_out;   // [rows, Hi, 128] e4m3, or null
-  float* q_scales_out;    // [rows, Hi], or null
+  uint8_t* q_codes_out;   // FP8: [rows, Hi, 128] e4m3; MXFP4: [rows, Hi, 64] e2m1 pairs; or null
+  float* q_scales_out;    // FP8: [rows, Hi], or null
+  uint8_t* q_e8m0_out;    // MXFP4: [rows, Hi, 4], or null
   const uint16_t* kv;     // [rows, nope + rope] bf16 (APPEND)
   int nope, rope;
   uint8_t* win;
@@ -129,18 +131,24 @@ struct IdxParams {
   int win_cap;
 };
 
-constexpr int kQPitch = 128 + 16;  // LDS bytes per quantized head row (padding spreads banks)
+// LDS bytes per quantized head row (padding spreads banks)
+template <int FMT>
+constexpr int q_pitch() { return FMT == kFp8 ? 128 + 16 : 64 + 16; }
 
 // One workgroup = 4 waves = one query row x kKeysPerWg keys (see the tiling note above).
-// QRAW: the query arrives as bf16 [Hi, 128] and each workgroup quantizes it (FP8 b128 of
-// owlet1/quant.py:72-86: one power-of-two scale per head) into LDS -- thread t owns head
-// t/4, channels 32(t%4)..+31 -- with v_cvt_pk_fp8_f32, which equals the e4m3 encoder of
-// the quantizer (round to nearest even, subnormals kept) for every |x| <= 448.
+// QRAW: the query arrives as bf16 [Hi, 128] and each workgroup quantizes it into LDS --
+// thread t owns head t/4, channels 32(t%4)..+31.  FP8 b128 (owlet1/quant.py:72-86: one
+// power-of-two scale per head) uses v_cvt_pk_fp8_f32, which equals the e4m3 encoder of the
+// quantizer (round to nearest even, subnormals kept) for every |x| <= 448.  MXFP4
+// (quant.py:49-66 with block 32 and ue8m0 scales): a thread's 32 channels are one scale
+// block, encoded with the quantizer's own e2m1 thresholds, and exactly one lane's MFMA
+// fragment (16 bytes of nibbles + the e8m0 byte).
 // APPEND: workgroup 0 of the row also writes the new token's FP8-b128 latent into its
 // window-ring slot (b * win_batch_entries + pos % win_cap).
 template <int FMT, int DI, int MB, bool QRAW, bool APPEND>
 __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxParams p) {
-  static_assert(!QRAW || (FMT == kFp8 && DI == 128), "in-kernel quantization: FP8 b128 queries only");
+  static_assert(!QRAW || ((FMT == kFp8 || FMT == kMxfp4) && DI == 128), "in-kernel quantization: Di = 128");
+  constexpr int QP = q_pitch<FMT>();
   constexpr int NST = DI / Step<FMT>::K;
   constexpr int RB = row_bytes<FMT>(DI);
   const int tid = threadIdx.x;
@@ -220,9 +228,55 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
   if (vis > G) vis = G;
   if (vis < 0) vis = 0;
 
-  __shared__ __align__(16) uint8_t q_lds[QRAW ? 64 * kQPitch : 16];
-  __shared__ float qs_lds[QRAW ? 64 : 1];
-  if constexpr (QRAW) {
+  __shared__ __align__(16) uint8_t q_lds[QRAW ? 64 * QP : 16];
+  __shared__ float qs_lds[QRAW && FMT == kFp8 ? 64 : 1];
+  __shared__ uint8_t qe_lds[QRAW && FMT == kMxfp4 ? 256 : 4];
+  if constexpr (QRAW && FMT == kMxfp4) {
+    // one MXFP4 block of 32 channels per thread: scale, then e2m1 codes (element 2i in the
+    // low nibble of byte i), as the quantizer's packed form
+    float amax = 0.0f;
+    uint32_t wd[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t wv[4] = {qr[i].x, qr[i].y, qr[i].z, qr[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = qh < Hi ? bf16_to_f32(static_cast<uint16_t>(wv[j] & 0xffffu)) : 0.0f;
+        const float hi2 = qh < Hi ? bf16_to_f32(static_cast<uint16_t>(wv[j] >> 16)) : 0.0f;
+        amax = fmaxf(amax, fmaxf(fabsf(lo), fabsf(hi2)));
+      }
+    }
+    const float sc = fp4_scale_from_amax(amax, false);
+    // x / sc == x * (1 / sc) exactly: sc is a power of two in [2^-126, 2^127], so 1 / sc is
+    // exact and both sides are the correctly rounded x * 2^-e
+    const float inv = 1.0f / sc;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t wv[4] = {qr[i].x, qr[i].y, qr[i].z, qr[i].w};
+      uint32_t word = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = qh < Hi ? bf16_to_f32(static_cast<uint16_t>(wv[j] & 0xffffu)) : 0.0f;
+        const float hi2 = qh < Hi ? bf16_to_f32(static_cast<uint16_t>(wv[j] >> 16)) : 0.0f;
+        word |= e2m1_code(clampf(lo * inv, 6.0f)) << (8 * j);
+        word |= e2m1_code(clampf(hi2 * inv, 6.0f)) << (8 * j + 4);
+      }
+      wd[i] = word;
+    }
+    *reinterpret_cast<uint4*>(q_lds + qh * QP + 16 * qc) = uint4{wd[0], wd[1], wd[2], wd[3]};
+    qe_lds[qh * 4 + qc] = static_cast<uint8_t>(__float_as_uint(sc) >> 23);
+    __syncthreads();
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int h = mb * 32 + (lane & 31);
+#pragma unroll
+      for (int st = 0; st < NST; ++st) {
+        const uint4 u = *reinterpret_cast<const uint4*>(q_lds + h * QP + st * 32 + hi * 16);
+        a[mb][st].v = v8i{(int)u.x, (int)u.y, (int)u.z, (int)u.w, 0, 0, 0, 0};
+        a[mb][st].scale = qe_lds[h * 4 + st * 2 + hi];
+      }
+    }
+  } else if constexpr (QRAW) {
     float x[32];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -248,14 +302,14 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
       wd[i] = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(clampf(x[4 * i + 2] * inv, 448.0f),
                                                                     clampf(x[4 * i + 3] * inv, 448.0f), lo, true));
     }
-    uint4* dst = reinterpret_cast<uint4*>(q_lds + qh * kQPitch + 32 * qc);
+    uint4* dst = reinterpret_cast<uint4*>(q_lds + qh * QP + 32 * qc);
     dst[0] = uint4{wd[0], wd[1], wd[2], wd[3]};
     dst[1] = uint4{wd[4], wd[5], wd[6], wd[7]};
     if (qc == 0) qs_lds[qh] = sc;
     __syncthreads();
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
-      const uint4* src = reinterpret_cast<const uint4*>(q_lds + (mb * 32 + (lane & 31)) * kQPitch);
+      const uint4* src = reinterpret_cast<const uint4*>(q_lds + (mb * 32 + (lane & 31)) * QP);
 #pragma unroll
       for (int st = 0; st < NST; ++st) {
         const uint4 u = src[4 * st + 2 * hi], v = src[4 * st + 2 * hi + 1];
@@ -301,12 +355,20 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
   if constexpr (QRAW) {
     if (blockIdx.x == 0) {
       // the quantized query, for callers that keep it (the codes are still in LDS)
-      if (p.q_codes_out && qh < Hi) {
-        const uint4* src = reinterpret_cast<const uint4*>(q_lds + qh * kQPitch + 32 * qc);
-        uint4* dst = reinterpret_cast<uint4*>(p.q_codes_out + (row * Hi + qh) * 128 + 32 * qc);
-        dst[0] = src[0];
-        dst[1] = src[1];
-        if (qc == 0) p.q_scales_out[row * Hi + qh] = qs_lds[qh];
+      if constexpr (FMT == kFp8) {
+        if (p.q_codes_out && qh < Hi) {
+          const uint4* src = reinterpret_cast<const uint4*>(q_lds + qh * QP + 32 * qc);
+          uint4* dst = reinterpret_cast<uint4*>(p.q_codes_out + (row * Hi + qh) * 128 + 32 * qc);
+          dst[0] = src[0];
+          dst[1] = src[1];
+          if (qc == 0) p.q_scales_out[row * Hi + qh] = qs_lds[qh];
+        }
+      } else {
+        if (p.q_codes_out && qh < Hi) {
+          *reinterpret_cast<uint4*>(p.q_codes_out + (row * Hi + qh) * 64 + 16 * qc) =
+              *reinterpret_cast<const uint4*>(q_lds + qh * QP + 16 * qc);
+          p.q_e8m0_out[(row * Hi + qh) * 4 + qc] = qe_lds[qh * 4 + qc];
+        }
       }
       if constexpr (APPEND) {
         // FP8-b128 latent entry (as pack_latent_row): threads t < nope/4 hold 4 nope
@@ -486,5 +548,52 @@ extern "C" int mzk_indexer_decode_fp8(const void* q_idx, const float* w, const u
     else indexer_scores_kernel<kFp8, 128, 2, true, false><<<grid, kWaves * 64, 0, s>>>(p);
   }
   MZK_LAUNCH_CHECK("indexer_decode_fp8");
+  return MZK_OK;
+}
+
+extern "C" int mzk_indexer_decode_mxfp4(const void* q_idx, const float* w, const uint8_t* k_packed,
+                                        const uint8_t* k_e8m0, int64_t B, int Hi, int Di, int64_t G,
+                                        int64_t k_batch_stride, const int64_t* positions, int ratio, float* scores,
+                                        int64_t score_stride, uint8_t* q_packed, uint8_t* q_e8m0, const void* kv,
+                                        int nope, int rope, uint8_t* win_cache, int64_t win_batch_entries,
+                                        int win_cap, void* stream) {
+  int rc = check_common(B, 1, Hi, Di, G, k_batch_stride, ratio, score_stride);
+  if (rc) return rc;
+  MZK_CHECK_ARG(Di == 128, "indexer_decode_mxfp4: the fused decode form needs Di = 128 (got %d)", Di);
+  MZK_CHECK_ARG(positions != nullptr, "indexer_decode_mxfp4: positions are required");
+  MZK_CHECK_ARG((q_packed == nullptr) == (q_e8m0 == nullptr), "indexer_decode_mxfp4: q_packed and q_e8m0 go together");
+  if (kv) {
+    MZK_CHECK_ARG(win_cache && win_cap >= 1 && win_batch_entries >= win_cap, "indexer_decode_mxfp4: bad window ring");
+    MZK_CHECK_ARG(nope >= 128 && nope % 128 == 0 && nope <= 4 * kWaves * 64 && rope >= 1 && rope <= kWaves * 64 &&
+                      rope % 2 == 0,
+                  "indexer_decode_mxfp4: latent %d+%d unsupported (nope a multiple of 128 up to 1024, rope even up to 256)",
+                  nope, rope);
+  }
+  if (B == 0) return MZK_OK;
+  MZK_CHECK_ARG(G >= 1, "indexer_decode_mxfp4: at least one key group is required");
+  MZK_CHECK_ARG(q_idx && w && k_packed && k_e8m0 && scores, "indexer_decode_mxfp4: null pointer");
+  MZK_CHECK_ARG(aligned16(q_idx) && aligned16(k_packed) && aligned16(q_packed) && aligned16(kv) && aligned16(win_cache),
+                "indexer_decode_mxfp4: q_idx, k_packed, q_packed, kv and the window cache must be 16-byte aligned");
+  IdxParams p = make_params(nullptr, nullptr, nullptr, w, k_packed, nullptr, k_e8m0, 1, Hi, G, k_batch_stride,
+                            positions, ratio, scores, score_stride);
+  p.q_raw = static_cast<const uint16_t*>(q_idx);
+  p.q_codes_out = q_packed;
+  p.q_e8m0_out = q_e8m0;
+  p.kv = static_cast<const uint16_t*>(kv);
+  p.nope = nope;
+  p.rope = rope;
+  p.win = win_cache;
+  p.win_batch_entries = win_batch_entries;
+  p.win_cap = win_cap;
+  dim3 grid(static_cast<unsigned>((G + kKeysPerWg - 1) / kKeysPerWg), static_cast<unsigned>(B));
+  hipStream_t s = as_stream(stream);
+  if (Hi <= 32) {
+    if (kv) indexer_scores_kernel<kMxfp4, 128, 1, true, true><<<grid, kWaves * 64, 0, s>>>(p);
+    else indexer_scores_kernel<kMxfp4, 128, 1, true, false><<<grid, kWaves * 64, 0, s>>>(p);
+  } else {
+    if (kv) indexer_scores_kernel<kMxfp4, 128, 2, true, true><<<grid, kWaves * 64, 0, s>>>(p);
+    else indexer_scores_kernel<kMxfp4, 128, 2, true, false><<<grid, kWaves * 64, 0, s>>>(p);
+  }
+  MZK_LAUNCH_CHECK("indexer_decode_mxfp4");
   return MZK_OK;
 }

@@ -14,13 +14,6 @@
 namespace mzk {
 namespace {
 
-constexpr float kInv6 = 1.0f / 6.0f;
-
-__device__ __forceinline__ float fp4_scale_from_amax(float amax, bool e4m3_scales) {
-  if (e4m3_scales) return e4m3_decode(e4m3_encode(div_rn(fmaxf(amax, 0x1.8p-7f /* 6*2^-9 */), 6.0f)));
-  return pow2_ceil(fmaxf(amax, 0x1.8p-124f /* 6*2^-126 */) * kInv6);
-}
-
 // ---- fake quant (value round trips) ------------------------------------------------
 
 template <int DT, bool FP4>

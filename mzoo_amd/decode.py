@@ -150,6 +150,11 @@ class SparseDecodeLayer:
             indexer.decode_fp8(q_idx, w.view(b, -1), self.k_codes, self.k_scales, compress_ratio=cfg.ratio,
                                positions=pos, out=self.scores, kv=kvc, win_cache=self.win, nope=cfg.nope,
                                rope=cfg.rope)
+        elif cfg.index_dim == 128:
+            # the same single launch for the MXFP4 index
+            indexer.decode_mxfp4(q_idx, w.view(b, -1), self.k_packed, self.k_e8m0, compress_ratio=cfg.ratio,
+                                 positions=pos, out=self.scores, kv=kvc, win_cache=self.win, nope=cfg.nope,
+                                 rope=cfg.rope)
         else:
             # window append + indexer-query quantization (one launch), then scores
             qc = q_idx.contiguous()

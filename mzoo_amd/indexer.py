@@ -173,6 +173,41 @@ def decode_fp8(q_idx: torch.Tensor, w: torch.Tensor, k_codes: torch.Tensor, k_sc
     return out
 
 
+def decode_mxfp4(q_idx: torch.Tensor, w: torch.Tensor, k_packed: torch.Tensor, k_e8m0: torch.Tensor, *,
+                 compress_ratio: int, positions: torch.Tensor, out: torch.Tensor | None = None,
+                 q_packed: torch.Tensor | None = None, q_e8m0: torch.Tensor | None = None,
+                 kv: torch.Tensor | None = None, win_cache: torch.Tensor | None = None, nope: int = 512,
+                 rope: int = 64) -> torch.Tensor:
+    """Decode-step MXFP4 indexer with the step's prologue fused in (one launch): q_idx bf16
+    [B,Hi,128] is quantized in the kernel (MXFP4, block 32, ue8m0 scales) and scored against
+    k_packed uint8 [B,Gcap,64] / k_e8m0 uint8 [B,Gcap,4] -> fp32 [B,1,Gcap].  Optionally
+    also writes the quantized query (q_packed uint8 [B,Hi,64] + q_e8m0 uint8 [B,Hi,4]) and
+    appends the new latent kv bf16 [B, nope+rope] to the window ring, as ``decode_fp8``."""
+    b, hi, di = q_idx.shape
+    gcap = k_packed.shape[1]
+    if q_idx.dtype != torch.bfloat16 or k_packed.shape != (b, gcap, di // 2) or k_e8m0.shape != (b, gcap, di // 32) \
+            or w.shape[-1] != hi or w.numel() != b * hi:
+        raise ValueError("decode_mxfp4: shape/dtype mismatch")
+    if (q_packed is None) != (q_e8m0 is None):
+        raise ValueError("decode_mxfp4: q_packed and q_e8m0 go together")
+    if kv is not None and (kv.dtype != torch.bfloat16 or kv.shape != (b, nope + rope) or win_cache is None):
+        raise ValueError("decode_mxfp4: kv must be bf16 [B, nope+rope] with a window cache")
+    _lib.require_gpu(q_idx, k_packed, positions)
+    out = _check_scores_out(b, 1, gcap, q_idx.device, out)
+    pos = torch.as_tensor(positions, device=q_idx.device).to(torch.int64).reshape(b).contiguous()  # [B] or [B,1]
+    for t in (q_packed, q_e8m0, win_cache):
+        if t is not None and not t.is_contiguous():
+            raise ValueError("decode_mxfp4: q_packed, q_e8m0 and win_cache must be contiguous")
+    qc = q_idx.contiguous()
+    kvc = None if kv is None else kv.contiguous()
+    wcap = 0 if win_cache is None else win_cache.shape[1]
+    _lib.call("mzk_indexer_decode_mxfp4", qc.data_ptr(), w.float().contiguous().data_ptr(),
+              k_packed.contiguous().data_ptr(), k_e8m0.contiguous().data_ptr(), b, hi, di, gcap, gcap, pos.data_ptr(),
+              compress_ratio, out.data_ptr(), out.stride(1), _lib.ptr(q_packed), _lib.ptr(q_e8m0), _lib.ptr(kvc),
+              nope, rope, _lib.ptr(win_cache), wcap, wcap, _lib.stream_of(qc))
+    return out
+
+
 def scores_mxfp4(q_packed: torch.Tensor, q_e8m0: torch.Tensor, w: torch.Tensor, k_packed: torch.Tensor,
                  k_e8m0: torch.Tensor, *, compress_ratio: int, positions=None, groups: int | None = None,
                  out: torch.Tensor | None = None) -> torch.Tensor:

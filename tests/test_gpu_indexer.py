@@ -249,3 +249,46 @@ def test_fused_decode_indexer_fp8(dev, b, hi, g, append):
     assert torch.equal(got, two)
     ref = OA.indexer_scores(qd, kd, w, 4, pos.view(b, 1))
     assert_scores_close(got, ref, OA.indexer_abs_scores(qd, kd, w, 4, pos.view(b, 1)))
+
+
+@pytest.mark.parametrize("b,hi,g,append", [(5, 64, 1000, True), (3, 20, 512, True), (4, 64, 2048, False)])
+def test_fused_decode_indexer_mxfp4(dev, b, hi, g, append):
+    """mzk_indexer_decode_mxfp4 = query MXFP4 quantization + window append + MXFP4 scores in
+    one launch: the packed query and its e8m0 scales, and the appended window entry, are
+    bit-exact against the oracle's quantizer / packer; the scores are bit-identical to the
+    two-launch path (mzk_indexer_scores_mxfp4 on the oracle-quantized query) and within
+    tolerance of the oracle's fp32 scores, with the group-causal mask."""
+    q, k, w = _inputs(b, 1, hi, 128, g, seed=2 * hi + g)
+    q = q[:, 0]                                                     # [B, Hi, 128]
+    q[0, 0, :6] = torch.tensor([0.0, -0.0, 1e-30, 3e-3, -6.0, 0.25])  # zeros, underflow, ties of the grid
+    q[1 % b, hi - 1] = 0                                             # an all-zero head (scale floor)
+    qp_ref, qe_ref = Q.quant_mxfp4(q.float().numpy())
+    kp, ke = Q.quant_mxfp4(k.float().numpy())
+    qd, kd = torch.from_numpy(Q.dequant_mxfp4(qp_ref, qe_ref)), torch.from_numpy(Q.dequant_mxfp4(kp, ke))
+    pos = torch.tensor([4 * g - 1, 37, 4 * g + 9, 0, 1000][:b], dtype=torch.int64)
+    wcap = 16
+    kv = torch.randn(b, 576, generator=torch.Generator().manual_seed(b + 1)).bfloat16()
+    win = torch.zeros(b, wcap, 656, dtype=torch.uint8, device=dev)
+    q_packed = torch.zeros(b, hi, 64, dtype=torch.uint8, device=dev)
+    q_e8m0 = torch.zeros(b, hi, 4, dtype=torch.uint8, device=dev)
+    kpd, ked = torch.from_numpy(kp).to(dev), torch.from_numpy(ke).to(dev)
+    got = MI.decode_mxfp4(q.to(dev), w[:, 0].to(dev), kpd, ked, compress_ratio=4, positions=pos.to(dev),
+                          q_packed=q_packed, q_e8m0=q_e8m0, kv=kv.to(dev) if append else None,
+                          win_cache=win if append else None)
+    assert np.array_equal(q_packed.cpu().numpy(), qp_ref)
+    assert np.array_equal(q_e8m0.cpu().numpy(), qe_ref)
+    wc = win.cpu().numpy()
+    if append:
+        want = Q.pack_latent_fp8_b128(kv.float().numpy())
+        for r in range(b):
+            assert np.array_equal(wc[r, int(pos[r]) % wcap], want[r])
+            others = [i for i in range(wcap) if i != int(pos[r]) % wcap]
+            assert not wc[r, others].any()
+    else:
+        assert not wc.any()
+    two = MI.scores_mxfp4(torch.from_numpy(qp_ref).reshape(b, 1, hi, 64).to(dev),
+                          torch.from_numpy(qe_ref).reshape(b, 1, hi, 4).to(dev), w.to(dev), kpd, ked,
+                          compress_ratio=4, positions=pos.view(b, 1).to(dev))
+    assert torch.equal(got, two)
+    ref = OA.indexer_scores(qd.unsqueeze(1), kd, w, 4, pos.view(b, 1))
+    assert_scores_close(got, ref, OA.indexer_abs_scores(qd.unsqueeze(1), kd, w, 4, pos.view(b, 1)))
