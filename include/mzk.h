@@ -208,6 +208,23 @@ int mzk_topk_workspace_bytes(int64_t rows, int64_t cols, int64_t* bytes);
 int mzk_topk_rows_ws(const float* scores, int64_t rows, int64_t cols, int64_t row_stride, int topk,
                      int32_t* out, int64_t out_stride, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Level one of the two-level candidate selection -- replaces select_candidate_blocks
+ * (owlet1/indexer.py:14-40; tickets/0009-indexer-hierarchical.md).  logits [rows, width]
+ * fp32 (row stride row_stride; unreachable positions already -inf), compress_lens [rows]
+ * int64 (the query's visible group count): block maxima over blocks of block_size
+ * positions (the tail block padded with -inf), the block holding position
+ * compress_lens-1 pinned to +inf, the top topk_blocks blocks whose score is above -inf
+ * (lowest block index first among equal scores; the reference leaves ties unspecified).
+ * Outputs (either may be NULL, not both): mask [rows, width] uint8 0/1 (row stride
+ * mask_stride) -- the reference's bool mask -- and block_idx_out [rows, topk_blocks] int32,
+ * the selected blocks ascending then -1 (the compact candidate list).  workspace:
+ * mzk_candidate_blocks_workspace_bytes, 16-byte aligned. */
+int mzk_candidate_blocks_workspace_bytes(int64_t rows, int64_t width, int block_size, int topk_blocks, int64_t* bytes);
+int mzk_candidate_blocks(const float* logits, int64_t rows, int64_t width, int64_t row_stride,
+                         const int64_t* compress_lens, int topk_blocks, int block_size, uint8_t* mask,
+                         int64_t mask_stride, int32_t* block_idx_out, void* workspace, int64_t workspace_bytes,
+                         void* stream);
+
 /* ---------------------------------------------------------------------------------
  * Piece 5: sparse shared-latent MQA attention
  * --------------------------------------------------------------------------------- */

@@ -42,6 +42,8 @@ _SIGS = {
     "mzk_topk_rows": [_P, _I64, _I64, _I64, _I32, _P, _I64, _P],
     "mzk_topk_workspace_bytes": [_I64, _I64, ctypes.POINTER(_I64)],
     "mzk_topk_rows_ws": [_P, _I64, _I64, _I64, _I32, _P, _I64, _P, _I64, _P],
+    "mzk_candidate_blocks_workspace_bytes": [_I64, _I64, _I32, _I32, ctypes.POINTER(_I64)],
+    "mzk_candidate_blocks": [_P, _I64, _I64, _I64, _P, _I32, _I32, _P, _I64, _P, _P, _I64, _P],
     "mzk_indexer_scores_fp8": [_P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P, _I64, _P],
     "mzk_indexer_decode_fp8": [_P, _P, _P, _P, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P, _I64, _P, _P, _P, _I32, _I32,
                                _P, _I64, _I32, _P],

@@ -831,6 +831,54 @@ int topk_multi_chunks(int64_t rows, int64_t cols) {
   return static_cast<int>((cols + kChunk - 1) / kChunk);
 }
 
+// ---- two-level candidate selection, level one (select_candidate_blocks) -------------
+//
+// owlet1/indexer.py:14-40: block maxima of the scores (blocks of block_size positions,
+// the tail block padded with -inf), the block holding the query's newest position
+// ((compress_len - 1) // block_size) pinned to +inf, the top topk_blocks blocks with a
+// score above -inf, expanded back to a per-position mask.  The top-k in between is
+// mzk_topk_rows (lowest block index first among equal block scores).
+
+// One thread per (row, block): the block maximum, or +inf for the newest (partial) block.
+__global__ void candidate_pool_kernel(const float* __restrict__ logits, int64_t rows, int64_t width,
+                                      int64_t row_stride, const int64_t* __restrict__ compress_lens, int block_size,
+                                      int64_t nb, float* __restrict__ block_scores) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= rows * nb) return;
+  const int64_t row = t / nb, blk = t - row * nb;
+  const float* src = logits + row * row_stride;
+  const int64_t p0 = blk * block_size;
+  const int64_t p1 = p0 + block_size < width ? p0 + block_size : width;
+  float m = -__builtin_huge_valf();
+  for (int64_t p = p0; p < p1; ++p) m = fmaxf(m, src[p]);
+  const int64_t cl = compress_lens[row];
+  const int64_t last = cl > 0 ? (cl - 1) / block_size : -1;  // floor division (cl = 0 pins nothing)
+  block_scores[t] = blk == last ? __builtin_huge_valf() : m;
+}
+
+// One workgroup per row: the selected blocks into an LDS bitmap, then mask[p] = bit(p / bs).
+__global__ void __launch_bounds__(256) candidate_expand_kernel(const int32_t* __restrict__ block_idx, int topk,
+                                                                int64_t width, int block_size, int nb,
+                                                                uint8_t* __restrict__ mask, int64_t mask_stride) {
+  extern __shared__ uint32_t bits[];  // nb bits
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int nwords = (nb + 31) / 32;
+  for (int i = tid; i < nwords; i += 256) bits[i] = 0u;
+  __syncthreads();
+  const int32_t* bi = block_idx + row * static_cast<int64_t>(topk);
+  for (int i = tid; i < topk; i += 256) {
+    const int b = bi[i];
+    if (b >= 0 && b < nb) atomicOr(&bits[b >> 5], 1u << (b & 31));
+  }
+  __syncthreads();
+  uint8_t* dst = mask + row * mask_stride;
+  for (int64_t p = tid; p < width; p += 256) {
+    const int64_t b = p / block_size;
+    dst[p] = static_cast<uint8_t>((bits[b >> 5] >> (b & 31)) & 1u);
+  }
+}
+
 }  // namespace
 }  // namespace mzk
 
@@ -895,5 +943,55 @@ extern "C" int mzk_topk_rows_ws(const float* scores, int64_t rows, int64_t cols,
   topk_chunk_select_write_kernel<<<grid, kThreads, 0, s>>>(scores, row_stride, G, topk, nch, hist, above, sel, cand,
                                                             out, out_stride);
   MZK_LAUNCH_CHECK("topk_rows_ws");
+  return MZK_OK;
+}
+
+extern "C" int mzk_candidate_blocks_workspace_bytes(int64_t rows, int64_t width, int block_size, int topk_blocks,
+                                                    int64_t* bytes) {
+  MZK_CHECK_ARG(rows >= 0 && width >= 0 && block_size >= 1 && topk_blocks >= 0 && bytes != nullptr,
+                "candidate_blocks_workspace_bytes: bad arguments");
+  const int64_t nb = (width + block_size - 1) / block_size;
+  int64_t tk = 0;
+  MZK_CHECK_ARG(mzk_topk_workspace_bytes(rows, nb, &tk) == MZK_OK, "candidate_blocks_workspace_bytes: bad sizes");
+  // block scores [rows, nb] fp32 | block indices [rows, topk_blocks] int32 | top-k workspace
+  *bytes = round16(rows * nb * 4) + round16(rows * static_cast<int64_t>(topk_blocks) * 4) + tk;
+  return MZK_OK;
+}
+
+extern "C" int mzk_candidate_blocks(const float* logits, int64_t rows, int64_t width, int64_t row_stride,
+                                    const int64_t* compress_lens, int topk_blocks, int block_size, uint8_t* mask,
+                                    int64_t mask_stride, int32_t* block_idx_out, void* workspace,
+                                    int64_t workspace_bytes, void* stream) {
+  MZK_CHECK_ARG(rows >= 0 && width >= 0 && topk_blocks >= 0 && block_size >= 1 && block_size <= (1 << 20),
+                "candidate_blocks: bad sizes");
+  MZK_CHECK_ARG(row_stride >= width && (mask == nullptr || mask_stride >= width), "candidate_blocks: bad strides");
+  if (rows == 0 || width == 0) return MZK_OK;
+  const int64_t nb = (width + block_size - 1) / block_size;
+  MZK_CHECK_ARG(nb <= (int64_t(1) << 24) && rows <= 0x7fffffff, "candidate_blocks: too many blocks");
+  MZK_CHECK_ARG(logits && compress_lens && (mask || block_idx_out), "candidate_blocks: null pointer");
+  int64_t need = 0;
+  mzk_candidate_blocks_workspace_bytes(rows, width, block_size, topk_blocks, &need);
+  MZK_CHECK_ARG(workspace && workspace_bytes >= need && aligned16(workspace),
+                "candidate_blocks: needs a 16-byte aligned workspace of %lld bytes", (long long)need);
+  hipStream_t s = as_stream(stream);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  float* bscore = reinterpret_cast<float*>(ws);
+  int32_t* bidx = block_idx_out ? block_idx_out : reinterpret_cast<int32_t*>(ws + round16(rows * nb * 4));
+  void* tkws = ws + round16(rows * nb * 4) + round16(rows * static_cast<int64_t>(topk_blocks) * 4);
+  const int64_t tk_bytes = need - (round16(rows * nb * 4) + round16(rows * static_cast<int64_t>(topk_blocks) * 4));
+  const int64_t n = rows * nb;
+  candidate_pool_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(logits, rows, width, row_stride,
+                                                                                compress_lens, block_size, nb, bscore);
+  if (topk_blocks > 0) {
+    const int rc = mzk_topk_rows_ws(bscore, rows, nb, nb, topk_blocks, bidx, topk_blocks, tkws, tk_bytes, stream);
+    if (rc) return rc;
+  }
+  if (mask) {
+    const size_t lds = static_cast<size_t>((nb + 31) / 32) * 4;
+    MZK_CHECK_ARG(lds <= 64 * 1024, "candidate_blocks: %lld blocks exceed the mask kernel's LDS bitmap", (long long)nb);
+    candidate_expand_kernel<<<static_cast<unsigned>(rows), 256, lds, s>>>(bidx, topk_blocks, width, block_size,
+                                                                           static_cast<int>(nb), mask, mask_stride);
+  }
+  MZK_LAUNCH_CHECK("candidate_blocks");
   return MZK_OK;
 }

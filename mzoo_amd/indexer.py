@@ -76,6 +76,37 @@ def topk(scores: torch.Tensor, k: int, out: torch.Tensor | None = None,
 _topk_rows = topk
 
 
+def select_candidate_blocks(logits: torch.Tensor, compress_lens: torch.Tensor, topk_blocks: int,
+                            block_size: int) -> torch.Tensor:
+    """Level one of the two-level top-k (reference ``select_candidate_blocks``): keep the
+    ``topk_blocks`` highest-scoring blocks of ``block_size`` positions per query, the block
+    holding the query's newest position pinned in; bool mask shaped like ``logits``.
+    ``compress_lens`` carries a trailing axis ([..., 1]) as in the reference.  Among equal
+    block scores the lower block index wins (the reference leaves ties unspecified)."""
+    _lib.require_gpu(logits, compress_lens)
+    if logits.dtype != torch.float32:
+        raise TypeError(f"select_candidate_blocks: logits must be float32, got {logits.dtype}")
+    width = logits.shape[-1]
+    lead = logits.shape[:-1]
+    rows = 1
+    for d in lead:
+        rows *= d
+    cl = torch.as_tensor(compress_lens, device=logits.device).to(torch.int64).expand(*lead, 1).reshape(rows)
+    cl = cl.contiguous()
+    flat = logits.reshape(rows, width)
+    if width and flat.stride(-1) != 1:
+        flat = flat.contiguous()
+    mask = torch.empty(*lead, width, dtype=torch.bool, device=logits.device)
+    if rows == 0 or width == 0:
+        return mask
+    n = ctypes.c_int64(0)
+    _lib.call("mzk_candidate_blocks_workspace_bytes", rows, width, block_size, topk_blocks, ctypes.byref(n))
+    ws = torch.empty(max(n.value, 16), dtype=torch.uint8, device=logits.device)
+    _lib.call("mzk_candidate_blocks", flat.data_ptr(), rows, width, flat.stride(0), cl.data_ptr(), topk_blocks,
+              block_size, mask.data_ptr(), width, None, ws.data_ptr(), ws.numel(), _lib.stream_of(logits))
+    return mask
+
+
 def _check_scores_out(b, s, g, device, out):
     if out is None:
         return torch.empty(b, s, g, dtype=torch.float32, device=device)

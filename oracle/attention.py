@@ -12,6 +12,8 @@ torch fp32 on the CPU, following ``src/mzoo/layers/attn/golden_ref.py``:
                          this build's tie rule made explicit: among equal scores the lower
                          index wins, and the kept indices are listed in ascending order
                          followed by the ``-1`` padding
+* ``select_candidate_blocks`` -- ``owlet1/indexer.py:14-40`` (level one of the two-level
+                         top-k), its top-k over block scores with the same tie rule
 * ``attend_entries``  -- one query row against an explicit list of K==V latent entries
                          plus a sink: what ``eager_attention_forward``
                          (``owlet1/attention.py:42-71``) computes for one decode row once
@@ -123,6 +125,31 @@ def topk_indices(scores, topk: int) -> np.ndarray:
         order.sort()
         out[r, :len(order)] = order
     return out.reshape(*lead, topk)
+
+
+def select_candidate_blocks(logits, compress_lens, topk_blocks: int, block_size: int) -> np.ndarray:
+    """owlet1/indexer.py:14-40: block maxima of ``logits`` [..., W] over blocks of
+    ``block_size`` (the tail padded with -inf), the block ``(compress_lens - 1) //
+    block_size`` (floor division, so a length of 0 pins nothing) set to +inf, the top
+    ``min(topk_blocks, blocks)`` blocks whose score is above -inf (``topk_indices``: lower
+    block first among equals), expanded to a bool mask [..., W].  ``compress_lens`` carries
+    a trailing axis ([..., 1]) as in the reference."""
+    x = np.asarray(logits, np.float32)
+    w = x.shape[-1]
+    lead = x.shape[:-1]
+    nb = -(-w // block_size)
+    pad = np.full((*lead, nb * block_size - w), -np.inf, np.float32)
+    blocks = np.concatenate([x, pad], -1).reshape(*lead, nb, block_size).max(-1)
+    cl = np.broadcast_to(np.asarray(compress_lens, np.int64), (*lead, 1))
+    last = (cl - 1) // block_size
+    blocks = np.where(np.arange(nb) == last, np.float32(np.inf), blocks)
+    sel = topk_indices(blocks, min(topk_blocks, nb))
+    keep = np.zeros((*lead, nb), bool)
+    flat_keep, flat_sel = keep.reshape(-1, nb), sel.reshape(-1, sel.shape[-1])
+    for r in range(flat_sel.shape[0]):
+        chosen = flat_sel[r][flat_sel[r] >= 0]
+        flat_keep[r, chosen] = True
+    return np.repeat(keep, block_size, axis=-1)[..., :w]
 
 
 def attend_entries(q, entries, sinks=None):

@@ -292,3 +292,26 @@ def test_fused_decode_indexer_mxfp4(dev, b, hi, g, append):
     assert torch.equal(got, two)
     ref = OA.indexer_scores(qd.unsqueeze(1), kd, w, 4, pos.view(b, 1))
     assert_scores_close(got, ref, OA.indexer_abs_scores(qd.unsqueeze(1), kd, w, 4, pos.view(b, 1)))
+
+
+@pytest.mark.parametrize("b,s,t,bs,k,kind", [(2, 3, 13, 8, 1, "distinct"), (2, 5, 1000, 8, 20, "ties"),
+                                             (1, 4, 16384, 8, 2048, "distinct"), (1, 2, 65536, 8, 2048, "ties"),
+                                             (3, 2, 37, 4, 50, "distinct"), (1, 3, 40, 8, 2, "all_masked")])
+def test_select_candidate_blocks(dev, b, s, t, bs, k, kind):
+    """Level one of the two-level top-k (owlet1/indexer.py:14-40) against the oracle: bool
+    mask equal, with the newest partial block pinned, unreachable blocks dropped, T not a
+    multiple of the block size and the ticket-0009 sizes; ties resolve to the lower block
+    (the same rule in both)."""
+    gen = torch.Generator().manual_seed(b * 7 + t)
+    logits = torch.randn(b, s, t, generator=gen)
+    if kind == "ties":
+        logits = torch.round(logits * 4) / 4
+    pos = torch.randint(0, 4 * t, (b, s), generator=gen)
+    lens = ((pos + 1) // 4).clamp(max=t).unsqueeze(-1)
+    if kind == "all_masked":
+        lens[0, 0, 0] = 0
+    logits = logits.masked_fill(torch.arange(t).view(1, 1, -1) >= lens, float("-inf"))
+    got = MI.select_candidate_blocks(logits.to(dev), lens.to(dev), k, bs)
+    assert got.dtype == torch.bool and got.shape == logits.shape
+    want = OA.select_candidate_blocks(logits.numpy(), lens.numpy(), k, bs)
+    assert np.array_equal(got.cpu().numpy(), want)

@@ -176,3 +176,76 @@ def test_topk_brute_force_with_ties(seed):
 
 def test_topk_empty():
     assert OA.topk_indices(np.zeros((2, 0), np.float32), 3).tolist() == [[-1] * 3] * 2
+
+
+# ---- select_candidate_blocks (owlet1/indexer.py:14-40) ------------------------------------
+
+def _torch_candidate_blocks(logits, compress_lens, topk_blocks, block_size):
+    """The reference's steps in torch ops (pad/amax/masked_fill/topk/scatter), valid where
+    no two block scores tie at the selection boundary."""
+    import torch.nn.functional as F
+    width = logits.size(-1)
+    sc = F.pad(logits, (0, -width % block_size), value=float("-inf"))
+    sc = sc.unflatten(-1, (-1, block_size)).amax(dim=-1)
+    nb = sc.size(-1)
+    last = (compress_lens - 1) // block_size
+    sc = sc.masked_fill(torch.arange(nb).view(-1) == last, torch.inf)
+    top = sc.topk(min(topk_blocks, nb), dim=-1)
+    keep = torch.zeros_like(sc, dtype=torch.bool).scatter_(-1, top.indices, top.values > float("-inf"))
+    return keep.repeat_interleave(block_size, dim=-1)[..., :width]
+
+
+@pytest.mark.parametrize("b,s,t,bs,k", [(2, 3, 13, 8, 1), (1, 4, 64, 8, 3), (2, 2, 1000, 8, 20), (1, 3, 37, 4, 50)])
+def test_candidate_blocks_match_torch_formulation(b, s, t, bs, k):
+    gen = torch.Generator().manual_seed(b * 100 + t)
+    logits = torch.randn(b, s, t, generator=gen)          # distinct block maxima: no ties
+    pos = torch.randint(0, 4 * t, (b, s), generator=gen)
+    lens = ((pos + 1) // 4).clamp(max=t).unsqueeze(-1)
+    logits = logits.masked_fill(torch.arange(t).view(1, 1, -1) >= lens, float("-inf"))
+    want = _torch_candidate_blocks(logits, lens, k, bs).numpy()
+    got = OA.select_candidate_blocks(logits.numpy(), lens.numpy(), k, bs)
+    assert np.array_equal(got, want)
+
+
+def test_candidate_blocks_ticket_cases():
+    """tickets/0009-indexer-hierarchical.md acceptance cases: T not a multiple of 8, fewer
+    reachable blocks than topk_blocks (only reachable ones kept), the newest (partial)
+    block pinned even when it scores lowest, and when it also scores highest."""
+    ninf = float("-inf")
+    # T = 13, block 8: two blocks; newest position 12 is in block 1, which scores lowest
+    x = np.array([[5.0] * 8 + [1.0] * 5], np.float32)
+    got = OA.select_candidate_blocks(x, np.array([[13]]), 1, 8)
+    assert got.tolist() == [[False] * 8 + [True] * 5]      # the pinned partial block wins
+    # fewer reachable blocks than topk_blocks: unreachable (-inf) blocks are never kept
+    x = np.array([[3.0, 1.0, ninf, ninf, ninf, ninf]], np.float32)
+    got = OA.select_candidate_blocks(x, np.array([[2]]), 3, 2)
+    assert got.tolist() == [[True, True, False, False, False, False]]
+    # newest block also the highest: kept once, the next best fills the other slot
+    x = np.array([[1.0, 2.0, 9.0, 3.0, 4.0, 8.0]], np.float32)
+    got = OA.select_candidate_blocks(x, np.array([[6]]), 2, 2)
+    assert got.tolist() == [[False, False, True, True, True, True]]
+    # nothing visible yet (length 0): nothing is pinned and every block is -inf
+    x = np.full((1, 5), ninf, np.float32)
+    assert not OA.select_candidate_blocks(x, np.array([[0]]), 4, 2).any()
+
+
+def test_candidate_blocks_invariants():
+    gen = np.random.default_rng(7)
+    for _ in range(20):
+        t, bs = int(gen.integers(1, 200)), int(gen.integers(1, 9))
+        k = int(gen.integers(1, 12))
+        x = np.round(gen.standard_normal((3, t)) * 4).astype(np.float32)    # ties
+        lens = gen.integers(0, t + 1, (3, 1))
+        x = np.where(np.arange(t) < lens, x, -np.inf).astype(np.float32)
+        m = OA.select_candidate_blocks(x, lens, k, bs)
+        nb = -(-t // bs)
+        for r in range(3):
+            kept = {p // bs for p in range(t) if m[r, p]}
+            # a block is kept whole or not at all
+            assert all(m[r, p] == ((p // bs) in kept) for p in range(t))
+            reachable = {j for j in range(nb) if np.isfinite(x[r, j * bs:(j + 1) * bs]).any()}
+            if lens[r, 0] > 0:
+                last = (lens[r, 0] - 1) // bs
+                assert last in kept
+                reachable.add(last)
+            assert kept <= reachable and len(kept) == min(k, nb, len(reachable))
