@@ -6,8 +6,12 @@ one token per row for B=32 rows at context 32768: bf16 queries, 128 heads over t
 compressed entries (ratio 4), top-2048, sliding window 128, per-head sink.  A "step" is one
 replay of a HIP graph holding ``SparseDecodeLayer.step`` of --layers (default 8)
 consecutive layers, each with its own caches and inputs, as a model's decode graph holds its
-layers: per layer the window append, indexer-query quantization, indexer scores, top-k,
-sparse MQA (split-KV) and the split merge.  Distinct layers keep one layer's working set
+layers: per layer the new token's kv RMSNorm + RoPE + window append, the indexer query's
+RoPE + quantization and the indexer scores (one launch), top-k, sparse MQA with the query's
+RoPE on load (split-KV), and the split merge with the output's inverse RoPE -- the
+per-token work of ``DeepseekV41Attention.forward`` between the projections
+(``--prologue rotated`` takes already-rotated q / q_idx / latent instead, as the kernels'
+reference signatures do).  Distinct layers keep one layer's working set
 (about 90 MB) from being served out of the last-level cache on the next step.  value =
 B x layers / replay time (token-rows through one attention layer per second); ms_per_step
 is per layer.  Inputs are synthetic and resident in HBM before timing starts.
@@ -67,6 +71,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--nsplit", type=int, default=0, help="attention splits per row (0: the config's default)")
     ap.add_argument("--layers", type=int, default=8, help="distinct attention layers in the replayed graph")
+    ap.add_argument("--prologue", choices=["fused", "rotated"], default="fused",
+                    help="fused: unrotated q / q_idx and the raw kv projection, norm and RoPE in the step's "
+                         "launches; rotated: inputs already normed and rotated")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline time budget")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--stage-iters", type=int, default=0, help="launches per stage timing (0: max(steps, 50))")
@@ -76,10 +83,25 @@ def parse():
     return ap.parse_args()
 
 
-def build_layer(torch, dev, nsplit=0, seed=None, config=2):
+ROPE_THETA, COMPRESS_ROPE_THETA = 10000.0, 160000.0
+
+
+def rope_inputs(torch, dev, positions):
+    """bf16 cos / sin [B, 32] of the main and the compress RoPE at `positions` (the
+    model-level position_embeddings and the indexer's tables)."""
+    out = []
+    for theta in (ROPE_THETA, COMPRESS_ROPE_THETA):
+        inv = 1.0 / (theta ** (torch.arange(0, 64, 2, dtype=torch.float32) / 64))
+        f = torch.as_tensor(positions, dtype=torch.float32)[:, None] * inv
+        out += [f.cos().bfloat16().to(dev), f.sin().bfloat16().to(dev)]
+    return tuple(out)
+
+
+def build_layer(torch, dev, nsplit=0, seed=None, config=2, fused=True):
     """A decode layer of BASELINE config `config` (2, 4 or 5) with synthetic history: the
     window ring holds tokens ctx-129 .. ctx-2, every compressed group is published, and the
-    step decodes the token at position ctx-1 (every group visible)."""
+    step decodes the token at position ctx-1 (every group visible).  With `fused` the
+    inputs end with the four RoPE tables and the layer holds a kv norm weight."""
     from mzoo_amd.decode import DecodeConfig, SparseDecodeLayer
     c = DECODE[config]
     cfg = DecodeConfig(batch=c["batch"], heads=128, nope=512, rope=64, index_heads=64, index_dim=128, ratio=4,
@@ -89,7 +111,8 @@ def build_layer(torch, dev, nsplit=0, seed=None, config=2):
     gen = torch.Generator(device=dev).manual_seed(c["seed"] if seed is None else seed)
     rnd = lambda *shape: torch.randn(*shape, generator=gen, device=dev)  # noqa: E731
     sinks = rnd(cfg.heads)
-    layer = SparseDecodeLayer(cfg, dev, sinks=sinks)
+    kv_w = (1.0 + 0.1 * rnd(cfg.dim)).bfloat16() if fused else None
+    layer = SparseDecodeLayer(cfg, dev, sinks=sinks, kv_norm_weight=kv_w)
     b, d = cfg.batch, cfg.dim
     layer.fill_window(rnd(b, cfg.window, d).bfloat16(), ctx - 2)
     # groups in chunks (bounds the staging buffers of the larger configs)
@@ -104,7 +127,13 @@ def build_layer(torch, dev, nsplit=0, seed=None, config=2):
     kv = rnd(b, d).bfloat16()
     q_idx = rnd(b, cfg.index_heads, cfg.index_dim).bfloat16()
     w = rnd(b, cfg.index_heads) * cfg.index_heads ** -0.5
-    return layer, (q, kv, q_idx, w), sinks
+    rope = rope_inputs(torch, dev, [ctx - 1] * b) if fused else ()
+    return layer, (q, kv, q_idx, w) + rope, sinks
+
+
+def run_step(layer, inp):
+    """``SparseDecodeLayer.step`` on bench inputs (the RoPE tables, if any, last)."""
+    return layer.step(*inp[:4], rope=inp[4:] if len(inp) > 4 else None)
 
 
 def time_launches(torch, fn, iters):
@@ -130,12 +159,12 @@ def capture_layers(torch, layers, inputs):
     with torch.cuda.stream(side):
         for _ in range(2):
             for layer, st in zip(layers, statics):
-                layer.step(*st)
+                run_step(layer, st)
     torch.cuda.current_stream().wait_stream(side)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for layer, st in zip(layers, statics):
-            layer.step(*st)
+            run_step(layer, st)
     return g, statics
 
 
@@ -173,11 +202,26 @@ def stage_fns(torch, layer, inputs):
     from mzoo_amd import _lib, indexer
     cfg = layer.cfg
     b = cfg.batch
-    q, kv, q_idx, w = inputs
+    q, kv, q_idx, w = inputs[:4]
+    rope = inputs[4:]
     ws = layer.workspace
     st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
     fns = {}
-    if cfg.index_format == "fp8":
+    fp8 = cfg.index_format == "fp8"
+    if rope:
+        cos, sin, icos, isin = rope
+
+        def indexer_fused():
+            # kv RMSNorm + RoPE + window append, query RoPE + quantization, scores: one launch
+            _lib.call("mzk_indexer_decode_fused", 0 if fp8 else 1, q_idx.data_ptr(), w.data_ptr(),
+                      (layer.k_codes if fp8 else layer.k_packed).data_ptr(),
+                      (layer.k_scales if fp8 else layer.k_e8m0).data_ptr(), b, cfg.index_heads, cfg.index_dim,
+                      cfg.max_groups, cfg.max_groups, layer.positions.data_ptr(), cfg.ratio, layer.scores.data_ptr(),
+                      cfg.max_groups, None, None, icos.data_ptr(), isin.data_ptr(), 64, kv.data_ptr(),
+                      layer.kv_norm_weight.data_ptr(), layer.kv_norm_eps, cos.data_ptr(), sin.data_ptr(), cfg.nope,
+                      cfg.rope, layer.win.data_ptr(), cfg.window, cfg.window, st())
+        fns["indexer_decode_fp8" if fp8 else "indexer_decode_mxfp4"] = indexer_fused
+    elif fp8:
         def indexer_decode():
             # window append + indexer-query quantization + FP8 scores: the step's first launch
             _lib.call("mzk_indexer_decode_fp8", q_idx.data_ptr(), w.data_ptr(), layer.k_codes.data_ptr(),
@@ -200,16 +244,26 @@ def stage_fns(torch, layer, inputs):
     def attn():
         # the split-KV attention kernel alone: with no `out` the entry point writes the
         # split partials into the workspace and launches nothing else
-        _lib.call("mzk_sparse_mqa", q.data_ptr(), b, 1, cfg.heads, cfg.dim, 1, cfg.nope, layer.positions.data_ptr(),
-                  layer.win.data_ptr(), cfg.window, cfg.window, cfg.window,
-                  None if coarse is None else coarse.data_ptr(), cfg.coarse_groups, cfg.coarse_groups,
-                  max(cfg.coarse_ratio, 1), layer.main.data_ptr(), cfg.max_groups, cfg.max_groups,
-                  layer.idx.data_ptr(), cfg.topk, cfg.topk, layer.sinks.data_ptr(), cfg.nsplit, ws.data_ptr(),
-                  ws.numel() * ws.element_size(), None, None, st())
+        args = (q.data_ptr(), b, 1, cfg.heads, cfg.dim, 1, cfg.nope, layer.positions.data_ptr(),
+                layer.win.data_ptr(), cfg.window, cfg.window, cfg.window,
+                None if coarse is None else coarse.data_ptr(), cfg.coarse_groups, cfg.coarse_groups,
+                max(cfg.coarse_ratio, 1), layer.main.data_ptr(), cfg.max_groups, cfg.max_groups,
+                layer.idx.data_ptr(), cfg.topk, cfg.topk, layer.sinks.data_ptr(), cfg.nsplit, ws.data_ptr(),
+                ws.numel() * ws.element_size(), None, None)
+        if rope:
+            _lib.call("mzk_sparse_mqa_rope", *args, rope[0].data_ptr(), rope[1].data_ptr(), cfg.rope, st())
+        else:
+            _lib.call("mzk_sparse_mqa", *args, st())
     fns["sparse_mqa"] = attn
-    fns["sparse_mqa_combine"] = lambda: _lib.call(
-        "mzk_sparse_mqa_combine", ws.data_ptr(), b, 1, cfg.heads, cfg.dim, cfg.nsplit, layer.sinks.data_ptr(),
-        layer.out.data_ptr(), layer.lse.data_ptr(), st())
+    if rope:
+        fns["sparse_mqa_combine"] = lambda: _lib.call(
+            "mzk_sparse_mqa_combine_rope", ws.data_ptr(), b, 1, cfg.heads, cfg.dim, cfg.nsplit,
+            layer.sinks.data_ptr(), rope[0].data_ptr(), rope[1].data_ptr(), cfg.rope, layer.out.data_ptr(),
+            layer.lse.data_ptr(), st())
+    else:
+        fns["sparse_mqa_combine"] = lambda: _lib.call(
+            "mzk_sparse_mqa_combine", ws.data_ptr(), b, 1, cfg.heads, cfg.dim, cfg.nsplit, layer.sinks.data_ptr(),
+            layer.out.data_ptr(), layer.lse.data_ptr(), st())
     return fns
 
 
@@ -219,10 +273,13 @@ def cpu_baseline(torch, layer, inputs, budget_s, rows=None):
     all) of the batch, on this host's cores; median of repeated steps."""
     from mzoo_amd import quant
     from oracle import attention as OA
+    from oracle import compressor as OC
     from oracle import quant as OQ
     cfg = layer.cfg
     rows = list(range(cfg.batch)) if rows is None else rows
-    q, kv, q_idx, w = (t.float().cpu()[rows] for t in inputs)
+    q, kv, q_idx, w = (t.float().cpu()[rows] for t in inputs[:4])
+    tabs = [t.float().cpu()[rows].numpy() for t in inputs[4:]]
+    kv_w = None if layer.kv_norm_weight is None else layer.kv_norm_weight.float().cpu().numpy()
     win = quant.unpack_latent_fp8_b128(layer.win[rows], dtype=torch.float32).cpu()
     main = quant.unpack_latent_fp8_b128(layer.main[rows], dtype=torch.float32).cpu()
     coarse = None
@@ -239,17 +296,26 @@ def cpu_baseline(torch, layer, inputs, budget_s, rows=None):
     threads = torch.get_num_threads()
 
     def step():
+        qx, qi = q, q_idx
+        if tabs:
+            # the fused prologue: query / indexer-query RoPE, the new latent's norm + RoPE + packing
+            cos, sin, icos, isin = tabs
+            qx = torch.from_numpy(OC.rope(q.numpy(), cos[:, None], sin[:, None], dtype="bfloat16"))
+            qi = torch.from_numpy(OC.rope(q_idx.numpy(), icos[:, None], isin[:, None], dtype="bfloat16"))
+            OQ.pack_latent_fp8_b128(OC.decode_kv_latent(kv.numpy(), kv_w, layer.kv_norm_eps, cos, sin))
         if cfg.index_format == "fp8":
-            qd = torch.from_numpy(OQ.fake_quant_fp8_block(q_idx.numpy(), cfg.index_dim))
+            qd = torch.from_numpy(OQ.fake_quant_fp8_block(qi.numpy(), cfg.index_dim))
         else:
-            qd = torch.from_numpy(OQ.fake_quant_fp4_block(q_idx.numpy(), 32))
+            qd = torch.from_numpy(OQ.fake_quant_fp4_block(qi.numpy(), 32))
         sc = OA.indexer_scores(qd.unsqueeze(1), kd, w.unsqueeze(1), cfg.ratio, positions)
         idx = torch.from_numpy(OA.topk_indices(sc[:, 0], cfg.topk))
         toks = torch.arange(pos - cfg.window + 1, pos + 1) % cfg.window
         for i in range(len(rows)):
             parts = [win[i, toks]] + ([coarse[i, :nc]] if coarse is not None else [])
             ents = torch.cat(parts + [main[i, idx[i][idx[i] >= 0]]])
-            OA.attend_entries(q[i], ents, sinks)
+            o = OA.attend_entries(qx[i], ents, sinks)[0]
+            if tabs:
+                OC.rope(o.numpy(), tabs[0][i], tabs[1][i], inverse=True, dtype="bfloat16")
 
     times = []
     t_start = time.perf_counter()
@@ -261,7 +327,8 @@ def cpu_baseline(torch, layer, inputs, budget_s, rows=None):
     med = times[len(times) // 2]
     entries = cfg.window + nc + cfg.topk
     return {"value": len(rows) / med, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"decode step of {len(rows)} of {cfg.batch} rows ({cfg.index_format} indexer over "
+            "sample": f"decode step of {len(rows)} of {cfg.batch} rows ("
+                      f"{'kv norm + RoPE, q / q_idx RoPE, ' if tabs else ''}{cfg.index_format} indexer over "
                       f"{cfg.max_groups} keys, top-{cfg.topk}, attention over {entries} entries x {cfg.heads} heads), "
                       f"fp32 torch on dequantized caches, median of {len(times)} steps"}
 
@@ -290,7 +357,9 @@ def roofline(kind, flops, nbytes, t_us, peak_tflops=BF16_PEAK_TFLOPS):
 def run_decode(torch, dev, args):
     c = DECODE[args.config]
     nl = max(1, args.layers)
-    built = [build_layer(torch, dev, args.nsplit, seed=c["seed"] + i, config=args.config) for i in range(nl)]
+    fused = args.prologue == "fused"
+    built = [build_layer(torch, dev, args.nsplit, seed=c["seed"] + i, config=args.config, fused=fused)
+             for i in range(nl)]
     layers = [b_[0] for b_ in built]
     inputs_all = [b_[1] for b_ in built]
     layer, inputs = layers[0], inputs_all[0]
@@ -351,7 +420,10 @@ def run_decode(torch, dev, args):
         "config": {"workload": c["text"], "batch": cfg.batch, "context": c["ctx"], "heads": cfg.heads,
                    "latent": "512+64", "index": f"64x128 {cfg.index_format}", "topk": cfg.topk,
                    "window": cfg.window, "coarse": nc, "nsplit": cfg.nsplit, "graph_layers": nl,
-                   "step": "per attention layer, inside a graph replay of graph_layers layers"},
+                   "step": "per attention layer, inside a graph replay of graph_layers layers",
+                   "prologue": ("fused: kv RMSNorm + RoPE + window append, q / q_idx RoPE and the output's "
+                                "inverse RoPE inside the step's launches") if fused else
+                               "rotated: q, q_idx and the new latent arrive normed and rotated"},
         "roofline": roof,
         "cpu_baseline": cpu,
         "stages_us": stages,

@@ -181,6 +181,28 @@ int mzk_indexer_decode_mxfp4(const void* q_idx, const float* w, const uint8_t* k
                              int win_cap, void* stream);
 
 /* bf16 q [rows, Hi, Di] and k [B, G, Di] -- the contract of layers/attn/indexer/fwd.py:112. */
+/* The decode step's whole per-token prologue and its indexer in one launch
+ * (q_format 0: FP8 as mzk_indexer_decode_fp8, k_scales fp32 [B, kbs], q_scales fp32 [B, Hi];
+ * 1: MXFP4 as mzk_indexer_decode_mxfp4, k_scales = e8m0 [B, kbs, 4], q_scales = e8m0
+ * [B, Hi, 4]).  Replaces, for one new token per row (owlet1/attention.py:150-155 and
+ * owlet1/indexer.py:126-133):
+ *   q_idx bf16 [B, Hi, 128] unrotated -> apply_rotary_pos_emb on its trailing q_rope_dim
+ *     channels (32, 64, 96 or 128) with q_cos / q_sin bf16 [B, q_rope_dim/2] (the compress
+ *     RoPE) -> quantized and scored as the two entries above;
+ *   kv bf16 [B, 576] (the wkv projection) -> DeepseekV41RMSNorm (kv_weight bf16 [576],
+ *     kv_eps; sum of squares in 64 lane partials combined by an xor butterfly) -> RoPE of
+ *     channels 512..575 with kv_cos / kv_sin bf16 [B, 32] -> FP8-b128 entry (as
+ *     mzk_pack_latent_fp8_b128) at ring slot b*win_batch_entries + positions[b] % win_cap.
+ * nope / rope must be 512 / 64.  q_idx, k_codes, q_codes, q_cos, q_sin 16-byte aligned. */
+int mzk_indexer_decode_fused(int q_format, const void* q_idx, const float* w, const uint8_t* k_codes,
+                             const void* k_scales, int64_t B, int Hi, int Di, int64_t G,
+                             int64_t k_batch_stride, const int64_t* positions, int ratio,
+                             float* scores, int64_t score_stride, uint8_t* q_codes, void* q_scales,
+                             const void* q_cos, const void* q_sin, int q_rope_dim, const void* kv,
+                             const void* kv_weight, float kv_eps, const void* kv_cos,
+                             const void* kv_sin, int nope, int rope, uint8_t* win_cache,
+                             int64_t win_batch_entries, int win_cap, void* stream);
+
 int mzk_indexer_scores_bf16(const void* q, const float* w, const void* k, int64_t B, int64_t S,
                             int Hi, int Di, int64_t G, int64_t k_batch_stride,
                             const int64_t* positions, int ratio, float* scores,
@@ -263,6 +285,28 @@ int mzk_sparse_mqa(const void* q, int64_t B, int64_t S, int H, int D, int fmt, i
  * owlet1/attention.py:64-70 over all entries). */
 int mzk_sparse_mqa_combine(const float* workspace, int64_t B, int64_t S, int H, int D,
                            int nsplit, const float* sinks, void* out, float* lse, void* stream);
+
+/* mzk_sparse_mqa with the query's RoPE and the output's inverse RoPE fused in
+ * (owlet1/attention.py:147 and :226 around the attention of :217-229): q arrives unrotated
+ * and its channels nope..D-1 are rotated with rope_cos / rope_sin bf16 [rows, rope_dim/2]
+ * (the row's position_embeddings, apply_rotary_pos_emb) as the kernel loads it; the bf16
+ * output gets the inverse rotation (sin negated) -- in the split merge when nsplit > 1.
+ * FP8 latent rows only (fmt 1, D 576, nope 512, rope_dim 64); cos / sin 16-byte aligned. */
+int mzk_sparse_mqa_rope(const void* q, int64_t B, int64_t S, int H, int D, int fmt, int nope,
+                        const int64_t* positions, const void* win, int64_t win_batch_entries,
+                        int win_cap, int window, const void* dense, int64_t dense_batch_entries,
+                        int dense_cap, int dense_ratio, const void* main_kv,
+                        int64_t main_batch_entries, int64_t G, const int32_t* idx,
+                        int64_t idx_row_stride, int topk, const float* sinks, int nsplit,
+                        float* workspace, int64_t workspace_bytes, void* out, float* lse,
+                        const void* rope_cos, const void* rope_sin, int rope_dim, void* stream);
+
+/* mzk_sparse_mqa_combine followed by the inverse RoPE of the merged bf16 output's trailing
+ * rope_dim channels (owlet1/attention.py:226), cos / sin bf16 [rows, rope_dim/2]. */
+int mzk_sparse_mqa_combine_rope(const float* workspace, int64_t B, int64_t S, int H, int D,
+                                int nsplit, const float* sinks, const void* rope_cos,
+                                const void* rope_sin, int rope_dim, void* out, float* lse,
+                                void* stream);
 
 #ifdef __cplusplus
 }

@@ -84,16 +84,26 @@ def sparse_mqa_decode(q: torch.Tensor, positions: torch.Tensor, win_cache: torch
                       dense_cache: torch.Tensor | None = None, dense_ratio: int = 1,
                       sinks: torch.Tensor | None = None, nsplit: int = 1, nope: int = 512,
                       workspace: torch.Tensor | None = None, out: torch.Tensor | None = None,
-                      lse: torch.Tensor | None = None):
+                      lse: torch.Tensor | None = None, rope: tuple | None = None):
     """One decode token per batch row over FP8-b128 caches.
 
     q bf16 [B,H,D]; positions int64 [B] (absolute position of the new token, whose own
     entry is already in the window ring); win_cache uint8 [B,Wcap,EB] ring (token t at slot
     t % Wcap); main_cache uint8 [B,Gcap,EB] with int32 ``indices`` [B,topk] over its first
     ``groups`` entries; dense_cache uint8 [B,Dcap,EB] scanned over its first
-    ``(pos+1)//dense_ratio`` entries.  Returns (o bf16 [B,H,D], lse fp32 [B,H])."""
+    ``(pos+1)//dense_ratio`` entries.  Returns (o bf16 [B,H,D], lse fp32 [B,H]).
+
+    ``rope=(cos, sin)`` (bf16 [B, (D-nope)/2], the row's ``position_embeddings``): q arrives
+    unrotated and the kernels apply ``apply_rotary_pos_emb`` to it on load and the inverse
+    rotation to the output (``owlet1/attention.py:147`` and ``:226`` fused in)."""
     b, h, d = q.shape
     _lib.require_gpu(q, positions, win_cache)
+    rc = rs = None
+    if rope is not None:
+        rc, rs = (t.contiguous() for t in rope)
+        if rc.dtype != torch.bfloat16 or rs.dtype != torch.bfloat16 or rc.shape != (b, (d - nope) // 2) \
+                or rs.shape != rc.shape:
+            raise ValueError(f"sparse_mqa_decode: rope cos/sin must be bf16 [B, {(d - nope) // 2}]")
     if out is None:
         out = torch.empty_like(q)
     if lse is None:
@@ -102,11 +112,15 @@ def sparse_mqa_decode(q: torch.Tensor, positions: torch.Tensor, win_cache: torch
     if nsplit > 1 and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = new_workspace(b, h, d, nsplit, q.device)
     topk = 0 if indices is None else indices.shape[-1]
-    _lib.call("mzk_sparse_mqa", q.data_ptr(), b, 1, h, d, FMT_FP8, nope, positions.data_ptr(),
-              win_cache.data_ptr(), win_cache.shape[1], win_cache.shape[1], window,
-              _lib.ptr(dense_cache), 0 if dense_cache is None else dense_cache.shape[1],
-              0 if dense_cache is None else dense_cache.shape[1], dense_ratio,
-              _lib.ptr(main_cache), 0 if main_cache is None else main_cache.shape[1], groups,
-              _lib.ptr(indices), topk, topk, _lib.ptr(sinks), nsplit, _lib.ptr(workspace), need,
-              out.data_ptr(), lse.data_ptr(), _lib.stream_of(q))
+    args = (q.data_ptr(), b, 1, h, d, FMT_FP8, nope, positions.data_ptr(),
+            win_cache.data_ptr(), win_cache.shape[1], win_cache.shape[1], window,
+            _lib.ptr(dense_cache), 0 if dense_cache is None else dense_cache.shape[1],
+            0 if dense_cache is None else dense_cache.shape[1], dense_ratio,
+            _lib.ptr(main_cache), 0 if main_cache is None else main_cache.shape[1], groups,
+            _lib.ptr(indices), topk, topk, _lib.ptr(sinks), nsplit, _lib.ptr(workspace), need,
+            out.data_ptr(), lse.data_ptr())
+    if rope is None:
+        _lib.call("mzk_sparse_mqa", *args, _lib.stream_of(q))
+    else:
+        _lib.call("mzk_sparse_mqa_rope", *args, rc.data_ptr(), rs.data_ptr(), d - nope, _lib.stream_of(q))
     return out, lse

@@ -85,6 +85,11 @@ struct AttnParams {
   float* lse;     // [B, H, S]       (nsplit == 1)
   uint16_t* part_o;  // [rows, nsplit, H, D] bf16: the split's output O / l
   float* part_ml;    // [rows, nsplit, H, 2]: the split's running max m (log2 units) and sum l
+  // RoPE of the rope slice (channels NOPE .. D-1, FP8 latent rows): null, or cos / sin
+  // [rows, (D - NOPE) / 2] bf16 -- q arrives unrotated and is rotated on load, and the
+  // final output (nsplit == 1) gets the inverse rotation
+  const uint16_t* rope_cos;
+  const uint16_t* rope_sin;
 };
 
 template <int FMT, int D, int NOPE>
@@ -387,7 +392,7 @@ __device__ __forceinline__ int pv_lane_offset(int lane, int d_base) {
 
 // Final bf16 output + lse (one split) or fp32 partials (several) for one lane's head and
 // O^T blocks [b_lo, b_lo + nb): acc[db][j] holds O^T[d][head], d = (b_lo+db)*32 + c_entry(j).
-template <int D, int NDBM>
+template <int D, int NOPE, int NDBM>
 __device__ __forceinline__ void write_result(const AttnParams& p, int64_t row, int64_t b, int split, int head, int half,
                                              bool lse_lane, int b_lo, int nb, float m_run, float l_run,
                                              const v16f (&acc)[NDBM]) {
@@ -410,10 +415,23 @@ __device__ __forceinline__ void write_result(const AttnParams& p, int64_t row, i
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
           const int d0 = db * 32 + 8 * g4 + 4 * half;
-          const uint32_t w0 = f32_to_bf16(acc[db][4 * g4 + 0] * o_scale) |
-                              (static_cast<uint32_t>(f32_to_bf16(acc[db][4 * g4 + 1] * o_scale)) << 16);
-          const uint32_t w1 = f32_to_bf16(acc[db][4 * g4 + 2] * o_scale) |
-                              (static_cast<uint32_t>(f32_to_bf16(acc[db][4 * g4 + 3] * o_scale)) << 16);
+          uint32_t w0 = f32_to_bf16(acc[db][4 * g4 + 0] * o_scale) |
+                        (static_cast<uint32_t>(f32_to_bf16(acc[db][4 * g4 + 1] * o_scale)) << 16);
+          uint32_t w1 = f32_to_bf16(acc[db][4 * g4 + 2] * o_scale) |
+                        (static_cast<uint32_t>(f32_to_bf16(acc[db][4 * g4 + 3] * o_scale)) << 16);
+          if constexpr (NOPE < D) {
+            // the inverse rotation of the bf16 output (owlet1/attention.py:226)
+            const int ch = b_lo * 32 + d0;
+            if (p.rope_cos && ch >= NOPE) {
+              const int64_t ci = row * ((D - NOPE) / 2) + (ch - NOPE) / 2;
+              const uint32_t cp = *reinterpret_cast<const uint32_t*>(p.rope_cos + ci);
+              const uint32_t sp = *reinterpret_cast<const uint32_t*>(p.rope_sin + ci);
+              w0 = rope_pair_bf16(w0, bf16_to_f32(static_cast<uint16_t>(cp & 0xffffu)),
+                                  -bf16_to_f32(static_cast<uint16_t>(sp & 0xffffu)));
+              w1 = rope_pair_bf16(w1, bf16_to_f32(static_cast<uint16_t>(cp >> 16)),
+                                  -bf16_to_f32(static_cast<uint16_t>(sp >> 16)));
+            }
+          }
           *reinterpret_cast<uint2*>(orow + d0) = uint2{w0, w1};
         }
       }
@@ -578,7 +596,7 @@ __global__ void __launch_bounds__(HG * 64) sparse_mqa_kernel(const AttnParams p)
   }
 
   if (!head_ok) return;
-  write_result<D, NB>(p, rp.row, rp.b, rp.split, head, half, half == 0, 0, NB, m_run, l_run, acc_o);
+  write_result<D, NOPE, NB>(p, rp.row, rp.b, rp.split, head, half, half == 0, 0, NB, m_run, l_run, acc_o);
 }
 
 // ------------------------------------------------------------------------------------
@@ -667,6 +685,23 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
       v4i v = *reinterpret_cast<const v4i*>(qbase + qoff + 16 * st);
       if (!head_ok) v = v4i{0, 0, 0, 0};
       qf[st] = __builtin_bit_cast(v8bf, v);
+    }
+  }
+  // RoPE of q: the rope slice is the last RST K-steps of the last D-quarter; every lane
+  // reads the cos / sin of the 4 pairs those steps give it (of the row's first pairs when
+  // no table is given), and the last D-quarter rotates them before its first QK
+  constexpr int RST = (D - NOPE) / 16;
+  static_assert(RST == 0 || ((D - NOPE) % 16 == 0 && D - NOPE <= D / DS), "rope slice inside the last D-quarter");
+  uint2 qrc[RST > 0 ? RST : 1], qrs[RST > 0 ? RST : 1];
+  const bool q_rope = RST > 0 && p.rope_cos != nullptr && ds == DS - 1;
+  if constexpr (RST > 0) {
+    const uint16_t* cb = p.rope_cos ? p.rope_cos : p.q;
+    const uint16_t* sb = p.rope_cos ? p.rope_sin : p.q;
+    const uint32_t roff = static_cast<uint32_t>(rp.row * ((D - NOPE) / 2)) + 4 * half;
+#pragma unroll
+    for (int r = 0; r < RST; ++r) {
+      qrc[r] = *reinterpret_cast<const uint2*>(cb + roff + 8 * r);
+      qrs[r] = *reinterpret_cast<const uint2*>(sb + roff + 8 * r);
     }
   }
   rp.plan(p, row_pos);
@@ -898,6 +933,25 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
       if (tid < kTile) g_pref = rp.slot(rp.v_begin + 4 * kTile + tid);
       __syncthreads();
       rp.fetch(0, ptid, raw);
+      if constexpr (!kExact && RST > 0) {
+        // q's rope steps are rotated while tile 0's gathers are in flight (q and the tables
+        // were requested before them, so the wait covers no gather)
+        if (q_rope) {
+#pragma unroll
+          for (int r = 0; r < RST; ++r) {
+            v4i v = __builtin_bit_cast(v4i, qf[QST - RST + r]);
+            const uint32_t cw_[2] = {qrc[r].x, qrc[r].y}, sw_[2] = {qrs[r].x, qrs[r].y};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              const uint32_t cp = cw_[k >> 1], sp = sw_[k >> 1];
+              v[k] = static_cast<int>(rope_pair_bf16(static_cast<uint32_t>(v[k]),
+                                                     bf16_to_f32(static_cast<uint16_t>((k & 1) ? cp >> 16 : cp & 0xffffu)),
+                                                     bf16_to_f32(static_cast<uint16_t>((k & 1) ? sp >> 16 : sp & 0xffffu))));
+            }
+            qf[QST - RST + r] = __builtin_bit_cast(v8bf, v);
+          }
+        }
+      }
       rp.store(ktile(0), KT_PITCH, ptid, raw);
       rp.fetch(1, ptid, raw);
       if (hg == 1) {  // group 1 also writes its half of tile 1 and holds tile 2
@@ -952,7 +1006,7 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
       if (redo) return false;  // uniform: every wave reads the flag after the same barrier
     }
     if (head_ok)
-      write_result<D, NDBM>(p, rp.row, rp.b, rp.split, head, half, ds == 0 && half == 0, b_lo, nb_mine, m_run, l_run,
+      write_result<D, NOPE, NDBM>(p, rp.row, rp.b, rp.split, head, half, ds == 0 && half == 0, b_lo, nb_mine, m_run, l_run,
                             acc_o);
     return true;
   };
@@ -969,7 +1023,9 @@ template <int D>
 __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict__ part_o,
                                                       const float* __restrict__ part_ml, int nsplit, int H, int64_t S,
                                                       int64_t rows, const float* __restrict__ sinks,
-                                                      uint16_t* __restrict__ out, float* __restrict__ lse) {
+                                                      uint16_t* __restrict__ out, float* __restrict__ lse,
+                                                      const uint16_t* __restrict__ rope_cos,
+                                                      const uint16_t* __restrict__ rope_sin, int rope_dim) {
   constexpr int C8 = D / 8;
   const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (t >= rows * H * C8) return;
@@ -980,6 +1036,15 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
   const float* ml = part_ml + (row * nsplit * H + head) * 2;  // split s at + 2 s H
   const uint16_t* po = part_o + (row * nsplit * H + head) * static_cast<int64_t>(D) + 8 * c;
   const float sk = sinks ? sinks[head] * kLog2e : -__builtin_huge_valf();
+  // the inverse RoPE of the merged bf16 output (owlet1/attention.py:226): cos / sin of this
+  // thread's 4 pairs when its 8 channels lie in the trailing rope_dim
+  const int rope_ch = 8 * c - (D - rope_dim);
+  const bool rot = rope_cos != nullptr && rope_ch >= 0;
+  uint2 rc = uint2{0u, 0u}, rs = uint2{0u, 0u};
+  if (rot) {
+    rc = *reinterpret_cast<const uint2*>(rope_cos + row * (rope_dim / 2) + rope_ch / 2);
+    rs = *reinterpret_cast<const uint2*>(rope_sin + row * (rope_dim / 2) + rope_ch / 2);
+  }
   // Splits are merged kCombineRegSplits at a time: a chunk's (m, l) pairs and output pieces
   // are all requested before any is used (one memory round trip per chunk), then folded
   // into a running (M, L, acc) -- the sink first, as a split of weight 1 at sk.  A split
@@ -1023,9 +1088,18 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
     }
   }
   const float inv = 1.0f / L;
-  *reinterpret_cast<uint4*>(out + rh * static_cast<int64_t>(D) + 8 * c) =
-      uint4{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv),
-            pack_bf16x2(acc[4] * inv, acc[5] * inv), pack_bf16x2(acc[6] * inv, acc[7] * inv)};
+  uint32_t o[4] = {pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv),
+                   pack_bf16x2(acc[4] * inv, acc[5] * inv), pack_bf16x2(acc[6] * inv, acc[7] * inv)};
+  if (rot) {
+    const uint32_t cw_[2] = {rc.x, rc.y}, sw_[2] = {rs.x, rs.y};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t cp = cw_[k >> 1], sp = sw_[k >> 1];
+      o[k] = rope_pair_bf16(o[k], bf16_to_f32(static_cast<uint16_t>((k & 1) ? cp >> 16 : cp & 0xffffu)),
+                            -bf16_to_f32(static_cast<uint16_t>((k & 1) ? sp >> 16 : sp & 0xffffu)));
+    }
+  }
+  *reinterpret_cast<uint4*>(out + rh * static_cast<int64_t>(D) + 8 * c) = uint4{o[0], o[1], o[2], o[3]};
   if (c == 0) lse[((row / S) * H + head) * S + row % S] = (M + __log2f(L)) * kLn2;
 }
 
@@ -1096,10 +1170,11 @@ int dispatch(int fmt, int D, int nope, const AttnParams& p, int64_t rows, hipStr
 
 template <int D>
 void launch_combine(const uint16_t* po, const float* pml, int nsplit, int H, int64_t S, const float* sinks,
-                    uint16_t* out, float* lse, int64_t rows, hipStream_t s) {
+                    uint16_t* out, float* lse, int64_t rows, const uint16_t* rope_cos, const uint16_t* rope_sin,
+                    int rope_dim, hipStream_t s) {
   const int64_t n = rows * H * (D / 8);
   combine_kernel<D><<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(po, pml, nsplit, H, S, rows, sinks, out,
-                                                                           lse);
+                                                                           lse, rope_cos, rope_sin, rope_dim);
 }
 
 }  // namespace
@@ -1107,13 +1182,24 @@ void launch_combine(const uint16_t* po, const float* pml, int nsplit, int H, int
 
 using namespace mzk;
 
-extern "C" int mzk_sparse_mqa(const void* q, int64_t B, int64_t S, int H, int D, int fmt, int nope,
-                              const int64_t* positions, const void* win, int64_t win_batch_entries, int win_cap,
-                              int window, const void* dense, int64_t dense_batch_entries, int dense_cap,
-                              int dense_ratio, const void* main_kv, int64_t main_batch_entries, int64_t G,
-                              const int32_t* idx, int64_t idx_row_stride, int topk, const float* sinks, int nsplit,
-                              float* workspace, int64_t workspace_bytes, void* out, float* lse, void* stream) {
+namespace {
+int combine_impl(const float* workspace, int64_t B, int64_t S, int H, int D, int nsplit, const float* sinks,
+                 const void* rope_cos, const void* rope_sin, int rope_dim, void* out, float* lse, void* stream);
+
+int sparse_mqa_impl(const void* q, int64_t B, int64_t S, int H, int D, int fmt, int nope, const int64_t* positions,
+                    const void* win, int64_t win_batch_entries, int win_cap, int window, const void* dense,
+                    int64_t dense_batch_entries, int dense_cap, int dense_ratio, const void* main_kv,
+                    int64_t main_batch_entries, int64_t G, const int32_t* idx, int64_t idx_row_stride, int topk,
+                    const float* sinks, int nsplit, float* workspace, int64_t workspace_bytes, void* out, float* lse,
+                    const void* rope_cos, const void* rope_sin, int rope_dim, void* stream) {
   MZK_CHECK_ARG(B >= 0 && S >= 0 && H >= 1 && D > 0, "sparse_mqa: bad sizes");
+  if (rope_cos || rope_sin) {
+    MZK_CHECK_ARG(rope_cos && rope_sin, "sparse_mqa_rope: cos and sin go together");
+    MZK_CHECK_ARG(fmt == 1 && D == 576 && nope == 512 && rope_dim == 64,
+                  "sparse_mqa_rope: the fused RoPE needs FP8 latent rows of 512 + 64 with rope_dim 64 "
+                  "(got fmt %d, D %d, nope %d, rope_dim %d)", fmt, D, nope, rope_dim);
+    MZK_CHECK_ARG(aligned16(rope_cos) && aligned16(rope_sin), "sparse_mqa_rope: cos and sin must be 16-byte aligned");
+  }
   MZK_CHECK_ARG(fmt == 0 || fmt == 1, "sparse_mqa: fmt must be 0 (bf16) or 1 (fp8-b128)");
   MZK_CHECK_ARG(nsplit >= 1 && nsplit <= 65535, "sparse_mqa: nsplit must be in [1, 65535]");
   MZK_CHECK_ARG(window >= 1 && win != nullptr, "sparse_mqa: a window source (window >= 1) is required");
@@ -1167,17 +1253,27 @@ extern "C" int mzk_sparse_mqa(const void* q, int64_t B, int64_t S, int H, int D,
   p.lse = lse;
   p.part_o = reinterpret_cast<uint16_t*>(workspace);
   p.part_ml = workspace ? reinterpret_cast<float*>(p.part_o + rows * nsplit * static_cast<int64_t>(H) * D) : nullptr;
+  p.rope_cos = static_cast<const uint16_t*>(rope_cos);
+  p.rope_sin = static_cast<const uint16_t*>(rope_sin);
   hipStream_t s = as_stream(stream);
   int rc = dispatch(fmt, D, nope, p, rows, s);
   if (rc) return rc;
   MZK_LAUNCH_CHECK("sparse_mqa");
-  if (nsplit > 1 && out != nullptr) return mzk_sparse_mqa_combine(workspace, B, S, H, D, nsplit, sinks, out, lse, stream);
+  if (nsplit > 1 && out != nullptr)
+    return combine_impl(workspace, B, S, H, D, nsplit, sinks, rope_cos, rope_sin, rope_dim, out, lse, stream);
   return MZK_OK;
 }
 
-extern "C" int mzk_sparse_mqa_combine(const float* workspace, int64_t B, int64_t S, int H, int D, int nsplit,
-                                      const float* sinks, void* out, float* lse, void* stream) {
+int combine_impl(const float* workspace, int64_t B, int64_t S, int H, int D, int nsplit, const float* sinks,
+                 const void* rope_cos, const void* rope_sin, int rope_dim, void* out, float* lse, void* stream) {
   MZK_CHECK_ARG(B >= 0 && S >= 0 && H >= 1 && nsplit >= 1, "sparse_mqa_combine: bad sizes");
+  if (rope_cos || rope_sin) {
+    MZK_CHECK_ARG(rope_cos && rope_sin, "sparse_mqa_combine_rope: cos and sin go together");
+    MZK_CHECK_ARG(rope_dim >= 8 && rope_dim <= D && rope_dim % 8 == 0,
+                  "sparse_mqa_combine_rope: rope_dim must be a multiple of 8 in [8, D] (got %d)", rope_dim);
+    MZK_CHECK_ARG(aligned16(rope_cos) && aligned16(rope_sin),
+                  "sparse_mqa_combine_rope: cos and sin must be 16-byte aligned");
+  }
   const int64_t rows = B * S;
   if (rows == 0) return MZK_OK;
   MZK_CHECK_ARG(workspace && out && lse, "sparse_mqa_combine: null pointer");
@@ -1185,16 +1281,57 @@ extern "C" int mzk_sparse_mqa_combine(const float* workspace, int64_t B, int64_t
   const uint16_t* po = reinterpret_cast<const uint16_t*>(workspace);
   const float* pml = reinterpret_cast<const float*>(po + rows * nsplit * static_cast<int64_t>(H) * D);
   uint16_t* o = static_cast<uint16_t*>(out);
+  const uint16_t* rc_ = static_cast<const uint16_t*>(rope_cos);
+  const uint16_t* rs_ = static_cast<const uint16_t*>(rope_sin);
   hipStream_t s = as_stream(stream);
   switch (D) {
-    case 64: launch_combine<64>(po, pml, nsplit, H, S, sinks, o, lse, rows, s); break;
-    case 96: launch_combine<96>(po, pml, nsplit, H, S, sinks, o, lse, rows, s); break;
-    case 128: launch_combine<128>(po, pml, nsplit, H, S, sinks, o, lse, rows, s); break;
-    case 160: launch_combine<160>(po, pml, nsplit, H, S, sinks, o, lse, rows, s); break;
-    case 256: launch_combine<256>(po, pml, nsplit, H, S, sinks, o, lse, rows, s); break;
-    case 576: launch_combine<576>(po, pml, nsplit, H, S, sinks, o, lse, rows, s); break;
+    case 64: launch_combine<64>(po, pml, nsplit, H, S, sinks, o, lse, rows, rc_, rs_, rope_dim, s); break;
+    case 96: launch_combine<96>(po, pml, nsplit, H, S, sinks, o, lse, rows, rc_, rs_, rope_dim, s); break;
+    case 128: launch_combine<128>(po, pml, nsplit, H, S, sinks, o, lse, rows, rc_, rs_, rope_dim, s); break;
+    case 160: launch_combine<160>(po, pml, nsplit, H, S, sinks, o, lse, rows, rc_, rs_, rope_dim, s); break;
+    case 256: launch_combine<256>(po, pml, nsplit, H, S, sinks, o, lse, rows, rc_, rs_, rope_dim, s); break;
+    case 576: launch_combine<576>(po, pml, nsplit, H, S, sinks, o, lse, rows, rc_, rs_, rope_dim, s); break;
     default: set_last_error("sparse_mqa_combine: unsupported head dim %d", D); return MZK_EUNSUPPORTED;
   }
   MZK_LAUNCH_CHECK("sparse_mqa_combine");
   return MZK_OK;
+}
+}  // namespace
+
+extern "C" int mzk_sparse_mqa(const void* q, int64_t B, int64_t S, int H, int D, int fmt, int nope,
+                              const int64_t* positions, const void* win, int64_t win_batch_entries, int win_cap,
+                              int window, const void* dense, int64_t dense_batch_entries, int dense_cap,
+                              int dense_ratio, const void* main_kv, int64_t main_batch_entries, int64_t G,
+                              const int32_t* idx, int64_t idx_row_stride, int topk, const float* sinks, int nsplit,
+                              float* workspace, int64_t workspace_bytes, void* out, float* lse, void* stream) {
+  return sparse_mqa_impl(q, B, S, H, D, fmt, nope, positions, win, win_batch_entries, win_cap, window, dense,
+                         dense_batch_entries, dense_cap, dense_ratio, main_kv, main_batch_entries, G, idx,
+                         idx_row_stride, topk, sinks, nsplit, workspace, workspace_bytes, out, lse, nullptr, nullptr, 0,
+                         stream);
+}
+
+extern "C" int mzk_sparse_mqa_rope(const void* q, int64_t B, int64_t S, int H, int D, int fmt, int nope,
+                                   const int64_t* positions, const void* win, int64_t win_batch_entries, int win_cap,
+                                   int window, const void* dense, int64_t dense_batch_entries, int dense_cap,
+                                   int dense_ratio, const void* main_kv, int64_t main_batch_entries, int64_t G,
+                                   const int32_t* idx, int64_t idx_row_stride, int topk, const float* sinks,
+                                   int nsplit, float* workspace, int64_t workspace_bytes, void* out, float* lse,
+                                   const void* rope_cos, const void* rope_sin, int rope_dim, void* stream) {
+  MZK_CHECK_ARG(rope_cos && rope_sin, "sparse_mqa_rope: cos and sin are required");
+  return sparse_mqa_impl(q, B, S, H, D, fmt, nope, positions, win, win_batch_entries, win_cap, window, dense,
+                         dense_batch_entries, dense_cap, dense_ratio, main_kv, main_batch_entries, G, idx,
+                         idx_row_stride, topk, sinks, nsplit, workspace, workspace_bytes, out, lse, rope_cos, rope_sin,
+                         rope_dim, stream);
+}
+
+extern "C" int mzk_sparse_mqa_combine(const float* workspace, int64_t B, int64_t S, int H, int D, int nsplit,
+                                      const float* sinks, void* out, float* lse, void* stream) {
+  return combine_impl(workspace, B, S, H, D, nsplit, sinks, nullptr, nullptr, 0, out, lse, stream);
+}
+
+extern "C" int mzk_sparse_mqa_combine_rope(const float* workspace, int64_t B, int64_t S, int H, int D, int nsplit,
+                                           const float* sinks, const void* rope_cos, const void* rope_sin,
+                                           int rope_dim, void* out, float* lse, void* stream) {
+  MZK_CHECK_ARG(rope_cos && rope_sin, "sparse_mqa_combine_rope: cos and sin are required");
+  return combine_impl(workspace, B, S, H, D, nsplit, sinks, rope_cos, rope_sin, rope_dim, out, lse, stream);
 }

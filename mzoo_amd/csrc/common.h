@@ -221,12 +221,62 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// One RoPE pair of bf16 channels (even in the low half): bf16(e*c - o*s), bf16(e*s + o*c),
+// each product and sum rounded to fp32 (no fused multiply-add), then to bf16 by the
+// hardware's round-to-nearest-even pack -- owlet1/norm_rope.py:141-145.  The inverse
+// rotation is the same call with -s (the reference negates sin).
+__device__ __forceinline__ uint32_t rope_pair_bf16(uint32_t pair, float c, float s) {
+  const float e = __uint_as_float(pair << 16);
+  const float o = __uint_as_float(pair & 0xffff0000u);
+  return pack_bf16x2(e * c - o * s, e * s + o * c);
+}
+
+
 // ------------------------------------------------------------------------------------
 // wave helpers (wave64)
 // ------------------------------------------------------------------------------------
 __device__ __forceinline__ float wave_max_group(float v, int group) {
   for (int m = group >> 1; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
   return v;
+}
+
+// The value of lane (lane ^ M), exactly: DPP quad permutes for 1 and 2, DPP row shifts up
+// or down (by lane bit M) for 4 and 8, a swizzle for 16, a permute through LDS for 32.
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) {
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16 || M == 32, "xor partner distance");
+  const int x = __float_as_int(v);
+  if constexpr (M == 1) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+  } else if constexpr (M == 2) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+  } else if constexpr (M == 4 || M == 8) {
+    const int from_up = __builtin_amdgcn_mov_dpp(x, 0x100 + M, 0xF, 0xF, false);  // row_shl: lane + M
+    const int from_dn = __builtin_amdgcn_mov_dpp(x, 0x110 + M, 0xF, 0xF, false);  // row_shr: lane - M
+    return __int_as_float((threadIdx.x & M) ? from_dn : from_up);
+  } else if constexpr (M == 16) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(x, 0x401F));  // and 0x1f, xor 0x10
+  } else {
+    return __shfl_xor(v, 32, 64);
+  }
+}
+
+// Maximum of v >= 0 over the 16 lanes of each DPP row, in the row's last lane (lane 15 of
+// the row); the shifts bring in 0 from beyond the row, which a maximum of values >= 0
+// ignores.
+__device__ __forceinline__ float row_max_nonneg(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x111, 0xF, 0xF, true)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x112, 0xF, 0xF, true)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x114, 0xF, 0xF, true)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x118, 0xF, 0xF, true)));
+  return v;
+}
+
+// Maximum of v >= 0 over the wave, as a wave-uniform value.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+  const int r = __float_as_int(row_max_nonneg(v));
+  return fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(r, 15)), __int_as_float(__builtin_amdgcn_readlane(r, 31))),
+               fmaxf(__int_as_float(__builtin_amdgcn_readlane(r, 47)), __int_as_float(__builtin_amdgcn_readlane(r, 63))));
 }
 
 }  // namespace mzk

@@ -124,11 +124,106 @@ struct IdxParams {
   uint8_t* q_codes_out;   // FP8: [rows, Hi, 128] e4m3; MXFP4: [rows, Hi, 64] e2m1 pairs; or null
   float* q_scales_out;    // FP8: [rows, Hi], or null
   uint8_t* q_e8m0_out;    // MXFP4: [rows, Hi, 4], or null
-  const uint16_t* kv;     // [rows, nope + rope] bf16 (APPEND)
+  const uint16_t* kv;     // [rows, nope + rope] bf16 (APPEND: rotated; FUSE: the kv projection)
   int nope, rope;
   uint8_t* win;
   int64_t win_batch_entries;
   int win_cap;
+  // FUSE (Di = 128, latent 512 + 64): the query's trailing q_rope_dim channels are rotated
+  // with q_cos / q_sin [rows, q_rope_dim / 2] bf16 before quantization, and one extra
+  // workgroup per row normalizes kv (RMSNorm, weight kv_w [576] bf16, kv_eps), rotates its
+  // rope slice with kv_cos / kv_sin [rows, 32] bf16 and appends the FP8-b128 entry
+  const uint16_t* q_cos;
+  const uint16_t* q_sin;
+  int q_rope_dim;
+  const uint16_t* kv_w;
+  float kv_eps;
+  const uint16_t* kv_cos;
+  const uint16_t* kv_sin;
+};
+
+constexpr int kFuseNope = 512, kFuseRope = 64, kFuseChunks = (kFuseNope + kFuseRope) / 64;
+
+// The fused kv prologue (owlet1/attention.py:150-154 with the 656-byte window entry), done
+// by wave 0 of each row's first workgroup: lane l holds channels l + 64 i.  Its loads are
+// issued between the query's and the keys', and the work runs once the query is quantized,
+// while the key loads are in flight.
+//   RMSNorm (norm_rope.py:25-30): sum of squares in 64 partials (lane l over its channels in
+//   order) combined by the xor butterfly 32 .. 1, var = sum / 576, inv = 1 / sqrt(var + eps),
+//   y = bf16(w * bf16(h * inv));
+//   RoPE of channels 512 .. 575 (pairs (2j, 2j+1) = lanes 2j, 2j+1 of chunk 8) at the row's
+//   cos / sin;
+//   pack: FP8 e4m3 codes of the 4 nope blocks of 128 with their power-of-two scales, then the
+//   rotated rope slice in bf16, into ring slot b * win_batch_entries + pos % win_cap.
+typedef unsigned short mzk_u16x2 __attribute__((ext_vector_type(2)));
+
+struct FusedKv {
+  // two 16-bit values per register (d16 / d16_hi loads): kv and weight channels
+  // lane + 64 i, i = 0 .. 8, then cos / sin of the lane's rope pair
+  static constexpr int kRegs = (2 * kFuseChunks + 2 + 1) / 2;
+  mzk_u16x2 v[kRegs];
+
+  __device__ __forceinline__ void load(const IdxParams& p, int64_t row, int lane) {
+    const uint16_t* kvrow = p.kv + row * (kFuseNope + kFuseRope);
+#pragma unroll
+    for (int i = 0; i < kFuseChunks; ++i) {
+      v[i / 2][i & 1] = kvrow[lane + 64 * i];
+      v[(kFuseChunks + i) / 2][(kFuseChunks + i) & 1] = p.kv_w[lane + 64 * i];
+    }
+    v[kFuseChunks][0] = p.kv_cos[row * (kFuseRope / 2) + (lane >> 1)];
+    v[kFuseChunks][1] = p.kv_sin[row * (kFuseRope / 2) + (lane >> 1)];
+  }
+  __device__ __forceinline__ uint16_t at(int k) const { return v[k / 2][k & 1]; }
+
+  __device__ __forceinline__ void append(const IdxParams& p, int64_t b, int64_t pos, int lane) const {
+    if (pos < 0) return;  // no ring slot for a negative position
+    float h[kFuseChunks];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kFuseChunks; ++i) {
+      h[i] = bf16_to_f32(at(i));
+      ss = ss + h[i] * h[i];
+    }
+    // p[l] + p[l ^ m] for m = 32 .. 1: every lane ends with the same total
+    ss = ss + lane_xor<32>(ss);
+    ss = ss + lane_xor<16>(ss);
+    ss = ss + lane_xor<8>(ss);
+    ss = ss + lane_xor<4>(ss);
+    ss = ss + lane_xor<2>(ss);
+    ss = ss + lane_xor<1>(ss);
+    const float var = div_rn(ss, static_cast<float>(kFuseNope + kFuseRope));
+    const float inv = div_rn(1.0f, sqrt_rn(var + p.kv_eps));
+    float y[kFuseChunks];
+#pragma unroll
+    for (int i = 0; i < kFuseChunks; ++i)
+      y[i] = bf16_to_f32(f32_to_bf16(bf16_to_f32(at(kFuseChunks + i)) * bf16_to_f32(f32_to_bf16(h[i] * inv))));
+    // rope slice: lane 2j holds the even channel of pair j, lane 2j+1 the odd one
+    const float cf = bf16_to_f32(at(2 * kFuseChunks)), sf = bf16_to_f32(at(2 * kFuseChunks + 1));
+    const float partner = lane_xor<1>(y[kFuseChunks - 1]);
+    const bool odd = lane & 1;
+    const float e = odd ? partner : y[kFuseChunks - 1];
+    const float o = odd ? y[kFuseChunks - 1] : partner;
+    const uint16_t rot = f32_to_bf16(odd ? e * sf + o * cf : e * cf - o * sf);
+    uint8_t* ent =
+        p.win + (b * p.win_batch_entries + pos % p.win_cap) * (kFuseNope + 4 * (kFuseNope / 128) + 2 * kFuseRope);
+    static_assert(kFuseNope / 128 == 4, "four nope blocks");
+    float scs[4], invs[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      scs[k] = fp8_scale_from_amax(wave_max_nonneg(fmaxf(fabsf(y[2 * k]), fabsf(y[2 * k + 1]))));
+      // x / sc == x * (1 / sc) exactly: sc is a power of two in [2^-22, 2^127]
+      invs[k] = 1.0f / scs[k];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      // v_cvt_pk_fp8_f32 is the quantizer's e4m3 encoder for |x| <= 448
+      const int code = __builtin_amdgcn_cvt_pk_fp8_f32(clampf(y[i] * invs[i >> 1], 448.0f), 0.0f, 0, false);
+      ent[lane + 64 * i] = static_cast<uint8_t>(code & 0xff);
+    }
+    if (lane < 4) reinterpret_cast<float*>(ent + kFuseNope)[lane] =
+        lane == 0 ? scs[0] : lane == 1 ? scs[1] : lane == 2 ? scs[2] : scs[3];
+    reinterpret_cast<uint16_t*>(ent + kFuseNope + 4 * (kFuseNope / 128))[lane] = rot;
+  }
 };
 
 // LDS bytes per quantized head row (padding spreads banks)
@@ -145,9 +240,13 @@ constexpr int q_pitch() { return FMT == kFp8 ? 128 + 16 : 64 + 16; }
 // fragment (16 bytes of nibbles + the e8m0 byte).
 // APPEND: workgroup 0 of the row also writes the new token's FP8-b128 latent into its
 // window-ring slot (b * win_batch_entries + pos % win_cap).
-template <int FMT, int DI, int MB, bool QRAW, bool APPEND>
+// FUSE: the query is rotated before it is quantized, and wave 0 of each row's workgroup 0
+// runs the kv prologue (FusedKv): loads before the keys', the work after the query's
+// quantization.
+template <int FMT, int DI, int MB, bool QRAW, bool APPEND, bool FUSE = false>
 __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxParams p) {
   static_assert(!QRAW || ((FMT == kFp8 || FMT == kMxfp4) && DI == 128), "in-kernel quantization: Di = 128");
+  static_assert(!FUSE || (QRAW && !APPEND), "the fused prologue quantizes the raw query and appends on its own");
   constexpr int QP = q_pitch<FMT>();
   constexpr int NST = DI / Step<FMT>::K;
   constexpr int RB = row_bytes<FMT>(DI);
@@ -175,12 +274,21 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
   // compiler's in-order wait counts stay exact.
   Frag a[MB][NST];
   uint4 qr[4];  // QRAW: 32 bf16 channels of head tid/4
+  uint4 qtab = uint4{0u, 0u, 0u, 0u};  // FUSE: 16 bytes of the row's query cos / sin tables
   const int qh = tid >> 2, qc = tid & 3;
   if constexpr (QRAW) {
     const int hq = qh < Hi ? qh : Hi - 1;
     const uint4* src = reinterpret_cast<const uint4*>(p.q_raw + (row * Hi + hq) * 128 + 32 * qc);
 #pragma unroll
     for (int i = 0; i < 4; ++i) qr[i] = src[i];
+    if constexpr (FUSE) {
+      // the row's cos then sin tables (q_rope_dim / 16 pieces of 16 bytes each), one piece
+      // per thread of the first 2 * q_rope_dim / 16; the rest read piece 0 and drop it
+      const int n4 = p.q_rope_dim / 16;
+      const int t = tid < 2 * n4 ? tid : 0;
+      const uint16_t* tab = t < n4 ? p.q_cos : p.q_sin;
+      qtab = reinterpret_cast<const uint4*>(tab + row * (p.q_rope_dim / 2))[t < n4 ? t : t - n4];
+    }
   } else {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
@@ -199,6 +307,12 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
   float cq = 1.0f;
   if constexpr (FMT == kFp8 && !QRAW) cq = p.q_scale[row * Hi + hl];
   cw = lane < Hi ? cw : 0.0f;
+  // FUSE: the kv prologue's operands come after the query's (whose wait ends in a barrier of
+  // the whole workgroup) and before the keys (which the score loop waits for)
+  FusedKv fkv;
+  if constexpr (FUSE) {
+    if (blockIdx.x == 0 && tid < 64) fkv.load(p, row, tid);
+  }
   Frag bf[kNkb][NST];
   float ksv[kNkb];  // FP8: the per-key scales
 #pragma unroll
@@ -231,6 +345,31 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
   __shared__ __align__(16) uint8_t q_lds[QRAW ? 64 * QP : 16];
   __shared__ float qs_lds[QRAW && FMT == kFp8 ? 64 : 1];
   __shared__ uint8_t qe_lds[QRAW && FMT == kMxfp4 ? 256 : 4];
+  __shared__ uint4 qtab_lds[FUSE ? 16 : 1];
+  if constexpr (FUSE) {
+    // RoPE of the query's rope channels (owlet1/indexer.py:126-128, compress cos / sin),
+    // bf16 in and out as the reference's rotated query.  q_rope_dim is a multiple of 32, so
+    // a thread's 32 channels are all rope or all nope.
+    const int n4 = p.q_rope_dim / 16;
+    if (tid < 2 * n4) qtab_lds[tid] = qtab;
+    __syncthreads();
+    const int first = 32 * qc - (128 - p.q_rope_dim);
+    if (first >= 0) {
+      // this thread's 16 pairs: 32 bytes of cos and of sin (two 16-byte pieces each)
+      const uint4* ct = qtab_lds + first / 16;
+      const uint4* st = ct + p.q_rope_dim / 16;
+      const uint4 c0 = ct[0], c1 = ct[1], s0 = st[0], s1 = st[1];
+      const uint32_t cw_[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+      const uint32_t sw_[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+      uint32_t* wq = reinterpret_cast<uint32_t*>(qr);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const uint32_t cp = cw_[k >> 1], sp = sw_[k >> 1];
+        wq[k] = rope_pair_bf16(wq[k], __uint_as_float((k & 1) ? cp & 0xffff0000u : cp << 16),
+                               __uint_as_float((k & 1) ? sp & 0xffff0000u : sp << 16));
+      }
+    }
+  }
   if constexpr (QRAW && FMT == kMxfp4) {
     // one MXFP4 block of 32 channels per thread: scale, then e2m1 codes (element 2i in the
     // low nibble of byte i), as the quantizer's packed form
@@ -318,6 +457,11 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
       }
     }
     cq = qs_lds[hl];
+  }
+  if constexpr (FUSE) {
+    // the row's kv prologue, while the key loads are still in flight (its registers are
+    // free again before the score loop)
+    if (blockIdx.x == 0 && tid < 64) fkv.append(p, b, pos, tid);
   }
   const float cwq = cw * cq;
   float coef[MB][16];
@@ -595,5 +739,67 @@ extern "C" int mzk_indexer_decode_mxfp4(const void* q_idx, const float* w, const
     else indexer_scores_kernel<kMxfp4, 128, 2, true, false><<<grid, kWaves * 64, 0, s>>>(p);
   }
   MZK_LAUNCH_CHECK("indexer_decode_mxfp4");
+  return MZK_OK;
+}
+
+extern "C" int mzk_indexer_decode_fused(int q_format, const void* q_idx, const float* w, const uint8_t* k_codes,
+                                        const void* k_scales, int64_t B, int Hi, int Di, int64_t G,
+                                        int64_t k_batch_stride, const int64_t* positions, int ratio, float* scores,
+                                        int64_t score_stride, uint8_t* q_codes, void* q_scales, const void* q_cos,
+                                        const void* q_sin, int q_rope_dim, const void* kv, const void* kv_weight,
+                                        float kv_eps, const void* kv_cos, const void* kv_sin, int nope, int rope,
+                                        uint8_t* win_cache, int64_t win_batch_entries, int win_cap, void* stream) {
+  int rc = check_common(B, 1, Hi, Di, G, k_batch_stride, ratio, score_stride);
+  if (rc) return rc;
+  MZK_CHECK_ARG(q_format == 0 || q_format == 1, "indexer_decode_fused: q_format must be 0 (FP8) or 1 (MXFP4), got %d",
+                q_format);
+  MZK_CHECK_ARG(Di == 128, "indexer_decode_fused: the fused decode form needs Di = 128 (got %d)", Di);
+  MZK_CHECK_ARG(q_rope_dim >= 32 && q_rope_dim <= 128 && q_rope_dim % 32 == 0,
+                "indexer_decode_fused: q_rope_dim must be 32, 64, 96 or 128 (got %d)", q_rope_dim);
+  MZK_CHECK_ARG(nope == kFuseNope && rope == kFuseRope, "indexer_decode_fused: latent %d+%d unsupported (needs 512+64)",
+                nope, rope);
+  MZK_CHECK_ARG(kv_eps >= 0.0f, "indexer_decode_fused: negative eps");
+  MZK_CHECK_ARG(positions != nullptr, "indexer_decode_fused: positions are required");
+  MZK_CHECK_ARG((q_codes == nullptr) == (q_scales == nullptr), "indexer_decode_fused: q_codes and q_scales go together");
+  MZK_CHECK_ARG(win_cap >= 1 && win_batch_entries >= win_cap, "indexer_decode_fused: bad window ring");
+  if (B == 0) return MZK_OK;
+  MZK_CHECK_ARG(G >= 1, "indexer_decode_fused: at least one key group is required");
+  MZK_CHECK_ARG(q_idx && w && k_codes && k_scales && scores && q_cos && q_sin && kv && kv_weight && kv_cos && kv_sin &&
+                    win_cache,
+                "indexer_decode_fused: null pointer");
+  MZK_CHECK_ARG(aligned16(q_idx) && aligned16(k_codes) && aligned16(q_codes) && aligned16(q_cos) && aligned16(q_sin),
+                "indexer_decode_fused: q_idx, k_codes, q_codes, q_cos and q_sin must be 16-byte aligned");
+  MZK_CHECK_ARG(B <= 65535, "indexer_decode_fused: at most 65535 rows (got %lld)", (long long)B);
+  const bool fp8 = q_format == 0;
+  IdxParams p = make_params(nullptr, nullptr, nullptr, w, k_codes, fp8 ? static_cast<const float*>(k_scales) : nullptr,
+                            fp8 ? nullptr : static_cast<const uint8_t*>(k_scales), 1, Hi, G, k_batch_stride, positions,
+                            ratio, scores, score_stride);
+  p.q_raw = static_cast<const uint16_t*>(q_idx);
+  p.q_codes_out = q_codes;
+  if (fp8) p.q_scales_out = static_cast<float*>(q_scales);
+  else p.q_e8m0_out = static_cast<uint8_t*>(q_scales);
+  p.q_cos = static_cast<const uint16_t*>(q_cos);
+  p.q_sin = static_cast<const uint16_t*>(q_sin);
+  p.q_rope_dim = q_rope_dim;
+  p.kv = static_cast<const uint16_t*>(kv);
+  p.kv_w = static_cast<const uint16_t*>(kv_weight);
+  p.kv_eps = kv_eps;
+  p.kv_cos = static_cast<const uint16_t*>(kv_cos);
+  p.kv_sin = static_cast<const uint16_t*>(kv_sin);
+  p.nope = nope;
+  p.rope = rope;
+  p.win = win_cache;
+  p.win_batch_entries = win_batch_entries;
+  p.win_cap = win_cap;
+  dim3 grid(static_cast<unsigned>((G + kKeysPerWg - 1) / kKeysPerWg), static_cast<unsigned>(B));
+  hipStream_t s = as_stream(stream);
+  if (fp8) {
+    if (Hi <= 32) indexer_scores_kernel<kFp8, 128, 1, true, false, true><<<grid, kWaves * 64, 0, s>>>(p);
+    else indexer_scores_kernel<kFp8, 128, 2, true, false, true><<<grid, kWaves * 64, 0, s>>>(p);
+  } else {
+    if (Hi <= 32) indexer_scores_kernel<kMxfp4, 128, 1, true, false, true><<<grid, kWaves * 64, 0, s>>>(p);
+    else indexer_scores_kernel<kMxfp4, 128, 2, true, false, true><<<grid, kWaves * 64, 0, s>>>(p);
+  }
+  MZK_LAUNCH_CHECK("indexer_decode_fused");
   return MZK_OK;
 }

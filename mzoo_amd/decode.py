@@ -27,6 +27,14 @@ preallocated on the device so the whole step records into one HIP graph:
   5. sparse MQA over window + [coarse] + top-k entries with the sink, split-KV + merge,
   6. ``positions += 1`` when ``advance``.
 Group emission (the compressor, one entry per ``ratio`` steps) is ``append_groups``.
+
+With ``rope=(cos, sin, index_cos, index_sin)`` (bf16 [B, 32] each: the new token's
+``position_embeddings`` and the indexer's compress-RoPE tables) the step also takes over the
+per-token prologue and epilogue of ``DeepseekV41Attention.forward``: q and q_idx arrive
+unrotated, kv is the raw ``wkv`` projection (RMSNorm with ``kv_norm_weight``, RoPE and the
+window append happen in the indexer launch, ``attention.py:147-155``, ``indexer.py:126-128``),
+q is rotated as the attention kernel loads it, and the output carries the inverse rotation
+(``attention.py:226``) -- the same four launches as without it.
 """
 
 from __future__ import annotations
@@ -61,7 +69,8 @@ class DecodeConfig:
 
 
 class SparseDecodeLayer:
-    def __init__(self, cfg: DecodeConfig, device, sinks: torch.Tensor | None = None):
+    def __init__(self, cfg: DecodeConfig, device, sinks: torch.Tensor | None = None,
+                 kv_norm_weight: torch.Tensor | None = None, kv_norm_eps: float = 1e-6):
         if cfg.index_format not in ("fp8", "mxfp4"):
             raise ValueError(f"index_format must be 'fp8' or 'mxfp4', got {cfg.index_format!r}")
         if cfg.index_format == "fp8" and cfg.index_dim != 128:
@@ -82,6 +91,9 @@ class SparseDecodeLayer:
             self.k_e8m0 = torch.full((b, cfg.max_groups, di // 32), 127, **u8)
         self.positions = torch.zeros(b, dtype=torch.int64, device=self.device)
         self.sinks = None if sinks is None else sinks.float().to(self.device).contiguous()
+        self.kv_norm_weight = None if kv_norm_weight is None else \
+            kv_norm_weight.to(device=self.device, dtype=torch.bfloat16).contiguous()
+        self.kv_norm_eps = float(kv_norm_eps)
         # per-step buffers (fixed addresses, so a captured graph can replay them)
         self.scores = torch.empty(b, 1, cfg.max_groups, dtype=torch.float32, device=self.device)
         self.idx = torch.empty(b, cfg.topk, dtype=torch.int32, device=self.device)
@@ -137,14 +149,18 @@ class SparseDecodeLayer:
 
     # ---- the step ------------------------------------------------------------------------
     def step(self, q: torch.Tensor, kv: torch.Tensor | None, q_idx: torch.Tensor, w: torch.Tensor,
-             advance: bool = False) -> torch.Tensor:
+             advance: bool = False, rope: tuple | None = None) -> torch.Tensor:
         """q bf16 [B,H,D] (rotated), kv bf16 [B,D] (the new token's rotated latent, or None
-        if already in the ring), q_idx bf16 [B,Hi,Di] (rotated), w fp32 [B,Hi] (x Hi^-0.5)."""
+        if already in the ring), q_idx bf16 [B,Hi,Di] (rotated), w fp32 [B,Hi] (x Hi^-0.5).
+        With ``rope`` (see the module docstring) q, q_idx are unrotated, kv is the raw
+        projection, and the returned output has the inverse rotation applied."""
         cfg = self.cfg
         b = cfg.batch
         fp8 = cfg.index_format == "fp8"
         kvc = None if kv is None else kv.contiguous()
         pos = self.positions.view(b, 1)
+        if rope is not None:
+            return self._step_fused(q, kvc, q_idx, w, advance, rope)
         if fp8:
             # window append + indexer-query quantization + scores, one launch
             indexer.decode_fp8(q_idx, w.view(b, -1), self.k_codes, self.k_scales, compress_ratio=cfg.ratio,
@@ -174,21 +190,52 @@ class SparseDecodeLayer:
             self.positions.add_(1)
         return self.out
 
-    def capture(self, q, kv, q_idx, w, advance: bool = False, warmup: int = 2) -> torch.cuda.CUDAGraph:
+    def _step_fused(self, q, kv, q_idx, w, advance, rope):
+        cfg = self.cfg
+        b = cfg.batch
+        if kv is None or self.kv_norm_weight is None:
+            raise ValueError("step(rope=...): needs the kv projection and the layer's kv_norm_weight")
+        if cfg.index_dim != 128:
+            raise ValueError(f"step(rope=...): the fused prologue needs index_dim 128, got {cfg.index_dim}")
+        cos, sin, icos, isin = rope
+        fp8 = cfg.index_format == "fp8"
+        indexer.decode_fused(q_idx, w.view(b, -1), self.k_codes if fp8 else self.k_packed,
+                             self.k_scales if fp8 else self.k_e8m0, fmt=cfg.index_format, compress_ratio=cfg.ratio,
+                             positions=self.positions.view(b, 1), q_rope=(icos, isin), kv=kv,
+                             kv_weight=self.kv_norm_weight, kv_eps=self.kv_norm_eps, kv_rope=(cos, sin),
+                             win_cache=self.win, out=self.scores, nope=cfg.nope, rope=cfg.rope)
+        indexer.topk(self.scores.view(b, cfg.max_groups), cfg.topk, out=self.idx, workspace=self.topk_ws)
+        csa2_attn.sparse_mqa_decode(q, self.positions, self.win, cfg.window, main_cache=self.main,
+                                    groups=cfg.max_groups, indices=self.idx, dense_cache=self.coarse,
+                                    dense_ratio=max(cfg.coarse_ratio, 1), sinks=self.sinks, nsplit=cfg.nsplit,
+                                    nope=cfg.nope, workspace=self.workspace, out=self.out, lse=self.lse,
+                                    rope=(cos, sin))
+        if advance:
+            self.positions.add_(1)
+        return self.out
+
+    def capture(self, q, kv, q_idx, w, advance: bool = False, warmup: int = 2,
+                rope: tuple | None = None) -> torch.cuda.CUDAGraph:
         """Record ``step`` into a HIP graph over static copies of the inputs; ``replay``
-        then reruns it after the caller writes new inputs into ``static_inputs``."""
-        self._static = tuple(None if t is None else t.clone() for t in (q, kv, q_idx, w))
+        then reruns it after the caller writes new inputs into ``static_inputs`` (with
+        ``rope``, its four tables are the last four static inputs: a replay that advances
+        the positions needs the next position's tables written there too)."""
+        ins = (q, kv, q_idx, w) + (() if rope is None else tuple(rope))
+        self._static = tuple(None if t is None else t.clone() for t in ins)
+        st = self._static
+        run = (lambda adv: self.step(*st[:4], advance=adv)) if rope is None else \
+            (lambda adv: self.step(*st[:4], advance=adv, rope=st[4:]))
         s = torch.cuda.Stream(device=self.device)
         s.wait_stream(torch.cuda.current_stream(self.device))
         saved = self.positions.clone()
         with torch.cuda.stream(s):
             for _ in range(warmup):
-                self.step(*self._static, advance=False)
+                run(False)
         torch.cuda.current_stream(self.device).wait_stream(s)
         self.positions.copy_(saved)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            self.step(*self._static, advance=advance)
+            run(advance)
         self._graph = g
         return g
 

@@ -239,6 +239,57 @@ def decode_mxfp4(q_idx: torch.Tensor, w: torch.Tensor, k_packed: torch.Tensor, k
     return out
 
 
+def decode_fused(q_idx: torch.Tensor, w: torch.Tensor, k: torch.Tensor, k_scales: torch.Tensor, *, fmt: str,
+                 compress_ratio: int, positions: torch.Tensor, q_rope: tuple, kv: torch.Tensor,
+                 kv_weight: torch.Tensor, kv_eps: float, kv_rope: tuple, win_cache: torch.Tensor,
+                 out: torch.Tensor | None = None, q_codes: torch.Tensor | None = None,
+                 q_scales: torch.Tensor | None = None, nope: int = 512, rope: int = 64) -> torch.Tensor:
+    """The decode step's whole prologue and indexer in one launch (``fmt`` "fp8" or "mxfp4").
+
+    The unrotated indexer query q_idx bf16 [B,Hi,128] is rotated with ``q_rope`` = (cos,
+    sin) bf16 [B, rd/2] (the compress RoPE; ``owlet1/indexer.py:126-128``), quantized and
+    scored as in ``decode_fp8`` / ``decode_mxfp4``; the new token's kv projection kv bf16
+    [B, nope+rope] is normalized (RMSNorm with ``kv_weight`` bf16 [nope+rope] and
+    ``kv_eps``), its rope slice rotated with ``kv_rope`` = (cos, sin) bf16 [B, rope/2] and the
+    FP8-b128 entry appended to the window ring -- ``owlet1/attention.py:150-155`` for one
+    token.  k / k_scales: FP8 codes [B,Gcap,128] + fp32 [B,Gcap], or MXFP4 [B,Gcap,64] +
+    e8m0 [B,Gcap,4]."""
+    if fmt not in ("fp8", "mxfp4"):
+        raise ValueError(f"decode_fused: fmt must be 'fp8' or 'mxfp4', got {fmt!r}")
+    b, hi, di = q_idx.shape
+    gcap = k.shape[1]
+    fp8 = fmt == "fp8"
+    kshape, sshape = ((b, gcap, di), (b, gcap)) if fp8 else ((b, gcap, di // 2), (b, gcap, di // 32))
+    if q_idx.dtype != torch.bfloat16 or k.shape != kshape or k_scales.shape != sshape or w.numel() != b * hi:
+        raise ValueError("decode_fused: shape/dtype mismatch")
+    qc_, qs_ = (t.contiguous() for t in q_rope)
+    kc_, ks_ = (t.contiguous() for t in kv_rope)
+    for name, t, shape in (("q_rope", qc_, None), ("q_rope", qs_, qc_.shape), ("kv_rope", kc_, (b, rope // 2)),
+                           ("kv_rope", ks_, (b, rope // 2))):
+        if t.dtype != torch.bfloat16 or t.dim() != 2 or t.shape[0] != b or (shape is not None and t.shape != shape):
+            raise ValueError(f"decode_fused: {name} cos/sin must be bf16 [B, rd/2] of one shape")
+    if kv.dtype != torch.bfloat16 or kv.shape != (b, nope + rope) or kv_weight.dtype != torch.bfloat16 \
+            or kv_weight.numel() != nope + rope:
+        raise ValueError("decode_fused: kv and kv_weight must be bf16 [B, nope+rope] / [nope+rope]")
+    if (q_codes is None) != (q_scales is None):
+        raise ValueError("decode_fused: q_codes and q_scales go together")
+    for t in (q_codes, q_scales, win_cache):
+        if t is not None and not t.is_contiguous():
+            raise ValueError("decode_fused: q_codes, q_scales and win_cache must be contiguous")
+    _lib.require_gpu(q_idx, k, positions, kv, win_cache)
+    out = _check_scores_out(b, 1, gcap, q_idx.device, out)
+    pos = torch.as_tensor(positions, device=q_idx.device).to(torch.int64).reshape(b).contiguous()
+    qc = q_idx.contiguous()
+    kscales = k_scales.float().contiguous() if fp8 else k_scales.contiguous()
+    wcap = win_cache.shape[1]
+    _lib.call("mzk_indexer_decode_fused", 0 if fp8 else 1, qc.data_ptr(), w.float().contiguous().data_ptr(),
+              k.contiguous().data_ptr(), kscales.data_ptr(), b, hi, di, gcap, gcap, pos.data_ptr(), compress_ratio,
+              out.data_ptr(), out.stride(1), _lib.ptr(q_codes), _lib.ptr(q_scales), qc_.data_ptr(), qs_.data_ptr(),
+              2 * qc_.shape[1], kv.contiguous().data_ptr(), kv_weight.contiguous().data_ptr(), float(kv_eps),
+              kc_.data_ptr(), ks_.data_ptr(), nope, rope, win_cache.data_ptr(), wcap, wcap, _lib.stream_of(qc))
+    return out
+
+
 def scores_mxfp4(q_packed: torch.Tensor, q_e8m0: torch.Tensor, w: torch.Tensor, k_packed: torch.Tensor,
                  k_e8m0: torch.Tensor, *, compress_ratio: int, positions=None, groups: int | None = None,
                  out: torch.Tensor | None = None) -> torch.Tensor:

@@ -10,7 +10,9 @@ Follows
   (interleaved (even, odd) pairs on the trailing rope slice, fp32 math, ``inverse``
   negates ``sin``),
 * ``DeepseekV41CSACache.store_compression_weights`` ``owlet1/cache.py:96-113``
-  (group alignment and the partial-group carry, as ``split_groups``).
+  (group alignment and the partial-group carry, as ``split_groups``),
+* the decode prologue of the new token's latent ``owlet1/attention.py:150-151``
+  (``rope(kv_norm(kv))``, as ``decode_kv_latent``: a composition of the two above).
 
 The reference evaluates ``softmax`` / ``mean`` with torch, whose exp and reduction order
 are implementation-defined (they differ between torch's CPU and GPU builds in the last
@@ -156,6 +158,14 @@ def rope(x, cos, sin, inverse: bool = False, dtype: str = "float32") -> np.ndarr
     out[..., 0::2] = even * cos - odd * sin
     out[..., 1::2] = even * sin + odd * cos
     return np.concatenate([nope, round_to(out, dtype)], -1)
+
+
+def decode_kv_latent(kv, weight, eps: float, cos, sin, dtype: str = "bfloat16") -> np.ndarray:
+    """The new token's window latent, ``owlet1/attention.py:150-151``:
+    ``apply_rotary_pos_emb(kv_norm(wkv(x)), cos, sin)`` on the projection ``kv`` [..., D]
+    (values of ``dtype``) with cos/sin [..., rd/2]; the result is what the window cache
+    stores before its FP8 packing."""
+    return rope(rms_norm(kv, weight, eps, dtype), cos, sin, dtype=dtype)
 
 
 def rope_tables(positions, rope_dim: int, theta: float):

@@ -10,7 +10,9 @@ these checks show it still computes the reference's functions:
   vector normalises to +-weight;
 * ``rope``: position 0 is the identity, inverse after forward restores x, and the
   rotation preserves each pair's norm;
-* ``split_groups``: the carry invariant of ``store_compression_weights``.
+* ``split_groups``: the carry invariant of ``store_compression_weights``;
+* ``decode_kv_latent`` against the reference's norm-then-rotate steps run by torch in
+  bf16, and at position 0 equal to the plain norm.
 """
 
 import numpy as np
@@ -102,6 +104,43 @@ def test_rope_identities():
     n_in = x[..., 128::2] ** 2 + x[..., 129::2] ** 2
     n_out = y[..., 128::2] ** 2 + y[..., 129::2] ** 2
     assert np.allclose(n_in, n_out, rtol=1e-5)
+
+
+def _torch_decode_latent(kv, w, eps, cos, sin):
+    """attention.py:150-151 stated with torch's own ops in bf16: kv_norm (norm_rope.py:25-30)
+    then apply_rotary_pos_emb (norm_rope.py:126-145) on the trailing 2*len(cos) channels."""
+    h = kv.float()
+    normed = w * (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)).to(torch.bfloat16)
+    rd = cos.shape[-1] * 2
+    nope, rope = normed[..., :-rd], normed[..., -rd:]
+    even, odd = rope[..., 0::2].float(), rope[..., 1::2].float()
+    rot = torch.stack([even * cos - odd * sin, even * sin + odd * cos], dim=-1).flatten(-2)
+    return torch.cat([nope, rot.to(torch.bfloat16)], -1)
+
+
+def test_decode_kv_latent_matches_torch():
+    """The composition order (norm, weight in bf16, then the rotation of the trailing 64
+    channels) against the reference's steps run by torch: equal up to torch's own rsqrt /
+    mean rounding (a bf16 ulp on a few channels)."""
+    rng = np.random.default_rng(8)
+    kv = Q.round_bf16(rng.standard_normal((64, 576)).astype(np.float32) * rng.uniform(0.01, 50, (64, 1)))
+    w = Q.round_bf16(rng.uniform(0.5, 1.5, 576).astype(np.float32))
+    cos, sin = C.rope_tables(rng.integers(0, 1 << 19, 64), 64, 10000.0)
+    cos, sin = Q.round_bf16(cos), Q.round_bf16(sin)
+    got = C.decode_kv_latent(kv, w, 1e-6, cos, sin)
+    ref = _torch_decode_latent(torch.from_numpy(kv).bfloat16(), torch.from_numpy(w).bfloat16(), 1e-6,
+                               torch.from_numpy(cos).bfloat16(), torch.from_numpy(sin).bfloat16()).float().numpy()
+    rel = np.abs(got - ref) / np.maximum(np.abs(ref), 1e-30)
+    assert np.max(rel) <= 2 * 2.0 ** -8
+    assert np.mean(got == ref) > 0.98
+    # the rope slice is rotated and the nope slice is not: swapping the two steps, or
+    # rotating the leading channels, breaks the match above; and at position 0 the latent
+    # is the plain norm
+    c0, s0 = C.rope_tables(np.zeros(64), 64, 10000.0)
+    assert np.array_equal(C.decode_kv_latent(kv, w, 1e-6, Q.round_bf16(c0), Q.round_bf16(s0)),
+                          C.rms_norm(kv, w, 1e-6, "bfloat16"))
+    assert not np.array_equal(got[:, 512:], C.rms_norm(kv, w, 1e-6, "bfloat16")[:, 512:])
+    assert np.array_equal(got[:, :512], C.rms_norm(kv, w, 1e-6, "bfloat16")[:, :512])
 
 
 def test_split_groups_carry():
