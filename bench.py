@@ -457,11 +457,12 @@ def run_prefill(torch, dev, args):
     state = {}
 
     def quant_q():
-        state["q"] = quant.quant_fp8_block(q_idx, 128)
+        qc, qs = quant.quant_fp8_block(q_idx, 128)
+        state["q"] = (qc, qs[..., 0].contiguous())
 
     def scores_fp8():
         qc, qs = state["q"]
-        indexer.scores_fp8(qc, qs[..., 0], w, kc, ks, compress_ratio=ratio, out=scores)
+        indexer.scores_fp8(qc, qs, w, kc, ks, compress_ratio=ratio, out=scores)
 
     def topk():
         indexer.topk(scores, k, out=idx)
@@ -485,8 +486,10 @@ def run_prefill(torch, dev, args):
         step()
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) / steps * 1e3
-    stages = {"quant_q": time_launches(torch, quant_q, 5), "indexer_fp8": time_launches(torch, scores_fp8, 5),
-              "topk": time_launches(torch, topk, 5), "sparse_mqa": time_launches(torch, attn, 5)}
+    # each stage alone, as a graph of back-to-back launches (the kernels' own time, without
+    # the host's launch gaps, which exceed the shorter kernels)
+    stages = {"quant_q": graph_time(torch, [quant_q], 64), "indexer_fp8": graph_time(torch, [scores_fp8], 64),
+              "topk": graph_time(torch, [topk], 64), "sparse_mqa": graph_time(torch, [attn], 32)}
     t = torch.arange(s, dtype=torch.float64)
     pairs = float((torch.clamp((t + 1) // ratio, max=k) + torch.clamp(t + 1, max=win)).sum())
     attn_flops = 4.0 * d * h * pairs

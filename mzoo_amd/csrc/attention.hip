@@ -111,7 +111,6 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 
 constexpr int kIdxCap = 4096;       // sparse indices of one split staged in LDS (D <= 256 kernel)
 constexpr int kSplitIdxCap = 1024;  // the same for the D-split kernel (its LDS holds three tiles)
-constexpr int kMaxDevices = 64;     // per-device one-time launch attributes
 
 typedef const uint8_t __attribute__((address_space(1)))* gptr_t;  // global (not flat) loads
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));

@@ -53,6 +53,8 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 static inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+constexpr int kMaxDevices = 64;  // per-device one-time launch attributes (dynamic-LDS limits)
+
 // ------------------------------------------------------------------------------------
 // scalar conversions
 // ------------------------------------------------------------------------------------

@@ -86,6 +86,15 @@ __device__ __forceinline__ Frag keep_or_zero(Frag f, bool keep) {
   return f;
 }
 
+// One term of the ReLU-weighted head sum: part + c * max(x, 0), as one fused multiply-add.
+// max(x, 0) is an integer max on the bits (a negative float's bit pattern is a negative
+// integer, so it becomes +0; a positive one is kept): one instruction, where fmaxf also
+// canonicalizes its operand.
+__device__ __forceinline__ float relu_fma(float c, float x, float part) {
+  const float r = __int_as_float(__builtin_elementwise_max(__float_as_int(x), 0));
+  return __builtin_fmaf(c, r, part);
+}
+
 template <int FMT>
 __device__ __forceinline__ v16f mma(const Frag& a, const Frag& b, v16f c) {
   if constexpr (FMT == kFp8) {
@@ -486,7 +495,7 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
 #pragma unroll
       for (int st = 0; st < NST; ++st) acc = mma<FMT>(a[mb][st], bf[t][st], acc);
 #pragma unroll
-      for (int j = 0; j < 16; ++j) part = part + coef[mb][j] * fmaxf(acc[j], 0.0f);
+      for (int j = 0; j < 16; ++j) part = relu_fma(coef[mb][j], acc[j], part);
     }
     const float total = part + __shfl_xor(part, 32, 64);
     if (lane < 32 && g < G) {
@@ -537,6 +546,201 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
       }
     }
   }
+}
+
+// ------------------------------------------------------------------------------------
+// Prefill form (FP8, Di = 128): many query rows against the same keys.  The decode tiling
+// re-streams every key for every query row; here one workgroup takes kPfQb query rows and
+// walks the key blocks of 512: per block a wave holds 128 keys (4 N-blocks of 32, two
+// 64-channel steps) as the MFMA B operand and runs the rows through them (A = a row's 64
+// heads as two 32-row M-blocks).  The rows' codes are staged in LDS once, at the start (one
+// memory round trip; 144-byte row pitch against bank conflicts), with the per-head weights
+// w * q_scale next to them; each lane reads the 16 accumulator rows it holds.  Within a
+// row the next key tile's MFMAs are issued while the current tile's ReLU-weighted head sum
+// runs (the two take about as long).  Keys a row cannot see (at or beyond (pos + 1) //
+// ratio) are written as -inf without MFMA work, blocks beyond every row's visibility
+// without loading them, and the workgroups with the most visible keys are dispatched first
+// (the grid runs the query blocks from the last to the first).  The head sum runs in the
+// row kernel's order, so the scores are the row kernel's bit for bit.
+// ------------------------------------------------------------------------------------
+constexpr int kPfQb = 8;               // query rows per workgroup
+constexpr int kPfPrefillMinRows = 64;  // rows per batch from which the prefill form is used
+constexpr int kPfPitch = 144;          // LDS bytes per staged head row
+constexpr int kPfLds = kPfQb * 64 * kPfPitch + kPfQb * 64 * 4 + kPfQb * 8;
+
+__global__ void __launch_bounds__(kWaves * 64, 2) indexer_prefill_fp8_kernel(const IdxParams p, int64_t nqb) {
+  constexpr int DI = 128, NST = 2;
+  extern __shared__ __align__(16) uint8_t pf_smem[];
+  uint8_t* q_lds = pf_smem;                                                   // [qb][64][kPfPitch]
+  float* coef_lds = reinterpret_cast<float*>(pf_smem + kPfQb * 64 * kPfPitch);  // [qb][64]
+  int64_t* vis_lds = reinterpret_cast<int64_t*>(coef_lds + kPfQb * 64);        // [qb]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int hi = lane >> 5;
+  const int64_t nkb = (p.G + kKeysPerWg - 1) / kKeysPerWg;
+  const int64_t qb_all = static_cast<int64_t>(gridDim.x) - 1 - blockIdx.x;  // last query block first
+  const int64_t b = qb_all / nqb;
+  const int64_t s0 = (qb_all % nqb) * kPfQb;
+  const int Hi = p.Hi;
+  const int64_t G = p.G, S = p.S;
+  const float inv_sqrt_di = 1.0f / sqrt_rn(static_cast<float>(DI));
+  const int nq = static_cast<int>(S - s0 < kPfQb ? S - s0 : kPfQb);
+  const uint8_t* kb_base = p.k + b * p.kbs * DI;
+  const float* ks_base = p.k_scale + b * p.kbs;
+  // the rows' codes: 16-byte piece i = (row, head, piece) of the block, every load issued
+  // before any is stored (rows beyond the block and heads beyond Hi read row 0 / head 0 and
+  // store zeros)
+  constexpr int kPieces = kPfQb * 64 * (DI / 16);
+  constexpr int kPerThread = kPieces / (kWaves * 64);
+  uint4 pc[kPerThread];
+#pragma unroll
+  for (int k = 0; k < kPerThread; ++k) {
+    const int i = tid + k * kWaves * 64;
+    const int qi = i / (64 * (DI / 16)), h = (i / (DI / 16)) % 64, c = i % (DI / 16);
+    const bool ok = qi < nq && h < Hi;
+    const int64_t r = b * S + s0 + (ok ? qi : 0);
+    pc[k] = *reinterpret_cast<const uint4*>(p.q + (r * Hi + (ok ? h : 0)) * DI + 16 * c);
+  }
+  for (int i = tid; i < kPfQb * 64; i += kWaves * 64) {
+    const int qi = i >> 6, h = i & 63;
+    float c = 0.0f;
+    if (qi < nq && h < Hi) {
+      const int64_t r = b * S + s0 + qi;
+      c = p.w[r * Hi + h] * p.q_scale[r * Hi + h];
+    }
+    coef_lds[i] = c;
+  }
+  if (tid < kPfQb) {
+    int64_t v = 0;
+    if (tid < nq) {
+      const int64_t r = b * S + s0 + tid;
+      const int64_t pos = p.positions ? p.positions[r] : s0 + tid;
+      v = (pos + 1) / p.ratio;
+      v = v > G ? G : (v < 0 ? 0 : v);
+    }
+    vis_lds[tid] = v;
+  }
+#pragma unroll
+  for (int k = 0; k < kPerThread; ++k) {
+    const int i = tid + k * kWaves * 64;
+    const int qi = i / (64 * (DI / 16)), h = (i / (DI / 16)) % 64, c = i % (DI / 16);
+    const bool ok = qi < nq && h < Hi;
+    *reinterpret_cast<uint4*>(q_lds + (qi * 64 + h) * kPfPitch + 16 * c) = ok ? pc[k] : uint4{0u, 0u, 0u, 0u};
+  }
+  __syncthreads();
+  int64_t vis_max = 0;
+  for (int qi = 0; qi < nq; ++qi) vis_max = vis_lds[qi] > vis_max ? vis_lds[qi] : vis_max;
+
+  // the key blocks in turn: every block with a visible key is scored, and the blocks
+  // beyond every row's visibility are written as -inf
+  for (int64_t kb = 0; kb < nkb; ++kb) {
+    const int64_t key0 = kb * kKeysPerWg + wave * (kNkb * 32);
+    if (kb * kKeysPerWg >= vis_max) {
+      if (lane < 32) {
+        for (int qi = 0; qi < nq; ++qi) {
+          float* out = p.scores + (b * S + s0 + qi) * p.sstride;
+#pragma unroll
+          for (int t = 0; t < kNkb; ++t) {
+            const int64_t g = key0 + t * 32 + lane;
+            if (g < G) out[g] = -__builtin_huge_valf();
+          }
+        }
+      }
+      continue;
+    }
+    // the wave's keys: B fragments and per-key scales (keys at or beyond G read key G-1;
+    // their score columns are never written)
+    Frag bf[kNkb][NST];
+    float ksv[kNkb];
+#pragma unroll
+    for (int t = 0; t < kNkb; ++t) {
+      const int64_t g = key0 + t * 32 + (lane & 31);
+      const int64_t gc = g < G ? g : G - 1;
+#pragma unroll
+      for (int st = 0; st < NST; ++st) bf[t][st] = load_frag<kFp8, DI>(kb_base + gc * DI, nullptr, st, hi);
+      ksv[t] = ks_base[gc];
+    }
+    for (int qi = 0; qi < nq; ++qi) {
+      const int64_t vis = vis_lds[qi];
+      float* out = p.scores + (b * S + s0 + qi) * p.sstride;
+      if (key0 < vis) {
+        Frag a[2][NST];
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+          for (int st = 0; st < NST; ++st) {
+            const uint4* src =
+                reinterpret_cast<const uint4*>(q_lds + (qi * 64 + mb * 32 + (lane & 31)) * kPfPitch + st * 64 + hi * 32);
+            const uint4 u = src[0], v = src[1];
+            a[mb][st].v = v8i{(int)u.x, (int)u.y, (int)u.z, (int)u.w, (int)v.x, (int)v.y, (int)v.z, (int)v.w};
+            a[mb][st].scale = 127;
+          }
+        // this lane's 16 accumulator rows of each M-block: 4 runs of 4 consecutive heads
+        float cf[2][16];
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const float4 c4 = *reinterpret_cast<const float4*>(coef_lds + qi * 64 + mb * 32 + 8 * r4 + 4 * hi);
+            cf[mb][4 * r4 + 0] = c4.x;
+            cf[mb][4 * r4 + 1] = c4.y;
+            cf[mb][4 * r4 + 2] = c4.z;
+            cf[mb][4 * r4 + 3] = c4.w;
+          }
+        // Software pipeline over the 4 key tiles: the MFMAs of tile t+1 are issued while the
+        // head sum of tile t runs (one MFMA per 16 VALU operations, about one MFMA's duration),
+        // so the matrix and vector units work at the same time; the stores come after.
+        float total[kNkb];
+        v16f acc[2][2];  // [tile parity][M-block]
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+          acc[0][mb] = v16f{};
+#pragma unroll
+          for (int st = 0; st < NST; ++st) acc[0][mb] = mma<kFp8>(a[mb][st], bf[0][st], acc[0][mb]);
+        }
+#pragma unroll
+        for (int t = 0; t < kNkb; ++t) {
+          const int cur = t & 1, nxt = cur ^ 1;
+          if (t + 1 < kNkb) {
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb) {
+              acc[nxt][mb] = v16f{};
+#pragma unroll
+              for (int st = 0; st < NST; ++st) acc[nxt][mb] = mma<kFp8>(a[mb][st], bf[t + 1][st], acc[nxt][mb]);
+            }
+          }
+          float part = 0.0f;
+#pragma unroll
+          for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) part = relu_fma(cf[mb][j], acc[cur][mb][j], part);
+          if (t + 1 < kNkb) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+              __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);  // sixteen VALU
+            }
+          }
+          total[t] = part + __shfl_xor(part, 32, 64);
+        }
+        if (lane < 32) {
+#pragma unroll
+          for (int t = 0; t < kNkb; ++t) {
+            const int64_t g = key0 + t * 32 + lane;
+            if (g < G) out[g] = g < vis ? (total[t] * inv_sqrt_di) * ksv[t] : -__builtin_huge_valf();
+          }
+        }
+      } else if (lane < 32) {
+#pragma unroll
+        for (int t = 0; t < kNkb; ++t) {
+          const int64_t g = key0 + t * 32 + lane;
+          if (g < G) out[g] = -__builtin_huge_valf();
+        }
+      }
+    }
+  }
+
 }
 
 template <int FMT, int DI>
@@ -609,9 +813,32 @@ extern "C" int mzk_indexer_scores_fp8(const uint8_t* q_codes, const float* q_sca
   if (B * S == 0 || G == 0) return MZK_OK;
   MZK_CHECK_ARG(q_codes && q_scales && w && k_codes && k_scales && scores, "indexer_scores_fp8: null pointer");
   MZK_CHECK_ARG(Di % 64 == 0, "indexer_scores_fp8: Di must be a multiple of 64 (got %d)", Di);
-  rc = launch<kFp8>(make_params(q_codes, q_scales, nullptr, w, k_codes, k_scales, nullptr, S, Hi, G, k_batch_stride,
-                                positions, ratio, scores, score_stride),
-                    B * S, Di, as_stream(stream));
+  const IdxParams prm = make_params(q_codes, q_scales, nullptr, w, k_codes, k_scales, nullptr, S, Hi, G, k_batch_stride,
+                                    positions, ratio, scores, score_stride);
+  if (Di == 128 && S >= kPfPrefillMinRows) {
+    // prefill: query rows stream through key tiles held in registers
+    const int64_t nqb = (S + kPfQb - 1) / kPfQb;
+    const int64_t nblocks = B * nqb;
+    MZK_CHECK_ARG(nblocks <= 0x7fffffff, "indexer_scores_fp8: %lld workgroups exceed the grid limit", (long long)nblocks);
+    // the staged query rows need more than the default dynamic-LDS limit: set once per device
+    static bool attr_set[kMaxDevices] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+      set_last_error("indexer_scores_fp8: no usable current device");
+      return MZK_ELAUNCH;
+    }
+    if (!attr_set[dev]) {
+      if (hipFuncSetAttribute(reinterpret_cast<const void*>(indexer_prefill_fp8_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kPfLds) != hipSuccess) {
+        set_last_error("indexer_scores_fp8: cannot raise the prefill kernel's LDS limit to %d bytes", kPfLds);
+        return MZK_ELAUNCH;
+      }
+      attr_set[dev] = true;
+    }
+    indexer_prefill_fp8_kernel<<<static_cast<unsigned>(nblocks), kWaves * 64, kPfLds, as_stream(stream)>>>(prm, nqb);
+  } else {
+    rc = launch<kFp8>(prm, B * S, Di, as_stream(stream));
+  }
   if (rc) return rc;
   MZK_LAUNCH_CHECK("indexer_scores_fp8");
   return MZK_OK;

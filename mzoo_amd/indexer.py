@@ -161,10 +161,13 @@ def scores_fp8(q_codes: torch.Tensor, q_scales: torch.Tensor, w: torch.Tensor, k
     _lib.require_gpu(q_codes, k_codes)
     out = _check_scores_out(b, s, g, q_codes.device, out)
     pos = _positions(positions, b, s, q_codes.device)
-    _lib.call("mzk_indexer_scores_fp8", q_codes.contiguous().data_ptr(), q_scales.float().contiguous().data_ptr(),
-              w.float().contiguous().data_ptr(), k_codes.contiguous().data_ptr(),
-              k_scales.float().contiguous().data_ptr(), b, s, hi, di, g, gcap, _lib.ptr(pos), compress_ratio,
-              out.data_ptr(), out.stride(1), _lib.stream_of(q_codes))
+    # converted copies stay referenced until the launch is queued: a temporary freed after
+    # data_ptr() would return its memory to the caching allocator for the next copy
+    qc, qs, wc, kc, ks = (q_codes.contiguous(), q_scales.float().contiguous(), w.float().contiguous(),
+                          k_codes.contiguous(), k_scales.float().contiguous())
+    _lib.call("mzk_indexer_scores_fp8", qc.data_ptr(), qs.data_ptr(), wc.data_ptr(), kc.data_ptr(), ks.data_ptr(),
+              b, s, hi, di, g, gcap, _lib.ptr(pos), compress_ratio, out.data_ptr(), out.stride(1),
+              _lib.stream_of(q_codes))
     return out
 
 
@@ -197,8 +200,9 @@ def decode_fp8(q_idx: torch.Tensor, w: torch.Tensor, k_codes: torch.Tensor, k_sc
     qc = q_idx.contiguous()
     kvc = None if kv is None else kv.contiguous()
     wcap = 0 if win_cache is None else win_cache.shape[1]
-    _lib.call("mzk_indexer_decode_fp8", qc.data_ptr(), w.float().contiguous().data_ptr(), k_codes.contiguous().data_ptr(),
-              k_scales.float().contiguous().data_ptr(), b, hi, di, gcap, gcap, pos.data_ptr(), compress_ratio,
+    wc, kc, ks = w.float().contiguous(), k_codes.contiguous(), k_scales.float().contiguous()
+    _lib.call("mzk_indexer_decode_fp8", qc.data_ptr(), wc.data_ptr(), kc.data_ptr(),
+              ks.data_ptr(), b, hi, di, gcap, gcap, pos.data_ptr(), compress_ratio,
               out.data_ptr(), out.stride(1), _lib.ptr(q_codes), _lib.ptr(q_scales), _lib.ptr(kvc), nope, rope,
               _lib.ptr(win_cache), wcap, wcap, _lib.stream_of(qc))
     return out
@@ -232,8 +236,9 @@ def decode_mxfp4(q_idx: torch.Tensor, w: torch.Tensor, k_packed: torch.Tensor, k
     qc = q_idx.contiguous()
     kvc = None if kv is None else kv.contiguous()
     wcap = 0 if win_cache is None else win_cache.shape[1]
-    _lib.call("mzk_indexer_decode_mxfp4", qc.data_ptr(), w.float().contiguous().data_ptr(),
-              k_packed.contiguous().data_ptr(), k_e8m0.contiguous().data_ptr(), b, hi, di, gcap, gcap, pos.data_ptr(),
+    wc, kp, ke = w.float().contiguous(), k_packed.contiguous(), k_e8m0.contiguous()
+    _lib.call("mzk_indexer_decode_mxfp4", qc.data_ptr(), wc.data_ptr(),
+              kp.data_ptr(), ke.data_ptr(), b, hi, di, gcap, gcap, pos.data_ptr(),
               compress_ratio, out.data_ptr(), out.stride(1), _lib.ptr(q_packed), _lib.ptr(q_e8m0), _lib.ptr(kvc),
               nope, rope, _lib.ptr(win_cache), wcap, wcap, _lib.stream_of(qc))
     return out
@@ -282,10 +287,11 @@ def decode_fused(q_idx: torch.Tensor, w: torch.Tensor, k: torch.Tensor, k_scales
     qc = q_idx.contiguous()
     kscales = k_scales.float().contiguous() if fp8 else k_scales.contiguous()
     wcap = win_cache.shape[1]
-    _lib.call("mzk_indexer_decode_fused", 0 if fp8 else 1, qc.data_ptr(), w.float().contiguous().data_ptr(),
-              k.contiguous().data_ptr(), kscales.data_ptr(), b, hi, di, gcap, gcap, pos.data_ptr(), compress_ratio,
+    wc, kk, kvc, kvw = w.float().contiguous(), k.contiguous(), kv.contiguous(), kv_weight.contiguous()
+    _lib.call("mzk_indexer_decode_fused", 0 if fp8 else 1, qc.data_ptr(), wc.data_ptr(),
+              kk.data_ptr(), kscales.data_ptr(), b, hi, di, gcap, gcap, pos.data_ptr(), compress_ratio,
               out.data_ptr(), out.stride(1), _lib.ptr(q_codes), _lib.ptr(q_scales), qc_.data_ptr(), qs_.data_ptr(),
-              2 * qc_.shape[1], kv.contiguous().data_ptr(), kv_weight.contiguous().data_ptr(), float(kv_eps),
+              2 * qc_.shape[1], kvc.data_ptr(), kvw.data_ptr(), float(kv_eps),
               kc_.data_ptr(), ks_.data_ptr(), nope, rope, win_cache.data_ptr(), wcap, wcap, _lib.stream_of(qc))
     return out
 
@@ -305,8 +311,9 @@ def scores_mxfp4(q_packed: torch.Tensor, q_e8m0: torch.Tensor, w: torch.Tensor, 
     _lib.require_gpu(q_packed, k_packed)
     out = _check_scores_out(b, s, g, q_packed.device, out)
     pos = _positions(positions, b, s, q_packed.device)
-    _lib.call("mzk_indexer_scores_mxfp4", q_packed.contiguous().data_ptr(), q_e8m0.contiguous().data_ptr(),
-              w.float().contiguous().data_ptr(), k_packed.contiguous().data_ptr(), k_e8m0.contiguous().data_ptr(),
+    qp, qe, wc, kp, ke = (q_packed.contiguous(), q_e8m0.contiguous(), w.float().contiguous(), k_packed.contiguous(),
+                          k_e8m0.contiguous())
+    _lib.call("mzk_indexer_scores_mxfp4", qp.data_ptr(), qe.data_ptr(), wc.data_ptr(), kp.data_ptr(), ke.data_ptr(),
               b, s, hi, di, g, gcap, _lib.ptr(pos), compress_ratio, out.data_ptr(), out.stride(1),
               _lib.stream_of(q_packed))
     return out

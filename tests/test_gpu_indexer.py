@@ -172,6 +172,30 @@ def test_fp8_scores_match_oracle(dev, b, s, g, ratio, pos):
     assert_scores_close(got, ref, OA.indexer_abs_scores(qd, kd, w, ratio, positions))
 
 
+@pytest.mark.parametrize("b,s,hi,g,ratio,base", [(2, 300, 64, 1000, 4, None), (1, 200, 40, 700, 1, 5000),
+                                                  (1, 128, 64, 64, 4, None), (3, 64, 64, 2048, 4, 0)])
+def test_fp8_prefill_kernel_matches_row_kernel(dev, b, s, hi, g, ratio, base):
+    """From 64 rows per batch the FP8 scores run the prefill tiling (key tiles held, query
+    rows streamed); it sums in the row kernel's order, so the scores must equal, bit for
+    bit, the row kernel's over chunks of 32 rows with the same positions (ragged row and
+    key counts, fewer than 64 heads, chunked-prefill positions, fully masked key blocks)."""
+    q, k, w = _inputs(b, s, hi, 128, g, seed=s + g)
+    qc, qs, kc, ks, qd, kd = _fp8_operands(q, k)
+    pos = torch.arange(s, dtype=torch.int64).expand(b, s) + (0 if base is None else base)
+    qc, qs, w_d, kc, ks = (t.to(dev) for t in (qc, qs, w, kc, ks))
+    print(f"prefill fp8 scores: B={b} S={s} Hi={hi} G={g} ratio={ratio} base={base}", flush=True)
+    full = MI.scores_fp8(qc, qs, w_d, kc, ks, compress_ratio=ratio, positions=None if base is None else pos.to(dev))
+    parts = [MI.scores_fp8(qc[:, c:c + 32], qs[:, c:c + 32], w_d[:, c:c + 32], kc, ks, compress_ratio=ratio,
+                           positions=pos[:, c:c + 32].to(dev)) for c in range(0, s, 32)]
+    rows = [0, 31, 32, s // 2, s - 1]
+    ref = OA.indexer_scores(qd[:, rows], kd, w[:, rows], ratio, pos[:, rows])
+    mag = OA.indexer_abs_scores(qd[:, rows], kd, w[:, rows], ratio, pos[:, rows])
+    chunked = torch.cat(parts, 1)
+    assert_scores_close(chunked[:, rows], ref, mag)
+    assert_scores_close(full[:, rows], ref, mag)
+    assert torch.equal(full, chunked)
+
+
 def test_fp8_quantizer_feeds_scores(dev):
     """GPU quantizer -> GPU scores equals oracle quantizer -> oracle scores."""
     q, k, w = _inputs(4, 1, 64, 128, 2048, seed=3)
