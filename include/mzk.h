@@ -301,6 +301,23 @@ int mzk_sparse_mqa_rope(const void* q, int64_t B, int64_t S, int H, int D, int f
                         float* workspace, int64_t workspace_bytes, void* out, float* lse,
                         const void* rope_cos, const void* rope_sin, int rope_dim, void* stream);
 
+/* The split partials of part of a row's entry list, for launches that share one workspace:
+ * splits split_base .. split_base + nsplit - 1 of a workspace holding split_total splits
+ * per row (rows*split_total*H*(2*D+8) bytes, laid out as for mzk_sparse_mqa), over the
+ * sources this call is given -- e.g. the window and dense branches in one launch and the
+ * top-k entries in another, which a caller can run concurrently when the top-k is not yet
+ * known; mzk_sparse_mqa_combine(_rope) with nsplit = split_total then merges them as one
+ * softmax (owlet1/attention.py:64-70 over the concatenated entries).  window may be 0 (no
+ * window source); rope_cos / rope_sin (or NULL) as mzk_sparse_mqa_rope. */
+int mzk_sparse_mqa_part(const void* q, int64_t B, int64_t S, int H, int D, int fmt, int nope,
+                        const int64_t* positions, const void* win, int64_t win_batch_entries,
+                        int win_cap, int window, const void* dense, int64_t dense_batch_entries,
+                        int dense_cap, int dense_ratio, const void* main_kv,
+                        int64_t main_batch_entries, int64_t G, const int32_t* idx,
+                        int64_t idx_row_stride, int topk, int nsplit, int split_base,
+                        int split_total, float* workspace, int64_t workspace_bytes,
+                        const void* rope_cos, const void* rope_sin, int rope_dim, void* stream);
+
 /* mzk_sparse_mqa_combine followed by the inverse RoPE of the merged bf16 output's trailing
  * rope_dim channels (owlet1/attention.py:226), cos / sin bf16 [rows, rope_dim/2]. */
 int mzk_sparse_mqa_combine_rope(const float* workspace, int64_t B, int64_t S, int H, int D,

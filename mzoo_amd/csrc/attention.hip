@@ -83,8 +83,10 @@ struct AttnParams {
   // outputs
   uint16_t* out;  // [rows, H, D] bf16 (nsplit == 1)
   float* lse;     // [B, H, S]       (nsplit == 1)
-  uint16_t* part_o;  // [rows, nsplit, H, D] bf16: the split's output O / l
-  float* part_ml;    // [rows, nsplit, H, 2]: the split's running max m (log2 units) and sum l
+  uint16_t* part_o;  // [rows, split_stride, H, D] bf16: the split's output O / l
+  float* part_ml;    // [rows, split_stride, H, 2]: the split's running max m (log2 units) and sum l
+  int split_stride;  // splits per row in the workspace (nsplit, or more when launches share it)
+  int write_final;   // one split writes the final output and lse instead of partials
   // RoPE of the rope slice (channels NOPE .. D-1, FP8 latent rows): null, or cos / sin
   // [rows, (D - NOPE) / 2] bf16 -- q arrives unrotated and is rotated on load, and the
   // final output (nsplit == 1) gets the inverse rotation
@@ -395,7 +397,7 @@ template <int D, int NOPE, int NDBM>
 __device__ __forceinline__ void write_result(const AttnParams& p, int64_t row, int64_t b, int split, int head, int half,
                                              bool lse_lane, int b_lo, int nb, float m_run, float l_run,
                                              const v16f (&acc)[NDBM]) {
-  if (p.nsplit == 1) {
+  if (p.write_final) {
     float m_fin = m_run, l_fin = l_run, o_scale;
     if (p.sinks) {
       const float sk = p.sinks[head] * kLog2e;
@@ -442,7 +444,7 @@ __device__ __forceinline__ void write_result(const AttnParams& p, int64_t row, i
   } else {
     // the split's own normalized output in bf16 (a split that saw no entry writes zeros)
     const float inv_l = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-    uint16_t* prow = p.part_o + (row * p.nsplit + split) * p.H * static_cast<int64_t>(D) +
+    uint16_t* prow = p.part_o + (row * p.split_stride + split) * p.H * static_cast<int64_t>(D) +
                      static_cast<uint32_t>(head * D + b_lo * 32);
 #pragma unroll
     for (int db = 0; db < NDBM; ++db) {
@@ -457,7 +459,7 @@ __device__ __forceinline__ void write_result(const AttnParams& p, int64_t row, i
       }
     }
     if (lse_lane) {
-      float* ml = p.part_ml + (row * p.nsplit + split) * p.H * 2 + static_cast<uint32_t>(head * 2);
+      float* ml = p.part_ml + (row * p.split_stride + split) * p.H * 2 + static_cast<uint32_t>(head * 2);
       ml[0] = m_run;
       ml[1] = l_run;
     }
@@ -1185,12 +1187,17 @@ namespace {
 int combine_impl(const float* workspace, int64_t B, int64_t S, int H, int D, int nsplit, const float* sinks,
                  const void* rope_cos, const void* rope_sin, int rope_dim, void* out, float* lse, void* stream);
 
+// split_total < 0: a whole call (partials of nsplit splits then the merge, or the final
+// output directly with one split); split_total >= 1: partials only, of splits split_base ..
+// split_base + nsplit - 1 of a workspace holding split_total splits per row.
 int sparse_mqa_impl(const void* q, int64_t B, int64_t S, int H, int D, int fmt, int nope, const int64_t* positions,
                     const void* win, int64_t win_batch_entries, int win_cap, int window, const void* dense,
                     int64_t dense_batch_entries, int dense_cap, int dense_ratio, const void* main_kv,
                     int64_t main_batch_entries, int64_t G, const int32_t* idx, int64_t idx_row_stride, int topk,
                     const float* sinks, int nsplit, float* workspace, int64_t workspace_bytes, void* out, float* lse,
-                    const void* rope_cos, const void* rope_sin, int rope_dim, void* stream) {
+                    const void* rope_cos, const void* rope_sin, int rope_dim, int split_base, int split_total,
+                    void* stream) {
+  const bool part_only = split_total >= 1;
   MZK_CHECK_ARG(B >= 0 && S >= 0 && H >= 1 && D > 0, "sparse_mqa: bad sizes");
   if (rope_cos || rope_sin) {
     MZK_CHECK_ARG(rope_cos && rope_sin, "sparse_mqa_rope: cos and sin go together");
@@ -1201,14 +1208,23 @@ int sparse_mqa_impl(const void* q, int64_t B, int64_t S, int H, int D, int fmt, 
   }
   MZK_CHECK_ARG(fmt == 0 || fmt == 1, "sparse_mqa: fmt must be 0 (bf16) or 1 (fp8-b128)");
   MZK_CHECK_ARG(nsplit >= 1 && nsplit <= 65535, "sparse_mqa: nsplit must be in [1, 65535]");
-  MZK_CHECK_ARG(window >= 1 && win != nullptr, "sparse_mqa: a window source (window >= 1) is required");
+  if (part_only) {
+    MZK_CHECK_ARG(window == 0 || win != nullptr, "sparse_mqa_part: a window of %d entries needs its cache", window);
+    MZK_CHECK_ARG(window >= 0, "sparse_mqa_part: negative window");
+    MZK_CHECK_ARG(split_base >= 0 && split_base + static_cast<int64_t>(nsplit) <= split_total,
+                  "sparse_mqa_part: splits %d .. %d exceed the workspace's %d", split_base, split_base + nsplit - 1,
+                  split_total);
+    MZK_CHECK_ARG(out == nullptr && lse == nullptr, "sparse_mqa_part: writes partials only");
+  } else {
+    MZK_CHECK_ARG(window >= 1 && win != nullptr, "sparse_mqa: a window source (window >= 1) is required");
+  }
   MZK_CHECK_ARG(win_cap == 0 || win_cap >= window, "sparse_mqa: ring capacity smaller than the window");
   MZK_CHECK_ARG(!dense || (dense_ratio >= 1 && dense_cap >= 0), "sparse_mqa: dense source needs ratio >= 1");
   MZK_CHECK_ARG(!main_kv || (idx && topk >= 0 && G >= 0 && idx_row_stride >= topk && main_batch_entries >= G),
                 "sparse_mqa: sparse source needs idx [rows, >= topk] and main_batch_entries >= G");
   const int64_t rows = B * S;
   if (rows == 0) return MZK_OK;
-  MZK_CHECK_ARG(q && positions && (nsplit > 1 || (out && lse)), "sparse_mqa: null pointer");
+  MZK_CHECK_ARG(q && positions && (part_only || nsplit > 1 || (out && lse)), "sparse_mqa: null pointer");
   MZK_CHECK_ARG((out == nullptr) == (lse == nullptr), "sparse_mqa: out and lse go together");
   MZK_CHECK_ARG(rows <= 0x7fffffff, "sparse_mqa: too many rows");
   {
@@ -1218,8 +1234,9 @@ int sparse_mqa_impl(const void* q, int64_t B, int64_t S, int H, int D, int fmt, 
     MZK_CHECK_ARG(chunk <= kIdxCap, "sparse_mqa: %lld entries per split exceed %d; use nsplit >= %lld",
                   (long long)chunk, kIdxCap, (long long)((total_max + kIdxCap - 33) / (kIdxCap - 32)));
   }
-  if (nsplit > 1) {
-    const int64_t need = rows * nsplit * static_cast<int64_t>(H) * (2 * D + 8);
+  const int stride = part_only ? split_total : nsplit;
+  if (part_only || nsplit > 1) {
+    const int64_t need = rows * stride * static_cast<int64_t>(H) * (2 * D + 8);
     MZK_CHECK_ARG(workspace && workspace_bytes >= need, "sparse_mqa: workspace needs %lld bytes", (long long)need);
   }
   MZK_CHECK_ARG(aligned16(q) && aligned16(win) && aligned16(dense) && aligned16(main_kv) && aligned16(workspace) &&
@@ -1250,15 +1267,22 @@ int sparse_mqa_impl(const void* q, int64_t B, int64_t S, int H, int D, int fmt, 
   p.nsplit = nsplit;
   p.out = static_cast<uint16_t*>(out);
   p.lse = lse;
-  p.part_o = reinterpret_cast<uint16_t*>(workspace);
-  p.part_ml = workspace ? reinterpret_cast<float*>(p.part_o + rows * nsplit * static_cast<int64_t>(H) * D) : nullptr;
+  p.split_stride = stride;
+  p.write_final = !part_only && nsplit == 1;
+  if (workspace) {
+    uint16_t* po = reinterpret_cast<uint16_t*>(workspace);
+    float* pml = reinterpret_cast<float*>(po + rows * stride * static_cast<int64_t>(H) * D);
+    const int base = part_only ? split_base : 0;
+    p.part_o = po + static_cast<int64_t>(base) * H * D;
+    p.part_ml = pml + static_cast<int64_t>(base) * H * 2;
+  }
   p.rope_cos = static_cast<const uint16_t*>(rope_cos);
   p.rope_sin = static_cast<const uint16_t*>(rope_sin);
   hipStream_t s = as_stream(stream);
   int rc = dispatch(fmt, D, nope, p, rows, s);
   if (rc) return rc;
   MZK_LAUNCH_CHECK("sparse_mqa");
-  if (nsplit > 1 && out != nullptr)
+  if (!part_only && nsplit > 1 && out != nullptr)
     return combine_impl(workspace, B, S, H, D, nsplit, sinks, rope_cos, rope_sin, rope_dim, out, lse, stream);
   return MZK_OK;
 }
@@ -1306,7 +1330,7 @@ extern "C" int mzk_sparse_mqa(const void* q, int64_t B, int64_t S, int H, int D,
   return sparse_mqa_impl(q, B, S, H, D, fmt, nope, positions, win, win_batch_entries, win_cap, window, dense,
                          dense_batch_entries, dense_cap, dense_ratio, main_kv, main_batch_entries, G, idx,
                          idx_row_stride, topk, sinks, nsplit, workspace, workspace_bytes, out, lse, nullptr, nullptr, 0,
-                         stream);
+                         0, -1, stream);
 }
 
 extern "C" int mzk_sparse_mqa_rope(const void* q, int64_t B, int64_t S, int H, int D, int fmt, int nope,
@@ -1320,7 +1344,21 @@ extern "C" int mzk_sparse_mqa_rope(const void* q, int64_t B, int64_t S, int H, i
   return sparse_mqa_impl(q, B, S, H, D, fmt, nope, positions, win, win_batch_entries, win_cap, window, dense,
                          dense_batch_entries, dense_cap, dense_ratio, main_kv, main_batch_entries, G, idx,
                          idx_row_stride, topk, sinks, nsplit, workspace, workspace_bytes, out, lse, rope_cos, rope_sin,
-                         rope_dim, stream);
+                         rope_dim, 0, -1, stream);
+}
+
+extern "C" int mzk_sparse_mqa_part(const void* q, int64_t B, int64_t S, int H, int D, int fmt, int nope,
+                                   const int64_t* positions, const void* win, int64_t win_batch_entries, int win_cap,
+                                   int window, const void* dense, int64_t dense_batch_entries, int dense_cap,
+                                   int dense_ratio, const void* main_kv, int64_t main_batch_entries, int64_t G,
+                                   const int32_t* idx, int64_t idx_row_stride, int topk, int nsplit, int split_base,
+                                   int split_total, float* workspace, int64_t workspace_bytes, const void* rope_cos,
+                                   const void* rope_sin, int rope_dim, void* stream) {
+  MZK_CHECK_ARG(split_total >= 1, "sparse_mqa_part: split_total must be >= 1");
+  return sparse_mqa_impl(q, B, S, H, D, fmt, nope, positions, win, win_batch_entries, win_cap, window, dense,
+                         dense_batch_entries, dense_cap, dense_ratio, main_kv, main_batch_entries, G, idx,
+                         idx_row_stride, topk, nullptr, nsplit, workspace, workspace_bytes, nullptr, nullptr, rope_cos,
+                         rope_sin, rope_dim, split_base, split_total, stream);
 }
 
 extern "C" int mzk_sparse_mqa_combine(const float* workspace, int64_t B, int64_t S, int H, int D, int nsplit,

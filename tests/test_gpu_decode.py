@@ -21,9 +21,9 @@ from tests.helpers import assert_attn_close, assert_topk_sets_match
 pytestmark = pytest.mark.gpu
 
 
-def _layer(dev, fmt, coarse=False, seed=0, pos=2047):
+def _layer(dev, fmt, coarse=False, seed=0, pos=2047, overlap=False):
     cfg = DecodeConfig(batch=4, max_groups=512, topk=128, index_format=fmt, nsplit=3,
-                       coarse_ratio=64 if coarse else 0, coarse_groups=32 if coarse else 0)
+                       coarse_ratio=64 if coarse else 0, coarse_groups=32 if coarse else 0, branch_overlap=overlap)
     gen = torch.Generator().manual_seed(seed)
     sinks = torch.randn(cfg.heads, generator=gen)
     layer = SparseDecodeLayer(cfg, dev, sinks=sinks)
@@ -72,9 +72,13 @@ def _oracle(layer, inputs, sinks):
     return torch.stack(outs), sc, mag
 
 
-@pytest.mark.parametrize("fmt,coarse", [("fp8", False), ("mxfp4", False), ("fp8", True)])
-def test_decode_step_matches_oracle(dev, fmt, coarse):
-    layer, inputs, sinks = _layer(dev, fmt, coarse)
+@pytest.mark.parametrize("fmt,coarse,overlap", [("fp8", False, False), ("mxfp4", False, False), ("fp8", True, False),
+                                                ("fp8", False, True), ("mxfp4", True, True)])
+def test_decode_step_matches_oracle(dev, fmt, coarse, overlap):
+    """overlap: the window / dense branches run in their own launch on a second stream and
+    write their own splits of the workspace (mzk_sparse_mqa_part), merged with the top-k
+    entries' splits by one combine."""
+    layer, inputs, sinks = _layer(dev, fmt, coarse, overlap=overlap)
     out = layer.step(*inputs).clone()
     ref, sc, mag = _oracle(layer, inputs, sinks)
     assert_topk_sets_match(layer.idx, sc[:, 0], mag[:, 0], layer.cfg.topk)
@@ -96,6 +100,17 @@ def test_graph_replay_matches_eager(dev):
     layer.static_inputs[0].copy_(q2)
     out2 = layer.replay().clone()
     assert torch.equal(out2, layer.step(q2, *inputs[1:]))
+
+
+def test_graph_replay_overlapped_branches(dev):
+    layer, inputs, _ = _layer(dev, "mxfp4", coarse=True, seed=5, overlap=True)
+    eager = layer.step(*inputs).clone()
+    layer.capture(*inputs)
+    for i in range(3):
+        torch.randn(1000, device=dev).sum()
+        out = layer.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i} differs from the eager step"
 
 
 def test_graph_advances_positions(dev):
