@@ -46,6 +46,33 @@ import torch
 from . import _lib, csa2_attn, indexer, quant
 
 
+class GroupedOutputProjection:
+    """The attention output's projection, ``wo_b(wo_a(o.reshape(..., G, -1)).flatten(-2))``:
+    ``DeepseekV41GroupedLinear`` (owlet1/attention.py:20-39; a block-diagonal projection of
+    each of the ``o_groups`` head groups to ``o_lora_rank``) then ``wo_b``
+    (owlet1/attention.py:233-235).  Both are plain GEMMs and run on hipBLASLt (torch's
+    ``bmm`` / ``linear``); the grouped weight is stored once as ``[G, H*D/G, r]``, so the
+    batched product's right operand is contiguous.  Input: o [..., H, D] with the inverse
+    RoPE already applied (what ``SparseDecodeLayer.step(..., rope=...)`` returns)."""
+
+    def __init__(self, wo_a_weight: torch.Tensor, wo_b_weight: torch.Tensor, o_groups: int):
+        g = o_groups
+        if wo_a_weight.shape[0] % g or wo_b_weight.shape[1] != wo_a_weight.shape[0]:
+            raise ValueError("GroupedOutputProjection: wo_a [G*r, H*D/G] and wo_b [hidden, G*r] expected")
+        self.groups = g
+        self.rank = wo_a_weight.shape[0] // g
+        self.in_per_group = wo_a_weight.shape[1]
+        self.wa = wo_a_weight.view(g, self.rank, self.in_per_group).transpose(1, 2).contiguous()
+        self.wb = wo_b_weight.contiguous()
+
+    def __call__(self, o: torch.Tensor) -> torch.Tensor:
+        lead = o.shape[:-2]
+        x = o.reshape(-1, self.groups, self.in_per_group).transpose(0, 1).contiguous()  # [G, N, H*D/G]
+        y = torch.bmm(x, self.wa)                                                         # [G, N, r]
+        y = y.transpose(0, 1).reshape(*lead, self.groups * self.rank)
+        return torch.nn.functional.linear(y, self.wb)
+
+
 @dataclass
 class DecodeConfig:
     batch: int
@@ -75,7 +102,8 @@ class DecodeConfig:
 
 class SparseDecodeLayer:
     def __init__(self, cfg: DecodeConfig, device, sinks: torch.Tensor | None = None,
-                 kv_norm_weight: torch.Tensor | None = None, kv_norm_eps: float = 1e-6):
+                 kv_norm_weight: torch.Tensor | None = None, kv_norm_eps: float = 1e-6,
+                 out_proj: GroupedOutputProjection | None = None):
         if cfg.index_format not in ("fp8", "mxfp4"):
             raise ValueError(f"index_format must be 'fp8' or 'mxfp4', got {cfg.index_format!r}")
         if cfg.index_format == "fp8" and cfg.index_dim != 128:
@@ -99,6 +127,7 @@ class SparseDecodeLayer:
         self.kv_norm_weight = None if kv_norm_weight is None else \
             kv_norm_weight.to(device=self.device, dtype=torch.bfloat16).contiguous()
         self.kv_norm_eps = float(kv_norm_eps)
+        self.out_proj = out_proj  # with it, step(..., rope=...) returns the projected output
         # per-step buffers (fixed addresses, so a captured graph can replay them)
         self.scores = torch.empty(b, 1, cfg.max_groups, dtype=torch.float32, device=self.device)
         self.idx = torch.empty(b, cfg.topk, dtype=torch.int32, device=self.device)
@@ -211,7 +240,7 @@ class SparseDecodeLayer:
         self._select_and_attend(q, (cos, sin))
         if advance:
             self.positions.add_(1)
-        return self.out
+        return self.out if self.out_proj is None else self.out_proj(self.out)
 
     def _select_and_attend(self, q, rope):
         """Top-k, then the attention over [window ; dense ; top-k entries] with the sink.  With

@@ -221,3 +221,24 @@ def test_decode_step_fused_graph_replay(dev):
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {i} differs from the eager step"
         assert torch.equal(layer.win, win_eager)
+
+
+def test_grouped_output_projection(dev):
+    """wo_b(wo_a(grouped)) of owlet1/attention.py:20-39, :233-235 against the reference's
+    steps in float32 on the CPU (GroupedLinear's view / transpose / bmm, then the linear);
+    bf16 operands, fp32 accumulation."""
+    from mzoo_amd.decode import GroupedOutputProjection
+    gen = torch.Generator().manual_seed(15)
+    b, h, d, groups, rank, hidden = 6, 128, 576, 8, 64, 256
+    o = torch.randn(b, h, d, generator=gen).bfloat16()
+    wa = (torch.randn(groups * rank, h * d // groups, generator=gen) * (h * d // groups) ** -0.5).bfloat16()
+    wb = (torch.randn(hidden, groups * rank, generator=gen) * (groups * rank) ** -0.5).bfloat16()
+    proj = GroupedOutputProjection(wa.to(dev), wb.to(dev), groups)
+    got = proj(o.to(dev)).float().cpu()
+    # the reference's formulation, float32
+    x = o.float().reshape(b, 1, groups, -1)
+    w = wa.float().view(groups, -1, x.shape[-1]).transpose(1, 2)
+    y = torch.bmm(x.reshape(-1, groups, x.shape[-1]).transpose(0, 1), w).transpose(0, 1).reshape(b, 1, groups, -1)
+    ref = torch.nn.functional.linear(y.flatten(2), wb.float())[:, 0]
+    assert got.shape == ref.shape
+    assert_attn_close(got, ref, name="projected output")
