@@ -79,6 +79,20 @@ int mzk_pack_latent_fp8_b128(const void* x, int dtype, int64_t rows, int nope, i
 int mzk_unpack_latent_fp8_b128(const uint8_t* cache, int64_t rows, int nope, int rope, void* y,
                                int dtype, void* stream);
 
+/* DeepSeek-V4.1 cache entries, FlashMLA's kv_cache_format ("V4.1" and "V4.1 fp4" rows):
+ *   fmt 0: [D e4m3 codes][D/32 e8m0 scale bytes] -- _fake_quant_fp8_block(x, 32)
+ *          (owlet1/quant.py:72-86; the window cache of owlet1/attention.py:154); D=512: 528 B
+ *   fmt 1: [D/2 e2m1 bytes, element 2i in the low nibble][D/16 e4m3 scale bytes]
+ *          -- _fake_quant_fp4_block(x, 16, e4m3_scales=True) (quant.py:49-66; the
+ *          compressed cache of attention.py:183); D=512: 288 B
+ * x [rows, D] (D a multiple of 32, dtype 0/1/2, 16-byte aligned); entry r goes to cache row
+ * dst_index[r] (or r when dst_index is NULL).  Unpacking gives exactly the fake-quantized
+ * values. */
+int mzk_pack_cache_v41(const void* x, int dtype, int64_t rows, int D, int fmt, uint8_t* out,
+                       const int64_t* dst_index, void* stream);
+int mzk_unpack_cache_v41(const uint8_t* cache, int64_t rows, int D, int fmt, void* y, int dtype,
+                         void* stream);
+
 /* Decode-step prologue in one launch, for one new token per batch row:
  *  (1) the token's latent kv [B, nope+rope] (kv_dtype) into its window-ring slot, entry
  *      b*win_batch_entries + positions[b] % win_cap of win_cache (FP8-b128 entries as

@@ -39,6 +39,8 @@ _SIGS = {
     "mzk_decode_prologue": [_P, _I32, _I64, _I32, _I32, _P, _P, _I64, _I32, _P, _I32, _I64, _I32, _I32, _P, _P, _P,
                             _P],
     "mzk_unpack_latent_fp8_b128": [_P, _I64, _I32, _I32, _P, _I32, _P],
+    "mzk_pack_cache_v41": [_P, _I32, _I64, _I32, _I32, _P, _P, _P],
+    "mzk_unpack_cache_v41": [_P, _I64, _I32, _I32, _P, _I32, _P],
     "mzk_topk_rows": [_P, _I64, _I64, _I64, _I32, _P, _I64, _P],
     "mzk_topk_workspace_bytes": [_I64, _I64, ctypes.POINTER(_I64)],
     "mzk_topk_rows_ws": [_P, _I64, _I64, _I64, _I32, _P, _I64, _P, _I64, _P],

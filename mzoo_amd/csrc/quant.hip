@@ -138,6 +138,67 @@ __global__ void dequant_mxfp4_kernel(const uint8_t* __restrict__ packed, const u
   for (int i = 0; i < 4; ++i) store_from_f32<DT>(y, t * 4 + i, e2m1_value((two >> (4 * i)) & 0xfu) * s);
 }
 
+// ---- DeepSeek-V4.1 cache entries (FlashMLA kv_cache_format) ---------------------------
+// fp8: [D e4m3 codes][D/32 e8m0 scale bytes]    -- _fake_quant_fp8_block(x, 32), owlet1/quant.py:72-86
+//      (the window cache's quantizer, owlet1/attention.py:154); D = 512 gives 528 bytes
+// fp4: [D/2 e2m1 bytes, element 2i in the low nibble][D/16 e4m3 scale bytes]
+//      -- _fake_quant_fp4_block(x, 16, e4m3_scales=True), quant.py:49-66 (the compressed
+//      cache's quantizer, attention.py:183); D = 512 gives 288 bytes
+// Thread t encodes elements 4t..4t+3 of the flattened [rows, D]; the 8 (fp8) or 4 (fp4)
+// threads of a scale block are consecutive lanes of one wave.
+__host__ __device__ constexpr int64_t v41_entry_bytes(int d, int fmt) { return fmt == 0 ? d + d / 32 : d / 2 + d / 16; }
+
+template <int DT, int FMT>
+__global__ void pack_v41_kernel(const void* __restrict__ x, int d, int64_t nthreads, const int64_t* __restrict__ dst,
+                                uint8_t* __restrict__ out) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= nthreads) return;
+  const int64_t row = (t * 4) / d;
+  const int c = static_cast<int>(t * 4 - row * d);
+  uint8_t* e = out + (dst ? dst[row] : row) * v41_entry_bytes(d, FMT);
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = load_as_f32<DT>(x, t * 4 + i);
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  if constexpr (FMT == 0) {
+    amax = wave_max_group(amax, 8);
+    const float sc = fp8_scale_from_amax(amax);
+    uint32_t word = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) word |= static_cast<uint32_t>(e4m3_encode(clampf(div_rn(v[i], sc), 448.0f))) << (8 * i);
+    *reinterpret_cast<uint32_t*>(e + c) = word;
+    if ((c & 31) == 0) e[d + c / 32] = static_cast<uint8_t>(__float_as_uint(sc) >> 23);
+  } else {
+    amax = wave_max_group(amax, 4);
+    const float sc = fp4_scale_from_amax(amax, true);
+    uint32_t q[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = e2m1_code(clampf(div_rn(v[i], sc), 6.0f));
+    *reinterpret_cast<uint16_t*>(e + c / 2) = static_cast<uint16_t>(q[0] | (q[1] << 4) | (q[2] << 8) | (q[3] << 12));
+    if ((c & 15) == 0) e[d / 2 + c / 16] = e4m3_encode(sc);
+  }
+}
+
+template <int DT, int FMT>
+__global__ void unpack_v41_kernel(const uint8_t* __restrict__ cache, int d, int64_t nthreads, void* __restrict__ y) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= nthreads) return;
+  const int64_t row = (t * 4) / d;
+  const int c = static_cast<int>(t * 4 - row * d);
+  const uint8_t* e = cache + row * v41_entry_bytes(d, FMT);
+  if constexpr (FMT == 0) {
+    const uint32_t word = *reinterpret_cast<const uint32_t*>(e + c);
+    const float sc = __uint_as_float(static_cast<uint32_t>(e[d + c / 32]) << 23);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) store_from_f32<DT>(y, t * 4 + i, e4m3_decode((word >> (8 * i)) & 0xffu) * sc);
+  } else {
+    const uint32_t two = *reinterpret_cast<const uint16_t*>(e + c / 2);
+    const float sc = e4m3_decode(e[d / 2 + c / 16]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) store_from_f32<DT>(y, t * 4 + i, e2m1_value((two >> (4 * i)) & 0xfu) * sc);
+  }
+}
+
 // ---- FP8-b128 latent entries ---------------------------------------------------------
 // One workgroup per row; thread t < nope/4 quantizes nope channels 4t..4t+3 (32 lanes per
 // 128-channel block), then the rope channels are rounded to bf16.
@@ -256,6 +317,23 @@ template <int DT>
 void launch_quant_fp8(const void* x, int64_t rows, int64_t n, int bs, uint8_t* codes, float* scales, hipStream_t s) {
   const int64_t nthreads = rows * n / 4;
   quant_fp8_block_kernel<DT><<<grid_for(nthreads, 256), 256, 0, s>>>(x, codes, scales, nthreads, bs / 4);
+}
+
+template <int DT>
+void launch_pack_v41_fp8(const void* x, int d, int64_t n, const int64_t* dst, uint8_t* out, hipStream_t s) {
+  pack_v41_kernel<DT, 0><<<grid_for(n, 256), 256, 0, s>>>(x, d, n, dst, out);
+}
+template <int DT>
+void launch_pack_v41_fp4(const void* x, int d, int64_t n, const int64_t* dst, uint8_t* out, hipStream_t s) {
+  pack_v41_kernel<DT, 1><<<grid_for(n, 256), 256, 0, s>>>(x, d, n, dst, out);
+}
+template <int DT>
+void launch_unpack_v41_fp8(const uint8_t* cache, int d, int64_t n, void* y, hipStream_t s) {
+  unpack_v41_kernel<DT, 0><<<grid_for(n, 256), 256, 0, s>>>(cache, d, n, y);
+}
+template <int DT>
+void launch_unpack_v41_fp4(const uint8_t* cache, int d, int64_t n, void* y, hipStream_t s) {
+  unpack_v41_kernel<DT, 1><<<grid_for(n, 256), 256, 0, s>>>(cache, d, n, y);
 }
 
 template <int DT>
@@ -437,5 +515,42 @@ extern "C" int mzk_unpack_latent_fp8_b128(const uint8_t* cache, int64_t rows, in
   if (rows == 0) return MZK_OK;
   MZK_DISPATCH_DT(dtype, launch_unpack_latent, cache, rows, nope, rope, y, as_stream(stream));
   MZK_LAUNCH_CHECK("unpack_latent_fp8_b128");
+  return MZK_OK;
+}
+
+extern "C" int mzk_pack_cache_v41(const void* x, int dtype, int64_t rows, int d, int fmt, uint8_t* out,
+                                  const int64_t* dst_index, void* stream) {
+  MZK_CHECK_ARG(rows >= 0 && d >= 32 && d % 32 == 0, "pack_cache_v41: D must be a positive multiple of 32 (got %d)", d);
+  MZK_CHECK_ARG(fmt == 0 || fmt == 1, "pack_cache_v41: fmt must be 0 (fp8, e8m0 per 32) or 1 (fp4, e4m3 per 16)");
+  if (rows == 0) return MZK_OK;
+  MZK_CHECK_ARG(x && out, "pack_cache_v41: null pointer");
+  MZK_CHECK_ARG(aligned16(x) && reinterpret_cast<uintptr_t>(out) % 4 == 0, "pack_cache_v41: x 16-byte, out 4-byte aligned");
+  const int64_t nthreads = rows * d / 4;
+  hipStream_t s = as_stream(stream);
+  if (fmt == 0) {
+    MZK_DISPATCH_DT(dtype, launch_pack_v41_fp8, x, d, nthreads, dst_index, out, s);
+  } else {
+    MZK_DISPATCH_DT(dtype, launch_pack_v41_fp4, x, d, nthreads, dst_index, out, s);
+  }
+  MZK_LAUNCH_CHECK("pack_cache_v41");
+  return MZK_OK;
+}
+
+extern "C" int mzk_unpack_cache_v41(const uint8_t* cache, int64_t rows, int d, int fmt, void* y, int dtype,
+                                    void* stream) {
+  MZK_CHECK_ARG(rows >= 0 && d >= 32 && d % 32 == 0, "unpack_cache_v41: D must be a positive multiple of 32 (got %d)",
+                d);
+  MZK_CHECK_ARG(fmt == 0 || fmt == 1, "unpack_cache_v41: fmt must be 0 (fp8) or 1 (fp4)");
+  if (rows == 0) return MZK_OK;
+  MZK_CHECK_ARG(cache && y, "unpack_cache_v41: null pointer");
+  MZK_CHECK_ARG(reinterpret_cast<uintptr_t>(cache) % 4 == 0, "unpack_cache_v41: cache must be 4-byte aligned");
+  const int64_t nthreads = rows * d / 4;
+  hipStream_t s = as_stream(stream);
+  if (fmt == 0) {
+    MZK_DISPATCH_DT(dtype, launch_unpack_v41_fp8, cache, d, nthreads, y, s);
+  } else {
+    MZK_DISPATCH_DT(dtype, launch_unpack_v41_fp4, cache, d, nthreads, y, s);
+  }
+  MZK_LAUNCH_CHECK("unpack_cache_v41");
   return MZK_OK;
 }

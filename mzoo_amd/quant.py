@@ -146,3 +146,59 @@ def unpack_latent_fp8_b128(entries: torch.Tensor, nope: int = ENTRY_NOPE, rope: 
     _lib.call("mzk_unpack_latent_fp8_b128", e.data_ptr(), rows, nope, rope, y.data_ptr(), _lib.dtype_code(dtype),
               _lib.stream_of(e))
     return y
+
+
+# ---- DeepSeek-V4.1 cache entries (FlashMLA kv_cache_format) -------------------------------
+V41_FORMATS = {"fp8": 0, "fp4": 1}
+
+
+def v41_entry_bytes(d: int, fmt: str) -> int:
+    """Bytes of one V4.1 cache entry of D channels: fp8 D + D/32 (528 at D=512), fp4
+    D/2 + D/16 (288 at D=512)."""
+    return d + d // 32 if fmt == "fp8" else d // 2 + d // 16
+
+
+def pack_cache_v41(x: torch.Tensor, fmt: str, out: torch.Tensor | None = None,
+                   dst_index: torch.Tensor | None = None) -> torch.Tensor:
+    """x [..., D] -> V4.1 entries uint8 [..., v41_entry_bytes(D, fmt)]: ``fmt`` "fp8" is
+    ``_fake_quant_fp8_block(x, 32)`` (owlet1/quant.py:72-86) stored as e4m3 codes then e8m0
+    scales, "fp4" is ``_fake_quant_fp4_block(x, 16, e4m3_scales=True)`` (quant.py:49-66)
+    stored as e2m1 nibbles then e4m3 scales.  With ``out`` (a cache viewed as [entries,
+    bytes]) and ``dst_index`` (int64 [rows]) the rows go to those entries."""
+    if fmt not in V41_FORMATS:
+        raise ValueError(f"pack_cache_v41: fmt must be 'fp8' or 'fp4', got {fmt!r}")
+    _lib.require_gpu(x)
+    d = x.shape[-1]
+    if d % 32:
+        raise ValueError(f"pack_cache_v41: D must be a multiple of 32, got {d}")
+    xc = x.contiguous()
+    rows = _rows(xc)
+    eb = v41_entry_bytes(d, fmt)
+    if out is None:
+        out = torch.empty(*x.shape[:-1], eb, dtype=torch.uint8, device=x.device)
+    if out.dtype != torch.uint8 or out.shape[-1] != eb or not out.is_contiguous():
+        raise ValueError(f"pack_cache_v41: out must be contiguous uint8 [..., {eb}]")
+    if dst_index is not None:
+        dst_index = dst_index.to(device=x.device, dtype=torch.int64).contiguous()
+        if dst_index.numel() != rows:
+            raise ValueError("pack_cache_v41: dst_index needs one entry per row")
+    elif out.numel() // eb < rows:
+        raise ValueError("pack_cache_v41: out holds fewer entries than x has rows")
+    _lib.call("mzk_pack_cache_v41", xc.data_ptr(), _lib.dtype_code(x.dtype), rows, d, V41_FORMATS[fmt],
+              out.data_ptr(), _lib.ptr(dst_index), _lib.stream_of(x))
+    return out
+
+
+def unpack_cache_v41(entries: torch.Tensor, d: int, fmt: str, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """V4.1 entries uint8 [..., bytes] -> the fake-quantized values [..., D]."""
+    if fmt not in V41_FORMATS:
+        raise ValueError(f"unpack_cache_v41: fmt must be 'fp8' or 'fp4', got {fmt!r}")
+    _lib.require_gpu(entries)
+    e = entries.contiguous()
+    if e.shape[-1] != v41_entry_bytes(d, fmt):
+        raise ValueError(f"unpack_cache_v41: entries of {v41_entry_bytes(d, fmt)} bytes expected")
+    rows = _rows(e)
+    y = torch.empty(*e.shape[:-1], d, dtype=dtype, device=e.device)
+    _lib.call("mzk_unpack_cache_v41", e.data_ptr(), rows, d, V41_FORMATS[fmt], y.data_ptr(), _lib.dtype_code(dtype),
+              _lib.stream_of(e))
+    return y

@@ -267,3 +267,19 @@ def dequant_fp8_block(codes, scales, block_size: int) -> np.ndarray:
     c = np.asarray(codes, np.uint8)
     v = e4m3_decode(c).reshape(*c.shape[:-1], -1, block_size) * np.asarray(scales, F32)[..., None]
     return v.reshape(c.shape)
+
+
+def pack_cache_v41(x, fmt: str) -> np.ndarray:
+    """DeepSeek-V4.1 cache entries (FlashMLA ``kv_cache_format`` rows "V4.1" / "V4.1 fp4",
+    ``layers/attn/fp_attn_notes.md:1123-1131``) of x [..., D]: "fp8" = the e4m3 codes of
+    ``_fake_quant_fp8_block(x, 32)`` then their e8m0 scale bytes; "fp4" = the e2m1 codes of
+    ``_fake_quant_fp4_block(x, 16, e4m3_scales=True)`` two per byte (element 2i low) then
+    their e4m3 scale bytes."""
+    x = np.asarray(x, F32)
+    lead = x.shape[:-1]
+    if fmt == "fp8":
+        codes, scales = fp8_block_codes(x, 32)
+        return np.concatenate([codes.astype(np.uint8), e8m0_from_pow2(scales).reshape(*lead, -1)], -1)
+    codes, scales = fp4_block_codes(x, 16, e4m3_scales=True)
+    packed = ((codes[..., 0::2] & 0xF) | ((codes[..., 1::2] & 0xF) << 4)).astype(np.uint8)
+    return np.concatenate([packed, e4m3_encode(scales).astype(np.uint8).reshape(*lead, -1)], -1)

@@ -159,3 +159,30 @@ def test_decode_prologue_bit_exact(dev, fmt):
         p_ref, e_ref = Q.quant_mxfp4(q.float().numpy())
         assert np.array_equal(codes.cpu().numpy(), p_ref)
         assert np.array_equal(e8.cpu().numpy(), e_ref)
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "fp4"])
+@pytest.mark.parametrize("d", [512, 576])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_pack_cache_v41_bit_exact(dev, fmt, d, dtype):
+    """V4.1 cache entries (FlashMLA kv_cache_format): the packed bytes equal the oracle's,
+    the unpacked values equal the reference quantizer's, and dst_index scatters rows."""
+    from mzoo_amd import quant as MQ
+    gen = torch.Generator().manual_seed(d + (7 if fmt == "fp4" else 0))
+    # rows spread over about 2^-9 .. 2^9 in scale; values stay below 6 * 448, the largest
+    # amax an e4m3 fp4 scale represents (a larger one makes the reference's scale NaN)
+    x = (torch.randn(37, d, generator=gen).clamp(-4, 4) * torch.exp(torch.randn(37, 1, generator=gen).clamp(-4, 4) * 1.5))
+    x = x.to(dtype)
+    x[0, :32] = 0
+    x[1, 5] = 2000.0 if dtype != torch.float16 else 1000.0
+    xf = x.float().numpy()
+    got = MQ.pack_cache_v41(x.to(dev), fmt)
+    assert np.array_equal(got.cpu().numpy(), Q.pack_cache_v41(xf, fmt))
+    back = MQ.unpack_cache_v41(got, d, fmt).cpu().numpy()
+    ref = Q.fake_quant_fp8_block(xf, 32) if fmt == "fp8" else Q.fake_quant_fp4_block(xf, 16, e4m3_scales=True)
+    assert np.array_equal(back, ref)
+    # scattered into a cache of 64 entries
+    cache = torch.zeros(64, MQ.v41_entry_bytes(d, fmt), dtype=torch.uint8, device=dev)
+    dst = torch.randperm(64, generator=gen)[:37]
+    MQ.pack_cache_v41(x.to(dev), fmt, out=cache, dst_index=dst)
+    assert torch.equal(cache[dst.to(dev)], got)

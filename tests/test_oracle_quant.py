@@ -169,3 +169,43 @@ def test_packed_formats_roundtrip():
     assert np.array_equal(Q.dequant_mxfp4(p, s), Q.fake_quant_fp4_block(x[:, :128], 32))
     c, sc = Q.fp8_block_codes(x[:, :128], 128)
     assert np.array_equal(Q.dequant_fp8_block(c, sc, 128), Q.fake_quant_fp8_block(x[:, :128], 128))
+
+
+def _decode_v41(entries, d, fmt):
+    """The V4.1 entry layout read back independently of the packer (codes, then scales)."""
+    e = np.asarray(entries, np.uint8)
+    if fmt == "fp8":
+        codes, sc = e[..., :d], e[..., d:d + d // 32]
+        vals = Q.e4m3_decode(codes).reshape(*e.shape[:-1], d // 32, 32)
+        scale = Q.e8m0_decode(sc)
+        return (vals * scale[..., None]).reshape(*e.shape[:-1], d)
+    nib = e[..., :d // 2]
+    codes = np.stack([nib & 0xF, nib >> 4], -1).reshape(*e.shape[:-1], d)
+    vals = Q.FP4_TABLE[codes.astype(np.int64)].reshape(*e.shape[:-1], d // 16, 16)
+    scale = Q.e4m3_decode(e[..., d // 2:d // 2 + d // 16])
+    return (vals * scale[..., None]).reshape(*e.shape[:-1], d)
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "fp4"])
+def test_v41_cache_entries_decode_to_fake_quant(fmt):
+    """FlashMLA's V4.1 rows (fp_attn_notes.md:1123-1131): 528 / 288 bytes per 512-channel
+    token, and the entry decodes exactly to the reference quantizer the cache stands for."""
+    rng = np.random.default_rng(21)
+    x = (rng.standard_normal((5, 512)) * rng.uniform(1e-3, 300, (5, 1))).astype(np.float32)
+    x[0, :32] = 0.0                       # an all-zero scale block
+    # a block with a large outlier (within the e4m3 scale's range, amax / 6 <= 448, for fp4)
+    x[1, 40] = 448.0 * 2.0 ** 20 if fmt == "fp8" else 2000.0
+    e = Q.pack_cache_v41(x, fmt)
+    assert e.shape == (5, 528 if fmt == "fp8" else 288) and e.dtype == np.uint8
+    ref = Q.fake_quant_fp8_block(x, 32) if fmt == "fp8" else Q.fake_quant_fp4_block(x, 16, e4m3_scales=True)
+    assert np.array_equal(_decode_v41(e, 512, fmt), ref)
+
+
+def test_v41_fp4_nibble_order():
+    """Element 2i sits in the low nibble: a block whose first value is its amax (code 7 =
+    6.0 x scale) and whose second is 0 packs its first byte as 0x07."""
+    x = np.zeros((1, 32), np.float32)
+    x[0, 0] = 3.0
+    e = Q.pack_cache_v41(x, "fp4")
+    assert e[0, 0] == 0x07
+    assert Q.e4m3_decode(e[0, 16:17])[0] == np.float32(0.5)   # scale amax / 6 = 0.5, exact in e4m3
