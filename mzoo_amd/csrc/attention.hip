@@ -220,7 +220,7 @@ struct RowPlan {
 
   // The row's entry list split, given its absolute position.
   __device__ void plan(const AttnParams& p, int64_t row_pos) {
-    pos = row_pos;
+    pos = row_pos < -1 ? -1 : row_pos;  // a negative position sees no window or dense entry
     nw = static_cast<int>(pos + 1 < p.window ? pos + 1 : p.window);
     int nd = 0;
     if (p.dense) {

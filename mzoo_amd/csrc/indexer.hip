@@ -525,24 +525,27 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
       }
       if constexpr (APPEND) {
         // FP8-b128 latent entry (as pack_latent_row): threads t < nope/4 hold 4 nope
-        // channels each (32 lanes per 128-channel block), threads t < rope one rope channel
-        const int64_t entry_bytes = p.nope + 4 * (p.nope / 128) + 2 * p.rope;
-        uint8_t* e = p.win + (b * p.win_batch_entries + pos % p.win_cap) * entry_bytes;
-        if (tid < p.nope / 4) {
-          const float v[4] = {bf16_to_f32(static_cast<uint16_t>(kv_nope.x & 0xffffu)),
-                              bf16_to_f32(static_cast<uint16_t>(kv_nope.x >> 16)),
-                              bf16_to_f32(static_cast<uint16_t>(kv_nope.y & 0xffffu)),
-                              bf16_to_f32(static_cast<uint16_t>(kv_nope.y >> 16))};
-          float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-          am = wave_max_group(am, 32);
-          const float sc = fp8_scale_from_amax(am);
-          uint32_t word = 0;
+        // channels each (32 lanes per 128-channel block), threads t < rope one rope channel;
+        // a negative position has no ring slot
+        if (pos >= 0) {
+          const int64_t entry_bytes = p.nope + 4 * (p.nope / 128) + 2 * p.rope;
+          uint8_t* e = p.win + (b * p.win_batch_entries + pos % p.win_cap) * entry_bytes;
+          if (tid < p.nope / 4) {
+            const float v[4] = {bf16_to_f32(static_cast<uint16_t>(kv_nope.x & 0xffffu)),
+                                bf16_to_f32(static_cast<uint16_t>(kv_nope.x >> 16)),
+                                bf16_to_f32(static_cast<uint16_t>(kv_nope.y & 0xffffu)),
+                                bf16_to_f32(static_cast<uint16_t>(kv_nope.y >> 16))};
+            float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+            am = wave_max_group(am, 32);
+            const float sc = fp8_scale_from_amax(am);
+            uint32_t word = 0;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) word |= static_cast<uint32_t>(e4m3_encode(clampf(div_rn(v[i], sc), 448.0f))) << (8 * i);
-          reinterpret_cast<uint32_t*>(e)[tid] = word;
-          if ((tid & 31) == 0) reinterpret_cast<float*>(e + p.nope)[tid >> 5] = sc;
+            for (int i = 0; i < 4; ++i) word |= static_cast<uint32_t>(e4m3_encode(clampf(div_rn(v[i], sc), 448.0f))) << (8 * i);
+            reinterpret_cast<uint32_t*>(e)[tid] = word;
+            if ((tid & 31) == 0) reinterpret_cast<float*>(e + p.nope)[tid >> 5] = sc;
+          }
+          if (tid < p.rope) reinterpret_cast<uint16_t*>(e + p.nope + 4 * (p.nope / 128))[tid] = kv_rope;
         }
-        if (tid < p.rope) reinterpret_cast<uint16_t*>(e + p.nope + 4 * (p.nope / 128))[tid] = kv_rope;
       }
     }
   }

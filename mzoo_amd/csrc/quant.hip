@@ -245,7 +245,9 @@ __global__ void __launch_bounds__(256) decode_prologue_kernel(
   const int64_t blk = blockIdx.x;
   if (blk < B) {
     const int64_t entry_bytes = nope + 4 * (nope / 128) + 2 * rope;
-    const int64_t slot = blk * win_batch_entries + positions[blk] % win_cap;
+    const int64_t pos = positions[blk];
+    if (pos < 0) return;  // no ring slot for a negative position
+    const int64_t slot = blk * win_batch_entries + pos % win_cap;
     pack_latent_row<DT>(kv, nope, rope, blk, win + slot * entry_bytes, threadIdx.x);
   } else {
     const int64_t t = (blk - B) * 256 + threadIdx.x;

@@ -242,3 +242,34 @@ def test_grouped_output_projection(dev):
     ref = torch.nn.functional.linear(y.flatten(2), wb.float())[:, 0]
     assert got.shape == ref.shape
     assert_attn_close(got, ref, name="projected output")
+
+
+@pytest.mark.parametrize("path", ["decode_fp8", "decode_fused"])
+def test_negative_position_appends_nothing(dev, path):
+    """A row at position -1 has no ring slot: its window ring stays as it was (the other
+    rows append as usual) and all its scores are -inf."""
+    b, hi, g, wcap = 4, 64, 512, 128
+    gen = torch.Generator().manual_seed(16)
+    pos = torch.tensor([5, -1, 300, -1], dtype=torch.int64, device=dev)
+    kv = torch.randn(b, 576, generator=gen).bfloat16().to(dev)
+    q_idx = torch.randn(b, hi, 128, generator=gen).bfloat16().to(dev)
+    w = (torch.randn(b, hi, generator=gen) * hi ** -0.5).to(dev)
+    kc, ks = quant.quant_fp8_block(torch.randn(b, g, 128, generator=gen).bfloat16().to(dev), 128)
+    ks = ks[..., 0].contiguous()
+    win0 = torch.randint(0, 256, (b, wcap, 656), generator=gen, dtype=torch.uint8).to(dev)
+    win = win0.clone()
+    print(f"negative position: {path}", flush=True)
+    if path == "decode_fp8":
+        scores = indexer.decode_fp8(q_idx, w, kc, ks, compress_ratio=4, positions=pos, kv=kv, win_cache=win)
+    else:
+        cs = _tables([5, 0, 300, 0], THETA, dev)
+        scores = indexer.decode_fused(q_idx, w, kc, ks, fmt="fp8", compress_ratio=4, positions=pos, q_rope=cs, kv=kv,
+                                      kv_weight=torch.ones(576, dtype=torch.bfloat16, device=dev), kv_eps=1e-6,
+                                      kv_rope=cs, win_cache=win)
+    torch.cuda.synchronize()
+    for r in (1, 3):
+        assert torch.equal(win[r], win0[r]), f"row {r} (position -1) changed its ring"
+        assert bool(torch.isinf(scores[r]).all()) and bool((scores[r] < 0).all())
+    for r, p_ in ((0, 5), (2, 300)):
+        changed = (win[r] != win0[r]).any(-1)
+        assert bool(changed[p_ % wcap]) and int(changed.sum()) == 1, f"row {r}: exactly slot {p_ % wcap} is written"
