@@ -1128,19 +1128,19 @@ int dispatch_heads(const AttnParams& p, int64_t rows, hipStream_t s) {
     static_assert(M::LDS + 4 * kSplitIdxCap + 8 * kTile * 8 + 64 <= 160 * 1024, "LDS budget");
     auto kern = sparse_mqa_dsplit_kernel<FMT, D, NOPE>;
     // the dynamic-LDS limit is a per-device function attribute: set once per device
-    static bool attr_set[kMaxDevices] = {};
+    static std::atomic<bool> attr_set[kMaxDevices] = {};  // setting it twice is harmless
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
       set_last_error("sparse_mqa: no usable current device");
       return MZK_ELAUNCH;
     }
-    if (!attr_set[dev]) {
+    if (!attr_set[dev].load(std::memory_order_acquire)) {
       if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                               M::LDS) != hipSuccess) {
         set_last_error("sparse_mqa: cannot raise the kernel's LDS limit to %d bytes", M::LDS);
         return MZK_ELAUNCH;
       }
-      attr_set[dev] = true;
+      attr_set[dev].store(true, std::memory_order_release);
     }
     return launch_kernel(kern, M::LDS, 512, 64, p, rows, s);
   } else {

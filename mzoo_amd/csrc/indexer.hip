@@ -824,19 +824,19 @@ extern "C" int mzk_indexer_scores_fp8(const uint8_t* q_codes, const float* q_sca
     const int64_t nblocks = B * nqb;
     MZK_CHECK_ARG(nblocks <= 0x7fffffff, "indexer_scores_fp8: %lld workgroups exceed the grid limit", (long long)nblocks);
     // the staged query rows need more than the default dynamic-LDS limit: set once per device
-    static bool attr_set[kMaxDevices] = {};
+    static std::atomic<bool> attr_set[kMaxDevices] = {};  // setting it twice is harmless
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
       set_last_error("indexer_scores_fp8: no usable current device");
       return MZK_ELAUNCH;
     }
-    if (!attr_set[dev]) {
+    if (!attr_set[dev].load(std::memory_order_acquire)) {
       if (hipFuncSetAttribute(reinterpret_cast<const void*>(indexer_prefill_fp8_kernel),
                               hipFuncAttributeMaxDynamicSharedMemorySize, kPfLds) != hipSuccess) {
         set_last_error("indexer_scores_fp8: cannot raise the prefill kernel's LDS limit to %d bytes", kPfLds);
         return MZK_ELAUNCH;
       }
-      attr_set[dev] = true;
+      attr_set[dev].store(true, std::memory_order_release);
     }
     indexer_prefill_fp8_kernel<<<static_cast<unsigned>(nblocks), kWaves * 64, kPfLds, as_stream(stream)>>>(prm, nqb);
   } else {
