@@ -212,8 +212,11 @@ struct RowPlan {
       hgrp = static_cast<int>(L0 % nhg);
       unit = L0 / nhg;
     }
-    const uint32_t row32 = unit / static_cast<uint32_t>(p.nsplit);
+    uint32_t row32 = unit / static_cast<uint32_t>(p.nsplit);
     split = static_cast<int>(unit - row32 * static_cast<uint32_t>(p.nsplit));
+    // with several rows per batch (prefill) a row's entry count grows with its position:
+    // the last rows go first, so the longest workgroups do not form the tail
+    if (p.S > 1) row32 = static_cast<uint32_t>(p.rows) - 1u - row32;
     row = row32;
     b = row32 / static_cast<uint32_t>(p.S);
   }
