@@ -895,7 +895,12 @@ extern "C" int mzk_topk_rows(const float* scores, int64_t rows, int64_t cols, in
   hipStream_t s = as_stream(stream);
   const int G = static_cast<int>(cols);
   const unsigned nr = static_cast<unsigned>(rows);
-  if (G <= 8 * kThreads)
+  // short rows take a workgroup sized to them (8 keys per thread), long ones 1024 threads
+  if (G <= 8 * 256)
+    topk_rows_reg_kernel<8, 256><<<nr, 256, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
+  else if (G <= 8 * 512)
+    topk_rows_reg_kernel<8, 512><<<nr, 512, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
+  else if (G <= 8 * kThreads)
     topk_rows_reg_kernel<8, kThreads><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
   else if (G <= 16 * kThreads)
     topk_rows_reg_kernel<16, kThreads><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
