@@ -104,6 +104,27 @@ __device__ __forceinline__ float load_as_f32(const void* p, int64_t i) {
   else return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
 }
 
+// Elements i .. i+3 (i a multiple of 4) as fp32: one 8- or 16-byte load when `vec` (the
+// caller has checked that the base pointer is 16-byte aligned), else four element loads.
+template <int DT>
+__device__ __forceinline__ void load4_as_f32(const void* p, int64_t i, bool vec, float (&v)[4]) {
+  if (vec) {
+    if constexpr (DT == MZK_F32) {
+      const float4 f = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+      v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+    } else {
+      const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
+      const uint16_t h[4] = {static_cast<uint16_t>(u.x & 0xffffu), static_cast<uint16_t>(u.x >> 16),
+                             static_cast<uint16_t>(u.y & 0xffffu), static_cast<uint16_t>(u.y >> 16)};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[k] = DT == MZK_BF16 ? bf16_to_f32(h[k]) : f16_to_f32(h[k]);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = load_as_f32<DT>(p, i + k);
+  }
+}
+
 // Round fp32 to the dtype and store (the ".to(x.dtype)" of the reference).
 template <int DT>
 __device__ __forceinline__ void store_from_f32(void* p, int64_t i, float v) {
@@ -263,6 +284,20 @@ __device__ __forceinline__ float lane_xor(float v) {
     return __shfl_xor(v, 32, 64);
   }
 }
+
+// Maximum over aligned groups of `group` consecutive lanes (a power of two <= 32), by
+// exact xor-partner exchanges; every lane of a group ends with the group's maximum.
+__device__ __forceinline__ float group_max(float v, int group) {
+  if (group > 16) v = fmaxf(v, lane_xor<16>(v));
+  if (group > 8) v = fmaxf(v, lane_xor<8>(v));
+  if (group > 4) v = fmaxf(v, lane_xor<4>(v));
+  if (group > 2) v = fmaxf(v, lane_xor<2>(v));
+  if (group > 1) v = fmaxf(v, lane_xor<1>(v));
+  return v;
+}
+
+// 1 / s for a power of two s in [2^-126, 2^126] (exact): the exponent negated
+__device__ __forceinline__ float pow2_reciprocal(float s) { return __uint_as_float((254u << 23) - __float_as_uint(s)); }
 
 // Maximum of v >= 0 over the 16 lanes of each DPP row, in the row's last lane (lane 15 of
 // the row); the shifts bring in 0 from beyond the row, which a maximum of values >= 0

@@ -69,34 +69,37 @@ __global__ void fake_quant_serial_kernel(const void* __restrict__ x, void* __res
 // one amax (lane shuffles), so groups must not straddle a wave.
 template <int DT>
 __device__ __forceinline__ void quant_fp8_4(const void* __restrict__ x, uint8_t* __restrict__ codes,
-                                            float* __restrict__ scales, int64_t t, int group) {
+                                            float* __restrict__ scales, int64_t t, int group, bool vec) {
   const int64_t base = t * 4;
   float v[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = load_as_f32<DT>(x, base + i);
+  load4_as_f32<DT>(x, base, vec, v);
   float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-  amax = wave_max_group(amax, group);
+  amax = group_max(amax, group);
   const float s = fp8_scale_from_amax(amax);
-  uint32_t word = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) word |= static_cast<uint32_t>(e4m3_encode(clampf(div_rn(v[i], s), 448.0f))) << (8 * i);
+  // x / s == x * (1 / s) exactly (s is a power of two in [2^-22, 2^120] for finite input,
+  // 1 / s a normal float), and v_cvt_pk_fp8_f32 is the e4m3 encoder (round to nearest even)
+  // for |x| <= 448; an infinite amax keeps the division's behaviour through 1 / s
+  const float inv = s <= 0x1p120f ? pow2_reciprocal(s) : 1.0f / s;
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(clampf(v[0] * inv, 448.0f), clampf(v[1] * inv, 448.0f), 0, false);
+  const uint32_t word = static_cast<uint32_t>(
+      __builtin_amdgcn_cvt_pk_fp8_f32(clampf(v[2] * inv, 448.0f), clampf(v[3] * inv, 448.0f), lo, true));
   reinterpret_cast<uint32_t*>(codes)[t] = word;
   if ((t % group) == 0) scales[t / group] = s;
 }
 
 template <int DT>
 __device__ __forceinline__ void quant_mxfp4_4(const void* __restrict__ x, uint8_t* __restrict__ packed,
-                                              uint8_t* __restrict__ e8m0, int64_t t) {
+                                              uint8_t* __restrict__ e8m0, int64_t t, bool vec) {
   const int64_t base = t * 4;
   float v[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = load_as_f32<DT>(x, base + i);
+  load4_as_f32<DT>(x, base, vec, v);
   float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
   amax = wave_max_group(amax, 8);
   const float s = fp4_scale_from_amax(amax, false);
+  const float inv = 1.0f / s;  // a power of two: x * inv == x / s exactly
   uint32_t c[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) c[i] = e2m1_code(clampf(div_rn(v[i], s), 6.0f));
+  for (int i = 0; i < 4; ++i) c[i] = e2m1_code(clampf(v[i] * inv, 6.0f));
   const uint16_t two = static_cast<uint16_t>(c[0] | (c[1] << 4) | (c[2] << 8) | (c[3] << 12));
   reinterpret_cast<uint16_t*>(packed)[t] = two;
   if ((t & 7) == 0) e8m0[t >> 3] = static_cast<uint8_t>(__float_as_uint(s) >> 23);
@@ -104,16 +107,16 @@ __device__ __forceinline__ void quant_mxfp4_4(const void* __restrict__ x, uint8_
 
 template <int DT>
 __global__ void quant_fp8_block_kernel(const void* __restrict__ x, uint8_t* __restrict__ codes,
-                                       float* __restrict__ scales, int64_t nthreads, int group) {
+                                       float* __restrict__ scales, int64_t nthreads, int group, bool vec) {
   const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (t < nthreads) quant_fp8_4<DT>(x, codes, scales, t, group);
+  if (t < nthreads) quant_fp8_4<DT>(x, codes, scales, t, group, vec);
 }
 
 template <int DT>
 __global__ void quant_mxfp4_kernel(const void* __restrict__ x, uint8_t* __restrict__ packed,
-                                   uint8_t* __restrict__ e8m0, int64_t nthreads) {
+                                   uint8_t* __restrict__ e8m0, int64_t nthreads, bool vec) {
   const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (t < nthreads) quant_mxfp4_4<DT>(x, packed, e8m0, t);
+  if (t < nthreads) quant_mxfp4_4<DT>(x, packed, e8m0, t, vec);
 }
 
 template <int DT>
@@ -241,7 +244,7 @@ template <int DT, int QDT, bool MX>
 __global__ void __launch_bounds__(256) decode_prologue_kernel(
     const void* __restrict__ kv, int64_t B, int nope, int rope, const int64_t* __restrict__ positions,
     uint8_t* __restrict__ win, int64_t win_batch_entries, int win_cap, const void* __restrict__ q, int64_t qthreads,
-    int qgroup, uint8_t* __restrict__ qcodes, float* __restrict__ qscales, uint8_t* __restrict__ qe8m0) {
+    int qgroup, uint8_t* __restrict__ qcodes, float* __restrict__ qscales, uint8_t* __restrict__ qe8m0, bool qvec) {
   const int64_t blk = blockIdx.x;
   if (blk < B) {
     const int64_t entry_bytes = nope + 4 * (nope / 128) + 2 * rope;
@@ -252,8 +255,8 @@ __global__ void __launch_bounds__(256) decode_prologue_kernel(
   } else {
     const int64_t t = (blk - B) * 256 + threadIdx.x;
     if (t < qthreads) {
-      if constexpr (MX) quant_mxfp4_4<QDT>(q, qcodes, qe8m0, t);
-      else quant_fp8_4<QDT>(q, qcodes, qscales, t, qgroup);
+      if constexpr (MX) quant_mxfp4_4<QDT>(q, qcodes, qe8m0, t, qvec);
+      else quant_fp8_4<QDT>(q, qcodes, qscales, t, qgroup, qvec);
     }
   }
 }
@@ -318,7 +321,7 @@ void launch_fake(const void* x, void* y, int64_t rows, int64_t n, int bs, bool f
 template <int DT>
 void launch_quant_fp8(const void* x, int64_t rows, int64_t n, int bs, uint8_t* codes, float* scales, hipStream_t s) {
   const int64_t nthreads = rows * n / 4;
-  quant_fp8_block_kernel<DT><<<grid_for(nthreads, 256), 256, 0, s>>>(x, codes, scales, nthreads, bs / 4);
+  quant_fp8_block_kernel<DT><<<grid_for(nthreads, 256), 256, 0, s>>>(x, codes, scales, nthreads, bs / 4, aligned16(x));
 }
 
 template <int DT>
@@ -341,7 +344,7 @@ void launch_unpack_v41_fp4(const uint8_t* cache, int d, int64_t n, void* y, hipS
 template <int DT>
 void launch_quant_mxfp4(const void* x, int64_t rows, int64_t n, uint8_t* packed, uint8_t* e8m0, hipStream_t s) {
   const int64_t nthreads = rows * n / 4;
-  quant_mxfp4_kernel<DT><<<grid_for(nthreads, 256), 256, 0, s>>>(x, packed, e8m0, nthreads);
+  quant_mxfp4_kernel<DT><<<grid_for(nthreads, 256), 256, 0, s>>>(x, packed, e8m0, nthreads, aligned16(x));
 }
 
 template <int DT>
@@ -380,10 +383,10 @@ int launch_prologue(const void* kv, int64_t B, int nope, int rope, const int64_t
   const unsigned grid = static_cast<unsigned>(B + (qthreads + 255) / 256);
   if (qfmt == 0)
     decode_prologue_kernel<DT, QDT, false><<<grid, 256, 0, s>>>(kv, B, nope, rope, positions, win, wbe, wcap, q,
-                                                                 qthreads, 32, qcodes, qscales, qe8m0);
+                                                                 qthreads, 32, qcodes, qscales, qe8m0, aligned16(q));
   else
     decode_prologue_kernel<DT, QDT, true><<<grid, 256, 0, s>>>(kv, B, nope, rope, positions, win, wbe, wcap, q,
-                                                                qthreads, 8, qcodes, qscales, qe8m0);
+                                                                qthreads, 8, qcodes, qscales, qe8m0, aligned16(q));
   return MZK_OK;
 }
 
