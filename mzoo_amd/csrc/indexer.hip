@@ -397,7 +397,7 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
     const float sc = fp4_scale_from_amax(amax, false);
     // x / sc == x * (1 / sc) exactly: sc is a power of two in [2^-126, 2^127], so 1 / sc is
     // exact and both sides are the correctly rounded x * 2^-e
-    const float inv = 1.0f / sc;
+    const float inv = sc <= 0x1p126f ? pow2_reciprocal(sc) : 1.0f / sc;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t wv[4] = {qr[i].x, qr[i].y, qr[i].z, qr[i].w};
@@ -438,10 +438,10 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
-    amax = wave_max_group(amax, 4);  // the 4 threads of a head are consecutive lanes
+    amax = group_max(amax, 4);  // the 4 threads of a head are consecutive lanes
     const float sc = fp8_scale_from_amax(amax);
-    // x / sc == x * (1 / sc) exactly: sc is a power of two in [2^-22, 2^127]
-    const float inv = 1.0f / sc;
+    // x / sc == x * (1 / sc) exactly: sc is a power of two, in [2^-22, 2^120] for finite input
+    const float inv = sc <= 0x1p120f ? pow2_reciprocal(sc) : 1.0f / sc;
     uint32_t wd[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
