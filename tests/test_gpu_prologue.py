@@ -139,9 +139,9 @@ def _attention_inputs(dev, seed, b=4, pos=1500):
     return layer, idx, q
 
 
-@pytest.mark.parametrize("nsplit", [1, 4])
-def test_sparse_mqa_rope(dev, nsplit):
-    layer, idx, q = _attention_inputs(dev, seed=12)
+@pytest.mark.parametrize("nsplit,pos", [(1, 1500), (4, 1500), (4, 9)])
+def test_sparse_mqa_rope(dev, nsplit, pos):
+    layer, idx, q = _attention_inputs(dev, seed=12, pos=pos)
     cfg = layer.cfg
     pos = int(layer.positions[0])
     print(f"sparse_mqa rope: nsplit {nsplit} position {pos}", flush=True)
@@ -157,8 +157,9 @@ def test_sparse_mqa_rope(dev, nsplit):
     win = torch.from_numpy(Q.unpack_latent_fp8_b128(layer.win.cpu().numpy()))
     main = torch.from_numpy(Q.unpack_latent_fp8_b128(layer.main.cpu().numpy()))
     outs = []
+    nw = min(cfg.window, pos + 1)
     for r in range(cfg.batch):
-        toks = [(pos - cfg.window + 1 + i) % cfg.window for i in range(cfg.window)]
+        toks = [(pos - nw + 1 + i) % cfg.window for i in range(nw)]
         sel = idx[r].cpu()
         ents = torch.cat([win[r, toks], main[r, sel[sel >= 0].long()]])
         outs.append(OA.attend_entries(q_rot[r].float().cpu(), ents, layer.sinks.cpu())[0])
@@ -195,9 +196,10 @@ def _step_layers(dev, fmt, coarse, seed, pos=2047):
     return layers, (q, kv, q_idx, w), rope, kv_w
 
 
-@pytest.mark.parametrize("fmt,coarse", [("fp8", False), ("mxfp4", False), ("mxfp4", True)])
-def test_decode_step_fused_matches_unfused(dev, fmt, coarse):
-    (lf, lu), (q, kv, q_idx, w), rope, kv_w = _step_layers(dev, fmt, coarse, seed=13)
+@pytest.mark.parametrize("fmt,coarse,pos", [("fp8", False, 2047), ("mxfp4", False, 2047), ("mxfp4", True, 2047),
+                                            ("fp8", False, 6)])
+def test_decode_step_fused_matches_unfused(dev, fmt, coarse, pos):
+    (lf, lu), (q, kv, q_idx, w), rope, kv_w = _step_layers(dev, fmt, coarse, seed=13, pos=pos)
     print(f"decode step fused {fmt} coarse={coarse}", flush=True)
     out_f = lf.step(q, kv, q_idx, w, rope=rope).clone()
     cs, ics = rope[:2], rope[2:]
