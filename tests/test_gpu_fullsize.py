@@ -146,3 +146,49 @@ def test_prefill_config3_full_size(dev):
         ref_o, ref_lse = OA.attend_entries(q_c[i], ents, sinks.cpu())
         assert_attn_close(o[0, tq], ref_o, name=f"o[t={tq}]")
         torch.testing.assert_close(lse_c[:, i], ref_lse.float(), atol=2e-3, rtol=2e-3, msg=f"lse[t={tq}]")
+
+
+@pytest.mark.parametrize("name", ["config2", "config5"])
+def test_decode_step_fused_full_size(dev, name):
+    """The fused prologue / epilogue at full size: a layer stepped on the raw projections
+    with the RoPE tables equals, bit for bit, an identically filled layer stepped on the
+    oracle's normed and rotated inputs (window ring, top-k, output after the inverse RoPE)."""
+    import numpy as np
+    from oracle import compressor as C
+    b, pos, groups, fmt, cr, cg, nsplit = DECODE[name]
+    gen = torch.Generator(device=dev).manual_seed(31)
+    rnd = lambda *shape: torch.randn(*shape, generator=gen, device=dev)  # noqa: E731
+    cfg = DecodeConfig(batch=b, max_groups=groups, topk=2048, index_format=fmt, nsplit=nsplit, coarse_ratio=cr,
+                       coarse_groups=cg)
+    d = cfg.dim
+    sinks, kv_w = rnd(cfg.heads), (1.0 + 0.1 * rnd(d)).bfloat16()
+    hist = (rnd(b, cfg.window, d).bfloat16(), rnd(b, groups, d).bfloat16(), rnd(b, groups, cfg.index_dim).bfloat16(),
+            rnd(b, max(cg, 1), d).bfloat16())
+    layers = []
+    for _ in range(2):
+        layer = SparseDecodeLayer(cfg, dev, sinks=sinks, kv_norm_weight=kv_w)
+        layer.fill_window(hist[0], pos - 1)
+        layer.append_groups(0, hist[1], hist[2])
+        if cr:
+            layer.fill_coarse(hist[3][:, :cg])
+        layer.set_positions(pos)
+        layers.append(layer)
+    q, kv, q_idx = rnd(b, cfg.heads, d).bfloat16(), (3 * rnd(b, d)).bfloat16(), rnd(b, 64, 128).bfloat16()
+    w = rnd(b, 64) * 0.125
+    tabs = []
+    for theta in (10000.0, 160000.0):
+        c, s = C.rope_tables(np.full(b, pos), 64, theta)
+        tabs += [torch.from_numpy(c).bfloat16().to(dev), torch.from_numpy(s).bfloat16().to(dev)]
+    print(f"{name}: fused step at full size, B={b} G={groups}", flush=True)
+    out_f = layers[0].step(q, kv, q_idx, w, rope=tuple(tabs)).clone()
+    f = lambda t: t.float().cpu().numpy()  # noqa: E731
+    cos, sin, icos, isin = (f(t) for t in tabs)
+    q_rot = torch.from_numpy(C.rope(f(q), cos[:, None], sin[:, None], dtype="bfloat16")).bfloat16().to(dev)
+    qi_rot = torch.from_numpy(C.rope(f(q_idx), icos[:, None], isin[:, None], dtype="bfloat16")).bfloat16().to(dev)
+    kv_rot = torch.from_numpy(C.decode_kv_latent(f(kv), f(kv_w), 1e-6, cos, sin)).bfloat16().to(dev)
+    out_u = layers[1].step(q_rot, kv_rot, qi_rot, w).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(layers[0].win, layers[1].win), "window rings differ"
+    assert torch.equal(layers[0].idx, layers[1].idx), "top-k differs"
+    back = torch.from_numpy(C.rope(f(out_u), cos[:, None], sin[:, None], inverse=True, dtype="bfloat16")).bfloat16()
+    assert torch.equal(out_f.cpu(), back)
