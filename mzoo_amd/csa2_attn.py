@@ -98,6 +98,22 @@ def sparse_mqa_decode(q: torch.Tensor, positions: torch.Tensor, win_cache: torch
     rotation to the output (``owlet1/attention.py:147`` and ``:226`` fused in)."""
     b, h, d = q.shape
     _lib.require_gpu(q, positions, win_cache)
+    # the kernels read these buffers through raw pointers with the layouts below: a wrong
+    # dtype or a strided view would be read as other data, so it is rejected, not converted
+    checks = (("q", q, torch.bfloat16, (b, h, d)), ("positions", positions, torch.int64, None),
+              ("win_cache", win_cache, torch.uint8, None), ("main_cache", main_cache, torch.uint8, None),
+              ("dense_cache", dense_cache, torch.uint8, None), ("indices", indices, torch.int32, None),
+              ("sinks", sinks, torch.float32, (h,)), ("out", out, torch.bfloat16, (b, h, d)),
+              ("lse", lse, torch.float32, (b, h)))
+    for name, t, dt, shape in checks:
+        if t is None:
+            continue
+        if t.dtype != dt or not t.is_contiguous() or (shape is not None and tuple(t.shape) != shape):
+            raise ValueError(f"sparse_mqa_decode: {name} must be a contiguous {dt} tensor"
+                             + (f" of shape {list(shape)}" if shape is not None else "")
+                             + f", got {t.dtype} {list(t.shape)}{'' if t.is_contiguous() else ' (strided)'}")
+    if positions.numel() != b or (indices is not None and (indices.dim() != 2 or indices.shape[0] != b)):
+        raise ValueError("sparse_mqa_decode: positions [B] and indices [B, topk] expected")
     rc = rs = None
     if rope is not None:
         rc, rs = (t.contiguous() for t in rope)

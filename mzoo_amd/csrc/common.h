@@ -188,19 +188,37 @@ __device__ __forceinline__ float e4m3_decode(uint32_t c) {
 // s = pow2ceil(max(amax, 1e-4) * fp32(1/448)); codes are e4m3(clamp(x / s, +-448)).
 constexpr float kInv448 = 1.0f / 448.0f;  // the fp32-rounded reciprocal the reference multiplies by
 
-__device__ __forceinline__ float fp8_scale_from_amax(float amax) {
-  return pow2_ceil(fmaxf(amax, 1e-4f) * kInv448);
+// Maximum of two values that are >= 0 or NaN (block maxima of |x|), as the integer maximum
+// of their bit patterns: for such values the patterns order as the values do, and a NaN
+// (any payload, sign cleared by fabsf) sorts above +inf -- so a NaN anywhere in a block
+// makes its maximum NaN, as torch's amax does (fmaxf would drop it).
+__device__ __forceinline__ float nn_max(float a, float b) {
+  return __uint_as_float(max(__float_as_uint(a), __float_as_uint(b)));
 }
 
-__device__ __forceinline__ float clampf(float v, float lim) { return fminf(fmaxf(v, -lim), lim); }
+// max |v[i]| over four values, NaN-propagating (see nn_max).
+__device__ __forceinline__ float abs_max4(const float (&v)[4]) {
+  return nn_max(nn_max(fabsf(v[0]), fabsf(v[1])), nn_max(fabsf(v[2]), fabsf(v[3])));
+}
+
+// The floors of the reference's scales are torch clamp_min calls, which keep a NaN amax:
+// nn_max keeps it too.  pow2_ceil maps a NaN or infinite amax to an infinite scale, so
+// x / s is 0 for finite x and the dequantized block is NaN (0 * inf), as in the reference.
+__device__ __forceinline__ float fp8_scale_from_amax(float amax) {
+  return pow2_ceil(nn_max(amax, 1e-4f) * kInv448);
+}
+
+// clamp(v, -lim, lim) keeping NaN, like torch's clamp (fminf / fmaxf would turn a NaN
+// into one of the bounds).
+__device__ __forceinline__ float clampf(float v, float lim) { return v != v ? v : fminf(fmaxf(v, -lim), lim); }
 
 // FP4 block scale of the reference's fake quantizer (owlet1/quant.py:49-66): ue8m0
 // pow2ceil(max(amax, 6*2^-126) * fp32(1/6)), or with e4m3 scales e4m3(max(amax, 6*2^-9) / 6).
 constexpr float kInv6 = 1.0f / 6.0f;  // the fp32-rounded reciprocal the reference multiplies by
 
 __device__ __forceinline__ float fp4_scale_from_amax(float amax, bool e4m3_scales) {
-  if (e4m3_scales) return e4m3_decode(e4m3_encode(div_rn(fmaxf(amax, 0x1.8p-7f /* 6*2^-9 */), 6.0f)));
-  return pow2_ceil(fmaxf(amax, 0x1.8p-124f /* 6*2^-126 */) * kInv6);
+  if (e4m3_scales) return e4m3_decode(e4m3_encode(div_rn(nn_max(amax, 0x1.8p-7f /* 6*2^-9 */), 6.0f)));
+  return pow2_ceil(nn_max(amax, 0x1.8p-124f /* 6*2^-126 */) * kInv6);
 }
 
 // ------------------------------------------------------------------------------------
@@ -259,8 +277,10 @@ __device__ __forceinline__ uint32_t rope_pair_bf16(uint32_t pair, float c, float
 // ------------------------------------------------------------------------------------
 // wave helpers (wave64)
 // ------------------------------------------------------------------------------------
+// Maximum of values >= 0 or NaN (block maxima of |x|; NaN wins, see nn_max) over aligned
+// groups of `group` consecutive lanes.
 __device__ __forceinline__ float wave_max_group(float v, int group) {
-  for (int m = group >> 1; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  for (int m = group >> 1; m >= 1; m >>= 1) v = nn_max(v, __shfl_xor(v, m, 64));
   return v;
 }
 
@@ -285,36 +305,37 @@ __device__ __forceinline__ float lane_xor(float v) {
   }
 }
 
-// Maximum over aligned groups of `group` consecutive lanes (a power of two <= 32), by
-// exact xor-partner exchanges; every lane of a group ends with the group's maximum.
+// Maximum of values >= 0 or NaN (NaN wins, see nn_max) over aligned groups of `group`
+// consecutive lanes (a power of two <= 32), by exact xor-partner exchanges; every lane of a
+// group ends with the group's maximum.
 __device__ __forceinline__ float group_max(float v, int group) {
-  if (group > 16) v = fmaxf(v, lane_xor<16>(v));
-  if (group > 8) v = fmaxf(v, lane_xor<8>(v));
-  if (group > 4) v = fmaxf(v, lane_xor<4>(v));
-  if (group > 2) v = fmaxf(v, lane_xor<2>(v));
-  if (group > 1) v = fmaxf(v, lane_xor<1>(v));
+  if (group > 16) v = nn_max(v, lane_xor<16>(v));
+  if (group > 8) v = nn_max(v, lane_xor<8>(v));
+  if (group > 4) v = nn_max(v, lane_xor<4>(v));
+  if (group > 2) v = nn_max(v, lane_xor<2>(v));
+  if (group > 1) v = nn_max(v, lane_xor<1>(v));
   return v;
 }
 
 // 1 / s for a power of two s in [2^-126, 2^126] (exact): the exponent negated
 __device__ __forceinline__ float pow2_reciprocal(float s) { return __uint_as_float((254u << 23) - __float_as_uint(s)); }
 
-// Maximum of v >= 0 over the 16 lanes of each DPP row, in the row's last lane (lane 15 of
-// the row); the shifts bring in 0 from beyond the row, which a maximum of values >= 0
-// ignores.
+// Maximum of v >= 0 or NaN (NaN wins, see nn_max) over the 16 lanes of each DPP row, in
+// the row's last lane (lane 15 of the row); the shifts bring in 0 from beyond the row,
+// which a maximum of values >= 0 ignores.
 __device__ __forceinline__ float row_max_nonneg(float v) {
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x111, 0xF, 0xF, true)));
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x112, 0xF, 0xF, true)));
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x114, 0xF, 0xF, true)));
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x118, 0xF, 0xF, true)));
+  v = nn_max(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x111, 0xF, 0xF, true)));
+  v = nn_max(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x112, 0xF, 0xF, true)));
+  v = nn_max(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x114, 0xF, 0xF, true)));
+  v = nn_max(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x118, 0xF, 0xF, true)));
   return v;
 }
 
-// Maximum of v >= 0 over the wave, as a wave-uniform value.
+// Maximum of v >= 0 or NaN over the wave, as a wave-uniform value.
 __device__ __forceinline__ float wave_max_nonneg(float v) {
   const int r = __float_as_int(row_max_nonneg(v));
-  return fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(r, 15)), __int_as_float(__builtin_amdgcn_readlane(r, 31))),
-               fmaxf(__int_as_float(__builtin_amdgcn_readlane(r, 47)), __int_as_float(__builtin_amdgcn_readlane(r, 63))));
+  return nn_max(nn_max(__int_as_float(__builtin_amdgcn_readlane(r, 15)), __int_as_float(__builtin_amdgcn_readlane(r, 31))),
+                nn_max(__int_as_float(__builtin_amdgcn_readlane(r, 47)), __int_as_float(__builtin_amdgcn_readlane(r, 63))));
 }
 
 }  // namespace mzk

@@ -219,7 +219,7 @@ struct FusedKv {
     float scs[4], invs[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      scs[k] = fp8_scale_from_amax(wave_max_nonneg(fmaxf(fabsf(y[2 * k]), fabsf(y[2 * k + 1]))));
+      scs[k] = fp8_scale_from_amax(wave_max_nonneg(nn_max(fabsf(y[2 * k]), fabsf(y[2 * k + 1]))));
       // x / sc == x * (1 / sc) exactly: sc is a power of two in [2^-22, 2^127]
       invs[k] = 1.0f / scs[k];
     }
@@ -391,7 +391,7 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
       for (int j = 0; j < 4; ++j) {
         const float lo = qh < Hi ? bf16_to_f32(static_cast<uint16_t>(wv[j] & 0xffffu)) : 0.0f;
         const float hi2 = qh < Hi ? bf16_to_f32(static_cast<uint16_t>(wv[j] >> 16)) : 0.0f;
-        amax = fmaxf(amax, fmaxf(fabsf(lo), fabsf(hi2)));
+        amax = nn_max(amax, nn_max(fabsf(lo), fabsf(hi2)));
       }
     }
     const float sc = fp4_scale_from_amax(amax, false);
@@ -437,7 +437,7 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
     }
     float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
+    for (int i = 0; i < 32; ++i) amax = nn_max(amax, fabsf(x[i]));
     amax = group_max(amax, 4);  // the 4 threads of a head are consecutive lanes
     const float sc = fp8_scale_from_amax(amax);
     // x / sc == x * (1 / sc) exactly: sc is a power of two, in [2^-22, 2^120] for finite input
@@ -535,7 +535,7 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
                                 bf16_to_f32(static_cast<uint16_t>(kv_nope.x >> 16)),
                                 bf16_to_f32(static_cast<uint16_t>(kv_nope.y & 0xffffu)),
                                 bf16_to_f32(static_cast<uint16_t>(kv_nope.y >> 16))};
-            float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+            float am = abs_max4(v);
             am = wave_max_group(am, 32);
             const float sc = fp8_scale_from_amax(am);
             uint32_t word = 0;

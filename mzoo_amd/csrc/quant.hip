@@ -25,7 +25,7 @@ __global__ void fake_quant_kernel(const void* __restrict__ x, void* __restrict__
   float v[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) v[i] = load_as_f32<DT>(x, base + i);
-  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  float amax = abs_max4(v);
   amax = wave_max_group(amax, group);
   if constexpr (FP4) {
     const float s = fp4_scale_from_amax(amax, e4m3_scales);
@@ -52,7 +52,7 @@ __global__ void fake_quant_serial_kernel(const void* __restrict__ x, void* __res
   if (j >= nblocks) return;
   const int64_t base = j * bs;
   float amax = 0.0f;
-  for (int i = 0; i < bs; ++i) amax = fmaxf(amax, fabsf(load_as_f32<DT>(x, base + i)));
+  for (int i = 0; i < bs; ++i) amax = nn_max(amax, fabsf(load_as_f32<DT>(x, base + i)));
   const float s = FP4 ? fp4_scale_from_amax(amax, e4m3_scales) : fp8_scale_from_amax(amax);
   for (int i = 0; i < bs; ++i) {
     const float v = load_as_f32<DT>(x, base + i);
@@ -73,7 +73,7 @@ __device__ __forceinline__ void quant_fp8_4(const void* __restrict__ x, uint8_t*
   const int64_t base = t * 4;
   float v[4];
   load4_as_f32<DT>(x, base, vec, v);
-  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  float amax = abs_max4(v);
   amax = group_max(amax, group);
   const float s = fp8_scale_from_amax(amax);
   // x / s == x * (1 / s) exactly (s is a power of two in [2^-22, 2^120] for finite input,
@@ -93,7 +93,7 @@ __device__ __forceinline__ void quant_mxfp4_4(const void* __restrict__ x, uint8_
   const int64_t base = t * 4;
   float v[4];
   load4_as_f32<DT>(x, base, vec, v);
-  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  float amax = abs_max4(v);
   amax = wave_max_group(amax, 8);
   const float s = fp4_scale_from_amax(amax, false);
   const float inv = 1.0f / s;  // a power of two: x * inv == x / s exactly
@@ -162,7 +162,7 @@ __global__ void pack_v41_kernel(const void* __restrict__ x, int d, int64_t nthre
   float v[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) v[i] = load_as_f32<DT>(x, t * 4 + i);
-  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  float amax = abs_max4(v);
   if constexpr (FMT == 0) {
     amax = wave_max_group(amax, 8);
     const float sc = fp8_scale_from_amax(amax);
@@ -216,7 +216,7 @@ __device__ __forceinline__ void pack_latent_row(const void* __restrict__ x, int 
     float v[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = load_as_f32<DT>(x, xrow + 4 * t + i);
-    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    float amax = abs_max4(v);
     amax = wave_max_group(amax, 32);
     const float s = fp8_scale_from_amax(amax);
     uint32_t word = 0;

@@ -257,13 +257,18 @@ class SparseDecodeLayer:
                                         nope=cfg.nope, workspace=self.workspace, out=self.out, lse=self.lse,
                                         rope=rope)
             return
-        qc = q.contiguous()
+        # the side stream reads q and the RoPE tables while the main stream runs on: they
+        # must be the caller's own tensors, not temporaries the caching allocator could hand
+        # to main-stream work before the side-stream launch has read them
+        qc = q
         _lib.require_gpu(qc)
-        if qc.dtype != torch.bfloat16 or qc.shape != (b, cfg.heads, cfg.dim):
-            raise ValueError(f"step: q must be bf16 [{b}, {cfg.heads}, {cfg.dim}]")
+        if qc.dtype != torch.bfloat16 or qc.shape != (b, cfg.heads, cfg.dim) or not qc.is_contiguous():
+            raise ValueError(f"step: q must be a contiguous bf16 [{b}, {cfg.heads}, {cfg.dim}] tensor")
         rc = rs = None
         if rope is not None:
-            rc, rs = (t.contiguous() for t in rope)
+            rc, rs = rope[0], rope[1]
+            if not (rc.is_contiguous() and rs.is_contiguous()):
+                raise ValueError("step(branch_overlap): the RoPE tables must be contiguous")
         total = self.nsplit_wd + cfg.nsplit
         ws = self.workspace
         wsb = ws.numel() * ws.element_size()

@@ -150,3 +150,45 @@ def test_split_groups_carry():
         assert usable % ratio == 0 and 0 <= buffered < ratio
         emitted += usable // ratio
     assert emitted == (5 + 1 + 1 + 1 + 9 + 0 + 3) // ratio
+
+
+def test_rope_is_complex_multiplication():
+    """norm_rope.py:128-131 names the convention: the (even, odd) pairs of the rope slice are
+    complex numbers ``view_as_complex(x.unflatten(-1, (-1, 2)))`` multiplied by
+    ``cos + i sin``; the inverse multiplies by the conjugate.  Checked against torch's
+    complex arithmetic (not a restatement of the oracle's real-arithmetic formula), so a
+    flipped sign of ``sin`` or swapped pair order fails here."""
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((3, 5, 4, 96)).astype(np.float32)
+    cos, sin = C.rope_tables(rng.integers(0, 1 << 20, (3, 5)), 32, 10000.0)
+    got = C.rope(x, cos[:, :, None], sin[:, :, None])
+    z = torch.view_as_complex(torch.from_numpy(x[..., 64:]).double().unflatten(-1, (-1, 2)).contiguous())
+    rot = torch.complex(torch.from_numpy(cos).double(), torch.from_numpy(sin).double())[:, :, None]
+    want = torch.view_as_real(z * rot).flatten(-2).numpy()
+    assert np.allclose(got[..., 64:], want, rtol=0, atol=2e-6)
+    assert np.array_equal(got[..., :64], x[..., :64])
+    inv = C.rope(x, cos[:, :, None], sin[:, :, None], inverse=True)
+    want_inv = torch.view_as_real(z * rot.conj()).flatten(-2).numpy()
+    assert np.allclose(inv[..., 64:], want_inv, rtol=0, atol=2e-6)
+
+
+def test_rope_quarter_turn_closed_form():
+    """cos = 0, sin = 1 is multiplication by i: (e, o) -> (-o, e); the inverse gives (o, -e)."""
+    x = np.arange(1, 9, dtype=np.float32).reshape(1, 8)
+    c, s = np.zeros((1, 2), np.float32), np.ones((1, 2), np.float32)
+    assert C.rope(x, c, s).tolist() == [[1, 2, 3, 4, -6, 5, -8, 7]]
+    assert C.rope(x, c, s, inverse=True).tolist() == [[1, 2, 3, 4, 6, -5, 8, -7]]
+
+
+def test_rope_tables_closed_form():
+    """inv_freq_i = theta^(-2i/rd) (dsv4 modeling_deepseek_v41.py:127-137): pair 0 rotates by
+    the position itself, pair i by pos * theta^(-2i/rd); checked in float64 math."""
+    pos = np.array([0, 1, 2, 3, 1000, 65535], np.float64)
+    for rd, theta in ((64, 10000.0), (32, 160000.0)):
+        cos, sin = C.rope_tables(pos, rd, theta)
+        assert np.allclose(cos[:, 0], np.cos(pos), atol=1e-6) and np.allclose(sin[:, 0], np.sin(pos), atol=1e-6)
+        i = np.arange(rd // 2)
+        ang = pos[:, None] * theta ** (-2.0 * i / rd)
+        # fp32 angle rounding grows with the position: |pos * inv_freq| ulp
+        tol = 4 * np.abs(ang) * 2.0 ** -24 + 1e-6
+        assert np.all(np.abs(cos - np.cos(ang)) <= tol) and np.all(np.abs(sin - np.sin(ang)) <= tol)

@@ -209,3 +209,34 @@ def test_v41_fp4_nibble_order():
     e = Q.pack_cache_v41(x, "fp4")
     assert e[0, 0] == 0x07
     assert Q.e4m3_decode(e[0, 16:17])[0] == np.float32(0.5)   # scale amax / 6 = 0.5, exact in e4m3
+
+
+def test_nonfinite_blocks_follow_torch_semantics():
+    """A NaN or an infinity in a block: the reference's torch ops keep it through ``amax``
+    and ``clamp_min`` (checked here on the library), ``_pow2_ceil_scale`` of a NaN / inf is
+    2^129 / 2^128 = inf, so ``x / scale`` is 0 (or NaN) and the block dequantizes to NaN
+    everywhere (0 * inf); an e4m3 scale above e4m3's range casts to NaN.  Blocks without
+    such values are untouched by their neighbours."""
+    t = torch.tensor([[1.0, float("nan"), 2.0]])
+    assert torch.isnan(t.abs().amax(-1)).all() and torch.isnan(t.abs().amax(-1).clamp_min(1e-4)).all()
+    assert torch.isnan(torch.tensor([float("nan")]).clamp(-448.0, 448.0)).all()
+    e4 = torch.tensor([float("nan"), float("inf"), 500.0, 470.0]).to(torch.float8_e4m3fn).float()
+    assert torch.isnan(e4).all()
+    assert math.isinf(float(torch.exp2(torch.tensor(129.0))))
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((6, 64)).astype(np.float32)
+    x[0, 5], x[1, 40], x[2, 17], x[3, :] = np.nan, np.inf, -np.inf, 5000.0
+    with np.errstate(all="ignore"):
+        for fq, bs, bad in ((lambda v: Q.fake_quant_fp8_block(v, 32), 32, {(0, 0), (1, 1), (2, 0)}),
+                            (lambda v: Q.fake_quant_fp4_block(v, 32), 32, {(0, 0), (1, 1), (2, 0)}),
+                            (lambda v: Q.fake_quant_fp4_block(v, 16, True), 16,
+                             {(0, 0), (1, 2), (2, 1), (3, 0), (3, 1), (3, 2), (3, 3)})):
+            y = fq(x)
+            clean = fq(np.nan_to_num(x, nan=0.0, posinf=0.0, neginf=0.0))
+            for r in range(6):
+                for blk in range(64 // bs):
+                    sl = y[r, blk * bs:(blk + 1) * bs]
+                    if (r, blk) in bad:
+                        assert np.isnan(sl).all(), (r, blk)
+                    elif not np.isnan(x[r, blk * bs:(blk + 1) * bs]).any() and np.isfinite(x[r, blk * bs:(blk + 1) * bs]).all():
+                        assert np.array_equal(sl, clean[r, blk * bs:(blk + 1) * bs]), (r, blk)
