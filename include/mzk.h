@@ -339,6 +339,27 @@ int mzk_sparse_mqa_combine_rope(const float* workspace, int64_t B, int64_t S, in
                                 const void* rope_sin, int rope_dim, void* out, float* lse,
                                 void* stream);
 
+/* mzk_sparse_mqa_rope without a workspace, for callers that cannot allocate (code under
+ * HIP-graph capture that must not call hipMalloc, tight serving loops, harnesses that forbid
+ * allocation).  No counterpart in the reference: it is mzk_sparse_mqa_rope with the split
+ * partials kept in a file-scope device array of MZK_NOALLOC_SCRATCH_BYTES bytes (one copy
+ * per GPU the library runs on, held until the process ends) instead of `workspace`; it
+ * never allocates.  rope_cos / rope_sin may be NULL (then it is mzk_sparse_mqa).  Limit:
+ * rows * nsplit * H * (2*D + 8) <= MZK_NOALLOC_SCRATCH_BYTES when nsplit > 1 (config 2:
+ * 32 x 4 x 128 x 1160 = 19 MB), else MZK_EINVAL.  Every call on one GPU shares that GPU's
+ * array, so calls that overlap on one GPU (concurrent streams, or host threads) race: the
+ * caller must order them, e.g. on one stream.  The device address is looked up
+ * (hipGetSymbolAddress) on the first call on each device: make that first call outside
+ * graph capture. */
+#define MZK_NOALLOC_SCRATCH_BYTES (32ll << 20)
+int mzk_sparse_mqa_noalloc(const void* q, int64_t B, int64_t S, int H, int D, int fmt, int nope,
+                           const int64_t* positions, const void* win, int64_t win_batch_entries, int win_cap,
+                           int window, const void* dense, int64_t dense_batch_entries, int dense_cap,
+                           int dense_ratio, const void* main_kv, int64_t main_batch_entries, int64_t G,
+                           const int32_t* idx, int64_t idx_row_stride, int topk, const float* sinks, int nsplit,
+                           void* out, float* lse, const void* rope_cos, const void* rope_sin, int rope_dim,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

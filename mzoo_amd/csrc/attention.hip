@@ -31,6 +31,8 @@
 // (unnormalized O, running max m, sum l) that mzk combine kernel merges with the sink.
 #include <type_traits>
 
+#include <mutex>
+
 #include "common.h"
 
 namespace mzk {
@@ -1362,6 +1364,64 @@ extern "C" int mzk_sparse_mqa_part(const void* q, int64_t B, int64_t S, int H, i
                          dense_batch_entries, dense_cap, dense_ratio, main_kv, main_batch_entries, G, idx,
                          idx_row_stride, topk, nullptr, nsplit, workspace, workspace_bytes, nullptr, nullptr, rope_cos,
                          rope_sin, rope_dim, split_base, split_total, stream);
+}
+
+// ---- the allocation-free form -------------------------------------------------------
+// The split partials live in a file-scope device array instead of a caller's workspace.
+// In host code `scratch` is only a stand-in symbol: its device address (one per GPU) comes
+// from hipGetSymbolAddress, taken once per device on that device's first call and kept.
+namespace {
+constexpr int64_t kScratchBytes = MZK_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The calling thread's current device's copy of `scratch` (nullptr + error text on failure).
+void* device_scratch() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_last_error("sparse_mqa_noalloc: no current HIP device (or device id >= %d)", kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      set_last_error("sparse_mqa_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                     hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" int mzk_sparse_mqa_noalloc(const void* q, int64_t B, int64_t S, int H, int D, int fmt, int nope,
+                                      const int64_t* positions, const void* win, int64_t win_batch_entries,
+                                      int win_cap, int window, const void* dense, int64_t dense_batch_entries,
+                                      int dense_cap, int dense_ratio, const void* main_kv, int64_t main_batch_entries,
+                                      int64_t G, const int32_t* idx, int64_t idx_row_stride, int topk,
+                                      const float* sinks, int nsplit, void* out, float* lse, const void* rope_cos,
+                                      const void* rope_sin, int rope_dim, void* stream) {
+  MZK_CHECK_ARG(B >= 0 && S >= 0 && H >= 1 && D > 0 && nsplit >= 1, "sparse_mqa_noalloc: bad sizes");
+  const int64_t need = nsplit > 1 ? B * S * nsplit * static_cast<int64_t>(H) * (2 * D + 8) : 0;
+  MZK_CHECK_ARG(need <= kScratchBytes,
+                "sparse_mqa_noalloc: %lld rows x %d splits x %d heads need %lld bytes of split partials, above the "
+                "%lld-byte scratch; use fewer splits or rows, or mzk_sparse_mqa with a workspace",
+                (long long)(B * S), nsplit, H, (long long)need, (long long)kScratchBytes);
+  float* ws = nullptr;
+  if (need > 0 && B * S > 0) {
+    ws = static_cast<float*>(device_scratch());
+    if (!ws) return MZK_ELAUNCH;
+  }
+  return sparse_mqa_impl(q, B, S, H, D, fmt, nope, positions, win, win_batch_entries, win_cap, window, dense,
+                         dense_batch_entries, dense_cap, dense_ratio, main_kv, main_batch_entries, G, idx,
+                         idx_row_stride, topk, sinks, nsplit, ws, need, out, lse, rope_cos, rope_sin, rope_dim, 0, -1,
+                         stream);
 }
 
 extern "C" int mzk_sparse_mqa_combine(const float* workspace, int64_t B, int64_t S, int H, int D, int nsplit,
