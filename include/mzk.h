@@ -130,6 +130,15 @@ int mzk_compress(const float* kv, const float* gate, int64_t B, int64_t n_groups
 int mzk_rope(const void* x, int dtype, const float* cos_t, const float* sin_t, int64_t rows,
              int D, int rope_dim, int heads, int inverse, void* y, void* stream);
 
+/* DeepseekV41RMSNorm.forward (owlet1/norm_rope.py:25-30) of any width:
+ *   out[r] = out_dtype( weight * x_dtype( h * (1 / sqrt(sum(h^2) / D + eps)) ) ),  h = fp32(x[r])
+ * the sum of squares in a fixed order (lane l of a wave sums channels l, l+64, ... from 0,
+ * then an xor butterfly), so results are reproducible bit for bit.  x [rows, D] with row
+ * stride x_row_stride elements; out [rows, D] contiguous.  out_dtype is the promotion of
+ * weight_dtype and x_dtype (the reference's `self.weight * hidden_states`). */
+int mzk_rms_norm(const void* x, int x_dtype, int64_t rows, int D, int64_t x_row_stride, const void* weight,
+                 int weight_dtype, float eps, void* out, int out_dtype, void* stream);
+
 /* ---------------------------------------------------------------------------------
  * Piece 3: lightning-indexer scores (MFMA)
  *   score[row, g] = Di^-0.5 * sum_h w[row,h] * relu(q[row,h] . k[b,g])  for g < vis,
@@ -244,6 +253,24 @@ int mzk_topk_workspace_bytes(int64_t rows, int64_t cols, int64_t* bytes);
 int mzk_topk_rows_ws(const float* scores, int64_t rows, int64_t cols, int64_t row_stride, int topk,
                      int32_t* out, int64_t out_stride, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* The indexer's published block bias from a top-k index list -- owlet1/indexer.py:158-165
+ * (`block_bias.scatter_(-1, safe, 0.0)` over a -inf row, the -inf picks and -1 slots
+ * dropped): bias [rows, G] fp32 (row stride bias_row_stride) is 0 at the columns
+ * idx[r, :topk] names (entries outside [0, G) are empty) and -inf elsewhere. */
+int mzk_topk_bias(const int32_t* idx, int64_t rows, int topk, int64_t idx_row_stride, int64_t G, float* bias,
+                  int64_t bias_row_stride, void* stream);
+
+/* The inverse: the visible columns of an additive attention mask as index lists, for the
+ * attention interface that receives the reference's dense mask (eager_attention_forward,
+ * owlet1/attention.py:42-71, with the mask of :202-214).  mask [rows, cols] of mask_dtype
+ * (row stride row_stride); a column is visible where the mask is 0 and masked where it is
+ * -inf or the dtype's lowest finite value (transformers' eager fill).  idx [rows, cap] int32:
+ * the visible columns ascending, then -1; counts [rows].  flags (one int, zeroed by the
+ * caller) gets bit 0 if any other value occurs (not representable as a selection) and bit 1
+ * if a row has more than cap visible columns (its list is then truncated). */
+int mzk_mask_to_indices(const void* mask, int mask_dtype, int64_t rows, int64_t cols, int64_t row_stride, int cap,
+                        int32_t* idx, int32_t* counts, int* flags, void* stream);
+
 /* Level one of the two-level candidate selection -- replaces select_candidate_blocks
  * (owlet1/indexer.py:14-40; tickets/0009-indexer-hierarchical.md).  logits [rows, width]
  * fp32 (row stride row_stride; unreachable positions already -inf), compress_lens [rows]
@@ -272,7 +299,8 @@ int mzk_candidate_blocks(const float* logits, int64_t rows, int64_t width, int64
  *   q          [B*S rows, H, D] bf16; row = b*S + s; positions [rows] int64 (absolute)
  *   fmt        0: entries are bf16 [D]; 1: FP8-b128 latent entries (nope = 512 or 128)
  *   window src win: row sees tokens max(0, pos-window+1)..pos of batch b at entry
- *              b*win_batch_entries + (win_cap ? tok % win_cap : tok)          (required)
+ *              b*win_batch_entries + (win_cap ? tok % win_cap : tok)  (window 0 and
+ *              win NULL: no window source; at least one source must be given)
  *   dense src  entries 0..min(dense_cap, (pos+1)/dense_ratio)-1 at b*dense_batch_entries
  *              (dense may be NULL)
  *   sparse src main_kv entries idx[row*idx_row_stride + j], j < topk; idx < 0 or >= G is

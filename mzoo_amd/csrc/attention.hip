@@ -1221,7 +1221,10 @@ int sparse_mqa_impl(const void* q, int64_t B, int64_t S, int H, int D, int fmt, 
                   split_total);
     MZK_CHECK_ARG(out == nullptr && lse == nullptr, "sparse_mqa_part: writes partials only");
   } else {
-    MZK_CHECK_ARG(window >= 1 && win != nullptr, "sparse_mqa: a window source (window >= 1) is required");
+    MZK_CHECK_ARG(window >= 0 && (window == 0 || win != nullptr), "sparse_mqa: a window of %d entries needs its cache",
+                  window);
+    MZK_CHECK_ARG(window >= 1 || dense != nullptr || main_kv != nullptr,
+                  "sparse_mqa: no source (window, dense or sparse) given");
   }
   MZK_CHECK_ARG(win_cap == 0 || win_cap >= window, "sparse_mqa: ring capacity smaller than the window");
   MZK_CHECK_ARG(!dense || (dense_ratio >= 1 && dense_cap >= 0), "sparse_mqa: dense source needs ratio >= 1");
@@ -1374,15 +1377,15 @@ namespace {
 constexpr int64_t kScratchBytes = MZK_NOALLOC_SCRATCH_BYTES;
 __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
-constexpr int kMaxDevices = 64;
+constexpr int kScratchDevices = 64;
 std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxDevices] = {};
+void* g_scratch_ptr[kScratchDevices] = {};
 
 // The calling thread's current device's copy of `scratch` (nullptr + error text on failure).
 void* device_scratch() {
   int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-    set_last_error("sparse_mqa_noalloc: no current HIP device (or device id >= %d)", kMaxDevices);
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices) {
+    set_last_error("sparse_mqa_noalloc: no current HIP device (or device id >= %d)", kScratchDevices);
     return nullptr;
   }
   std::lock_guard<std::mutex> lock(g_scratch_mu);

@@ -105,6 +105,57 @@ __global__ void __launch_bounds__(256) compress_kernel(const float* __restrict__
   }
 }
 
+// DeepseekV41RMSNorm (owlet1/norm_rope.py:25-30) of any width: one wave per row, the sum
+// of squares in the pinned order above (lane l sums channels l, l+64, ... from 0, then the
+// xor butterfly), var = sum / D, inv = 1 / sqrt(var + eps); normed = IDT(h * inv) (the
+// ".to(input_dtype)"), out = ODT(weight * normed).  Two passes over the row (L2-resident).
+template <int IDT, int WDT, int ODT>
+__global__ void __launch_bounds__(256) rms_norm_kernel(const void* __restrict__ x, int64_t rows, int D,
+                                                       int64_t x_stride, const void* __restrict__ weight, float eps,
+                                                       void* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // whole waves
+  const int64_t base = row * x_stride;
+  float ss = 0.0f;
+  for (int d = lane; d < D; d += 64) {
+    const float v = load_as_f32<IDT>(x, base + d);
+    ss = ss + v * v;
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) ss = ss + __shfl_xor(ss, m, 64);
+  const float var = div_rn(ss, static_cast<float>(D));
+  const float inv = div_rn(1.0f, sqrt_rn(var + eps));
+  for (int d = lane; d < D; d += 64) {
+    const float normed = round_to_dtype<IDT>(load_as_f32<IDT>(x, base + d) * inv);
+    store_from_f32<ODT>(out, row * D + d, load_as_f32<WDT>(weight, d) * normed);
+  }
+}
+
+template <int IDT, int WDT>
+int launch_rms_norm_o(int odt, const void* x, int64_t rows, int D, int64_t xs, const void* w, float eps, void* out,
+                      hipStream_t s) {
+  const unsigned grid = static_cast<unsigned>((rows + 3) / 4);
+  switch (odt) {
+    case MZK_F32: rms_norm_kernel<IDT, WDT, MZK_F32><<<grid, 256, 0, s>>>(x, rows, D, xs, w, eps, out); break;
+    case MZK_BF16: rms_norm_kernel<IDT, WDT, MZK_BF16><<<grid, 256, 0, s>>>(x, rows, D, xs, w, eps, out); break;
+    case MZK_F16: rms_norm_kernel<IDT, WDT, MZK_F16><<<grid, 256, 0, s>>>(x, rows, D, xs, w, eps, out); break;
+    default: set_last_error("rms_norm: unsupported out dtype %d", odt); return MZK_EINVAL;
+  }
+  return MZK_OK;
+}
+
+template <int IDT>
+int launch_rms_norm(int wdt, int odt, const void* x, int64_t rows, int D, int64_t xs, const void* w, float eps,
+                    void* out, hipStream_t s) {
+  switch (wdt) {
+    case MZK_F32: return launch_rms_norm_o<IDT, MZK_F32>(odt, x, rows, D, xs, w, eps, out, s);
+    case MZK_BF16: return launch_rms_norm_o<IDT, MZK_BF16>(odt, x, rows, D, xs, w, eps, out, s);
+    case MZK_F16: return launch_rms_norm_o<IDT, MZK_F16>(odt, x, rows, D, xs, w, eps, out, s);
+    default: set_last_error("rms_norm: unsupported weight dtype %d", wdt); return MZK_EINVAL;
+  }
+}
+
 // rows x D (dtype DT); cos/sin [rows / heads, rd/2] fp32, broadcast over `heads`
 // consecutive rows.  Nope channels are copied through unchanged.
 template <int DT>
@@ -188,5 +239,23 @@ extern "C" int mzk_rope(const void* x, int dtype, const float* cos_t, const floa
   MZK_CHECK_ARG(x && y && (rope_dim == 0 || (cos_t && sin_t)), "rope: null pointer");
   MZK_DISPATCH_DT(dtype, launch_rope, x, cos_t, sin_t, rows, D, rope_dim, heads, inverse, y, as_stream(stream));
   MZK_LAUNCH_CHECK("rope");
+  return MZK_OK;
+}
+
+extern "C" int mzk_rms_norm(const void* x, int x_dtype, int64_t rows, int D, int64_t x_row_stride,
+                            const void* weight, int weight_dtype, float eps, void* out, int out_dtype, void* stream) {
+  MZK_CHECK_ARG(rows >= 0 && D >= 1 && x_row_stride >= D, "rms_norm: bad sizes (D >= 1, row stride >= D)");
+  if (rows == 0) return MZK_OK;
+  MZK_CHECK_ARG(x && weight && out, "rms_norm: null pointer");
+  hipStream_t s = as_stream(stream);
+  int rc;
+  switch (x_dtype) {
+    case MZK_F32: rc = launch_rms_norm<MZK_F32>(weight_dtype, out_dtype, x, rows, D, x_row_stride, weight, eps, out, s); break;
+    case MZK_BF16: rc = launch_rms_norm<MZK_BF16>(weight_dtype, out_dtype, x, rows, D, x_row_stride, weight, eps, out, s); break;
+    case MZK_F16: rc = launch_rms_norm<MZK_F16>(weight_dtype, out_dtype, x, rows, D, x_row_stride, weight, eps, out, s); break;
+    default: set_last_error("rms_norm: unsupported input dtype %d", x_dtype); return MZK_EINVAL;
+  }
+  if (rc) return rc;
+  MZK_LAUNCH_CHECK("rms_norm");
   return MZK_OK;
 }

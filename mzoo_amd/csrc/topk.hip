@@ -879,6 +879,78 @@ __global__ void __launch_bounds__(256) candidate_expand_kernel(const int32_t* __
   }
 }
 
+// ---- selection formats ----------------------------------------------------------------
+
+// The additive block bias of owlet1/indexer.py:158-165 from a top-k index list: row r of
+// `bias` is 0 at the columns idx[r, :k] names (entries outside [0, G) are empty) and -inf
+// elsewhere.  One workgroup per row: fill, barrier, scatter.
+__global__ void __launch_bounds__(256) topk_bias_kernel(const int32_t* __restrict__ idx, int k, int64_t idx_stride,
+                                                        int64_t G, float* __restrict__ bias, int64_t bias_stride) {
+  const int64_t row = blockIdx.x;
+  float* brow = bias + row * bias_stride;
+  for (int64_t g = threadIdx.x; g < G; g += blockDim.x) brow[g] = -__builtin_huge_valf();
+  __syncthreads();
+  const int32_t* irow = idx + row * idx_stride;
+  for (int j = threadIdx.x; j < k; j += blockDim.x) {
+    const int32_t g = irow[j];
+    if (g >= 0 && g < G) brow[g] = 0.0f;
+  }
+}
+
+// The visible columns of an additive attention mask, in ascending order: a column is
+// visible where the mask is 0, masked where it is -inf or the dtype's lowest finite value
+// (what transformers' eager masks hold); anything else sets bit 0 of flags (a mask this
+// conversion cannot represent), more than `cap` visible columns in a row sets bit 1.
+// idx [rows, cap] (-1 after the last visible column), counts [rows].  One workgroup per row,
+// 256 columns per step: a wave ballot ranks the visible lanes, LDS holds the wave totals.
+template <int DT>
+__global__ void __launch_bounds__(256) mask_to_indices_kernel(const void* __restrict__ mask, int64_t T,
+                                                              int64_t row_stride, int cap, int32_t* __restrict__ idx,
+                                                              int32_t* __restrict__ counts, int* __restrict__ flags) {
+  __shared__ int wave_cnt[4];
+  const int64_t row = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const float lowest = DT == MZK_F32 ? -3.4028234663852886e38f : (DT == MZK_BF16 ? -3.3895313892515355e38f : -65504.0f);
+  int32_t* irow = idx + row * static_cast<int64_t>(cap);
+  int base = 0;
+  bool bad = false;
+  for (int64_t t0 = 0; t0 < T; t0 += 256) {
+    const int64_t t = t0 + threadIdx.x;
+    bool vis = false;
+    if (t < T) {
+      const float v = load_as_f32<DT>(mask, row * row_stride + t);
+      vis = v == 0.0f;
+      if (!vis && !(v == -__builtin_huge_valf() || v == lowest)) bad = true;
+    }
+    const uint64_t bal = __ballot(vis);
+    const int rank = __popcll(bal & ((uint64_t{1} << lane) - 1));
+    if (lane == 0) wave_cnt[wave] = __popcll(bal);
+    __syncthreads();
+    int off = base, total = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      if (w < wave) off += wave_cnt[w];
+      total += wave_cnt[w];
+    }
+    if (vis && off + rank < cap) irow[off + rank] = static_cast<int32_t>(t);
+    base += total;
+    __syncthreads();
+  }
+  for (int j = base + threadIdx.x; j < cap; j += 256) irow[j] = -1;
+  if (threadIdx.x == 0) {
+    counts[row] = base;
+    if (base > cap) atomicOr(flags, 2);
+  }
+  if (bad) atomicOr(flags, 1);
+}
+
+template <int DT>
+void launch_mask_to_indices(const void* mask, int64_t rows, int64_t T, int64_t rs, int cap, int32_t* idx,
+                            int32_t* counts, int* flags, hipStream_t s) {
+  mask_to_indices_kernel<DT><<<static_cast<unsigned>(rows), 256, 0, s>>>(mask, T, rs, cap, idx, counts, flags);
+}
+
 }  // namespace
 }  // namespace mzk
 
@@ -998,5 +1070,30 @@ extern "C" int mzk_candidate_blocks(const float* logits, int64_t rows, int64_t w
                                                                            static_cast<int>(nb), mask, mask_stride);
   }
   MZK_LAUNCH_CHECK("candidate_blocks");
+  return MZK_OK;
+}
+
+extern "C" int mzk_topk_bias(const int32_t* idx, int64_t rows, int topk, int64_t idx_row_stride, int64_t G,
+                             float* bias, int64_t bias_row_stride, void* stream) {
+  MZK_CHECK_ARG(rows >= 0 && topk >= 0 && G >= 0 && idx_row_stride >= topk && bias_row_stride >= G,
+                "topk_bias: bad sizes");
+  if (rows == 0 || G == 0) return MZK_OK;
+  MZK_CHECK_ARG(bias && (topk == 0 || idx), "topk_bias: null pointer");
+  MZK_CHECK_ARG(rows <= 0x7fffffff, "topk_bias: too many rows");
+  topk_bias_kernel<<<static_cast<unsigned>(rows), 256, 0, as_stream(stream)>>>(idx, topk, idx_row_stride, G, bias,
+                                                                                 bias_row_stride);
+  MZK_LAUNCH_CHECK("topk_bias");
+  return MZK_OK;
+}
+
+extern "C" int mzk_mask_to_indices(const void* mask, int mask_dtype, int64_t rows, int64_t cols, int64_t row_stride,
+                                   int cap, int32_t* idx, int32_t* counts, int* flags, void* stream) {
+  MZK_CHECK_ARG(rows >= 0 && cols >= 0 && cap >= 0 && row_stride >= cols, "mask_to_indices: bad sizes");
+  if (rows == 0) return MZK_OK;
+  MZK_CHECK_ARG(mask && idx && counts && flags, "mask_to_indices: null pointer");
+  MZK_CHECK_ARG(rows <= 0x7fffffff && cols <= 0x7fffffff, "mask_to_indices: too many rows or columns");
+  MZK_DISPATCH_DT(mask_dtype, launch_mask_to_indices, mask, rows, cols, row_stride, cap, idx, counts, flags,
+                  as_stream(stream));
+  MZK_LAUNCH_CHECK("mask_to_indices");
   return MZK_OK;
 }
