@@ -108,6 +108,30 @@ int mzk_decode_prologue(const void* kv, int kv_dtype, int64_t B, int nope, int r
                         int q_format, uint8_t* q_codes, float* q_scales, uint8_t* q_e8m0,
                         void* stream);
 
+/* Group emission inside a decode step, for one new token per batch row (positions [B]):
+ * the per-token work of DeepseekV41Compressor.forward with its cache layer
+ * (owlet1/cache.py:96-124, :159-172), the compressed-cache append (owlet1/attention.py:173-192)
+ * and the indexer's key publication (owlet1/indexer.py:96-117), with all state on the device.
+ *   kv, gate    fp32 [B, 576]: the token's compressor projections (gate unused at ratio 1)
+ *   carry_kv/_gate  fp32 [B, ratio, 576]: the partial group; the token goes to slot pos % ratio
+ * When (pos + 1) % ratio == 0 the row's group g = (pos+1)/ratio - 1 (if g < cache_cap):
+ *   latent = RMSNorm(bf16(sum_r kv_r * softmax_r(gate_r)))  (norm_weight bf16 [576], eps;
+ *            the pinned order of mzk_compress), bf16;
+ *   cache entry b*cache_batch_entries + g = FP8-b128 of the latent with its trailing 64
+ *            channels rotated at position g*ratio (row g*ratio of rope_table);
+ *   with wk (bf16 [128, 576]): key = RoPE(k_norm(bf16(latent . wk^T))) -- each output sums
+ *            channels [0, 288) and [288, 576) in order, then the halves --, quantized as key
+ *            b*key_batch_entries + g: key_format 0 FP8 b128 (k_codes [.., 128] e4m3 +
+ *            k_scales fp32), 1 MXFP4 (k_codes [.., 64] e2m1 + k_scales e8m0 [.., 4]).
+ * rope_table: bf16 [table_rows, 64], row p = cos (32) | sin (32) of position p (the compress
+ * RoPE).  step_cos / step_sin (bf16 [B, 32], or NULL): receive row pos of the table -- the
+ * token's RoPE for the step's later launches.  Rows with pos < 0 do nothing. */
+int mzk_decode_emit(const int64_t* positions, int64_t B, const float* kv, const float* gate, float* carry_kv,
+                    float* carry_gate, int ratio, const void* norm_weight, float eps, uint8_t* cache,
+                    int64_t cache_batch_entries, int64_t cache_cap, const void* wk, const void* k_norm_weight,
+                    float k_eps, int key_format, uint8_t* k_codes, void* k_scales, int64_t key_batch_entries,
+                    const void* rope_table, int64_t table_rows, void* step_cos, void* step_sin, void* stream);
+
 /* ---------------------------------------------------------------------------------
  * Piece 2: KV compressor and RoPE
  * --------------------------------------------------------------------------------- */

@@ -275,6 +275,37 @@ __device__ __forceinline__ uint32_t rope_pair_bf16(uint32_t pair, float c, float
 
 
 // ------------------------------------------------------------------------------------
+// The compressor's pinned float32 exp (the CPU restatement oracle/compressor.py evaluates
+// the same operation sequence): n = rint(x*log2e), r = (x - n*ln2_hi) - n*ln2_lo, degree-7
+// Taylor in Horner form, times 2^n through the exponent field (two steps below 2^-126);
+// no fused operations.  Max error ~2 ulp.
+// ------------------------------------------------------------------------------------
+__device__ __forceinline__ float exp_pinned(float x) {
+  const float kLog2e = 1.44269504088896341f;
+  const float kLn2Hi = 0.693145751953125f;
+  const float kLn2Lo = 1.42860682030941723e-06f;
+  const float c[8] = {1.0f, 1.0f, 0.5f, 1.0f / 6.0f, 1.0f / 24.0f, 1.0f / 120.0f, 1.0f / 720.0f, 1.0f / 5040.0f};
+  float n = __builtin_rintf(x * kLog2e);
+  n = fminf(fmaxf(n, -160.0f), 160.0f);
+  const float r = (x - n * kLn2Hi) - n * kLn2Lo;
+  float p = c[7];
+#pragma unroll
+  for (int i = 6; i >= 0; --i) p = p * r + c[i];
+  const int ni = static_cast<int>(n);
+  const int hi = ni < -126 ? -126 : (ni > 127 ? 127 : ni);
+  float out = p * pow2i(hi);
+  if (ni < -126) {
+    int lo = ni + 64;
+    lo = lo < -126 ? -126 : (lo > 127 ? 127 : lo);
+    out = (p * pow2i(lo)) * 5.421010862427522e-20f;  // * 2^-64
+  }
+  if (x < -104.0f) out = 0.0f;
+  if (x > 88.8f) out = __builtin_huge_valf();
+  if (x != x) out = x;
+  return out;
+}
+
+// ------------------------------------------------------------------------------------
 // wave helpers (wave64)
 // ------------------------------------------------------------------------------------
 // Maximum of values >= 0 or NaN (block maxima of |x|; NaN wins, see nn_max) over aligned

@@ -26,7 +26,17 @@ preallocated on the device so the whole step records into one HIP graph:
   4. top-k (lowest index wins ties),
   5. sparse MQA over window + [coarse] + top-k entries with the sink, split-KV + merge,
   6. ``positions += 1`` when ``advance``.
-Group emission (the compressor, one entry per ``ratio`` steps) is ``append_groups``.
+
+Group emission -- the compressor, the cache append and the indexer's key publication, one
+entry per ``ratio`` tokens (``owlet1/cache.py:96-124``, ``:159-172``, ``owlet1/indexer.py:96-117``,
+``owlet1/attention.py:173-192``) -- runs inside the step when the layer has its
+``CompressorWeights`` and the step gets the token's fp32 compressor projections
+(``step(..., compress=(kv, gate))``): a first launch writes them to a device carry ring and,
+when the token completes a group, pools the group, normalizes it, writes its rotated FP8-b128
+entry and its index key, before the indexer scores the keys -- so a graph replay that
+advances the positions emits groups itself.  The same launch copies the token's RoPE tables
+out of a position-indexed device table (``rope="table"``), so nothing on the host changes
+between replays.  ``append_groups`` writes groups from the host (prefill).
 
 With ``rope=(cos, sin, index_cos, index_sin)`` (bf16 [B, 32] each: the new token's
 ``position_embeddings`` and the indexer's compress-RoPE tables) the step also takes over the
@@ -74,6 +84,32 @@ class GroupedOutputProjection:
 
 
 @dataclass
+class CompressorWeights:
+    """What the in-step group emission reads: the compressor's RMSNorm weight
+    (``owlet1/cache.py:140``), the indexer's key projection ``wk`` [Di, D] and ``k_norm`` weight
+    (``owlet1/indexer.py:75-76``), their epsilons, the coarse branch's compressor norm weight
+    (hierarchical config), and the compress-RoPE base the group positions rotate with
+    (``compress_rope_theta``, ``owlet1/config.py:238``)."""
+    norm_weight: torch.Tensor
+    wk: torch.Tensor
+    k_norm_weight: torch.Tensor
+    eps: float = 1e-6
+    k_eps: float = 1e-6
+    coarse_norm_weight: torch.Tensor | None = None
+    rope_theta: float = 160000.0
+
+
+def rope_table(positions: int, rope_dim: int, theta: float) -> torch.Tensor:
+    """bf16 [positions, rope_dim]: row p holds the cos (first rope_dim/2) and sin of position
+    p, as ``DeepseekV41RotaryEmbedding.forward`` computes them (``owlet1/norm_rope.py:108-124``:
+    ``inv_freq = 1 / theta^(arange(0, rd, 2) / rd)``, ``pos * inv_freq`` in fp32, cos / sin,
+    then the activations' dtype), on the CPU."""
+    inv = 1.0 / (theta ** (torch.arange(0, rope_dim, 2, dtype=torch.float) / rope_dim))
+    freqs = torch.arange(positions, dtype=torch.float).view(-1, 1) * inv.view(1, -1)
+    return torch.cat([freqs.cos(), freqs.sin()], -1).to(torch.bfloat16)
+
+
+@dataclass
 class DecodeConfig:
     batch: int
     heads: int = 128
@@ -103,7 +139,8 @@ class DecodeConfig:
 class SparseDecodeLayer:
     def __init__(self, cfg: DecodeConfig, device, sinks: torch.Tensor | None = None,
                  kv_norm_weight: torch.Tensor | None = None, kv_norm_eps: float = 1e-6,
-                 out_proj: GroupedOutputProjection | None = None):
+                 out_proj: GroupedOutputProjection | None = None, compressor: CompressorWeights | None = None,
+                 max_position: int | None = None):
         if cfg.index_format not in ("fp8", "mxfp4"):
             raise ValueError(f"index_format must be 'fp8' or 'mxfp4', got {cfg.index_format!r}")
         if cfg.index_format == "fp8" and cfg.index_dim != 128:
@@ -146,6 +183,35 @@ class SparseDecodeLayer:
             self.q_e8m0 = torch.empty(b, 1, hi, di // 32, **u8)
         self._graph = None
         self._static = None
+        self.compressor = None
+        if compressor is not None:
+            self._init_emission(compressor, max_position)
+
+    def _init_emission(self, cw: CompressorWeights, max_position: int | None) -> None:
+        cfg = self.cfg
+        b, d, dev = cfg.batch, cfg.dim, self.device
+        if cfg.index_dim != 128 or cfg.nope != 512 or cfg.rope != 64:
+            raise ValueError("in-step emission: latent 512 + 64 and index keys of 128 channels")
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        self.compressor = CompressorWeights(
+            norm_weight=cw.norm_weight.to(**bf).contiguous(), wk=cw.wk.to(**bf).contiguous(),
+            k_norm_weight=cw.k_norm_weight.to(**bf).contiguous(), eps=float(cw.eps), k_eps=float(cw.k_eps),
+            coarse_norm_weight=None if cw.coarse_norm_weight is None else cw.coarse_norm_weight.to(**bf).contiguous(),
+            rope_theta=float(cw.rope_theta))
+        if tuple(self.compressor.wk.shape) != (cfg.index_dim, d):
+            raise ValueError(f"in-step emission: wk must be [{cfg.index_dim}, {d}]")
+        if cfg.coarse_ratio and self.compressor.coarse_norm_weight is None:
+            raise ValueError("in-step emission: the coarse branch needs coarse_norm_weight")
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.carry_kv = torch.zeros(b, cfg.ratio, d, **f32)
+        self.carry_gate = torch.zeros(b, cfg.ratio, d, **f32)
+        if cfg.coarse_ratio:
+            self.coarse_carry_kv = torch.zeros(b, cfg.coarse_ratio, d, **f32)
+            self.coarse_carry_gate = torch.zeros(b, cfg.coarse_ratio, d, **f32)
+        npos = max_position or max(cfg.max_groups * cfg.ratio, cfg.coarse_groups * max(cfg.coarse_ratio, 1)) + 1
+        self.rope_table = rope_table(npos, cfg.rope, self.compressor.rope_theta).to(dev).contiguous()
+        self.step_cos = torch.zeros(b, cfg.rope // 2, **bf)
+        self.step_sin = torch.zeros(b, cfg.rope // 2, **bf)
 
     # ---- state ---------------------------------------------------------------------------
     def set_positions(self, pos) -> None:
@@ -176,6 +242,48 @@ class SparseDecodeLayer:
             self.k_packed[:, start:start + n] = packed
             self.k_e8m0[:, start:start + n] = e8
 
+    def set_carry(self, kv: torch.Tensor, gate: torch.Tensor, coarse: bool = False) -> None:
+        """The partial group carried into the next step (prefill): kv / gate fp32 [B, n, D],
+        the compressor projections of the last n tokens before the current position, n =
+        position % ratio -- store_compression_weights' buffer (owlet1/cache.py:96-113)."""
+        ratio = self.cfg.coarse_ratio if coarse else self.cfg.ratio
+        ck, cg = (self.coarse_carry_kv, self.coarse_carry_gate) if coarse else (self.carry_kv, self.carry_gate)
+        n = kv.shape[1]
+        if n >= ratio:
+            raise ValueError(f"set_carry: a partial group holds fewer than {ratio} tokens, got {n}")
+        ck[:, :n] = kv.float()
+        cg[:, :n] = gate.float()
+
+    def _emit(self, compress, rope_from_table: bool) -> None:
+        """The in-step emission launches (one per compressed branch), see the module doc."""
+        cfg, cw = self.cfg, self.compressor
+        b = cfg.batch
+        st = _lib.stream_of(self.positions)
+        fp8 = cfg.index_format == "fp8"
+        kv, gate = (t.contiguous() for t in compress[:2])
+        for t in (kv, gate):
+            if t.dtype != torch.float32 or t.shape != (b, cfg.dim):
+                raise ValueError(f"step(compress=...): fp32 [{b}, {cfg.dim}] projections expected")
+        keys = (self.k_codes, self.k_scales) if fp8 else (self.k_packed, self.k_e8m0)
+        tabs = (self.step_cos.data_ptr(), self.step_sin.data_ptr()) if rope_from_table else (None, None)
+        _lib.call("mzk_decode_emit", self.positions.data_ptr(), b, kv.data_ptr(), gate.data_ptr(),
+                  self.carry_kv.data_ptr(), self.carry_gate.data_ptr(), cfg.ratio, cw.norm_weight.data_ptr(), cw.eps,
+                  self.main.data_ptr(), cfg.max_groups, cfg.max_groups, cw.wk.data_ptr(),
+                  cw.k_norm_weight.data_ptr(), cw.k_eps, 0 if fp8 else 1, keys[0].data_ptr(), keys[1].data_ptr(),
+                  cfg.max_groups, self.rope_table.data_ptr(), self.rope_table.shape[0], *tabs, st)
+        if cfg.coarse_ratio:
+            if len(compress) != 4:
+                raise ValueError("step(compress=...): the coarse branch needs (kv, gate, coarse_kv, coarse_gate)")
+            ckv, cg = (t.contiguous() for t in compress[2:])
+            for t in (ckv, cg):
+                if t.dtype != torch.float32 or t.shape != (b, cfg.dim):
+                    raise ValueError(f"step(compress=...): fp32 [{b}, {cfg.dim}] projections expected")
+            _lib.call("mzk_decode_emit", self.positions.data_ptr(), b, ckv.data_ptr(), cg.data_ptr(),
+                      self.coarse_carry_kv.data_ptr(), self.coarse_carry_gate.data_ptr(), cfg.coarse_ratio,
+                      cw.coarse_norm_weight.data_ptr(), cw.eps, self.coarse.data_ptr(), cfg.coarse_groups,
+                      cfg.coarse_groups, None, None, 0.0, 0, None, None, 0, self.rope_table.data_ptr(),
+                      self.rope_table.shape[0], None, None, st)
+
     def fill_coarse(self, latents: torch.Tensor) -> None:
         """latents [B, n, D] -> coarse entries 0..n-1 of every row."""
         n = latents.shape[1]
@@ -186,16 +294,30 @@ class SparseDecodeLayer:
 
     # ---- the step ------------------------------------------------------------------------
     def step(self, q: torch.Tensor, kv: torch.Tensor | None, q_idx: torch.Tensor, w: torch.Tensor,
-             advance: bool = False, rope: tuple | None = None) -> torch.Tensor:
+             advance: bool = False, rope: tuple | str | None = None, compress: tuple | None = None) -> torch.Tensor:
         """q bf16 [B,H,D] (rotated), kv bf16 [B,D] (the new token's rotated latent, or None
         if already in the ring), q_idx bf16 [B,Hi,Di] (rotated), w fp32 [B,Hi] (x Hi^-0.5).
         With ``rope`` (see the module docstring) q, q_idx are unrotated, kv is the raw
-        projection, and the returned output has the inverse rotation applied."""
+        projection, and the returned output has the inverse rotation applied; ``rope="table"``
+        takes the four tables from the device table at the rows' positions (needs the
+        layer's ``CompressorWeights``).  ``compress`` = (kv, gate[, coarse_kv, coarse_gate]):
+        the token's fp32 compressor projections [B, D], emitted into the caches in the step."""
         cfg = self.cfg
         b = cfg.batch
         fp8 = cfg.index_format == "fp8"
         kvc = None if kv is None else kv.contiguous()
         pos = self.positions.view(b, 1)
+        from_table = isinstance(rope, str)
+        if from_table and rope != "table":
+            raise ValueError(f"step: rope must be a tuple of tables or 'table', got {rope!r}")
+        if (compress is not None or from_table) and self.compressor is None:
+            raise ValueError("step(compress=... / rope='table'): the layer was built without CompressorWeights")
+        if compress is not None:
+            self._emit(compress, from_table)
+        elif from_table:
+            raise ValueError("step(rope='table'): the tables are gathered by the emission launch (compress=...)")
+        if from_table:
+            rope = (self.step_cos, self.step_sin, self.step_cos, self.step_sin)
         if rope is not None:
             return self._step_fused(q, kvc, q_idx, w, advance, rope)
         if fp8:
@@ -297,16 +419,29 @@ class SparseDecodeLayer:
                       self.lse.data_ptr(), main.cuda_stream)
 
     def capture(self, q, kv, q_idx, w, advance: bool = False, warmup: int = 2,
-                rope: tuple | None = None) -> torch.cuda.CUDAGraph:
+                rope: tuple | str | None = None, compress: tuple | None = None,
+                allow_stale_groups: bool = False) -> torch.cuda.CUDAGraph:
         """Record ``step`` into a HIP graph over static copies of the inputs; ``replay``
-        then reruns it after the caller writes new inputs into ``static_inputs`` (with
-        ``rope``, its four tables are the last four static inputs: a replay that advances
-        the positions needs the next position's tables written there too)."""
-        ins = (q, kv, q_idx, w) + (() if rope is None else tuple(rope))
+        then reruns it after the caller writes new inputs into ``static_inputs`` (q, kv,
+        q_idx, w, then the ``rope`` tables when given as a tuple -- a replay that advances the
+        positions needs the next position's tables written there too, which ``rope="table"``
+        does on the device -- then the ``compress`` projections).
+
+        ``advance=True`` needs the in-step emission (``compress``): without it a replay that
+        completes a group would expose a cache slot nothing wrote.  ``allow_stale_groups``
+        waives that for a caller whose caches already hold every group a replay can reach."""
+        if advance and compress is None and not allow_stale_groups:
+            raise ValueError("capture(advance=True) needs compress=(...) projections (in-step group emission); "
+                             "pass allow_stale_groups=True if the caches already hold every reachable group")
+        tabs = tuple(rope) if isinstance(rope, tuple) else ()
+        comp = () if compress is None else tuple(compress)
+        ins = (q, kv, q_idx, w) + tabs + comp
         self._static = tuple(None if t is None else t.clone() for t in ins)
         st = self._static
-        run = (lambda adv: self.step(*st[:4], advance=adv)) if rope is None else \
-            (lambda adv: self.step(*st[:4], advance=adv, rope=st[4:]))
+        nt = len(tabs)
+        rope_arg = rope if isinstance(rope, str) else (st[4:4 + nt] if nt else None)
+        comp_arg = st[4 + nt:] if comp else None
+        run = lambda adv: self.step(*st[:4], advance=adv, rope=rope_arg, compress=comp_arg)  # noqa: E731
         s = torch.cuda.Stream(device=self.device)
         s.wait_stream(torch.cuda.current_stream(self.device))
         saved = self.positions.clone()

@@ -177,3 +177,40 @@ def rope_tables(positions, rope_dim: int, theta: float):
     pos = torch.as_tensor(np.asarray(positions)).float()
     freqs = pos[..., None] * inv
     return freqs.cos().numpy(), freqs.sin().numpy()
+
+
+def linear_pinned(x, w, dtype: str = "bfloat16") -> np.ndarray:
+    """``nn.Linear`` (no bias) of x [..., D] by w [out, D] in the order the decode-step
+    emission kernel evaluates it: each output sums channels [0, D/2) and then, separately,
+    [D/2, D) in ascending order in float32 (a bf16 x bf16 product is exact in float32), adds
+    the two halves and rounds to ``dtype``.  Differs from a library GEMM's order only in
+    float32 rounding (tests bound it against float64)."""
+    x = np.asarray(x, F32)
+    w = np.asarray(w, F32)
+    d = x.shape[-1]
+    h = d // 2
+    acc = [np.zeros(x.shape[:-1] + (w.shape[0],), F32) for _ in range(2)]
+    for half in range(2):
+        a = acc[half]
+        for i in range(half * h, (half + 1) * h):
+            a = a + x[..., i:i + 1] * w[:, i]
+        acc[half] = a
+    return round_to(acc[0] + acc[1], dtype)
+
+
+def emit_group(kv, gate, ratio: int, norm_w, eps: float, cos, sin, wk=None, k_norm_w=None, k_eps: float = 1e-6,
+               dtype: str = "bfloat16"):
+    """One compressed group as the decode step emits it: ``kv`` / ``gate`` [B, ratio, D] fp32
+    (the group's compressor projections, owlet1/cache.py:155-158), ``cos`` / ``sin`` [B, rd/2]
+    the compress RoPE at the group's position ``g * ratio`` (attention.py:174-180).
+
+    Returns (rotated latent [B, D] -- what the main cache stores before its packing,
+    attention.py:180 --, index key [B, Di] or None -- ``rope(k_norm(wk(latent)))`` before its
+    quantization, indexer.py:96-103).  The latent is ``compress`` (pool + RMSNorm,
+    cache.py:168-172); the key projection uses ``linear_pinned``."""
+    latent = compress(kv, gate, ratio, norm_w, eps, dtype)[:, 0]
+    rot = rope(latent, cos, sin, dtype=dtype)
+    if wk is None:
+        return rot, None
+    k = rms_norm(linear_pinned(latent, wk, dtype), k_norm_w, k_eps, dtype)
+    return rot, rope(k, cos, sin, dtype=dtype)

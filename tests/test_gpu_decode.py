@@ -115,7 +115,7 @@ def test_graph_replay_overlapped_branches(dev):
 
 def test_graph_advances_positions(dev):
     layer, inputs, _ = _layer(dev, "fp8", seed=4, pos=1000)
-    layer.capture(*inputs, advance=True)
+    layer.capture(*inputs, advance=True, allow_stale_groups=True)  # every reachable group prefilled
     for _ in range(3):
         layer.replay()
     torch.cuda.synchronize()

@@ -1,0 +1,198 @@
+"""GPU: the decode step with in-step group emission, captured once and replayed with
+advancing positions across group boundaries, against the oracle's step-by-step decode.
+
+The layer starts mid-sequence (groups emitted from the history's compressor projections by
+the oracle, the partial group in the carry ring, the window holding the last tokens).  Each
+replay gets new inputs (q, kv, the indexer query and weights, the compressor projections of
+the token) through the graph's static buffers and advances every row's position; on the
+device the step emits each completed group into the main cache and the key cache, gathers
+the token's RoPE tables from the position table, appends the window entry, scores, selects
+and attends.  Checked after every replay:
+
+* the RoPE table against the oracle's tables, bit for bit;
+* the window ring, the main-cache entries and the index keys (FP8 b128 or MXFP4), bit for
+  bit against the oracle (``compressor.emit_group`` + the packers; ``decode_kv_latent``);
+* the selection against the oracle's top-k of the oracle's scores up to near-ties;
+* the output (inverse RoPE applied) against the oracle's attention over the window, the
+  coarse entries (hierarchical case) and the selected entries, to the attention bar.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from mzoo_amd.decode import CompressorWeights, DecodeConfig, SparseDecodeLayer
+from oracle import attention as OA
+from oracle import compressor as C
+from oracle import quant as Q
+from tests.helpers import assert_attn_close, assert_topk_sets_match
+
+pytestmark = pytest.mark.gpu
+
+D, HI, DI, W = 576, 64, 128, 128
+THETA_C = 160000.0
+
+
+def _bf(x):
+    return Q.round_bf16(np.asarray(x, np.float32))
+
+
+def _keys(keys, fmt):
+    if fmt == "fp8":
+        codes, scales = Q.fp8_block_codes(keys, 128)
+        return codes, scales[..., 0]
+    return Q.quant_mxfp4(keys)
+
+
+def _dequant_keys(a, s, fmt):
+    return Q.dequant_fp8_block(a, s[..., None], 128) if fmt == "fp8" else Q.dequant_mxfp4(a, s)
+
+
+def _emit_history(kv, gate, ratio, ngroups, nw, cos_t, sin_t, wk=None, kw=None):
+    rots, keys = [], []
+    for g in range(ngroups):
+        c, s = cos_t[g * ratio][None], sin_t[g * ratio][None]
+        c = np.repeat(c, kv.shape[0], 0)
+        s = np.repeat(s, kv.shape[0], 0)
+        rot, key = C.emit_group(kv[:, g * ratio:(g + 1) * ratio], gate[:, g * ratio:(g + 1) * ratio], ratio, nw,
+                                1e-6, c, s, wk, kw, 1e-6)
+        rots.append(rot)
+        keys.append(key)
+    return np.stack(rots, 1), (np.stack(keys, 1) if wk is not None else None)
+
+
+@pytest.mark.parametrize("fmt,coarse", [("fp8", False), ("mxfp4", False), ("mxfp4", True)])
+def test_replays_across_group_boundaries(dev, fmt, coarse):
+    b, ratio, gcap, topk, p0, steps = 3, 4, 64, 16, 150, 11
+    cratio, cgroups = (8, 32) if coarse else (0, 0)
+    gen = torch.Generator().manual_seed(31 + coarse)
+    rnd = lambda *s: torch.randn(*s, generator=gen)  # noqa: E731
+    print(f"emission replay: fmt={fmt} coarse={coarse} positions {p0}..{p0 + steps - 1}", flush=True)
+    nw, kvw = _bf(1 + 0.1 * rnd(D).numpy()), _bf(1 + 0.1 * rnd(D).numpy())
+    wk, kw = _bf(0.04 * rnd(DI, D).numpy()), _bf(1 + 0.1 * rnd(DI).numpy())
+    cnw = _bf(1 + 0.1 * rnd(D).numpy())
+    sinks = rnd(128)
+    cfg = DecodeConfig(batch=b, max_groups=gcap, topk=topk, index_format=fmt, nsplit=2, coarse_ratio=cratio,
+                       coarse_groups=cgroups)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))  # noqa: E731
+    cw = CompressorWeights(t(nw), t(wk), t(kw), 1e-6, 1e-6, t(cnw) if coarse else None, THETA_C)
+    layer = SparseDecodeLayer(cfg, dev, sinks=sinks, kv_norm_weight=t(kvw), kv_norm_eps=1e-6, compressor=cw)
+
+    # the position table: the reference's cos / sin (fp32) rounded to bf16
+    tab = layer.rope_table.cpu()
+    cos_t, sin_t = C.rope_tables(np.arange(tab.shape[0]), 64, THETA_C)
+    cos_t, sin_t = _bf(cos_t), _bf(sin_t)
+    assert np.array_equal(tab[:, :32].float().numpy(), cos_t) and np.array_equal(tab[:, 32:].float().numpy(), sin_t)
+
+    # history: compressor projections of tokens 0..p0-1 -> groups emitted by the oracle
+    hkv, hgate = rnd(b, p0, D).numpy(), rnd(b, p0, D).numpy()
+    n0 = p0 // ratio
+    rots, keys = _emit_history(hkv, hgate, ratio, n0, nw, cos_t, sin_t, wk, kw)
+    main = np.zeros((b, gcap, 656), np.uint8)
+    main[:, :n0] = Q.pack_latent_fp8_b128(rots)
+    ka, ks = _keys(keys, fmt)
+    key_a = np.zeros((b, gcap) + ka.shape[2:], np.uint8)
+    key_s = (np.ones((b, gcap), np.float32) if fmt == "fp8" else np.full((b, gcap, DI // 32), 127, np.uint8))
+    key_a[:, :n0], key_s[:, :n0] = ka, ks
+    if fmt == "fp8":
+        layer.k_codes.copy_(t(key_a)), layer.k_scales.copy_(t(key_s))
+    else:
+        layer.k_packed.copy_(t(key_a)), layer.k_e8m0.copy_(t(key_s))
+    layer.main.copy_(t(main))
+    layer.set_carry(t(hkv[:, n0 * ratio:]), t(hgate[:, n0 * ratio:]))
+    coarse_ent = None
+    if coarse:
+        cn0 = p0 // cratio
+        crots, _ = _emit_history(hkv, hgate, cratio, cn0, cnw, cos_t, sin_t)
+        coarse_ent = np.zeros((b, cgroups, 656), np.uint8)
+        coarse_ent[:, :cn0] = Q.pack_latent_fp8_b128(crots)
+        layer.coarse.copy_(t(coarse_ent))
+        layer.set_carry(t(hkv[:, cn0 * cratio:]), t(hgate[:, cn0 * cratio:]), coarse=True)
+    # window: the last W tokens' entries
+    win = np.zeros((b, W, 656), np.uint8)
+    for tok in range(p0 - W, p0):
+        win[:, tok % W] = Q.pack_latent_fp8_b128(_bf(rnd(b, D).numpy()))
+    layer.win.copy_(t(win))
+    layer.set_positions(p0)
+    carry = np.zeros((b, ratio, D), np.float32), np.zeros((b, ratio, D), np.float32)
+    carry[0][:, :p0 % ratio], carry[1][:, :p0 % ratio] = hkv[:, n0 * ratio:], hgate[:, n0 * ratio:]
+    if coarse:
+        ccarry = np.zeros((b, cratio, D), np.float32), np.zeros((b, cratio, D), np.float32)
+        ccarry[0][:, :p0 % cratio], ccarry[1][:, :p0 % cratio] = hkv[:, cn0 * cratio:], hgate[:, cn0 * cratio:]
+
+    def new_inputs():
+        ins = [rnd(b, 128, D).bfloat16(), rnd(b, D).bfloat16(), rnd(b, HI, DI).bfloat16(), rnd(b, HI) * HI ** -0.5,
+               rnd(b, D), rnd(b, D)]
+        if coarse:
+            ins += [rnd(b, D), rnd(b, D)]
+        return ins
+
+    first = [x.to(dev) for x in new_inputs()]
+    layer.capture(*first[:4], advance=True, rope="table", compress=tuple(first[4:]))
+    for i in range(steps):
+        pos = p0 + i
+        ins = new_inputs()
+        for dst, src in zip(layer.static_inputs, ins):
+            dst.copy_(src)
+        out = layer.replay().clone()
+        torch.cuda.synchronize()
+        q, kv, q_idx, w, kvc, gate = [x.float().numpy() for x in ins[:6]]
+        cs, sn = np.repeat(cos_t[pos][None], b, 0), np.repeat(sin_t[pos][None], b, 0)
+        # window entry
+        win[:, pos % W] = Q.pack_latent_fp8_b128(C.decode_kv_latent(kv, kvw, 1e-6, cs, sn))
+        assert np.array_equal(layer.win.cpu().numpy(), win), f"step {i}: window ring"
+        # carry + emission
+        carry[0][:, pos % ratio], carry[1][:, pos % ratio] = kvc, gate
+        if (pos + 1) % ratio == 0:
+            g = (pos + 1) // ratio - 1
+            cg, sg = np.repeat(cos_t[g * ratio][None], b, 0), np.repeat(sin_t[g * ratio][None], b, 0)
+            rot, key = C.emit_group(carry[0], carry[1], ratio, nw, 1e-6, cg, sg, wk, kw, 1e-6)
+            main[:, g] = Q.pack_latent_fp8_b128(rot)
+            ka, ks = _keys(key[:, None], fmt)
+            key_a[:, g], key_s[:, g] = ka[:, 0], ks[:, 0]
+        assert np.array_equal(layer.main.cpu().numpy(), main), f"step {i} (position {pos}): main cache"
+        ga, gs = (layer.k_codes, layer.k_scales) if fmt == "fp8" else (layer.k_packed, layer.k_e8m0)
+        assert np.array_equal(ga.cpu().numpy(), key_a), f"step {i} (position {pos}): key codes"
+        assert np.array_equal(gs.cpu().numpy().view(np.uint8), key_s.view(np.uint8)), f"step {i}: key scales"
+        if coarse:
+            ccarry[0][:, pos % cratio], ccarry[1][:, pos % cratio] = ins[6].numpy(), ins[7].numpy()
+            if (pos + 1) % cratio == 0:
+                g = (pos + 1) // cratio - 1
+                cg, sg = np.repeat(cos_t[g * cratio][None], b, 0), np.repeat(sin_t[g * cratio][None], b, 0)
+                rot, _ = C.emit_group(ccarry[0], ccarry[1], cratio, cnw, 1e-6, cg, sg)
+                coarse_ent[:, g] = Q.pack_latent_fp8_b128(rot)
+            assert np.array_equal(layer.coarse.cpu().numpy(), coarse_ent), f"step {i}: coarse cache"
+        # indexer + top-k
+        q_rot = C.rope(q_idx, cs[:, None], sn[:, None], dtype="bfloat16")
+        qd = Q.fake_quant_fp8_block(q_rot, 128) if fmt == "fp8" else Q.fake_quant_fp4_block(q_rot, 32)
+        kd = _dequant_keys(key_a, key_s, fmt)
+        posv = torch.full((b, 1), pos)
+        sc = OA.indexer_scores(torch.from_numpy(qd)[:, None], torch.from_numpy(kd), torch.from_numpy(w)[:, None],
+                               ratio, posv)
+        mag = OA.indexer_abs_scores(torch.from_numpy(qd)[:, None], torch.from_numpy(kd),
+                                    torch.from_numpy(w)[:, None], ratio, posv)
+        assert_topk_sets_match(layer.idx, sc[:, 0], mag[:, 0], topk)
+        # attention over the window, the coarse entries and the GPU's own selection
+        wd = Q.unpack_latent_fp8_b128(win)
+        md = Q.unpack_latent_fp8_b128(main)
+        qr = C.rope(q, cs[:, None], sn[:, None], dtype="bfloat16")
+        idx = layer.idx.cpu().numpy()
+        refs = []
+        for r in range(b):
+            ents = [wd[r, [(pos - W + 1 + j) % W for j in range(W)]]]
+            if coarse:
+                ents.append(Q.unpack_latent_fp8_b128(coarse_ent[r, :(pos + 1) // cratio]))
+            ents.append(md[r, idx[r][idx[r] >= 0]])
+            o, _ = OA.attend_entries(torch.from_numpy(qr[r]), torch.from_numpy(np.concatenate(ents)), sinks)
+            refs.append(C.rope(o.numpy(), cs[r][None], sn[r][None], inverse=True))
+        assert_attn_close(out, torch.from_numpy(np.stack(refs)), name=f"step {i} output")
+    assert int(layer.positions[0]) == p0 + steps
+
+
+def test_capture_advance_requires_emission(dev):
+    cfg = DecodeConfig(batch=2, max_groups=64, topk=16)
+    layer = SparseDecodeLayer(cfg, dev)
+    ins = (torch.zeros(2, 128, D, dtype=torch.bfloat16, device=dev), None,
+           torch.zeros(2, HI, DI, dtype=torch.bfloat16, device=dev), torch.zeros(2, HI, device=dev))
+    with pytest.raises(ValueError, match="in-step group emission"):
+        layer.capture(*ins, advance=True)

@@ -192,3 +192,62 @@ def test_rope_tables_closed_form():
         # fp32 angle rounding grows with the position: |pos * inv_freq| ulp
         tol = 4 * np.abs(ang) * 2.0 ** -24 + 1e-6
         assert np.all(np.abs(cos - np.cos(ang)) <= tol) and np.all(np.abs(sin - np.sin(ang)) <= tol)
+
+
+def test_linear_pinned_against_float64():
+    """The pinned-order key projection: within one float32 rounding chain of the exact
+    (float64) product, and after rounding to bf16 equal to the exact product's rounding
+    except where the exact value sits within that error of a bf16 rounding boundary."""
+    rng = np.random.default_rng(12)
+    x = Q.round_bf16(rng.standard_normal((64, 576)).astype(np.float32))
+    w = Q.round_bf16((rng.standard_normal((128, 576)) * 0.05).astype(np.float32))
+    exact = x.astype(np.float64) @ w.astype(np.float64).T
+    got32 = C.linear_pinned(x, w, "float32")
+    bound = 576 * 2.0 ** -24 * (np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64).T)
+    assert np.all(np.abs(got32 - exact) <= bound)
+    got = C.linear_pinned(x, w, "bfloat16")
+    want = Q.round_bf16(exact.astype(np.float32))
+    mism = got != want
+    assert mism.mean() < 0.01
+    # a mismatch only where the exact value is close to a bf16 midpoint
+    ulp = np.abs(want) * 2.0 ** -8
+    assert np.all(np.abs(got[mism] - exact[mism]) <= ulp[mism] + bound[mism])
+
+
+def test_emit_group_matches_the_reference_steps():
+    """emit_group against the reference's own steps run by torch in bf16: compressor pooling
+    (fp32 softmax-weighted sum, cache.py:168-172) -> kv norm -> RoPE, and k_norm(wk(latent))
+    -> RoPE (indexer.py:96-103) with torch's bf16 linear: equal up to torch's own rounding
+    (exp / rsqrt / GEMM order), a bf16 ulp on a few channels."""
+    rng = np.random.default_rng(13)
+    b, r, d, di = 8, 4, 576, 128
+    kv = rng.standard_normal((b, r, d)).astype(np.float32)
+    gate = rng.standard_normal((b, r, d)).astype(np.float32)
+    nw = Q.round_bf16(rng.uniform(0.5, 1.5, d).astype(np.float32))
+    wk = Q.round_bf16((rng.standard_normal((di, d)) * 0.04).astype(np.float32))
+    kw = Q.round_bf16(rng.uniform(0.5, 1.5, di).astype(np.float32))
+    cos, sin = C.rope_tables(np.arange(b) * 4 * 97, 64, 160000.0)
+    cos, sin = Q.round_bf16(cos), Q.round_bf16(sin)
+    rot, key = C.emit_group(kv, gate, r, nw, 1e-6, cos, sin, wk, kw, 1e-6)
+
+    def norm(h, w, eps):
+        hf = h.float()
+        return w * (hf * torch.rsqrt(hf.pow(2).mean(-1, keepdim=True) + eps)).to(torch.bfloat16)
+
+    def rot_t(x, c, s):
+        rd = c.shape[-1] * 2
+        even, odd = x[..., -rd::2].float(), x[..., -rd + 1::2].float()
+        out = torch.stack([even * c - odd * s, even * s + odd * c], -1).flatten(-2).to(torch.bfloat16)
+        return torch.cat([x[..., :-rd], out], -1)
+
+    kt, gt = torch.from_numpy(kv), torch.from_numpy(gate)
+    lat = norm((kt * gt.softmax(dim=1, dtype=torch.float32)).sum(1).to(torch.bfloat16),
+               torch.from_numpy(nw).bfloat16(), 1e-6)
+    ct, st = torch.from_numpy(cos).bfloat16(), torch.from_numpy(sin).bfloat16()
+    ref_rot = rot_t(lat, ct, st).float().numpy()
+    k = torch.nn.functional.linear(lat, torch.from_numpy(wk).bfloat16())
+    ref_key = rot_t(norm(k, torch.from_numpy(kw).bfloat16(), 1e-6), ct, st).float().numpy()
+    for got, ref in ((rot, ref_rot), (key, ref_key)):
+        rel = np.abs(got - ref) / np.maximum(np.abs(ref), 1e-30)
+        assert np.max(rel) <= 4 * 2.0 ** -8
+        assert np.mean(got == ref) > 0.95
