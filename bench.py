@@ -6,12 +6,16 @@ one token per row for B=32 rows at context 32768: bf16 queries, 128 heads over t
 compressed entries (ratio 4), top-2048, sliding window 128, per-head sink.  A "step" is one
 replay of a HIP graph holding ``SparseDecodeLayer.step`` of --layers (default 8)
 consecutive layers, each with its own caches and inputs, as a model's decode graph holds its
-layers: per layer the new token's kv RMSNorm + RoPE + window append, the indexer query's
-RoPE + quantization and the indexer scores (one launch), top-k, sparse MQA with the query's
-RoPE on load (split-KV), and the split merge with the output's inverse RoPE -- the
-per-token work of ``DeepseekV41Attention.forward`` between the projections
-(``--prologue rotated`` takes already-rotated q / q_idx / latent instead, as the kernels'
-reference signatures do).  Distinct layers keep one layer's working set
+layers: per layer the group emission (the token's compressor projections into the carry
+ring; every 4th token the group's pooling + norm, its rotated FP8-b128 cache entry and its
+index key; the token's RoPE tables from the position table), the new token's kv RMSNorm +
+RoPE + window append, the indexer query's RoPE + quantization and the indexer scores (one
+launch), top-k, sparse MQA with the query's RoPE on load (split-KV), and the split merge with
+the output's inverse RoPE -- the per-token work of ``DeepseekV41Attention.forward`` between
+the projections.  Every replay advances the positions, so the replays decode consecutive
+tokens ending at position ctx-1 and emit a group every 4th step, as a decode loop does
+(``--prologue rotated`` takes already-rotated q / q_idx / latent at a fixed position instead,
+without emission, as the kernels' reference signatures do).  Distinct layers keep one layer's working set
 (about 90 MB) from being served out of the last-level cache on the next step.  value =
 B x layers / replay time (token-rows through one attention layer per second); ms_per_step
 is per layer.  Inputs are synthetic and resident in HBM before timing starts.
@@ -97,24 +101,34 @@ def rope_inputs(torch, dev, positions):
     return tuple(out)
 
 
-def build_layer(torch, dev, nsplit=0, seed=None, config=2, fused=True):
+def build_layer(torch, dev, nsplit=0, seed=None, config=2, fused=True, start=None):
     """A decode layer of BASELINE config `config` (2, 4 or 5) with synthetic history: the
-    window ring holds tokens ctx-129 .. ctx-2, every compressed group is published, and the
-    step decodes the token at position ctx-1 (every group visible).  With `fused` the
-    inputs end with the four RoPE tables and the layer holds a kv norm weight."""
-    from mzoo_amd.decode import DecodeConfig, SparseDecodeLayer
+    window ring holds the 128 tokens before the start position, every compressed group is
+    published, and the first step decodes the token at `start` (default ctx-1).  With
+    `fused` the layer holds a kv norm weight and the compressor weights of the in-step
+    emission, and the inputs end with the token's fp32 compressor projections (the RoPE
+    tables come from the layer's position table); otherwise they are pre-rotated."""
+    from mzoo_amd.decode import CompressorWeights, DecodeConfig, SparseDecodeLayer
     c = DECODE[config]
     cfg = DecodeConfig(batch=c["batch"], heads=128, nope=512, rope=64, index_heads=64, index_dim=128, ratio=4,
                        window=128, topk=2048, max_groups=c["groups"], index_format=c["index_format"],
                        coarse_ratio=c["coarse_ratio"], coarse_groups=c["coarse_groups"], nsplit=nsplit or c["nsplit"])
     ctx = c["ctx"]
+    start = ctx - 1 if start is None else start
     gen = torch.Generator(device=dev).manual_seed(c["seed"] if seed is None else seed)
     rnd = lambda *shape: torch.randn(*shape, generator=gen, device=dev)  # noqa: E731
     sinks = rnd(cfg.heads)
     kv_w = (1.0 + 0.1 * rnd(cfg.dim)).bfloat16() if fused else None
-    layer = SparseDecodeLayer(cfg, dev, sinks=sinks, kv_norm_weight=kv_w)
+    cw = None
+    if fused:
+        cw = CompressorWeights(norm_weight=(1.0 + 0.1 * rnd(cfg.dim)).bfloat16(),
+                               wk=(0.04 * rnd(cfg.index_dim, cfg.dim)).bfloat16(),
+                               k_norm_weight=(1.0 + 0.1 * rnd(cfg.index_dim)).bfloat16(),
+                               coarse_norm_weight=(1.0 + 0.1 * rnd(cfg.dim)).bfloat16() if cfg.coarse_ratio else None,
+                               rope_theta=COMPRESS_ROPE_THETA)
+    layer = SparseDecodeLayer(cfg, dev, sinks=sinks, kv_norm_weight=kv_w, compressor=cw, max_position=ctx)
     b, d = cfg.batch, cfg.dim
-    layer.fill_window(rnd(b, cfg.window, d).bfloat16(), ctx - 2)
+    layer.fill_window(rnd(b, cfg.window, d).bfloat16(), start - 1)
     # groups in chunks (bounds the staging buffers of the larger configs)
     step = max(1, (1 << 27) // (b * d))
     for g0 in range(0, cfg.max_groups, step):
@@ -122,18 +136,28 @@ def build_layer(torch, dev, nsplit=0, seed=None, config=2, fused=True):
         layer.append_groups(g0, rnd(b, n, d).bfloat16(), rnd(b, n, cfg.index_dim).bfloat16())
     if cfg.coarse_ratio:
         layer.fill_coarse(rnd(b, cfg.coarse_groups, d).bfloat16())
-    layer.set_positions(ctx - 1)
+    layer.set_positions(start)
     q = rnd(b, cfg.heads, d).bfloat16()
     kv = rnd(b, d).bfloat16()
     q_idx = rnd(b, cfg.index_heads, cfg.index_dim).bfloat16()
     w = rnd(b, cfg.index_heads) * cfg.index_heads ** -0.5
-    rope = rope_inputs(torch, dev, [ctx - 1] * b) if fused else ()
-    return layer, (q, kv, q_idx, w) + rope, sinks
+    extra = ()
+    if fused:
+        # the carried partial group and the token's compressor projections
+        layer.set_carry(rnd(b, start % cfg.ratio, d), rnd(b, start % cfg.ratio, d))
+        extra = (rnd(b, d), rnd(b, d))
+        if cfg.coarse_ratio:
+            layer.set_carry(rnd(b, start % cfg.coarse_ratio, d), rnd(b, start % cfg.coarse_ratio, d), coarse=True)
+            extra += (rnd(b, d), rnd(b, d))
+    return layer, (q, kv, q_idx, w) + extra, sinks
 
 
-def run_step(layer, inp):
-    """``SparseDecodeLayer.step`` on bench inputs (the RoPE tables, if any, last)."""
-    return layer.step(*inp[:4], rope=inp[4:] if len(inp) > 4 else None)
+def run_step(layer, inp, advance=False):
+    """``SparseDecodeLayer.step`` on bench inputs: with compressor projections (the fused
+    step) the emission runs first and the RoPE tables come from the position table."""
+    if len(inp) > 4:
+        return layer.step(*inp[:4], rope="table", compress=inp[4:], advance=advance)
+    return layer.step(*inp[:4])
 
 
 def time_launches(torch, fn, iters):
@@ -164,7 +188,7 @@ def capture_layers(torch, layers, inputs):
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for layer, st in zip(layers, statics):
-            run_step(layer, st)
+            run_step(layer, st, advance=len(st) > 4)
     return g, statics
 
 
@@ -192,9 +216,24 @@ def graph_time(torch, fns, iters):
 
 def stage_times(torch, layers, inputs, iters):
     """Average duration of each kernel of the step alone, launch after launch cycling
-    through the layers (consecutive launches read different caches, as in the decode graph)."""
+    through the layers (consecutive launches read different caches, as in the decode graph).
+    The emission is timed at a group-completing position and at one that only carries the
+    token; 1 of `ratio` steps completes a group."""
     per_layer = [stage_fns(torch, layer, inp) for layer, inp in zip(layers, inputs)]
-    return {name: graph_time(torch, [d[name] for d in per_layer], iters) for name in per_layer[0]}
+    out = {name: graph_time(torch, [d[name] for d in per_layer], iters) for name in per_layer[0]}
+    if "decode_emit" in out:
+        cfg = layers[0].cfg
+        pos = [int(layer.positions[0]) for layer in layers]
+        completing = (pos[0] + 1) % cfg.ratio == 0
+        for layer, p in zip(layers, pos):
+            layer.set_positions(p - 1)
+        other = graph_time(torch, [d["decode_emit"] for d in per_layer], iters)
+        for layer, p in zip(layers, pos):
+            layer.set_positions(p)
+        out["decode_emit_group"], out["decode_emit_carry"] = (out.pop("decode_emit"), other) if completing \
+            else (other, out.pop("decode_emit"))
+        out["decode_emit"] = (out["decode_emit_group"] + (cfg.ratio - 1) * out["decode_emit_carry"]) / cfg.ratio
+    return out
 
 
 def stage_fns(torch, layer, inputs):
@@ -203,12 +242,29 @@ def stage_fns(torch, layer, inputs):
     cfg = layer.cfg
     b = cfg.batch
     q, kv, q_idx, w = inputs[:4]
-    rope = inputs[4:]
+    emit = len(inputs) > 4
+    rope = (layer.step_cos, layer.step_sin, layer.step_cos, layer.step_sin) if emit else ()
     ws = layer.workspace
     st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
     fns = {}
     fp8 = cfg.index_format == "fp8"
-    if rope:
+    pro = emit and layer._emit_prologue
+    if emit:
+        # the in-step group emission (one launch per compressed branch); the first launch also
+        # runs the step's prologue (window entry, indexer query RoPE + quantization)
+        fns["decode_emit"] = lambda: layer._emit(inputs[4:], True, prologue=(kv, q_idx) if pro else None)
+    pos = layer.positions.view(b, 1)
+    if pro:
+        # the plain scorer over the quantized query
+        if fp8:
+            fns["indexer_scores_fp8"] = lambda: indexer.scores_fp8(
+                layer.q_codes, layer.q_scales, w.view(b, 1, -1), layer.k_codes, layer.k_scales,
+                compress_ratio=cfg.ratio, positions=pos, out=layer.scores)
+        else:
+            fns["indexer_scores_mxfp4"] = lambda: indexer.scores_mxfp4(
+                layer.q_codes, layer.q_e8m0, w.view(b, 1, -1), layer.k_packed, layer.k_e8m0,
+                compress_ratio=cfg.ratio, positions=pos, out=layer.scores)
+    elif rope:
         cos, sin, icos, isin = rope
 
         def indexer_fused():
@@ -271,6 +327,8 @@ def cpu_baseline(torch, layer, inputs, budget_s, rows=None):
     """The CPU oracle's decode step (indexer scores -> top-k -> attention over window
     [+ coarse] + selected entries) in fp32 on the dequantized caches, for `rows` (default
     all) of the batch, on this host's cores; median of repeated steps."""
+    import numpy as np
+
     from mzoo_amd import quant
     from oracle import attention as OA
     from oracle import compressor as OC
@@ -278,7 +336,17 @@ def cpu_baseline(torch, layer, inputs, budget_s, rows=None):
     cfg = layer.cfg
     rows = list(range(cfg.batch)) if rows is None else rows
     q, kv, q_idx, w = (t.float().cpu()[rows] for t in inputs[:4])
-    tabs = [t.float().cpu()[rows].numpy() for t in inputs[4:]]
+    emit = len(inputs) > 4
+    tabs = []
+    if emit:
+        # the step's RoPE tables: row `pos` of the layer's position table (main and indexer)
+        p_ = int(layer.positions[0])
+        row = layer.rope_table[p_].float().cpu().numpy()
+        c_, s_ = (np.repeat(row[None, :32], len(rows), 0), np.repeat(row[None, 32:], len(rows), 0))
+        tabs = [c_, s_, c_, s_]
+        cw = layer.compressor
+        e_nw, e_wk, e_kw = (t.float().cpu().numpy() for t in (cw.norm_weight, cw.wk, cw.k_norm_weight))
+        e_kv = np.random.default_rng(0).standard_normal((len(rows), cfg.ratio, cfg.dim)).astype(np.float32)
     kv_w = None if layer.kv_norm_weight is None else layer.kv_norm_weight.float().cpu().numpy()
     win = quant.unpack_latent_fp8_b128(layer.win[rows], dtype=torch.float32).cpu()
     main = quant.unpack_latent_fp8_b128(layer.main[rows], dtype=torch.float32).cpu()
@@ -297,6 +365,11 @@ def cpu_baseline(torch, layer, inputs, budget_s, rows=None):
 
     def step():
         qx, qi = q, q_idx
+        if emit:
+            # the group emission, amortized: one row in `ratio` completes a group per step
+            n_emit = max(1, -(-len(rows) // cfg.ratio))
+            OC.emit_group(e_kv[:n_emit], e_kv[:n_emit], cfg.ratio, e_nw, cw.eps, tabs[0][:n_emit], tabs[1][:n_emit],
+                          e_wk, e_kw, cw.k_eps)
         if tabs:
             # the fused prologue: query / indexer-query RoPE, the new latent's norm + RoPE + packing
             cos, sin, icos, isin = tabs
@@ -328,6 +401,7 @@ def cpu_baseline(torch, layer, inputs, budget_s, rows=None):
     entries = cfg.window + nc + cfg.topk
     return {"value": len(rows) / med, "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"decode step of {len(rows)} of {cfg.batch} rows ("
+                      f"{'group emission for 1 row in ' + str(cfg.ratio) + ', ' if emit else ''}"
                       f"{'kv norm + RoPE, q / q_idx RoPE, ' if tabs else ''}{cfg.index_format} indexer over "
                       f"{cfg.max_groups} keys, top-{cfg.topk}, attention over {entries} entries x {cfg.heads} heads), "
                       f"fp32 torch on dequantized caches, median of {len(times)} steps"}
@@ -358,8 +432,10 @@ def run_decode(torch, dev, args):
     c = DECODE[args.config]
     nl = max(1, args.layers)
     fused = args.prologue == "fused"
-    built = [build_layer(torch, dev, args.nsplit, seed=c["seed"] + i, config=args.config, fused=fused)
-             for i in range(nl)]
+    # the replays advance the positions: the last timed replay decodes position ctx-1
+    start = c["ctx"] - 1 - (args.warmup + args.steps) if fused else None
+    built = [build_layer(torch, dev, args.nsplit, seed=c["seed"] + i, config=args.config, fused=fused,
+                         start=start) for i in range(nl)]
     layers = [b_[0] for b_ in built]
     inputs_all = [b_[1] for b_ in built]
     layer, inputs = layers[0], inputs_all[0]
@@ -386,7 +462,8 @@ def run_decode(torch, dev, args):
     attn_flops = rows * 4.0 * cfg.dim * cfg.heads * entries
     idx_bytes = rows * cfg.max_groups * KEY_BYTES[cfg.index_format]
     idx_flops = rows * 2.0 * cfg.index_heads * cfg.index_dim * cfg.max_groups
-    idx_stage = "indexer_decode_fp8" if cfg.index_format == "fp8" else "indexer_decode_mxfp4"
+    idx_stage = next(k for k in ("indexer_scores_fp8", "indexer_scores_mxfp4", "indexer_decode_fp8",
+                                 "indexer_decode_mxfp4") if k in stages)
     dominant = max(("sparse_mqa", idx_stage, "topk"), key=lambda k: stages[k])
     if dominant == "sparse_mqa":
         roof = roofline(None, attn_flops, attn_bytes, stages[dominant])
@@ -421,8 +498,10 @@ def run_decode(torch, dev, args):
                    "latent": "512+64", "index": f"64x128 {cfg.index_format}", "topk": cfg.topk,
                    "window": cfg.window, "coarse": nc, "nsplit": cfg.nsplit, "graph_layers": nl,
                    "step": "per attention layer, inside a graph replay of graph_layers layers",
-                   "prologue": ("fused: kv RMSNorm + RoPE + window append, q / q_idx RoPE and the output's "
-                                "inverse RoPE inside the step's launches") if fused else
+                   "prologue": ("fused: in-step group emission (carry ring, pooling + norm, cache entry and "
+                                "index key every 4th token; RoPE tables from the position table), kv RMSNorm + "
+                                "RoPE + window append, q / q_idx RoPE and the output's inverse RoPE inside the "
+                                "step's launches; positions advance every replay") if fused else
                                "rotated: q, q_idx and the new latent arrive normed and rotated"},
         "roofline": roof,
         "cpu_baseline": cpu,

@@ -119,18 +119,31 @@ int mzk_decode_prologue(const void* kv, int kv_dtype, int64_t B, int nope, int r
  *            the pinned order of mzk_compress), bf16;
  *   cache entry b*cache_batch_entries + g = FP8-b128 of the latent with its trailing 64
  *            channels rotated at position g*ratio (row g*ratio of rope_table);
- *   with wk (bf16 [128, 576]): key = RoPE(k_norm(bf16(latent . wk^T))) -- each output sums
- *            channels [0, 288) and [288, 576) in order, then the halves --, quantized as key
+ *   with wk (bf16 [128, 576]): key = RoPE(k_norm(bf16(latent . wk^T))) -- 8 partials per output
+ *            (partial j: 16-byte chunks j, j+8, ... in order) meet in an xor butterfly --, quantized as key
  *            b*key_batch_entries + g: key_format 0 FP8 b128 (k_codes [.., 128] e4m3 +
  *            k_scales fp32), 1 MXFP4 (k_codes [.., 64] e2m1 + k_scales e8m0 [.., 4]).
  * rope_table: bf16 [table_rows, 64], row p = cos (32) | sin (32) of position p (the compress
  * RoPE).  step_cos / step_sin (bf16 [B, 32], or NULL): receive row pos of the table -- the
- * token's RoPE for the step's later launches.  Rows with pos < 0 do nothing. */
+ * token's RoPE for the step's later launches.  Rows with pos < 0 do nothing.
+ * The step's prologue (kv_proj non-NULL; skipped for rows with pos >= table_rows), at the
+ * token's RoPE (row pos of the table):
+ *   kv_proj bf16 [B, 576] (the wkv projection) -> RoPE(kv_norm(kv_proj)) (kv_weight bf16 [576],
+ *            kv_eps; the pinned order of mzk_rms_norm) packed FP8-b128 into window-ring slot
+ *            b*win_batch_entries + pos % win_cap (owlet1/attention.py:149-154), as
+ *            mzk_decode_prologue;
+ *   q_idx bf16 [B, 64, 128] (or NULL) -> RoPE of channels 64..127 (owlet1/indexer.py:126-128),
+ *            quantized per head: q_format 0 FP8 b128 (q_codes [B, 64, 128] e4m3 + q_scales
+ *            fp32 [B, 64]), 1 MXFP4 (q_codes [B, 64, 64] e2m1 + q_scales e8m0 [B, 64, 4]) --
+ *            the query operands of mzk_indexer_scores_fp8 / _mxfp4. */
 int mzk_decode_emit(const int64_t* positions, int64_t B, const float* kv, const float* gate, float* carry_kv,
                     float* carry_gate, int ratio, const void* norm_weight, float eps, uint8_t* cache,
                     int64_t cache_batch_entries, int64_t cache_cap, const void* wk, const void* k_norm_weight,
                     float k_eps, int key_format, uint8_t* k_codes, void* k_scales, int64_t key_batch_entries,
-                    const void* rope_table, int64_t table_rows, void* step_cos, void* step_sin, void* stream);
+                    const void* rope_table, int64_t table_rows, void* step_cos, void* step_sin,
+                    const void* kv_proj, const void* kv_weight, float kv_eps, uint8_t* win_cache,
+                    int64_t win_batch_entries, int win_cap, const void* q_idx, int q_format, uint8_t* q_codes,
+                    void* q_scales, void* stream);
 
 /* ---------------------------------------------------------------------------------
  * Piece 2: KV compressor and RoPE

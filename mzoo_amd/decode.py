@@ -212,6 +212,12 @@ class SparseDecodeLayer:
         self.rope_table = rope_table(npos, cfg.rope, self.compressor.rope_theta).to(dev).contiguous()
         self.step_cos = torch.zeros(b, cfg.rope // 2, **bf)
         self.step_sin = torch.zeros(b, cfg.rope // 2, **bf)
+        # 64 indexer heads: the emission launch also runs the step's prologue (window entry,
+        # the indexer query's RoPE and quantization) and the indexer is the plain scorer
+        self._emit_prologue = cfg.index_heads == 64
+        if self._emit_prologue and cfg.index_format == "fp8":
+            self.q_codes = torch.empty(b, 1, cfg.index_heads, cfg.index_dim, dtype=torch.uint8, device=dev)
+            self.q_scales = torch.empty(b, 1, cfg.index_heads, dtype=torch.float32, device=dev)
 
     # ---- state ---------------------------------------------------------------------------
     def set_positions(self, pos) -> None:
@@ -254,8 +260,10 @@ class SparseDecodeLayer:
         ck[:, :n] = kv.float()
         cg[:, :n] = gate.float()
 
-    def _emit(self, compress, rope_from_table: bool) -> None:
-        """The in-step emission launches (one per compressed branch), see the module doc."""
+    def _emit(self, compress, rope_from_table: bool, prologue=None) -> None:
+        """The in-step emission launches (one per compressed branch), see the module doc.
+        ``prologue`` = (kv projection bf16 [B, D], indexer query bf16 [B, 64, Di]): the first
+        launch also writes the token's window entry and the quantized indexer query."""
         cfg, cw = self.cfg, self.compressor
         b = cfg.batch
         st = _lib.stream_of(self.positions)
@@ -266,11 +274,24 @@ class SparseDecodeLayer:
                 raise ValueError(f"step(compress=...): fp32 [{b}, {cfg.dim}] projections expected")
         keys = (self.k_codes, self.k_scales) if fp8 else (self.k_packed, self.k_e8m0)
         tabs = (self.step_cos.data_ptr(), self.step_sin.data_ptr()) if rope_from_table else (None, None)
+        pro = (None, None, 0.0, None, 0, 0, None, 0, None, None)
+        if prologue is not None:
+            pkv, pq = prologue
+            if pkv.dtype != torch.bfloat16 or pkv.shape != (b, cfg.dim) or not pkv.is_contiguous():
+                raise ValueError(f"step: kv must be a contiguous bf16 [{b}, {cfg.dim}] projection")
+            if pq.dtype != torch.bfloat16 or pq.shape != (b, cfg.index_heads, cfg.index_dim) \
+                    or not pq.is_contiguous():
+                raise ValueError(f"step: q_idx must be a contiguous bf16 [{b}, {cfg.index_heads}, "
+                                 f"{cfg.index_dim}] tensor")
+            _lib.require_gpu(pkv, pq)
+            qs = self.q_scales if fp8 else self.q_e8m0
+            pro = (pkv.data_ptr(), self.kv_norm_weight.data_ptr(), self.kv_norm_eps, self.win.data_ptr(),
+                   cfg.window, cfg.window, pq.data_ptr(), 0 if fp8 else 1, self.q_codes.data_ptr(), qs.data_ptr())
         _lib.call("mzk_decode_emit", self.positions.data_ptr(), b, kv.data_ptr(), gate.data_ptr(),
                   self.carry_kv.data_ptr(), self.carry_gate.data_ptr(), cfg.ratio, cw.norm_weight.data_ptr(), cw.eps,
                   self.main.data_ptr(), cfg.max_groups, cfg.max_groups, cw.wk.data_ptr(),
                   cw.k_norm_weight.data_ptr(), cw.k_eps, 0 if fp8 else 1, keys[0].data_ptr(), keys[1].data_ptr(),
-                  cfg.max_groups, self.rope_table.data_ptr(), self.rope_table.shape[0], *tabs, st)
+                  cfg.max_groups, self.rope_table.data_ptr(), self.rope_table.shape[0], *tabs, *pro, st)
         if cfg.coarse_ratio:
             if len(compress) != 4:
                 raise ValueError("step(compress=...): the coarse branch needs (kv, gate, coarse_kv, coarse_gate)")
@@ -282,7 +303,7 @@ class SparseDecodeLayer:
                       self.coarse_carry_kv.data_ptr(), self.coarse_carry_gate.data_ptr(), cfg.coarse_ratio,
                       cw.coarse_norm_weight.data_ptr(), cw.eps, self.coarse.data_ptr(), cfg.coarse_groups,
                       cfg.coarse_groups, None, None, 0.0, 0, None, None, 0, self.rope_table.data_ptr(),
-                      self.rope_table.shape[0], None, None, st)
+                      self.rope_table.shape[0], None, None, None, None, 0.0, None, 0, 0, None, 0, None, None, st)
 
     def fill_coarse(self, latents: torch.Tensor) -> None:
         """latents [B, n, D] -> coarse entries 0..n-1 of every row."""
@@ -312,10 +333,25 @@ class SparseDecodeLayer:
             raise ValueError(f"step: rope must be a tuple of tables or 'table', got {rope!r}")
         if (compress is not None or from_table) and self.compressor is None:
             raise ValueError("step(compress=... / rope='table'): the layer was built without CompressorWeights")
+        if from_table and compress is None:
+            raise ValueError("step(rope='table'): the tables are gathered by the emission launch (compress=...)")
+        if from_table and self._emit_prologue:
+            if kvc is None or self.kv_norm_weight is None:
+                raise ValueError("step(rope='table'): needs the kv projection and the layer's kv_norm_weight")
+            self._emit(compress, True, prologue=(kvc, q_idx.contiguous()))
+            pos = self.positions.view(b, 1)
+            if fp8:
+                indexer.scores_fp8(self.q_codes, self.q_scales, w.view(b, 1, -1), self.k_codes, self.k_scales,
+                                   compress_ratio=cfg.ratio, positions=pos, out=self.scores)
+            else:
+                indexer.scores_mxfp4(self.q_codes, self.q_e8m0, w.view(b, 1, -1), self.k_packed, self.k_e8m0,
+                                     compress_ratio=cfg.ratio, positions=pos, out=self.scores)
+            self._select_and_attend(q, (self.step_cos, self.step_sin))
+            if advance:
+                self.positions.add_(1)
+            return self.out if self.out_proj is None else self.out_proj(self.out)
         if compress is not None:
             self._emit(compress, from_table)
-        elif from_table:
-            raise ValueError("step(rope='table'): the tables are gathered by the emission launch (compress=...)")
         if from_table:
             rope = (self.step_cos, self.step_sin, self.step_cos, self.step_sin)
         if rope is not None:

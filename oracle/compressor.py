@@ -181,21 +181,28 @@ def rope_tables(positions, rope_dim: int, theta: float):
 
 def linear_pinned(x, w, dtype: str = "bfloat16") -> np.ndarray:
     """``nn.Linear`` (no bias) of x [..., D] by w [out, D] in the order the decode-step
-    emission kernel evaluates it: each output sums channels [0, D/2) and then, separately,
-    [D/2, D) in ascending order in float32 (a bf16 x bf16 product is exact in float32), adds
-    the two halves and rounds to ``dtype``.  Differs from a library GEMM's order only in
-    float32 rounding (tests bound it against float64)."""
+    emission kernel evaluates it (D a multiple of 64): the row is cut into 16-byte chunks of
+    8 channels; partial j (j = 0..7) sums, in float32 from 0, chunk j, j+8, j+16, ... with its
+    8 channels in order (a bf16 x bf16 product is exact in float32); the partials meet in an
+    xor butterfly -- ((p0+p4)+(p2+p6)) + ((p1+p5)+(p3+p7)) -- and the total is rounded to
+    ``dtype``.  Differs from a library GEMM's order only in float32 rounding (tests bound it
+    against float64)."""
     x = np.asarray(x, F32)
     w = np.asarray(w, F32)
     d = x.shape[-1]
-    h = d // 2
-    acc = [np.zeros(x.shape[:-1] + (w.shape[0],), F32) for _ in range(2)]
-    for half in range(2):
-        a = acc[half]
-        for i in range(half * h, (half + 1) * h):
-            a = a + x[..., i:i + 1] * w[:, i]
-        acc[half] = a
-    return round_to(acc[0] + acc[1], dtype)
+    nchunk = d // 8
+    parts = []
+    for j in range(8):
+        a = np.zeros(x.shape[:-1] + (w.shape[0],), F32)
+        for c in range(j, nchunk, 8):
+            for e in range(8):
+                i = 8 * c + e
+                a = a + x[..., i:i + 1] * w[:, i]
+        parts.append(a)
+    s1 = [parts[j] + parts[j ^ 4] for j in range(8)]
+    s2 = [s1[j] + s1[j ^ 2] for j in range(8)]
+    total = s2[0] + s2[1]
+    return round_to(total, dtype)
 
 
 def emit_group(kv, gate, ratio: int, norm_w, eps: float, cos, sin, wk=None, k_norm_w=None, k_eps: float = 1e-6,

@@ -6,12 +6,12 @@ the oracle, the partial group in the carry ring, the window holding the last tok
 replay gets new inputs (q, kv, the indexer query and weights, the compressor projections of
 the token) through the graph's static buffers and advances every row's position; on the
 device the step emits each completed group into the main cache and the key cache, gathers
-the token's RoPE tables from the position table, appends the window entry, scores, selects
-and attends.  Checked after every replay:
+the token's RoPE tables from the position table, appends the window entry, rotates and
+quantizes the indexer query, scores, selects and attends.  Checked after every replay:
 
 * the RoPE table against the oracle's tables, bit for bit;
-* the window ring, the main-cache entries and the index keys (FP8 b128 or MXFP4), bit for
-  bit against the oracle (``compressor.emit_group`` + the packers; ``decode_kv_latent``);
+* the window ring, the main-cache entries, the index keys and the quantized indexer query
+  (FP8 b128 or MXFP4), bit for bit against the oracle (``compressor.emit_group`` + the packers; ``decode_kv_latent``);
 * the selection against the oracle's top-k of the oracle's scores up to near-ties;
 * the output (inverse RoPE applied) against the oracle's attention over the window, the
   coarse entries (hierarchical case) and the selected entries, to the attention bar.
@@ -164,6 +164,12 @@ def test_replays_across_group_boundaries(dev, fmt, coarse):
             assert np.array_equal(layer.coarse.cpu().numpy(), coarse_ent), f"step {i}: coarse cache"
         # indexer + top-k
         q_rot = C.rope(q_idx, cs[:, None], sn[:, None], dtype="bfloat16")
+        # the quantized indexer query the emission launch's prologue wrote
+        qa, qsc = _keys(q_rot, fmt)
+        gq = layer.q_codes.cpu().numpy().reshape(qa.shape)
+        gqs = (layer.q_scales if fmt == "fp8" else layer.q_e8m0).cpu().numpy().reshape(qsc.shape)
+        assert np.array_equal(gq, qa), f"step {i}: indexer query codes"
+        assert np.array_equal(gqs.view(np.uint8), qsc.view(np.uint8)), f"step {i}: indexer query scales"
         qd = Q.fake_quant_fp8_block(q_rot, 128) if fmt == "fp8" else Q.fake_quant_fp4_block(q_rot, 32)
         kd = _dequant_keys(key_a, key_s, fmt)
         posv = torch.full((b, 1), pos)
