@@ -81,6 +81,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline time budget")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--stage-iters", type=int, default=0, help="launches per stage timing (0: max(steps, 50))")
+    ap.add_argument("--kernels", action="store_true",
+                    help="instead of the step: time the compressor and the quant / dequant kernels alone in "
+                         "prefill shape (batch 1, seq 8192) and print their GB/s against 8 TB/s")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (3 launches): the reference kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -645,6 +648,50 @@ def prefill_cpu_baseline(torch, q, kv, main, q_idx, k_idx, w, sinks, win, ratio,
                       f"attention over window + selected entries x 128 heads), fp32 torch, median of {len(times)} runs"}
 
 
+def run_kernels(torch, dev, args):
+    """The compressor and the quant / dequant kernels alone, in the prefill shape of BASELINE
+    config 3 (batch 1, seq 8192, latent 512 + 64, indexer 64 x 128, ratio 4): each launch
+    timed in a graph of back-to-back launches (HIP events on the launch stream), bytes =
+    the kernel's algorithmic reads + writes."""
+    from mzoo_amd import cache, quant
+    t, d, hi, di, r = 8192, 576, 64, 128, 4
+    gen = torch.Generator(device=dev).manual_seed(3)
+    rnd = lambda *shape: torch.randn(*shape, generator=gen, device=dev)  # noqa: E731
+    kv, gate = rnd(1, t, d), rnd(1, t, d)
+    nw = (1.0 + 0.1 * rnd(d)).bfloat16()
+    out_lat = torch.empty(1, t // r, d, dtype=torch.bfloat16, device=dev)
+    q = rnd(t, hi, di).bfloat16()
+    x = rnd(t, d).bfloat16()
+    ent = quant.pack_latent_fp8_b128(x)
+    codes, scales = quant.quant_fp8_block(q, 128)
+    packed, e8 = quant.quant_mxfp4(q)
+    iters = max(args.stage_iters, 200)
+    eb = quant.entry_bytes()
+    cases = {
+        # the compressor: fp32 kv + gate of 8192 tokens -> 2048 normed bf16 groups
+        "compress_r4": (lambda: cache.compress(kv, gate, r, nw, 1e-6, torch.bfloat16, out=out_lat),
+                        2 * t * d * 4 + (t // r) * d * 2 + d * 2),
+        # the indexer query quantizers: bf16 [8192 x 64 x 128] -> FP8 b128 / MXFP4
+        "quant_fp8_b128": (lambda: quant.quant_fp8_block(q, 128), t * hi * di * 2 + t * hi * di + t * hi * 4),
+        "quant_mxfp4": (lambda: quant.quant_mxfp4(q), t * hi * di * 2 + t * hi * di // 2 + t * hi * di // 32),
+        "dequant_fp8_b128": (lambda: quant.dequant_fp8_block(codes, scales, 128, dtype=torch.bfloat16),
+                             t * hi * di + t * hi * 4 + t * hi * di * 2),
+        "dequant_mxfp4": (lambda: quant.dequant_mxfp4(packed, e8, dtype=torch.bfloat16),
+                          t * hi * di // 2 + t * hi * di // 32 + t * hi * di * 2),
+        # the latent cache entries: bf16 [8192 x 576] <-> 656-byte FP8-b128 entries
+        "pack_latent_fp8_b128": (lambda: quant.pack_latent_fp8_b128(x, out=ent), t * d * 2 + t * eb),
+        "unpack_latent_fp8_b128": (lambda: quant.unpack_latent_fp8_b128(ent), t * eb + t * d * 2),
+    }
+    res = {}
+    for name, (fn, nbytes) in cases.items():
+        us = graph_time(torch, [fn], iters)
+        res[name] = {"us": round(us, 3), "bytes": int(nbytes), "GB/s": round(nbytes / us / 1e3, 1),
+                     "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+    return {"metric": "prefill-shape kernel bandwidth", "unit": "GB/s", "peak": HBM_PEAK_GBS,
+            "config": {"workload": "config3 prefill shape: batch 1, seq 8192, latent 512+64, indexer 64x128, "
+                                   "ratio 4", "iters": iters}, "kernels": res}
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -661,6 +708,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4}))
+        return
+    if args.kernels:
+        print(json.dumps(run_kernels(torch, dev, args)))
         return
     out = run_prefill(torch, dev, args) if args.config == 3 else run_decode(torch, dev, args)
     print(json.dumps(out))

@@ -223,8 +223,9 @@ struct RowPlan {
     b = row32 / static_cast<uint32_t>(p.S);
   }
 
-  // The row's entry list split, given its absolute position.
-  __device__ void plan(const AttnParams& p, int64_t row_pos) {
+  // The row's entry list split, given its absolute position; `ns_used` (-1: topk) is the
+  // length of the sparse list to walk.
+  __device__ void plan(const AttnParams& p, int64_t row_pos, int ns_used = -1) {
     pos = row_pos < -1 ? -1 : row_pos;  // a negative position sees no window or dense entry
     nw = static_cast<int>(pos + 1 < p.window ? pos + 1 : p.window);
     int nd = 0;
@@ -232,7 +233,7 @@ struct RowPlan {
       const int64_t n = (pos + 1) / p.dense_ratio;
       nd = static_cast<int>(n < p.dense_cap ? n : p.dense_cap);
     }
-    const int ns = p.main ? p.topk : 0;
+    const int ns = p.main ? (ns_used >= 0 ? ns_used : p.topk) : 0;
     nwd = nw + nd;
     const int total = nwd + ns;
     int chunk = (total + p.nsplit - 1) / p.nsplit;
@@ -293,6 +294,39 @@ struct RowPlan {
     }
     sidx = (const __attribute__((address_space(3))) int32_t*)(sidx_lds);
     sidx_cap = cap;
+  }
+
+  // With the whole list prefetched (prefetch_indices returned true): the number of its
+  // leading valid indices (0 <= g < G) when every valid index precedes every invalid one --
+  // the form the top-k launch writes (ascending picks, then -1) -- else topk.  Walking only
+  // that prefix skips tiles that would be all masked.  `wred` is 2 * (NT / 64) ints of LDS;
+  // two workgroup barriers.
+  __device__ int valid_prefix(const AttnParams& p, int tid, const v4i& pre, int* wred) const {
+    constexpr int NW = NT / 64;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int64_t glim = p.G;
+    auto valid = [&](int j) { return 4 * tid + j < p.topk && pre[j] >= 0 && pre[j] < glim; };
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) c += valid(j);
+    int wc = c;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) wc += __shfl_xor(wc, m, 64);
+    if (lane == 0) wred[wave] = wc;
+    __syncthreads();
+    int n = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) n += wred[w];
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bad |= valid(j) && 4 * tid + j >= n;
+    const uint64_t bb = __ballot(bad);
+    if (lane == 0) wred[NW + wave] = bb != 0;
+    __syncthreads();
+    int nb = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) nb += wred[NW + w];
+    return nb ? p.topk : n;
   }
 
   // sparse index of list position v (-1 outside the sparse part of this split)
@@ -710,7 +744,8 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
       qrs[r] = *reinterpret_cast<const uint2*>(sb + roff + 8 * r);
     }
   }
-  rp.plan(p, row_pos);
+  __shared__ int wred[2 * 8];
+  rp.plan(p, row_pos, pre_ok ? rp.valid_prefix(p, tid, pre, wred) : -1);
   if (pre_ok) rp.stage_prefetched(sidx, kSplitIdxCap, tid, pre);
   else rp.stage_indices(p, sidx, kSplitIdxCap, tid);
   __syncthreads();
@@ -1130,7 +1165,7 @@ int dispatch_heads(const AttnParams& p, int64_t rows, hipStream_t s) {
   if constexpr (D > 256) {
     // 64 heads per workgroup, each 32-head group split by D over 4 waves
     using M = SplitSmem<FMT, D, NOPE>;
-    static_assert(M::LDS + 4 * kSplitIdxCap + 8 * kTile * 8 + 64 <= 160 * 1024, "LDS budget");
+    static_assert(M::LDS + 4 * kSplitIdxCap + 8 * kTile * 8 + 128 <= 160 * 1024, "LDS budget");
     auto kern = sparse_mqa_dsplit_kernel<FMT, D, NOPE>;
     // the dynamic-LDS limit is a per-device function attribute: set once per device
     static std::atomic<bool> attr_set[kMaxDevices] = {};  // setting it twice is harmless
