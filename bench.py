@@ -220,22 +220,38 @@ def graph_time(torch, fns, iters):
 def stage_times(torch, layers, inputs, iters):
     """Average duration of each kernel of the step alone, launch after launch cycling
     through the layers (consecutive launches read different caches, as in the decode graph).
-    The emission is timed at a group-completing position and at one that only carries the
-    token; 1 of `ratio` steps completes a group."""
+    The emission is timed at three positions -- one that completes a group of every branch,
+    one that completes a fine group only (configs with a coarse branch) and one that only
+    carries the token -- and amortized over the branches' ratios (1 of `ratio` steps completes
+    a fine group, 1 of `coarse_ratio` a coarse one)."""
     per_layer = [stage_fns(torch, layer, inp) for layer, inp in zip(layers, inputs)]
+    emit = per_layer[0].pop("decode_emit", None)
+    if emit is not None:
+        emits = [d.pop("decode_emit") for d in per_layer[1:]]
     out = {name: graph_time(torch, [d[name] for d in per_layer], iters) for name in per_layer[0]}
-    if "decode_emit" in out:
+    if emit is not None:
         cfg = layers[0].cfg
-        pos = [int(layer.positions[0]) for layer in layers]
-        completing = (pos[0] + 1) % cfg.ratio == 0
-        for layer, p in zip(layers, pos):
-            layer.set_positions(p - 1)
-        other = graph_time(torch, [d["decode_emit"] for d in per_layer], iters)
-        for layer, p in zip(layers, pos):
+        saved = [int(layer.positions[0]) for layer in layers]
+        period = cfg.ratio * max(cfg.coarse_ratio // cfg.ratio, 1) if cfg.coarse_ratio else cfg.ratio
+        p_all = (saved[0] + 1) // period * period - 1  # completes every branch's group
+        if p_all < period:
+            p_all += period
+
+        def at(pos):
+            for layer in layers:
+                layer.set_positions(pos)
+            return graph_time(torch, [emit] + emits, iters)
+        out["decode_emit_group"] = at(p_all)
+        out["decode_emit_carry"] = at(p_all - 1)
+        amort = (out["decode_emit_group"] + (cfg.ratio - 1) * out["decode_emit_carry"]) / cfg.ratio
+        if cfg.coarse_ratio:
+            out["decode_emit_fine_group"] = at(p_all - cfg.ratio)
+            n_fine = cfg.coarse_ratio // cfg.ratio
+            amort = (out["decode_emit_group"] + (n_fine - 1) * out["decode_emit_fine_group"] +
+                     (cfg.coarse_ratio - n_fine) * out["decode_emit_carry"]) / cfg.coarse_ratio
+        out["decode_emit"] = amort
+        for layer, p in zip(layers, saved):
             layer.set_positions(p)
-        out["decode_emit_group"], out["decode_emit_carry"] = (out.pop("decode_emit"), other) if completing \
-            else (other, out.pop("decode_emit"))
-        out["decode_emit"] = (out["decode_emit_group"] + (cfg.ratio - 1) * out["decode_emit_carry"]) / cfg.ratio
     return out
 
 
