@@ -1232,9 +1232,11 @@ template <int D>
 void launch_combine(const uint16_t* po, const float* pml, int nsplit, int H, int64_t S, const float* sinks,
                     uint16_t* out, float* lse, int64_t rows, const uint16_t* rope_cos, const uint16_t* rope_sin,
                     int rope_dim, hipStream_t s) {
-  // two 16-byte pieces per thread where a thread's channels cannot straddle the rope slice
-  // (measured faster than one; four are slower again)
-  if (D % 16 == 0 && (rope_cos == nullptr || (D - rope_dim) % 16 == 0)) {
+  // two 16-byte pieces per thread for a few splits, where a thread's channels cannot straddle
+  // the rope slice (config 2, 4 splits: 7.4 vs 7.9 us); with more splits, whose chunk of 8
+  // then holds 16 pieces in flight per thread, one is faster (configs 4 / 5, 16 / 32 splits:
+  // 7.9 vs 8.4 and 9.2 vs 11.2 us)
+  if (nsplit <= 4 && D % 16 == 0 && (rope_cos == nullptr || (D - rope_dim) % 16 == 0)) {
     const int64_t n = rows * H * (D / 16);
     combine_kernel<D, 2><<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(po, pml, nsplit, H, S, rows, sinks,
                                                                                 out, lse, rope_cos, rope_sin, rope_dim);

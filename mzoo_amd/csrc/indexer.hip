@@ -35,12 +35,8 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 constexpr int kWaves = 4;
-constexpr int kNkb = 4;                          // 32-key tiles per wave (prefill form)
+constexpr int kNkb = 4;                          // 32-key tiles per wave
 constexpr int kKeysPerWg = kWaves * kNkb * 32;   // 512
-// The row kernel's tiles per wave: 4 for FP8 keys (132 B), 2 for MXFP4 keys (68 B) -- the
-// faster of 2 / 4 / 8 at configs 2 and 4 (twice the workgroups for the smaller keys)
-__host__ __device__ constexpr int nkb_of(int fmt) { return fmt == 1 ? 2 : 4; }
-__host__ __device__ constexpr int keys_per_wg(int fmt) { return kWaves * nkb_of(fmt) * 32; }
 
 // channels consumed by one MFMA step, per format
 template <int FMT> struct Step;
@@ -243,7 +239,7 @@ struct FusedKv {
 template <int FMT>
 constexpr int q_pitch() { return FMT == kFp8 ? 128 + 16 : 64 + 16; }
 
-// One workgroup = 4 waves = one query row x keys_per_wg(FMT) keys (see the tiling note above).
+// One workgroup = 4 waves = one query row x kKeysPerWg keys (see the tiling note above).
 // QRAW: the query arrives as bf16 [Hi, 128] and each workgroup quantizes it into LDS --
 // thread t owns head t/4, channels 32(t%4)..+31.  FP8 b128 (owlet1/quant.py:72-86: one
 // power-of-two scale per head) uses v_cvt_pk_fp8_f32, which equals the e4m3 encoder of the
@@ -278,8 +274,7 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
   const uint8_t* ke_base = FMT == kMxfp4 ? p.k_e8m0 + b * p.kbs * (DI / 32) : nullptr;
   float* out = p.scores + row * p.sstride;
 
-  constexpr int NKB = nkb_of(FMT);
-  const int64_t wave_key0 = static_cast<int64_t>(blockIdx.x) * keys_per_wg(FMT) + wave * (NKB * 32);
+  const int64_t wave_key0 = static_cast<int64_t>(blockIdx.x) * kKeysPerWg + wave * (kNkb * 32);
   // Load order.  Vector-memory loads complete in issue order, so the small operands every
   // tile needs -- the query (fragments, or the bf16 rows to quantize) and the head
   // weights -- go first; then all key fragments of the wave's tiles, so tile 0's MFMAs
@@ -327,10 +322,10 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
   if constexpr (FUSE) {
     if (blockIdx.x == 0 && tid < 64) fkv.load(p, row, tid);
   }
-  Frag bf[NKB][NST];
-  float ksv[NKB];  // FP8: the per-key scales
+  Frag bf[kNkb][NST];
+  float ksv[kNkb];  // FP8: the per-key scales
 #pragma unroll
-  for (int t = 0; t < NKB; ++t) {
+  for (int t = 0; t < kNkb; ++t) {
     // keys at or beyond G read row G-1 instead: their score columns are never written
     const int64_t g = wave_key0 + t * 32 + (lane & 31);
     const int64_t gc = g < G ? g : G - 1;
@@ -485,7 +480,7 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
     for (int j = 0; j < 16; ++j) coef[mb][j] = __shfl(cwq, mb * 32 + acc_row(j, lane), 64);
 
 #pragma unroll
-  for (int t = 0; t < NKB; ++t) {
+  for (int t = 0; t < kNkb; ++t) {
     const int64_t g0 = wave_key0 + t * 32;
     const int64_t g = g0 + (lane & 31);
     if (g0 >= G) break;
@@ -753,7 +748,7 @@ __global__ void __launch_bounds__(kWaves * 64, 2) indexer_prefill_fp8_kernel(con
 
 template <int FMT, int DI>
 int launch_di(const IdxParams& p, int64_t rows, hipStream_t s) {
-  dim3 grid(static_cast<unsigned>((p.G + keys_per_wg(FMT) - 1) / keys_per_wg(FMT)), static_cast<unsigned>(rows));
+  dim3 grid(static_cast<unsigned>((p.G + kKeysPerWg - 1) / kKeysPerWg), static_cast<unsigned>(rows));
   if (p.Hi <= 32) indexer_scores_kernel<FMT, DI, 1, false, false><<<grid, kWaves * 64, 0, s>>>(p);
   else indexer_scores_kernel<FMT, DI, 2, false, false><<<grid, kWaves * 64, 0, s>>>(p);
   return MZK_OK;
@@ -917,7 +912,7 @@ extern "C" int mzk_indexer_decode_fp8(const void* q_idx, const float* w, const u
   p.win = win_cache;
   p.win_batch_entries = win_batch_entries;
   p.win_cap = win_cap;
-  dim3 grid(static_cast<unsigned>((G + keys_per_wg(kFp8) - 1) / keys_per_wg(kFp8)), static_cast<unsigned>(B));
+  dim3 grid(static_cast<unsigned>((G + kKeysPerWg - 1) / kKeysPerWg), static_cast<unsigned>(B));
   hipStream_t s = as_stream(stream);
   if (Hi <= 32) {
     if (kv) indexer_scores_kernel<kFp8, 128, 1, true, true><<<grid, kWaves * 64, 0, s>>>(p);
@@ -964,7 +959,7 @@ extern "C" int mzk_indexer_decode_mxfp4(const void* q_idx, const float* w, const
   p.win = win_cache;
   p.win_batch_entries = win_batch_entries;
   p.win_cap = win_cap;
-  dim3 grid(static_cast<unsigned>((G + keys_per_wg(kMxfp4) - 1) / keys_per_wg(kMxfp4)), static_cast<unsigned>(B));
+  dim3 grid(static_cast<unsigned>((G + kKeysPerWg - 1) / kKeysPerWg), static_cast<unsigned>(B));
   hipStream_t s = as_stream(stream);
   if (Hi <= 32) {
     if (kv) indexer_scores_kernel<kMxfp4, 128, 1, true, true><<<grid, kWaves * 64, 0, s>>>(p);
@@ -1026,8 +1021,7 @@ extern "C" int mzk_indexer_decode_fused(int q_format, const void* q_idx, const f
   p.win = win_cache;
   p.win_batch_entries = win_batch_entries;
   p.win_cap = win_cap;
-  const int kpw = keys_per_wg(fp8 ? kFp8 : kMxfp4);
-  dim3 grid(static_cast<unsigned>((G + kpw - 1) / kpw), static_cast<unsigned>(B));
+  dim3 grid(static_cast<unsigned>((G + kKeysPerWg - 1) / kKeysPerWg), static_cast<unsigned>(B));
   hipStream_t s = as_stream(stream);
   if (fp8) {
     if (Hi <= 32) indexer_scores_kernel<kFp8, 128, 1, true, false, true><<<grid, kWaves * 64, 0, s>>>(p);
