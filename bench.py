@@ -84,6 +84,9 @@ def parse():
     ap.add_argument("--kernels", action="store_true",
                     help="instead of the step: time the compressor and the quant / dequant kernels alone in "
                          "prefill shape (batch 1, seq 8192) and print their GB/s against 8 TB/s")
+    ap.add_argument("--reindex", action="store_true",
+                    help="instead of the step: time the two-level selection (dense scores + top-k, level one, "
+                         "level two's candidate scorer + top-k) at growing cache lengths")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (3 launches): the reference kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -708,6 +711,65 @@ def run_kernels(torch, dev, args):
                                    "ratio 4", "iters": iters}, "kernels": res}
 
 
+def run_reindex(torch, dev, args):
+    """The two-level selection's cost against the cache length T (tickets/0009: level two
+    is O(candidates), not O(T)).  Per T, batch rows at their last position, MXFP4 (B=4, the
+    config-5 indexer) and FP8 (B=32, the config-2 indexer) keys: the dense score kernel and
+    its top-2048 (what a layer without candidates pays), level one's block selection (the
+    candidate source's extra work), and level two -- the candidate scorer over 2048 blocks
+    of 8 plus its top-2048 mapped to key positions.  Each launch timed in a graph of
+    back-to-back launches (HIP events on the launch stream)."""
+    from mzoo_amd import indexer as MI
+    from mzoo_amd import quant
+    nblk, bs, k, hi, di, ratio = 2048, 8, 2048, 64, 128, 4
+    iters = max(args.stage_iters, 200)
+    out = {}
+    for fmt, b in (("mxfp4", 4), ("fp8", 32)):
+        for t in (16384, 65536, 131072, 262144):
+            gen = torch.Generator(device=dev).manual_seed(t + b)
+            q = torch.randn(b, 1, hi, di, generator=gen, device=dev).bfloat16()
+            kk = torch.randn(b, t, di, generator=gen, device=dev).bfloat16()
+            w = torch.randn(b, 1, hi, generator=gen, device=dev) * hi ** -0.5
+            pos = torch.full((b, 1), t * ratio - 1, dtype=torch.int64, device=dev)
+            lens = torch.full((b, 1, 1), t, dtype=torch.int64, device=dev)
+            if fmt == "mxfp4":
+                qa, qb = quant.quant_mxfp4(q)
+                ka, kb = quant.quant_mxfp4(kk)
+                dense_fn, cand_fn = MI.scores_mxfp4, MI.candidate_scores_mxfp4
+            else:
+                qa, qs = quant.quant_fp8_block(q, 128)
+                ka, ks = quant.quant_fp8_block(kk, 128)
+                qb, kb = qs[..., 0].contiguous(), ks[..., 0].contiguous()
+                dense_fn, cand_fn = MI.scores_fp8, MI.candidate_scores_fp8
+            del kk
+            dense = torch.empty(b, 1, t, dtype=torch.float32, device=dev)
+            cs = torch.empty(b, 1, nblk * bs, dtype=torch.float32, device=dev)
+            idx = torch.empty(b, 1, k, dtype=torch.int32, device=dev)
+            cidx = torch.empty(b, 1, k, dtype=torch.int32, device=dev)
+            ws = torch.empty(max(MI.topk_workspace_bytes(b, t), MI.topk_workspace_bytes(b, nblk * bs), 16),
+                             dtype=torch.uint8, device=dev)
+            dense_fn(qa, qb, w, ka, kb, compress_ratio=ratio, positions=pos, out=dense)
+            cand = MI.candidate_block_list(dense, lens, nblk, bs)
+            fns = {
+                "dense_scores": lambda: dense_fn(qa, qb, w, ka, kb, compress_ratio=ratio, positions=pos, out=dense),
+                "dense_topk": lambda: MI.topk(dense, k, out=idx, workspace=ws),
+                "level1_select": lambda: MI.candidate_block_list(dense, lens, nblk, bs, out=cand),
+                "level2_scores": lambda: cand_fn(qa, qb, w, ka, kb, cand, block_size=bs, compress_ratio=ratio,
+                                                 positions=pos, out=cs),
+                "level2_topk": lambda: MI.candidate_topk(cs, cand, bs, k, out=cidx, workspace=ws),
+            }
+            row = {name: round(graph_time(torch, [fn], iters), 3) for name, fn in fns.items()}
+            kb_bytes = (di // 2 + di // 32) if fmt == "mxfp4" else di + 4
+            row["level2_score_GB/s"] = round(b * nblk * bs * (kb_bytes + 4) / row["level2_scores"] / 1e3, 1)
+            out[f"{fmt}_B{b}_T{t}"] = row
+            print(f"reindex {fmt} B={b} T={t}: {row}", file=sys.stderr, flush=True)
+            del qa, qb, ka, kb, dense, cs
+    return {"metric": "two-level selection cost vs cache length", "unit": "us per launch",
+            "config": {"workload": "decode rows at their last position; 2048 candidate blocks of 8, top-2048; "
+                                   "mxfp4 B=4 and fp8 B=32, 64 index heads x 128", "iters": iters},
+            "cases": out}
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -727,6 +789,9 @@ def main():
         return
     if args.kernels:
         print(json.dumps(run_kernels(torch, dev, args)))
+        return
+    if args.reindex:
+        print(json.dumps(run_reindex(torch, dev, args)))
         return
     out = run_prefill(torch, dev, args) if args.config == 3 else run_decode(torch, dev, args)
     print(json.dumps(out))

@@ -325,6 +325,34 @@ int mzk_candidate_blocks(const float* logits, int64_t rows, int64_t width, int64
                          int64_t mask_stride, int32_t* block_idx_out, void* workspace, int64_t workspace_bytes,
                          void* stream);
 
+/* Level two: score only the candidates -- replaces a candidate-using layer's dense scoring
+ * plus `index_scores.masked_fill(~shared["candidates"], -inf)` (owlet1/indexer.py:150-151;
+ * the gather form of tickets/0009-indexer-hierarchical.md:29-32; the score itself as
+ * mzk_indexer_scores_fp8 / _mxfp4, owlet1/indexer.py:129-143).  cand_blocks [B*S, cand_stride]
+ * int32 is the compact list of mzk_candidate_blocks (blocks ascending, then -1; n_blocks
+ * entries used).  scores [B*S, n_blocks*block_size] fp32 (row stride score_stride) on the
+ * candidate axis: slot j holds key cand_blocks[row][j / block_size] * block_size +
+ * j % block_size, with the same bits as the dense kernel's score of that key, or -inf if the
+ * block entry is -1, the key is >= G or not visible at the row's position.  Di = 128,
+ * B*S <= 65535. */
+int mzk_indexer_candidate_scores_fp8(const uint8_t* q_codes, const float* q_scales, const float* w,
+                                     const uint8_t* k_codes, const float* k_scales, int64_t B, int64_t S, int Hi,
+                                     int Di, int64_t G, int64_t k_batch_stride, const int64_t* positions, int ratio,
+                                     const int32_t* cand_blocks, int64_t cand_stride, int n_blocks, int block_size,
+                                     float* scores, int64_t score_stride, void* stream);
+int mzk_indexer_candidate_scores_mxfp4(const uint8_t* q_packed, const uint8_t* q_e8m0, const float* w,
+                                       const uint8_t* k_packed, const uint8_t* k_e8m0, int64_t B, int64_t S, int Hi,
+                                       int Di, int64_t G, int64_t k_batch_stride, const int64_t* positions, int ratio,
+                                       const int32_t* cand_blocks, int64_t cand_stride, int n_blocks, int block_size,
+                                       float* scores, int64_t score_stride, void* stream);
+/* The top-k over the candidate axis back to key positions, i.e. the top-k of the masked
+ * dense row (owlet1/indexer.py:158-161): slot_idx [rows, k] (row stride idx_stride, -1 =
+ * empty) -> pos_out [rows, k] (out_stride; may be slot_idx itself with equal strides).
+ * Ascending slots map to ascending positions; -1 and empty slots stay -1. */
+int mzk_candidate_positions(const int32_t* slot_idx, int64_t rows, int k, int64_t idx_stride,
+                            const int32_t* cand_blocks, int64_t cand_stride, int n_blocks, int block_size,
+                            int32_t* pos_out, int64_t out_stride, void* stream);
+
 /* ---------------------------------------------------------------------------------
  * Piece 5: sparse shared-latent MQA attention
  * --------------------------------------------------------------------------------- */

@@ -46,6 +46,11 @@ _SIGS = {
     "mzk_topk_rows_ws": [_P, _I64, _I64, _I64, _I32, _P, _I64, _P, _I64, _P],
     "mzk_candidate_blocks_workspace_bytes": [_I64, _I64, _I32, _I32, ctypes.POINTER(_I64)],
     "mzk_candidate_blocks": [_P, _I64, _I64, _I64, _P, _I32, _I32, _P, _I64, _P, _P, _I64, _P],
+    "mzk_indexer_candidate_scores_fp8": [_P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P, _I64,
+                                         _I32, _I32, _P, _I64, _P],
+    "mzk_indexer_candidate_scores_mxfp4": [_P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P,
+                                           _I64, _I32, _I32, _P, _I64, _P],
+    "mzk_candidate_positions": [_P, _I64, _I32, _I64, _P, _I64, _I32, _I32, _P, _I64, _P],
     "mzk_indexer_scores_fp8": [_P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P, _I64, _P],
     "mzk_indexer_decode_fp8": [_P, _P, _P, _P, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P, _I64, _P, _P, _P, _I32, _I32,
                                _P, _I64, _I32, _P],

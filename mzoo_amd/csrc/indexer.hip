@@ -149,6 +149,13 @@ struct IdxParams {
   float kv_eps;
   const uint16_t* kv_cos;
   const uint16_t* kv_sin;
+  // GATHER (level two of the two-level selection): the score axis is the row's candidate
+  // slots j < cand_nb * cand_bs; slot j is key cand[row][j / cand_bs] * cand_bs + j % cand_bs
+  // (a block index < 0 or a key >= G is empty: -inf)
+  const int32_t* cand;
+  int64_t cand_stride;
+  int cand_nb, cand_bs;
+  int64_t cand_keys;  // keys per batch row (the slots' key range)
 };
 
 constexpr int kFuseNope = 512, kFuseRope = 64, kFuseChunks = (kFuseNope + kFuseRope) / 64;
@@ -252,10 +259,19 @@ constexpr int q_pitch() { return FMT == kFp8 ? 128 + 16 : 64 + 16; }
 // FUSE: the query is rotated before it is quantized, and wave 0 of each row's workgroup 0
 // runs the kv prologue (FusedKv): loads before the keys', the work after the query's
 // quantization.
-template <int FMT, int DI, int MB, bool QRAW, bool APPEND, bool FUSE = false>
+// GATHER: the key of candidate slot j of `row` (-1: empty slot).  p.G is the slot count;
+// the key count is p.cand_keys.
+__device__ __forceinline__ int64_t cand_key(const IdxParams& p, int64_t row, int64_t j) {
+  const int32_t blk = p.cand[row * p.cand_stride + j / p.cand_bs];
+  const int64_t k = static_cast<int64_t>(blk) * p.cand_bs + j % p.cand_bs;
+  return (blk >= 0 && k < p.cand_keys) ? k : -1;
+}
+
+template <int FMT, int DI, int MB, bool QRAW, bool APPEND, bool FUSE = false, bool GATHER = false>
 __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxParams p) {
   static_assert(!QRAW || ((FMT == kFp8 || FMT == kMxfp4) && DI == 128), "in-kernel quantization: Di = 128");
   static_assert(!FUSE || (QRAW && !APPEND), "the fused prologue quantizes the raw query and appends on its own");
+  static_assert(!GATHER || !QRAW, "the candidate scorer takes the quantized query");
   constexpr int QP = q_pitch<FMT>();
   constexpr int NST = DI / Step<FMT>::K;
   constexpr int RB = row_bytes<FMT>(DI);
@@ -328,7 +344,13 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
   for (int t = 0; t < kNkb; ++t) {
     // keys at or beyond G read row G-1 instead: their score columns are never written
     const int64_t g = wave_key0 + t * 32 + (lane & 31);
-    const int64_t gc = g < G ? g : G - 1;
+    int64_t gc = g < G ? g : G - 1;
+    if constexpr (GATHER) {
+      // candidate slot gc -> its key (an empty slot reads key 0: its score is never written;
+      // slots at or beyond G were clamped to G-1 above, so the list read stays in the row)
+      const int64_t kg = cand_key(p, row, gc);
+      gc = kg >= 0 ? kg : 0;
+    }
     const uint8_t* krow = kb_base + gc * RB;
     const uint8_t* kerow = FMT == kMxfp4 ? ke_base + gc * (DI / 32) : nullptr;
 #pragma unroll
@@ -348,7 +370,8 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
   }
   const int64_t pos = p.positions ? p.positions[row] : row % p.S;
   int64_t vis = (pos + 1) / p.ratio;
-  if (vis > G) vis = G;
+  const int64_t nkeys = GATHER ? p.cand_keys : G;
+  if (vis > nkeys) vis = nkeys;
   if (vis < 0) vis = 0;
 
   __shared__ __align__(16) uint8_t q_lds[QRAW ? 64 * QP : 16];
@@ -484,7 +507,7 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
     const int64_t g0 = wave_key0 + t * 32;
     const int64_t g = g0 + (lane & 31);
     if (g0 >= G) break;
-    if (g0 >= vis) {  // nothing in this tile is visible to the row
+    if (!GATHER && g0 >= vis) {  // nothing in this tile is visible to the row
       if (lane < 32 && g < G) out[g] = -__builtin_huge_valf();
       continue;
     }
@@ -501,7 +524,9 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
     if (lane < 32 && g < G) {
       float s = total * inv_sqrt_di;
       if constexpr (FMT == kFp8) s = s * ksv[t];
-      out[g] = (g < vis) ? s : -__builtin_huge_valf();
+      int64_t kpos = g;
+      if constexpr (GATHER) kpos = cand_key(p, row, g);
+      out[g] = (kpos >= 0 && kpos < vis) ? s : -__builtin_huge_valf();
     }
   }
 
@@ -754,6 +779,37 @@ int launch_di(const IdxParams& p, int64_t rows, hipStream_t s) {
   return MZK_OK;
 }
 
+// The candidate scorer: p.G is the row's slot count (n_blocks * block_size).
+template <int FMT>
+int launch_gather(const IdxParams& p, int64_t rows, int Di, hipStream_t s) {
+  dim3 grid(static_cast<unsigned>((p.G + kKeysPerWg - 1) / kKeysPerWg), static_cast<unsigned>(rows));
+  if (Di != 128) {
+    set_last_error("indexer_candidate_scores: index head dim must be 128 (got %d)", Di);
+    return MZK_EUNSUPPORTED;
+  }
+  if (p.Hi <= 32) indexer_scores_kernel<FMT, 128, 1, false, false, false, true><<<grid, kWaves * 64, 0, s>>>(p);
+  else indexer_scores_kernel<FMT, 128, 2, false, false, false, true><<<grid, kWaves * 64, 0, s>>>(p);
+  return MZK_OK;
+}
+
+// Slot indices of the candidate axis -> key positions (in place allowed): one thread per
+// entry; -1 and empty slots stay -1.  Ascending slots give ascending positions, since the
+// candidate blocks are ascending.
+__global__ void candidate_positions_kernel(const int32_t* __restrict__ slot_idx, int64_t rows, int k,
+                                           int64_t idx_stride, const int32_t* __restrict__ cand, int64_t cand_stride,
+                                           int n_blocks, int block_size, int32_t* __restrict__ pos, int64_t pos_stride) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= rows * k) return;
+  const int64_t row = t / k, j = t - row * k;
+  const int32_t sl = slot_idx[row * idx_stride + j];
+  int32_t out = -1;
+  if (sl >= 0 && sl < n_blocks * block_size) {
+    const int32_t blk = cand[row * cand_stride + sl / block_size];
+    if (blk >= 0) out = blk * block_size + sl % block_size;
+  }
+  pos[row * pos_stride + j] = out;
+}
+
 template <int FMT>
 int launch(const IdxParams& p, int64_t rows, int Di, hipStream_t s) {
   switch (Di) {
@@ -800,6 +856,31 @@ int check_common(int64_t B, int64_t S, int Hi, int Di, int64_t G, int64_t kbs, i
   MZK_CHECK_ARG(B * S <= 0x7fffffff, "indexer_scores: too many query rows");
   (void)Di;
   return MZK_OK;
+}
+
+int check_candidates(int64_t B, int64_t S, int64_t G, const int32_t* cand, int64_t cand_stride, int n_blocks,
+                     int block_size, int64_t slots_stride) {
+  MZK_CHECK_ARG(n_blocks >= 0 && block_size >= 1 && cand_stride >= n_blocks,
+                "indexer_candidate_scores: bad candidate list shape");
+  MZK_CHECK_ARG(static_cast<int64_t>(n_blocks) * block_size <= (int64_t(1) << 30),
+                "indexer_candidate_scores: more than 2^30 candidate slots");
+  MZK_CHECK_ARG(static_cast<int64_t>(n_blocks) * block_size <= slots_stride,
+                "indexer_candidate_scores: score stride smaller than n_blocks * block_size");
+  MZK_CHECK_ARG(G < (int64_t(1) << 31), "indexer_candidate_scores: key count must fit int32");
+  MZK_CHECK_ARG(B * S <= 65535, "indexer_candidate_scores: at most 65535 query rows (got %lld)", (long long)(B * S));
+  MZK_CHECK_ARG(n_blocks == 0 || cand != nullptr, "indexer_candidate_scores: null candidate list");
+  return MZK_OK;
+}
+
+IdxParams with_candidates(IdxParams p, int64_t G, const int32_t* cand, int64_t cand_stride, int n_blocks,
+                          int block_size) {
+  p.G = static_cast<int64_t>(n_blocks) * block_size;
+  p.cand = cand;
+  p.cand_stride = cand_stride;
+  p.cand_nb = n_blocks;
+  p.cand_bs = block_size;
+  p.cand_keys = G;
+  return p;
 }
 
 }  // namespace
@@ -1031,5 +1112,86 @@ extern "C" int mzk_indexer_decode_fused(int q_format, const void* q_idx, const f
     else indexer_scores_kernel<kMxfp4, 128, 2, true, false, true><<<grid, kWaves * 64, 0, s>>>(p);
   }
   MZK_LAUNCH_CHECK("indexer_decode_fused");
+  return MZK_OK;
+}
+
+// ---- two-level selection, level two: the candidate scorer ------------------------------
+//
+// tickets/0009-indexer-hierarchical.md:29-32 (layers after the candidate source score only
+// the candidates; owlet1/indexer.py:150-151 applies it as
+// index_scores.masked_fill(~candidates, -inf) before the top-k).  Scores go to the candidate axis, slot j of a row holding key
+// cand_blocks[row][j / block_size] * block_size + j % block_size, so the cost follows the
+// candidate count, not the key count.  A slot's score has the same bits as the dense row
+// kernel's score of its key.
+
+namespace mzk {
+namespace {
+template <int FMT>
+int candidate_scores(const char* name, const IdxParams& base, int64_t B, int64_t S, int Hi, int Di, int64_t G,
+                     int64_t kbs, int ratio, const int32_t* cand, int64_t cand_stride, int n_blocks, int block_size,
+                     int64_t sstride, hipStream_t s) {
+  MZK_CHECK_ARG(B >= 0 && S >= 0 && G >= 0, "%s: negative size", name);
+  MZK_CHECK_ARG(Hi >= 1 && Hi <= 64, "%s: index heads must be in [1, 64] (got %d)", name, Hi);
+  MZK_CHECK_ARG(ratio >= 1, "%s: compress_ratio must be >= 1 (got %d)", name, ratio);
+  MZK_CHECK_ARG(kbs >= G, "%s: key batch stride smaller than G", name);
+  int rc = check_candidates(B, S, G, cand, cand_stride, n_blocks, block_size, sstride);
+  if (rc) return rc;
+  if (B * S == 0 || n_blocks == 0) return MZK_OK;
+  MZK_CHECK_ARG(G > 0, "%s: candidates over an empty key cache", name);
+  rc = launch_gather<FMT>(with_candidates(base, G, cand, cand_stride, n_blocks, block_size), B * S, Di, s);
+  if (rc) return rc;
+  MZK_LAUNCH_CHECK(name);
+  return MZK_OK;
+}
+}  // namespace
+}  // namespace mzk
+
+extern "C" int mzk_indexer_candidate_scores_fp8(const uint8_t* q_codes, const float* q_scales, const float* w,
+                                                const uint8_t* k_codes, const float* k_scales, int64_t B, int64_t S,
+                                                int Hi, int Di, int64_t G, int64_t k_batch_stride,
+                                                const int64_t* positions, int ratio, const int32_t* cand_blocks,
+                                                int64_t cand_stride, int n_blocks, int block_size, float* scores,
+                                                int64_t score_stride, void* stream) {
+  MZK_CHECK_ARG(B * S == 0 || n_blocks == 0 || (q_codes && q_scales && w && k_codes && k_scales && scores),
+                "indexer_candidate_scores_fp8: null pointer");
+  return candidate_scores<kFp8>("indexer_candidate_scores_fp8",
+                                make_params(q_codes, q_scales, nullptr, w, k_codes, k_scales, nullptr, S, Hi, G,
+                                            k_batch_stride, positions, ratio, scores, score_stride),
+                                B, S, Hi, Di, G, k_batch_stride, ratio, cand_blocks, cand_stride, n_blocks, block_size,
+                                score_stride, as_stream(stream));
+}
+
+extern "C" int mzk_indexer_candidate_scores_mxfp4(const uint8_t* q_packed, const uint8_t* q_e8m0, const float* w,
+                                                  const uint8_t* k_packed, const uint8_t* k_e8m0, int64_t B, int64_t S,
+                                                  int Hi, int Di, int64_t G, int64_t k_batch_stride,
+                                                  const int64_t* positions, int ratio, const int32_t* cand_blocks,
+                                                  int64_t cand_stride, int n_blocks, int block_size, float* scores,
+                                                  int64_t score_stride, void* stream) {
+  MZK_CHECK_ARG(B * S == 0 || n_blocks == 0 || (q_packed && q_e8m0 && w && k_packed && k_e8m0 && scores),
+                "indexer_candidate_scores_mxfp4: null pointer");
+  return candidate_scores<kMxfp4>("indexer_candidate_scores_mxfp4",
+                                  make_params(q_packed, nullptr, q_e8m0, w, k_packed, nullptr, k_e8m0, S, Hi, G,
+                                              k_batch_stride, positions, ratio, scores, score_stride),
+                                  B, S, Hi, Di, G, k_batch_stride, ratio, cand_blocks, cand_stride, n_blocks,
+                                  block_size, score_stride, as_stream(stream));
+}
+
+extern "C" int mzk_candidate_positions(const int32_t* slot_idx, int64_t rows, int k, int64_t idx_stride,
+                                       const int32_t* cand_blocks, int64_t cand_stride, int n_blocks, int block_size,
+                                       int32_t* pos_out, int64_t out_stride, void* stream) {
+  MZK_CHECK_ARG(rows >= 0 && k >= 0 && n_blocks >= 0 && block_size >= 1 && idx_stride >= k && out_stride >= k &&
+                    cand_stride >= n_blocks,
+                "candidate_positions: bad sizes");
+  MZK_CHECK_ARG(static_cast<int64_t>(n_blocks) * block_size <= (int64_t(1) << 30),
+                "candidate_positions: more than 2^30 candidate slots");
+  if (rows == 0 || k == 0) return MZK_OK;
+  MZK_CHECK_ARG(slot_idx && pos_out && (n_blocks == 0 || cand_blocks), "candidate_positions: null pointer");
+  MZK_CHECK_ARG(slot_idx == pos_out ? idx_stride == out_stride : true,
+                "candidate_positions: in place needs equal strides");
+  const int64_t n = rows * k;
+  MZK_CHECK_ARG((n + 255) / 256 <= 0x7fffffff, "candidate_positions: too many entries");
+  candidate_positions_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, as_stream(stream)>>>(
+      slot_idx, rows, k, idx_stride, cand_blocks, cand_stride, n_blocks, block_size, pos_out, out_stride);
+  MZK_LAUNCH_CHECK("candidate_positions");
   return MZK_OK;
 }

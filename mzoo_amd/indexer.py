@@ -13,6 +13,9 @@ Quantized paths used by the decode step (same math on packed operands):
 * ``scores_fp8``   -- FP8-e4m3 q/k with one pow2 fp32 scale per row (V3.2 layout)
 * ``scores_mxfp4`` -- MXFP4 q/k (e2m1 + e8m0 per 32), the model's own indexer quantizer
 * ``topk``         -- per-row top-k, lowest index wins ties, ascending output, ``-1`` pad
+* ``candidate_block_list`` / ``candidate_scores_*`` / ``candidate_topk`` -- the two-level
+  selection: level one's compact block list, level two's scores over the gathered
+  candidates only (cost flat in the cache length) and their top-k as key positions
 
 ``positions`` (int64 ``[B,S]``) gives absolute query positions for the group-causal
 rule; omitted, query ``s`` sits at position ``s`` (a prefill from position 0).
@@ -105,6 +108,130 @@ def select_candidate_blocks(logits: torch.Tensor, compress_lens: torch.Tensor, t
     _lib.call("mzk_candidate_blocks", flat.data_ptr(), rows, width, flat.stride(0), cl.data_ptr(), topk_blocks,
               block_size, mask.data_ptr(), width, None, ws.data_ptr(), ws.numel(), _lib.stream_of(logits))
     return mask
+
+
+def candidate_block_list(logits: torch.Tensor, compress_lens: torch.Tensor, topk_blocks: int, block_size: int,
+                         out: torch.Tensor | None = None) -> torch.Tensor:
+    """Level one in the compact form level two gathers from: the blocks
+    ``select_candidate_blocks`` keeps, as int32 [..., topk_blocks] block indices ascending,
+    then ``-1`` (tickets/0009-indexer-hierarchical.md:36-37 asks for an index list, not a
+    mask).  ``out`` (int32 [..., topk_blocks], contiguous) is filled when given."""
+    _lib.require_gpu(logits, compress_lens)
+    if logits.dtype != torch.float32:
+        raise TypeError(f"candidate_block_list: logits must be float32, got {logits.dtype}")
+    width = logits.shape[-1]
+    lead = logits.shape[:-1]
+    rows = 1
+    for d in lead:
+        rows *= d
+    if out is None:
+        out = torch.empty(*lead, topk_blocks, dtype=torch.int32, device=logits.device)
+    elif out.shape != (*lead, topk_blocks) or out.dtype != torch.int32 or not out.is_contiguous():
+        raise ValueError(f"candidate_block_list: out must be contiguous int32 {(*lead, topk_blocks)}")
+    if rows == 0 or topk_blocks == 0:
+        return out
+    if width == 0:
+        return out.fill_(-1)
+    cl = torch.as_tensor(compress_lens, device=logits.device).to(torch.int64).expand(*lead, 1).reshape(rows)
+    cl = cl.contiguous()
+    flat = logits.reshape(rows, width)
+    if flat.stride(-1) != 1:
+        flat = flat.contiguous()
+    n = ctypes.c_int64(0)
+    _lib.call("mzk_candidate_blocks_workspace_bytes", rows, width, block_size, topk_blocks, ctypes.byref(n))
+    ws = torch.empty(max(n.value, 16), dtype=torch.uint8, device=logits.device)
+    _lib.call("mzk_candidate_blocks", flat.data_ptr(), rows, width, flat.stride(0), cl.data_ptr(), topk_blocks,
+              block_size, None, 0, out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(logits))
+    return out
+
+
+def _check_cand(cand_blocks, b, s, block_size):
+    if cand_blocks.dtype != torch.int32 or cand_blocks.dim() != 3 or cand_blocks.shape[:2] != (b, s) \
+            or cand_blocks.stride(-1) != 1 or cand_blocks.stride(0) != s * cand_blocks.stride(1):
+        raise ValueError("candidate list must be int32 [B, S, n_blocks] with unit column stride")
+    if block_size < 1:
+        raise ValueError(f"block_size must be >= 1, got {block_size}")
+    return cand_blocks.shape[2]
+
+
+def candidate_scores_fp8(q_codes: torch.Tensor, q_scales: torch.Tensor, w: torch.Tensor, k_codes: torch.Tensor,
+                         k_scales: torch.Tensor, cand_blocks: torch.Tensor, *, block_size: int, compress_ratio: int,
+                         positions=None, groups: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Level two on FP8 operands (as ``scores_fp8``): only the candidates' scores, on the
+    candidate axis -- fp32 [B, S, n_blocks * block_size], slot j the key
+    ``cand_blocks[b, s, j // block_size] * block_size + j % block_size`` (``-inf`` for a
+    ``-1`` block, a key >= ``groups`` or one not yet visible).  The bits of a slot equal
+    ``scores_fp8``'s score of its key (decode-shape rows).  Cost follows the candidate
+    count, not the cache length (tickets/0009-indexer-hierarchical.md:29-32)."""
+    b, s, hi, di = q_codes.shape
+    gcap = k_codes.shape[1]
+    g = gcap if groups is None else groups
+    if k_codes.shape != (b, gcap, di) or k_scales.shape != (b, gcap) or q_scales.shape != (b, s, hi) \
+            or w.shape != (b, s, hi) or q_codes.dtype != torch.uint8 or k_codes.dtype != torch.uint8:
+        raise ValueError("candidate_scores_fp8: shape/dtype mismatch")
+    _lib.require_gpu(q_codes, k_codes, cand_blocks)
+    nb = _check_cand(cand_blocks, b, s, block_size)
+    out = _check_scores_out(b, s, nb * block_size, q_codes.device, out)
+    pos = _positions(positions, b, s, q_codes.device)
+    qc, qs, wc, kc, ks = (q_codes.contiguous(), q_scales.float().contiguous(), w.float().contiguous(),
+                          k_codes.contiguous(), k_scales.float().contiguous())
+    _lib.call("mzk_indexer_candidate_scores_fp8", qc.data_ptr(), qs.data_ptr(), wc.data_ptr(), kc.data_ptr(),
+              ks.data_ptr(), b, s, hi, di, g, gcap, _lib.ptr(pos), compress_ratio, cand_blocks.data_ptr(),
+              cand_blocks.stride(1), nb, block_size, out.data_ptr(), out.stride(1), _lib.stream_of(q_codes))
+    return out
+
+
+def candidate_scores_mxfp4(q_packed: torch.Tensor, q_e8m0: torch.Tensor, w: torch.Tensor, k_packed: torch.Tensor,
+                           k_e8m0: torch.Tensor, cand_blocks: torch.Tensor, *, block_size: int, compress_ratio: int,
+                           positions=None, groups: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``candidate_scores_fp8`` on MXFP4 operands (as ``scores_mxfp4``)."""
+    b, s, hi, half = q_packed.shape
+    di = half * 2
+    gcap = k_packed.shape[1]
+    g = gcap if groups is None else groups
+    if k_packed.shape != (b, gcap, half) or k_e8m0.shape != (b, gcap, di // 32) \
+            or q_e8m0.shape != (b, s, hi, di // 32) or w.shape != (b, s, hi):
+        raise ValueError("candidate_scores_mxfp4: shape mismatch")
+    _lib.require_gpu(q_packed, k_packed, cand_blocks)
+    nb = _check_cand(cand_blocks, b, s, block_size)
+    out = _check_scores_out(b, s, nb * block_size, q_packed.device, out)
+    pos = _positions(positions, b, s, q_packed.device)
+    qp, qe, wc, kp, ke = (q_packed.contiguous(), q_e8m0.contiguous(), w.float().contiguous(), k_packed.contiguous(),
+                          k_e8m0.contiguous())
+    _lib.call("mzk_indexer_candidate_scores_mxfp4", qp.data_ptr(), qe.data_ptr(), wc.data_ptr(), kp.data_ptr(),
+              ke.data_ptr(), b, s, hi, di, g, gcap, _lib.ptr(pos), compress_ratio, cand_blocks.data_ptr(),
+              cand_blocks.stride(1), nb, block_size, out.data_ptr(), out.stride(1), _lib.stream_of(q_packed))
+    return out
+
+
+def candidate_positions(slot_idx: torch.Tensor, cand_blocks: torch.Tensor, block_size: int,
+                        out: torch.Tensor | None = None) -> torch.Tensor:
+    """Top-k picks on the candidate axis (int32 [..., k], ``-1`` = empty) -> key positions
+    (same shape; ``out`` may be ``slot_idx`` itself).  Ascending slots give ascending keys."""
+    _lib.require_gpu(slot_idx, cand_blocks)
+    k = slot_idx.shape[-1]
+    nb = cand_blocks.shape[-1]
+    if slot_idx.dtype != torch.int32 or not slot_idx.is_contiguous() or cand_blocks.dtype != torch.int32 \
+            or cand_blocks.shape[:-1] != slot_idx.shape[:-1] or not cand_blocks.is_contiguous():
+        raise ValueError("candidate_positions: slot_idx / cand_blocks must be contiguous int32 [..., k] / [..., nb]")
+    if out is None:
+        out = torch.empty_like(slot_idx)
+    elif out.shape != slot_idx.shape or out.dtype != torch.int32 or not out.is_contiguous():
+        raise ValueError("candidate_positions: out must be contiguous int32 like slot_idx")
+    rows = slot_idx.numel() // k if k else 0
+    _lib.call("mzk_candidate_positions", slot_idx.data_ptr(), rows, k, k, cand_blocks.data_ptr(), nb, nb, block_size,
+              out.data_ptr(), k, _lib.stream_of(slot_idx))
+    return out
+
+
+def candidate_topk(scores: torch.Tensor, cand_blocks: torch.Tensor, block_size: int, k: int,
+                   out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Top-k of candidate-axis scores as key positions: the same list ``topk`` gives on the
+    dense row masked to the candidates (owlet1/indexer.py:150-151 then :158-161), since
+    slot order follows key order -- ascending, lower key first among equal scores, ``-1``
+    pad."""
+    idx = topk(scores, k, out=out, workspace=workspace)
+    return candidate_positions(idx, cand_blocks, block_size, out=idx)
 
 
 def _check_scores_out(b, s, g, device, out):

@@ -35,3 +35,21 @@ def test_version_and_error_text():
 def test_missing_library_raises(tmp_path):
     with pytest.raises(ImportError, match="not built"):
         _lib.load(tmp_path / "nope.so")
+
+
+def test_candidate_entry_points_reject_bad_shapes():
+    """The level-two entry points fail in their argument checks, before any HIP call."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    args = [p] * 5 + [70000, 1, 64, 128, 4096, 4096, None, 4, p, 2048, 2048, 8, p, 16384, None]
+    assert lib.mzk_indexer_candidate_scores_fp8(*args) == -1
+    assert b"65535" in lib.mzk_last_error()
+    args = [p] * 5 + [4, 1, 64, 128, 4096, 4096, None, 4, p, 2048, 2048, 8, p, 8192, None]
+    assert lib.mzk_indexer_candidate_scores_mxfp4(*args) == -1
+    assert b"score stride" in lib.mzk_last_error()
+    args = [p] * 5 + [4, 1, 64, 128, 4096, 4096, None, 4, p, 100, 2048, 8, p, 16384, None]
+    assert lib.mzk_indexer_candidate_scores_fp8(*args) == -1
+    assert b"candidate list shape" in lib.mzk_last_error()
+    # in place with different strides
+    assert lib.mzk_candidate_positions(p, 2, 16, 32, p, 8, 8, 8, p, 16, None) == -1
+    assert b"in place" in lib.mzk_last_error()
