@@ -281,7 +281,7 @@ int mzk_indexer_scores_bf16(const void* q, const float* w, const void* k, int64_
 int mzk_topk_rows(const float* scores, int64_t rows, int64_t cols, int64_t row_stride, int topk,
                   int32_t* out, int64_t out_stride, void* stream);
 
-/* mzk_topk_rows with a caller-owned workspace, for long rows: rows of 8193 .. 524288
+/* mzk_topk_rows with a caller-owned workspace, for long rows: rows of 32769 .. 524288
  * columns are split over 8192-column chunk workgroups (histogram -> per-row selection ->
  * index-ordered write, three launches), so a few long rows still fill the GPU; other sizes
  * run mzk_topk_rows.  Same contract and results.  `workspace` (16-byte aligned) holds

@@ -259,14 +259,6 @@ constexpr int q_pitch() { return FMT == kFp8 ? 128 + 16 : 64 + 16; }
 // FUSE: the query is rotated before it is quantized, and wave 0 of each row's workgroup 0
 // runs the kv prologue (FusedKv): loads before the keys', the work after the query's
 // quantization.
-// GATHER: the key of candidate slot j of `row` (-1: empty slot).  p.G is the slot count;
-// the key count is p.cand_keys.
-__device__ __forceinline__ int64_t cand_key(const IdxParams& p, int64_t row, int64_t j) {
-  const int32_t blk = p.cand[row * p.cand_stride + j / p.cand_bs];
-  const int64_t k = static_cast<int64_t>(blk) * p.cand_bs + j % p.cand_bs;
-  return (blk >= 0 && k < p.cand_keys) ? k : -1;
-}
-
 template <int FMT, int DI, int MB, bool QRAW, bool APPEND, bool FUSE = false, bool GATHER = false>
 __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxParams p) {
   static_assert(!QRAW || ((FMT == kFp8 || FMT == kMxfp4) && DI == 128), "in-kernel quantization: Di = 128");
@@ -340,16 +332,26 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
   }
   Frag bf[kNkb][NST];
   float ksv[kNkb];  // FP8: the per-key scales
+  int32_t cblk[kNkb];  // GATHER: the candidate block of each tile's slot, all loaded first
+  if constexpr (GATHER) {
+    // (loads complete in order: list entries issued between key loads would make each
+    // tile's key loads wait for the previous tile's keys)
+#pragma unroll
+    for (int t = 0; t < kNkb; ++t) {
+      const int64_t g = wave_key0 + t * 32 + (lane & 31);
+      const int64_t gc = g < G ? g : G - 1;  // slots at or beyond G: the row's last slot
+      cblk[t] = p.cand[row * p.cand_stride + gc / p.cand_bs];
+    }
+  }
 #pragma unroll
   for (int t = 0; t < kNkb; ++t) {
     // keys at or beyond G read row G-1 instead: their score columns are never written
     const int64_t g = wave_key0 + t * 32 + (lane & 31);
     int64_t gc = g < G ? g : G - 1;
     if constexpr (GATHER) {
-      // candidate slot gc -> its key (an empty slot reads key 0: its score is never written;
-      // slots at or beyond G were clamped to G-1 above, so the list read stays in the row)
-      const int64_t kg = cand_key(p, row, gc);
-      gc = kg >= 0 ? kg : 0;
+      // candidate slot gc -> its key (an empty slot reads key 0: its score is never written)
+      const int64_t kg = static_cast<int64_t>(cblk[t]) * p.cand_bs + gc % p.cand_bs;
+      gc = (cblk[t] >= 0 && kg < p.cand_keys) ? kg : 0;
     }
     const uint8_t* krow = kb_base + gc * RB;
     const uint8_t* kerow = FMT == kMxfp4 ? ke_base + gc * (DI / 32) : nullptr;
@@ -525,7 +527,10 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
       float s = total * inv_sqrt_di;
       if constexpr (FMT == kFp8) s = s * ksv[t];
       int64_t kpos = g;
-      if constexpr (GATHER) kpos = cand_key(p, row, g);
+      if constexpr (GATHER) {  // g < G here, so cblk[t] is slot g's block
+        kpos = static_cast<int64_t>(cblk[t]) * p.cand_bs + g % p.cand_bs;
+        if (cblk[t] < 0) kpos = -1;
+      }
       out[g] = (kpos >= 0 && kpos < vis) ? s : -__builtin_huge_valf();
     }
   }

@@ -7,18 +7,19 @@
 //   * among equal scores the LOWER index wins (the reference leaves ties unspecified);
 //   * the selected indices are written in ascending index order, then -1 up to k.
 //
-// Algorithm (one 1024-thread workgroup per row):
+// Algorithm:
 //   key(x) = order-preserving uint32 of the fp32 score; -inf -> 0x007fffff.
-//   1. count finite entries; if <= k, threshold T = key(-inf) and every finite entry is taken.
-//   2. otherwise 4 MSB-first 8-bit digit passes: LDS histogram of the entries matching the
-//      digits fixed so far, a suffix scan picks the digit holding the k-th largest key.
-//      After the last pass T is the k-th largest key and `need_eq` entries equal to T
-//      are still to be taken.
+//   1. first-level histogram of the finite keys over their top 11 bits; a block scan finds
+//      the bin b1 of the k-th largest key (or: at most k finite keys, take them all);
+//   2. the keys of b1 are resolved by re-binning the window of keys still open over its
+//      own min .. max (at most two passes for 21 bits) -- T, the k-th largest key, and
+//      `need_eq`, the entries equal to T still to be taken;
 //   3. compaction in index order: take key > T, and the first `need_eq` entries with
-//      key == T; two block-wide exclusive scans per 4096-entry chunk give the ranks.
-// Rows up to 32 * 1024 keys keep them in registers (topk_rows_reg_kernel); longer rows
-// re-read the row every pass (L2-resident after the first pass).  mzk_topk_rows_ws splits
-// rows of 8193 .. 64 x 8192 keys over chunk workgroups (three launches, see below).
+//      key == T.
+// Rows up to 32 * 1024 keys keep them in registers (topk_row_kernel, one workgroup per
+// row); longer rows without a workspace stream the row through 8-bit digit passes
+// (topk_rows_kernel).  mzk_topk_rows_ws splits rows of 32769 .. 64 x 8192 keys over chunk
+// workgroups (two launches, see below).
 #include "common.h"
 
 namespace mzk {
@@ -210,86 +211,94 @@ __device__ __forceinline__ int wave_incl_scan_dpp(int v) {
   return v;
 }
 
-// Every bin of the radix histogram has kSub counters, lane l adding to counter l % kSub:
-// lanes whose keys share a digit (the leading digits of similar scores) then collide on
-// at most 64 / kSub addresses per LDS atomic instead of all 64.
-constexpr int kSub = 16;
-constexpr int kHist = 256 * kSub;
+// ---- rows of G <= KPT * NT, one workgroup per row, keys held in registers -------------
+//
+// Three levels of bins, each a histogram in LDS over the keys still open: the top 11 bits of
+// the key (sign, exponent and two mantissa bits of the score: four bins per octave; finite
+// keys lie in bins >= 4, -inf is key 0x007fffff in bin 3, the padding key 0 in bin 0), then
+// bits 20..10 and bits 9..0 of the keys in the bin holding the k-th largest.  A level stops
+// the search when that bin is taken whole (its keys are all among the k largest), which for
+// distinct scores happens after the first or the second.  The three histograms are cleared
+// up front, so a level costs one barrier for its histogram and two for its bin search:
+// workgroup barriers, not arithmetic, are what a level costs here.  Compaction: the output
+// slot of an entry is (#key > T before it) + min(#key == T before it, need_eq), from one
+// scan of the packed pair (n_gt << 16 | n_eq).
+constexpr int kBinBits = 11;
+constexpr int kBins = 1 << kBinBits;           // 2048 first-level bins
+constexpr int kLowBits = 32 - kBinBits;        // 21 bits below a first-level bin
+constexpr int kSub1 = 4;                       // first-level sub-counters per bin (lane % 4)
 
-// Digit selection in two steps.  (1) Every wave folds the sub-counters of its 256 / NW
-// bins into bin totals: consecutive lanes read consecutive 16 B (conflict-free), each
-// int4 being the four counters 4(l%4).. of one bin, and a quad reduction completes the
-// bin.  (2) After a barrier, one wave owns bins 255-4l .. 252-4l in lane l (descending),
-// so an inclusive prefix over lanes counts the entries in higher bins; it finds the bin
-// holding the rem-th largest key and returns its digit, the rank left inside it, and
-// whether the whole bin is taken (rank == count).
-struct DigitSel {
-  int digit, rem, whole;
-};
-template <int NW>
-__device__ __forceinline__ void reduce_bins(const int* hist, int* tot, int wave, int lane) {
-  static_assert(kSub == 16, "one int4 per lane covers a quarter of a bin");
-  constexpr int R = 1024 / NW / 64;  // int4 reads per lane (each wave folds 1024/NW int4)
-  const int4* h4 = reinterpret_cast<const int4*>(hist) + wave * (1024 / NW);
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int4 v = h4[r * 64 + lane];  // bin (wave * 1024/NW + 64 r + lane) / 4
-    int c = (v.x + v.y) + (v.z + v.w);
-    c += __builtin_amdgcn_update_dpp(0, c, 0xb1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
-    c += __builtin_amdgcn_update_dpp(0, c, 0x4e, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
-    if ((lane & 3) == 0) tot[(wave * (1024 / NW) + r * 64 + lane) >> 2] = c;
-  }
-}
-__device__ __forceinline__ DigitSel select_digit(const int* tot, int rem, int lane) {
-  const int4 t4 = reinterpret_cast<const int4*>(tot)[63 - lane];  // bins 252-4l .. 255-4l
-  const int h[4] = {t4.w, t4.z, t4.y, t4.x};                      // h[j] = bin 255-4l-j
-  const int s = (h[0] + h[1]) + (h[2] + h[3]);
-  int above = wave_incl_scan_dpp(s) - s;
-  DigitSel res{0, 0, 0};
-  bool hit = false;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    if (above < rem && rem <= above + h[j]) {
-      res.digit = 255 - 4 * lane - j;
-      res.rem = rem - above;
-      res.whole = (rem - above) == h[j];
-      hit = true;
-    }
-    above += h[j];
-  }
-  // exactly one lane hits (the counts above the k-th key are < rem <= counts down to it)
-  const uint64_t m = __ballot(hit);
-  const int src_lane = m ? __builtin_ctzll(m) : 0;
-  res.digit = __builtin_amdgcn_readlane(res.digit, src_lane);
-  res.rem = __builtin_amdgcn_readlane(res.rem, src_lane);
-  res.whole = __builtin_amdgcn_readlane(res.whole, src_lane);
-  return res;
-}
-
-// Thread t holds keys t*KPT .. t*KPT+KPT-1.  The first digit's histogram is built while
-// the finite entries are counted, and a pass stops the search early when the bin of the
-// k-th largest key is taken whole (threshold: every key >= the bin's lowest key), which
-// for distinct scores usually happens after two or three of the four 8-bit digits.
-// Compaction: the output slot of an entry is (#key > T before it) +
-// min(#key == T before it, need_eq), so one exclusive scan of the packed pair
-// (n_gt << 16 | n_eq) gives every position.
-template <int KPT, int NT>
-__global__ void __launch_bounds__(NT) topk_rows_reg_kernel(const float* __restrict__ scores, int64_t row_stride,
-                                                                 int G, int k, int32_t* __restrict__ out,
-                                                                 int64_t out_stride) {
-  __shared__ __align__(16) int hist[2][kHist];
+// Inclusive scan over the NT threads of one int each (one barrier); `total` is the sum.
+// wsum [NT/64] may be written again after the caller's next barrier.
+template <int NT>
+__device__ __forceinline__ int block_incl_scan(int v, int* wsum, int& total) {
   constexpr int NW = NT / 64;
-  static_assert(NW % 4 == 0, "wave sums are read as int4");
-  __shared__ __align__(16) int wsum[NW];
-  __shared__ int sel[2][3];  // digit, rem, whole of the pass using hist[p & 1]
-  __shared__ __align__(16) int bin_tot[256];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int incl = wave_incl_scan_dpp(v);
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  int before = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const int x = wsum[w];
+    before += w < wave ? x : 0;
+    tot += x;
+  }
+  total = tot;
+  return incl + before;
+}
+
+// The bin holding the rem-th largest entry of an NB-bin histogram: thread t holds the counts
+// c[j] of bins NB-1-(BPT*t+j) (descending), so the block scan counts the entries above each
+// thread's bins.  Every thread returns the same (bin = rem = count = 0 when rem exceeds the
+// total).  Two barriers; sh [3] may be written again after the caller's next barrier.
+struct BinHit {
+  int bin, rem, count, total;  // the bin, the rank left inside it, its count, the histogram total
+};
+template <int NT, int NB>
+__device__ __forceinline__ BinHit find_bin(const int (&c)[NB / NT], int rem, int* wsum, int* sh) {
+  constexpr int BPT = NB / NT;
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    sh[0] = 0;
+    sh[1] = 0;
+    sh[2] = 0;
+  }
+  int s = 0;
+#pragma unroll
+  for (int j = 0; j < BPT; ++j) s += c[j];
+  int total;
+  const int incl = block_incl_scan<NT>(s, wsum, total);
+  int above = incl - s;
+#pragma unroll
+  for (int j = 0; j < BPT; ++j) {
+    if (above < rem && rem <= above + c[j]) {  // exactly one (thread, j) when rem <= total
+      sh[0] = NB - 1 - (BPT * tid + j);
+      sh[1] = rem - above;
+      sh[2] = c[j];
+    }
+    above += c[j];
+  }
+  __syncthreads();
+  return BinHit{sh[0], sh[1], sh[2], total};
+}
+
+template <int KPT, int NT>
+__global__ void __launch_bounds__(NT) topk_row_kernel(const float* __restrict__ scores, int64_t row_stride, int G,
+                                                      int k, int32_t* __restrict__ out, int64_t out_stride) {
+  constexpr int NW = NT / 64;
+  static_assert(KPT * NT <= 32768, "packed counts: at most 2^15 keys per row");
+  __shared__ __align__(16) int hist1[kBins * kSub1];
+  __shared__ __align__(16) int hist2[kBins];       // bits 20..10 of the keys in the first level's bin
+  __shared__ __align__(16) int hist3[kBins / 2];   // bits 9..0 of the keys in the second level's bin
+  __shared__ int wsum[NW];
+  __shared__ int sh[2][3];  // bin searches alternate between the two
 
   const int64_t row = blockIdx.x;
   const float* src = scores + row * row_stride;
   int32_t* dst = out + row * out_stride;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
   const int i0 = tid * KPT;
 
   float x[KPT];
@@ -307,78 +316,60 @@ __global__ void __launch_bounds__(NT) topk_rows_reg_kernel(const float* __restri
     for (int j = 0; j < KPT; ++j) x[j] = (i0 + j < G) ? src[i0 + j] : 0.0f;
   }
   {
-    int4* h4 = reinterpret_cast<int4*>(&hist[0][0]);
-    for (int i = tid; i < 2 * kHist / 4; i += NT) h4[i] = int4{0, 0, 0, 0};
+    int4* h4 = reinterpret_cast<int4*>(hist1);
+    for (int i = tid; i < kBins * kSub1 / 4; i += NT) h4[i] = int4{0, 0, 0, 0};
+    for (int i = tid; i < kBins / 4; i += NT) reinterpret_cast<int4*>(hist2)[i] = int4{0, 0, 0, 0};
+    for (int i = tid; i < kBins / 8; i += NT) reinterpret_cast<int4*>(hist3)[i] = int4{0, 0, 0, 0};
   }
   __syncthreads();  // histograms cleared (while the scores are in flight)
 
   uint32_t key[KPT];
-  int nfin = 0;  // wave-uniform
-  int* h0 = &hist[0][lane % kSub];
+  int* hl = hist1 + (lane & (kSub1 - 1));
 #pragma unroll
   for (int j = 0; j < KPT; ++j) {
     key[j] = (i0 + j < G) ? order_key(x[j]) : 0u;  // 0 sorts below -inf: never taken
-    nfin += __popcll(__ballot(key[j] > kNegInfKey));
-    atomicAdd(h0 + (key[j] >> 24) * kSub, 1);
+    if (key[j] > kNegInfKey) atomicAdd(hl + (key[j] >> kLowBits) * kSub1, 1);
   }
-  if (lane == 0) wsum[wave] = nfin;
-  __syncthreads();  // first histogram and the finite counts complete
-  int total_fin = 0;
-  {
-    const int4* w4 = reinterpret_cast<const int4*>(wsum);
+  __syncthreads();
+  int c1[kBins / NT];
 #pragma unroll
-    for (int q = 0; q < NW / 4; ++q) {
-      const int4 v = w4[q];
-      total_fin += (v.x + v.y) + (v.z + v.w);
-    }
+  for (int j = 0; j < kBins / NT; ++j) {
+    const int4 v = reinterpret_cast<const int4*>(hist1)[kBins - 1 - ((kBins / NT) * tid + j)];
+    c1[j] = (v.x + v.y) + (v.z + v.w);
   }
+  const BinHit h1 = find_bin<NT, kBins>(c1, k, wsum, sh[0]);
 
-  uint32_t T = kNegInfKey;
+  uint32_t T = kNegInfKey;  // at most k finite keys: take them all
   int need_eq = 0;
-  if (total_fin > k) {
-    uint32_t prefix = 0, mask = 0;
-    int rem = k;
-#pragma unroll 1
-    for (int pass = 0; pass < 4; ++pass) {
-      const int shift = 24 - 8 * pass;
-      const int cur = pass & 1;
-      reduce_bins<NW>(hist[cur], bin_tot, wave, lane);
-      if (pass > 0) {
-        // the next pass's copy (its last reader, the reduction two passes ago, is done);
-        // hist[1] is still clear for the second pass
-        int4* h4 = reinterpret_cast<int4*>(&hist[cur ^ 1][0]);
-        for (int i = tid; i < kHist / 4; i += NT) h4[i] = int4{0, 0, 0, 0};
-      }
-      __syncthreads();  // bin totals complete
-      if (wave == 0) {
-        const DigitSel r = select_digit(bin_tot, rem, lane);
-        if (lane == 0) {
-          sel[cur][0] = r.digit;
-          sel[cur][1] = r.rem;
-          sel[cur][2] = r.whole;
-        }
-      }
-      __syncthreads();  // selection published, next copy cleared
-      const uint32_t digit = static_cast<uint32_t>(sel[cur][0]);
-      rem = sel[cur][1];
-      const uint32_t low = prefix | (digit << shift);
-      if (sel[cur][2] && low != 0u) {  // bin taken whole: every key >= low
-        T = low - 1u;
-        need_eq = 0;
-        break;
-      }
-      prefix = low;
-      mask |= 255u << shift;
-      if (shift == 0) {
-        T = prefix;
-        need_eq = rem;
-        break;
-      }
-      int* hn = &hist[cur ^ 1][lane % kSub];
+  if (h1.total > k) {
+    const uint32_t b1 = static_cast<uint32_t>(h1.bin);  // >= 4
+    if (h1.count == h1.rem) {
+      T = (b1 << kLowBits) - 1u;
+    } else {
 #pragma unroll
       for (int j = 0; j < KPT; ++j)
-        if ((key[j] & mask) == prefix) atomicAdd(hn + ((key[j] >> (shift - 8)) & 255u) * kSub, 1);
-      __syncthreads();  // next histogram complete
+        if ((key[j] >> kLowBits) == b1) atomicAdd(&hist2[(key[j] >> 10) & (kBins - 1)], 1);
+      __syncthreads();
+      int c2[kBins / NT];
+#pragma unroll
+      for (int j = 0; j < kBins / NT; ++j) c2[j] = hist2[kBins - 1 - ((kBins / NT) * tid + j)];
+      const BinHit h2 = find_bin<NT, kBins>(c2, h1.rem, wsum, sh[1]);
+      const uint32_t p2 = (b1 << kLowBits) | (static_cast<uint32_t>(h2.bin) << 10);
+      if (h2.count == h2.rem) {
+        T = p2 - 1u;
+      } else {
+#pragma unroll
+        for (int j = 0; j < KPT; ++j)
+          if ((key[j] >> 10) == (p2 >> 10)) atomicAdd(&hist3[key[j] & 1023u], 1);
+        __syncthreads();
+        constexpr int B3 = kBins / 2;
+        int c3[B3 / NT];
+#pragma unroll
+        for (int j = 0; j < B3 / NT; ++j) c3[j] = hist3[B3 - 1 - ((B3 / NT) * tid + j)];
+        const BinHit h3 = find_bin<NT, B3>(c3, h2.rem, wsum, sh[0]);
+        T = p2 | static_cast<uint32_t>(h3.bin);  // the k-th largest key itself
+        need_eq = h3.rem;
+      }
     }
   }
 
@@ -391,24 +382,9 @@ __global__ void __launch_bounds__(NT) topk_rows_reg_kernel(const float* __restri
   }
   // packed as unsigned: n_gt <= G <= 32768 fills bit 31 at most, n_eq stays below 2^16
   const int packed = (n_gt << 16) | n_eq;
-  const int incl = wave_incl_scan_dpp(packed);
-  __syncthreads();  // every wave is done reading wsum (finite counts)
-  if (lane == 63) wsum[wave] = incl;
-  __syncthreads();
-  uint32_t before = static_cast<uint32_t>(incl - packed), tot = 0;
-  {
-    const int4* w4 = reinterpret_cast<const int4*>(wsum);
-#pragma unroll
-    for (int q = 0; q < NW / 4; ++q) {
-      const int4 v = w4[q];
-      const int w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if (4 * q + e < wave) before += static_cast<uint32_t>(w[e]);
-        tot += static_cast<uint32_t>(w[e]);
-      }
-    }
-  }
+  int tot_p;
+  const int incl = block_incl_scan<NT>(packed, wsum, tot_p);
+  const uint32_t before = static_cast<uint32_t>(incl - packed), tot = static_cast<uint32_t>(tot_p);
   int gt_before = static_cast<int>(before >> 16), eq_before = static_cast<int>(before & 0xffffu);
   const int written = static_cast<int>(tot >> 16) + min(static_cast<int>(tot & 0xffffu), need_eq);
 #pragma unroll
@@ -423,7 +399,6 @@ __global__ void __launch_bounds__(NT) topk_rows_reg_kernel(const float* __restri
   }
   for (int i = written + tid; i < k; i += NT) dst[i] = -1;
 }
-
 
 // ---- long rows, few of them: the row split over chunk workgroups ---------------------
 //
@@ -442,12 +417,12 @@ __global__ void __launch_bounds__(NT) topk_rows_reg_kernel(const float* __restri
 //      more than kCandCap keys the selection streams the row instead (slow, but exact).
 // Same contract and results as the single-workgroup kernels.
 constexpr int kChunk = 8 * kThreads;           // keys per chunk workgroup
-constexpr int kBinBits = 11;
-constexpr int kBins = 1 << kBinBits;           // 2048 first-level bins
-constexpr int kLowBits = 32 - kBinBits;        // 21 bits resolved in C
 constexpr int kCandCap = 12288;                // keys of bin b1 held in LDS
 constexpr int kMaxChunks = 64;                 // rows up to 64 x 8192 keys
-constexpr int64_t kMultiMinG = 8 * kThreads;   // shorter rows stay on one workgroup
+// shorter rows stay on one workgroup: up to 16384 keys it is twice as fast as the three
+// chunk launches, at 32768 even (measured on MI355X in HIP graphs: 8.6 vs 16.2 us at
+// 4 x 16384, 16.1 vs 16.8 us at 8 x 32768)
+constexpr int64_t kMultiMinG = 32 * kThreads;
 
 // Workspace: hist [rows][nch][kBins] int32 | above [rows][nch] int32 | sel [rows] int4
 // (mode, b1, rem, finite total) | cand [rows][nch][kChunk] (key, index): chunk c of a row
@@ -969,15 +944,15 @@ extern "C" int mzk_topk_rows(const float* scores, int64_t rows, int64_t cols, in
   const unsigned nr = static_cast<unsigned>(rows);
   // short rows take a workgroup sized to them (8 keys per thread), long ones 1024 threads
   if (G <= 8 * 256)
-    topk_rows_reg_kernel<8, 256><<<nr, 256, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
+    topk_row_kernel<8, 256><<<nr, 256, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
   else if (G <= 8 * 512)
-    topk_rows_reg_kernel<8, 512><<<nr, 512, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
+    topk_row_kernel<8, 512><<<nr, 512, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
   else if (G <= 8 * kThreads)
-    topk_rows_reg_kernel<8, kThreads><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
+    topk_row_kernel<8, kThreads><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
   else if (G <= 16 * kThreads)
-    topk_rows_reg_kernel<16, kThreads><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
+    topk_row_kernel<16, kThreads><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
   else if (G <= 32 * kThreads)
-    topk_rows_reg_kernel<32, kThreads><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
+    topk_row_kernel<32, kThreads><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride);
   else if (G <= kLdsKeys)
     topk_rows_kernel<true><<<nr, kThreads, static_cast<size_t>(G) * 4, s>>>(scores, row_stride, G, topk, out,
                                                                            out_stride);

@@ -46,7 +46,7 @@ def test_topk_kat_dummy_slot(dev):
 
 
 @pytest.mark.parametrize("rows,g,k", [(32, 8192, 2048), (8, 32768, 2048), (4, 131072, 2048), (7, 1000, 128),
-                                      (3, 100, 135), (5, 4097, 4096), (2, 0, 16), (64, 256, 1)])
+                                      (3, 100, 135), (5, 4097, 4096), (2, 0, 16), (64, 256, 1), (3, 8000, 5000)])
 def test_topk_exact_with_ties(dev, rows, g, k):
     gen = torch.Generator().manual_seed(rows * 7 + g)
     sc = torch.randn(rows, g, generator=gen)
@@ -64,12 +64,14 @@ def test_topk_exact_with_ties(dev, rows, g, k):
 
 @pytest.mark.parametrize("rows,g,k,kind", [(4, 131072, 2048, "distinct"), (3, 40003, 2048, "distinct"),
                                            (2, 524288, 2048, "distinct"), (5, 16384, 16384, "ties"),
-                                           (6, 9000, 100, "ties"), (4, 65536, 4096, "three_values"),
-                                           (3, 20000, 2048, "negative")])
+                                           (2, 40000, 40000, "ties"), (6, 9000, 100, "ties"),
+                                           (6, 33000, 100, "ties"), (4, 65536, 4096, "three_values"),
+                                           (3, 20000, 2048, "negative"), (3, 36000, 2048, "negative"),
+                                           (2, 30000, 2048, "three_values")])
 def test_topk_long_rows_split_over_workgroups(dev, rows, g, k, kind):
-    """Rows of 8193 .. 524288 scores go through mzk_topk_rows_ws (chunk histograms ->
-    per-row selection -> index-ordered write): exact against the oracle and equal to the
-    single-workgroup kernel.  'distinct' keeps the k-th key's bin small (its keys are
+    """Rows of 32769 .. 524288 scores go through mzk_topk_rows_ws (chunk histograms ->
+    per-row selection -> index-ordered write), shorter ones through the single-workgroup
+    kernel: exact against the oracle, and the workspace entry equal to mzk_topk_rows.  'distinct' keeps the k-th key's bin small (its keys are
     selected in LDS); 'three_values' puts tens of thousands of equal keys in that bin (the
     selection streams the row instead); partial last chunks, k = G, -inf entries and rows
     with fewer visible entries than k are covered too."""
@@ -86,7 +88,7 @@ def test_topk_long_rows_split_over_workgroups(dev, rows, g, k, kind):
     else:
         sc = -torch.rand(rows, g, generator=gen) - 1.0
         sc[0, :] = float("-inf")
-    assert MI.topk_workspace_bytes(rows, g) > 0
+    assert (MI.topk_workspace_bytes(rows, g) > 0) == (g > 32768)
     got = MI.topk(sc.to(dev), k).cpu().numpy()
     want = OA.topk_indices(sc.numpy(), k)
     assert np.array_equal(got, want)
