@@ -352,14 +352,51 @@ __global__ void __launch_bounds__(256) emit_kernel(EmitParams p) {
       for (int i = 0; i < R; ++i) acc = acc + (i == R - 1 ? kin[c] : ck[i][c]) * div_rn(e[i], s);
       v = acc;
     } else {
-      float m = cgt[d];
-      for (int i = 1; i < r; ++i) m = fmaxf(m, i == r - 1 ? gin[c] : cgt[i * kD + d]);
+      // the carried slots stream through registers kSB at a time: a batch's loads are all
+      // issued before the first is used (clamped to slot r-2; slot r-1 is this token, still
+      // in registers), so a pass over r slots costs r / kSB memory round trips, not r; the
+      // arithmetic is the pinned order (max, the sum of exps from slot 0, the weighted sum
+      // from slot 0)
+      constexpr int kSB = 32;
+      float m = -__builtin_huge_valf();
+      for (int i0 = 0; i0 < r; i0 += kSB) {
+        float gv[kSB];
+#pragma unroll
+        for (int ii = 0; ii < kSB; ++ii) gv[ii] = cgt[min(i0 + ii, r - 2) * kD + d];
+#pragma unroll
+        for (int ii = 0; ii < kSB; ++ii) {
+          const int i = i0 + ii;
+          if (i < r) m = fmaxf(m, i == r - 1 ? gin[c] : gv[ii]);
+        }
+      }
       float s = 0.0f;
-      for (int i = 0; i < r; ++i) s = s + exp_pinned((i == r - 1 ? gin[c] : cgt[i * kD + d]) - m);
+      for (int i0 = 0; i0 < r; i0 += kSB) {
+        float gv[kSB];
+#pragma unroll
+        for (int ii = 0; ii < kSB; ++ii) gv[ii] = cgt[min(i0 + ii, r - 2) * kD + d];
+#pragma unroll
+        for (int ii = 0; ii < kSB; ++ii) {
+          const int i = i0 + ii;
+          if (i < r) s = s + exp_pinned((i == r - 1 ? gin[c] : gv[ii]) - m);
+        }
+      }
       float acc = 0.0f;
-      for (int i = 0; i < r; ++i) {
-        const float e = exp_pinned((i == r - 1 ? gin[c] : cgt[i * kD + d]) - m);
-        acc = acc + (i == r - 1 ? kin[c] : ckv[i * kD + d]) * div_rn(e, s);
+      for (int i0 = 0; i0 < r; i0 += kSB / 2) {
+        float gv[kSB / 2], kv[kSB / 2];
+#pragma unroll
+        for (int ii = 0; ii < kSB / 2; ++ii) {
+          const int i = min(i0 + ii, r - 2);
+          gv[ii] = cgt[i * kD + d];
+          kv[ii] = ckv[i * kD + d];
+        }
+#pragma unroll
+        for (int ii = 0; ii < kSB / 2; ++ii) {
+          const int i = i0 + ii;
+          if (i < r) {
+            const float e = exp_pinned((i == r - 1 ? gin[c] : gv[ii]) - m);
+            acc = acc + (i == r - 1 ? kin[c] : kv[ii]) * div_rn(e, s);
+          }
+        }
       }
       v = acc;
     }

@@ -61,11 +61,13 @@ def _emit_history(kv, gate, ratio, ngroups, nw, cos_t, sin_t, wk=None, kw=None):
     return np.stack(rots, 1), (np.stack(keys, 1) if wk is not None else None)
 
 
-@pytest.mark.parametrize("fmt,coarse", [("fp8", False), ("mxfp4", False), ("mxfp4", True)])
+@pytest.mark.parametrize("fmt,coarse", [("fp8", False), ("mxfp4", False), ("mxfp4", 8), ("fp8", 40)])
 def test_replays_across_group_boundaries(dev, fmt, coarse):
+    """``coarse``: the coarse branch's ratio (40: its carried slots stream through the
+    kernel in more than one batch, the last one partial)."""
     b, ratio, gcap, topk, p0, steps = 3, 4, 64, 16, 150, 11
-    cratio, cgroups = (8, 32) if coarse else (0, 0)
-    gen = torch.Generator().manual_seed(31 + coarse)
+    cratio, cgroups = (coarse, 32) if coarse else (0, 0)
+    gen = torch.Generator().manual_seed(31 + bool(coarse))
     rnd = lambda *s: torch.randn(*s, generator=gen)  # noqa: E731
     print(f"emission replay: fmt={fmt} coarse={coarse} positions {p0}..{p0 + steps - 1}", flush=True)
     nw, kvw = _bf(1 + 0.1 * rnd(D).numpy()), _bf(1 + 0.1 * rnd(D).numpy())
