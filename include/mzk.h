@@ -352,6 +352,14 @@ int mzk_indexer_candidate_scores_mxfp4(const uint8_t* q_packed, const uint8_t* q
 int mzk_candidate_positions(const int32_t* slot_idx, int64_t rows, int k, int64_t idx_stride,
                             const int32_t* cand_blocks, int64_t cand_stride, int n_blocks, int block_size,
                             int32_t* pos_out, int64_t out_stride, void* stream);
+/* The two in one launch (block_size 8, the model's candidate_block_size; other sizes run
+ * the two): the top-k of candidate-axis scores [rows, slots] (row stride row_stride; slots =
+ * n_blocks * block_size <= 32768) written as key positions into out [rows, topk] --
+ * ascending, lowest position first among equal scores, then -1; the list mzk_topk_rows +
+ * mzk_candidate_positions give. */
+int mzk_candidate_topk(const float* scores, int64_t rows, int64_t slots, int64_t row_stride, int topk,
+                       const int32_t* cand_blocks, int64_t cand_stride, int n_blocks, int block_size, int32_t* out,
+                       int64_t out_stride, void* stream);
 
 /* ---------------------------------------------------------------------------------
  * Piece 5: sparse shared-latent MQA attention

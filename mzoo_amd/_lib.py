@@ -51,6 +51,7 @@ _SIGS = {
     "mzk_indexer_candidate_scores_mxfp4": [_P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P,
                                            _I64, _I32, _I32, _P, _I64, _P],
     "mzk_candidate_positions": [_P, _I64, _I32, _I64, _P, _I64, _I32, _I32, _P, _I64, _P],
+    "mzk_candidate_topk": [_P, _I64, _I64, _I64, _I32, _P, _I64, _I32, _I32, _P, _I64, _P],
     "mzk_indexer_scores_fp8": [_P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P, _I64, _P],
     "mzk_indexer_decode_fp8": [_P, _P, _P, _P, _I64, _I32, _I32, _I64, _I64, _P, _I32, _P, _I64, _P, _P, _P, _I32, _I32,
                                _P, _I64, _I32, _P],

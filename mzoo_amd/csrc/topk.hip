@@ -283,9 +283,21 @@ __device__ __forceinline__ BinHit find_bin(const int (&c)[NB / NT], int rem, int
   return BinHit{sh[0], sh[1], sh[2], total};
 }
 
-template <int KPT, int NT>
+// MAP: the row is a candidate axis of blocks of kMapBs slots (slot j = key
+// cand[row][j / kMapBs] * kMapBs + j % kMapBs, the level-two scores); the index list is
+// written as key positions.  A thread's KPT slots are whole blocks, so it loads KPT / kMapBs
+// list entries with its scores.
+constexpr int kMapBs = 8;
+struct SlotMap {
+  const int32_t* cand;
+  int64_t stride;
+  int nb;
+};
+
+template <int KPT, int NT, bool MAP = false>
 __global__ void __launch_bounds__(NT) topk_row_kernel(const float* __restrict__ scores, int64_t row_stride, int G,
-                                                      int k, int32_t* __restrict__ out, int64_t out_stride) {
+                                                      int k, int32_t* __restrict__ out, int64_t out_stride,
+                                                      SlotMap sm = SlotMap{}) {
   constexpr int NW = NT / 64;
   static_assert(KPT * NT <= 32768, "packed counts: at most 2^15 keys per row");
   __shared__ __align__(16) int hist1[kBins * kSub1];
@@ -315,33 +327,45 @@ __global__ void __launch_bounds__(NT) topk_row_kernel(const float* __restrict__ 
 #pragma unroll
     for (int j = 0; j < KPT; ++j) x[j] = (i0 + j < G) ? src[i0 + j] : 0.0f;
   }
-  {
+  static_assert(!MAP || KPT % kMapBs == 0, "whole candidate blocks per thread");
+  int32_t cb[MAP ? KPT / kMapBs : 1];  // MAP: the candidate blocks of this thread's slots
+  if constexpr (MAP) {
+    const int32_t* crow = sm.cand + row * sm.stride;
+#pragma unroll
+    for (int m = 0; m < KPT / kMapBs; ++m) cb[m] = crow[min(i0 / kMapBs + m, sm.nb - 1)];
+  }
+  // G <= k (workgroup-uniform): every finite key is taken, no search
+  const bool search = G > k;
+  if (search) {
     int4* h4 = reinterpret_cast<int4*>(hist1);
     for (int i = tid; i < kBins * kSub1 / 4; i += NT) h4[i] = int4{0, 0, 0, 0};
     for (int i = tid; i < kBins / 4; i += NT) reinterpret_cast<int4*>(hist2)[i] = int4{0, 0, 0, 0};
     for (int i = tid; i < kBins / 8; i += NT) reinterpret_cast<int4*>(hist3)[i] = int4{0, 0, 0, 0};
+    __syncthreads();  // histograms cleared (while the scores are in flight)
   }
-  __syncthreads();  // histograms cleared (while the scores are in flight)
 
   uint32_t key[KPT];
-  int* hl = hist1 + (lane & (kSub1 - 1));
 #pragma unroll
-  for (int j = 0; j < KPT; ++j) {
-    key[j] = (i0 + j < G) ? order_key(x[j]) : 0u;  // 0 sorts below -inf: never taken
-    if (key[j] > kNegInfKey) atomicAdd(hl + (key[j] >> kLowBits) * kSub1, 1);
-  }
-  __syncthreads();
-  int c1[kBins / NT];
+  for (int j = 0; j < KPT; ++j) key[j] = (i0 + j < G) ? order_key(x[j]) : 0u;  // 0 sorts below -inf: never taken
+  BinHit h1{0, 0, 0, 0};
+  if (search) {
+    int* hl = hist1 + (lane & (kSub1 - 1));
 #pragma unroll
-  for (int j = 0; j < kBins / NT; ++j) {
-    const int4 v = reinterpret_cast<const int4*>(hist1)[kBins - 1 - ((kBins / NT) * tid + j)];
-    c1[j] = (v.x + v.y) + (v.z + v.w);
+    for (int j = 0; j < KPT; ++j)
+      if (key[j] > kNegInfKey) atomicAdd(hl + (key[j] >> kLowBits) * kSub1, 1);
+    __syncthreads();
+    int c1[kBins / NT];
+#pragma unroll
+    for (int j = 0; j < kBins / NT; ++j) {
+      const int4 v = reinterpret_cast<const int4*>(hist1)[kBins - 1 - ((kBins / NT) * tid + j)];
+      c1[j] = (v.x + v.y) + (v.z + v.w);
+    }
+    h1 = find_bin<NT, kBins>(c1, k, wsum, sh[0]);
   }
-  const BinHit h1 = find_bin<NT, kBins>(c1, k, wsum, sh[0]);
 
   uint32_t T = kNegInfKey;  // at most k finite keys: take them all
   int need_eq = 0;
-  if (h1.total > k) {
+  if (search && h1.total > k) {
     const uint32_t b1 = static_cast<uint32_t>(h1.bin);  // >= 4
     if (h1.count == h1.rem) {
       T = (b1 << kLowBits) - 1u;
@@ -389,11 +413,15 @@ __global__ void __launch_bounds__(NT) topk_row_kernel(const float* __restrict__ 
   const int written = static_cast<int>(tot >> 16) + min(static_cast<int>(tot & 0xffffu), need_eq);
 #pragma unroll
   for (int j = 0; j < KPT; ++j) {
+    // the value written: the index, or under MAP the slot's key position (a taken slot has a
+    // finite score, which the candidate scorer writes only for slots of a listed block)
+    int32_t v = i0 + j;
+    if constexpr (MAP) v = cb[j / kMapBs] >= 0 ? cb[j / kMapBs] * kMapBs + j % kMapBs : -1;
     if (key[j] > T) {
-      dst[gt_before + min(eq_before, need_eq)] = i0 + j;
+      dst[gt_before + min(eq_before, need_eq)] = v;
       ++gt_before;
     } else if (key[j] == T && T != kNegInfKey) {
-      if (eq_before < need_eq) dst[gt_before + eq_before] = i0 + j;
+      if (eq_before < need_eq) dst[gt_before + eq_before] = v;
       ++eq_before;
     }
   }
@@ -995,6 +1023,45 @@ extern "C" int mzk_topk_rows_ws(const float* scores, int64_t rows, int64_t cols,
   topk_chunk_select_write_kernel<<<grid, kThreads, 0, s>>>(scores, row_stride, G, topk, nch, hist, above, sel, cand,
                                                             out, out_stride);
   MZK_LAUNCH_CHECK("topk_rows_ws");
+  return MZK_OK;
+}
+
+extern "C" int mzk_candidate_topk(const float* scores, int64_t rows, int64_t slots, int64_t row_stride, int topk,
+                                  const int32_t* cand_blocks, int64_t cand_stride, int n_blocks, int block_size,
+                                  int32_t* out, int64_t out_stride, void* stream) {
+  MZK_CHECK_ARG(rows >= 0 && slots >= 0 && topk >= 0 && n_blocks >= 0 && block_size >= 1,
+                "candidate_topk: negative size");
+  MZK_CHECK_ARG(slots == static_cast<int64_t>(n_blocks) * block_size,
+                "candidate_topk: the candidate axis holds n_blocks * block_size slots");
+  MZK_CHECK_ARG(slots <= 32 * kThreads, "candidate_topk: at most %d candidate slots (got %lld)", 32 * kThreads,
+                (long long)slots);
+  MZK_CHECK_ARG(row_stride >= slots && out_stride >= topk && cand_stride >= n_blocks, "candidate_topk: bad strides");
+  if (rows == 0 || topk == 0) return MZK_OK;
+  if (slots == 0) return mzk_topk_rows(scores, rows, 0, row_stride, topk, out, out_stride, stream);  // all -1
+  MZK_CHECK_ARG(rows <= 0x7fffffff, "candidate_topk: too many rows");
+  MZK_CHECK_ARG(out != nullptr && (slots == 0 || (scores != nullptr && cand_blocks != nullptr)),
+                "candidate_topk: null pointer");
+  if (block_size != kMapBs) {  // other block sizes: the top-k, then the position map
+    const int rc = mzk_topk_rows(scores, rows, slots, row_stride, topk, out, out_stride, stream);
+    if (rc) return rc;
+    return mzk_candidate_positions(out, rows, topk, out_stride, cand_blocks, cand_stride, n_blocks, block_size, out,
+                                   out_stride, stream);
+  }
+  hipStream_t s = as_stream(stream);
+  const int G = static_cast<int>(slots);
+  const unsigned nr = static_cast<unsigned>(rows);
+  const SlotMap sm{cand_blocks, cand_stride, n_blocks};
+  if (G <= 8 * 256)
+    topk_row_kernel<8, 256, true><<<nr, 256, 0, s>>>(scores, row_stride, G, topk, out, out_stride, sm);
+  else if (G <= 8 * 512)
+    topk_row_kernel<8, 512, true><<<nr, 512, 0, s>>>(scores, row_stride, G, topk, out, out_stride, sm);
+  else if (G <= 8 * kThreads)
+    topk_row_kernel<8, kThreads, true><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride, sm);
+  else if (G <= 16 * kThreads)
+    topk_row_kernel<16, kThreads, true><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride, sm);
+  else
+    topk_row_kernel<32, kThreads, true><<<nr, kThreads, 0, s>>>(scores, row_stride, G, topk, out, out_stride, sm);
+  MZK_LAUNCH_CHECK("candidate_topk");
   return MZK_OK;
 }
 

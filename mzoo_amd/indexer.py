@@ -229,9 +229,29 @@ def candidate_topk(scores: torch.Tensor, cand_blocks: torch.Tensor, block_size: 
     """Top-k of candidate-axis scores as key positions: the same list ``topk`` gives on the
     dense row masked to the candidates (owlet1/indexer.py:150-151 then :158-161), since
     slot order follows key order -- ascending, lower key first among equal scores, ``-1``
-    pad."""
-    idx = topk(scores, k, out=out, workspace=workspace)
-    return candidate_positions(idx, cand_blocks, block_size, out=idx)
+    pad.  Up to 32768 slots one launch (``mzk_candidate_topk``); longer candidate axes take
+    ``topk`` (with ``workspace``) and ``candidate_positions``."""
+    _lib.require_gpu(scores, cand_blocks)
+    slots = scores.shape[-1]
+    nb = cand_blocks.shape[-1]
+    if slots > 32768:
+        idx = topk(scores, k, out=out, workspace=workspace)
+        return candidate_positions(idx, cand_blocks, block_size, out=idx)
+    if scores.dtype != torch.float32 or cand_blocks.dtype != torch.int32 or not cand_blocks.is_contiguous() \
+            or cand_blocks.shape[:-1] != scores.shape[:-1] or slots != nb * block_size:
+        raise ValueError("candidate_topk: scores fp32 [..., n_blocks * block_size], cand_blocks int32 [..., n_blocks]")
+    sc = scores if scores.stride(-1) == 1 else scores.contiguous()
+    flat = sc.reshape(-1, slots) if sc.dim() != 2 else sc
+    rows = flat.shape[0]
+    if out is None:
+        out = torch.empty(*scores.shape[:-1], k, dtype=torch.int32, device=scores.device)
+    elif out.shape != (*scores.shape[:-1], k) or out.dtype != torch.int32 or not out.is_contiguous():
+        raise ValueError("candidate_topk: out must be contiguous int32 [..., k]")
+    if rows == 0 or k == 0:
+        return out
+    _lib.call("mzk_candidate_topk", flat.data_ptr(), rows, slots, flat.stride(0) if slots else max(slots, 1), k,
+              cand_blocks.data_ptr(), nb, nb, block_size, out.data_ptr(), k, _lib.stream_of(scores))
+    return out
 
 
 def _check_scores_out(b, s, g, device, out):

@@ -162,3 +162,24 @@ def test_candidate_edge_cases(dev):
     out = MI.candidate_positions(slots, blocks, 8, out=slots)
     assert out.data_ptr() == slots.data_ptr()
     assert out.cpu().tolist() == [[[24, 76, 241, -1, -1, -1]]] * b
+
+
+@pytest.mark.parametrize("rows,nb,bs,k", [(3, 40, 8, 64), (4, 2048, 8, 2048), (2, 5000, 8, 2048), (5, 300, 4, 1000)])
+def test_candidate_topk_one_launch_equals_two(dev, rows, nb, bs, k):
+    """mzk_candidate_topk (one launch up to 32768 slots) equals mzk_topk_rows followed by
+    mzk_candidate_positions, with ties, empty blocks and -inf slots; past 32768 slots the
+    wrapper takes the two-step path (checked against the oracle's top-k mapped by hand)."""
+    gen = torch.Generator().manual_seed(rows * 31 + nb)
+    sc = torch.round(torch.randn(rows, nb * bs, generator=gen) * 8) / 8  # ties
+    cand = torch.stack([torch.randperm(4 * nb, generator=gen)[:nb].sort().values for _ in range(rows)]).int()
+    cand[:, -3:] = -1
+    sc.view(rows, nb, bs)[:, -3:] = NEG  # empty blocks score -inf (as the scorer writes)
+    sc[:, ::7] = NEG
+    print(f"candidate top-k: rows={rows} nb={nb} bs={bs} k={k}", flush=True)
+    got = MI.candidate_topk(sc.to(dev), cand.to(dev), bs, k).cpu().numpy()
+    slots = OA.topk_indices(sc.numpy(), k)
+    want = np.where(slots >= 0, cand.numpy()[np.arange(rows)[:, None], np.maximum(slots, 0) // bs] * bs + slots % bs, -1)
+    assert np.array_equal(got, want)
+    if nb * bs <= 32768:
+        two = MI.candidate_positions(MI.topk(sc.to(dev), k), cand.to(dev), bs).cpu().numpy()
+        assert np.array_equal(got, two)
