@@ -430,6 +430,21 @@ __device__ __forceinline__ int pv_lane_offset(int lane, int d_base) {
   return e0 * KT_PITCH + 2 * (d_base + 16 * (grp & 1) + 4 * (j & 3));
 }
 
+// Stores one 32-channel O^T block of a head.  Lane (head, half) holds channels
+// 8 g4 + 4 half + [0, 4) of the block as the bf16 pairs w[2 g4], w[2 g4 + 1]; one
+// v_permlane32_swap per word pair (the upper half-wave's first operand trades places with
+// the lower half-wave's second) leaves each lane 8 consecutive channels per two g4, so
+// the two lanes of a head write 32 contiguous bytes per store instead of two 8-byte
+// pieces 8 bytes apart.  Both lanes of a head must execute it together.
+__device__ __forceinline__ void store_o_block(uint16_t* blk, const uint32_t (&w)[8], int half) {
+#pragma unroll
+  for (int pr = 0; pr < 2; ++pr) {
+    const auto s0 = __builtin_amdgcn_permlane32_swap(w[4 * pr], w[4 * pr + 2], false, false);
+    const auto s1 = __builtin_amdgcn_permlane32_swap(w[4 * pr + 1], w[4 * pr + 3], false, false);
+    *reinterpret_cast<uint4*>(blk + 16 * pr + 8 * half) = uint4{s0[0], s1[0], s0[1], s1[1]};
+  }
+}
+
 // Final bf16 output + lse (one split) or fp32 partials (several) for one lane's head and
 // O^T blocks [b_lo, b_lo + nb): acc[db][j] holds O^T[d][head], d = (b_lo+db)*32 + c_entry(j).
 template <int D, int NOPE, int NDBM>
@@ -452,6 +467,7 @@ __device__ __forceinline__ void write_result(const AttnParams& p, int64_t row, i
 #pragma unroll
     for (int db = 0; db < NDBM; ++db) {
       if (db < nb) {
+        uint32_t w[8];
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
           const int d0 = db * 32 + 8 * g4 + 4 * half;
@@ -472,8 +488,10 @@ __device__ __forceinline__ void write_result(const AttnParams& p, int64_t row, i
                                   -bf16_to_f32(static_cast<uint16_t>(sp >> 16)));
             }
           }
-          *reinterpret_cast<uint2*>(orow + d0) = uint2{w0, w1};
+          w[2 * g4] = w0;
+          w[2 * g4 + 1] = w1;
         }
+        store_o_block(orow + db * 32, w, half);
       }
     }
     if (lse_lane) {
@@ -488,13 +506,13 @@ __device__ __forceinline__ void write_result(const AttnParams& p, int64_t row, i
 #pragma unroll
     for (int db = 0; db < NDBM; ++db) {
       if (db < nb) {
+        uint32_t w[8];
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
-          const int d0 = db * 32 + 8 * g4 + 4 * half;
-          *reinterpret_cast<uint2*>(prow + d0) =
-              uint2{pack_bf16x2(acc[db][4 * g4] * inv_l, acc[db][4 * g4 + 1] * inv_l),
-                    pack_bf16x2(acc[db][4 * g4 + 2] * inv_l, acc[db][4 * g4 + 3] * inv_l)};
+          w[2 * g4] = pack_bf16x2(acc[db][4 * g4] * inv_l, acc[db][4 * g4 + 1] * inv_l);
+          w[2 * g4 + 1] = pack_bf16x2(acc[db][4 * g4 + 2] * inv_l, acc[db][4 * g4 + 3] * inv_l);
         }
+        store_o_block(prow + db * 32, w, half);
       }
     }
     if (lse_lane) {
