@@ -115,6 +115,7 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 
 constexpr int kIdxCap = 4096;       // sparse indices of one split staged in LDS (D <= 256 kernel)
 constexpr int kSplitIdxCap = 1024;  // the same for the D-split kernel (its LDS holds three tiles)
+constexpr int kAllTabCap = 1024;    // D-split kernel: splits of at most this many entries keep every tile's table
 
 typedef const uint8_t __attribute__((address_space(1)))* gptr_t;  // global (not flat) loads
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -182,8 +183,9 @@ struct RowPlan {
   const uint8_t* win_b;
   const uint8_t* dense_b;
   const uint8_t* main_b;
-  const uint8_t** tab_ptr;   // [NSLOT][kTile] in LDS: tile t uses slot t % NSLOT
+  const uint8_t** tab_ptr;   // [NSLOT][kTile] in LDS: tile t uses slot t & slot_mask
   uint32_t* tab_mask;        // [NSLOT] in LDS
+  uint32_t slot_mask = NSLOT - 1;  // all the split's tables at once (build_all_tables): ~0
   // typed address spaces: a generic pointer would make these FLAT loads, which count
   // against the LDS wait counter too and force every later LDS wait to drain completely
   const __attribute__((address_space(3))) int32_t* sidx;     // this split's sparse indices (the first sidx_cap), in LDS
@@ -359,9 +361,9 @@ struct RowPlan {
   __device__ void build_table(const AttnParams& p, int t, int g, int tid) {
     if (tid < kTile) {
       const uint8_t* ptr = entry_ptr(p, t, tid, g);
-      tab_ptr[(t % NSLOT) * kTile + tid] = ptr;
+      tab_ptr[(t & slot_mask) * kTile + tid] = ptr;
       const uint64_t bal = __ballot(ptr != nullptr);
-      if (tid == 0) tab_mask[t % NSLOT] = static_cast<uint32_t>(bal);
+      if (tid == 0) tab_mask[t & slot_mask] = static_cast<uint32_t>(bal);
     }
   }
 
@@ -378,11 +380,47 @@ struct RowPlan {
     }
   }
 
+  // Tables the D-split tile loop reads: tiles 0..3 (its prologue) and up to three past the
+  // last tile (it fetches tile u+3 while at tile u), whose entries are all empty.
+  __device__ int table_tiles() const { return ntiles + 3 > 4 ? ntiles + 3 : 4; }
+
+  // Every entry table the tile loop reads (table_tiles()), at once, when they fit `CAP`
+  // pointers at `all` (which may overlap the staged sparse indices: each thread reads its
+  // indices before a barrier, then writes).  Tile t then uses table t, and the tile loop
+  // builds none.  Entry e = tid + NT * r; a wave's ballot covers tiles 2w' and 2w'+1.
+  // One workgroup barrier; the caller synchronises before the tables are read.
+  template <int CAP>
+  __device__ void build_all_tables(const AttnParams& p, int tid, const uint8_t** all, uint32_t* masks) {
+    static_assert(CAP % NT == 0 && NT % 64 == 0, "whole waves per round");
+    constexpr int R = CAP / NT;
+    const int n = table_tiles() * kTile;  // <= CAP (the caller checks)
+    int g[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int e = tid + NT * r;
+      g[r] = e < n ? slot(v_begin + e) : -1;
+    }
+    __syncthreads();  // every staged index is read before the tables overwrite them
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int e = tid + NT * r;
+      const bool in = e < n;
+      const uint8_t* ptr = in ? entry_ptr(p, e / kTile, e % kTile, g[r]) : nullptr;
+      if (in) all[e] = ptr;
+      const uint64_t bal = __ballot(ptr != nullptr);
+      const int lane = tid & 63;
+      if (in && (lane & 31) == 0) masks[e / kTile] = static_cast<uint32_t>(lane ? bal >> 32 : bal);
+    }
+    tab_ptr = all;
+    tab_mask = masks;
+    slot_mask = ~0u;
+  }
+
   // The tile's pieces for this thread: entry tid / TPE, pieces (tid % TPE) + TPE*k, so the
   // TPE threads of an entry read TPE consecutive 16-byte pieces per load instruction.
   // Empty slots load zeros.
   __device__ void fetch(int t, int tid, Piece (&raw)[PPT]) const {
-    const gptr_t e = (gptr_t)(tab_ptr[(t % NSLOT) * kTile + tid / TPE]);
+    const gptr_t e = (gptr_t)(tab_ptr[(t & slot_mask) * kTile + tid / TPE]);
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
       const int q = tid % TPE + TPE * k;
@@ -706,9 +744,14 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
   float* pm = reinterpret_cast<float*>(smem + M::NKT * M::KT + M::SX);
   uint4* pb = reinterpret_cast<uint4*>(smem + M::NKT * M::KT + M::SX + M::PM);
   float* pe = reinterpret_cast<float*>(smem + M::NKT * M::KT + M::SX + M::PM + M::PB);
-  __shared__ const uint8_t* tab_ptr[NSLOT * kTile];
-  __shared__ uint32_t tab_mask[NSLOT];
-  __shared__ int32_t sidx[kSplitIdxCap];
+  // one LDS region for the entry tables: the staged sparse indices (first 4 KB) and a ring
+  // of NSLOT tables after them, or -- when the split has at most kAllTabCap entries --
+  // every table of the split over the whole region (built once, before the passes)
+  static_assert(kSplitIdxCap * 4 + NSLOT * kTile * 8 <= kAllTabCap * 8, "ring and indices share the region");
+  __shared__ __align__(16) const uint8_t* tabs[kAllTabCap];
+  __shared__ uint32_t tab_mask[kAllTabCap / kTile];
+  int32_t* sidx = reinterpret_cast<int32_t*>(tabs);
+  const uint8_t** tab_ptr = tabs + kSplitIdxCap / 2;
   __shared__ int redo;  // set when the fast pass's running max drifted too far above the truth
 
   const int tid = threadIdx.x;
@@ -767,6 +810,12 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
   if (pre_ok) rp.stage_prefetched(sidx, kSplitIdxCap, tid, pre);
   else rp.stage_indices(p, sidx, kSplitIdxCap, tid);
   __syncthreads();
+  // Splits of at most kAllTabCap entries (every decode configuration) get all their entry
+  // tables here, so the tile loop builds none (a table build costs the building wave an
+  // LDS round trip and the pointer arithmetic on the critical half-step); longer splits
+  // (long prefill rows) build them in a ring as the loop goes.
+  const bool all_tables = rp.table_tiles() * kTile <= kAllTabCap;
+  if (all_tables) rp.template build_all_tables<kAllTabCap>(p, tid, tabs, tab_mask);
   const int b_lo = ds * NB / DS;
   const int nb_mine = (ds + 1) * NB / DS - b_lo;
   const int pv_off = pv_lane_offset<KT_PITCH>(lane, b_lo * 32);
@@ -840,7 +889,7 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
 
     // softmax of tile u for this wave's heads: S^T partials -> running max / sum -> P^T
     auto softmax = [&](int u) __attribute__((always_inline)) {
-      const uint32_t vmask = tab_mask[u % NSLOT];
+      const uint32_t vmask = tab_mask[u & rp.slot_mask];
       // entries 8ds..8ds+7 of tile u for this lane's head
       float4 a = sx[((hg * DS) * 4 + ds) * 64 + lane];
 #pragma unroll
@@ -971,9 +1020,9 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
       rp.store(ktile(u + 1), KT_PITCH, ptid, r0);
       // the index of tile u+5 is read before the fetch is issued: the wait on that read
       // (the compiler's counters are in order) then covers no fetch load
-      const int g_next = tid < kTile ? rp.slot(rp.v_begin + (u + 5) * kTile + tid) : -1;
+      const int g_next = !all_tables && tid < kTile ? rp.slot(rp.v_begin + (u + 5) * kTile + tid) : -1;
       rp.fetch(u + 2, ptid, r0);
-      rp.build_table(p, u + 4, g_pref, tid);
+      if (!all_tables) rp.build_table(p, u + 4, g_pref, tid);
       g_pref = g_next;
       lds_barrier();
       mfma_step(u, true, true);
@@ -988,8 +1037,10 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
       rp.fetch(u + 3, ptid, r1);
     };
     if (rp.ntiles > 0) {
-      rp.build_first_tables(p, tid);
-      if (tid < kTile) g_pref = rp.slot(rp.v_begin + 4 * kTile + tid);
+      if (!all_tables) {
+        rp.build_first_tables(p, tid);
+        if (tid < kTile) g_pref = rp.slot(rp.v_begin + 4 * kTile + tid);
+      }
       __syncthreads();
       rp.fetch(0, ptid, raw);
       if constexpr (!kExact && RST > 0) {
@@ -1202,7 +1253,7 @@ int dispatch_heads(const AttnParams& p, int64_t rows, hipStream_t s) {
   if constexpr (D > 256) {
     // 64 heads per workgroup, each 32-head group split by D over 4 waves
     using M = SplitSmem<FMT, D, NOPE>;
-    static_assert(M::LDS + 4 * kSplitIdxCap + 8 * kTile * 8 + 128 <= 160 * 1024, "LDS budget");
+    static_assert(M::LDS + 8 * kAllTabCap + 4 * (kAllTabCap / kTile) + 128 <= 160 * 1024, "LDS budget");
     auto kern = sparse_mqa_dsplit_kernel<FMT, D, NOPE>;
     // the dynamic-LDS limit is a per-device function attribute: set once per device
     static std::atomic<bool> attr_set[kMaxDevices] = {};  // setting it twice is harmless
