@@ -723,7 +723,11 @@ struct SplitSmem {
   static constexpr int LDS = NKT * KT + SX + PM + PB + PE;
 };
 
-template <int FMT, int D, int NOPE>
+// ALLTAB: the host has checked that every split of the launch keeps all its entry tables
+// (its longest possible split does), so the ring of tables and its index reads (which may
+// go to global memory, and whose waits would then also drain the tile loads in flight) are
+// compiled out.
+template <int FMT, int D, int NOPE, bool ALLTAB>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 sparse_mqa_dsplit_kernel(const AttnParams p) {
   using M = SplitSmem<FMT, D, NOPE>;
@@ -814,7 +818,9 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
   // tables here, so the tile loop builds none (a table build costs the building wave an
   // LDS round trip and the pointer arithmetic on the critical half-step); longer splits
   // (long prefill rows) build them in a ring as the loop goes.
-  const bool all_tables = rp.table_tiles() * kTile <= kAllTabCap;
+  const bool tables_fit = rp.table_tiles() * kTile <= kAllTabCap;
+  const bool all_tables = ALLTAB || tables_fit;
+  if (ALLTAB && !tables_fit) rp.ntiles = 0;  // excluded by the host's check: never read past the tables
   if (all_tables) rp.template build_all_tables<kAllTabCap>(p, tid, tabs, tab_mask);
   const int b_lo = ds * NB / DS;
   const int nb_mine = (ds + 1) * NB / DS - b_lo;
@@ -1254,7 +1260,8 @@ int dispatch_heads(const AttnParams& p, int64_t rows, hipStream_t s) {
     // 64 heads per workgroup, each 32-head group split by D over 4 waves
     using M = SplitSmem<FMT, D, NOPE>;
     static_assert(M::LDS + 8 * kAllTabCap + 4 * (kAllTabCap / kTile) + 128 <= 160 * 1024, "LDS budget");
-    auto kern = sparse_mqa_dsplit_kernel<FMT, D, NOPE>;
+    auto kern_all = sparse_mqa_dsplit_kernel<FMT, D, NOPE, true>;
+    auto kern_ring = sparse_mqa_dsplit_kernel<FMT, D, NOPE, false>;
     // the dynamic-LDS limit is a per-device function attribute: set once per device
     static std::atomic<bool> attr_set[kMaxDevices] = {};  // setting it twice is harmless
     int dev = 0;
@@ -1263,14 +1270,20 @@ int dispatch_heads(const AttnParams& p, int64_t rows, hipStream_t s) {
       return MZK_ELAUNCH;
     }
     if (!attr_set[dev].load(std::memory_order_acquire)) {
-      if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              M::LDS) != hipSuccess) {
-        set_last_error("sparse_mqa: cannot raise the kernel's LDS limit to %d bytes", M::LDS);
-        return MZK_ELAUNCH;
+      for (const void* k : {reinterpret_cast<const void*>(kern_all), reinterpret_cast<const void*>(kern_ring)}) {
+        if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, M::LDS) != hipSuccess) {
+          set_last_error("sparse_mqa: cannot raise the kernel's LDS limit to %d bytes", M::LDS);
+          return MZK_ELAUNCH;
+        }
       }
       attr_set[dev].store(true, std::memory_order_release);
     }
-    return launch_kernel(kern, M::LDS, 512, 64, p, rows, s);
+    // the longest split any workgroup can plan (RowPlan::plan with every source full) and
+    // the entry tables it needs (RowPlan::table_tiles)
+    const int64_t total_max = static_cast<int64_t>(p.window) + (p.dense ? p.dense_cap : 0) + (p.main ? p.topk : 0);
+    const int64_t chunk_max = ((total_max + p.nsplit - 1) / p.nsplit + kTile - 1) / kTile * kTile;
+    const int64_t tables_max = chunk_max / kTile + 3 > 4 ? chunk_max / kTile + 3 : 4;
+    return launch_kernel(tables_max * kTile <= kAllTabCap ? kern_all : kern_ring, M::LDS, 512, 64, p, rows, s);
   } else {
     if (p.H <= 32) return launch_kernel(sparse_mqa_kernel<FMT, D, NOPE, 1>, 0, 64, 32, p, rows, s);
     return launch_kernel(sparse_mqa_kernel<FMT, D, NOPE, 2>, 0, 128, 64, p, rows, s);
