@@ -185,6 +185,26 @@ def test_decode_fp8_config2_shape(dev, nsplit):
     torch.testing.assert_close(lse.cpu(), ref_lse, **LSE_TOL)
 
 
+def test_decode_table_kernels_agree_bitwise(dev):
+    """A launch whose longest possible split keeps every entry table runs the kernel instance
+    without the table ring; the same rows through the ring-capable instance -- a longer index
+    list (top-k form: ascending picks, then -1) with the same valid prefix, so its workgroups
+    build all their tables at run time -- give the same bits, and both match the oracle."""
+    b, h, gcap, pos = 4, 128, 8192, 32767
+    q, win_c, main_c, _, _, sinks, g = _decode_case(dev, b, h, gcap, 2048, pos, seed=41)
+    gen = torch.Generator().manual_seed(42)
+    picks = torch.stack([torch.randperm(g, generator=gen)[:300].sort().values for _ in range(b)]).int()
+    short = torch.cat([picks, torch.full((b, 20), -1, dtype=torch.int32)], 1)  # 128 + 320 entries at most
+    full = torch.cat([picks, torch.full((b, 2048 - 300), -1, dtype=torch.int32)], 1)  # 128 + 2048
+    positions = torch.full((b,), pos, dtype=torch.int64, device=dev)
+    outs = [MA.sparse_mqa_decode(q.to(dev), positions, win_c, 128, main_cache=main_c, groups=g,
+                                 indices=ix.to(dev), sinks=sinks.to(dev), nsplit=1) for ix in (short, full)]
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    ref, ref_lse = _decode_oracle(q, win_c, main_c, None, short, sinks, pos, 128, 1, g)
+    assert_attn_close(outs[0][0], ref)
+    torch.testing.assert_close(outs[0][1].cpu(), ref_lse, **LSE_TOL)
+
+
 def test_decode_fp8_early_position_and_dense(dev):
     """Short history (window not yet full, fewer groups than topk) plus a dense coarse source."""
     b, h, pos = 4, 128, 300
