@@ -204,3 +204,62 @@ def test_capture_advance_requires_emission(dev):
            torch.zeros(2, HI, DI, dtype=torch.bfloat16, device=dev), torch.zeros(2, HI, device=dev))
     with pytest.raises(ValueError, match="in-step group emission"):
         layer.capture(*ins, advance=True)
+
+
+@pytest.mark.parametrize("ratio", [2, 8, 40, 128, 160])
+def test_emission_kernels_agree(dev, ratio):
+    """``mzk_decode_emit`` pools a keyless branch of ratio <= 128 on nine workgroups per row
+    (the coarse branch's kernel) and a branch with an index key, or a longer ratio, on one
+    workgroup per row: for the same group both write the same main-cache entry, bit for bit,
+    equal to the oracle's packed entry; carry-only steps leave the entries alone."""
+    from mzoo_amd import _lib
+    b, cap = 3, 6
+    rng = np.random.default_rng(ratio)
+    groups = np.array([0, 2, 5])
+    pos = (groups + 1) * ratio - 1  # every row completes its group
+    rows = int(cap * ratio)
+    tab = _bf(rng.uniform(-1, 1, (rows, 64)).astype(np.float32))
+    nw = _bf(rng.uniform(0.5, 1.5, D).astype(np.float32))
+    wk = _bf(rng.normal(0, 0.05, (DI, D)).astype(np.float32))
+    kw = _bf(rng.uniform(0.5, 1.5, DI).astype(np.float32))
+    carry_kv = rng.normal(0, 1, (b, ratio, D)).astype(np.float32)
+    carry_gate = rng.normal(0, 2, (b, ratio, D)).astype(np.float32)
+    kv, gate = carry_kv[:, -1].copy(), carry_gate[:, -1].copy()
+    carry_kv[:, -1] = carry_gate[:, -1] = 1e30  # the token's slot: written by the launch
+    bf16 = lambda a: torch.from_numpy(np.ascontiguousarray(a)).bfloat16().to(dev)  # noqa: E731
+    dv = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731  (keeps the dtype)
+    tab_d, nw_d, wk_d, kw_d = bf16(tab), bf16(nw), bf16(wk), bf16(kw)
+
+    def emit(key, position):
+        cache = torch.zeros(b, cap, 656, dtype=torch.uint8, device=dev)
+        ckv, cgt = dv(carry_kv), dv(carry_gate)
+        kc = torch.zeros(b, cap, DI, dtype=torch.uint8, device=dev)
+        ks = torch.zeros(b, cap, dtype=torch.float32, device=dev)
+        k = (wk_d.data_ptr(), kw_d.data_ptr(), 1e-6, 0, kc.data_ptr(), ks.data_ptr(), cap) if key else \
+            (None, None, 0.0, 0, None, None, 0)
+        p_d, kv_d, gate_d = dv(position), dv(kv), dv(gate)
+        _lib.call("mzk_decode_emit", p_d.data_ptr(), b, kv_d.data_ptr(), gate_d.data_ptr(),
+                  ckv.data_ptr(), cgt.data_ptr(), ratio, nw_d.data_ptr(), 1e-6, cache.data_ptr(), cap, cap, *k,
+                  tab_d.data_ptr(), rows, None, None, None, None, 0.0, None, 0, 0, None, 0, None, None,
+                  _lib.stream_of(cache))
+        torch.cuda.synchronize()
+        return cache.cpu().numpy(), ckv.cpu().numpy()
+
+    pos_d = pos.astype(np.int64)
+    plain, ckv_plain = emit(False, pos_d)
+    keyed, _ = emit(True, pos_d)
+    assert np.array_equal(plain, keyed)
+    for r in range(b):
+        g = groups[r]
+        kvg = carry_kv[r:r + 1].copy()
+        gtg = carry_gate[r:r + 1].copy()
+        kvg[:, -1], gtg[:, -1] = kv[r], gate[r]
+        cs, sn = tab[g * ratio:g * ratio + 1, :32], tab[g * ratio:g * ratio + 1, 32:]
+        rot, _ = C.emit_group(kvg, gtg, ratio, nw, 1e-6, cs, sn)
+        assert np.array_equal(plain[r, g], Q.pack_latent_fp8_b128(rot)[0]), f"row {r}: main entry"
+        assert np.array_equal(ckv_plain[r, -1], kv[r]), f"row {r}: the token's carry slot"
+    # a step that completes no group writes only the carry slot
+    idle, ckv_idle = emit(False, pos_d - 1)
+    assert not idle.any()
+    for r in range(b):
+        assert np.array_equal(ckv_idle[r, -2], kv[r])
