@@ -397,32 +397,48 @@ __global__ void __launch_bounds__(NT) topk_row_kernel(const float* __restrict__ 
     }
   }
 
-  // compaction in index order
-  int n_gt = 0, n_eq = 0;
+  // compaction in index order: a key is taken when it lies above T, or equals T with fewer
+  // than need_eq keys equal to T before it; its output slot is the number of taken keys
+  // before it
+  static_assert(KPT <= 32, "one bit per key of a thread");
+  uint32_t gt_mask = 0u, eq_mask = 0u;
 #pragma unroll
   for (int j = 0; j < KPT; ++j) {
-    n_gt += key[j] > T;
-    n_eq += (key[j] == T) && (T != kNegInfKey);
+    gt_mask |= static_cast<uint32_t>(key[j] > T) << j;
+    eq_mask |= static_cast<uint32_t>((key[j] == T) && (T != kNegInfKey)) << j;
   }
+  const int n_gt = __builtin_popcount(gt_mask), n_eq = __builtin_popcount(eq_mask);
   // packed as unsigned: n_gt <= G <= 32768 fills bit 31 at most, n_eq stays below 2^16
   const int packed = (n_gt << 16) | n_eq;
   int tot_p;
   const int incl = block_incl_scan<NT>(packed, wsum, tot_p);
   const uint32_t before = static_cast<uint32_t>(incl - packed), tot = static_cast<uint32_t>(tot_p);
-  int gt_before = static_cast<int>(before >> 16), eq_before = static_cast<int>(before & 0xffffu);
+  const int gt_before = static_cast<int>(before >> 16), eq_before = static_cast<int>(before & 0xffffu);
   const int written = static_cast<int>(tot >> 16) + min(static_cast<int>(tot & 0xffffu), need_eq);
+  uint32_t sel = gt_mask;  // this thread's taken keys
+  for (int m = need_eq - eq_before; m > 0 && eq_mask != 0u; --m) {
+    const uint32_t low = eq_mask & (0u - eq_mask);  // its lowest-indexed keys equal to T first
+    sel |= low;
+    eq_mask ^= low;
+  }
+  // Written in rounds, one taken key per thread (lowest index first), so a wave issues as
+  // many store instructions as its busiest thread has taken keys rather than KPT.
+  int pos = gt_before + min(eq_before, need_eq);
+  while (__any(sel != 0u)) {
+    if (sel != 0u) {
+      const int j = __builtin_ctz(sel);
+      // the value written: the index, or under MAP the slot's key position (a taken slot has
+      // a finite score, which the candidate scorer writes only for slots of a listed block)
+      int32_t v = i0 + j;
+      if constexpr (MAP) {
+        int32_t c = cb[0];
 #pragma unroll
-  for (int j = 0; j < KPT; ++j) {
-    // the value written: the index, or under MAP the slot's key position (a taken slot has a
-    // finite score, which the candidate scorer writes only for slots of a listed block)
-    int32_t v = i0 + j;
-    if constexpr (MAP) v = cb[j / kMapBs] >= 0 ? cb[j / kMapBs] * kMapBs + j % kMapBs : -1;
-    if (key[j] > T) {
-      dst[gt_before + min(eq_before, need_eq)] = v;
-      ++gt_before;
-    } else if (key[j] == T && T != kNegInfKey) {
-      if (eq_before < need_eq) dst[gt_before + eq_before] = v;
-      ++eq_before;
+        for (int b = 1; b < KPT / kMapBs; ++b)
+          if (j / kMapBs == b) c = cb[b];
+        v = c >= 0 ? c * kMapBs + j % kMapBs : -1;
+      }
+      dst[pos++] = v;
+      sel &= sel - 1u;
     }
   }
   for (int i = written + tid; i < k; i += NT) dst[i] = -1;
