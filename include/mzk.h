@@ -380,9 +380,10 @@ int mzk_candidate_topk(const float* scores, int64_t rows, int64_t slots, int64_t
  *              empty (main_kv may be NULL)
  *   sinks      [H] fp32 natural-log logit or NULL
  *   nsplit     splits of the entry axis per row; > 1 needs a workspace of
- *              rows*nsplit*H*(2*D+8) bytes: each split's output O/l in bf16
- *              [rows, nsplit, H, D], then its (m, l) in fp32 [rows, nsplit, H, 2] (m in log2
- *              units); merged by a second kernel
+ *              rows*nsplit*H*(2*D+8) bytes: each split's output O/l in bf16 by
+ *              16-channel group, [rows, nsplit, D/16, H, 16] (a workgroup's stores are then
+ *              contiguous), then its (m, l) in fp32 [rows, nsplit, H, 2] (m in log2 units);
+ *              merged by a second kernel
  *   out        [rows, H, D] bf16;  lse [B, H, S] fp32 (natural log, sink included).
  *              With nsplit > 1, out == lse == NULL writes only the partials (the merge is
  *              then mzk_sparse_mqa_combine). */

@@ -85,7 +85,7 @@ struct AttnParams {
   // outputs
   uint16_t* out;  // [rows, H, D] bf16 (nsplit == 1)
   float* lse;     // [B, H, S]       (nsplit == 1)
-  uint16_t* part_o;  // [rows, split_stride, H, D] bf16: the split's output O / l
+  uint16_t* part_o;  // [rows, split_stride, D/16, H, 16] bf16: the split's output O / l, by 16-channel group
   float* part_ml;    // [rows, split_stride, H, 2]: the split's running max m (log2 units) and sum l
   int split_stride;  // splits per row in the workspace (nsplit, or more when launches share it)
   int write_final;   // one split writes the final output and lse instead of partials
@@ -537,10 +537,11 @@ __device__ __forceinline__ void write_result(const AttnParams& p, int64_t row, i
       p.lse[(b * p.H + head) * p.S + s_idx] = (m_fin + __log2f(l_fin)) * kLn2;
     }
   } else {
-    // the split's own normalized output in bf16 (a split that saw no entry writes zeros)
+    // the split's own normalized output in bf16 (a split that saw no entry writes zeros), in
+    // 16-channel groups with the heads innermost: a store instruction of the two group halves
+    // the permlane swap gives a head's two lanes covers 32 heads x 32 bytes, 1 KB contiguous
     const float inv_l = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-    uint16_t* prow = p.part_o + (row * p.split_stride + split) * p.H * static_cast<int64_t>(D) +
-                     static_cast<uint32_t>(head * D + b_lo * 32);
+    uint16_t* pbase = p.part_o + (row * p.split_stride + split) * p.H * static_cast<int64_t>(D);
 #pragma unroll
     for (int db = 0; db < NDBM; ++db) {
       if (db < nb) {
@@ -550,7 +551,14 @@ __device__ __forceinline__ void write_result(const AttnParams& p, int64_t row, i
           w[2 * g4] = pack_bf16x2(acc[db][4 * g4] * inv_l, acc[db][4 * g4 + 1] * inv_l);
           w[2 * g4 + 1] = pack_bf16x2(acc[db][4 * g4 + 2] * inv_l, acc[db][4 * g4 + 3] * inv_l);
         }
-        store_o_block(prow + db * 32, w, half);
+        // groups 2 (b_lo + db) and 2 (b_lo + db) + 1 of the head
+        uint16_t* grp = pbase + static_cast<uint32_t>((b_lo + db) * p.H * 32 + head * 16);
+#pragma unroll
+        for (int pr = 0; pr < 2; ++pr) {
+          const auto s0 = __builtin_amdgcn_permlane32_swap(w[4 * pr], w[4 * pr + 2], false, false);
+          const auto s1 = __builtin_amdgcn_permlane32_swap(w[4 * pr + 1], w[4 * pr + 3], false, false);
+          *reinterpret_cast<uint4*>(grp + static_cast<uint32_t>(pr * p.H * 16) + 8 * half) = uint4{s0[0], s1[0], s0[1], s1[1]};
+        }
       }
     }
     if (lse_lane) {
@@ -1133,7 +1141,10 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
 // Merge the split partials with the sink: split s contributes its normalized output O_s
 // with weight l_s exp2(m_s - M) / L, where M = max(m_s, sink) and
 // L = sum_s l_s exp2(m_s - M) + exp2(sink - M).  One thread per 8 * NP channels of a
-// (row, head): NP 16-byte pieces of every split in flight per memory round trip.
+// (row, head), NP 16-byte pieces of every split in flight per memory round trip.  A wave
+// takes 16 heads x 4 runs of 8 * NP channels (lane % 16 the head, lane / 16 the run): it
+// reads 16 heads x 16 NP bytes contiguous per run from the partials' 16-channel groups and
+// writes 4 x 16 NP contiguous bytes of each head's output row.
 constexpr int kCombineRegSplits = 8;  // splits merged per memory round trip
 
 template <int D, int NP>
@@ -1143,20 +1154,27 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
                                                       uint16_t* __restrict__ out, float* __restrict__ lse,
                                                       const uint16_t* __restrict__ rope_cos,
                                                       const uint16_t* __restrict__ rope_sin, int rope_dim) {
-  static_assert(D % (8 * NP) == 0, "whole pieces per thread");
-  constexpr int CT = D / (8 * NP);  // threads per (row, head)
+  static_assert(D % 16 == 0 && (NP == 1 || NP == 2), "16-channel groups, one or two pieces per thread");
+  constexpr int CPW = 4 * 8 * NP;             // channels per wave
+  constexpr int NWB = (D + CPW - 1) / CPW;    // waves per 16 heads of a row
   const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (t >= rows * H * CT) return;
-  const int c = static_cast<int>(t % CT);
-  const int64_t rh = t / CT;
-  const int head = static_cast<int>(rh % H);
-  const int64_t row = rh / H;
+  const int lane = static_cast<int>(t & 63);
+  const int64_t wv = t >> 6;
+  const int nhb = (H + 15) / 16;
+  const int wb = static_cast<int>(wv % NWB);
+  const int hb = static_cast<int>((wv / NWB) % nhb);
+  const int64_t row = wv / (static_cast<int64_t>(NWB) * nhb);
+  const int head = hb * 16 + (lane & 15);
+  const int ch0 = wb * CPW + (lane >> 4) * 8 * NP;  // this thread's first channel
+  if (row >= rows || head >= H || ch0 >= D) return;
+  const int64_t rh = row * H + head;
   const float* ml = part_ml + (row * nsplit * H + head) * 2;  // split s at + 2 s H
-  const uint16_t* po = part_o + (row * nsplit * H + head) * static_cast<int64_t>(D) + 8 * NP * c;
+  // split s's channel ch0 of this head: group ch0 / 16, heads innermost
+  const uint16_t* po = part_o + row * nsplit * H * static_cast<int64_t>(D) + (ch0 >> 4) * (H * 16) + head * 16 + (ch0 & 15);
   const float sk = sinks ? sinks[head] * kLog2e : -__builtin_huge_valf();
   // the inverse RoPE of the merged bf16 output (owlet1/attention.py:226): cos / sin of this
   // thread's pairs when its channels lie in the trailing rope_dim
-  const int rope_ch = 8 * NP * c - (D - rope_dim);
+  const int rope_ch = ch0 - (D - rope_dim);
   const bool rot = rope_cos != nullptr && rope_ch >= 0;
   uint2 rc[NP], rs[NP];
 #pragma unroll
@@ -1233,9 +1251,9 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
                               -bf16_to_f32(static_cast<uint16_t>((k & 1) ? sp >> 16 : sp & 0xffffu)));
       }
     }
-    *reinterpret_cast<uint4*>(out + rh * static_cast<int64_t>(D) + 8 * NP * c + 8 * i) = uint4{o[0], o[1], o[2], o[3]};
+    *reinterpret_cast<uint4*>(out + rh * static_cast<int64_t>(D) + ch0 + 8 * i) = uint4{o[0], o[1], o[2], o[3]};
   }
-  if (c == 0) lse[((row / S) * H + head) * S + row % S] = (M + __log2f(L)) * kLn2;
+  if (ch0 == 0) lse[((row / S) * H + head) * S + row % S] = (M + __log2f(L)) * kLn2;
 }
 
 template <typename K>
@@ -1318,12 +1336,14 @@ void launch_combine(const uint16_t* po, const float* pml, int nsplit, int H, int
   // the rope slice (config 2, 4 splits: 7.4 vs 7.9 us); with more splits, whose chunk of 8
   // then holds 16 pieces in flight per thread, one is faster (configs 4 / 5, 16 / 32 splits:
   // 7.9 vs 8.4 and 9.2 vs 11.2 us)
-  if (nsplit <= 4 && D % 16 == 0 && (rope_cos == nullptr || (D - rope_dim) % 16 == 0)) {
-    const int64_t n = rows * H * (D / 16);
+  const int64_t nhb = (H + 15) / 16;
+  auto threads = [&](int np) { return rows * nhb * ((D + 32 * np - 1) / (32 * np)) * 64; };
+  if (nsplit <= 4 && (rope_cos == nullptr || (D - rope_dim) % 16 == 0)) {
+    const int64_t n = threads(2);
     combine_kernel<D, 2><<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(po, pml, nsplit, H, S, rows, sinks,
                                                                                 out, lse, rope_cos, rope_sin, rope_dim);
   } else {
-    const int64_t n = rows * H * (D / 8);
+    const int64_t n = threads(1);
     combine_kernel<D, 1><<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(po, pml, nsplit, H, S, rows, sinks,
                                                                                 out, lse, rope_cos, rope_sin, rope_dim);
   }
