@@ -192,9 +192,12 @@ struct RowPlan {
   const __attribute__((address_space(1))) int32_t* idx_row;  // the row's sparse indices in global memory
   int sidx_cap;
 
-  // Workgroup -> (row, split, head group).  The head groups of one (row, split) read the
-  // same entries: they get consecutive slots of one XCD (workgroups are dealt to the 8
-  // XCDs round-robin), so the second and later reads of an entry hit that XCD's L2.
+  // Workgroup -> (row, split, head group).  Workgroups are dealt to the 8 XCDs round-robin
+  // (workgroup i runs on XCD i % 8).  With rows a multiple of 8, every workgroup of row r
+  // runs on XCD r % 8: the head groups of a (row, split), which read the same entries, and
+  // the splits, which read the same q, share an L2, and so does the merge launch, which maps
+  // its workgroups the same way and finds the row's partials there.  Otherwise the head
+  // groups of one (row, split) get consecutive slots of one XCD.
   // 32-bit arithmetic: the host keeps the grid below 2^31 workgroups and the list
   // lengths (window + dense_cap + topk) below 2^31.
   __device__ void init(const AttnParams& p, int heads_per_wg) {
@@ -208,7 +211,13 @@ struct RowPlan {
     const uint32_t units = static_cast<uint32_t>(p.rows) * static_cast<uint32_t>(p.nsplit);
     const uint32_t L0 = blockIdx.x;
     uint32_t unit;
-    if ((units & 7u) == 0) {
+    if ((p.rows & 7) == 0) {  // row-per-XCD
+      const uint32_t per_row = static_cast<uint32_t>(p.nsplit) * nhg;
+      const uint32_t k = L0 >> 3;
+      const uint32_t r8 = k / per_row, i = k - r8 * per_row;
+      hgrp = static_cast<int>(i % nhg);
+      unit = (r8 * 8 + (L0 & 7u)) * static_cast<uint32_t>(p.nsplit) + i / nhg;
+    } else if ((units & 7u) == 0) {
       const uint32_t w = L0 >> 3;
       hgrp = static_cast<int>(w % nhg);
       unit = (w / nhg) * 8 + (L0 & 7u);
@@ -1157,10 +1166,18 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
   static_assert(D % 16 == 0 && (NP == 1 || NP == 2), "16-channel groups, one or two pieces per thread");
   constexpr int CPW = 4 * 8 * NP;             // channels per wave
   constexpr int NWB = (D + CPW - 1) / CPW;    // waves per 16 heads of a row
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int nhb = (H + 15) / 16;
+  // a row's workgroups on XCD row % 8, where the attention launch left its partials
+  // (rows a multiple of 8, whole workgroups per row)
+  const int64_t wg_per_row = (static_cast<int64_t>(NWB) * nhb + 3) / 4;
+  int64_t bid = blockIdx.x;
+  if ((rows & 7) == 0 && (static_cast<int64_t>(NWB) * nhb) % 4 == 0) {
+    const int64_t k = bid >> 3, x = bid & 7;
+    bid = ((k / wg_per_row) * 8 + x) * wg_per_row + k % wg_per_row;
+  }
+  const int64_t t = bid * 256 + threadIdx.x;
   const int lane = static_cast<int>(t & 63);
   const int64_t wv = t >> 6;
-  const int nhb = (H + 15) / 16;
   const int wb = static_cast<int>(wv % NWB);
   const int hb = static_cast<int>((wv / NWB) % nhb);
   const int64_t row = wv / (static_cast<int64_t>(NWB) * nhb);
