@@ -193,8 +193,8 @@ struct RowPlan {
   int sidx_cap;
 
   // Workgroup -> (row, split, head group).  Workgroups are dealt to the 8 XCDs round-robin
-  // (workgroup i runs on XCD i % 8).  With rows a multiple of 8, every workgroup of row r
-  // runs on XCD r % 8: the head groups of a (row, split), which read the same entries, and
+  // (workgroup i runs on XCD i % 8).  ROW_XCD (the decode kernel instance) with rows a
+  // multiple of 8: every workgroup of row r runs on XCD r % 8: the head groups of a (row, split), which read the same entries, and
   // the splits, which read the same q, share an L2, and so does the merge launch, which maps
   // its workgroups the same way and finds the row's partials there.  Otherwise the head
   // groups of one (row, split) get consecutive slots of one XCD.
@@ -205,13 +205,16 @@ struct RowPlan {
     plan(p, p.positions[row]);
   }
 
-  // The workgroup's (row, split, head group); no memory access.
+  // The workgroup's (row, split, head group); no memory access.  (ROW_XCD is a template
+  // argument so that the other kernel instances compile without its branch: their code,
+  // the prefill's long tile loops included, stays as it was.)
+  template <bool ROW_XCD = false>
   __device__ void locate(const AttnParams& p, int heads_per_wg) {
     const uint32_t nhg = static_cast<uint32_t>((p.H + heads_per_wg - 1) / heads_per_wg);
     const uint32_t units = static_cast<uint32_t>(p.rows) * static_cast<uint32_t>(p.nsplit);
     const uint32_t L0 = blockIdx.x;
     uint32_t unit;
-    if ((p.rows & 7) == 0) {  // row-per-XCD
+    if (ROW_XCD && (p.rows & 7) == 0) {  // row-per-XCD
       const uint32_t per_row = static_cast<uint32_t>(p.nsplit) * nhg;
       const uint32_t k = L0 >> 3;
       const uint32_t r8 = k / per_row, i = k - r8 * per_row;
@@ -785,7 +788,7 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
   RP rp;
   rp.tab_ptr = tab_ptr;
   rp.tab_mask = tab_mask;
-  rp.locate(p, HG * 32);
+  rp.template locate<ALLTAB>(p, HG * 32);
   // The row's index list, its position and this lane's query fragment are requested
   // together: one memory round trip at the start instead of three dependent ones.
   v4i pre;
