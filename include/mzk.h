@@ -145,6 +145,26 @@ int mzk_decode_emit(const int64_t* positions, int64_t B, const float* kv, const 
                     int64_t win_batch_entries, int win_cap, const void* q_idx, int q_format, uint8_t* q_codes,
                     void* q_scales, void* stream);
 
+/* The two compressors of a hierarchical decode step (owlet1/cache.py:96-124, :159-172 with the
+ * 4x fine compressor and the dense coarse one, owlet1/attention.py:173-192) in one launch: the
+ * fine branch exactly as mzk_decode_emit with the arguments up to q_scales, and a coarse
+ * branch without index key, prologue or step tables -- as mzk_decode_emit(positions, B,
+ * c_kv, c_gate, c_carry_kv, c_carry_gate, c_ratio, c_norm_weight, c_eps, c_cache,
+ * c_cache_batch_entries, c_cache_cap, NULL, ..., rope_table, table_rows, NULL, ...) -- the
+ * same results as those two calls.  One kernel when the fine ratio is 4 and the coarse
+ * ratio 2..128 with B <= 1024 rows (else the two launches).  Both branches share positions
+ * and the RoPE table. */
+int mzk_decode_emit_pair(const int64_t* positions, int64_t B, const float* kv, const float* gate, float* carry_kv,
+                         float* carry_gate, int ratio, const void* norm_weight, float eps, uint8_t* cache,
+                         int64_t cache_batch_entries, int64_t cache_cap, const void* wk, const void* k_norm_weight,
+                         float k_eps, int key_format, uint8_t* k_codes, void* k_scales, int64_t key_batch_entries,
+                         const void* rope_table, int64_t table_rows, void* step_cos, void* step_sin,
+                         const void* kv_proj, const void* kv_weight, float kv_eps, uint8_t* win_cache,
+                         int64_t win_batch_entries, int win_cap, const void* q_idx, int q_format, uint8_t* q_codes,
+                         void* q_scales, const float* c_kv, const float* c_gate, float* c_carry_kv,
+                         float* c_carry_gate, int c_ratio, const void* c_norm_weight, float c_eps, uint8_t* c_cache,
+                         int64_t c_cache_batch_entries, int64_t c_cache_cap, void* stream);
+
 /* ---------------------------------------------------------------------------------
  * Piece 2: KV compressor and RoPE
  * --------------------------------------------------------------------------------- */

@@ -220,22 +220,24 @@ __device__ __forceinline__ void kv_prologue(const EmitParams& p, int64_t b, int 
 }
 
 // R > 0: the ratio is R (the group stays in registers); R == 0: any ratio (br.ratio).
+// Workgroup `blk` of an emission launch (emit_kernel, or the first workgroups of
+// emit_pair_kernel).
 template <int R>
-__global__ void __launch_bounds__(256) emit_kernel(EmitParams p) {
+__device__ __forceinline__ void emit_body(const EmitParams& p, int64_t blk) {
   __shared__ float lat[kD];
   __shared__ float kvec[kDi];
   __shared__ float inv_s[2];
   const int t = threadIdx.x;
-  if (static_cast<int64_t>(blockIdx.x) >= p.B) {  // uniform: a prologue workgroup
+  if (blk >= p.B) {  // uniform: a prologue workgroup
     // per row: kQBlocks query workgroups (with a query), then one for the window entry
     const int nq = p.q_idx ? kQBlocks : 0;
-    const int64_t w = blockIdx.x - p.B;
+    const int64_t w = blk - p.B;
     const int64_t row = w / (nq + 1), k = w % (nq + 1);
     if (k < nq) query_prologue(p, row * kQBlocks + k, t);
     else if (t < 64) kv_prologue(p, row, t);
     return;
   }
-  const int64_t b = blockIdx.x;
+  const int64_t b = blk;
   const EmitBranch& br = p.br;
   const int64_t pos = p.positions[b];
   if (pos < 0) return;  // an inactive row: nothing to carry or emit
@@ -511,6 +513,11 @@ __global__ void __launch_bounds__(256) emit_kernel(EmitParams p) {
   }
 }
 
+template <int R>
+__global__ void __launch_bounds__(256) emit_kernel(EmitParams p) {
+  emit_body<R>(p, blockIdx.x);
+}
+
 // ---- a long-ratio branch without an index key (the coarse branch), its group step
 // spread over workgroups ------------------------------------------------------------------
 // Pooling r carried slots of 576 channels in the pinned order (the running max, the sum of
@@ -531,7 +538,9 @@ constexpr int kCoarseMaxRatio = 128;       // slots held in LDS
 constexpr int kCoarseMaxRows = 1024;
 __device__ unsigned g_coarse_arrivals[kCoarseMaxRows];  // zero at load; every group step leaves it zero
 
-__global__ void __launch_bounds__(256) coarse_emit_kernel(EmitParams p) {
+// Workgroup `blk` of a coarse-branch launch (coarse_emit_kernel, or the workgroups after the
+// fine branch's in emit_pair_kernel).
+__device__ __forceinline__ void coarse_body(const EmitParams& p, int64_t blk) {
   __shared__ float ev[kCoarseMaxRatio][64];  // a part's gates, then exps, then weighted terms
   __shared__ float pmax[4][64];
   __shared__ float psum[64];
@@ -539,8 +548,8 @@ __global__ void __launch_bounds__(256) coarse_emit_kernel(EmitParams p) {
   __shared__ float inv_s;
   __shared__ int last;
   const int t = threadIdx.x;
-  const int64_t b = blockIdx.x / kCoarseParts;
-  const int part = static_cast<int>(blockIdx.x % kCoarseParts);
+  const int64_t b = blk / kCoarseParts;
+  const int part = static_cast<int>(blk % kCoarseParts);
   const EmitBranch& br = p.br;
   const int64_t pos = p.positions[b];
   if (pos < 0) return;  // an inactive row: nothing to carry or emit
@@ -658,29 +667,35 @@ __global__ void __launch_bounds__(256) coarse_emit_kernel(EmitParams p) {
   }
 }
 
-}  // namespace
-}  // namespace mzk
+__global__ void __launch_bounds__(256) coarse_emit_kernel(EmitParams p) { coarse_body(p, blockIdx.x); }
 
-using namespace mzk;
+// Both branches of a hierarchical step in one launch: workgroups [0, nfine) are the fine
+// (ratio-4) branch's emit_kernel<4> launch with its prologue, the rest the coarse branch's
+// coarse_emit_kernel launch -- the same work, one launch instead of two.
+__global__ void __launch_bounds__(256) emit_pair_kernel(EmitParams pf, EmitParams pc, unsigned nfine) {
+  if (blockIdx.x < nfine) emit_body<4>(pf, blockIdx.x);
+  else coarse_body(pc, static_cast<int64_t>(blockIdx.x) - nfine);
+}
 
-extern "C" int mzk_decode_emit(const int64_t* positions, int64_t B, const float* kv, const float* gate,
-                               float* carry_kv, float* carry_gate, int ratio, const void* norm_weight, float eps,
-                               uint8_t* cache, int64_t cache_batch_entries, int64_t cache_cap, const void* wk,
-                               const void* k_norm_weight, float k_eps, int key_format, uint8_t* k_codes,
-                               void* k_scales, int64_t key_batch_entries, const void* rope_table, int64_t table_rows,
-                               void* step_cos, void* step_sin, const void* kv_proj, const void* kv_weight, float kv_eps,
-                               uint8_t* win_cache, int64_t win_batch_entries, int win_cap, const void* q_idx,
-                               int q_format, uint8_t* q_codes, void* q_scales, void* stream) {
+// The checked parameters of one emission launch (mzk_decode_emit's contract).
+int build_emit(const int64_t* positions, int64_t B, const float* kv, const float* gate,
+               float* carry_kv, float* carry_gate, int ratio, const void* norm_weight, float eps,
+               uint8_t* cache, int64_t cache_batch_entries, int64_t cache_cap, const void* wk,
+               const void* k_norm_weight, float k_eps, int key_format, uint8_t* k_codes,
+               void* k_scales, int64_t key_batch_entries, const void* rope_table, int64_t table_rows,
+               void* step_cos, void* step_sin, const void* kv_proj, const void* kv_weight, float kv_eps,
+               uint8_t* win_cache, int64_t win_batch_entries, int win_cap, const void* q_idx,
+               int q_format, uint8_t* q_codes, void* q_scales, EmitParams& p) {
   MZK_CHECK_ARG(B >= 0 && B <= 0x7fffffff, "decode_emit: bad B");
   MZK_CHECK_ARG(ratio >= 1 && ratio <= 1024, "decode_emit: ratio %d not in [1, 1024]", ratio);
-  if (B == 0) return MZK_OK;
+  if (B == 0) return MZK_OK;  // nothing to launch (the caller checks B too)
   MZK_CHECK_ARG(positions && kv && carry_kv && norm_weight && cache && rope_table && (ratio == 1 || (gate && carry_gate)),
                 "decode_emit: null pointer");
   MZK_CHECK_ARG(table_rows >= 1, "decode_emit: empty RoPE table");
   MZK_CHECK_ARG((step_cos == nullptr) == (step_sin == nullptr), "decode_emit: step cos and sin go together");
   MZK_CHECK_ARG(aligned16(cache) && cache_cap >= 0 && cache_batch_entries >= cache_cap,
                 "decode_emit: the cache must be 16-byte aligned with cache_batch_entries >= cache_cap");
-  EmitParams p{};
+  p = EmitParams{};
   EmitBranch& br = p.br;
   br.kv = kv;
   br.gate = gate;
@@ -733,14 +748,81 @@ extern "C" int mzk_decode_emit(const int64_t* positions, int64_t B, const float*
     MZK_CHECK_ARG(q_idx == nullptr, "decode_emit: the query prologue comes with the kv prologue");
   }
   p.B = B;
-  const unsigned grid = static_cast<unsigned>(B * (p.kv_raw ? (p.q_idx ? 2 + kQBlocks : 2) : 1));
-  if (ratio == 4) {
-    emit_kernel<4><<<grid, 256, 0, as_stream(stream)>>>(p);
-  } else if (ratio >= 2 && ratio <= kCoarseMaxRatio && !wk && !kv_proj && !step_cos && B <= kCoarseMaxRows) {
-    coarse_emit_kernel<<<static_cast<unsigned>(B * kCoarseParts), 256, 0, as_stream(stream)>>>(p);
+  return MZK_OK;
+}
+
+// The workgroups of an emission launch (its rows, and the prologue's per row).
+unsigned emit_grid(const EmitParams& p) {
+  return static_cast<unsigned>(p.B * (p.kv_raw ? (p.q_idx ? 2 + kQBlocks : 2) : 1));
+}
+
+// The coarse kernel's branch: a ratio of 2 .. kCoarseMaxRatio without key, prologue or step tables.
+bool coarse_form(const EmitParams& p) {
+  return p.br.ratio >= 2 && p.br.ratio <= kCoarseMaxRatio && !p.br.wk && !p.kv_raw && !p.step_cos &&
+         p.B <= kCoarseMaxRows;
+}
+
+int launch_emit(const EmitParams& p, void* stream) {
+  if (p.br.ratio == 4) {
+    emit_kernel<4><<<emit_grid(p), 256, 0, as_stream(stream)>>>(p);
+  } else if (coarse_form(p)) {
+    coarse_emit_kernel<<<static_cast<unsigned>(p.B * kCoarseParts), 256, 0, as_stream(stream)>>>(p);
   } else {
-    emit_kernel<0><<<grid, 256, 0, as_stream(stream)>>>(p);
+    emit_kernel<0><<<emit_grid(p), 256, 0, as_stream(stream)>>>(p);
   }
   MZK_LAUNCH_CHECK("decode_emit");
   return MZK_OK;
+}
+
+}  // namespace
+}  // namespace mzk
+
+using namespace mzk;
+
+extern "C" int mzk_decode_emit(const int64_t* positions, int64_t B, const float* kv, const float* gate,
+                               float* carry_kv, float* carry_gate, int ratio, const void* norm_weight, float eps,
+                               uint8_t* cache, int64_t cache_batch_entries, int64_t cache_cap, const void* wk,
+                               const void* k_norm_weight, float k_eps, int key_format, uint8_t* k_codes,
+                               void* k_scales, int64_t key_batch_entries, const void* rope_table, int64_t table_rows,
+                               void* step_cos, void* step_sin, const void* kv_proj, const void* kv_weight, float kv_eps,
+                               uint8_t* win_cache, int64_t win_batch_entries, int win_cap, const void* q_idx,
+                               int q_format, uint8_t* q_codes, void* q_scales, void* stream) {
+  EmitParams p;
+  const int rc = build_emit(positions, B, kv, gate, carry_kv, carry_gate, ratio, norm_weight, eps, cache,
+                            cache_batch_entries, cache_cap, wk, k_norm_weight, k_eps, key_format, k_codes, k_scales,
+                            key_batch_entries, rope_table, table_rows, step_cos, step_sin, kv_proj, kv_weight, kv_eps,
+                            win_cache, win_batch_entries, win_cap, q_idx, q_format, q_codes, q_scales, p);
+  if (rc || B == 0) return rc;
+  return launch_emit(p, stream);
+}
+
+extern "C" int mzk_decode_emit_pair(const int64_t* positions, int64_t B, const float* kv, const float* gate,
+                                    float* carry_kv, float* carry_gate, int ratio, const void* norm_weight, float eps,
+                                    uint8_t* cache, int64_t cache_batch_entries, int64_t cache_cap, const void* wk,
+                                    const void* k_norm_weight, float k_eps, int key_format, uint8_t* k_codes,
+                                    void* k_scales, int64_t key_batch_entries, const void* rope_table,
+                                    int64_t table_rows, void* step_cos, void* step_sin, const void* kv_proj,
+                                    const void* kv_weight, float kv_eps, uint8_t* win_cache, int64_t win_batch_entries,
+                                    int win_cap, const void* q_idx, int q_format, uint8_t* q_codes, void* q_scales,
+                                    const float* c_kv, const float* c_gate, float* c_carry_kv, float* c_carry_gate,
+                                    int c_ratio, const void* c_norm_weight, float c_eps, uint8_t* c_cache,
+                                    int64_t c_cache_batch_entries, int64_t c_cache_cap, void* stream) {
+  EmitParams pf, pc;
+  int rc = build_emit(positions, B, kv, gate, carry_kv, carry_gate, ratio, norm_weight, eps, cache,
+                      cache_batch_entries, cache_cap, wk, k_norm_weight, k_eps, key_format, k_codes, k_scales,
+                      key_batch_entries, rope_table, table_rows, step_cos, step_sin, kv_proj, kv_weight, kv_eps,
+                      win_cache, win_batch_entries, win_cap, q_idx, q_format, q_codes, q_scales, pf);
+  if (rc) return rc;
+  rc = build_emit(positions, B, c_kv, c_gate, c_carry_kv, c_carry_gate, c_ratio, c_norm_weight, c_eps, c_cache,
+                  c_cache_batch_entries, c_cache_cap, nullptr, nullptr, 0.0f, 0, nullptr, nullptr, 0, rope_table,
+                  table_rows, nullptr, nullptr, nullptr, nullptr, 0.0f, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, pc);
+  if (rc || B == 0) return rc;
+  if (pf.br.ratio == 4 && coarse_form(pc)) {
+    const unsigned nfine = emit_grid(pf);
+    emit_pair_kernel<<<nfine + static_cast<unsigned>(B * kCoarseParts), 256, 0, as_stream(stream)>>>(pf, pc, nfine);
+    MZK_LAUNCH_CHECK("decode_emit_pair");
+    return MZK_OK;
+  }
+  rc = launch_emit(pf, stream);
+  return rc ? rc : launch_emit(pc, stream);
 }

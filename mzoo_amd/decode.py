@@ -261,7 +261,8 @@ class SparseDecodeLayer:
         cg[:, :n] = gate.float()
 
     def _emit(self, compress, rope_from_table: bool, prologue=None) -> None:
-        """The in-step emission launches (one per compressed branch), see the module doc.
+        """The in-step emission launch (both compressed branches in one when there is a coarse
+        branch: ``mzk_decode_emit_pair``), see the module doc.
         ``prologue`` = (kv projection bf16 [B, D], indexer query bf16 [B, 64, Di]): the first
         launch also writes the token's window entry and the quantized indexer query."""
         cfg, cw = self.cfg, self.compressor
@@ -287,23 +288,24 @@ class SparseDecodeLayer:
             qs = self.q_scales if fp8 else self.q_e8m0
             pro = (pkv.data_ptr(), self.kv_norm_weight.data_ptr(), self.kv_norm_eps, self.win.data_ptr(),
                    cfg.window, cfg.window, pq.data_ptr(), 0 if fp8 else 1, self.q_codes.data_ptr(), qs.data_ptr())
-        _lib.call("mzk_decode_emit", self.positions.data_ptr(), b, kv.data_ptr(), gate.data_ptr(),
-                  self.carry_kv.data_ptr(), self.carry_gate.data_ptr(), cfg.ratio, cw.norm_weight.data_ptr(), cw.eps,
-                  self.main.data_ptr(), cfg.max_groups, cfg.max_groups, cw.wk.data_ptr(),
-                  cw.k_norm_weight.data_ptr(), cw.k_eps, 0 if fp8 else 1, keys[0].data_ptr(), keys[1].data_ptr(),
-                  cfg.max_groups, self.rope_table.data_ptr(), self.rope_table.shape[0], *tabs, *pro, st)
-        if cfg.coarse_ratio:
-            if len(compress) != 4:
-                raise ValueError("step(compress=...): the coarse branch needs (kv, gate, coarse_kv, coarse_gate)")
-            ckv, cg = (t.contiguous() for t in compress[2:])
-            for t in (ckv, cg):
-                if t.dtype != torch.float32 or t.shape != (b, cfg.dim):
-                    raise ValueError(f"step(compress=...): fp32 [{b}, {cfg.dim}] projections expected")
-            _lib.call("mzk_decode_emit", self.positions.data_ptr(), b, ckv.data_ptr(), cg.data_ptr(),
-                      self.coarse_carry_kv.data_ptr(), self.coarse_carry_gate.data_ptr(), cfg.coarse_ratio,
-                      cw.coarse_norm_weight.data_ptr(), cw.eps, self.coarse.data_ptr(), cfg.coarse_groups,
-                      cfg.coarse_groups, None, None, 0.0, 0, None, None, 0, self.rope_table.data_ptr(),
-                      self.rope_table.shape[0], None, None, None, None, 0.0, None, 0, 0, None, 0, None, None, st)
+        fine = (self.positions.data_ptr(), b, kv.data_ptr(), gate.data_ptr(),
+                self.carry_kv.data_ptr(), self.carry_gate.data_ptr(), cfg.ratio, cw.norm_weight.data_ptr(), cw.eps,
+                self.main.data_ptr(), cfg.max_groups, cfg.max_groups, cw.wk.data_ptr(),
+                cw.k_norm_weight.data_ptr(), cw.k_eps, 0 if fp8 else 1, keys[0].data_ptr(), keys[1].data_ptr(),
+                cfg.max_groups, self.rope_table.data_ptr(), self.rope_table.shape[0], *tabs, *pro)
+        if not cfg.coarse_ratio:
+            _lib.call("mzk_decode_emit", *fine, st)
+            return
+        if len(compress) != 4:
+            raise ValueError("step(compress=...): the coarse branch needs (kv, gate, coarse_kv, coarse_gate)")
+        ckv, cg = (t.contiguous() for t in compress[2:])
+        for t in (ckv, cg):
+            if t.dtype != torch.float32 or t.shape != (b, cfg.dim):
+                raise ValueError(f"step(compress=...): fp32 [{b}, {cfg.dim}] projections expected")
+        # both compressors in one launch (the coarse branch has no key, prologue or step tables)
+        _lib.call("mzk_decode_emit_pair", *fine, ckv.data_ptr(), cg.data_ptr(), self.coarse_carry_kv.data_ptr(),
+                  self.coarse_carry_gate.data_ptr(), cfg.coarse_ratio, cw.coarse_norm_weight.data_ptr(), cw.eps,
+                  self.coarse.data_ptr(), cfg.coarse_groups, cfg.coarse_groups, st)
 
     def fill_coarse(self, latents: torch.Tensor) -> None:
         """latents [B, n, D] -> coarse entries 0..n-1 of every row."""

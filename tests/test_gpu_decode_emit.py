@@ -263,3 +263,60 @@ def test_emission_kernels_agree(dev, ratio):
     assert not idle.any()
     for r in range(b):
         assert np.array_equal(ckv_idle[r, -2], kv[r])
+
+
+def test_emission_pair_equals_two_launches(dev):
+    """``mzk_decode_emit_pair`` (the fine branch with its index key and step tables, and a
+    keyless coarse branch, in one launch) writes what the two ``mzk_decode_emit`` calls write,
+    bit for bit -- caches, keys, carried slots, step tables -- over steps that complete groups
+    of both branches and steps that only carry."""
+    from mzoo_amd import _lib
+    b, fr, cr, fcap, ccap = 3, 4, 8, 8, 4
+    rng = np.random.default_rng(77)
+    rows = 64
+    tab = _bf(rng.uniform(-1, 1, (rows, 64)).astype(np.float32))
+    nw = _bf(rng.uniform(0.5, 1.5, D).astype(np.float32))
+    cnw = _bf(rng.uniform(0.5, 1.5, D).astype(np.float32))
+    wk = _bf(rng.normal(0, 0.05, (DI, D)).astype(np.float32))
+    kw = _bf(rng.uniform(0.5, 1.5, DI).astype(np.float32))
+    bf16 = lambda a: torch.from_numpy(np.ascontiguousarray(a)).bfloat16().to(dev)  # noqa: E731
+    dv = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731  (keeps the dtype)
+    tab_d, nw_d, cnw_d, wk_d, kw_d = bf16(tab), bf16(nw), bf16(cnw), bf16(wk), bf16(kw)
+
+    def state():
+        return dict(fkv=torch.zeros(b, fr, D, device=dev), fgt=torch.zeros(b, fr, D, device=dev),
+                    ckv=torch.zeros(b, cr, D, device=dev), cgt=torch.zeros(b, cr, D, device=dev),
+                    main=torch.zeros(b, fcap, 656, dtype=torch.uint8, device=dev),
+                    coarse=torch.zeros(b, ccap, 656, dtype=torch.uint8, device=dev),
+                    kc=torch.zeros(b, fcap, DI, dtype=torch.uint8, device=dev),
+                    ks=torch.zeros(b, fcap, dtype=torch.float32, device=dev),
+                    scos=torch.zeros(b, 32, dtype=torch.bfloat16, device=dev),
+                    ssin=torch.zeros(b, 32, dtype=torch.bfloat16, device=dev))
+
+    pair, two = state(), state()
+    start = np.array([0, 5, 13], dtype=np.int64)
+    for step in range(3 * cr):
+        print(f"emission pair: step {step}", flush=True)
+        pos_d = dv(start + step)
+        kv, gt = dv(rng.normal(0, 1, (b, D)).astype(np.float32)), dv(rng.normal(0, 2, (b, D)).astype(np.float32))
+        ckv, cgt = dv(rng.normal(0, 1, (b, D)).astype(np.float32)), dv(rng.normal(0, 2, (b, D)).astype(np.float32))
+        st = _lib.stream_of(pos_d)
+        for s, paired in ((pair, True), (two, False)):
+            fine = (pos_d.data_ptr(), b, kv.data_ptr(), gt.data_ptr(), s["fkv"].data_ptr(), s["fgt"].data_ptr(), fr,
+                    nw_d.data_ptr(), 1e-6, s["main"].data_ptr(), fcap, fcap, wk_d.data_ptr(), kw_d.data_ptr(), 1e-6, 0,
+                    s["kc"].data_ptr(), s["ks"].data_ptr(), fcap, tab_d.data_ptr(), rows, s["scos"].data_ptr(),
+                    s["ssin"].data_ptr(), None, None, 0.0, None, 0, 0, None, 0, None, None)
+            coarse = (ckv.data_ptr(), cgt.data_ptr(), s["ckv"].data_ptr(), s["cgt"].data_ptr(), cr, cnw_d.data_ptr(),
+                      1e-6, s["coarse"].data_ptr(), ccap, ccap)
+            if paired:
+                _lib.call("mzk_decode_emit_pair", *fine, *coarse, st)
+            else:
+                _lib.call("mzk_decode_emit", *fine, st)
+                _lib.call("mzk_decode_emit", pos_d.data_ptr(), b, *coarse[:6], coarse[6], *coarse[7:], None, None,
+                          0.0, 0, None, None, 0, tab_d.data_ptr(), rows, None, None, None, None, 0.0, None, 0, 0,
+                          None, 0, None, None, st)
+        torch.cuda.synchronize()
+        for name in pair:
+            assert torch.equal(pair[name], two[name]), f"step {step}: {name} differs"
+    # groups of both branches were written
+    assert pair["main"].any() and pair["coarse"].any() and pair["kc"].any()
