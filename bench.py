@@ -20,7 +20,12 @@ without emission, as the kernels' reference signatures do).  Distinct layers kee
 B x layers / replay time (token-rows through one attention layer per second); ms_per_step
 is per layer.  Inputs are synthetic and resident in HBM before timing starts.
 
---config 4 / 5 run the MXFP4-index decode (B=8, 32768 groups) and the hierarchical decode
+--config 1 times the module drop-in (``mzoo_amd.owlet1.DeepseekV41Attention``) at BASELINE
+config 1 -- one layer's forward over B=1, S=1024 (8 heads over 128+32, indexer 4x64, ratio 4,
+top-128, window 64, fp32 weights ~N(0, 0.02), seed 0), value = tokens/s -- beside the CPU
+oracle's module forward, and one module decode step at config-2 dimensions (B=32, context
+32768, 128 heads over 512+64, indexer 64x128, top-2048, window 128, bf16) through the module's
+cache layer.  --config 4 / 5 run the MXFP4-index decode (B=8, 32768 groups) and the hierarchical decode
 (B=4: dense coarse branch of 4096 entries + MXFP4 fine index over 131072 groups) the same
 way; --config 3 times the causal prefill (B=1, S=8192: FP8 indexer over 2048 groups ->
 top-2048 -> sparse MQA with window 128 on every query row), value = query tokens/s.
@@ -70,7 +75,7 @@ DECODE = {
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5], help="BASELINE configuration")
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5], help="BASELINE configuration")
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--nsplit", type=int, default=0, help="attention splits per row (0: the config's default)")
@@ -770,6 +775,208 @@ def run_reindex(torch, dev, args):
             "cases": out}
 
 
+# ---- the module path (and a module decode step at config-2 dimensions) ----
+
+MODULE_C1 = dict(hidden_size=512, num_attention_heads=8, head_dim=160, qk_rope_head_dim=32, q_lora_rank=256,
+                 o_groups=2, o_lora_rank=128, index_n_heads=4, index_head_dim=64, index_topk=128, compress_ratio=4,
+                 sliding_window=64, seq=1024, batch=1, seed=0)
+# config-2 dimensions for the attention; hidden / low-rank sizes are not named by the config
+MODULE_C2 = dict(hidden_size=4096, num_attention_heads=128, head_dim=576, qk_rope_head_dim=64, q_lora_rank=1536,
+                 o_groups=16, o_lora_rank=1024, index_n_heads=64, index_head_dim=128, index_topk=2048,
+                 compress_ratio=4, sliding_window=128, ctx=32768, batch=32, seed=6)
+
+
+def module_param_shapes(c):
+    """name -> shape of the parameters of DeepseekV41Attention for a KV + index source
+    layer (owlet1/attention.py:106-127, cache.py:134-140, indexer.py:63-76)."""
+    h, d, hid, ql = c["num_attention_heads"], c["head_dim"], c["hidden_size"], c["q_lora_rank"]
+    hi, di, og, orank = c["index_n_heads"], c["index_head_dim"], c["o_groups"], c["o_lora_rank"]
+    return {"wq_a.weight": (ql, hid), "q_norm.weight": (ql,), "wq_b.weight": (h * d, ql), "wkv.weight": (d, hid),
+            "kv_norm.weight": (d,), "wo_a.weight": (og * orank, h * d // og), "wo_b.weight": (hid, og * orank),
+            "attn_sink": (h,), "compressor.wkv.weight": (d, hid), "compressor.wgate.weight": (d, hid),
+            "compressor.norm.weight": (d,), "indexer.wq_b.weight": (hi * di, ql),
+            "indexer.weights_proj.weight": (hi, hid), "indexer.wk.weight": (di, d), "indexer.k_norm.weight": (di,)}
+
+
+def module_layer(torch, dev, c, dtype):
+    """(DeepseekV41Attention on `dev` in `dtype`, its fp32 parameters on the CPU): every
+    weight and the sink ~N(0, 0.02), norm weights 1 (BASELINE config 1's initialisation)."""
+    from mzoo_amd import owlet1 as MO
+    cfg = MO.AttentionConfig(
+        hidden_size=c["hidden_size"], num_attention_heads=c["num_attention_heads"], head_dim=c["head_dim"],
+        qk_rope_head_dim=c["qk_rope_head_dim"], q_lora_rank=c["q_lora_rank"], o_groups=c["o_groups"],
+        o_lora_rank=c["o_lora_rank"], rope_theta=ROPE_THETA, compress_rope_theta=COMPRESS_ROPE_THETA,
+        sliding_window=c["sliding_window"], compress_ratios=[c["compress_ratio"]], kv_source_layer_ids=[0],
+        index_source_layer_ids=[0], candidate_source_layer_id=-1, index_n_heads=c["index_n_heads"],
+        index_head_dim=c["index_head_dim"], index_topk=c["index_topk"], rms_norm_eps=1e-20)
+    gen = torch.Generator(device=dev).manual_seed(c["seed"])
+    params = {}
+    for name, shape in sorted(module_param_shapes(c).items()):
+        params[name] = (torch.ones(shape, device=dev) if name.endswith("norm.weight")
+                        else torch.randn(shape, generator=gen, device=dev) * 0.02)
+    mod = MO.DeepseekV41Attention(cfg, 0)
+    mod.load_state_dict({k: v.cpu() for k, v in params.items()}, strict=True)
+    return mod.to(device=dev, dtype=dtype).eval(), params, gen
+
+
+def module_decode_step(torch, dev, steps, warmup):
+    """One module decode step at config-2 dimensions: DeepseekV41Attention.forward on one
+    new token per row of B=32 through DeepseekV41CSACache holding a context of 32767 tokens
+    (8191 compressed groups + the carried partial group, the last 127 window entries, the
+    MXFP4-packed keys), bf16 model, no mask; the steps advance to position 32767."""
+    from transformers.cache_utils import Cache
+
+    from mzoo_amd import owlet1 as MO
+    from mzoo_amd import quant
+    c = MODULE_C2
+    mod, _, gen = module_layer(torch, dev, c, torch.bfloat16)
+    cfg = mod.config
+    b, d, di, r, w = c["batch"], c["head_dim"], c["index_head_dim"], c["compress_ratio"], c["sliding_window"]
+    start = c["ctx"] - 1 - warmup - steps
+    cache = Cache(layers=[MO.DeepseekV41CSACache(cfg)])
+    layer = cache.layers[0]
+    rnd = lambda *shape: torch.randn(*shape, generator=gen, device=dev)  # noqa: E731
+    win = rnd(b, 1, w - 1, d).bfloat16()
+    layer.update(win, win)
+    layer.cumulative_length = start
+    g0 = start // r
+    layer._store["compressor"].append(rnd(b, g0, d).bfloat16())   # a bf16 model's cache is read in place
+    keys = rnd(b, g0, di).bfloat16()
+    layer._store["indexer"].append(keys)
+    layer.append_packed_index_k(*quant.quant_mxfp4(keys))
+    layer.entry_count["compressor"] = g0
+    layer.buffer_kv["compressor"] = rnd(b, start - g0 * r, d)
+    layer.buffer_gate["compressor"] = rnd(b, start - g0 * r, d)
+    rot = MO.DeepseekV41RotaryEmbedding(cfg).to(dev)
+    xs = [rnd(b, 1, c["hidden_size"]).bfloat16() for _ in range(4)]
+
+    def one(i):
+        pos = torch.full((b, 1), start + i, dtype=torch.int64, device=dev)
+        x = xs[i % len(xs)]
+        pe = {"main": rot(x, pos, "main"), "compress": rot(x, pos, "compress")}
+        with torch.no_grad():
+            return mod(x, position_embeddings=pe, attention_mask=None, past_key_values=cache,
+                       shared=MO.SharedState(), position_ids=pos)[0]
+
+    for i in range(warmup):
+        one(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(warmup, warmup + steps):
+        one(i)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    weight_bytes = sum(p.numel() * p.element_size() for p in mod.parameters())
+    return {"ms_per_step": ms, "tokens_per_s": b / (ms * 1e-3), "batch": b, "context": c["ctx"],
+            "steps": steps, "weight_bytes": weight_bytes,
+            "workload": "DeepseekV41Attention.forward, one token per row, B=32 at context 32768 (positions "
+                        f"{start + warmup}..{start + warmup + steps - 1}), 128 heads x (512+64), indexer 64x128 "
+                        "MXFP4 over 8191-8192 groups, top-2048, window 128, bf16 weights (hidden 4096, q rank 1536, "
+                        "16 output groups of rank 1024), eager launches, no mask",
+            "note": "includes the projections (the weights are read once per step) and the host's launch "
+                    "overhead of the eager module; the graph-captured kernel step is the --config 2 line"}
+
+
+def run_module(torch, dev, args):
+    """the module drop-in's layer forward (no cache) over B=1, S=1024."""
+    from mzoo_amd import owlet1 as MO
+    c = MODULE_C1
+    mod, params, gen = module_layer(torch, dev, c, torch.float32)
+    b, s = c["batch"], c["seq"]
+    x = torch.randn(b, s, c["hidden_size"], generator=gen, device=dev)
+    pos = torch.arange(s, device=dev).unsqueeze(0).expand(b, -1).contiguous()
+    rot = MO.DeepseekV41RotaryEmbedding(mod.config).to(dev)
+    w = c["sliding_window"]
+    kk = torch.arange(s, device=dev)
+    band = (kk[None, :] <= kk[:, None]) & (kk[None, :] > kk[:, None] - w)
+    mask = torch.zeros(b, 1, s, s, device=dev).masked_fill_(~band, torch.finfo(torch.float32).min)
+
+    def fwd(m=None):
+        pe = {"main": rot(x, pos, "main"), "compress": rot(x, pos, "compress")}
+        with torch.no_grad():
+            return mod(x, position_embeddings=pe, attention_mask=m, past_key_values=None, shared=MO.SharedState(),
+                       position_ids=pos)[0]
+
+    def timed(m, n):
+        for _ in range(3):
+            fwd(m)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fwd(m)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n * 1e3
+
+    steps = max(5, min(args.steps, 50))
+    ms = timed(None, steps)
+    ms_mask = timed(mask, steps)
+
+    # the attention kernel alone (its inputs at the layer's shapes), back-to-back launches
+    from mzoo_amd import indexer as IDX
+    h, d, k, r = c["num_attention_heads"], c["head_dim"], c["index_topk"], c["compress_ratio"]
+    g = s // r
+    q = torch.randn(b, s, h, d, generator=gen, device=dev).bfloat16()
+    full = torch.randn(b, s, d, generator=gen, device=dev).bfloat16()
+    comp = torch.randn(b, g, d, generator=gen, device=dev).bfloat16()
+    sc = torch.randn(b, s, g, generator=gen, device=dev)
+    sc = sc.masked_fill(torch.arange(g, device=dev)[None, None, :] >= (pos[..., None] + 1) // r, float("-inf"))
+    idx = IDX.topk(sc, k)
+    sinks = torch.randn(h, generator=gen, device=dev)
+    rel = pos.reshape(-1)
+    t_attn = graph_time(torch, [lambda: MO._sparse_attend(q, sinks, window=(full, rel, w), parts=[(comp, idx)])],
+                        64)
+    t = torch.arange(s, dtype=torch.float64)
+    pairs = float((torch.clamp(t + 1, max=w) + torch.clamp((t + 1) // r, max=k)).sum())
+    attn_flops = 4.0 * d * h * pairs
+    attn_bytes = 2.0 * s * h * d * 2 + (s + g) * d * 2 + s * k * 4
+    roof = roofline(None, attn_flops, attn_bytes, t_attn)
+    roof.update({"traffic": None, "kernel": "sparse_mqa (D=160, 8 heads)", "kernel_us": t_attn})
+
+    cpu = None
+    if not args.no_cpu:
+        from oracle import model as OM
+        torch.set_num_threads(os.cpu_count() or 1)
+        cp = {k_: v.float().cpu() for k_, v in params.items()}
+        ocfg = dict(c, rms_norm_eps=1e-20, compress_rope_theta=COMPRESS_ROPE_THETA)
+        xc, pc = x.cpu(), pos.cpu()
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < 5 and (time.perf_counter() - t_start < args.cpu_seconds or len(times) < 2):
+            t0 = time.perf_counter()
+            OM.layer_forward(cp, ocfg, xc, pc)
+            times.append(time.perf_counter() - t0)
+        times.sort()
+        med = times[len(times) // 2]
+        cpu = {"value": s / med, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"the whole config-1 layer forward (B=1, S=1024; the oracle's module composition in fp32), "
+                         f"median of {len(times)} runs"}
+    dec = module_decode_step(torch, dev, steps=max(5, min(args.steps, 20)), warmup=3)
+    return {
+        "metric": METRIC,
+        "value": s * b / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": 3,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32 weights and projections; bf16 attention (MFMA), FP8 / FP4 fake-quantized caches",
+        "data": "synthetic (seed 0): weights ~N(0, 0.02), norm weights 1, hidden states ~N(0, 1), on the GPU",
+        "config": {"workload": "config1: DeepseekV41Attention.forward (mzoo_amd drop-in) over B=1 S=1024, 8 heads x "
+                               "(128+32) latent, indexer 4x64 MXFP4, ratio 4, top-128, window 64, sink, no cache, "
+                               "eager launches",
+                   "batch": b, "seq_len": s, "heads": h, "topk": k, "window": w,
+                   "step": "one layer forward without a mask (the window in token order); "
+                           "ms_with_mask: with the model's sliding causal mask"},
+        "ms_with_mask": ms_mask,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "module_decode_c2": dec,
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -793,7 +1000,12 @@ def main():
     if args.reindex:
         print(json.dumps(run_reindex(torch, dev, args)))
         return
-    out = run_prefill(torch, dev, args) if args.config == 3 else run_decode(torch, dev, args)
+    if args.config == 1:
+        out = run_module(torch, dev, args)
+    elif args.config == 3:
+        out = run_prefill(torch, dev, args)
+    else:
+        out = run_decode(torch, dev, args)
     print(json.dumps(out))
 
 

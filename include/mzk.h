@@ -125,9 +125,11 @@ int mzk_decode_prologue(const void* kv, int kv_dtype, int64_t B, int nope, int r
  *            k_scales fp32), 1 MXFP4 (k_codes [.., 64] e2m1 + k_scales e8m0 [.., 4]).
  * rope_table: bf16 [table_rows, 64], row p = cos (32) | sin (32) of position p (the compress
  * RoPE).  step_cos / step_sin (bf16 [B, 32], or NULL): receive row pos of the table -- the
- * token's RoPE for the step's later launches.  Rows with pos < 0 do nothing.
- * The step's prologue (kv_proj non-NULL; skipped for rows with pos >= table_rows), at the
- * token's RoPE (row pos of the table):
+ * token's RoPE for the step's later launches.  Rows with pos < 0 do nothing.  Limit: every
+ * position must be below table_rows -- a row at pos >= table_rows gets no step tables and no
+ * prologue (its step_cos / step_sin, window slot and quantized query keep their previous
+ * contents, with no error); SparseDecodeLayer refuses such positions on the host.
+ * The step's prologue (kv_proj non-NULL), at the token's RoPE (row pos of the table):
  *   kv_proj bf16 [B, 576] (the wkv projection) -> RoPE(kv_norm(kv_proj)) (kv_weight bf16 [576],
  *            kv_eps; the pinned order of mzk_rms_norm) packed FP8-b128 into window-ring slot
  *            b*win_batch_entries + pos % win_cap (owlet1/attention.py:149-154), as

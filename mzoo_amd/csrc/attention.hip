@@ -1604,6 +1604,9 @@ extern "C" int mzk_sparse_mqa_noalloc(const void* q, int64_t B, int64_t S, int H
                                       const float* sinks, int nsplit, void* out, float* lse, const void* rope_cos,
                                       const void* rope_sin, int rope_dim, void* stream) {
   MZK_CHECK_ARG(B >= 0 && S >= 0 && H >= 1 && D > 0 && nsplit >= 1, "sparse_mqa_noalloc: bad sizes");
+  MZK_CHECK_ARG(B == 0 || S <= 0x7fffffff / B, "sparse_mqa_noalloc: too many rows");
+  // the partials stay in the private scratch array: only the merged output is observable
+  MZK_CHECK_ARG(out != nullptr && lse != nullptr, "sparse_mqa_noalloc: out and lse are required");
   const int64_t need = nsplit > 1 ? B * S * nsplit * static_cast<int64_t>(H) * (2 * D + 8) : 0;
   MZK_CHECK_ARG(need <= kScratchBytes,
                 "sparse_mqa_noalloc: %lld rows x %d splits x %d heads need %lld bytes of split partials, above the "

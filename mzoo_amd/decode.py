@@ -183,6 +183,9 @@ class SparseDecodeLayer:
             self.q_e8m0 = torch.empty(b, 1, hi, di // 32, **u8)
         self._graph = None
         self._static = None
+        self._graph_advances = False
+        self.rope_table = None
+        self._pos_max = None  # host copy of the largest row position (None: not set from the host)
         self.compressor = None
         if compressor is not None:
             self._init_emission(compressor, max_position)
@@ -221,7 +224,18 @@ class SparseDecodeLayer:
 
     # ---- state ---------------------------------------------------------------------------
     def set_positions(self, pos) -> None:
-        self.positions.copy_(torch.as_tensor(pos, dtype=torch.int64).expand(self.cfg.batch))
+        p = torch.as_tensor(pos, dtype=torch.int64)
+        self._pos_max = int(p.max())
+        self._check_table()
+        self.positions.copy_(p.to(self.device).expand(self.cfg.batch))
+
+    def _check_table(self) -> None:
+        """The emission reads the token's RoPE tables from row `pos` of the position table
+        and skips rows beyond it (their window entry and quantized query would keep the
+        previous step's contents): refuse a step at a position the table does not hold."""
+        if self.rope_table is not None and self._pos_max is not None and self._pos_max >= self.rope_table.shape[0]:
+            raise ValueError(f"SparseDecodeLayer: position {self._pos_max} is beyond the RoPE position table "
+                             f"({self.rope_table.shape[0]} rows; raise max_position)")
 
     def fill_window(self, latents: torch.Tensor, last_position: int) -> None:
         """latents [B, W, D] for tokens last_position-W+1 .. last_position."""
@@ -325,6 +339,14 @@ class SparseDecodeLayer:
         takes the four tables from the device table at the rows' positions (needs the
         layer's ``CompressorWeights``).  ``compress`` = (kv, gate[, coarse_kv, coarse_gate]):
         the token's fp32 compressor projections [B, D], emitted into the caches in the step."""
+        if compress is not None or rope == "table":
+            self._check_table()
+        out = self._step(q, kv, q_idx, w, advance, rope, compress)
+        if advance and self._pos_max is not None:
+            self._pos_max += 1
+        return out
+
+    def _step(self, q, kv, q_idx, w, advance, rope, compress):
         cfg = self.cfg
         b = cfg.batch
         fp8 = cfg.index_format == "fp8"
@@ -483,6 +505,7 @@ class SparseDecodeLayer:
         s = torch.cuda.Stream(device=self.device)
         s.wait_stream(torch.cuda.current_stream(self.device))
         saved = self.positions.clone()
+        saved_max = self._pos_max
         with torch.cuda.stream(s):
             for _ in range(warmup):
                 run(False)
@@ -491,7 +514,9 @@ class SparseDecodeLayer:
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             run(advance)
+        self._pos_max = saved_max  # recording ran nothing
         self._graph = g
+        self._graph_advances = advance
         return g
 
     @property
@@ -499,5 +524,9 @@ class SparseDecodeLayer:
         return self._static
 
     def replay(self) -> torch.Tensor:
+        if self._graph_advances:
+            self._check_table()
         self._graph.replay()
+        if self._graph_advances and self._pos_max is not None:
+            self._pos_max += 1
         return self.out

@@ -230,6 +230,7 @@ def _topk_bias(idx: torch.Tensor, groups: int) -> torch.Tensor:
 
 def _publish_selection(shared: dict, idx: torch.Tensor, groups: int) -> None:
     shared["topk_idx"] = idx
+    shared["_topk_groups"] = groups
     if isinstance(shared, SharedState):
         dict.pop(shared, "topk_bias", None)
         dict.__setitem__(shared, "_topk_bias_src", (idx, groups))
@@ -302,11 +303,21 @@ class DeepseekV41CSACache(DynamicSlidingWindowLayer):
         self.buffer_gate: dict = {"compressor": None}
         self._store = {"compressor": _Growing(), "indexer": _Growing()}
         self._packed = (_Growing(), _Growing())
+        self._mirror = _Growing()  # bf16 copy of the compressed latents (a non-bf16 model)
         self.entry_count: dict = {"compressor": 0}
 
     @property
     def compressed_kv(self) -> dict:
         return {k: (None if g.buf is None else g.view().unsqueeze(1)) for k, g in self._store.items()}
+
+    def compressed_bf16(self):
+        """[B, G, D] bf16 view of the compressed latents, the attention kernel's entry
+        format: the running cache itself for a bf16 model, else its bf16 mirror, appended as
+        groups are emitted (the fake-quantized latents are exact in bf16)."""
+        st = self._store["compressor"]
+        if st.buf is None:
+            return None
+        return st.view() if st.buf.dtype == torch.bfloat16 else self._mirror.view()
 
     def packed_index_k(self):
         """(e2m1 codes [B, G, Di/2], e8m0 [B, G, Di/32]) of the indexer keys, or None."""
@@ -314,7 +325,7 @@ class DeepseekV41CSACache(DynamicSlidingWindowLayer):
         return None if p.buf is None else (p.view(), e.view())
 
     def _reindex(self, fn):
-        for g in (*self._store.values(), *self._packed):
+        for g in (*self._store.values(), *self._packed, self._mirror):
             g.reindex(fn)
         for attr in ("buffer_kv", "buffer_gate"):
             buf = getattr(self, attr)
@@ -363,6 +374,8 @@ class DeepseekV41CSACache(DynamicSlidingWindowLayer):
         """Append entries [B, 1, n, D] to the running cache ``name``; returns it [B, 1, G, D]."""
         if compressed.shape[2] > 0 or self._store[name].buf is None:
             self._store[name].append(compressed[:, 0])
+            if name == "compressor" and compressed.dtype != torch.bfloat16:
+                self._mirror.append(compressed[:, 0].to(torch.bfloat16))
         if name == "compressor":
             self.entry_count[name] += compressed.shape[2]
         return self._store[name].view().unsqueeze(1)
@@ -520,41 +533,119 @@ class DeepseekV41Indexer(nn.Module):
 
 # ---- attention ----------------------------------------------------------------------------
 
-def _window_ring(full: torch.Tensor, first_pos: int, window: int) -> torch.Tensor:
-    """[B, T, D] entries for positions first_pos .. first_pos+T-1 -> a bf16 ring of capacity
-    max(T, window) holding position p at slot p % capacity (the layout the kernel's window
-    source reads; a row's window never reaches before first_pos: either the cache kept the
-    window's earlier tokens or the sequence starts at 0)."""
-    b, t, d = full.shape
-    cap = max(t, window)
-    slots = (first_pos + torch.arange(t, device=full.device)) % cap
-    ring = torch.zeros(b, cap, d, dtype=torch.bfloat16, device=full.device)
-    ring[:, slots] = full.to(torch.bfloat16)
-    return ring
+# keys of `shared` that belong to one group: a KV-source layer without a cache drops them
+# before it opens its group, so a later group (possibly at another ratio) does not append to
+# an earlier group's entries (archs/dsv4/modeling_deepseek_v41.py:722-732; the owlet1 module
+# lacks the reset, archs/owlet1/GAPS.md item 2)
+_GROUP_KEYS = ("compress_kv", "index_k", "index_k_packed", "topk_bias", "_topk_bias_src", "topk_idx",
+               "_topk_groups", "candidates", "_compress_kv_bf16")
 
 
-def _sparse_attend(q: torch.Tensor, positions: torch.Tensor, ring: torch.Tensor | None, window: int,
-                   compressed: torch.Tensor | None, idx: torch.Tensor | None, sinks: torch.Tensor) -> torch.Tensor:
-    """q [B, S, H, D] (any float dtype) over the window ring and the selected compressed
-    entries -> bf16 [B, S, H, D] (``mzk_sparse_mqa``, bf16 entries)."""
+def _entries(x: torch.Tensor) -> tuple[torch.Tensor, int]:
+    """[B, T, D] entries -> (bf16 [B, >= T, D] rows read in place when possible, entries
+    between batches)."""
+    d = x.shape[-1]
+    if x.dtype == torch.bfloat16 and x.stride(-1) == 1 and x.stride(1) == d and x.stride(0) % d == 0 \
+            and x.data_ptr() % 16 == 0:
+        return x, x.stride(0) // d
+    y = x.to(torch.bfloat16).contiguous()
+    return y, y.shape[1]
+
+
+def _compressed_bf16(shared: dict):
+    """The group's compressed latents as bf16 [B, G, D] (converted once per forward, or the
+    cache layer's persistent mirror its KV source published)."""
+    src = shared.get("compress_kv")
+    if src is None or src.shape[2] == 0:
+        return None
+    hit = shared.get("_compress_kv_bf16")
+    if hit is not None and hit[0] is src:
+        return hit[1]
+    bf = src[:, 0].to(torch.bfloat16).contiguous()
+    shared["_compress_kv_bf16"] = (src, bf)
+    return bf
+
+
+def _nsplit(rows: int) -> int:
+    return 1 if rows >= 128 else max(1, min(16, 256 // max(rows, 1)))
+
+
+def _sparse_attend(q: torch.Tensor, sinks: torch.Tensor, *, window=None, parts=()) -> torch.Tensor:
+    """q [B, S, H, D] (any float dtype) -> bf16 [B, S, H, D] on ``mzk_sparse_mqa``, one softmax
+    (with the sink) over every source:
+
+    * ``window = (entries [B, T, D], rel_pos int64 [B*S], W)``: row r sees entries
+      rel_pos[r]-W+1 .. rel_pos[r] of its batch (the kernel's linear window source);
+    * ``parts = [(entries [B, T, D], idx int32 [B*S, k]), ...]``: row r sees entries
+      idx[r, :] (-1 = none) -- at most one part beside a window; two parts without a window
+      run as two partial launches into one workspace and one merge."""
     b, s, h, d = q.shape
     qb = q.to(torch.bfloat16).contiguous()
     out = torch.empty(b, s, h, d, dtype=torch.bfloat16, device=q.device)
     lse = torch.empty(b, h, s, dtype=torch.float32, device=q.device)
     rows = b * s
-    nsplit = 1 if rows >= 128 else max(1, min(16, 256 // max(rows, 1)))
-    ws = csa2_attn.new_workspace(rows, h, d, nsplit, q.device) if nsplit > 1 else None
-    has_main = compressed is not None and idx is not None and idx.shape[-1] > 0 and compressed.shape[1] > 0
-    main = compressed.to(torch.bfloat16).contiguous() if has_main else None
-    ic = idx.to(torch.int32).contiguous() if has_main else None
-    topk = ic.shape[-1] if has_main else 0
-    g = main.shape[1] if has_main else 0
-    t = 0 if ring is None else ring.shape[1]
-    _lib.call("mzk_sparse_mqa", qb.data_ptr(), b, s, h, d, _FMT_BF16, d, positions.data_ptr(), _lib.ptr(ring), t, t,
-              window if ring is not None else 0, None, 0, 0, 1, _lib.ptr(main), g, g, _lib.ptr(ic), topk, topk,
-              sinks.data_ptr(), nsplit, _lib.ptr(ws), 0 if ws is None else ws.numel() * ws.element_size(),
-              out.data_ptr(), lse.data_ptr(), _lib.stream_of(q))
+    dev = q.device
+    parts = [(e, i) for e, i in parts if e is not None and i is not None and i.shape[-1] > 0 and e.shape[1] > 0]
+    if window is not None:
+        win, win_stride = _entries(window[0])
+        pos, w = window[1], window[2]
+    else:
+        win, win_stride, w = None, 0, 0
+        pos = torch.full((rows,), -1, dtype=torch.int64, device=dev)
+    if window is not None and len(parts) > 1:
+        raise ValueError("sparse attention: at most one indexed source beside the window")
+    prepared = []
+    for e, i in parts:
+        e2, est = _entries(e)
+        ic = i.reshape(rows, -1).to(torch.int32).contiguous()
+        prepared.append((e2, est, e.shape[1], ic))
+    if window is None and not prepared:
+        out.zero_()                                   # nothing visible: the sink takes all mass
+        return out
+    if len(prepared) <= 1:
+        ns = _nsplit(rows)
+        ws = csa2_attn.new_workspace(rows, h, d, ns, dev) if ns > 1 else None
+        e2, est, g, ic = prepared[0] if prepared else (None, 0, 0, None)
+        k = 0 if ic is None else ic.shape[1]
+        _lib.call("mzk_sparse_mqa", qb.data_ptr(), b, s, h, d, _FMT_BF16, d, pos.data_ptr(), _lib.ptr(win), win_stride,
+                  0, w, None, 0, 0, 1, _lib.ptr(e2), est, g, _lib.ptr(ic), k, k, sinks.data_ptr(), ns, _lib.ptr(ws),
+                  0 if ws is None else ws.numel() * ws.element_size(), out.data_ptr(), lse.data_ptr(),
+                  _lib.stream_of(q))
+        return out
+    ns = max(1, _nsplit(rows) // len(prepared))
+    total = ns * len(prepared)
+    ws = csa2_attn.new_workspace(rows, h, d, total, dev)
+    for j, (e2, est, g, ic) in enumerate(prepared):
+        k = ic.shape[1]
+        _lib.call("mzk_sparse_mqa_part", qb.data_ptr(), b, s, h, d, _FMT_BF16, d, pos.data_ptr(), None, 0, 0, 0, None, 0,
+                  0, 1, e2.data_ptr(), est, g, ic.data_ptr(), k, k, ns, j * ns, total, ws.data_ptr(),
+                  ws.numel() * ws.element_size(), None, None, 0, _lib.stream_of(q))
+    _lib.call("mzk_sparse_mqa_combine", ws.data_ptr(), b, s, h, d, total, sinks.data_ptr(), out.data_ptr(),
+              lse.data_ptr(), _lib.stream_of(q))
     return out
+
+
+def _window_lists(shared: dict, attention_mask: torch.Tensor, b: int, s: int, t: int, window: int) -> torch.Tensor:
+    """The visible window columns of the model's mask [B or 1, 1, S, >= T] as int32 index
+    lists [B*S, cap] (ascending, -1 after).  The layers of a forward receive the same mask
+    and the same window length, so the lists are built once per forward."""
+    hit = shared.get("_window_lists")
+    if hit is not None and hit[0] is attention_mask and hit[1] == t:
+        return hit[2]
+    m = attention_mask
+    if m.dim() != 4 or m.shape[-2] != s or m.shape[-1] != t:
+        raise ValueError(f"DeepseekV41Attention: attention_mask {tuple(m.shape)} does not cover the {s} queries "
+                         f"x {t} window entries of this call")
+    if m.dtype == torch.bool:
+        m = torch.zeros(m.shape, dtype=torch.float32, device=m.device).masked_fill_(~m, float("-inf"))
+    m = m.expand(b, 1, s, t).reshape(b * s, t)
+    cap = min(t, window)
+    try:
+        lists = _mask_to_indices(m, cap)
+    except ValueError:                                # more than `window` visible: not a sliding mask
+        lists = _mask_to_indices(m, t)
+    shared["_window_lists"] = (attention_mask, t, lists)
+    return lists
 
 
 class DeepseekV41Attention(nn.Module):
@@ -592,6 +683,14 @@ class DeepseekV41Attention(nn.Module):
         self.compress_rotary = DeepseekV41RotaryEmbedding(config) if self.is_kv_source else None
 
     def forward(self, hidden_states, position_embeddings, attention_mask, past_key_values, shared, **kwargs):
+        """attention.py:129-236.  The window is what the model's mask keeps of this call's
+        window entries (the cached ``sliding_window - 1`` and the new ones): a 4-D additive
+        (0 / -inf / the dtype's lowest value) or bool mask is turned into index lists, so
+        padding and any other 0 / -inf pattern are honoured exactly; other mask values raise
+        NotImplementedError.  Without a mask (an attention implementation that builds none)
+        row t sees the ``sliding_window`` entries ending at itself in token order.  The
+        compressed branch attends the entries the group's indexer selected, or none when no
+        index source ran in this forward (attention.py:202-214)."""
         if self.training and self.attention_dropout > 0:
             raise NotImplementedError("DeepseekV41Attention (mzoo_amd): inference only, no attention dropout")
         position_ids = kwargs["position_ids"]
@@ -605,13 +704,15 @@ class DeepseekV41Attention(nn.Module):
         kv = _fake_fp8(apply_rotary_pos_emb(kv, cos, sin), 32)                # attention.py:149-154
         if past_key_values is not None:
             full = past_key_values.update(kv.unsqueeze(1), kv.unsqueeze(1), self.layer_idx)[0][:, 0]
-            first_pos = past_key_values.layers[self.layer_idx].cumulative_length - full.shape[1]
         else:
-            full, first_pos = kv, 0
+            full = kv
 
         idx = comp = None
         if self.compress_ratio:
             cache_layer = past_key_values.layers[self.layer_idx] if past_key_values is not None else None
+            if self.is_kv_source and cache_layer is None:
+                for key in _GROUP_KEYS:
+                    shared.pop(key, None)
             latent, first_group_position = (None, 0)
             if self.is_kv_source:
                 latent, first_group_position = self.compressor(hidden_states, cache_layer)
@@ -630,22 +731,36 @@ class DeepseekV41Attention(nn.Module):
                     prev = shared.get("compress_kv")
                     shared["compress_kv"] = rotated if prev is None else torch.cat([prev, rotated], dim=2)
             if self.is_kv_source and cache_layer is not None:
-                shared["compress_kv"] = cache_layer.compressed_kv["compressor"]
-            comp = shared.get("compress_kv")
-            if comp is not None and comp.shape[2]:
-                idx = shared.get("topk_idx") if "topk_idx" in shared else None
-                if idx is None and shared.get("topk_bias") is not None:      # a reference indexer published
+                running = cache_layer.compressed_kv["compressor"]
+                shared["compress_kv"] = running
+                if hasattr(cache_layer, "compressed_bf16") and running is not None and running.shape[2]:
+                    shared["_compress_kv_bf16"] = (running, cache_layer.compressed_bf16())
+            comp = _compressed_bf16(shared)
+            if comp is not None:
+                g = comp.shape[1]
+                if "topk_idx" in shared:
+                    idx = shared["topk_idx"]
+                    if shared.get("_topk_groups", g) != g:
+                        raise ValueError(f"DeepseekV41Attention layer {self.layer_idx}: the selection published in "
+                                         f"this forward covers {shared.get('_topk_groups')} compressed entries, the "
+                                         f"group's cache holds {g}")
+                elif shared.get("topk_bias") is not None:                    # a reference indexer published
                     bias = shared["topk_bias"]
-                    idx = _mask_to_indices(bias.reshape(-1, bias.shape[-1]), min(self.config.index_topk,
-                                                                                  bias.shape[-1]))
-                    idx = idx.view(batch, seq_len, -1)
-                comp = comp[:, 0]
-            else:
-                comp = None
+                    if bias.shape[-1] != g:
+                        raise ValueError(f"DeepseekV41Attention layer {self.layer_idx}: topk_bias covers "
+                                         f"{bias.shape[-1]} compressed entries, the group's cache holds {g}")
+                    idx = _mask_to_indices(bias.reshape(-1, g), min(self.config.index_topk, g))
+                if idx is None:
+                    comp = None                                              # no index source: none attended
 
-        pos = position_ids.to(device=q.device, dtype=torch.int64).expand(batch, seq_len).contiguous()
-        ring = _window_ring(full, first_pos, self.sliding_window)
-        o = _sparse_attend(q, pos, ring, self.sliding_window, comp, idx, self.attn_sink.detach().float().contiguous())
+        sinks = self.attn_sink.detach().float().contiguous()
+        t = full.shape[1]
+        if isinstance(attention_mask, torch.Tensor):
+            lists = _window_lists(shared, attention_mask, batch, seq_len, t, self.sliding_window)
+            o = _sparse_attend(q, sinks, parts=[(full, lists), (comp, idx)])
+        else:
+            rel = (t - seq_len + torch.arange(seq_len, device=q.device, dtype=torch.int64)).repeat(batch)
+            o = _sparse_attend(q, sinks, window=(full, rel, self.sliding_window), parts=[(comp, idx)])
         o = apply_rotary_pos_emb(o.to(hidden_states.dtype), cos, sin, inverse=True)  # attention.py:231-233
         grouped = o.reshape(batch, seq_len, self.config.o_groups, -1)
         output = self.wo_b(self.wo_a(grouped).flatten(2))
@@ -676,8 +791,7 @@ def sparse_attention_forward(module, query, key, value, attention_mask, scaling,
     cap = min(t, cfg.sliding_window + (getattr(cfg, "index_topk", 0) if module.compress_ratio else 0))
     idx = _mask_to_indices(mask, cap).view(b, s, cap)
     q = query.transpose(1, 2)
-    pos = torch.full((b * s,), -1, dtype=torch.int64, device=query.device)
-    o = _sparse_attend(q, pos, None, 0, key[:, 0], idx, module.attn_sink.detach().float().contiguous())
+    o = _sparse_attend(q, module.attn_sink.detach().float().contiguous(), parts=[(key[:, 0], idx)])
     return o.to(query.dtype), None
 
 

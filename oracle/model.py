@@ -86,9 +86,15 @@ class LayerState:
 
 
 def compressor(params, cfg, x, state: LayerState | None):
-    """cache.py:142-172 (ratio > 1).  Returns (pre-RoPE latent [B, n, D] or None,
-    first_group_position)."""
+    """cache.py:142-172.  Ratio > 1 pools with the softmax gate (fp32); ratio 1 is the plain
+    per-token projection + norm (no gate, cache.py:148-151).  Returns (pre-RoPE latent
+    [B, n, D] or None, first_group_position)."""
     r = cfg["compress_ratio"]
+    if r == 1:                                                         # cache.py:148-151
+        latent = rms_norm(linear(x, params["compressor.wkv.weight"]), params["compressor.norm.weight"],
+                          cfg["rms_norm_eps"])
+        fgp = 0 if state is None else state.entry_count
+        return latent, fgp
     kv = linear(x, params["compressor.wkv.weight"])
     gate = linear(x, params["compressor.wgate.weight"])
     if state is None:
@@ -108,26 +114,33 @@ def compressor(params, cfg, x, state: LayerState | None):
     return latent, fgp
 
 
-def indexer(params, cfg, x, q_residual, latent, fgp, positions, state, shared, select=None):
-    """indexer.py:78-165 for an index source that owns its keys.  Publishes
-    ``shared["index_k"]``, ``shared["selection"]`` (bool [B, S, G]) and ``shared["scores"]``."""
+def indexer(params, cfg, x, q_residual, latent, fgp, positions, state, shared, select=None, *, owns_k=True,
+            candidate_source=False, uses_candidates=False, candidates=None):
+    """indexer.py:78-165.  An index source that owns its keys publishes the keys of the
+    groups completed in this call (``:96-117``); a Reindex layer (``owns_k=False``) scores
+    the keys its group's source published in this forward.  Scores (``:124-133``),
+    visibility (``:141-143``), the two-level candidates (``:145-152``: the candidate source
+    publishes ``shared["candidates"]``, a later index source scores inside it; ``candidates``
+    imposes the candidate source's mask), top-k (``:158-165``).  Publishes ``shared["index_k"]``, ``shared["selection"]`` (bool
+    [B, S, G]) and ``shared["scores"]``."""
     b, s, _ = x.shape
     r, hi, di = cfg["compress_ratio"], cfg["index_n_heads"], cfg["index_head_dim"]
     rd = cfg["qk_rope_head_dim"]
     theta = cfg["compress_rope_theta"]
-    if latent is not None:                                            # indexer.py:96-117
-        k = rms_norm(linear(latent, params["indexer.wk.weight"]), params["indexer.k_norm.weight"],
-                     cfg["rms_norm_eps"])
-        gpos = fgp + r * np.arange(latent.shape[1])
-        cos, sin = rope_tables(np.broadcast_to(gpos, (b, len(gpos))), rd, theta)
-        k = C.rope(k, cos, sin)
-        k = Q.fake_quant_fp4_block(k, 32)
+    if owns_k:
+        if latent is not None:                                        # indexer.py:96-117
+            k = rms_norm(linear(latent, params["indexer.wk.weight"]), params["indexer.k_norm.weight"],
+                         cfg["rms_norm_eps"])
+            gpos = fgp + r * np.arange(latent.shape[1])
+            cos, sin = rope_tables(np.broadcast_to(gpos, (b, len(gpos))), rd, theta)
+            k = C.rope(k, cos, sin)
+            k = Q.fake_quant_fp4_block(k, 32)
+            if state is not None:
+                state.index_k = k if state.index_k is None else np.concatenate([state.index_k, k], 1)
+            else:
+                shared["index_k"] = k if shared.get("index_k") is None else np.concatenate([shared["index_k"], k], 1)
         if state is not None:
-            state.index_k = k if state.index_k is None else np.concatenate([state.index_k, k], 1)
-        else:
-            shared["index_k"] = k if shared.get("index_k") is None else np.concatenate([shared["index_k"], k], 1)
-    if state is not None:
-        shared["index_k"] = state.index_k
+            shared["index_k"] = state.index_k
     index_k = shared.get("index_k")
     g = 0 if index_k is None else index_k.shape[1]
     if g == 0:
@@ -138,7 +151,17 @@ def indexer(params, cfg, x, q_residual, latent, fgp, positions, state, shared, s
     q = Q.fake_quant_fp4_block(q, 32)
     w = linear(x, params["indexer.weights_proj.weight"]) * F32(hi ** -0.5)
     scores = OA.indexer_scores(_t(q), _t(index_k), _t(w), r, torch.as_tensor(positions))
+    if candidate_source:                                              # indexer.py:147-150
+        lens = (np.asarray(positions, np.int64)[..., None] + 1) // r
+        shared["candidates"] = OA.select_candidate_blocks(scores, lens, cfg["candidate_topk_blocks"],
+                                                          cfg["candidate_block_size"])
+        if candidates is not None:
+            shared["candidates"] = np.asarray(candidates, bool)[..., :g]
+    elif uses_candidates and shared.get("candidates") is not None:    # indexer.py:151-152
+        scores = scores.masked_fill(~torch.as_tensor(np.asarray(shared["candidates"], bool)), float("-inf"))
     shared["scores"] = scores
+    # the magnitude the scores' rounding scales with (the indexer tolerance's basis)
+    shared["abs_scores"] = OA.indexer_abs_scores(_t(q), _t(index_k), _t(w), r, torch.as_tensor(positions))
     if select is None:                                                # indexer.py:158-165
         idx = OA.topk_indices(scores, min(cfg["index_topk"], g))
         sel = np.zeros((b, s, g + 1), bool)
@@ -147,18 +170,40 @@ def indexer(params, cfg, x, q_residual, latent, fgp, positions, state, shared, s
     shared["selection"] = np.asarray(select, bool)[..., :g]
 
 
-def layer_forward(params, cfg, x, positions, state: LayerState | None = None, select=None):
-    """attention.py:129-236 for a KV + index source layer.  x [B, S, hidden] fp32, positions
-    [B, S] absolute; ``state`` (LayerState) for a cached call.  Returns (out [B, S, hidden],
-    shared) with ``shared["selection"]`` the compressed entries each query attended."""
+# keys a KV-source layer drops from `shared` when there is no cache: each group starts
+# fresh (archs/dsv4/modeling_deepseek_v41.py:722-732; tickets/done/0012)
+_GROUP_KEYS = ("compress_kv", "index_k", "selection", "scores", "abs_scores", "candidates")
+
+
+def role(cfg, i: int) -> dict:
+    """Layer i's role in a schedule (owlet1/attention.py:95-127, indexer.py:60-64)."""
+    kv, ix = cfg["kv_source_layer_ids"], cfg["index_source_layer_ids"]
+    cand = cfg.get("candidate_source_layer_id", -1)
+    cand = -1 if cand is None else cand
+    return dict(ratio=cfg["compress_ratios"][i], kv_source=i in kv, index_source=i in ix,
+                owns_k=i in kv and i in ix, candidate_source=i == cand, uses_candidates=0 <= cand < i)
+
+
+def attention_layer(params, cfg, i: int, x, positions, state: LayerState | None, shared: dict, live=None,
+                    select=None, candidates=None):
+    """attention.py:129-236 for layer i of the schedule ``cfg`` (one layer of a forward
+    whose layers share ``shared``).  x [B, S, hidden] fp32; positions [B, S] absolute (the
+    running token count); ``state`` the layer's cache (window for every layer, group state
+    on a KV source) for a cached call; ``live`` bool [B, T] the liveness of every token seen
+    so far (the model's 2-D attention mask; None = all live); ``select`` an imposed
+    selection for an index source, ``candidates`` an imposed candidate mask for the candidate
+    source (the reference's ``torch.topk`` breaks ties between equal block scores in its own
+    order).  Returns out [B, S, hidden]."""
     x = _np(x)
     positions = np.asarray(positions, np.int64)
     b, s, _ = x.shape
+    ro = role(cfg, i)
+    r = ro["ratio"]
     h, d, rd, w_ = cfg["num_attention_heads"], cfg["head_dim"], cfg["qk_rope_head_dim"], cfg["sliding_window"]
     eps = cfg["rms_norm_eps"]
-    r = cfg["compress_ratio"]
-    cos, sin = rope_tables(positions, rd, cfg["compress_rope_theta"])   # position_embeddings["compress"]
-    shared: dict = {}
+    lcfg = dict(cfg, compress_ratio=r)
+    theta = cfg["compress_rope_theta"] if r else cfg.get("rope_theta", 10000.0)   # attention.py:100, :143
+    cos, sin = rope_tables(positions, rd, theta)
 
     q_res = rms_norm(linear(x, params["wq_a.weight"]), params["q_norm.weight"], eps)
     q = linear(q_res, params["wq_b.weight"]).reshape(b, s, h, d)
@@ -171,31 +216,49 @@ def layer_forward(params, cfg, x, positions, state: LayerState | None = None, se
         state.window = win[:, -(w_ - 1):] if w_ > 1 else win[:, :0]
     else:
         win = kv
-    win_pos0 = positions[0, 0] - (win.shape[1] - s)                    # absolute position of win[:, 0]
+    seen = state.positions_seen if state is not None else 0            # running index of this call's first token
+    win0 = seen + s - win.shape[1]                                     # running index of win[:, 0]
 
-    latent, fgp = compressor(params, cfg, x, state)
-    indexer(params, cfg, x, q_res, latent, fgp, positions, state, shared, select)
-    if latent is not None:                                             # attention.py:173-192
-        gpos = fgp + r * np.arange(latent.shape[1])
-        cc, ss = rope_tables(np.broadcast_to(gpos, (b, len(gpos))), rd, cfg["compress_rope_theta"])
-        rot = Q.fake_quant_fp4_block(C.rope(latent, cc, ss), 16, e4m3_scales=True)
-        if state is not None:
-            state.compressed = rot if state.compressed is None else np.concatenate([state.compressed, rot], 1)
-            state.entry_count += rot.shape[1]
-        else:
-            shared["compress_kv"] = rot
-    if state is not None:
-        shared["compress_kv"] = state.compressed
-    comp = shared.get("compress_kv")
-
-    # mask: window band (attention.py / masking: k in (t - W, t]) then the selection
-    t = positions[:, :, None]
-    kpos = win_pos0 + np.arange(win.shape[1])[None, None, :]
-    visible = (kpos <= t) & (kpos > t - w_)
     keys = win
-    if comp is not None and comp.shape[1]:
+    sel = None
+    comp = None
+    if r:
+        if ro["kv_source"] and state is None:
+            for key in _GROUP_KEYS:
+                shared.pop(key, None)
+        latent, fgp = (None, 0)
+        if ro["kv_source"]:
+            latent, fgp = compressor(params, lcfg, x, state)
+        if ro["index_source"]:
+            indexer(params, lcfg, x, q_res, latent, fgp, positions, state, shared, select, owns_k=ro["owns_k"],
+                    candidate_source=ro["candidate_source"], uses_candidates=ro["uses_candidates"],
+                    candidates=candidates)
         sel = shared.get("selection")
-        if sel is None:
+        if latent is not None:                                         # attention.py:173-192
+            gpos = fgp + r * np.arange(latent.shape[1])
+            cc, ss = rope_tables(np.broadcast_to(gpos, (b, len(gpos))), rd, cfg["compress_rope_theta"])
+            rot = Q.fake_quant_fp4_block(C.rope(latent, cc, ss), 16, e4m3_scales=True)
+            if state is not None:
+                state.compressed = rot if state.compressed is None else np.concatenate([state.compressed, rot], 1)
+                state.entry_count += rot.shape[1]
+            else:
+                shared["compress_kv"] = rot if shared.get("compress_kv") is None else np.concatenate(
+                    [shared["compress_kv"], rot], 1)
+        if ro["kv_source"] and state is not None:
+            shared["compress_kv"] = state.compressed
+        comp = shared.get("compress_kv")
+
+    # mask: the model's sliding causal mask over the running token index (k in (t - W, t],
+    # the key live), then the selection (attention.py:202-214)
+    t = seen + np.arange(s)[None, :, None]
+    kpos = win0 + np.arange(win.shape[1])[None, None, :]
+    visible = (kpos <= t) & (kpos > t - w_)
+    if live is not None:
+        lv = np.asarray(live, bool)
+        visible = visible & lv[:, kpos[0, 0]][:, None, :]
+    visible = np.broadcast_to(visible, (b, s, win.shape[1]))
+    if comp is not None and comp.shape[1]:
+        if sel is None or sel.shape[-1] != comp.shape[1]:
             sel = np.zeros((b, s, comp.shape[1]), bool)                # attention.py:208-214
         visible = np.concatenate([visible, sel], -1)
         keys = np.concatenate([win, comp], 1)
@@ -212,4 +275,35 @@ def layer_forward(params, cfg, x, positions, state: LayerState | None = None, se
     out = y @ torch.as_tensor(params["wo_b.weight"]).float().T
     if state is not None:
         state.positions_seen += s
-    return out.numpy(), shared
+    return out.numpy()
+
+
+def stack_forward(params, cfg, xs, positions, states=None, live=None, select=None, candidates=None):
+    """One forward of a layer schedule: layer i of ``cfg`` (``compress_ratios``,
+    ``kv_source_layer_ids``, ``index_source_layer_ids``, ``candidate_source_layer_id``, ...)
+    runs on its own input ``xs[i]`` with ``params[i]``; the layers share one ``shared`` dict,
+    as the reference decoder passes one per forward (owlet1/decoder.py:318-330).  ``states``
+    a list of LayerState (a cached call) or None; ``select`` {layer: imposed selection};
+    ``candidates`` an imposed candidate mask for the candidate source.
+    Returns (outs [layers] of [B, S, hidden], {layer: what the layer's indexer published})."""
+    shared: dict = {}
+    outs, published = [], {}
+    for i in range(len(cfg["compress_ratios"])):
+        st = None if states is None else states[i]
+        outs.append(attention_layer(params[i], cfg, i, xs[i], positions, st, shared, live,
+                                    None if select is None else select.get(i), candidates))
+        if role(cfg, i)["index_source"]:
+            published[i] = {k: shared.get(k) for k in ("selection", "scores", "abs_scores", "index_k", "candidates")}
+    return outs, published
+
+
+def layer_forward(params, cfg, x, positions, state: LayerState | None = None, select=None):
+    """attention.py:129-236 for a layer that is its group's KV and index source (ratio
+    ``cfg["compress_ratio"]``).  x [B, S, hidden] fp32, positions [B, S] absolute; ``state``
+    (LayerState) for a cached call.  Returns (out [B, S, hidden], shared) with
+    ``shared["selection"]`` the compressed entries each query attended."""
+    one = dict(cfg, compress_ratios=[cfg["compress_ratio"]], kv_source_layer_ids=[0], index_source_layer_ids=[0],
+               candidate_source_layer_id=-1)
+    shared: dict = {}
+    out = attention_layer(params, one, 0, x, positions, state, shared, None, select)
+    return out, shared
