@@ -468,7 +468,8 @@ int mzk_sparse_mqa_combine_rope(const float* workspace, int64_t B, int64_t S, in
  * allocation).  No counterpart in the reference: it is mzk_sparse_mqa_rope with the split
  * partials kept in a file-scope device array of MZK_NOALLOC_SCRATCH_BYTES bytes (one copy
  * per GPU the library runs on, held until the process ends) instead of `workspace`; it
- * never allocates.  rope_cos / rope_sin may be NULL (then it is mzk_sparse_mqa).  Limit:
+ * never allocates.  rope_cos / rope_sin may be NULL (then it is mzk_sparse_mqa); out and lse
+ * are required (the partials stay in the private array).  Limit:
  * rows * nsplit * H * (2*D + 8) <= MZK_NOALLOC_SCRATCH_BYTES when nsplit > 1 (config 2:
  * 32 x 4 x 128 x 1160 = 19 MB), else MZK_EINVAL.  Every call on one GPU shares that GPU's
  * array, so calls that overlap on one GPU (concurrent streams, or host threads) race: the

@@ -736,9 +736,9 @@ struct SplitSmem {
   static constexpr int KT_PITCH = 2 * D + 16;
   static constexpr int KT = kTile * KT_PITCH;             // one bf16 tile
   static constexpr int SX = HG * DS * 4 * 64 * 16;        // [wave][4][64] float4 partial S^T
-  static constexpr int PM = HG * 32 * 2 * DS * 4;         // [64 heads][8] partial maxima / row sums
+  static constexpr int PM = HG * 32 * 2 * DS * 4;         // [2][64 heads] float4: partial maxima / row sums
   static constexpr int PB = HG * 2 * 64 * 16;             // [hg][2 K-steps][64] P^T
-  static constexpr int PE = HG * 32 * 2 * DS * 4;         // [64 heads][8] true lane maxima
+  static constexpr int PE = HG * 32 * 2 * DS * 4;         // [2][64 heads] float4: true lane maxima
   static constexpr int NKT = 3;                            // bf16 tiles in flight: PV, QK, dequantized
   static constexpr int LDS = NKT * KT + SX + PM + PB + PE;
 };
@@ -799,6 +799,10 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
   const int head = rp.hgrp * (HG * 32) + hl;
   const bool head_ok = head < p.H;
   const int qc0 = ds * QST * 16;  // first QK channel of this wave
+  // this lane's slot k = 2 ds + half of its head's eight partial maxima / row sums, in a
+  // [2][64 heads] float4 layout: a head's eight values are two conflict-free float4 reads,
+  // and a wave's 64 b32 writes fall on 32 distinct banks (2-way; [64 heads][8] was 8-way)
+  const int pm_slot = (((2 * ds + half) >> 2) * 64 + hl) * 4 + ((2 * ds + half) & 3);
   v8bf qf[QST];
   {
     // branch-free loads (a missing head reads head 0 and is zeroed); uniform row base plus a
@@ -869,7 +873,7 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
     float mx = s[0];
 #pragma unroll
     for (int j = 1; j < 16; ++j) mx = fmaxf(mx, s[j]);
-    pm[hl * 8 + 2 * ds + half] = mx;
+    pm[pm_slot] = mx;
 #pragma unroll
     for (int j4 = 0; j4 < 4; ++j4)
       sx[(wave * 4 + j4) * 64 + lane] = float4{s[4 * j4], s[4 * j4 + 1], s[4 * j4 + 2], s[4 * j4 + 3]};
@@ -944,15 +948,15 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
       if constexpr (kExact) {
         // the head's true tile max: its 8 lanes' maxima through LDS (the other group
         // passes the matching barrier at the start of its MFMA half-step)
-        pe[hl * 8 + 2 * ds + half] = lane_max;
+        pe[pm_slot] = lane_max;
         lds_barrier();
-        const float4 t0 = *reinterpret_cast<const float4*>(pe + hl * 8);
-        const float4 t1 = *reinterpret_cast<const float4*>(pe + hl * 8 + 4);
+        const float4 t0 = reinterpret_cast<const float4*>(pe)[hl];
+        const float4 t1 = reinterpret_cast<const float4*>(pe)[64 + hl];
         bound = fmaxf(fmaxf(fmaxf(t0.x, t0.y), fmaxf(t0.z, t0.w)), fmaxf(fmaxf(t1.x, t1.y), fmaxf(t1.z, t1.w)));
       } else {
         m_seen = fmaxf(m_seen, lane_max);
-        const float4 t0 = *reinterpret_cast<const float4*>(pm + hl * 8);
-        const float4 t1 = *reinterpret_cast<const float4*>(pm + hl * 8 + 4);
+        const float4 t0 = reinterpret_cast<const float4*>(pm)[hl];
+        const float4 t1 = reinterpret_cast<const float4*>(pm)[64 + hl];
         bound = (((fmaxf(t0.x, t0.y) + fmaxf(t0.z, t0.w)) + fmaxf(t1.x, t1.y)) + fmaxf(t1.z, t1.w)) * p.scale_log2;
       }
       const bool raise = bound > m_run + kLazy;
@@ -1130,17 +1134,17 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
     // row sum: each lane holds the share of its entries (all scaled to the same running
     // max); the 8 shares of a head are reduced in a fixed order
     __syncthreads();  // every wave is done reading pm and pe
-    pm[hl * 8 + 2 * ds + half] = l_run;
-    if (!kExact) pe[hl * 8 + 2 * ds + half] = m_seen;
+    pm[pm_slot] = l_run;
+    if (!kExact) pe[pm_slot] = m_seen;
     __syncthreads();
     {
-      const float4 t0 = *reinterpret_cast<const float4*>(pm + hl * 8);
-      const float4 t1 = *reinterpret_cast<const float4*>(pm + hl * 8 + 4);
+      const float4 t0 = reinterpret_cast<const float4*>(pm)[hl];
+      const float4 t1 = reinterpret_cast<const float4*>(pm)[64 + hl];
       l_run = (((t0.x + t0.y) + (t0.z + t0.w)) + ((t1.x + t1.y) + (t1.z + t1.w)));
     }
     if constexpr (!kExact) {
-      const float4 t0 = *reinterpret_cast<const float4*>(pe + hl * 8);
-      const float4 t1 = *reinterpret_cast<const float4*>(pe + hl * 8 + 4);
+      const float4 t0 = reinterpret_cast<const float4*>(pe)[hl];
+      const float4 t1 = reinterpret_cast<const float4*>(pe)[64 + hl];
       const float m_true =
           fmaxf(fmaxf(fmaxf(t0.x, t0.y), fmaxf(t0.z, t0.w)), fmaxf(fmaxf(t1.x, t1.y), fmaxf(t1.z, t1.w)));
       // a head with no unmasked entry (m_true = -inf) contributes nothing and is exact

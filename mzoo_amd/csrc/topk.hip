@@ -19,7 +19,7 @@
 // Rows up to 32 * 1024 keys keep them in registers (topk_row_kernel, one workgroup per
 // row); longer rows without a workspace stream the row through 8-bit digit passes
 // (topk_rows_kernel).  mzk_topk_rows_ws splits rows of 32769 .. 64 x 8192 keys over chunk
-// workgroups (two launches, see below).
+// workgroups (three launches, see below).
 #include "common.h"
 
 namespace mzk {

@@ -53,3 +53,17 @@ def test_candidate_entry_points_reject_bad_shapes():
     # in place with different strides
     assert lib.mzk_candidate_positions(p, 2, 16, 32, p, 8, 8, 8, p, 16, None) == -1
     assert b"in place" in lib.mzk_last_error()
+
+
+def test_noalloc_argument_checks():
+    """mzk_sparse_mqa_noalloc refuses a call whose merged output has nowhere to go (the
+    partials would stay in its private array) and a row count past 2^31 before it sizes the
+    scratch -- both before any HIP call."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    common = [p, 4, 1, 128, 576, 1, 512, p, p, 128, 128, 128, None, 0, 0, 1, p, 8192, 8192, p, 2048, 2048, p, 4]
+    assert lib.mzk_sparse_mqa_noalloc(*common, None, None, None, None, 0, None) == -1
+    assert b"out and lse are required" in lib.mzk_last_error()
+    big = [p, 1 << 20, 1 << 12] + common[3:]
+    assert lib.mzk_sparse_mqa_noalloc(*big, p, p, None, None, 0, None) == -1
+    assert b"too many rows" in lib.mzk_last_error()

@@ -240,3 +240,34 @@ def test_nonfinite_blocks_follow_torch_semantics():
                         assert np.isnan(sl).all(), (r, blk)
                     elif not np.isnan(x[r, blk * bs:(blk + 1) * bs]).any() and np.isfinite(x[r, blk * bs:(blk + 1) * bs]).all():
                         assert np.array_equal(sl, clean[r, blk * bs:(blk + 1) * bs]), (r, blk)
+
+
+def test_latent_entry_byte_layout_known_answer():
+    """The 656 B FP8-b128 entry byte by byte, independently of the pack / unpack pair:
+    512 e4m3 codes, four little-endian fp32 block scales at bytes 512..527, 64 bf16 rope
+    channels at bytes 528..655 (FlashMLA's V3.2 layout, layers/attn/fp_attn_notes.md)."""
+    x = np.zeros((1, 576), np.float32)
+    x[0, 0], x[0, 1], x[0, 2], x[0, 3] = 448.0, -1.0, 0.5, 2.0 ** -9      # block 0: scale 1
+    x[0, 128] = 224.0                                                       # block 1: scale 1/2
+    x[0, 384] = 1000.0                                                      # block 3: scale 4; 250 -> 256
+    x[0, 512], x[0, 513], x[0, 575] = 1.0, -2.5, 3.140625                  # rope (bf16-exact)
+    e = Q.pack_latent_fp8_b128(x)[0]
+    assert e[0] == 0x7E and e[1] == 0xB8 and e[2] == 0x30 and e[3] == 0x01   # 448, -1, 0.5, 2^-9
+    assert e[128] == 0x7E and e[384] == 0x78 and not e[4:128].any() and not e[256:384].any()
+    scales = [bytes(e[512 + 4 * i:516 + 4 * i]) for i in range(4)]
+    assert scales[0] == bytes([0, 0, 0x80, 0x3F])                  # 1.0
+    assert scales[1] == bytes([0, 0, 0, 0x3F])                     # 0.5
+    assert scales[2] == bytes([0, 0, 0x80, 0x34])                  # 2^-22: the 1e-4 amax floor
+    assert scales[3] == bytes([0, 0, 0x80, 0x40])                  # 4.0
+    assert bytes(e[528:532]) == bytes([0x80, 0x3F, 0x20, 0xC0])    # 1.0, -2.5
+    assert bytes(e[654:656]) == bytes([0x49, 0x40]) and not e[532:654].any()
+    # and a hand-written entry reads back as the values its bytes spell
+    h = np.zeros(656, np.uint8)
+    h[5] = 0x7E                                                     # channel 5: 448 x block-0 scale 1
+    h[200] = 0xB8                                                   # channel 200: -1 x block-1 scale
+    h[512:516] = [0, 0, 0x80, 0x3F]
+    h[516:520] = [0, 0, 0, 0x40]                                    # block 1 scale 2.0
+    h[528 + 2 * 7:528 + 2 * 8] = [0x20, 0xC0]                       # rope channel 7 = -2.5
+    v = Q.unpack_latent_fp8_b128(h[None])[0]
+    assert v[5] == 448.0 and v[200] == -2.0 and v[512 + 7] == -2.5
+    assert np.count_nonzero(v) == 3
