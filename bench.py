@@ -83,6 +83,8 @@ def parse():
     ap.add_argument("--prologue", choices=["fused", "rotated"], default="fused",
                     help="fused: unrotated q / q_idx and the raw kv projection, norm and RoPE in the step's "
                          "launches; rotated: inputs already normed and rotated")
+    ap.add_argument("--emit", choices=["merged", "separate"], default="merged",
+                    help="group emission inside the indexer launch (merged) or in a launch of its own")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline time budget")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--stage-iters", type=int, default=0, help="launches per stage timing (0: max(steps, 50))")
@@ -112,7 +114,7 @@ def rope_inputs(torch, dev, positions):
     return tuple(out)
 
 
-def build_layer(torch, dev, nsplit=0, seed=None, config=2, fused=True, start=None):
+def build_layer(torch, dev, nsplit=0, seed=None, config=2, fused=True, start=None, merged_emit=True):
     """A decode layer of BASELINE config `config` (2, 4 or 5) with synthetic history: the
     window ring holds the 128 tokens before the start position, every compressed group is
     published, and the first step decodes the token at `start` (default ctx-1).  With
@@ -123,7 +125,8 @@ def build_layer(torch, dev, nsplit=0, seed=None, config=2, fused=True, start=Non
     c = DECODE[config]
     cfg = DecodeConfig(batch=c["batch"], heads=128, nope=512, rope=64, index_heads=64, index_dim=128, ratio=4,
                        window=128, topk=2048, max_groups=c["groups"], index_format=c["index_format"],
-                       coarse_ratio=c["coarse_ratio"], coarse_groups=c["coarse_groups"], nsplit=nsplit or c["nsplit"])
+                       coarse_ratio=c["coarse_ratio"], coarse_groups=c["coarse_groups"], nsplit=nsplit or c["nsplit"],
+                       merged_emit=merged_emit)
     ctx = c["ctx"]
     start = ctx - 1 if start is None else start
     gen = torch.Generator(device=dev).manual_seed(c["seed"] if seed is None else seed)
@@ -233,11 +236,12 @@ def stage_times(torch, layers, inputs, iters):
     carries the token -- and amortized over the branches' ratios (1 of `ratio` steps completes
     a fine group, 1 of `coarse_ratio` a coarse one)."""
     per_layer = [stage_fns(torch, layer, inp) for layer, inp in zip(layers, inputs)]
-    emit = per_layer[0].pop("decode_emit", None)
-    if emit is not None:
-        emits = [d.pop("decode_emit") for d in per_layer[1:]]
+    # the launches whose work depends on the position: the emission, or the merged emission +
+    # scores launch
+    moving = [k for k in per_layer[0] if k.startswith(("decode_emit", "indexer_emit"))]
+    timed = {k: [d.pop(k) for d in per_layer] for k in moving}
     out = {name: graph_time(torch, [d[name] for d in per_layer], iters) for name in per_layer[0]}
-    if emit is not None:
+    for key, fns in timed.items():
         cfg = layers[0].cfg
         saved = [int(layer.positions[0]) for layer in layers]
         period = cfg.ratio * max(cfg.coarse_ratio // cfg.ratio, 1) if cfg.coarse_ratio else cfg.ratio
@@ -248,16 +252,16 @@ def stage_times(torch, layers, inputs, iters):
         def at(pos):
             for layer in layers:
                 layer.set_positions(pos)
-            return graph_time(torch, [emit] + emits, iters)
-        out["decode_emit_group"] = at(p_all)
-        out["decode_emit_carry"] = at(p_all - 1)
-        amort = (out["decode_emit_group"] + (cfg.ratio - 1) * out["decode_emit_carry"]) / cfg.ratio
+            return graph_time(torch, fns, iters)
+        out[key + "_group"] = at(p_all)
+        out[key + "_carry"] = at(p_all - 1)
+        amort = (out[key + "_group"] + (cfg.ratio - 1) * out[key + "_carry"]) / cfg.ratio
         if cfg.coarse_ratio:
-            out["decode_emit_fine_group"] = at(p_all - cfg.ratio)
+            out[key + "_fine_group"] = at(p_all - cfg.ratio)
             n_fine = cfg.coarse_ratio // cfg.ratio
-            amort = (out["decode_emit_group"] + (n_fine - 1) * out["decode_emit_fine_group"] +
-                     (cfg.coarse_ratio - n_fine) * out["decode_emit_carry"]) / cfg.coarse_ratio
-        out["decode_emit"] = amort
+            amort = (out[key + "_group"] + (n_fine - 1) * out[key + "_fine_group"] +
+                     (cfg.coarse_ratio - n_fine) * out[key + "_carry"]) / cfg.coarse_ratio
+        out[key] = amort
         for layer, p in zip(layers, saved):
             layer.set_positions(p)
     return out
@@ -276,12 +280,19 @@ def stage_fns(torch, layer, inputs):
     fns = {}
     fp8 = cfg.index_format == "fp8"
     pro = emit and layer._emit_prologue
-    if emit:
+    merged = pro and cfg.merged_emit and cfg.ratio == 4 and not cfg.coarse_ratio
+    if merged:
+        # the emission and the scores in one launch (window entry and query prologue included)
+        fns["indexer_emit_fp8" if fp8 else "indexer_emit_mxfp4"] = \
+            lambda: layer._emit_scores(inputs[4:], kv, q_idx, w)
+    elif emit:
         # the in-step group emission (one launch per compressed branch); the first launch also
         # runs the step's prologue (window entry, indexer query RoPE + quantization)
         fns["decode_emit"] = lambda: layer._emit(inputs[4:], True, prologue=(kv, q_idx) if pro else None)
     pos = layer.positions.view(b, 1)
-    if pro:
+    if merged:
+        pass
+    elif pro:
         # the plain scorer over the quantized query
         if fp8:
             fns["indexer_scores_fp8"] = lambda: indexer.scores_fp8(
@@ -462,6 +473,7 @@ def run_decode(torch, dev, args):
     # the replays advance the positions: the last timed replay decodes position ctx-1
     start = c["ctx"] - 1 - (args.warmup + args.steps) if fused else None
     built = [build_layer(torch, dev, args.nsplit, seed=c["seed"] + i, config=args.config, fused=fused,
+                         merged_emit=args.emit == "merged",
                          start=start) for i in range(nl)]
     layers = [b_[0] for b_ in built]
     inputs_all = [b_[1] for b_ in built]
@@ -489,9 +501,12 @@ def run_decode(torch, dev, args):
     attn_flops = rows * 4.0 * cfg.dim * cfg.heads * entries
     idx_bytes = rows * cfg.max_groups * KEY_BYTES[cfg.index_format]
     idx_flops = rows * 2.0 * cfg.index_heads * cfg.index_dim * cfg.max_groups
-    idx_stage = next(k for k in ("indexer_scores_fp8", "indexer_scores_mxfp4", "indexer_decode_fp8",
-                                 "indexer_decode_mxfp4") if k in stages)
-    dominant = max(("sparse_mqa", idx_stage, "topk"), key=lambda k: stages[k])
+    idx_stage = next(k for k in ("indexer_emit_fp8", "indexer_emit_mxfp4", "indexer_scores_fp8",
+                                 "indexer_scores_mxfp4", "indexer_decode_fp8", "indexer_decode_mxfp4") if k in stages)
+    # the dominant single kernel: rows longer than 32768 keys run the top-k as three launches
+    # (a latency stage, not one kernel), so it is a candidate only as one launch
+    cands = ("sparse_mqa", idx_stage) + (("topk",) if cfg.max_groups <= 32768 else ())
+    dominant = max(cands, key=lambda k: stages[k])
     if dominant == "sparse_mqa":
         roof = roofline(None, attn_flops, attn_bytes, stages[dominant])
     elif dominant == idx_stage:
@@ -524,6 +539,8 @@ def run_decode(torch, dev, args):
         "config": {"workload": c["text"], "batch": cfg.batch, "context": c["ctx"], "heads": cfg.heads,
                    "latent": "512+64", "index": f"64x128 {cfg.index_format}", "topk": cfg.topk,
                    "window": cfg.window, "coarse": nc, "nsplit": cfg.nsplit, "graph_layers": nl,
+                   "emission": ("inside the indexer launch" if fused and cfg.merged_emit and not cfg.coarse_ratio
+                                else "launch of its own") if fused else None,
                    "step": "per attention layer, inside a graph replay of graph_layers layers",
                    "prologue": ("fused: in-step group emission (carry ring, pooling + norm, cache entry and "
                                 "index key every 4th token; RoPE tables from the position table), kv RMSNorm + "

@@ -167,6 +167,26 @@ int mzk_decode_emit_pair(const int64_t* positions, int64_t B, const float* kv, c
                          float* c_carry_gate, int c_ratio, const void* c_norm_weight, float c_eps, uint8_t* c_cache,
                          int64_t c_cache_batch_entries, int64_t c_cache_cap, void* stream);
 
+/* The decode step's group emission and indexer scores in one launch (owlet1/cache.py:96-124,
+ * :159-172 and owlet1/indexer.py:96-143 for one token per row): the same results as
+ * mzk_decode_emit (ratio 4, with the index key wk and the kv prologue; q_idx NULL) followed
+ * by mzk_indexer_decode_fused over the emitted keys with the query's RoPE from row `pos` of
+ * rope_table -- the carry, caches, keys, window entry, step tables and scores bit for bit.
+ * The emission arguments are mzk_decode_emit's up to win_cap; then q_idx bf16 [B, Hi, 128]
+ * (unrotated; its trailing 64 channels rotated with the table row), w fp32 [B, Hi] (already
+ * x Hi^-0.5), Hi <= 64 index heads, G keys per row (key batch stride key_batch_entries,
+ * format key_format), scores fp32 [B, score_stride] (-inf at and beyond the visible count).
+ * Per row one workgroup emits (and scores the new key itself), one writes the window entry,
+ * and ceil(G / 512) score.  ratio must be 4 (MZK_EINVAL otherwise). */
+int mzk_decode_emit_scores(const int64_t* positions, int64_t B, const float* kv, const float* gate, float* carry_kv,
+                           float* carry_gate, int ratio, const void* norm_weight, float eps, uint8_t* cache,
+                           int64_t cache_batch_entries, int64_t cache_cap, const void* wk, const void* k_norm_weight,
+                           float k_eps, int key_format, uint8_t* k_codes, void* k_scales, int64_t key_batch_entries,
+                           const void* rope_table, int64_t table_rows, void* step_cos, void* step_sin,
+                           const void* kv_proj, const void* kv_weight, float kv_eps, uint8_t* win_cache,
+                           int64_t win_batch_entries, int win_cap, const void* q_idx, const float* w, int Hi,
+                           int64_t G, float* scores, int64_t score_stride, void* stream);
+
 /* ---------------------------------------------------------------------------------
  * Piece 2: KV compressor and RoPE
  * --------------------------------------------------------------------------------- */

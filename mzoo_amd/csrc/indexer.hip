@@ -15,14 +15,16 @@
 //           into v_mfma_scale_f32_32x32x64_f8f6f4 (lane = one 32-element block).
 //   kBf16 : bf16 q/k (the reference kernel-level `indexer.fwd` contract).
 //
-// Tiling (one workgroup = 4 waves = one query row x 4*kNkb*32 keys):
+// Tiling (one workgroup = 4 waves = one query row x 4*NKB*32 keys, NKB = kNkb = 4 tiles
+// per wave, 5 in the merged emission launch):
 //   MFMA 32x32: M = 32 heads, N = 32 keys, K = Di.  A (queries) stays in VGPRs for the
-//   whole workgroup; each wave streams kNkb 32-key tiles of B straight from HBM.
+//   whole workgroup; each wave streams NKB 32-key tiles of B straight from HBM.
 //   The 32x32 f32 result holds, in lane l, key column l%32 and 16 head rows, so the
 //   ReLU-weighted head sum is lane-local, then one xor-32 shuffle adds the other half.
 //   For each operand a lane holds a contiguous run of channels; A and B use the same
 //   lane/slot -> channel assignment, so the K-order inside the MFMA is irrelevant.
 #include "common.h"
+#include "emit_core.h"
 
 namespace mzk {
 namespace {
@@ -246,24 +248,272 @@ struct FusedKv {
 template <int FMT>
 constexpr int q_pitch() { return FMT == kFp8 ? 128 + 16 : 64 + 16; }
 
-// One workgroup = 4 waves = one query row x kKeysPerWg keys (see the tiling note above).
+// The raw query's quantization (QRAW): thread t holds 32 channels of head t / 4 (bf16, already
+// rotated) in qr; they are quantized into LDS (FP8 b128 per head, or MXFP4 per 32 channels),
+// then every lane reads back its A fragments and, FP8, its head's scale into cq.  Thread t
+// owns head qh = t / 4, channels 32 qc .. 32 qc + 31 (qc = t % 4).
+//   amax: the magnitudes' bf16 bits compared as integers (two per word, v_pk_max_u16) -- the
+//   float order of values >= 0 with NaN above infinity, as nn_max;
+//   FP8: codes of clamp(x / s, +-448) by v_cvt_pk_fp8_f32 (s a power of two, x / s == x *
+//   (1 / s) exactly); with a finite amax every x * (1 / s) is finite and the clamp is a
+//   median, else the NaN-keeping clamp;
+//   MXFP4: with a finite amax, v_cvt_scalef32_pk_fp4_bf16 (x / s to e2m1, nearest even,
+//   saturating at 6), which equals e2m1_code(clamp(x * (1 / s), +-6)) for every finite bf16 x
+//   and power-of-two s in [2^-126, 2^127] (checked on the hardware for all bf16 inputs); a
+//   block with a NaN or an infinity takes the software encoder.
+typedef unsigned short mzk_u16x2v __attribute__((ext_vector_type(2)));
+typedef __bf16 mzk_bf16x2v __attribute__((ext_vector_type(2)));
+
+template <int FMT, int DI, int MB>
+__device__ __forceinline__ void quantize_query(const uint4 (&qr)[4], int qh, int qc, int Hi, int lane, int hi, int hl,
+                                               uint8_t* q_lds, float* qs_lds, uint8_t* qe_lds,
+                                               Frag (&a)[MB][DI / Step<FMT>::K], float& cq) {
+  constexpr int QP = q_pitch<FMT>();
+  constexpr int NST = DI / Step<FMT>::K;
+  // the thread's channels, two bf16 per word (the even channel low); heads beyond Hi are zeros
+  uint32_t wv[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    wv[4 * i] = qr[i].x;
+    wv[4 * i + 1] = qr[i].y;
+    wv[4 * i + 2] = qr[i].z;
+    wv[4 * i + 3] = qr[i].w;
+  }
+  if (qh >= Hi) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) wv[k] = 0u;
+  }
+  mzk_u16x2v m = __builtin_bit_cast(mzk_u16x2v, wv[0] & 0x7fff7fffu);
+#pragma unroll
+  for (int k = 1; k < 16; ++k) m = __builtin_elementwise_max(m, __builtin_bit_cast(mzk_u16x2v, wv[k] & 0x7fff7fffu));
+  float amax = __uint_as_float(static_cast<uint32_t>(m.x > m.y ? m.x : m.y) << 16);
+  if constexpr (FMT == kMxfp4) {
+    // one MXFP4 block of 32 channels per thread: scale, then e2m1 codes (element 2i in the
+    // low nibble of byte i), as the quantizer's packed form
+    const float sc = fp4_scale_from_amax(amax, false);
+    uint32_t wd[4];
+    if (amax <= 0x1.fffffep127f) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t word = 0;
+        word = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(word, __builtin_bit_cast(mzk_bf16x2v, wv[4 * i]), sc, 0);
+        word = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(word, __builtin_bit_cast(mzk_bf16x2v, wv[4 * i + 1]), sc, 1);
+        word = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(word, __builtin_bit_cast(mzk_bf16x2v, wv[4 * i + 2]), sc, 2);
+        word = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(word, __builtin_bit_cast(mzk_bf16x2v, wv[4 * i + 3]), sc, 3);
+        wd[i] = word;
+      }
+    } else {
+      // x / sc == x * (1 / sc) exactly: sc is a power of two (here infinite: 1 / sc = 0)
+      const float inv = 1.0f / sc;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float lo = __uint_as_float(wv[4 * i + j] << 16);
+          const float hi2 = __uint_as_float(wv[4 * i + j] & 0xffff0000u);
+          word |= e2m1_code(clampf(lo * inv, 6.0f)) << (8 * j);
+          word |= e2m1_code(clampf(hi2 * inv, 6.0f)) << (8 * j + 4);
+        }
+        wd[i] = word;
+      }
+    }
+    *reinterpret_cast<uint4*>(q_lds + qh * QP + 16 * qc) = uint4{wd[0], wd[1], wd[2], wd[3]};
+    qe_lds[qh * 4 + qc] = static_cast<uint8_t>(__float_as_uint(sc) >> 23);
+    __syncthreads();
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int h = mb * 32 + (lane & 31);
+#pragma unroll
+      for (int st = 0; st < NST; ++st) {
+        const uint4 u = *reinterpret_cast<const uint4*>(q_lds + h * QP + st * 32 + hi * 16);
+        a[mb][st].v = v8i{(int)u.x, (int)u.y, (int)u.z, (int)u.w, 0, 0, 0, 0};
+        a[mb][st].scale = qe_lds[h * 4 + st * 2 + hi];
+      }
+    }
+  } else {
+    amax = group_max(amax, 4);  // the 4 threads of a head are consecutive lanes
+    const float sc = fp8_scale_from_amax(amax);
+    // x / sc == x * (1 / sc) exactly: sc is a power of two, in [2^-22, 2^120] for finite input
+    const float inv = sc <= 0x1p120f ? pow2_reciprocal(sc) : 1.0f / sc;
+    uint32_t wd[8];
+    if (amax <= 0x1.fffffep127f) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float x[4];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          x[2 * j] = __builtin_amdgcn_fmed3f(__uint_as_float(wv[2 * i + j] << 16) * inv, -448.0f, 448.0f);
+          x[2 * j + 1] = __builtin_amdgcn_fmed3f(__uint_as_float(wv[2 * i + j] & 0xffff0000u) * inv, -448.0f, 448.0f);
+        }
+        const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false);
+        wd[i] = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], lo, true));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float x[4];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          x[2 * j] = clampf(__uint_as_float(wv[2 * i + j] << 16) * inv, 448.0f);
+          x[2 * j + 1] = clampf(__uint_as_float(wv[2 * i + j] & 0xffff0000u) * inv, 448.0f);
+        }
+        const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(x[0], x[1], 0, false);
+        wd[i] = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(x[2], x[3], lo, true));
+      }
+    }
+    uint4* dst = reinterpret_cast<uint4*>(q_lds + qh * QP + 32 * qc);
+    dst[0] = uint4{wd[0], wd[1], wd[2], wd[3]};
+    dst[1] = uint4{wd[4], wd[5], wd[6], wd[7]};
+    if (qc == 0) qs_lds[qh] = sc;
+    __syncthreads();
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const uint4* src = reinterpret_cast<const uint4*>(q_lds + (mb * 32 + (lane & 31)) * QP);
+#pragma unroll
+      for (int st = 0; st < NST; ++st) {
+        const uint4 u = src[4 * st + 2 * hi], v = src[4 * st + 2 * hi + 1];
+        a[mb][st].v = v8i{(int)u.x, (int)u.y, (int)u.z, (int)u.w, (int)v.x, (int)v.y, (int)v.z, (int)v.w};
+        a[mb][st].scale = 127;
+      }
+    }
+    cq = qs_lds[hl];
+  }
+}
+
+// ---- the merged emission + scores launch (EMIT) ------------------------------------------
+
+// Loads through the constant address space: with a workgroup-uniform address they become
+// scalar loads, which wait on their own counter and leave the in-order vector loads (and the
+// waits the score loop counts on them) alone.  Only for data no launch of the step writes
+// before this one ends (the positions, the position table).
+typedef const __attribute__((address_space(4))) uint32_t* const_u32_ptr;
+typedef const __attribute__((address_space(4))) int64_t* const_i64_ptr;
+
+// Row `pos` of the position table (clamped into it: the host refuses positions beyond the
+// table) as 32 words: cos of pairs 0..31 (bf16, pair j in the low half of word j / 2 for even
+// j) in words 0..15, sin in words 16..31; scalar loads.
+__device__ __forceinline__ void load_table_row(const EmitParams& e, int64_t pos, uint32_t (&tw)[kRopePairs]) {
+  const int64_t r = pos < 0 ? 0 : (pos >= e.tab_rows ? e.tab_rows - 1 : pos);
+  const const_u32_ptr src = (const_u32_ptr)(e.tab + r * 2 * kRopePairs);
+#pragma unroll
+  for (int i = 0; i < kRopePairs; ++i) tw[i] = src[i];
+}
+
+// The merged launch's compress ratio (emit_row<kEmitRatio>).
+constexpr int kEmitRatio = 4;
+
+// The group whose index key the step at position pos emits (emit_row's condition), or -1.
+__device__ __forceinline__ int64_t emitted_group(const EmitParams& e, int64_t pos) {
+  if (pos < 0 || (pos + 1) % kEmitRatio != 0 || e.br.wk == nullptr) return -1;
+  const int64_t g = (pos + 1) / kEmitRatio - 1;
+  return (g < e.br.cache_cap && g * kEmitRatio < e.tab_rows) ? g : -1;
+}
+
+// RoPE of the query's trailing 64 channels (owlet1/indexer.py:126-128) with the table row's
+// words: thread (head, qc) holds channels 32 qc .. 32 qc + 31, so qc = 2 rotates pairs 0..15
+// and qc = 3 pairs 16..31 (pair j = channels 64 + 2j, 65 + 2j) -- the fused prologue's
+// per-pair arithmetic (rope_pair_bf16).
+__device__ __forceinline__ void rope_query_table(uint4 (&qr)[4], int qc, const uint32_t (&tw)[kRopePairs]) {
+  if (qc < 2) return;
+  const bool upper = qc == 3;
+  uint32_t* wq = reinterpret_cast<uint32_t*>(qr);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const uint32_t cp = upper ? tw[8 + (k >> 1)] : tw[k >> 1];
+    const uint32_t sp = upper ? tw[24 + (k >> 1)] : tw[16 + (k >> 1)];
+    wq[k] = rope_pair_bf16(wq[k], __uint_as_float((k & 1) ? cp & 0xffff0000u : cp << 16),
+                           __uint_as_float((k & 1) ? sp & 0xffff0000u : sp << 16));
+  }
+}
+
+// Workgroup 0 of a row in the merged launch: the row's emission (emit_row), then, when the
+// step emitted index key g (< G), that key's score.  The score is computed as a scoring
+// workgroup computes it -- the same query quantization into the same A fragments, one 32x32
+// MFMA tile whose 32 key columns all hold key g (its codes straight from LDS), the same
+// ReLU-weighted head sum -- so its bits are those the separate emission + scores launches
+// give.
+template <int FMT, int MB>
+__device__ __forceinline__ void emit_and_score(const IdxParams& p, const EmitParams& e, int64_t row) {
+  constexpr int NST = kDi / Step<FMT>::K;
+  __shared__ __align__(16) uint8_t key_lds[kDi + 16];
+  __shared__ __align__(16) uint8_t q_lds[64 * q_pitch<FMT>()];
+  __shared__ float qs_lds[FMT == kFp8 ? 64 : 1];
+  __shared__ uint8_t qe_lds[FMT == kMxfp4 ? 256 : 4];
+  const int tid = threadIdx.x, lane = tid & 63, hi = lane >> 5;
+  const int qh = tid >> 2, qc = tid & 3;
+  const int Hi = p.Hi;
+  // the query, its head weight and the token's RoPE tables are requested before the
+  // emission, so they have arrived when it ends
+  const int64_t pos = *(const_i64_ptr)(e.positions + row);
+  uint4 qr[4];
+  const int hq = qh < Hi ? qh : Hi - 1;
+  const uint4* src = reinterpret_cast<const uint4*>(p.q_raw + (row * Hi + hq) * kDi + 32 * qc);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) qr[i] = src[i];
+  const int hl = lane < Hi ? lane : Hi - 1;
+  float cw = p.w[row * Hi + hl];
+  uint32_t tw[kRopePairs];
+  load_table_row(e, pos, tw);
+  if (!emit_row<kEmitRatio>(e, row, key_lds)) return;  // uniform
+  const int64_t g = (pos + 1) / kEmitRatio - 1;
+  if (g >= p.G) return;
+  cw = lane < Hi ? cw : 0.0f;
+  rope_query_table(qr, qc, tw);
+  Frag a[MB][NST];
+  float cq = 1.0f;
+  quantize_query<FMT, kDi, MB>(qr, qh, qc, Hi, lane, hi, hl, q_lds, qs_lds, qe_lds, a, cq);
+  if (tid >= 64) return;  // one wave scores the key (the key bytes were stored before the barrier above)
+  const float cwq = cw * cq;
+  float coef[MB][16];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) coef[mb][j] = __shfl(cwq, mb * 32 + acc_row(j, lane), 64);
+  Frag bk[NST];
+#pragma unroll
+  for (int st = 0; st < NST; ++st) bk[st] = load_frag<FMT, kDi>(key_lds, key_lds + kDi / 2, st, hi);
+  float part = 0.0f;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    v16f acc = {};
+#pragma unroll
+    for (int st = 0; st < NST; ++st) acc = mma<FMT>(a[mb][st], bk[st], acc);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) part = relu_fma(coef[mb][j], acc[j], part);
+  }
+  const float total = part + __shfl_xor(part, 32, 64);
+  float s = total * (1.0f / sqrt_rn(static_cast<float>(kDi)));
+  if constexpr (FMT == kFp8) s = s * *reinterpret_cast<const float*>(key_lds + kDi);
+  if (lane == 0) p.scores[row * p.sstride + g] = s;
+}
+
+// One workgroup = 4 waves = one query row x 4 * NKB * 32 keys (see the tiling note above).
 // QRAW: the query arrives as bf16 [Hi, 128] and each workgroup quantizes it into LDS --
-// thread t owns head t/4, channels 32(t%4)..+31.  FP8 b128 (owlet1/quant.py:72-86: one
-// power-of-two scale per head) uses v_cvt_pk_fp8_f32, which equals the e4m3 encoder of the
-// quantizer (round to nearest even, subnormals kept) for every |x| <= 448.  MXFP4
-// (quant.py:49-66 with block 32 and ue8m0 scales): a thread's 32 channels are one scale
-// block, encoded with the quantizer's own e2m1 thresholds, and exactly one lane's MFMA
-// fragment (16 bytes of nibbles + the e8m0 byte).
+// thread t owns head t/4, channels 32(t%4)..+31 (quantize_query).  FP8 b128
+// (owlet1/quant.py:72-86: one power-of-two scale per head) uses v_cvt_pk_fp8_f32, which
+// equals the e4m3 encoder of the quantizer (round to nearest even, subnormals kept) for
+// every |x| <= 448.  MXFP4 (quant.py:49-66 with block 32 and ue8m0 scales): a thread's 32
+// channels are one scale block and exactly one lane's MFMA fragment (16 bytes of nibbles +
+// the e8m0 byte).
 // APPEND: workgroup 0 of the row also writes the new token's FP8-b128 latent into its
 // window-ring slot (b * win_batch_entries + pos % win_cap).
 // FUSE: the query is rotated before it is quantized, and wave 0 of each row's workgroup 0
 // runs the kv prologue (FusedKv): loads before the keys', the work after the query's
 // quantization.
-template <int FMT, int DI, int MB, bool QRAW, bool APPEND, bool FUSE = false, bool GATHER = false>
-__global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxParams p) {
+// EMIT (with FUSE; one query row per batch row, ratio 4): the step's group emission joins
+// the launch.  Per row, workgroup 0 runs the emission (emit_row: carry slot, step tables,
+// and on a group step the group's entry and index key) and then scores the new key itself
+// (emit_and_score), workgroup 1 writes the token's window entry (kv_prologue), and the
+// scoring workgroups start at 2; they take the query's RoPE tables from row `pos` of the
+// position table and leave the new key's score to workgroup 0.
+template <int FMT, int DI, int MB, bool QRAW, bool APPEND, bool FUSE = false, bool GATHER = false, bool EMIT = false,
+          int NKB = kNkb>
+__global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxParams p, const EmitParams e) {
   static_assert(!QRAW || ((FMT == kFp8 || FMT == kMxfp4) && DI == 128), "in-kernel quantization: Di = 128");
   static_assert(!FUSE || (QRAW && !APPEND), "the fused prologue quantizes the raw query and appends on its own");
   static_assert(!GATHER || !QRAW, "the candidate scorer takes the quantized query");
+  static_assert(!EMIT || (FUSE && DI == kDi), "the merged emission takes the fused prologue's query, Di = 128");
   constexpr int QP = q_pitch<FMT>();
   constexpr int NST = DI / Step<FMT>::K;
   constexpr int RB = row_bytes<FMT>(DI);
@@ -282,7 +532,18 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
   const uint8_t* ke_base = FMT == kMxfp4 ? p.k_e8m0 + b * p.kbs * (DI / 32) : nullptr;
   float* out = p.scores + row * p.sstride;
 
-  const int64_t wave_key0 = static_cast<int64_t>(blockIdx.x) * kKeysPerWg + wave * (kNkb * 32);
+  if constexpr (EMIT) {
+    if (blockIdx.x == 0) {  // uniform: the row's emission
+      emit_and_score<FMT, MB>(p, e, row);
+      return;
+    }
+    if (blockIdx.x == 1) {  // uniform: the token's window entry
+      if (tid < 64) kv_prologue(e, row, tid);
+      return;
+    }
+  }
+  const int64_t wave_key0 =
+      (static_cast<int64_t>(blockIdx.x) - (EMIT ? 2 : 0)) * (kWaves * NKB * 32) + wave * (NKB * 32);
   // Load order.  Vector-memory loads complete in issue order, so the small operands every
   // tile needs -- the query (fragments, or the bf16 rows to quantize) and the head
   // weights -- go first; then all key fragments of the wave's tiles, so tile 0's MFMAs
@@ -292,13 +553,15 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
   Frag a[MB][NST];
   uint4 qr[4];  // QRAW: 32 bf16 channels of head tid/4
   uint4 qtab = uint4{0u, 0u, 0u, 0u};  // FUSE: 16 bytes of the row's query cos / sin tables
+  uint32_t tw[EMIT ? kRopePairs : 1];  // EMIT: the row's table row (cos | sin), uniform
+  int64_t epos = 0;                     // EMIT: the row's position (a scalar load)
   const int qh = tid >> 2, qc = tid & 3;
   if constexpr (QRAW) {
     const int hq = qh < Hi ? qh : Hi - 1;
     const uint4* src = reinterpret_cast<const uint4*>(p.q_raw + (row * Hi + hq) * 128 + 32 * qc);
 #pragma unroll
     for (int i = 0; i < 4; ++i) qr[i] = src[i];
-    if constexpr (FUSE) {
+    if constexpr (FUSE && !EMIT) {
       // the row's cos then sin tables (q_rope_dim / 16 pieces of 16 bytes each), one piece
       // per thread of the first 2 * q_rope_dim / 16; the rest read piece 0 and drop it
       const int n4 = p.q_rope_dim / 16;
@@ -327,24 +590,24 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
   // FUSE: the kv prologue's operands come after the query's (whose wait ends in a barrier of
   // the whole workgroup) and before the keys (which the score loop waits for)
   FusedKv fkv;
-  if constexpr (FUSE) {
+  if constexpr (FUSE && !EMIT) {
     if (blockIdx.x == 0 && tid < 64) fkv.load(p, row, tid);
   }
-  Frag bf[kNkb][NST];
-  float ksv[kNkb];  // FP8: the per-key scales
-  int32_t cblk[kNkb];  // GATHER: the candidate block of each tile's slot, all loaded first
+  Frag bf[NKB][NST];
+  float ksv[NKB];  // FP8: the per-key scales
+  int32_t cblk[NKB];  // GATHER: the candidate block of each tile's slot, all loaded first
   if constexpr (GATHER) {
     // (loads complete in order: list entries issued between key loads would make each
     // tile's key loads wait for the previous tile's keys)
 #pragma unroll
-    for (int t = 0; t < kNkb; ++t) {
+    for (int t = 0; t < NKB; ++t) {
       const int64_t g = wave_key0 + t * 32 + (lane & 31);
       const int64_t gc = g < G ? g : G - 1;  // slots at or beyond G: the row's last slot
       cblk[t] = p.cand[row * p.cand_stride + gc / p.cand_bs];
     }
   }
 #pragma unroll
-  for (int t = 0; t < kNkb; ++t) {
+  for (int t = 0; t < NKB; ++t) {
     // keys at or beyond G read row G-1 instead: their score columns are never written
     const int64_t g = wave_key0 + t * 32 + (lane & 31);
     int64_t gc = g < G ? g : G - 1;
@@ -370,17 +633,26 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
     kv_nope = *reinterpret_cast<const uint2*>(kvrow + 4 * tn);
     kv_rope = kvrow[p.nope + tr];
   }
-  const int64_t pos = p.positions ? p.positions[row] : row % p.S;
-  int64_t vis = (pos + 1) / p.ratio;
+  if constexpr (EMIT) {
+    // the row's position and RoPE tables, scalar loads issued behind the vector loads above
+    epos = *(const_i64_ptr)(p.positions + row);
+    load_table_row(e, epos, tw);
+  }
+  const int64_t pos = EMIT ? epos : (p.positions ? p.positions[row] : row % p.S);
+  int64_t vis = EMIT ? (pos + 1) / kEmitRatio : (pos + 1) / p.ratio;
   const int64_t nkeys = GATHER ? p.cand_keys : G;
   if (vis > nkeys) vis = nkeys;
   if (vis < 0) vis = 0;
+  // EMIT: the key the row's emission workgroup scores (-1: none), as emit_row decides
+  const int64_t g_own = EMIT ? emitted_group(e, pos) : -1;
 
   __shared__ __align__(16) uint8_t q_lds[QRAW ? 64 * QP : 16];
   __shared__ float qs_lds[QRAW && FMT == kFp8 ? 64 : 1];
   __shared__ uint8_t qe_lds[QRAW && FMT == kMxfp4 ? 256 : 4];
-  __shared__ uint4 qtab_lds[FUSE ? 16 : 1];
-  if constexpr (FUSE) {
+  __shared__ uint4 qtab_lds[FUSE && !EMIT ? 16 : 1];
+  if constexpr (EMIT) {
+    rope_query_table(qr, qc, tw);
+  } else if constexpr (FUSE) {
     // RoPE of the query's rope channels (owlet1/indexer.py:126-128, compress cos / sin),
     // bf16 in and out as the reference's rotated query.  q_rope_dim is a multiple of 32, so
     // a thread's 32 channels are all rope or all nope.
@@ -404,95 +676,8 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
       }
     }
   }
-  if constexpr (QRAW && FMT == kMxfp4) {
-    // one MXFP4 block of 32 channels per thread: scale, then e2m1 codes (element 2i in the
-    // low nibble of byte i), as the quantizer's packed form
-    float amax = 0.0f;
-    uint32_t wd[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t wv[4] = {qr[i].x, qr[i].y, qr[i].z, qr[i].w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float lo = qh < Hi ? bf16_to_f32(static_cast<uint16_t>(wv[j] & 0xffffu)) : 0.0f;
-        const float hi2 = qh < Hi ? bf16_to_f32(static_cast<uint16_t>(wv[j] >> 16)) : 0.0f;
-        amax = nn_max(amax, nn_max(fabsf(lo), fabsf(hi2)));
-      }
-    }
-    const float sc = fp4_scale_from_amax(amax, false);
-    // x / sc == x * (1 / sc) exactly: sc is a power of two in [2^-126, 2^127], so 1 / sc is
-    // exact and both sides are the correctly rounded x * 2^-e
-    const float inv = sc <= 0x1p126f ? pow2_reciprocal(sc) : 1.0f / sc;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t wv[4] = {qr[i].x, qr[i].y, qr[i].z, qr[i].w};
-      uint32_t word = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float lo = qh < Hi ? bf16_to_f32(static_cast<uint16_t>(wv[j] & 0xffffu)) : 0.0f;
-        const float hi2 = qh < Hi ? bf16_to_f32(static_cast<uint16_t>(wv[j] >> 16)) : 0.0f;
-        word |= e2m1_code(clampf(lo * inv, 6.0f)) << (8 * j);
-        word |= e2m1_code(clampf(hi2 * inv, 6.0f)) << (8 * j + 4);
-      }
-      wd[i] = word;
-    }
-    *reinterpret_cast<uint4*>(q_lds + qh * QP + 16 * qc) = uint4{wd[0], wd[1], wd[2], wd[3]};
-    qe_lds[qh * 4 + qc] = static_cast<uint8_t>(__float_as_uint(sc) >> 23);
-    __syncthreads();
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const int h = mb * 32 + (lane & 31);
-#pragma unroll
-      for (int st = 0; st < NST; ++st) {
-        const uint4 u = *reinterpret_cast<const uint4*>(q_lds + h * QP + st * 32 + hi * 16);
-        a[mb][st].v = v8i{(int)u.x, (int)u.y, (int)u.z, (int)u.w, 0, 0, 0, 0};
-        a[mb][st].scale = qe_lds[h * 4 + st * 2 + hi];
-      }
-    }
-  } else if constexpr (QRAW) {
-    float x[32];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t wv[4] = {qr[i].x, qr[i].y, qr[i].z, qr[i].w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        x[8 * i + 2 * j] = qh < Hi ? bf16_to_f32(static_cast<uint16_t>(wv[j] & 0xffffu)) : 0.0f;
-        x[8 * i + 2 * j + 1] = qh < Hi ? bf16_to_f32(static_cast<uint16_t>(wv[j] >> 16)) : 0.0f;
-      }
-    }
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) amax = nn_max(amax, fabsf(x[i]));
-    amax = group_max(amax, 4);  // the 4 threads of a head are consecutive lanes
-    const float sc = fp8_scale_from_amax(amax);
-    // x / sc == x * (1 / sc) exactly: sc is a power of two, in [2^-22, 2^120] for finite input
-    const float inv = sc <= 0x1p120f ? pow2_reciprocal(sc) : 1.0f / sc;
-    uint32_t wd[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(clampf(x[4 * i] * inv, 448.0f), clampf(x[4 * i + 1] * inv, 448.0f),
-                                                     0, false);
-      wd[i] = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(clampf(x[4 * i + 2] * inv, 448.0f),
-                                                                    clampf(x[4 * i + 3] * inv, 448.0f), lo, true));
-    }
-    uint4* dst = reinterpret_cast<uint4*>(q_lds + qh * QP + 32 * qc);
-    dst[0] = uint4{wd[0], wd[1], wd[2], wd[3]};
-    dst[1] = uint4{wd[4], wd[5], wd[6], wd[7]};
-    if (qc == 0) qs_lds[qh] = sc;
-    __syncthreads();
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const uint4* src = reinterpret_cast<const uint4*>(q_lds + (mb * 32 + (lane & 31)) * QP);
-#pragma unroll
-      for (int st = 0; st < NST; ++st) {
-        const uint4 u = src[4 * st + 2 * hi], v = src[4 * st + 2 * hi + 1];
-        a[mb][st].v = v8i{(int)u.x, (int)u.y, (int)u.z, (int)u.w, (int)v.x, (int)v.y, (int)v.z, (int)v.w};
-        a[mb][st].scale = 127;
-      }
-    }
-    cq = qs_lds[hl];
-  }
-  if constexpr (FUSE) {
+  if constexpr (QRAW) quantize_query<FMT, DI, MB>(qr, qh, qc, Hi, lane, hi, hl, q_lds, qs_lds, qe_lds, a, cq);
+  if constexpr (FUSE && !EMIT) {
     // the row's kv prologue, while the key loads are still in flight (its registers are
     // free again before the score loop)
     if (blockIdx.x == 0 && tid < 64) fkv.append(p, b, pos, tid);
@@ -505,7 +690,7 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
     for (int j = 0; j < 16; ++j) coef[mb][j] = __shfl(cwq, mb * 32 + acc_row(j, lane), 64);
 
 #pragma unroll
-  for (int t = 0; t < kNkb; ++t) {
+  for (int t = 0; t < NKB; ++t) {
     const int64_t g0 = wave_key0 + t * 32;
     const int64_t g = g0 + (lane & 31);
     if (g0 >= G) break;
@@ -523,7 +708,7 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
       for (int j = 0; j < 16; ++j) part = relu_fma(coef[mb][j], acc[j], part);
     }
     const float total = part + __shfl_xor(part, 32, 64);
-    if (lane < 32 && g < G) {
+    if (lane < 32 && g < G && (!EMIT || g != g_own)) {
       float s = total * inv_sqrt_di;
       if constexpr (FMT == kFp8) s = s * ksv[t];
       int64_t kpos = g;
@@ -559,7 +744,7 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
         // a negative position has no ring slot
         if (pos >= 0) {
           const int64_t entry_bytes = p.nope + 4 * (p.nope / 128) + 2 * p.rope;
-          uint8_t* e = p.win + (b * p.win_batch_entries + pos % p.win_cap) * entry_bytes;
+          uint8_t* ent = p.win + (b * p.win_batch_entries + pos % p.win_cap) * entry_bytes;
           if (tid < p.nope / 4) {
             const float v[4] = {bf16_to_f32(static_cast<uint16_t>(kv_nope.x & 0xffffu)),
                                 bf16_to_f32(static_cast<uint16_t>(kv_nope.x >> 16)),
@@ -571,15 +756,16 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
             uint32_t word = 0;
 #pragma unroll
             for (int i = 0; i < 4; ++i) word |= static_cast<uint32_t>(e4m3_encode(clampf(div_rn(v[i], sc), 448.0f))) << (8 * i);
-            reinterpret_cast<uint32_t*>(e)[tid] = word;
-            if ((tid & 31) == 0) reinterpret_cast<float*>(e + p.nope)[tid >> 5] = sc;
+            reinterpret_cast<uint32_t*>(ent)[tid] = word;
+            if ((tid & 31) == 0) reinterpret_cast<float*>(ent + p.nope)[tid >> 5] = sc;
           }
-          if (tid < p.rope) reinterpret_cast<uint16_t*>(e + p.nope + 4 * (p.nope / 128))[tid] = kv_rope;
+          if (tid < p.rope) reinterpret_cast<uint16_t*>(ent + p.nope + 4 * (p.nope / 128))[tid] = kv_rope;
         }
       }
     }
   }
 }
+
 
 // ------------------------------------------------------------------------------------
 // Prefill form (FP8, Di = 128): many query rows against the same keys.  The decode tiling
@@ -779,8 +965,8 @@ __global__ void __launch_bounds__(kWaves * 64, 2) indexer_prefill_fp8_kernel(con
 template <int FMT, int DI>
 int launch_di(const IdxParams& p, int64_t rows, hipStream_t s) {
   dim3 grid(static_cast<unsigned>((p.G + kKeysPerWg - 1) / kKeysPerWg), static_cast<unsigned>(rows));
-  if (p.Hi <= 32) indexer_scores_kernel<FMT, DI, 1, false, false><<<grid, kWaves * 64, 0, s>>>(p);
-  else indexer_scores_kernel<FMT, DI, 2, false, false><<<grid, kWaves * 64, 0, s>>>(p);
+  if (p.Hi <= 32) indexer_scores_kernel<FMT, DI, 1, false, false><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
+  else indexer_scores_kernel<FMT, DI, 2, false, false><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
   return MZK_OK;
 }
 
@@ -792,8 +978,8 @@ int launch_gather(const IdxParams& p, int64_t rows, int Di, hipStream_t s) {
     set_last_error("indexer_candidate_scores: index head dim must be 128 (got %d)", Di);
     return MZK_EUNSUPPORTED;
   }
-  if (p.Hi <= 32) indexer_scores_kernel<FMT, 128, 1, false, false, false, true><<<grid, kWaves * 64, 0, s>>>(p);
-  else indexer_scores_kernel<FMT, 128, 2, false, false, false, true><<<grid, kWaves * 64, 0, s>>>(p);
+  if (p.Hi <= 32) indexer_scores_kernel<FMT, 128, 1, false, false, false, true><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
+  else indexer_scores_kernel<FMT, 128, 2, false, false, false, true><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
   return MZK_OK;
 }
 
@@ -1001,11 +1187,11 @@ extern "C" int mzk_indexer_decode_fp8(const void* q_idx, const float* w, const u
   dim3 grid(static_cast<unsigned>((G + kKeysPerWg - 1) / kKeysPerWg), static_cast<unsigned>(B));
   hipStream_t s = as_stream(stream);
   if (Hi <= 32) {
-    if (kv) indexer_scores_kernel<kFp8, 128, 1, true, true><<<grid, kWaves * 64, 0, s>>>(p);
-    else indexer_scores_kernel<kFp8, 128, 1, true, false><<<grid, kWaves * 64, 0, s>>>(p);
+    if (kv) indexer_scores_kernel<kFp8, 128, 1, true, true><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
+    else indexer_scores_kernel<kFp8, 128, 1, true, false><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
   } else {
-    if (kv) indexer_scores_kernel<kFp8, 128, 2, true, true><<<grid, kWaves * 64, 0, s>>>(p);
-    else indexer_scores_kernel<kFp8, 128, 2, true, false><<<grid, kWaves * 64, 0, s>>>(p);
+    if (kv) indexer_scores_kernel<kFp8, 128, 2, true, true><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
+    else indexer_scores_kernel<kFp8, 128, 2, true, false><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
   }
   MZK_LAUNCH_CHECK("indexer_decode_fp8");
   return MZK_OK;
@@ -1048,11 +1234,11 @@ extern "C" int mzk_indexer_decode_mxfp4(const void* q_idx, const float* w, const
   dim3 grid(static_cast<unsigned>((G + kKeysPerWg - 1) / kKeysPerWg), static_cast<unsigned>(B));
   hipStream_t s = as_stream(stream);
   if (Hi <= 32) {
-    if (kv) indexer_scores_kernel<kMxfp4, 128, 1, true, true><<<grid, kWaves * 64, 0, s>>>(p);
-    else indexer_scores_kernel<kMxfp4, 128, 1, true, false><<<grid, kWaves * 64, 0, s>>>(p);
+    if (kv) indexer_scores_kernel<kMxfp4, 128, 1, true, true><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
+    else indexer_scores_kernel<kMxfp4, 128, 1, true, false><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
   } else {
-    if (kv) indexer_scores_kernel<kMxfp4, 128, 2, true, true><<<grid, kWaves * 64, 0, s>>>(p);
-    else indexer_scores_kernel<kMxfp4, 128, 2, true, false><<<grid, kWaves * 64, 0, s>>>(p);
+    if (kv) indexer_scores_kernel<kMxfp4, 128, 2, true, true><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
+    else indexer_scores_kernel<kMxfp4, 128, 2, true, false><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
   }
   MZK_LAUNCH_CHECK("indexer_decode_mxfp4");
   return MZK_OK;
@@ -1110,13 +1296,67 @@ extern "C" int mzk_indexer_decode_fused(int q_format, const void* q_idx, const f
   dim3 grid(static_cast<unsigned>((G + kKeysPerWg - 1) / kKeysPerWg), static_cast<unsigned>(B));
   hipStream_t s = as_stream(stream);
   if (fp8) {
-    if (Hi <= 32) indexer_scores_kernel<kFp8, 128, 1, true, false, true><<<grid, kWaves * 64, 0, s>>>(p);
-    else indexer_scores_kernel<kFp8, 128, 2, true, false, true><<<grid, kWaves * 64, 0, s>>>(p);
+    if (Hi <= 32) indexer_scores_kernel<kFp8, 128, 1, true, false, true><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
+    else indexer_scores_kernel<kFp8, 128, 2, true, false, true><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
   } else {
-    if (Hi <= 32) indexer_scores_kernel<kMxfp4, 128, 1, true, false, true><<<grid, kWaves * 64, 0, s>>>(p);
-    else indexer_scores_kernel<kMxfp4, 128, 2, true, false, true><<<grid, kWaves * 64, 0, s>>>(p);
+    if (Hi <= 32) indexer_scores_kernel<kMxfp4, 128, 1, true, false, true><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
+    else indexer_scores_kernel<kMxfp4, 128, 2, true, false, true><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
   }
   MZK_LAUNCH_CHECK("indexer_decode_fused");
+  return MZK_OK;
+}
+
+// The decode step's group emission and indexer scores in one launch (the EMIT scorer, grid
+// (2 + ceil(G / 512), B)):
+// mzk_decode_emit's arguments for the fine branch (ratio 4, with the index key and the kv
+// prologue; the scoring workgroups quantize the indexer query themselves, so it has no
+// q_codes / q_scales outputs), then the scorer's: q_idx bf16 [B, Hi, 128] (unrotated; its
+// RoPE from the table row of the token's position), w fp32 [B, Hi], G keys per row (key
+// batch stride key_batch_entries, the key format of the emission), scores fp32 [B,
+// score_stride].
+extern "C" int mzk_decode_emit_scores(const int64_t* positions, int64_t B, const float* kv, const float* gate,
+                                      float* carry_kv, float* carry_gate, int ratio, const void* norm_weight, float eps,
+                                      uint8_t* cache, int64_t cache_batch_entries, int64_t cache_cap, const void* wk,
+                                      const void* k_norm_weight, float k_eps, int key_format, uint8_t* k_codes,
+                                      void* k_scales, int64_t key_batch_entries, const void* rope_table,
+                                      int64_t table_rows, void* step_cos, void* step_sin, const void* kv_proj,
+                                      const void* kv_weight, float kv_eps, uint8_t* win_cache, int64_t win_batch_entries,
+                                      int win_cap, const void* q_idx, const float* w, int Hi, int64_t G, float* scores,
+                                      int64_t score_stride, void* stream) {
+  MZK_CHECK_ARG(ratio == 4, "decode_emit_scores: the merged launch takes compress ratio 4 (got %d)", ratio);
+  MZK_CHECK_ARG(wk && kv_proj && q_idx && w && scores,
+                "decode_emit_scores: needs the index key weights, the kv prologue, q_idx, w and scores");
+  EmitParams e;
+  int rc = build_emit(positions, B, kv, gate, carry_kv, carry_gate, ratio, norm_weight, eps, cache,
+                      cache_batch_entries, cache_cap, wk, k_norm_weight, k_eps, key_format, k_codes, k_scales,
+                      key_batch_entries, rope_table, table_rows, step_cos, step_sin, kv_proj, kv_weight, kv_eps,
+                      win_cache, win_batch_entries, win_cap, nullptr, 0, nullptr, nullptr, e);
+  if (rc) return rc;
+  rc = check_common(B, 1, Hi, kDi, G, key_batch_entries, ratio, score_stride);
+  if (rc) return rc;
+  if (B == 0) return MZK_OK;
+  MZK_CHECK_ARG(G >= 1, "decode_emit_scores: at least one key group is required");
+  MZK_CHECK_ARG(B <= 65535, "decode_emit_scores: at most 65535 rows (got %lld)", (long long)B);
+  MZK_CHECK_ARG(aligned16(q_idx), "decode_emit_scores: q_idx must be 16-byte aligned");
+  const bool fp8 = key_format == 0;
+  IdxParams p = make_params(nullptr, nullptr, nullptr, w, k_codes, fp8 ? static_cast<const float*>(k_scales) : nullptr,
+                            fp8 ? nullptr : static_cast<const uint8_t*>(k_scales), 1, Hi, G, key_batch_entries,
+                            positions, ratio, scores, score_stride);
+  p.q_raw = static_cast<const uint16_t*>(q_idx);
+  p.q_rope_dim = 2 * kRopePairs;
+  // five key tiles per wave (640 keys per workgroup): with the two extra workgroups per row
+  // the grid stays within one round of resident workgroups where four tiles would overflow it
+  constexpr int kEmitNkb = 5, kEmitKeys = kWaves * kEmitNkb * 32;
+  dim3 grid(static_cast<unsigned>(2 + (G + kEmitKeys - 1) / kEmitKeys), static_cast<unsigned>(B));
+  hipStream_t s = as_stream(stream);
+  if (fp8) {
+    if (Hi <= 32) indexer_scores_kernel<kFp8, kDi, 1, true, false, true, false, true, kEmitNkb><<<grid, kWaves * 64, 0, s>>>(p, e);
+    else indexer_scores_kernel<kFp8, kDi, 2, true, false, true, false, true, kEmitNkb><<<grid, kWaves * 64, 0, s>>>(p, e);
+  } else {
+    if (Hi <= 32) indexer_scores_kernel<kMxfp4, kDi, 1, true, false, true, false, true, kEmitNkb><<<grid, kWaves * 64, 0, s>>>(p, e);
+    else indexer_scores_kernel<kMxfp4, kDi, 2, true, false, true, false, true, kEmitNkb><<<grid, kWaves * 64, 0, s>>>(p, e);
+  }
+  MZK_LAUNCH_CHECK("decode_emit_scores");
   return MZK_OK;
 }
 

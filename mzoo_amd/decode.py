@@ -130,6 +130,10 @@ class DecodeConfig:
     # default: replayed in a graph the extra launch and the join cost more than the overlap
     # gains (config 2: 86.5 vs 74.3 us per layer, config 5: 83.9 vs 77.5)
     branch_overlap: bool = False
+    # with in-step emission (rope="table"), ratio 4 and no coarse branch: the emission joins
+    # the indexer launch (one workgroup per row emits the group and scores the new key) --
+    # one launch less per step; False keeps the emission launch of its own
+    merged_emit: bool = True
 
     @property
     def dim(self) -> int:
@@ -321,6 +325,39 @@ class SparseDecodeLayer:
                   self.coarse_carry_gate.data_ptr(), cfg.coarse_ratio, cw.coarse_norm_weight.data_ptr(), cw.eps,
                   self.coarse.data_ptr(), cfg.coarse_groups, cfg.coarse_groups, st)
 
+    def _emit_scores(self, compress, kv, q_idx, w) -> None:
+        """The emission and the indexer scores in one launch (``mzk_decode_emit_scores``): per
+        row one workgroup carries the token and emits a completed group (scoring its new key
+        itself), one writes the window entry, and the scoring workgroups rotate and quantize
+        the indexer query themselves."""
+        cfg, cw = self.cfg, self.compressor
+        b = cfg.batch
+        fp8 = cfg.index_format == "fp8"
+        if len(compress) != 2:
+            raise ValueError("step(compress=...): (kv, gate) for a layer without a coarse branch")
+        ckv, gate = (t.contiguous() for t in compress)
+        for t in (ckv, gate):
+            if t.dtype != torch.float32 or t.shape != (b, cfg.dim):
+                raise ValueError(f"step(compress=...): fp32 [{b}, {cfg.dim}] projections expected")
+        if kv.dtype != torch.bfloat16 or kv.shape != (b, cfg.dim):
+            raise ValueError(f"step: kv must be a contiguous bf16 [{b}, {cfg.dim}] projection")
+        if q_idx.dtype != torch.bfloat16 or q_idx.shape != (b, cfg.index_heads, cfg.index_dim):
+            raise ValueError(f"step: q_idx must be a contiguous bf16 [{b}, {cfg.index_heads}, {cfg.index_dim}] tensor")
+        wc = w.reshape(b, cfg.index_heads)
+        if wc.dtype != torch.float32:
+            raise ValueError("step: w must be fp32")
+        wc = wc.contiguous()
+        _lib.require_gpu(ckv, gate, kv, q_idx, wc)
+        keys = (self.k_codes, self.k_scales) if fp8 else (self.k_packed, self.k_e8m0)
+        _lib.call("mzk_decode_emit_scores", self.positions.data_ptr(), b, ckv.data_ptr(), gate.data_ptr(),
+                  self.carry_kv.data_ptr(), self.carry_gate.data_ptr(), cfg.ratio, cw.norm_weight.data_ptr(), cw.eps,
+                  self.main.data_ptr(), cfg.max_groups, cfg.max_groups, cw.wk.data_ptr(), cw.k_norm_weight.data_ptr(),
+                  cw.k_eps, 0 if fp8 else 1, keys[0].data_ptr(), keys[1].data_ptr(), cfg.max_groups,
+                  self.rope_table.data_ptr(), self.rope_table.shape[0], self.step_cos.data_ptr(),
+                  self.step_sin.data_ptr(), kv.data_ptr(), self.kv_norm_weight.data_ptr(), self.kv_norm_eps,
+                  self.win.data_ptr(), cfg.window, cfg.window, q_idx.data_ptr(), wc.data_ptr(), cfg.index_heads,
+                  cfg.max_groups, self.scores.data_ptr(), cfg.max_groups, _lib.stream_of(self.positions))
+
     def fill_coarse(self, latents: torch.Tensor) -> None:
         """latents [B, n, D] -> coarse entries 0..n-1 of every row."""
         n = latents.shape[1]
@@ -362,6 +399,12 @@ class SparseDecodeLayer:
         if from_table and self._emit_prologue:
             if kvc is None or self.kv_norm_weight is None:
                 raise ValueError("step(rope='table'): needs the kv projection and the layer's kv_norm_weight")
+            if cfg.merged_emit and cfg.ratio == 4 and not cfg.coarse_ratio:
+                self._emit_scores(compress, kvc, q_idx.contiguous(), w)
+                self._select_and_attend(q, (self.step_cos, self.step_sin))
+                if advance:
+                    self.positions.add_(1)
+                return self.out if self.out_proj is None else self.out_proj(self.out)
             self._emit(compress, True, prologue=(kvc, q_idx.contiguous()))
             pos = self.positions.view(b, 1)
             if fp8:

@@ -25,7 +25,7 @@ from mzoo_amd.decode import CompressorWeights, DecodeConfig, SparseDecodeLayer
 from oracle import attention as OA
 from oracle import compressor as C
 from oracle import quant as Q
-from tests.helpers import assert_attn_close, assert_topk_sets_match
+from tests.helpers import assert_attn_close, assert_scores_close, assert_topk_sets_match
 
 pytestmark = pytest.mark.gpu
 
@@ -61,21 +61,24 @@ def _emit_history(kv, gate, ratio, ngroups, nw, cos_t, sin_t, wk=None, kw=None):
     return np.stack(rots, 1), (np.stack(keys, 1) if wk is not None else None)
 
 
-@pytest.mark.parametrize("fmt,coarse", [("fp8", False), ("mxfp4", False), ("mxfp4", 8), ("fp8", 40)])
-def test_replays_across_group_boundaries(dev, fmt, coarse):
+@pytest.mark.parametrize("fmt,coarse,merged", [("fp8", False, True), ("fp8", False, False), ("mxfp4", False, True),
+                                               ("mxfp4", 8, True), ("fp8", 40, True)])
+def test_replays_across_group_boundaries(dev, fmt, coarse, merged):
     """``coarse``: the coarse branch's ratio (40: its carried slots stream through the
-    kernel in more than one batch, the last one partial)."""
+    kernel in more than one batch, the last one partial).  ``merged``: without a coarse
+    branch, the emission runs inside the indexer launch (``DecodeConfig.merged_emit``);
+    otherwise in a launch of its own, whose prologue also writes the quantized query."""
     b, ratio, gcap, topk, p0, steps = 3, 4, 64, 16, 150, 11
     cratio, cgroups = (coarse, 32) if coarse else (0, 0)
     gen = torch.Generator().manual_seed(31 + bool(coarse))
     rnd = lambda *s: torch.randn(*s, generator=gen)  # noqa: E731
-    print(f"emission replay: fmt={fmt} coarse={coarse} positions {p0}..{p0 + steps - 1}", flush=True)
+    print(f"emission replay: fmt={fmt} coarse={coarse} merged={merged} positions {p0}..{p0 + steps - 1}", flush=True)
     nw, kvw = _bf(1 + 0.1 * rnd(D).numpy()), _bf(1 + 0.1 * rnd(D).numpy())
     wk, kw = _bf(0.04 * rnd(DI, D).numpy()), _bf(1 + 0.1 * rnd(DI).numpy())
     cnw = _bf(1 + 0.1 * rnd(D).numpy())
     sinks = rnd(128)
     cfg = DecodeConfig(batch=b, max_groups=gcap, topk=topk, index_format=fmt, nsplit=2, coarse_ratio=cratio,
-                       coarse_groups=cgroups)
+                       coarse_groups=cgroups, merged_emit=merged)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a))  # noqa: E731
     cw = CompressorWeights(t(nw), t(wk), t(kw), 1e-6, 1e-6, t(cnw) if coarse else None, THETA_C)
     layer = SparseDecodeLayer(cfg, dev, sinks=sinks, kv_norm_weight=t(kvw), kv_norm_eps=1e-6, compressor=cw)
@@ -166,12 +169,13 @@ def test_replays_across_group_boundaries(dev, fmt, coarse):
             assert np.array_equal(layer.coarse.cpu().numpy(), coarse_ent), f"step {i}: coarse cache"
         # indexer + top-k
         q_rot = C.rope(q_idx, cs[:, None], sn[:, None], dtype="bfloat16")
-        # the quantized indexer query the emission launch's prologue wrote
-        qa, qsc = _keys(q_rot, fmt)
-        gq = layer.q_codes.cpu().numpy().reshape(qa.shape)
-        gqs = (layer.q_scales if fmt == "fp8" else layer.q_e8m0).cpu().numpy().reshape(qsc.shape)
-        assert np.array_equal(gq, qa), f"step {i}: indexer query codes"
-        assert np.array_equal(gqs.view(np.uint8), qsc.view(np.uint8)), f"step {i}: indexer query scales"
+        if coarse or not merged:
+            # the quantized indexer query the emission launch's prologue wrote
+            qa, qsc = _keys(q_rot, fmt)
+            gq = layer.q_codes.cpu().numpy().reshape(qa.shape)
+            gqs = (layer.q_scales if fmt == "fp8" else layer.q_e8m0).cpu().numpy().reshape(qsc.shape)
+            assert np.array_equal(gq, qa), f"step {i}: indexer query codes"
+            assert np.array_equal(gqs.view(np.uint8), qsc.view(np.uint8)), f"step {i}: indexer query scales"
         qd = Q.fake_quant_fp8_block(q_rot, 128) if fmt == "fp8" else Q.fake_quant_fp4_block(q_rot, 32)
         kd = _dequant_keys(key_a, key_s, fmt)
         posv = torch.full((b, 1), pos)
@@ -179,6 +183,7 @@ def test_replays_across_group_boundaries(dev, fmt, coarse):
                                ratio, posv)
         mag = OA.indexer_abs_scores(torch.from_numpy(qd)[:, None], torch.from_numpy(kd),
                                     torch.from_numpy(w)[:, None], ratio, posv)
+        assert_scores_close(layer.scores[:, 0].cpu(), sc[:, 0], mag[:, 0])
         assert_topk_sets_match(layer.idx, sc[:, 0], mag[:, 0], topk)
         # attention over the window, the coarse entries and the GPU's own selection
         wd = Q.unpack_latent_fp8_b128(win)
@@ -320,3 +325,74 @@ def test_emission_pair_equals_two_launches(dev):
             assert torch.equal(pair[name], two[name]), f"step {step}: {name} differs"
     # groups of both branches were written
     assert pair["main"].any() and pair["coarse"].any() and pair["kc"].any()
+
+
+@pytest.mark.parametrize("fmt,hi", [("fp8", 64), ("mxfp4", 64), ("fp8", 32), ("mxfp4", 20)])
+def test_emit_scores_equals_two_launches(dev, fmt, hi):
+    """``mzk_decode_emit_scores`` (the emission, the window entry, the indexer query's RoPE +
+    quantization and the scores in one launch, the new key scored by its emission workgroup)
+    writes what the emission launch followed by the fused scorer (``mzk_decode_emit`` +
+    ``mzk_indexer_decode_fused`` on the step's tables) writes, bit for bit -- carry, main cache,
+    keys, window ring, step tables and every score -- over steps that complete groups and steps
+    that only carry, with an inactive row (position -1) and a key axis of several scoring
+    workgroups with a partial last one."""
+    from mzoo_amd import _lib
+    b, ratio, cap, wcap, rows_tab = 5, 4, 1100, 16, 4 * 1100 + 8
+    rng = np.random.default_rng(5 + hi)
+    tab = _bf(rng.uniform(-1, 1, (rows_tab, 64)).astype(np.float32))
+    nw = _bf(rng.uniform(0.5, 1.5, D).astype(np.float32))
+    kvw = _bf(rng.uniform(0.5, 1.5, D).astype(np.float32))
+    wk = _bf(rng.normal(0, 0.05, (DI, D)).astype(np.float32))
+    kw = _bf(rng.uniform(0.5, 1.5, DI).astype(np.float32))
+    bf16 = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).bfloat16().to(dev)  # noqa: E731
+    dv = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731  (keeps the dtype)
+    tab_d, nw_d, kvw_d, wk_d, kw_d = bf16(tab), bf16(nw), bf16(kvw), bf16(wk), bf16(kw)
+    ka, ks = _keys(_bf(rng.normal(0, 1, (b, cap, DI)).astype(np.float32)), fmt)
+    fp8 = fmt == "fp8"
+
+    def state():
+        return dict(ckv=torch.zeros(b, ratio, D, device=dev), cgt=torch.zeros(b, ratio, D, device=dev),
+                    main=torch.zeros(b, cap, 656, dtype=torch.uint8, device=dev),
+                    ka=dv(ka), ks=dv(ks), win=torch.zeros(b, wcap, 656, dtype=torch.uint8, device=dev),
+                    scos=torch.zeros(b, 32, dtype=torch.bfloat16, device=dev),
+                    ssin=torch.zeros(b, 32, dtype=torch.bfloat16, device=dev),
+                    scores=torch.full((b, cap), 7.0, device=dev))
+
+    one, two = state(), state()
+    start = np.array([-1, 0, 5, 13, 4 * 700 + 2], dtype=np.int64)
+    for step in range(2 * ratio + 1):
+        print(f"emit+scores ({fmt}, Hi={hi}): step {step}", flush=True)
+        pos_d = dv(start + step)
+        kv, gt = dv(rng.normal(0, 1, (b, D)).astype(np.float32)), dv(rng.normal(0, 2, (b, D)).astype(np.float32))
+        kvp = bf16(rng.normal(0, 3, (b, D)).astype(np.float32))
+        q_idx = bf16(rng.normal(0, 1, (b, hi, DI)).astype(np.float32))
+        w = dv((rng.normal(0, 1, (b, hi)) * hi ** -0.5).astype(np.float32))
+        st = _lib.stream_of(pos_d)
+        for s, merged in ((one, True), (two, False)):
+            emit = (pos_d.data_ptr(), b, kv.data_ptr(), gt.data_ptr(), s["ckv"].data_ptr(), s["cgt"].data_ptr(),
+                    ratio, nw_d.data_ptr(), 1e-6, s["main"].data_ptr(), cap, cap, wk_d.data_ptr(), kw_d.data_ptr(),
+                    1e-6, 0 if fp8 else 1, s["ka"].data_ptr(), s["ks"].data_ptr(), cap, tab_d.data_ptr(), rows_tab,
+                    s["scos"].data_ptr(), s["ssin"].data_ptr())
+            if merged:
+                _lib.call("mzk_decode_emit_scores", *emit, kvp.data_ptr(), kvw_d.data_ptr(), 1e-6,
+                          s["win"].data_ptr(), wcap, wcap, q_idx.data_ptr(), w.data_ptr(), hi, cap,
+                          s["scores"].data_ptr(), cap, st)
+            else:
+                _lib.call("mzk_decode_emit", *emit, None, None, 0.0, None, 0, 0, None, 0, None, None, st)
+                _lib.call("mzk_indexer_decode_fused", 0 if fp8 else 1, q_idx.data_ptr(), w.data_ptr(),
+                          s["ka"].data_ptr(), s["ks"].data_ptr(), b, hi, DI, cap, cap, pos_d.data_ptr(), ratio,
+                          s["scores"].data_ptr(), cap, None, None, s["scos"].data_ptr(), s["ssin"].data_ptr(), 64,
+                          kvp.data_ptr(), kvw_d.data_ptr(), 1e-6, s["scos"].data_ptr(), s["ssin"].data_ptr(), 512,
+                          64, s["win"].data_ptr(), wcap, wcap, st)
+        torch.cuda.synchronize()
+        for name in one:
+            a, c = one[name], two[name]
+            same = torch.equal(a.view(torch.int32), c.view(torch.int32)) if a.dtype == torch.float32 \
+                else torch.equal(a, c)
+            assert same, f"step {step}: {name} differs"
+    # groups were emitted and the window written; each row's last step scored exactly its
+    # visible keys, min(cap, (pos + 1) // ratio), the last of them emitted by that step or before
+    assert one["main"].any() and one["win"].any()
+    last = start + 2 * ratio
+    finite = torch.isfinite(one["scores"]).sum(1).cpu().numpy()
+    assert np.array_equal(finite, np.minimum(cap, (last + 1) // ratio)), finite

@@ -133,6 +133,79 @@ def test_decode_query_hardware_encoder_exhaustive(dev, path, which):
     _check_codes(q_codes.view(-1, 128), q_scales, q, f"{path}/{which}")
 
 
+def _fp4_domain_blocks() -> np.ndarray:
+    """[n, 128] fp32 (bf16-exact) rows of four MXFP4 blocks of 32: each block = 6 then 31
+    values, so its scale is exactly 1 and the encoder sees every finite bf16 t with |t| <= 6
+    (the saturating domain, bf16 subnormals and both zeros included) itself."""
+    v = _bf16_values(np.arange(1 << 16))
+    v = v[np.isfinite(v) & (np.abs(v) <= 6)]
+    per = 31
+    nb = -(-v.size // per)
+    nb = -(-nb // 4) * 4
+    body = np.zeros(nb * per, np.float32)
+    body[:v.size] = v
+    blocks = np.concatenate([np.full((nb, 1), 6.0, np.float32), body.reshape(nb, per)], 1)
+    return blocks.reshape(-1, 128)
+
+
+@pytest.mark.parametrize("path", ["decode_mxfp4", "decode_fused"])
+@pytest.mark.parametrize("which", ["domain", "all_patterns", "nonfinite"])
+def test_decode_query_mxfp4_encoder_exhaustive(dev, path, which):
+    """The MXFP4 decode indexers quantize the bf16 query in the kernel (the scaled e2m1
+    conversion for blocks with a finite maximum, the software encoder for a block with a NaN
+    or an infinity); codes and e8m0 scales must equal the oracle's (``quant_mxfp4``) bit for
+    bit -- every finite bf16 value in the saturating domain as the encoder's own input, every
+    finite bf16 pattern with natural block scales, and blocks holding NaN / +-inf."""
+    if which == "domain":
+        blocks = _fp4_domain_blocks()
+    elif which == "all_patterns":
+        blocks = _all_pattern_blocks()
+    else:
+        blocks = _nonfinite_inputs(64 * 4, 128, 11).numpy()
+        blocks = Q.round_bf16(blocks)
+    hi = 64
+    n = blocks.shape[0]
+    b = -(-n // hi)
+    q = np.zeros((b * hi, 128), np.float32)
+    q[:n] = blocks
+    q_idx = torch.from_numpy(q).bfloat16().view(b, hi, 128).to(dev)
+    gen = torch.Generator().manual_seed(5)
+    w = (torch.randn(b, hi, generator=gen) * hi ** -0.5).to(dev)
+    kp, ke = MQ.quant_mxfp4(torch.randn(b, 64, 128, generator=gen).bfloat16().to(dev))
+    pos = torch.full((b,), 255, dtype=torch.int64, device=dev)
+    qp = torch.empty(b, hi, 64, dtype=torch.uint8, device=dev)
+    qe = torch.empty(b, hi, 4, dtype=torch.uint8, device=dev)
+    print(f"{path} MXFP4 query encoder: {which} B={b}", flush=True)
+    if path == "decode_mxfp4":
+        indexer.decode_mxfp4(q_idx, w, kp, ke, compress_ratio=4, positions=pos, q_packed=qp, q_e8m0=qe)
+    else:
+        ones = torch.ones(b, 32, dtype=torch.bfloat16, device=dev)
+        zeros = torch.zeros(b, 32, dtype=torch.bfloat16, device=dev)
+        win = torch.zeros(b, 128, 656, dtype=torch.uint8, device=dev)
+        kv = torch.randn(b, 576, generator=torch.Generator().manual_seed(4)).bfloat16().to(dev)
+        indexer.decode_fused(q_idx, w, kp, ke, fmt="mxfp4", compress_ratio=4, positions=pos, q_rope=(ones, zeros),
+                             kv=kv, kv_weight=torch.ones(576, dtype=torch.bfloat16, device=dev), kv_eps=1e-6,
+                             kv_rope=(ones, zeros), win_cache=win, q_codes=qp, q_scales=qe)
+        # an odd channel's -0.0 is rotated to +0 (norm_rope.py:144): the encoder's input is the
+        # oracle's rotation with the identity tables
+        one, zero = np.ones((q.shape[0], 1, 32), np.float32), np.zeros((q.shape[0], 1, 32), np.float32)
+        q = C.rope(q[:, None, :], one, zero, dtype="bfloat16")[:, 0, :]
+    torch.cuda.synchronize()
+    p_ref, e_ref = Q.quant_mxfp4(q.reshape(b, hi, 128))
+    got_p, got_e = qp.cpu().numpy(), qe.cpu().numpy()
+    assert np.array_equal(got_e, e_ref), f"{path}/{which}: e8m0 scales differ"
+    # a block with a NaN or an infinity has an infinite scale and dequantizes to NaN whatever
+    # its codes (0 * inf); the sign of a NaN code there (x86's default NaN of the oracle's
+    # inf / inf is negative) is no part of the format: such blocks compare dequantized
+    fin = np.isfinite(q.reshape(b, hi, 4, 32)).all(-1)                     # [b, hi, 4]
+    fin_bytes = np.repeat(fin, 16, -1)                                     # [b, hi, 64]
+    bad = np.argwhere((got_p != p_ref) & fin_bytes)
+    assert bad.size == 0, (f"{path}/{which}: {len(bad)} code bytes differ, first at {tuple(bad[0])}: "
+                           f"{got_p[tuple(bad[0])]:#x} vs {p_ref[tuple(bad[0])]:#x}")
+    if not fin.all():
+        _same_values(torch.from_numpy(Q.dequant_mxfp4(got_p, got_e)), Q.dequant_mxfp4(p_ref, e_ref))
+
+
 # ---- non-finite inputs -------------------------------------------------------------------
 
 def _nonfinite_inputs(rows, n, seed):
