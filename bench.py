@@ -280,7 +280,7 @@ def stage_fns(torch, layer, inputs):
     fns = {}
     fp8 = cfg.index_format == "fp8"
     pro = emit and layer._emit_prologue
-    merged = pro and cfg.merged_emit and cfg.ratio == 4 and not cfg.coarse_ratio
+    merged = pro and layer._merged_emit
     if merged:
         # the emission and the scores in one launch (window entry and query prologue included)
         fns["indexer_emit_fp8" if fp8 else "indexer_emit_mxfp4"] = \
@@ -539,8 +539,8 @@ def run_decode(torch, dev, args):
         "config": {"workload": c["text"], "batch": cfg.batch, "context": c["ctx"], "heads": cfg.heads,
                    "latent": "512+64", "index": f"64x128 {cfg.index_format}", "topk": cfg.topk,
                    "window": cfg.window, "coarse": nc, "nsplit": cfg.nsplit, "graph_layers": nl,
-                   "emission": ("inside the indexer launch" if fused and cfg.merged_emit and not cfg.coarse_ratio
-                                else "launch of its own") if fused else None,
+                   "emission": ("inside the indexer launch" if layer._merged_emit else "launch of its own")
+                   if fused else None,
                    "step": "per attention layer, inside a graph replay of graph_layers layers",
                    "prologue": ("fused: in-step group emission (carry ring, pooling + norm, cache entry and "
                                 "index key every 4th token; RoPE tables from the position table), kv RMSNorm + "

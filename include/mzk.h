@@ -176,8 +176,10 @@ int mzk_decode_emit_pair(const int64_t* positions, int64_t B, const float* kv, c
  * (unrotated; its trailing 64 channels rotated with the table row), w fp32 [B, Hi] (already
  * x Hi^-0.5), Hi <= 64 index heads, G keys per row (key batch stride key_batch_entries,
  * format key_format), scores fp32 [B, score_stride] (-inf at and beyond the visible count).
- * Per row one workgroup emits (and scores the new key itself), one writes the window entry,
- * and ceil(G / 512) score.  ratio must be 4 (MZK_EINVAL otherwise). */
+ * With c_kv non-NULL a keyless coarse branch joins the launch, as mzk_decode_emit_pair's
+ * (c_* arguments; c_ratio 2 .. 128, B <= 1024).  Per row one workgroup emits the fine group
+ * (and scores the new key itself), one writes the window entry, 9 pool the coarse group, and
+ * ceil(G / 640) score.  ratio must be 4 (MZK_EINVAL otherwise). */
 int mzk_decode_emit_scores(const int64_t* positions, int64_t B, const float* kv, const float* gate, float* carry_kv,
                            float* carry_gate, int ratio, const void* norm_weight, float eps, uint8_t* cache,
                            int64_t cache_batch_entries, int64_t cache_cap, const void* wk, const void* k_norm_weight,
@@ -185,7 +187,9 @@ int mzk_decode_emit_scores(const int64_t* positions, int64_t B, const float* kv,
                            const void* rope_table, int64_t table_rows, void* step_cos, void* step_sin,
                            const void* kv_proj, const void* kv_weight, float kv_eps, uint8_t* win_cache,
                            int64_t win_batch_entries, int win_cap, const void* q_idx, const float* w, int Hi,
-                           int64_t G, float* scores, int64_t score_stride, void* stream);
+                           int64_t G, float* scores, int64_t score_stride, const float* c_kv, const float* c_gate,
+                           float* c_carry_kv, float* c_carry_gate, int c_ratio, const void* c_norm_weight, float c_eps,
+                           uint8_t* c_cache, int64_t c_cache_batch_entries, int64_t c_cache_cap, void* stream);
 
 /* ---------------------------------------------------------------------------------
  * Piece 2: KV compressor and RoPE

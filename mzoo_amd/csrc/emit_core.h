@@ -534,6 +534,158 @@ __device__ __forceinline__ void emit_body(const EmitParams& p, int64_t blk) {
 }
 
 
+// ---- a long-ratio branch without an index key (the coarse branch), its group step
+// spread over workgroups ------------------------------------------------------------------
+// Pooling r carried slots of 576 channels in the pinned order (the running max, the sum of
+// exps from slot 0, the weighted sum from slot 0) is an exp, a correctly rounded divide and
+// a few more operations per (slot, channel): at r = 128, one workgroup per row spent ~130 us
+// on it.  Here kCoarseParts workgroups per row take 64 channels each.  In a part, four
+// threads per channel compute the exps and the weighted terms of a quarter of the slots
+// each, and one thread per channel adds them up in slot order over LDS, so every sum keeps
+// the pinned order and the latent its bits.  Each part writes its pooled channels into the
+// token's own carry slot r - 1 (whose inputs it has used), makes them visible device-wide
+// and counts itself in on the row's arrival counter; the last part to arrive reads the whole
+// latent back, finishes the group (norm, the FP8-b128 entry with its rope channels rotated
+// at the group's position) and resets the counter.  Steps that complete no group only write
+// their 64 channels of the carry slot.  Launches that overlap on one GPU would share the
+// counters: the decode step issues them in stream order.
+constexpr int kCoarseParts = kD / 64;      // 9 parts of 64 channels
+constexpr int kCoarseMaxRatio = 128;       // slots held in LDS
+constexpr int kCoarseMaxRows = 1024;
+// zero at load; every group step leaves it zero.  One array per translation unit that
+// includes this header: each is used only by that unit's kernels.
+__device__ unsigned g_coarse_arrivals[kCoarseMaxRows];
+
+// Workgroup `blk` = row * kCoarseParts + part of a coarse branch (coarse_emit_kernel, the
+// workgroups after the fine branch's in emit_pair_kernel, or those of the merged indexer
+// launch).
+__device__ __forceinline__ void coarse_body(const EmitParams& p, int64_t blk) {
+  __shared__ float ev[kCoarseMaxRatio][64];  // a part's gates, then exps, then weighted terms
+  __shared__ float pmax[4][64];
+  __shared__ float psum[64];
+  __shared__ float lat[kD];
+  __shared__ float inv_s;
+  __shared__ int last;
+  const int t = threadIdx.x;
+  const int64_t b = blk / kCoarseParts;
+  const int part = static_cast<int>(blk % kCoarseParts);
+  const EmitBranch& br = p.br;
+  const int64_t pos = p.positions[b];
+  if (pos < 0) return;  // an inactive row: nothing to carry or emit
+  const int r = br.ratio;  // 2 .. kCoarseMaxRatio (host check)
+  const int slot = static_cast<int>(pos % r);
+  const bool completes = (pos + 1) % r == 0;
+  const int64_t g = (pos + 1) / r - 1;
+  const int64_t gp = g * r;
+  const bool emit = completes && g < br.cache_cap && gp < p.tab_rows;
+  const int c = t & 63, k = t >> 6;  // channel of the part, quarter of the slots
+  const int d = 64 * part + c;
+  float* ckv = br.carry_kv + b * static_cast<int64_t>(r) * kD;
+  float* cgt = br.carry_gate + b * static_cast<int64_t>(r) * kD;
+  const float kin = br.kv[b * kD + d], gin = br.gate[b * kD + d];
+  if (k == 0) {
+    ckv[slot * kD + d] = kin;
+    cgt[slot * kD + d] = gin;
+  }
+  if (!emit) return;  // uniform over the workgroup
+
+  // the quarter's gates (slot r - 1 is this token, in registers) into LDS, and their max;
+  // every load of a pass is issued before the first is used (indices clamped to slot r - 2),
+  // so a pass costs one memory round trip
+  constexpr int kQ = kCoarseMaxRatio / 4;
+  const int q = (r + 3) / 4, i0 = k * q, i1 = min(i0 + q, r);
+  float m = -__builtin_huge_valf();
+  {
+    float gv[kQ];
+#pragma unroll
+    for (int j = 0; j < kQ; ++j) gv[j] = cgt[min(i0 + j, r - 2) * kD + d];
+#pragma unroll
+    for (int j = 0; j < kQ; ++j) {
+      const int i = i0 + j;
+      if (i < i1) {
+        const float x = i == r - 1 ? gin : gv[j];
+        ev[i][c] = x;
+        m = fmaxf(m, x);
+      }
+    }
+  }
+  pmax[k][c] = m;
+  __syncthreads();
+  // the max ignores the order of its operands
+  m = fmaxf(fmaxf(pmax[0][c], pmax[1][c]), fmaxf(pmax[2][c], pmax[3][c]));
+  for (int i = i0; i < i1; ++i) ev[i][c] = exp_pinned(ev[i][c] - m);
+  __syncthreads();
+  if (k == 0) {  // the sum of exps from slot 0
+    float s = 0.0f;
+    for (int i = 0; i < r; ++i) s = s + ev[i][c];
+    psum[c] = s;
+  }
+  __syncthreads();
+  const float s = psum[c];
+  {
+    float kvv[kQ];
+#pragma unroll
+    for (int j = 0; j < kQ; ++j) kvv[j] = ckv[min(i0 + j, r - 2) * kD + d];
+#pragma unroll
+    for (int j = 0; j < kQ; ++j) {
+      const int i = i0 + j;
+      if (i < i1) ev[i][c] = (i == r - 1 ? kin : kvv[j]) * div_rn(ev[i][c], s);
+    }
+  }
+  __syncthreads();
+  if (k == 0) {  // the weighted sum from slot 0, rounded to bf16 (latent.to(dtype))
+    float acc = 0.0f;
+    for (int i = 0; i < r; ++i) acc = acc + ev[i][c];
+    cgt[(r - 1) * kD + d] = bf(acc);
+  }
+  __threadfence();  // this part's channels are visible device-wide before it counts itself in
+  __syncthreads();
+  if (t == 0) last = atomicAdd(&g_coarse_arrivals[b], 1u) == kCoarseParts - 1;
+  __syncthreads();
+  if (!last) return;  // uniform
+  __threadfence();  // the other parts' channels
+  if (t == 0) g_coarse_arrivals[b] = 0u;
+  for (int dd = t; dd < kD; dd += 256) lat[dd] = cgt[(r - 1) * kD + dd];
+  __syncthreads();
+
+  // ---- RMSNorm of the latent (wave 0, pinned order), as emit_kernel
+  if (t < 64) {
+    float ss = 0.0f;
+    for (int dd = t; dd < kD; dd += 64) ss = ss + lat[dd] * lat[dd];
+#pragma unroll
+    for (int mm = 32; mm >= 1; mm >>= 1) ss = ss + __shfl_xor(ss, mm, 64);
+    if (t == 0) inv_s = div_rn(1.0f, sqrt_rn(div_rn(ss, static_cast<float>(kD)) + br.eps));
+  }
+  __syncthreads();
+  {
+    const float inv = inv_s;
+    for (int dd = t; dd < kD; dd += 256) lat[dd] = bf(bf16_to_f32(br.norm_w[dd]) * bf(lat[dd] * inv));
+  }
+  __syncthreads();
+  // ---- the entry: FP8-b128 nope blocks + the rope channels rotated at the group's position
+  const int64_t last_row = p.tab_rows - 1;
+  const uint16_t* tg = p.tab + min(max(gp, int64_t{0}), last_row) * 2 * kRopePairs;
+  uint8_t* ent = br.cache + (b * br.cache_batch + g) * kEntryBytes;
+  if (t < kNope / 4) {
+    float v[4] = {lat[4 * t], lat[4 * t + 1], lat[4 * t + 2], lat[4 * t + 3]};
+    float amax = abs_max4(v);
+    amax = wave_max_group(amax, 32);
+    const float sc = fp8_scale_from_amax(amax);
+    uint32_t word = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) word |= static_cast<uint32_t>(e4m3_encode(clampf(div_rn(v[i], sc), 448.0f))) << (8 * i);
+    reinterpret_cast<uint32_t*>(ent)[t] = word;
+    if ((t & 31) == 0) reinterpret_cast<float*>(ent + kNope)[t >> 5] = sc;
+  } else if (t < kNope / 4 + kRopePairs) {
+    const int i = t - kNope / 4;
+    float e = lat[kNope + 2 * i], o = lat[kNope + 2 * i + 1];
+    rope_pair(e, o, bf16_to_f32(tg[i]), bf16_to_f32(tg[kRopePairs + i]));
+    uint16_t* rp = reinterpret_cast<uint16_t*>(ent + kNope + 4 * (kNope / 128));
+    rp[2 * i] = f32_to_bf16(e);
+    rp[2 * i + 1] = f32_to_bf16(o);
+  }
+}
+
 // ---- host side ------------------------------------------------------------------------
 
 // The checked parameters of one emission launch (mzk_decode_emit's contract).
@@ -608,6 +760,13 @@ int build_emit(const int64_t* positions, int64_t B, const float* kv, const float
   }
   p.B = B;
   return MZK_OK;
+}
+
+
+// The coarse kernel's branch: a ratio of 2 .. kCoarseMaxRatio without key, prologue or step tables.
+bool coarse_form(const EmitParams& p) {
+  return p.br.ratio >= 2 && p.br.ratio <= kCoarseMaxRatio && !p.br.wk && !p.kv_raw && !p.step_cos &&
+         p.B <= kCoarseMaxRows;
 }
 
 }  // namespace

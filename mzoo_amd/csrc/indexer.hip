@@ -383,6 +383,13 @@ __device__ __forceinline__ void quantize_query(const uint4 (&qr)[4], int qh, int
 
 // ---- the merged emission + scores launch (EMIT) ------------------------------------------
 
+// The emission branches of a merged launch: the fine one (ratio 4, with the index key and
+// the kv prologue) and, with COARSE, a keyless coarse one (coarse_body's form).
+struct EmitSet {
+  EmitParams fine;
+  EmitParams coarse;
+};
+
 // Loads through the constant address space: with a workgroup-uniform address they become
 // scalar loads, which wait on their own counter and leave the in-order vector loads (and the
 // waits the score loop counts on them) alone.  Only for data no launch of the step writes
@@ -508,12 +515,16 @@ __device__ __forceinline__ void emit_and_score(const IdxParams& p, const EmitPar
 // scoring workgroups start at 2; they take the query's RoPE tables from row `pos` of the
 // position table and leave the new key's score to workgroup 0.
 template <int FMT, int DI, int MB, bool QRAW, bool APPEND, bool FUSE = false, bool GATHER = false, bool EMIT = false,
-          int NKB = kNkb>
-__global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxParams p, const EmitParams e) {
+          int NKB = kNkb, bool COARSE = false>
+__global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxParams p, const EmitSet es) {
   static_assert(!QRAW || ((FMT == kFp8 || FMT == kMxfp4) && DI == 128), "in-kernel quantization: Di = 128");
   static_assert(!FUSE || (QRAW && !APPEND), "the fused prologue quantizes the raw query and appends on its own");
   static_assert(!GATHER || !QRAW, "the candidate scorer takes the quantized query");
   static_assert(!EMIT || (FUSE && DI == kDi), "the merged emission takes the fused prologue's query, Di = 128");
+  static_assert(!COARSE || EMIT, "the coarse branch joins the merged emission");
+  const EmitParams& e = es.fine;
+  // EMIT: workgroups before the scoring ones (emitter, window entry, coarse parts)
+  constexpr int kLead = EMIT ? 2 + (COARSE ? kCoarseParts : 0) : 0;
   constexpr int QP = q_pitch<FMT>();
   constexpr int NST = DI / Step<FMT>::K;
   constexpr int RB = row_bytes<FMT>(DI);
@@ -541,9 +552,13 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
       if (tid < 64) kv_prologue(e, row, tid);
       return;
     }
+    if (COARSE && blockIdx.x < kLead) {  // uniform: a part of the coarse branch's group step
+      coarse_body(es.coarse, row * kCoarseParts + (blockIdx.x - 2));
+      return;
+    }
   }
   const int64_t wave_key0 =
-      (static_cast<int64_t>(blockIdx.x) - (EMIT ? 2 : 0)) * (kWaves * NKB * 32) + wave * (NKB * 32);
+      (static_cast<int64_t>(blockIdx.x) - kLead) * (kWaves * NKB * 32) + wave * (NKB * 32);
   // Load order.  Vector-memory loads complete in issue order, so the small operands every
   // tile needs -- the query (fragments, or the bf16 rows to quantize) and the head
   // weights -- go first; then all key fragments of the wave's tiles, so tile 0's MFMAs
@@ -965,8 +980,8 @@ __global__ void __launch_bounds__(kWaves * 64, 2) indexer_prefill_fp8_kernel(con
 template <int FMT, int DI>
 int launch_di(const IdxParams& p, int64_t rows, hipStream_t s) {
   dim3 grid(static_cast<unsigned>((p.G + kKeysPerWg - 1) / kKeysPerWg), static_cast<unsigned>(rows));
-  if (p.Hi <= 32) indexer_scores_kernel<FMT, DI, 1, false, false><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
-  else indexer_scores_kernel<FMT, DI, 2, false, false><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
+  if (p.Hi <= 32) indexer_scores_kernel<FMT, DI, 1, false, false><<<grid, kWaves * 64, 0, s>>>(p, EmitSet{});
+  else indexer_scores_kernel<FMT, DI, 2, false, false><<<grid, kWaves * 64, 0, s>>>(p, EmitSet{});
   return MZK_OK;
 }
 
@@ -978,8 +993,8 @@ int launch_gather(const IdxParams& p, int64_t rows, int Di, hipStream_t s) {
     set_last_error("indexer_candidate_scores: index head dim must be 128 (got %d)", Di);
     return MZK_EUNSUPPORTED;
   }
-  if (p.Hi <= 32) indexer_scores_kernel<FMT, 128, 1, false, false, false, true><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
-  else indexer_scores_kernel<FMT, 128, 2, false, false, false, true><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
+  if (p.Hi <= 32) indexer_scores_kernel<FMT, 128, 1, false, false, false, true><<<grid, kWaves * 64, 0, s>>>(p, EmitSet{});
+  else indexer_scores_kernel<FMT, 128, 2, false, false, false, true><<<grid, kWaves * 64, 0, s>>>(p, EmitSet{});
   return MZK_OK;
 }
 
@@ -1015,6 +1030,20 @@ int launch(const IdxParams& p, int64_t rows, int Di, hipStream_t s) {
       set_last_error("indexer_scores: unsupported index head dim %d", Di);
       return MZK_EUNSUPPORTED;
   }
+}
+
+// Workgroups resident at once on the current device at `per_cu` per compute unit (the
+// count read once per device; 256 compute units if the query fails).
+int resident_workgroups(int per_cu) {
+  static int cus[16] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) dev = 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return per_cu * cus[dev];
 }
 
 IdxParams make_params(const uint8_t* q, const float* qs, const uint8_t* qe, const float* w, const uint8_t* k,
@@ -1187,11 +1216,11 @@ extern "C" int mzk_indexer_decode_fp8(const void* q_idx, const float* w, const u
   dim3 grid(static_cast<unsigned>((G + kKeysPerWg - 1) / kKeysPerWg), static_cast<unsigned>(B));
   hipStream_t s = as_stream(stream);
   if (Hi <= 32) {
-    if (kv) indexer_scores_kernel<kFp8, 128, 1, true, true><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
-    else indexer_scores_kernel<kFp8, 128, 1, true, false><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
+    if (kv) indexer_scores_kernel<kFp8, 128, 1, true, true><<<grid, kWaves * 64, 0, s>>>(p, EmitSet{});
+    else indexer_scores_kernel<kFp8, 128, 1, true, false><<<grid, kWaves * 64, 0, s>>>(p, EmitSet{});
   } else {
-    if (kv) indexer_scores_kernel<kFp8, 128, 2, true, true><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
-    else indexer_scores_kernel<kFp8, 128, 2, true, false><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
+    if (kv) indexer_scores_kernel<kFp8, 128, 2, true, true><<<grid, kWaves * 64, 0, s>>>(p, EmitSet{});
+    else indexer_scores_kernel<kFp8, 128, 2, true, false><<<grid, kWaves * 64, 0, s>>>(p, EmitSet{});
   }
   MZK_LAUNCH_CHECK("indexer_decode_fp8");
   return MZK_OK;
@@ -1234,11 +1263,11 @@ extern "C" int mzk_indexer_decode_mxfp4(const void* q_idx, const float* w, const
   dim3 grid(static_cast<unsigned>((G + kKeysPerWg - 1) / kKeysPerWg), static_cast<unsigned>(B));
   hipStream_t s = as_stream(stream);
   if (Hi <= 32) {
-    if (kv) indexer_scores_kernel<kMxfp4, 128, 1, true, true><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
-    else indexer_scores_kernel<kMxfp4, 128, 1, true, false><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
+    if (kv) indexer_scores_kernel<kMxfp4, 128, 1, true, true><<<grid, kWaves * 64, 0, s>>>(p, EmitSet{});
+    else indexer_scores_kernel<kMxfp4, 128, 1, true, false><<<grid, kWaves * 64, 0, s>>>(p, EmitSet{});
   } else {
-    if (kv) indexer_scores_kernel<kMxfp4, 128, 2, true, true><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
-    else indexer_scores_kernel<kMxfp4, 128, 2, true, false><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
+    if (kv) indexer_scores_kernel<kMxfp4, 128, 2, true, true><<<grid, kWaves * 64, 0, s>>>(p, EmitSet{});
+    else indexer_scores_kernel<kMxfp4, 128, 2, true, false><<<grid, kWaves * 64, 0, s>>>(p, EmitSet{});
   }
   MZK_LAUNCH_CHECK("indexer_decode_mxfp4");
   return MZK_OK;
@@ -1296,24 +1325,24 @@ extern "C" int mzk_indexer_decode_fused(int q_format, const void* q_idx, const f
   dim3 grid(static_cast<unsigned>((G + kKeysPerWg - 1) / kKeysPerWg), static_cast<unsigned>(B));
   hipStream_t s = as_stream(stream);
   if (fp8) {
-    if (Hi <= 32) indexer_scores_kernel<kFp8, 128, 1, true, false, true><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
-    else indexer_scores_kernel<kFp8, 128, 2, true, false, true><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
+    if (Hi <= 32) indexer_scores_kernel<kFp8, 128, 1, true, false, true><<<grid, kWaves * 64, 0, s>>>(p, EmitSet{});
+    else indexer_scores_kernel<kFp8, 128, 2, true, false, true><<<grid, kWaves * 64, 0, s>>>(p, EmitSet{});
   } else {
-    if (Hi <= 32) indexer_scores_kernel<kMxfp4, 128, 1, true, false, true><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
-    else indexer_scores_kernel<kMxfp4, 128, 2, true, false, true><<<grid, kWaves * 64, 0, s>>>(p, EmitParams{});
+    if (Hi <= 32) indexer_scores_kernel<kMxfp4, 128, 1, true, false, true><<<grid, kWaves * 64, 0, s>>>(p, EmitSet{});
+    else indexer_scores_kernel<kMxfp4, 128, 2, true, false, true><<<grid, kWaves * 64, 0, s>>>(p, EmitSet{});
   }
   MZK_LAUNCH_CHECK("indexer_decode_fused");
   return MZK_OK;
 }
 
-// The decode step's group emission and indexer scores in one launch (the EMIT scorer, grid
-// (2 + ceil(G / 512), B)):
+// The decode step's group emission and indexer scores in one launch (the EMIT scorer):
 // mzk_decode_emit's arguments for the fine branch (ratio 4, with the index key and the kv
 // prologue; the scoring workgroups quantize the indexer query themselves, so it has no
 // q_codes / q_scales outputs), then the scorer's: q_idx bf16 [B, Hi, 128] (unrotated; its
 // RoPE from the table row of the token's position), w fp32 [B, Hi], G keys per row (key
 // batch stride key_batch_entries, the key format of the emission), scores fp32 [B,
-// score_stride].
+// score_stride]; then, with c_kv, a keyless coarse branch (mzk_decode_emit_pair's c_*
+// arguments; ratio 2 .. 128, B <= 1024).
 extern "C" int mzk_decode_emit_scores(const int64_t* positions, int64_t B, const float* kv, const float* gate,
                                       float* carry_kv, float* carry_gate, int ratio, const void* norm_weight, float eps,
                                       uint8_t* cache, int64_t cache_batch_entries, int64_t cache_cap, const void* wk,
@@ -1322,16 +1351,30 @@ extern "C" int mzk_decode_emit_scores(const int64_t* positions, int64_t B, const
                                       int64_t table_rows, void* step_cos, void* step_sin, const void* kv_proj,
                                       const void* kv_weight, float kv_eps, uint8_t* win_cache, int64_t win_batch_entries,
                                       int win_cap, const void* q_idx, const float* w, int Hi, int64_t G, float* scores,
-                                      int64_t score_stride, void* stream) {
-  MZK_CHECK_ARG(ratio == 4, "decode_emit_scores: the merged launch takes compress ratio 4 (got %d)", ratio);
+                                      int64_t score_stride, const float* c_kv, const float* c_gate, float* c_carry_kv,
+                                      float* c_carry_gate, int c_ratio, const void* c_norm_weight, float c_eps,
+                                      uint8_t* c_cache, int64_t c_cache_batch_entries, int64_t c_cache_cap,
+                                      void* stream) {
+  MZK_CHECK_ARG(ratio == kEmitRatio, "decode_emit_scores: the merged launch takes compress ratio 4 (got %d)", ratio);
   MZK_CHECK_ARG(wk && kv_proj && q_idx && w && scores,
                 "decode_emit_scores: needs the index key weights, the kv prologue, q_idx, w and scores");
-  EmitParams e;
+  EmitSet es;
   int rc = build_emit(positions, B, kv, gate, carry_kv, carry_gate, ratio, norm_weight, eps, cache,
                       cache_batch_entries, cache_cap, wk, k_norm_weight, k_eps, key_format, k_codes, k_scales,
                       key_batch_entries, rope_table, table_rows, step_cos, step_sin, kv_proj, kv_weight, kv_eps,
-                      win_cache, win_batch_entries, win_cap, nullptr, 0, nullptr, nullptr, e);
+                      win_cache, win_batch_entries, win_cap, nullptr, 0, nullptr, nullptr, es.fine);
   if (rc) return rc;
+  const bool coarse = c_kv != nullptr;
+  if (coarse) {
+    rc = build_emit(positions, B, c_kv, c_gate, c_carry_kv, c_carry_gate, c_ratio, c_norm_weight, c_eps, c_cache,
+                    c_cache_batch_entries, c_cache_cap, nullptr, nullptr, 0.0f, 0, nullptr, nullptr, 0, rope_table,
+                    table_rows, nullptr, nullptr, nullptr, nullptr, 0.0f, nullptr, 0, 0, nullptr, 0, nullptr, nullptr,
+                    es.coarse);
+    if (rc) return rc;
+    MZK_CHECK_ARG(B == 0 || coarse_form(es.coarse),
+                  "decode_emit_scores: the coarse branch needs a ratio of 2 .. %d and at most %d rows", kCoarseMaxRatio,
+                  kCoarseMaxRows);
+  }
   rc = check_common(B, 1, Hi, kDi, G, key_batch_entries, ratio, score_stride);
   if (rc) return rc;
   if (B == 0) return MZK_OK;
@@ -1344,18 +1387,38 @@ extern "C" int mzk_decode_emit_scores(const int64_t* positions, int64_t B, const
                             positions, ratio, scores, score_stride);
   p.q_raw = static_cast<const uint16_t*>(q_idx);
   p.q_rope_dim = 2 * kRopePairs;
-  // five key tiles per wave (640 keys per workgroup): with the two extra workgroups per row
-  // the grid stays within one round of resident workgroups where four tiles would overflow it
-  constexpr int kEmitNkb = 5, kEmitKeys = kWaves * kEmitNkb * 32;
-  dim3 grid(static_cast<unsigned>(2 + (G + kEmitKeys - 1) / kEmitKeys), static_cast<unsigned>(B));
+  // four key tiles per wave (512 keys per workgroup) when the grid, with the workgroups before
+  // the scoring ones, fits one round of resident workgroups (two per compute unit); else five
+  // (640 keys), which keeps it within one round where four would overflow it (config 2:
+  // 32 rows x (2 + 16) = 576 > 512, x (2 + 13) = 480 with five)
+  const int lead = 2 + (coarse ? kCoarseParts : 0);
+  const bool five = B * (lead + (G + kKeysPerWg - 1) / kKeysPerWg) > resident_workgroups(2);
+  const int keys_per_wg = kWaves * (five ? 5 : 4) * 32;
+  dim3 grid(static_cast<unsigned>(lead + (G + keys_per_wg - 1) / keys_per_wg), static_cast<unsigned>(B));
   hipStream_t s = as_stream(stream);
+#define MZK_EMIT_LAUNCH(F, M, C)                                                                                      \
+  do {                                                                                                               \
+    if (five) indexer_scores_kernel<F, kDi, M, true, false, true, false, true, 5, C><<<grid, kWaves * 64, 0, s>>>(p, es); \
+    else indexer_scores_kernel<F, kDi, M, true, false, true, false, true, 4, C><<<grid, kWaves * 64, 0, s>>>(p, es);      \
+  } while (0)
   if (fp8) {
-    if (Hi <= 32) indexer_scores_kernel<kFp8, kDi, 1, true, false, true, false, true, kEmitNkb><<<grid, kWaves * 64, 0, s>>>(p, e);
-    else indexer_scores_kernel<kFp8, kDi, 2, true, false, true, false, true, kEmitNkb><<<grid, kWaves * 64, 0, s>>>(p, e);
+    if (coarse) {
+      if (Hi <= 32) MZK_EMIT_LAUNCH(kFp8, 1, true);
+      else MZK_EMIT_LAUNCH(kFp8, 2, true);
+    } else {
+      if (Hi <= 32) MZK_EMIT_LAUNCH(kFp8, 1, false);
+      else MZK_EMIT_LAUNCH(kFp8, 2, false);
+    }
   } else {
-    if (Hi <= 32) indexer_scores_kernel<kMxfp4, kDi, 1, true, false, true, false, true, kEmitNkb><<<grid, kWaves * 64, 0, s>>>(p, e);
-    else indexer_scores_kernel<kMxfp4, kDi, 2, true, false, true, false, true, kEmitNkb><<<grid, kWaves * 64, 0, s>>>(p, e);
+    if (coarse) {
+      if (Hi <= 32) MZK_EMIT_LAUNCH(kMxfp4, 1, true);
+      else MZK_EMIT_LAUNCH(kMxfp4, 2, true);
+    } else {
+      if (Hi <= 32) MZK_EMIT_LAUNCH(kMxfp4, 1, false);
+      else MZK_EMIT_LAUNCH(kMxfp4, 2, false);
+    }
   }
+#undef MZK_EMIT_LAUNCH
   MZK_LAUNCH_CHECK("decode_emit_scores");
   return MZK_OK;
 }

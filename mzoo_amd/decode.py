@@ -130,9 +130,9 @@ class DecodeConfig:
     # default: replayed in a graph the extra launch and the join cost more than the overlap
     # gains (config 2: 86.5 vs 74.3 us per layer, config 5: 83.9 vs 77.5)
     branch_overlap: bool = False
-    # with in-step emission (rope="table"), ratio 4 and no coarse branch: the emission joins
-    # the indexer launch (one workgroup per row emits the group and scores the new key) --
-    # one launch less per step; False keeps the emission launch of its own
+    # with in-step emission (rope="table") and ratio 4: the emission (both branches) joins the
+    # indexer launch (one workgroup per row emits the group and scores the new key, nine pool
+    # a coarse group) -- one launch less per step; False keeps the emission launch of its own
     merged_emit: bool = True
 
     @property
@@ -222,6 +222,9 @@ class SparseDecodeLayer:
         # 64 indexer heads: the emission launch also runs the step's prologue (window entry,
         # the indexer query's RoPE and quantization) and the indexer is the plain scorer
         self._emit_prologue = cfg.index_heads == 64
+        # the emission inside the indexer launch (coarse branches of ratio <= 128, up to 1024 rows)
+        self._merged_emit = (self._emit_prologue and cfg.merged_emit and cfg.ratio == 4
+                             and (not cfg.coarse_ratio or (2 <= cfg.coarse_ratio <= 128 and b <= 1024)))
         if self._emit_prologue and cfg.index_format == "fp8":
             self.q_codes = torch.empty(b, 1, cfg.index_heads, cfg.index_dim, dtype=torch.uint8, device=dev)
             self.q_scales = torch.empty(b, 1, cfg.index_heads, dtype=torch.float32, device=dev)
@@ -333,9 +336,19 @@ class SparseDecodeLayer:
         cfg, cw = self.cfg, self.compressor
         b = cfg.batch
         fp8 = cfg.index_format == "fp8"
-        if len(compress) != 2:
-            raise ValueError("step(compress=...): (kv, gate) for a layer without a coarse branch")
-        ckv, gate = (t.contiguous() for t in compress)
+        if len(compress) != (4 if cfg.coarse_ratio else 2):
+            raise ValueError("step(compress=...): (kv, gate[, coarse_kv, coarse_gate]) for the layer's branches")
+        ckv, gate = (t.contiguous() for t in compress[:2])
+        coarse = (None,) * 4 + (0, None, 0.0, None, 0, 0)
+        if cfg.coarse_ratio:
+            c_kv, c_gate = (t.contiguous() for t in compress[2:])
+            for t in (c_kv, c_gate):
+                if t.dtype != torch.float32 or t.shape != (b, cfg.dim):
+                    raise ValueError(f"step(compress=...): fp32 [{b}, {cfg.dim}] projections expected")
+            _lib.require_gpu(c_kv, c_gate)
+            coarse = (c_kv.data_ptr(), c_gate.data_ptr(), self.coarse_carry_kv.data_ptr(),
+                      self.coarse_carry_gate.data_ptr(), cfg.coarse_ratio, cw.coarse_norm_weight.data_ptr(), cw.eps,
+                      self.coarse.data_ptr(), cfg.coarse_groups, cfg.coarse_groups)
         for t in (ckv, gate):
             if t.dtype != torch.float32 or t.shape != (b, cfg.dim):
                 raise ValueError(f"step(compress=...): fp32 [{b}, {cfg.dim}] projections expected")
@@ -356,7 +369,7 @@ class SparseDecodeLayer:
                   self.rope_table.data_ptr(), self.rope_table.shape[0], self.step_cos.data_ptr(),
                   self.step_sin.data_ptr(), kv.data_ptr(), self.kv_norm_weight.data_ptr(), self.kv_norm_eps,
                   self.win.data_ptr(), cfg.window, cfg.window, q_idx.data_ptr(), wc.data_ptr(), cfg.index_heads,
-                  cfg.max_groups, self.scores.data_ptr(), cfg.max_groups, _lib.stream_of(self.positions))
+                  cfg.max_groups, self.scores.data_ptr(), cfg.max_groups, *coarse, _lib.stream_of(self.positions))
 
     def fill_coarse(self, latents: torch.Tensor) -> None:
         """latents [B, n, D] -> coarse entries 0..n-1 of every row."""
@@ -399,7 +412,7 @@ class SparseDecodeLayer:
         if from_table and self._emit_prologue:
             if kvc is None or self.kv_norm_weight is None:
                 raise ValueError("step(rope='table'): needs the kv projection and the layer's kv_norm_weight")
-            if cfg.merged_emit and cfg.ratio == 4 and not cfg.coarse_ratio:
+            if self._merged_emit:
                 self._emit_scores(compress, kvc, q_idx.contiguous(), w)
                 self._select_and_attend(q, (self.step_cos, self.step_sin))
                 if advance:

@@ -62,12 +62,12 @@ def _emit_history(kv, gate, ratio, ngroups, nw, cos_t, sin_t, wk=None, kw=None):
 
 
 @pytest.mark.parametrize("fmt,coarse,merged", [("fp8", False, True), ("fp8", False, False), ("mxfp4", False, True),
-                                               ("mxfp4", 8, True), ("fp8", 40, True)])
+                                               ("mxfp4", 8, True), ("mxfp4", 8, False), ("fp8", 40, True)])
 def test_replays_across_group_boundaries(dev, fmt, coarse, merged):
     """``coarse``: the coarse branch's ratio (40: its carried slots stream through the
-    kernel in more than one batch, the last one partial).  ``merged``: without a coarse
-    branch, the emission runs inside the indexer launch (``DecodeConfig.merged_emit``);
-    otherwise in a launch of its own, whose prologue also writes the quantized query."""
+    kernel in more than one batch, the last one partial).  ``merged``: the emission (both
+    branches) runs inside the indexer launch (``DecodeConfig.merged_emit``); otherwise in a
+    launch of its own, whose prologue also writes the quantized query."""
     b, ratio, gcap, topk, p0, steps = 3, 4, 64, 16, 150, 11
     cratio, cgroups = (coarse, 32) if coarse else (0, 0)
     gen = torch.Generator().manual_seed(31 + bool(coarse))
@@ -169,7 +169,7 @@ def test_replays_across_group_boundaries(dev, fmt, coarse, merged):
             assert np.array_equal(layer.coarse.cpu().numpy(), coarse_ent), f"step {i}: coarse cache"
         # indexer + top-k
         q_rot = C.rope(q_idx, cs[:, None], sn[:, None], dtype="bfloat16")
-        if coarse or not merged:
+        if not merged:
             # the quantized indexer query the emission launch's prologue wrote
             qa, qsc = _keys(q_rot, fmt)
             gq = layer.q_codes.cpu().numpy().reshape(qa.shape)
@@ -327,43 +327,55 @@ def test_emission_pair_equals_two_launches(dev):
     assert pair["main"].any() and pair["coarse"].any() and pair["kc"].any()
 
 
-@pytest.mark.parametrize("fmt,hi", [("fp8", 64), ("mxfp4", 64), ("fp8", 32), ("mxfp4", 20)])
-def test_emit_scores_equals_two_launches(dev, fmt, hi):
+@pytest.mark.parametrize("fmt,hi,cratio,cap", [("fp8", 64, 0, 1100), ("mxfp4", 64, 0, 1100), ("fp8", 32, 0, 1100),
+                                               ("mxfp4", 20, 0, 1100), ("mxfp4", 64, 8, 1100), ("fp8", 64, 40, 1100),
+                                               ("fp8", 64, 0, 60000), ("mxfp4", 64, 8, 60000)])
+def test_emit_scores_equals_two_launches(dev, fmt, hi, cratio, cap):
     """``mzk_decode_emit_scores`` (the emission, the window entry, the indexer query's RoPE +
-    quantization and the scores in one launch, the new key scored by its emission workgroup)
-    writes what the emission launch followed by the fused scorer (``mzk_decode_emit`` +
-    ``mzk_indexer_decode_fused`` on the step's tables) writes, bit for bit -- carry, main cache,
-    keys, window ring, step tables and every score -- over steps that complete groups and steps
-    that only carry, with an inactive row (position -1) and a key axis of several scoring
-    workgroups with a partial last one."""
+    quantization and the scores in one launch, the new key scored by its emission workgroup;
+    with ``cratio`` a keyless coarse branch too) writes what the emission launch followed by
+    the fused scorer (``mzk_decode_emit`` / ``mzk_decode_emit_pair`` + ``mzk_indexer_decode_fused``
+    on the step's tables) writes, bit for bit -- carries, main and coarse caches, keys, window
+    ring, step tables and every score -- over steps that complete groups and steps that only
+    carry, with an inactive row (position -1) and a key axis of several scoring workgroups
+    with a partial last one.  ``cap`` 60000 takes the five-tile scoring workgroups (the grid
+    with four would not fit one round of resident workgroups), 1100 the four-tile ones."""
     from mzoo_amd import _lib
-    b, ratio, cap, wcap, rows_tab = 5, 4, 1100, 16, 4 * 1100 + 8
-    rng = np.random.default_rng(5 + hi)
+    b, ratio, wcap, ccap = 5, 4, 16, 120
+    rows_tab = 4 * cap + 8
+    steps = max(2 * ratio, cratio) + 1
+    rng = np.random.default_rng(5 + hi + cratio)
     tab = _bf(rng.uniform(-1, 1, (rows_tab, 64)).astype(np.float32))
     nw = _bf(rng.uniform(0.5, 1.5, D).astype(np.float32))
+    cnw = _bf(rng.uniform(0.5, 1.5, D).astype(np.float32))
     kvw = _bf(rng.uniform(0.5, 1.5, D).astype(np.float32))
     wk = _bf(rng.normal(0, 0.05, (DI, D)).astype(np.float32))
     kw = _bf(rng.uniform(0.5, 1.5, DI).astype(np.float32))
     bf16 = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).bfloat16().to(dev)  # noqa: E731
     dv = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731  (keeps the dtype)
-    tab_d, nw_d, kvw_d, wk_d, kw_d = bf16(tab), bf16(nw), bf16(kvw), bf16(wk), bf16(kw)
+    tab_d, nw_d, cnw_d, kvw_d, wk_d, kw_d = bf16(tab), bf16(nw), bf16(cnw), bf16(kvw), bf16(wk), bf16(kw)
     ka, ks = _keys(_bf(rng.normal(0, 1, (b, cap, DI)).astype(np.float32)), fmt)
     fp8 = fmt == "fp8"
 
     def state():
-        return dict(ckv=torch.zeros(b, ratio, D, device=dev), cgt=torch.zeros(b, ratio, D, device=dev),
-                    main=torch.zeros(b, cap, 656, dtype=torch.uint8, device=dev),
-                    ka=dv(ka), ks=dv(ks), win=torch.zeros(b, wcap, 656, dtype=torch.uint8, device=dev),
-                    scos=torch.zeros(b, 32, dtype=torch.bfloat16, device=dev),
-                    ssin=torch.zeros(b, 32, dtype=torch.bfloat16, device=dev),
-                    scores=torch.full((b, cap), 7.0, device=dev))
+        s = dict(ckv=torch.zeros(b, ratio, D, device=dev), cgt=torch.zeros(b, ratio, D, device=dev),
+                 main=torch.zeros(b, cap, 656, dtype=torch.uint8, device=dev),
+                 ka=dv(ka), ks=dv(ks), win=torch.zeros(b, wcap, 656, dtype=torch.uint8, device=dev),
+                 scos=torch.zeros(b, 32, dtype=torch.bfloat16, device=dev),
+                 ssin=torch.zeros(b, 32, dtype=torch.bfloat16, device=dev),
+                 scores=torch.full((b, cap), 7.0, device=dev))
+        if cratio:
+            s.update(cckv=torch.zeros(b, cratio, D, device=dev), ccgt=torch.zeros(b, cratio, D, device=dev),
+                     coarse=torch.zeros(b, ccap, 656, dtype=torch.uint8, device=dev))
+        return s
 
     one, two = state(), state()
     start = np.array([-1, 0, 5, 13, 4 * 700 + 2], dtype=np.int64)
-    for step in range(2 * ratio + 1):
-        print(f"emit+scores ({fmt}, Hi={hi}): step {step}", flush=True)
+    for step in range(steps):
+        print(f"emit+scores ({fmt}, Hi={hi}, coarse ratio {cratio}, G={cap}): step {step}", flush=True)
         pos_d = dv(start + step)
         kv, gt = dv(rng.normal(0, 1, (b, D)).astype(np.float32)), dv(rng.normal(0, 2, (b, D)).astype(np.float32))
+        ckv_in, cgt_in = dv(rng.normal(0, 1, (b, D)).astype(np.float32)), dv(rng.normal(0, 2, (b, D)).astype(np.float32))
         kvp = bf16(rng.normal(0, 3, (b, D)).astype(np.float32))
         q_idx = bf16(rng.normal(0, 1, (b, hi, DI)).astype(np.float32))
         w = dv((rng.normal(0, 1, (b, hi)) * hi ** -0.5).astype(np.float32))
@@ -373,12 +385,19 @@ def test_emit_scores_equals_two_launches(dev, fmt, hi):
                     ratio, nw_d.data_ptr(), 1e-6, s["main"].data_ptr(), cap, cap, wk_d.data_ptr(), kw_d.data_ptr(),
                     1e-6, 0 if fp8 else 1, s["ka"].data_ptr(), s["ks"].data_ptr(), cap, tab_d.data_ptr(), rows_tab,
                     s["scos"].data_ptr(), s["ssin"].data_ptr())
+            coarse = (ckv_in.data_ptr(), cgt_in.data_ptr(), s["cckv"].data_ptr(), s["ccgt"].data_ptr(), cratio,
+                      cnw_d.data_ptr(), 1e-6, s["coarse"].data_ptr(), ccap, ccap) if cratio else \
+                (None,) * 4 + (0, None, 0.0, None, 0, 0)
             if merged:
                 _lib.call("mzk_decode_emit_scores", *emit, kvp.data_ptr(), kvw_d.data_ptr(), 1e-6,
                           s["win"].data_ptr(), wcap, wcap, q_idx.data_ptr(), w.data_ptr(), hi, cap,
-                          s["scores"].data_ptr(), cap, st)
+                          s["scores"].data_ptr(), cap, *coarse, st)
             else:
-                _lib.call("mzk_decode_emit", *emit, None, None, 0.0, None, 0, 0, None, 0, None, None, st)
+                no_pro = (None, None, 0.0, None, 0, 0, None, 0, None, None)
+                if cratio:
+                    _lib.call("mzk_decode_emit_pair", *emit, *no_pro, *coarse, st)
+                else:
+                    _lib.call("mzk_decode_emit", *emit, *no_pro, st)
                 _lib.call("mzk_indexer_decode_fused", 0 if fp8 else 1, q_idx.data_ptr(), w.data_ptr(),
                           s["ka"].data_ptr(), s["ks"].data_ptr(), b, hi, DI, cap, cap, pos_d.data_ptr(), ratio,
                           s["scores"].data_ptr(), cap, None, None, s["scos"].data_ptr(), s["ssin"].data_ptr(), 64,
@@ -393,6 +412,8 @@ def test_emit_scores_equals_two_launches(dev, fmt, hi):
     # groups were emitted and the window written; each row's last step scored exactly its
     # visible keys, min(cap, (pos + 1) // ratio), the last of them emitted by that step or before
     assert one["main"].any() and one["win"].any()
-    last = start + 2 * ratio
+    if cratio:
+        assert one["coarse"].any()
+    last = start + steps - 1
     finite = torch.isfinite(one["scores"]).sum(1).cpu().numpy()
     assert np.array_equal(finite, np.minimum(cap, (last + 1) // ratio)), finite
