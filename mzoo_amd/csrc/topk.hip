@@ -226,7 +226,8 @@ __device__ __forceinline__ int wave_incl_scan_dpp(int v) {
 constexpr int kBinBits = 11;
 constexpr int kBins = 1 << kBinBits;           // 2048 first-level bins
 constexpr int kLowBits = 32 - kBinBits;        // 21 bits below a first-level bin
-constexpr int kSub1 = 4;                       // first-level sub-counters per bin (lane % 4)
+constexpr int kSub1 = 4;                       // first-level sub-counters per bin (lane % kSub1)
+static_assert(kSub1 % 4 == 0, "a bin's sub-counters are read as whole int4s");
 
 // Inclusive scan over the NT threads of one int each (one barrier); `total` is the sum.
 // wsum [NT/64] may be written again after the caller's next barrier.
@@ -357,8 +358,14 @@ __global__ void __launch_bounds__(NT) topk_row_kernel(const float* __restrict__ 
     int c1[kBins / NT];
 #pragma unroll
     for (int j = 0; j < kBins / NT; ++j) {
-      const int4 v = reinterpret_cast<const int4*>(hist1)[kBins - 1 - ((kBins / NT) * tid + j)];
-      c1[j] = (v.x + v.y) + (v.z + v.w);
+      const int4* hb = reinterpret_cast<const int4*>(hist1) + (kBins - 1 - ((kBins / NT) * tid + j)) * (kSub1 / 4);
+      int s = 0;
+#pragma unroll
+      for (int q = 0; q < kSub1 / 4; ++q) {
+        const int4 v = hb[q];
+        s += (v.x + v.y) + (v.z + v.w);
+      }
+      c1[j] = s;
     }
     h1 = find_bin<NT, kBins>(c1, k, wsum, sh[0]);
   }
@@ -437,7 +444,8 @@ __global__ void __launch_bounds__(NT) topk_row_kernel(const float* __restrict__ 
           if (j / kMapBs == b) c = cb[b];
         v = c >= 0 ? c * kMapBs + j % kMapBs : -1;
       }
-      dst[pos++] = v;
+      if (pos < k) dst[pos] = v;  // always true when the histograms count the row's keys
+      ++pos;
       sel &= sel - 1u;
     }
   }
