@@ -83,6 +83,8 @@ def parse():
     ap.add_argument("--prologue", choices=["fused", "rotated"], default="fused",
                     help="fused: unrotated q / q_idx and the raw kv projection, norm and RoPE in the step's "
                          "launches; rotated: inputs already normed and rotated")
+    ap.add_argument("--merge", choices=["inline", "launch"], default="launch",
+                    help="split merge in the merge kernel, or inside the attention launch where it applies")
     ap.add_argument("--emit", choices=["merged", "separate"], default="merged",
                     help="group emission inside the indexer launch (merged) or in a launch of its own")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline time budget")
@@ -270,6 +272,7 @@ def stage_times(torch, layers, inputs, iters):
 def stage_fns(torch, layer, inputs):
     """The step's launches for one layer, each callable alone."""
     from mzoo_amd import _lib, indexer
+    from mzoo_amd import csa2_attn as MA
     cfg = layer.cfg
     b = cfg.batch
     q, kv, q_idx, w = inputs[:4]
@@ -334,22 +337,29 @@ def stage_fns(torch, layer, inputs):
     fns["topk"] = lambda: indexer.topk(layer.scores.view(b, cfg.max_groups), cfg.topk, out=layer.idx,
                                        workspace=layer.topk_ws)
     coarse = layer.coarse
+    # the decode graph, replayed before the stages are timed, counted its in-launch merges in
+    # the workspace: then the attention launch is timed with its merge and nothing follows it
+    inline = MA.merge_status(ws, b, cfg.heads, cfg.dim, cfg.nsplit + layer.nsplit_wd)[1] > 0
 
     def attn():
         # the split-KV attention kernel alone: with no `out` the entry point writes the
-        # split partials into the workspace and launches nothing else
+        # split partials into the workspace and launches nothing else; with the in-launch
+        # merge the launch also merges them into `out`
         args = (q.data_ptr(), b, 1, cfg.heads, cfg.dim, 1, cfg.nope, layer.positions.data_ptr(),
                 layer.win.data_ptr(), cfg.window, cfg.window, cfg.window,
                 None if coarse is None else coarse.data_ptr(), cfg.coarse_groups, cfg.coarse_groups,
                 max(cfg.coarse_ratio, 1), layer.main.data_ptr(), cfg.max_groups, cfg.max_groups,
                 layer.idx.data_ptr(), cfg.topk, cfg.topk, layer.sinks.data_ptr(), cfg.nsplit, ws.data_ptr(),
-                ws.numel() * ws.element_size(), None, None)
+                ws.numel() * ws.element_size(), *((layer.out.data_ptr(), layer.lse.data_ptr()) if inline else
+                                                  (None, None)))
         if rope:
             _lib.call("mzk_sparse_mqa_rope", *args, rope[0].data_ptr(), rope[1].data_ptr(), cfg.rope, st())
         else:
             _lib.call("mzk_sparse_mqa", *args, st())
     fns["sparse_mqa"] = attn
-    if rope:
+    if inline:
+        pass
+    elif rope:
         fns["sparse_mqa_combine"] = lambda: _lib.call(
             "mzk_sparse_mqa_combine_rope", ws.data_ptr(), b, 1, cfg.heads, cfg.dim, cfg.nsplit,
             layer.sinks.data_ptr(), rope[0].data_ptr(), rope[1].data_ptr(), cfg.rope, layer.out.data_ptr(),
@@ -539,6 +549,7 @@ def run_decode(torch, dev, args):
         "config": {"workload": c["text"], "batch": cfg.batch, "context": c["ctx"], "heads": cfg.heads,
                    "latent": "512+64", "index": f"64x128 {cfg.index_format}", "topk": cfg.topk,
                    "window": cfg.window, "coarse": nc, "nsplit": cfg.nsplit, "graph_layers": nl,
+                   "split_merge": "merge kernel" if "sparse_mqa_combine" in stages else "inside the attention launch",
                    "emission": ("inside the indexer launch" if layer._merged_emit else "launch of its own")
                    if fused else None,
                    "step": "per attention layer, inside a graph replay of graph_layers layers",
@@ -1003,6 +1014,8 @@ def main():
     import torch
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    from mzoo_amd import csa2_attn
+    csa2_attn.set_merge(1 if args.merge == "inline" else 0)
     if args.copy_mib:
         src = torch.ones(args.copy_mib << 18, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)

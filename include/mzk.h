@@ -429,7 +429,14 @@ int mzk_candidate_topk(const float* scores, int64_t rows, int64_t slots, int64_t
  *              rows*nsplit*H*(2*D+8) bytes: each split's output O/l in bf16 by
  *              16-channel group, [rows, nsplit, D/16, H, 16] (a workgroup's stores are then
  *              contiguous), then its (m, l) in fp32 [rows, nsplit, H, 2] (m in log2 units);
- *              merged by a second kernel
+ *              merged by a second kernel -- or, with mzk_sparse_mqa_set_merge(1), inside
+ *              the attention launch when the workspace has mzk_sparse_mqa_workspace_bytes bytes (zero-filled before its
+ *              first use; every complete call leaves its merge records zero again), D > 256,
+ *              nsplit divides 64, rows or rows * ceil(H/64) is a multiple of 8, and
+ *              rows * nsplit * ceil(H/64)
+ *              workgroups fit the device's CUs (each split then waits for its siblings on
+ *              the XCD that ran them and merges 64/nsplit of their heads; the result is
+ *              bit-identical to the merge kernel's)
  *   out        [rows, H, D] bf16;  lse [B, H, S] fp32 (natural log, sink included).
  *              With nsplit > 1, out == lse == NULL writes only the partials (the merge is
  *              then mzk_sparse_mqa_combine). */
@@ -441,6 +448,23 @@ int mzk_sparse_mqa(const void* q, int64_t B, int64_t S, int H, int D, int fmt, i
                    int64_t idx_row_stride, int topk, const float* sinks, int nsplit,
                    float* workspace, int64_t workspace_bytes, void* out, float* lse,
                    void* stream);
+
+/* The workspace mzk_sparse_mqa / _rope take for nsplit splits of `rows` rows: the split
+ * partials (rows*nsplit*H*(2*D+8) bytes, 16-byte aligned) then the in-launch merge's records
+ * (16 bytes per row and 64-head group, then 16 bytes of status: word 0 is set to 1 by a split
+ * that gave up waiting for its siblings, word 1 counts the groups merged inside attention
+ * launches, word 2 the workgroups that took the cross-XCD cache path); 0 when nsplit is 1.  No counterpart in the
+ * reference (its split-free kernel needs no workspace). */
+int mzk_sparse_mqa_workspace_bytes(int64_t rows, int H, int D, int nsplit, int64_t* bytes);
+
+/* Where the split merge runs: 0: the merge kernel after the attention launch (the
+ * default); 1: inside the attention launch where it applies; 2: inside, with every workgroup
+ * taking the cache write-back / invalidate path of a group spread over several XCDs (a test
+ * mode).  Process-wide.  The in-launch merge is bit-identical to the merge kernel and, on
+ * MI355X, not faster (config 2 equal within noise, configs 4 and 5 slower).  No
+ * counterpart in the reference: a switch of this build's own launch structure, for tests
+ * and A/B timing. */
+int mzk_sparse_mqa_set_merge(int mode);
 
 /* Merge the nsplit partials a previous mzk_sparse_mqa call left in `workspace` with the
  * sink: the log-sum-exp combination of the split softmaxes (equal to the one softmax of

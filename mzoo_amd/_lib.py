@@ -64,6 +64,8 @@ _SIGS = {
     "mzk_sparse_mqa": [_P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _I64, _I32, _I32, _P, _I64, _I32, _I32, _P,
                        _I64, _I64, _P, _I64, _I32, _P, _I32, _P, _I64, _P, _P, _P],
     "mzk_sparse_mqa_combine": [_P, _I64, _I64, _I32, _I32, _I32, _P, _P, _P, _P],
+    "mzk_sparse_mqa_workspace_bytes": [_I64, _I32, _I32, _I32, ctypes.POINTER(_I64)],
+    "mzk_sparse_mqa_set_merge": [_I32],
     "mzk_sparse_mqa_rope": [_P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _I64, _I32, _I32, _P, _I64, _I32, _I32,
                             _P, _I64, _I64, _P, _I64, _I32, _P, _I32, _P, _I64, _P, _P, _P, _P, _I32, _P],
     "mzk_sparse_mqa_part": [_P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _I64, _I32, _I32, _P, _I64, _I32, _I32,

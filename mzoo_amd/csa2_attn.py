@@ -20,6 +20,8 @@ Decode form over the packed caches (used by ``mzoo_amd.decode``):
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -28,13 +30,35 @@ FMT_BF16, FMT_FP8 = 0, 1
 
 
 def workspace_bytes(rows: int, heads: int, dim: int, nsplit: int) -> int:
-    """Split-KV workspace: each split's output O/l in bf16, then its (m, l) in fp32."""
-    return 0 if nsplit <= 1 else rows * nsplit * heads * (2 * dim + 8)
+    """Split-KV workspace: each split's output O/l in bf16, then its (m, l) in fp32, then the
+    records of the split merge inside the attention launch (``mzk_sparse_mqa_workspace_bytes``)."""
+    if nsplit <= 1:
+        return 0
+    n = ctypes.c_int64(0)
+    _lib.call("mzk_sparse_mqa_workspace_bytes", rows, heads, dim, nsplit, ctypes.byref(n))
+    return n.value
 
 
 def new_workspace(rows: int, heads: int, dim: int, nsplit: int, device) -> torch.Tensor:
-    """A split-KV workspace for ``sparse_mqa_decode`` (zero-filled)."""
-    return torch.zeros(max(workspace_bytes(rows, heads, dim, nsplit) // 4, 1), dtype=torch.float32, device=device)
+    """A split-KV workspace for ``sparse_mqa_decode`` (zero-filled, as the in-launch merge's
+    records must be before their first use)."""
+    return torch.zeros(max((workspace_bytes(rows, heads, dim, nsplit) + 3) // 4, 1), dtype=torch.float32,
+                       device=device)
+
+
+def set_merge(mode: int) -> None:
+    """Where split partials are merged: 0 the merge kernel (default), 1 inside the attention
+    launch where it applies, 2 inside with the cross-XCD cache path forced (tests)."""
+    _lib.call("mzk_sparse_mqa_set_merge", mode)
+
+
+def merge_status(workspace: torch.Tensor, rows: int, heads: int, dim: int, nsplit: int) -> tuple[int, int]:
+    """The in-launch merge's status words of a workspace: (1 if a split ever gave up waiting
+    for its siblings, else 0; the number of (row, 64-head group) merges done inside attention
+    launches since the workspace was zeroed)."""
+    off = workspace_bytes(rows, heads, dim, nsplit) - 16
+    w = workspace.view(torch.uint8)[off:off + 8].view(torch.int32).cpu()
+    return int(w[0]), int(w[1])
 
 
 def fwd(q: torch.Tensor, kv: torch.Tensor, main_kv: torch.Tensor, indices: torch.Tensor, *, window: int,

@@ -94,6 +94,13 @@ struct AttnParams {
   // final output (nsplit == 1) gets the inverse rotation
   const uint16_t* rope_cos;
   const uint16_t* rope_sin;
+  // The split merge inside the launch (null: a merge launch follows): per (row, 64-head
+  // group) a record of four words -- the XCC registration (64 bits, 8 per XCC: the group's
+  // workgroups that started there), the arrivals, the departures -- zero between launches;
+  // merge_err is set when a workgroup gave up waiting for its group.
+  uint32_t* merge_rec;
+  uint32_t* merge_err;
+  int merge_fence;  // every workgroup takes the release / acquire path (a test mode)
 };
 
 template <int FMT, int D, int NOPE>
@@ -220,6 +227,14 @@ struct RowPlan {
       const uint32_t r8 = k / per_row, i = k - r8 * per_row;
       hgrp = static_cast<int>(i % nhg);
       unit = (r8 * 8 + (L0 & 7u)) * static_cast<uint32_t>(p.nsplit) + i / nhg;
+    } else if (ROW_XCD && p.merge_rec != nullptr && ((static_cast<uint32_t>(p.rows) * nhg) & 7u) == 0) {
+      // (row, head group)-per-XCD, for the in-launch merge of fewer rows: group g = row * nhg
+      // + head group runs on XCD g % 8
+      const uint32_t k = L0 >> 3;
+      const uint32_t g8 = k / static_cast<uint32_t>(p.nsplit);
+      const uint32_t grp = g8 * 8 + (L0 & 7u);
+      hgrp = static_cast<int>(grp % nhg);
+      unit = (grp / nhg) * static_cast<uint32_t>(p.nsplit) + (k - g8 * static_cast<uint32_t>(p.nsplit));
     } else if ((units & 7u) == 0) {
       const uint32_t w = L0 >> 3;
       hgrp = static_cast<int>(w % nhg);
@@ -583,6 +598,222 @@ __device__ __forceinline__ void write_result(const AttnParams& p, int64_t row, i
 
 constexpr float kLazy = 8.0f;  // log2 headroom before the running max must be raised
 
+// ---- the split merge's arithmetic (the merge launch and the in-launch merge share it) ----
+// Split s contributes its normalized output O_s with weight l_s exp2(m_s - M) / L, where
+// M = max(m_s, sink) and L = sum_s l_s exp2(m_s - M) + exp2(sink - M).  Splits are merged
+// kCombineRegSplits at a time into a running (M, L, acc) -- the sink first, as a split of
+// weight 1 at sk -- so 8 or fewer splits are a single pass with the global maximum.  A split
+// that saw no entry (l = 0) contributes nothing (its output is zeros, its m may be -inf).
+constexpr int kCombineRegSplits = 8;
+
+// NP 16-byte pieces (8 channels each) of one (row, head): piece i of split s at
+// po + s * sstride + (i / 2) * gstride + 8 * (i % 2) (gstride: the next 16-channel group),
+// the split's (m, l) at ml + 2 s H.  The loads of PRE splits are issued before any is used.
+template <int NP, int PRE>
+__device__ __forceinline__ void merge_pieces(const uint16_t* po, int64_t sstride, int64_t gstride, const float* ml,
+                                             int nsplit, int H, float sk, bool has_sink, float (&acc)[8 * NP],
+                                             float& M, float& L) {
+  static_assert(PRE % kCombineRegSplits == 0, "whole chunks per load batch");
+#pragma unroll
+  for (int i = 0; i < 8 * NP; ++i) acc[i] = 0.0f;
+  M = sk;
+  L = has_sink ? 1.0f : 0.0f;
+  for (int s0 = 0; s0 < nsplit; s0 += PRE) {
+    float2 ms[PRE];
+    uint4 v[PRE][NP];
+#pragma unroll
+    for (int j = 0; j < PRE; ++j) {
+      if (s0 + j < nsplit) {
+        ms[j] = *reinterpret_cast<const float2*>(ml + 2 * (s0 + j) * H);
+#pragma unroll
+        for (int i = 0; i < NP; ++i)
+          v[j][i] = *reinterpret_cast<const uint4*>(po + static_cast<int64_t>(s0 + j) * sstride + (i >> 1) * gstride +
+                                                    8 * (i & 1));
+      }
+    }
+#pragma unroll
+    for (int c0 = 0; c0 < PRE; c0 += kCombineRegSplits) {
+      if (s0 + c0 < nsplit) {
+        float M_new = M;
+#pragma unroll
+        for (int j = c0; j < c0 + kCombineRegSplits; ++j)
+          if (s0 + j < nsplit && ms[j].y > 0.0f) M_new = fmaxf(M_new, ms[j].x);
+        if (M_new != M) {  // rescale what is merged so far (nothing yet when M = -inf)
+          const float a = M == -__builtin_huge_valf() ? 0.0f : exp2f(M - M_new);
+          L = L * a;
+#pragma unroll
+          for (int i = 0; i < 8 * NP; ++i) acc[i] = acc[i] * a;
+          M = M_new;
+        }
+#pragma unroll
+        for (int j = c0; j < c0 + kCombineRegSplits; ++j) {
+          if (s0 + j < nsplit) {
+            const float wgt = ms[j].y > 0.0f ? ms[j].y * exp2f(ms[j].x - M) : 0.0f;
+            L = L + wgt;
+#pragma unroll
+            for (int i = 0; i < NP; ++i) {
+              const uint32_t w[4] = {v[j][i].x, v[j][i].y, v[j][i].z, v[j][i].w};
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                acc[8 * i + 2 * e] = acc[8 * i + 2 * e] + bf16_to_f32(static_cast<uint16_t>(w[e] & 0xffffu)) * wgt;
+                acc[8 * i + 2 * e + 1] = acc[8 * i + 2 * e + 1] + bf16_to_f32(static_cast<uint16_t>(w[e] >> 16)) * wgt;
+              }
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+// The merged pieces in bf16 at dst (NP x 8 contiguous channels), with the inverse RoPE of the
+// output (owlet1/attention.py:226) when `rot`: rc / rs [i] hold the cos / sin of piece i's
+// four pairs.
+template <int NP>
+__device__ __forceinline__ void store_merged(uint16_t* dst, const float (&acc)[8 * NP], float L, bool rot,
+                                             const uint2 (&rc)[NP], const uint2 (&rs)[NP]) {
+  const float inv = 1.0f / L;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    uint32_t o[4] = {pack_bf16x2(acc[8 * i] * inv, acc[8 * i + 1] * inv),
+                     pack_bf16x2(acc[8 * i + 2] * inv, acc[8 * i + 3] * inv),
+                     pack_bf16x2(acc[8 * i + 4] * inv, acc[8 * i + 5] * inv),
+                     pack_bf16x2(acc[8 * i + 6] * inv, acc[8 * i + 7] * inv)};
+    if (rot) {
+      const uint32_t cw_[2] = {rc[i].x, rc[i].y}, sw_[2] = {rs[i].x, rs[i].y};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t cp = cw_[k >> 1], sp = sw_[k >> 1];
+        o[k] = rope_pair_bf16(o[k], bf16_to_f32(static_cast<uint16_t>((k & 1) ? cp >> 16 : cp & 0xffffu)),
+                              -bf16_to_f32(static_cast<uint16_t>((k & 1) ? sp >> 16 : sp & 0xffffu)));
+      }
+    }
+    *reinterpret_cast<uint4*>(dst + 8 * i) = uint4{o[0], o[1], o[2], o[3]};
+  }
+}
+
+// ---- the split merge inside the attention launch ----------------------------------------
+// XCC (accelerator die) the calling wave runs on: HW_REG_XCC_ID, bits 3:0.
+__device__ __forceinline__ uint32_t xcc_id() { return __builtin_amdgcn_s_getreg(20 | (3 << 11)) & 15u; }
+
+constexpr int kMergeSpinLimit = 1 << 20;  // polls of the arrival counter before a workgroup gives up
+
+// Workgroup `split` of a (row, 64-head group) merges heads h0 + split * hs .. + hs - 1
+// (hs = 64 / nsplit) with merge_pieces, so its output and lse are bit-identical to the merge
+// launch's.  An item is NP pieces (NP / 2 whole 16-channel groups, or one half group at NP
+// = 1) of one head; consecutive threads take consecutive heads of the same channels, so they
+// read contiguous runs of the partials' [D/16][H][16] layout.
+template <int D, int NOPE, int NT, int NP>
+__device__ __forceinline__ void merge_slice(const AttnParams& p, int64_t row, int h0, int split, int tid) {
+  static_assert(D % (8 * NP) == 0 && NOPE % (8 * NP) == 0, "an item lies wholly inside or outside the rope slice");
+  const int hs = 64 / p.nsplit;
+  const int hlo = h0 + split * hs;
+  constexpr int CPH = D / (8 * NP);  // items per head
+  const int items = hs * CPH;
+  const float* mlrow = p.part_ml + row * p.split_stride * p.H * 2;
+  const uint16_t* porow = p.part_o + row * p.split_stride * p.H * static_cast<int64_t>(D);
+  for (int it = tid; it < items; it += NT) {
+    int head, ch0;
+    if constexpr (NP == 1) {  // (16-channel group, head, half)
+      const int g = it / (2 * hs), j = it - g * 2 * hs;
+      head = hlo + (j >> 1);
+      ch0 = 16 * g + 8 * (j & 1);
+    } else {                  // (item chunk, head)
+      const int c = it / hs;
+      head = hlo + (it - c * hs);
+      ch0 = 8 * NP * c;
+    }
+    if (head >= p.H) continue;
+    const uint16_t* po = porow + (ch0 >> 4) * (p.H * 16) + head * 16 + (ch0 & 15);
+    const float sk = p.sinks ? p.sinks[head] * kLog2e : -__builtin_huge_valf();
+    float acc[8 * NP];
+    float M, L;
+    merge_pieces<NP, NP == 1 ? 2 * kCombineRegSplits : kCombineRegSplits>(po, static_cast<int64_t>(p.H) * D, static_cast<int64_t>(p.H) * 16,
+                                            mlrow + head * 2, p.nsplit, p.H, sk, p.sinks != nullptr, acc, M, L);
+    uint2 rc[NP], rs[NP];
+    const bool rot = NOPE < D && p.rope_cos != nullptr && ch0 >= NOPE;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      rc[i] = rs[i] = uint2{0u, 0u};
+      if (rot) {
+        const int64_t ci = row * ((D - NOPE) / 2) + (ch0 - NOPE) / 2 + 4 * i;
+        rc[i] = *reinterpret_cast<const uint2*>(p.rope_cos + ci);
+        rs[i] = *reinterpret_cast<const uint2*>(p.rope_sin + ci);
+      }
+    }
+    store_merged<NP>(p.out + (row * p.H + head) * static_cast<int64_t>(D) + ch0, acc, L, rot, rc, rs);
+    if (ch0 == 0) p.lse[((row / p.S) * p.H + head) * p.S + row % p.S] = (M + __log2f(L)) * kLn2;
+  }
+}
+
+// The in-launch merge of a (row, 64-head group) whose nsplit workgroups all run at once (the
+// host allows it only when the whole grid fits the device, one workgroup per CU).  Each
+// workgroup's partial stores reach its XCD's L2 (the vector L1 writes through) before it
+// arrives; it then waits until all nsplit have arrived and merges its slice of the heads
+// (merge_slice).  With the row-per-XCD mapping every workgroup of the group runs on one XCD,
+// so the partials are read from the L2 they were written to; a workgroup that cannot see
+// its whole group registered on its own XCC releases its partials to memory (agent-scope
+// release: an L2 write-back) before arriving, and one whose group turned out spread
+// acquires (an L2 invalidate) before reading -- a group is either wholly on one XCC, where
+// every member saw it so or released, or spread, where every member released.  The wait is
+// bounded: after kMergeSpinLimit polls a workgroup gives up, sets merge_err and writes
+// nothing.  The last workgroup to leave clears the record for the next launch.
+template <int D, int NOPE, int NT>
+__device__ __forceinline__ void merge_in_launch(const AttnParams& p, int64_t row, int h0, int split, uint32_t* mrec,
+                                                int tid) {
+  __shared__ int m_go;
+  const uint32_t ns = static_cast<uint32_t>(p.nsplit);
+  uint64_t* reg = reinterpret_cast<uint64_t*>(mrec);
+  // the registration is read while the partial stores drain (one wait covers both)
+  uint64_t r = 0;
+  if (tid == 0) r = __hip_atomic_load(reg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // this wave's partial stores are done
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t me = xcc_id();
+    // every member registered on this XCC: the group is wholly here (registrations only grow)
+    const bool local = !p.merge_fence && ((r >> (8 * me)) & 0xffu) == ns;
+    if (!local) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // the write-back done before the arrival
+    }
+    // the last to arrive knows it from the count it replaces; the others poll
+    uint32_t a = __hip_atomic_fetch_add(mrec + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    for (int it = 0; a < ns && it < kMergeSpinLimit; ++it) {
+      __builtin_amdgcn_s_sleep(1);
+      a = __hip_atomic_load(mrec + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const int go = a >= ns;
+    if (!local) __hip_atomic_fetch_add(p.merge_err + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // diagnostic
+    if (go && !local) {
+      // every member has arrived, so every one has registered: the group's final placement
+      const uint64_t rf = __hip_atomic_load(reg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (p.merge_fence || ((rf >> (8 * me)) & 0xffu) != ns) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    if (!go) __hip_atomic_fetch_or(p.merge_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    m_go = go;
+  }
+  __syncthreads();
+  if (m_go) {
+    // an item = 8 * NP channels of a head; NP chosen so that the slice's items fit one pass
+    // of NT threads where it can (nsplit 4, 8, 16: 288 items)
+    switch (p.nsplit) {
+      case 2:
+      case 4: merge_slice<D, NOPE, NT, 4>(p, row, h0, split, tid); break;
+      case 8: merge_slice<D, NOPE, NT, 2>(p, row, h0, split, tid); break;
+      default: merge_slice<D, NOPE, NT, 1>(p, row, h0, split, tid); break;
+    }
+  }
+  // this workgroup reads the record no more: the last to leave clears it and counts the
+  // group's merge in merge_err[1] (a diagnostic: merged groups since the workspace was zeroed)
+  if (tid == 0 && __hip_atomic_fetch_add(mrec + 3, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ns - 1) {
+    __hip_atomic_store(mrec + 2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(mrec + 3, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(reg, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(p.merge_err + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 // ------------------------------------------------------------------------------------
 // D <= 256: one wave per 32 heads over the whole of D.  HG waves per workgroup.
 // Per tile: dequantize into Kt, S^T = K.Q^T (two MFMA chains), lane-local online
@@ -831,6 +1062,18 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
     for (int r = 0; r < RST; ++r) {
       qrc[r] = *reinterpret_cast<const uint2*>(cb + roff + 8 * r);
       qrs[r] = *reinterpret_cast<const uint2*>(sb + roff + 8 * r);
+    }
+  }
+  // in-launch merge: the workgroup registers the XCC it runs on with its (row, 64-head
+  // group), after its first loads (an atomic without return: no wait covers it)
+  uint32_t* mrec = nullptr;
+  if constexpr (ALLTAB) {
+    if (p.merge_rec != nullptr) {
+      const uint32_t nhg = static_cast<uint32_t>((p.H + HG * 32 - 1) / (HG * 32));
+      mrec = p.merge_rec + 4 * (static_cast<uint32_t>(rp.row) * nhg + static_cast<uint32_t>(rp.hgrp));
+      if (tid == 0)
+        __hip_atomic_fetch_add(reinterpret_cast<uint64_t*>(mrec), 1ull << (8 * xcc_id()), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   __shared__ int wred[2 * 8];
@@ -1159,17 +1402,16 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
   };
 
   if (!pass(std::false_type{})) pass(std::true_type{});
+  if constexpr (ALLTAB) {
+    if (mrec != nullptr) merge_in_launch<D, NOPE, NT>(p, rp.row, rp.hgrp * HG * 32, rp.split, mrec, tid);
+  }
 }
 
-// Merge the split partials with the sink: split s contributes its normalized output O_s
-// with weight l_s exp2(m_s - M) / L, where M = max(m_s, sink) and
-// L = sum_s l_s exp2(m_s - M) + exp2(sink - M).  One thread per 8 * NP channels of a
-// (row, head), NP 16-byte pieces of every split in flight per memory round trip.  A wave
-// takes 16 heads x 4 runs of 8 * NP channels (lane % 16 the head, lane / 16 the run): it
-// reads 16 heads x 16 NP bytes contiguous per run from the partials' 16-channel groups and
-// writes 4 x 16 NP contiguous bytes of each head's output row.
-constexpr int kCombineRegSplits = 8;  // splits merged per memory round trip
-
+// The merge launch: the split partials merged with the sink (merge_pieces).  One thread per
+// 8 * NP channels of a (row, head), NP 16-byte pieces of every split in flight per memory
+// round trip.  A wave takes 16 heads x 4 runs of 8 * NP channels (lane % 16 the head, lane /
+// 16 the run): it reads 16 heads x 16 NP bytes contiguous per run from the partials'
+// 16-channel groups and writes 4 x 16 NP contiguous bytes of each head's output row.
 template <int D, int NP>
 __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict__ part_o,
                                                       const float* __restrict__ part_ml, int nsplit, int H, int64_t S,
@@ -1217,73 +1459,11 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
       rs[i] = *reinterpret_cast<const uint2*>(rope_sin + row * (rope_dim / 2) + rope_ch / 2 + 4 * i);
     }
   }
-  // Splits are merged kCombineRegSplits at a time: a chunk's (m, l) pairs and output pieces
-  // are all requested before any is used (one memory round trip per chunk), then folded
-  // into a running (M, L, acc) -- the sink first, as a split of weight 1 at sk.  A split
-  // that saw no entry (l = 0) contributes nothing (its output is zeros, its m may be -inf).
-  // With at most kCombineRegSplits splits this is a single pass with the global maximum.
   float acc[8 * NP];
-#pragma unroll
-  for (int i = 0; i < 8 * NP; ++i) acc[i] = 0.0f;
-  float M = sk, L = sinks ? 1.0f : 0.0f;
-  for (int s0 = 0; s0 < nsplit; s0 += kCombineRegSplits) {
-    float2 ms[kCombineRegSplits];
-    uint4 v[kCombineRegSplits][NP];
-#pragma unroll
-    for (int j = 0; j < kCombineRegSplits; ++j) {
-      if (s0 + j < nsplit) {
-        ms[j] = *reinterpret_cast<const float2*>(ml + 2 * (s0 + j) * H);
-#pragma unroll
-        for (int i = 0; i < NP; ++i)
-          v[j][i] = *reinterpret_cast<const uint4*>(po + static_cast<int64_t>(s0 + j) * H * D + 8 * i);
-      }
-    }
-    float M_new = M;
-#pragma unroll
-    for (int j = 0; j < kCombineRegSplits; ++j)
-      if (s0 + j < nsplit && ms[j].y > 0.0f) M_new = fmaxf(M_new, ms[j].x);
-    if (M_new != M) {  // rescale what is merged so far (nothing yet when M = -inf)
-      const float a = M == -__builtin_huge_valf() ? 0.0f : exp2f(M - M_new);
-      L = L * a;
-#pragma unroll
-      for (int i = 0; i < 8 * NP; ++i) acc[i] = acc[i] * a;
-      M = M_new;
-    }
-#pragma unroll
-    for (int j = 0; j < kCombineRegSplits; ++j) {
-      if (s0 + j < nsplit) {
-        const float wgt = ms[j].y > 0.0f ? ms[j].y * exp2f(ms[j].x - M) : 0.0f;
-        L = L + wgt;
-#pragma unroll
-        for (int i = 0; i < NP; ++i) {
-          const uint32_t w[4] = {v[j][i].x, v[j][i].y, v[j][i].z, v[j][i].w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            acc[8 * i + 2 * e] = acc[8 * i + 2 * e] + bf16_to_f32(static_cast<uint16_t>(w[e] & 0xffffu)) * wgt;
-            acc[8 * i + 2 * e + 1] = acc[8 * i + 2 * e + 1] + bf16_to_f32(static_cast<uint16_t>(w[e] >> 16)) * wgt;
-          }
-        }
-      }
-    }
-  }
-  const float inv = 1.0f / L;
-#pragma unroll
-  for (int i = 0; i < NP; ++i) {
-    uint32_t o[4] = {pack_bf16x2(acc[8 * i] * inv, acc[8 * i + 1] * inv),
-                     pack_bf16x2(acc[8 * i + 2] * inv, acc[8 * i + 3] * inv),
-                     pack_bf16x2(acc[8 * i + 4] * inv, acc[8 * i + 5] * inv),
-                     pack_bf16x2(acc[8 * i + 6] * inv, acc[8 * i + 7] * inv)};
-    if (rot) {
-      const uint32_t cw_[2] = {rc[i].x, rc[i].y}, sw_[2] = {rs[i].x, rs[i].y};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint32_t cp = cw_[k >> 1], sp = sw_[k >> 1];
-        o[k] = rope_pair_bf16(o[k], bf16_to_f32(static_cast<uint16_t>((k & 1) ? cp >> 16 : cp & 0xffffu)),
-                              -bf16_to_f32(static_cast<uint16_t>((k & 1) ? sp >> 16 : sp & 0xffffu)));
-      }
-    }
-    *reinterpret_cast<uint4*>(out + rh * static_cast<int64_t>(D) + ch0 + 8 * i) = uint4{o[0], o[1], o[2], o[3]};
-  }
+  float M, L;
+  merge_pieces<NP, kCombineRegSplits>(po, static_cast<int64_t>(H) * D, static_cast<int64_t>(H) * 16, ml, nsplit, H, sk,
+                                      sinks != nullptr, acc, M, L);
+  store_merged<NP>(out + rh * static_cast<int64_t>(D) + ch0, acc, L, rot, rc, rs);
   if (ch0 == 0) lse[((row / S) * H + head) * S + row % S] = (M + __log2f(L)) * kLn2;
 }
 
@@ -1299,8 +1479,12 @@ int launch_kernel(K kern, size_t dyn_lds, int threads, int heads_per_wg, const A
   return MZK_OK;
 }
 
+// `merged` is set when the launch merges its splits itself (p.merge_rec given and the
+// launch takes the kernel instance that carries the merge).
 template <int FMT, int D, int NOPE>
-int dispatch_heads(const AttnParams& p, int64_t rows, hipStream_t s) {
+int dispatch_heads(const AttnParams& p_in, int64_t rows, hipStream_t s, bool* merged) {
+  AttnParams p = p_in;
+  *merged = false;
   if (p.H > 128) {
     set_last_error("sparse_mqa: at most 128 heads (got %d)", p.H);
     return MZK_EUNSUPPORTED;
@@ -1332,27 +1516,30 @@ int dispatch_heads(const AttnParams& p, int64_t rows, hipStream_t s) {
     const int64_t total_max = static_cast<int64_t>(p.window) + (p.dense ? p.dense_cap : 0) + (p.main ? p.topk : 0);
     const int64_t chunk_max = ((total_max + p.nsplit - 1) / p.nsplit + kTile - 1) / kTile * kTile;
     const int64_t tables_max = chunk_max / kTile + 3 > 4 ? chunk_max / kTile + 3 : 4;
-    return launch_kernel(tables_max * kTile <= kAllTabCap ? kern_all : kern_ring, M::LDS, 512, 64, p, rows, s);
+    const bool all_tables = tables_max * kTile <= kAllTabCap;
+    if (!all_tables) p.merge_rec = nullptr;  // only the decode instance carries the in-launch merge
+    *merged = p.merge_rec != nullptr;
+    return launch_kernel(all_tables ? kern_all : kern_ring, M::LDS, 512, 64, p, rows, s);
   } else {
     if (p.H <= 32) return launch_kernel(sparse_mqa_kernel<FMT, D, NOPE, 1>, 0, 64, 32, p, rows, s);
     return launch_kernel(sparse_mqa_kernel<FMT, D, NOPE, 2>, 0, 128, 64, p, rows, s);
   }
 }
 
-int dispatch(int fmt, int D, int nope, const AttnParams& p, int64_t rows, hipStream_t s) {
+int dispatch(int fmt, int D, int nope, const AttnParams& p, int64_t rows, hipStream_t s, bool* merged) {
   if (fmt == kFmtFp8) {
-    if (D == 576 && nope == 512) return dispatch_heads<kFmtFp8, 576, 512>(p, rows, s);
-    if (D == 160 && nope == 128) return dispatch_heads<kFmtFp8, 160, 128>(p, rows, s);
+    if (D == 576 && nope == 512) return dispatch_heads<kFmtFp8, 576, 512>(p, rows, s, merged);
+    if (D == 160 && nope == 128) return dispatch_heads<kFmtFp8, 160, 128>(p, rows, s, merged);
     set_last_error("sparse_mqa fp8: unsupported latent %d+%d (have 512+64, 128+32)", nope, D - nope);
     return MZK_EUNSUPPORTED;
   }
   switch (D) {
-    case 64: return dispatch_heads<kFmtBf16, 64, 64>(p, rows, s);
-    case 96: return dispatch_heads<kFmtBf16, 96, 96>(p, rows, s);
-    case 128: return dispatch_heads<kFmtBf16, 128, 128>(p, rows, s);
-    case 160: return dispatch_heads<kFmtBf16, 160, 160>(p, rows, s);
-    case 256: return dispatch_heads<kFmtBf16, 256, 256>(p, rows, s);
-    case 576: return dispatch_heads<kFmtBf16, 576, 576>(p, rows, s);
+    case 64: return dispatch_heads<kFmtBf16, 64, 64>(p, rows, s, merged);
+    case 96: return dispatch_heads<kFmtBf16, 96, 96>(p, rows, s, merged);
+    case 128: return dispatch_heads<kFmtBf16, 128, 128>(p, rows, s, merged);
+    case 160: return dispatch_heads<kFmtBf16, 160, 160>(p, rows, s, merged);
+    case 256: return dispatch_heads<kFmtBf16, 256, 256>(p, rows, s, merged);
+    case 576: return dispatch_heads<kFmtBf16, 576, 576>(p, rows, s, merged);
     default:
       set_last_error("sparse_mqa bf16: unsupported head dim %d (have 64, 96, 128, 160, 256, 576)", D);
       return MZK_EUNSUPPORTED;
@@ -1388,6 +1575,32 @@ using namespace mzk;
 namespace {
 int combine_impl(const float* workspace, int64_t B, int64_t S, int H, int D, int nsplit, const float* sinks,
                  const void* rope_cos, const void* rope_sin, int rope_dim, void* out, float* lse, void* stream);
+
+// Where the split merge runs: 0: the merge launch (the default); 1: inside the attention
+// launch where it applies; 2: inside, every workgroup on the release / acquire path (a test
+// mode: the path a group spread over several XCDs takes).  The in-launch merge is exact but
+// not faster on MI355X: its tail (the arrival, then each split's reads of its siblings'
+// partials) costs what the merge launch does at 4 splits, and more at 16 and 32, where the
+// splits of a group finish several microseconds apart.
+std::atomic<int> g_merge_mode{0};
+
+int64_t align16_bytes(int64_t x) { return (x + 15) & ~static_cast<int64_t>(15); }
+
+// The in-launch merge's records (16 bytes per (row, 64-head group)) and its error word.
+int64_t merge_rec_bytes(int64_t rows, int H) { return rows * ((H + 63) / 64) * 16 + 16; }
+
+// Compute units of the current device (cached per device), or 0 if unknown.
+int device_cus() {
+  static std::atomic<int> cus[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 0) n = 0;
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
 
 // split_total < 0: a whole call (partials of nsplit splits then the merge, or the final
 // output directly with one split); split_total >= 1: partials only, of splits split_base ..
@@ -1483,11 +1696,30 @@ int sparse_mqa_impl(const void* q, int64_t B, int64_t S, int H, int D, int fmt, 
   }
   p.rope_cos = static_cast<const uint16_t*>(rope_cos);
   p.rope_sin = static_cast<const uint16_t*>(rope_sin);
+  // The split merge inside the attention launch: a full call of the D-split kernel with
+  // nsplit dividing 64, rows or rows * (64-head groups) a multiple of 8 (the mappings that put
+  // a group's splits on one XCD), a workspace that holds the merge records, and a grid of at
+  // most one workgroup per CU (every workgroup of a group must run at once; one fills a CU's
+  // LDS).
+  const int merge_mode = g_merge_mode.load(std::memory_order_relaxed);
+  const int64_t nhg64 = (H + 63) / 64;
+  if (merge_mode != 0 && !part_only && nsplit > 1 && out != nullptr && D > 256 && 64 % nsplit == 0 &&
+      ((rows & 7) == 0 || ((rows * nhg64) & 7) == 0)) {
+    const int64_t nhg = nhg64;
+    const int64_t off = align16_bytes(rows * stride * static_cast<int64_t>(H) * (2 * D + 8));
+    const int cus = device_cus();
+    if (workspace_bytes >= off + merge_rec_bytes(rows, H) && cus > 0 && rows * nsplit * nhg <= cus) {
+      p.merge_rec = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(workspace) + off);
+      p.merge_err = p.merge_rec + 4 * rows * nhg;
+      p.merge_fence = merge_mode == 2;
+    }
+  }
   hipStream_t s = as_stream(stream);
-  int rc = dispatch(fmt, D, nope, p, rows, s);
+  bool merged = false;
+  int rc = dispatch(fmt, D, nope, p, rows, s, &merged);
   if (rc) return rc;
   MZK_LAUNCH_CHECK("sparse_mqa");
-  if (!part_only && nsplit > 1 && out != nullptr)
+  if (!part_only && nsplit > 1 && out != nullptr && !merged)
     return combine_impl(workspace, B, S, H, D, nsplit, sinks, rope_cos, rope_sin, rope_dim, out, lse, stream);
   return MZK_OK;
 }
@@ -1625,6 +1857,20 @@ extern "C" int mzk_sparse_mqa_noalloc(const void* q, int64_t B, int64_t S, int H
                          dense_batch_entries, dense_cap, dense_ratio, main_kv, main_batch_entries, G, idx,
                          idx_row_stride, topk, sinks, nsplit, ws, need, out, lse, rope_cos, rope_sin, rope_dim, 0, -1,
                          stream);
+}
+
+extern "C" int mzk_sparse_mqa_workspace_bytes(int64_t rows, int H, int D, int nsplit, int64_t* bytes) {
+  MZK_CHECK_ARG(bytes != nullptr, "sparse_mqa_workspace_bytes: null output");
+  MZK_CHECK_ARG(rows >= 0 && H >= 1 && D > 0 && nsplit >= 1, "sparse_mqa_workspace_bytes: bad sizes");
+  *bytes = nsplit > 1 ? align16_bytes(rows * nsplit * static_cast<int64_t>(H) * (2 * D + 8)) + merge_rec_bytes(rows, H)
+                      : 0;
+  return MZK_OK;
+}
+
+extern "C" int mzk_sparse_mqa_set_merge(int mode) {
+  MZK_CHECK_ARG(mode >= 0 && mode <= 2, "sparse_mqa_set_merge: mode must be 0, 1 or 2 (got %d)", mode);
+  g_merge_mode.store(mode, std::memory_order_relaxed);
+  return MZK_OK;
 }
 
 extern "C" int mzk_sparse_mqa_combine(const float* workspace, int64_t B, int64_t S, int H, int D, int nsplit,
