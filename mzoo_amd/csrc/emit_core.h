@@ -220,19 +220,90 @@ __device__ __forceinline__ void kv_prologue(const EmitParams& p, int64_t b, int 
   reinterpret_cast<uint16_t*>(went + kNope + 4 * (kNope / 128))[lane] = rot;
 }
 
+// The token's carry slot (slot pos % ratio of the row's ring, the reference's buffer_kv /
+// buffer_gate) for the merged launch, where emit_row<R, true> leaves it: NT threads from
+// thread 0, the projections requested with the position.
+template <int NT>
+__device__ __forceinline__ void carry_slot(const EmitParams& p, int64_t b, int t) {
+  static_assert(kD % NT == 0, "whole channels per thread");
+  constexpr int kPer = kD / NT;
+  const EmitBranch& br = p.br;
+  float kin[kPer], gin[kPer];
+#pragma unroll
+  for (int c = 0; c < kPer; ++c) {
+    kin[c] = br.kv[b * kD + t + NT * c];
+    gin[c] = br.gate[b * kD + t + NT * c];
+  }
+  const int64_t pos = p.positions[b];
+  if (pos < 0) return;  // an inactive row: nothing to carry
+  const int r = br.ratio;
+  float* ckv = br.carry_kv + (b * r + pos % r) * static_cast<int64_t>(kD);
+  float* cgt = br.carry_gate + (b * r + pos % r) * static_cast<int64_t>(kD);
+#pragma unroll
+  for (int c = 0; c < kPer; ++c) {
+    ckv[t + NT * c] = kin[c];
+    cgt[t + NT * c] = gin[c];
+  }
+}
+
 // R > 0: the ratio is R (the group stays in registers); R == 0: any ratio (br.ratio).
 // The carry / group work of row b (all threads of a 256-thread workgroup, uniform control
 // flow).  Returns whether the step emitted the row's index key (group g = (pos + 1) / r - 1);
 // with `key_out` (16-byte aligned LDS) the key's operand bytes are also left there for the
 // caller, after the workgroup's next barrier: FP8 -- 128 codes, then the fp32 scale at byte
 // 128; MXFP4 -- 64 bytes of e2m1 pairs, then the 4 e8m0 bytes at byte 64.
-template <int R>
+// MERGED (the merged emission + scores launch, R > 1): the token's carry slot and the step's
+// RoPE tables are written by other workgroups of that launch (carry_slot, the row's first
+// scoring workgroup), so a step that completes no group ends as soon as the position is
+// known.
+template <int R, bool MERGED = false>
 __device__ __forceinline__ bool emit_row(const EmitParams& p, int64_t b, uint8_t* key_out) {
+  static_assert(!MERGED || R > 1, "the merged form keeps the group in registers");
   __shared__ float lat[kD];
   __shared__ float kvec[kDi];
   __shared__ float inv_s[2];
   const int t = threadIdx.x;
   const EmitBranch& br = p.br;
+  const float* kvb = br.kv + b * kD;
+  const float* gtb = br.gate + b * kD;
+
+  // ---- every load the step needs, issued before any of them is waited on ----------------
+  // Loads are unconditional from always-valid addresses (clamped indices, a stand-in
+  // pointer when an operand is absent) or, for the large optional operands, sit in a
+  // workgroup-uniform branch into uninitialised registers; bf16 values stay raw until their
+  // use.  A `cond ? convert(load) : 0` form puts each load with a wait for it into a branch
+  // of its own: one memory round trip per load.  The operands that do not depend on the
+  // row's position -- the token's projections, the norm weight and (R > 1) the carried
+  // slots 0 .. R - 2, which a completing step pools -- are requested with the position, so a
+  // group step pays one round trip for them, not two (the carried slots cost 14 KB a row on
+  // the steps that do not pool them).
+  // this thread's channels: t, t + 256, t + 512 (the last only for t < 64; clamped)
+  constexpr int kCh = 3;
+  constexpr int kRegR = R > 1 ? R - 1 : 1;  // carried slots held in registers (R > 1)
+  float kin[kCh], gin[kCh] = {};
+  uint16_t nwr[kCh];
+  float ck[kRegR][kCh], cg[kRegR][kCh];
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) kin[c] = kvb[min(t + 256 * c, kD - 1)];
+  if (R != 1 && (R > 1 || br.ratio > 1)) {
+#pragma unroll
+    for (int c = 0; c < kCh; ++c) gin[c] = gtb[min(t + 256 * c, kD - 1)];
+  }
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) nwr[c] = br.norm_w[min(t + 256 * c, kD - 1)];
+  if constexpr (R > 1) {
+    const float* ckv0 = br.carry_kv + b * static_cast<int64_t>(R) * kD;
+    const float* cgt0 = br.carry_gate + b * static_cast<int64_t>(R) * kD;
+#pragma unroll
+    for (int c = 0; c < kCh; ++c) {
+      const int d = min(t + 256 * c, kD - 1);
+#pragma unroll
+      for (int i = 0; i < R - 1; ++i) {
+        ck[i][c] = ckv0[i * kD + d];
+        cg[i][c] = cgt0[i * kD + d];
+      }
+    }
+  }
   const int64_t pos = p.positions[b];
   if (pos < 0) return false;  // an inactive row: nothing to carry or emit
   const int r = R > 0 ? R : br.ratio;
@@ -242,44 +313,9 @@ __device__ __forceinline__ bool emit_row(const EmitParams& p, int64_t b, uint8_t
   const int64_t gp = g * r;  // the group's position (its first token)
   const bool emit = completes && g < br.cache_cap && gp < p.tab_rows;
   const bool key = emit && br.wk != nullptr;
-  const float* kvb = br.kv + b * kD;
-  const float* gtb = br.gate + b * kD;
   float* ckv = br.carry_kv + b * static_cast<int64_t>(r) * kD;
   float* cgt = br.carry_gate + b * static_cast<int64_t>(r) * kD;
-
-  // ---- every load the step needs, issued before any of them is waited on ----------------
-  // Loads are unconditional from always-valid addresses (clamped indices, a stand-in
-  // pointer when an operand is absent) or, for the large optional operands, sit in a
-  // workgroup-uniform branch into uninitialised registers; bf16 values stay raw until their
-  // use.  A `cond ? convert(load) : 0` form puts each load with a wait for it into a branch
-  // of its own: one memory round trip per load.
-  // this thread's channels: t, t + 256, t + 512 (the last only for t < 64; clamped)
-  constexpr int kCh = 3;
-  constexpr int kRegR = R > 1 ? R - 1 : 1;  // carried slots held in registers (R > 1)
-  float kin[kCh], gin[kCh] = {};
-  uint16_t nwr[kCh];
-  float ck[kRegR][kCh], cg[kRegR][kCh];
-#pragma unroll
-  for (int c = 0; c < kCh; ++c) kin[c] = kvb[min(t + 256 * c, kD - 1)];
-  if (r > 1) {
-#pragma unroll
-    for (int c = 0; c < kCh; ++c) gin[c] = gtb[min(t + 256 * c, kD - 1)];
-  }
-#pragma unroll
-  for (int c = 0; c < kCh; ++c) nwr[c] = br.norm_w[min(t + 256 * c, kD - 1)];
-  if (emit) {
-#pragma unroll
-    for (int c = 0; c < kCh; ++c) {
-      const int d = min(t + 256 * c, kD - 1);
-      if constexpr (R > 1) {
-#pragma unroll
-        for (int i = 0; i < R - 1; ++i) {
-          ck[i][c] = ckv[i * kD + d];
-          cg[i][c] = cgt[i * kD + d];
-        }
-      }
-    }
-  }
+  if (MERGED && !emit) return false;  // uniform: the carry slot is another workgroup's
   // key weights: lane j of each 8-lane group reads chunks j, j+8, ... of its output's row,
   // so one load instruction covers 8 rows x 128 contiguous bytes; a wave serves 8 outputs
   // per pass, 4 passes (outputs 32 w + 8 pass + lane / 8)
@@ -306,17 +342,19 @@ __device__ __forceinline__ bool emit_row(const EmitParams& p, int64_t b, uint8_t
   const uint16_t stab = trow[t & 63];
 
   // ---- the token into its carry slot; the step's RoPE tables --------------------------
+  if constexpr (!MERGED) {
 #pragma unroll
-  for (int c = 0; c < kCh; ++c) {
-    const int d = t + 256 * c;
-    if (d < kD) {
-      ckv[slot * kD + d] = kin[c];
-      if (r > 1) cgt[slot * kD + d] = gin[c];
+    for (int c = 0; c < kCh; ++c) {
+      const int d = t + 256 * c;
+      if (d < kD) {
+        ckv[slot * kD + d] = kin[c];
+        if (r > 1) cgt[slot * kD + d] = gin[c];
+      }
     }
-  }
-  if (step_tab && t < 2 * kRopePairs) {
-    if (t < kRopePairs) p.step_cos[b * kRopePairs + t] = stab;
-    else p.step_sin[b * kRopePairs + (t - kRopePairs)] = stab;
+    if (step_tab && t < 2 * kRopePairs) {
+      if (t < kRopePairs) p.step_cos[b * kRopePairs + t] = stab;
+      else p.step_sin[b * kRopePairs + (t - kRopePairs)] = stab;
+    }
   }
   if (!emit) return false;  // uniform over the workgroup
   float nw[kCh];
@@ -570,6 +608,10 @@ __device__ __forceinline__ void coarse_body(const EmitParams& p, int64_t blk) {
   const int64_t b = blk / kCoarseParts;
   const int part = static_cast<int>(blk % kCoarseParts);
   const EmitBranch& br = p.br;
+  const int c = t & 63, k = t >> 6;  // channel of the part, quarter of the slots
+  const int d = 64 * part + c;
+  // the token's projections are requested with the position (one round trip, not two)
+  const float kin = br.kv[b * kD + d], gin = br.gate[b * kD + d];
   const int64_t pos = p.positions[b];
   if (pos < 0) return;  // an inactive row: nothing to carry or emit
   const int r = br.ratio;  // 2 .. kCoarseMaxRatio (host check)
@@ -578,11 +620,8 @@ __device__ __forceinline__ void coarse_body(const EmitParams& p, int64_t blk) {
   const int64_t g = (pos + 1) / r - 1;
   const int64_t gp = g * r;
   const bool emit = completes && g < br.cache_cap && gp < p.tab_rows;
-  const int c = t & 63, k = t >> 6;  // channel of the part, quarter of the slots
-  const int d = 64 * part + c;
   float* ckv = br.carry_kv + b * static_cast<int64_t>(r) * kD;
   float* cgt = br.carry_gate + b * static_cast<int64_t>(r) * kD;
-  const float kin = br.kv[b * kD + d], gin = br.gate[b * kD + d];
   if (k == 0) {
     ckv[slot * kD + d] = kin;
     cgt[slot * kD + d] = gin;

@@ -462,7 +462,7 @@ __device__ __forceinline__ void emit_and_score(const IdxParams& p, const EmitPar
   float cw = p.w[row * Hi + hl];
   uint32_t tw[kRopePairs];
   load_table_row(e, pos, tw);
-  if (!emit_row<kEmitRatio>(e, row, key_lds)) return;  // uniform
+  if (!emit_row<kEmitRatio, true>(e, row, key_lds)) return;  // uniform
   const int64_t g = (pos + 1) / kEmitRatio - 1;
   if (g >= p.G) return;
   cw = lane < Hi ? cw : 0.0f;
@@ -548,8 +548,9 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
       emit_and_score<FMT, MB>(p, e, row);
       return;
     }
-    if (blockIdx.x == 1) {  // uniform: the token's window entry
+    if (blockIdx.x == 1) {  // uniform: the token's window entry and its carry slot
       if (tid < 64) kv_prologue(e, row, tid);
+      else carry_slot<kWaves * 64 - 64>(e, row, tid - 64);
       return;
     }
     if (COARSE && blockIdx.x < kLead) {  // uniform: a part of the coarse branch's group step
@@ -667,6 +668,18 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
   __shared__ uint4 qtab_lds[FUSE && !EMIT ? 16 : 1];
   if constexpr (EMIT) {
     rope_query_table(qr, qc, tw);
+    // the step's RoPE tables (row pos of the position table, which the later launches of
+    // the step read) from the row's first scoring workgroup, which holds the row already
+    // (emit_row<R, true> leaves them to it): cos in words 0..15 of tw, sin in 16..31
+    if (blockIdx.x == kLead && tid == 0 && e.step_cos && epos >= 0 && epos < e.tab_rows) {
+      uint4* dc = reinterpret_cast<uint4*>(e.step_cos + row * kRopePairs);
+      uint4* ds = reinterpret_cast<uint4*>(e.step_sin + row * kRopePairs);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        dc[k] = uint4{tw[4 * k], tw[4 * k + 1], tw[4 * k + 2], tw[4 * k + 3]};
+        ds[k] = uint4{tw[16 + 4 * k], tw[16 + 4 * k + 1], tw[16 + 4 * k + 2], tw[16 + 4 * k + 3]};
+      }
+    }
   } else if constexpr (FUSE) {
     // RoPE of the query's rope channels (owlet1/indexer.py:126-128, compress cos / sin),
     // bf16 in and out as the reference's rotated query.  q_rope_dim is a multiple of 32, so
