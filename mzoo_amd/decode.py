@@ -54,6 +54,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib, csa2_attn, indexer, quant
+from .rope import rope_inv_freq
 
 
 class GroupedOutputProjection:
@@ -88,8 +89,10 @@ class CompressorWeights:
     """What the in-step group emission reads: the compressor's RMSNorm weight
     (``owlet1/cache.py:140``), the indexer's key projection ``wk`` [Di, D] and ``k_norm`` weight
     (``owlet1/indexer.py:75-76``), their epsilons, the coarse branch's compressor norm weight
-    (hierarchical config), and the compress-RoPE base the group positions rotate with
-    (``compress_rope_theta``, ``owlet1/config.py:238``)."""
+    (hierarchical config), and the compress RoPE the group positions rotate with: its base
+    (``compress_rope_theta``, ``owlet1/config.py:238``) and, when the model extends its context
+    with YaRN (``owlet1/config.py:419-434``), the YaRN settings (the keywords of
+    ``mzoo_amd.rope.yarn_inv_freq``)."""
     norm_weight: torch.Tensor
     wk: torch.Tensor
     k_norm_weight: torch.Tensor
@@ -97,16 +100,17 @@ class CompressorWeights:
     k_eps: float = 1e-6
     coarse_norm_weight: torch.Tensor | None = None
     rope_theta: float = 160000.0
+    rope_yarn: dict | None = None
 
 
-def rope_table(positions: int, rope_dim: int, theta: float) -> torch.Tensor:
+def rope_table(positions: int, rope_dim: int, theta: float, yarn: dict | None = None) -> torch.Tensor:
     """bf16 [positions, rope_dim]: row p holds the cos (first rope_dim/2) and sin of position
     p, as ``DeepseekV41RotaryEmbedding.forward`` computes them (``owlet1/norm_rope.py:108-124``:
-    ``inv_freq = 1 / theta^(arange(0, rd, 2) / rd)``, ``pos * inv_freq`` in fp32, cos / sin,
-    then the activations' dtype), on the CPU."""
-    inv = 1.0 / (theta ** (torch.arange(0, rope_dim, 2, dtype=torch.float) / rope_dim))
+    ``inv_freq`` of the default RoPE or of YaRN, ``pos * inv_freq`` in fp32, cos / sin times
+    the attention factor, then the activations' dtype), on the CPU."""
+    inv, scale = rope_inv_freq(theta, rope_dim, yarn)
     freqs = torch.arange(positions, dtype=torch.float).view(-1, 1) * inv.view(1, -1)
-    return torch.cat([freqs.cos(), freqs.sin()], -1).to(torch.bfloat16)
+    return torch.cat([freqs.cos() * scale, freqs.sin() * scale], -1).to(torch.bfloat16)
 
 
 @dataclass
@@ -204,7 +208,7 @@ class SparseDecodeLayer:
             norm_weight=cw.norm_weight.to(**bf).contiguous(), wk=cw.wk.to(**bf).contiguous(),
             k_norm_weight=cw.k_norm_weight.to(**bf).contiguous(), eps=float(cw.eps), k_eps=float(cw.k_eps),
             coarse_norm_weight=None if cw.coarse_norm_weight is None else cw.coarse_norm_weight.to(**bf).contiguous(),
-            rope_theta=float(cw.rope_theta))
+            rope_theta=float(cw.rope_theta), rope_yarn=None if cw.rope_yarn is None else dict(cw.rope_yarn))
         if tuple(self.compressor.wk.shape) != (cfg.index_dim, d):
             raise ValueError(f"in-step emission: wk must be [{cfg.index_dim}, {d}]")
         if cfg.coarse_ratio and self.compressor.coarse_norm_weight is None:
@@ -216,7 +220,8 @@ class SparseDecodeLayer:
             self.coarse_carry_kv = torch.zeros(b, cfg.coarse_ratio, d, **f32)
             self.coarse_carry_gate = torch.zeros(b, cfg.coarse_ratio, d, **f32)
         npos = max_position or max(cfg.max_groups * cfg.ratio, cfg.coarse_groups * max(cfg.coarse_ratio, 1)) + 1
-        self.rope_table = rope_table(npos, cfg.rope, self.compressor.rope_theta).to(dev).contiguous()
+        self.rope_table = rope_table(npos, cfg.rope, self.compressor.rope_theta,
+                                     self.compressor.rope_yarn).to(dev).contiguous()
         self.step_cos = torch.zeros(b, cfg.rope // 2, **bf)
         self.step_sin = torch.zeros(b, cfg.rope // 2, **bf)
         # 64 indexer heads: the emission launch also runs the step's prologue (window entry,

@@ -34,12 +34,11 @@ compressed branch attends the groups the indexer kept; the top-k keeps ``min(k, 
 entries, never a masked one, the lower index winning among equal scores (the reference's
 ``torch.topk`` leaves ties unspecified).  Attention runs in bf16 on MFMA with fp32 softmax
 (the cached K = V entries are FP8 / FP4 fake-quantized, so exact in bf16); queries are
-rounded to bf16.  Training (dropout, backward) and YaRN RoPE scaling are not supported.
+rounded to bf16.  Training (dropout, backward) is not supported.
 """
 
 from __future__ import annotations
 
-import math
 from dataclasses import dataclass, field
 
 import torch
@@ -48,6 +47,7 @@ from torch import nn
 from transformers.cache_utils import DynamicSlidingWindowLayer
 
 from . import _lib, csa2_attn, indexer as _idx, quant
+from .rope import rope_inv_freq
 
 _FMT_BF16 = csa2_attn.FMT_BF16
 
@@ -82,18 +82,34 @@ class AttentionConfig:
     _attn_implementation: str = "mzoo_amd_sparse"
 
 
-def _rope_params(config, layer_type: str) -> tuple[float, float]:
-    """(theta, partial_rotary_factor) of a rope layer type ("main" / "compress"), from
+def _rope_params(config, layer_type: str) -> tuple[float, float, dict | None]:
+    """(theta, partial_rotary_factor, yarn) of a rope layer type ("main" / "compress"), from
     ``config.rope_parameters`` when present (owlet1/config.py:420-434), else from the flat
-    fields.  Only the default RoPE is built (YaRN is not used by the benchmark configs)."""
+    fields.  ``yarn`` is None for the default RoPE, else the YaRN settings ``yarn_inv_freq``
+    takes (owlet1/config.py:419-434: the reference applies YaRN to the compressed branches
+    only and fixes its attention factor at 1.0 unless one is given)."""
     rp = getattr(config, "rope_parameters", None)
     if isinstance(rp, dict) and isinstance(rp.get(layer_type), dict):
         sub = rp[layer_type]
-        if sub.get("rope_type", "default") != "default":
-            raise NotImplementedError(f"{layer_type} RoPE type {sub.get('rope_type')!r}: only the default RoPE is built")
-        return float(sub["rope_theta"]), float(sub.get("partial_rotary_factor", 1.0))
+        kind = sub.get("rope_type", "default")
+        yarn = None
+        if kind == "yarn":
+            orig = sub["original_max_position_embeddings"]
+            factor = sub["factor"]
+            if factor is None:
+                factor = getattr(config, "max_position_embeddings") / orig
+            yarn = dict(factor=float(factor), original_max_position_embeddings=orig,
+                        beta_fast=sub.get("beta_fast") or 32, beta_slow=sub.get("beta_slow") or 1,
+                        attention_factor=sub.get("attention_factor"), mscale=sub.get("mscale"),
+                        mscale_all_dim=sub.get("mscale_all_dim"),
+                        # read from the top level of rope_parameters, as the library the
+                        # reference calls does (transformers' _compute_yarn_parameters)
+                        truncate=rp.get("truncate", True))
+        elif kind != "default":
+            raise NotImplementedError(f"{layer_type} RoPE type {kind!r}: the default RoPE and YaRN are built")
+        return float(sub["rope_theta"]), float(sub.get("partial_rotary_factor", 1.0)), yarn
     theta = config.compress_rope_theta if layer_type == "compress" else config.rope_theta
-    return float(theta), config.qk_rope_head_dim / config.head_dim
+    return float(theta), config.qk_rope_head_dim / config.head_dim, None
 
 
 # ---- norm / rope --------------------------------------------------------------------------
@@ -125,26 +141,29 @@ class DeepseekV41RMSNorm(nn.Module):
 
 
 class DeepseekV41RotaryEmbedding(nn.Module):
-    """norm_rope.py:48-124 (default RoPE): per layer type ``inv_freq = 1 / theta^(2i/rd)``
-    with ``rd = int(head_dim * partial_rotary_factor)``; ``forward`` returns cos / sin
-    [B, S, rd/2] of ``position_ids`` in ``x.dtype``."""
+    """norm_rope.py:48-124: per layer type ``inv_freq`` -- the default RoPE ``1 /
+    theta^(2i/rd)``, or YaRN (``yarn_inv_freq``) where the config asks for it -- with ``rd =
+    int(head_dim * partial_rotary_factor)``; ``forward`` returns cos / sin [B, S, rd/2] of
+    ``position_ids`` times the type's attention factor, in ``x.dtype``."""
 
     def __init__(self, config, device=None):
         super().__init__()
         self.config = config
         self.layer_types = ["main", "compress"]
+        self.attention_scaling = {}
         for lt in self.layer_types:
-            theta, partial = _rope_params(config, lt)
-            dim = int(config.head_dim * partial)
-            inv = 1.0 / (theta ** (torch.arange(0, dim, 2, dtype=torch.float) / dim))
+            theta, partial, yarn = _rope_params(config, lt)
+            inv, scale = rope_inv_freq(theta, int(config.head_dim * partial), yarn)
+            self.attention_scaling[lt] = scale
             self.register_buffer(f"{lt}_inv_freq", inv.to(device) if device is not None else inv, persistent=False)
 
     @torch.no_grad()
     def forward(self, x, position_ids, layer_type=None):
         inv = getattr(self, f"{layer_type}_inv_freq").float().to(x.device)
+        scale = self.attention_scaling[layer_type]
         pos = position_ids.to(x.device).float()
         freqs = (inv[None, :, None].expand(pos.shape[0], -1, 1) @ pos[:, None, :]).transpose(1, 2)
-        return freqs.cos().to(dtype=x.dtype), freqs.sin().to(dtype=x.dtype)
+        return (freqs.cos() * scale).to(dtype=x.dtype), (freqs.sin() * scale).to(dtype=x.dtype)
 
 
 def apply_rotary_pos_emb(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, inverse: bool = False):

@@ -18,7 +18,8 @@ CPU in float32 (torch + numpy):
 ``cfg`` is a dict with the config fields the layer reads (``hidden_size``,
 ``num_attention_heads``, ``head_dim``, ``qk_rope_head_dim``, ``q_lora_rank``, ``o_groups``,
 ``o_lora_rank``, ``index_n_heads``, ``index_head_dim``, ``index_topk``, ``compress_ratio``,
-``sliding_window``, ``rms_norm_eps``, ``compress_rope_theta``); ``params`` maps the
+``sliding_window``, ``rms_norm_eps``, ``compress_rope_theta``, optionally ``compress_yarn``:
+the compress rope's YaRN settings, see ``rope_tables``); ``params`` maps the
 reference's parameter names to float32 tensors.  RMSNorm, the compressor's pooling and the
 quantizers are the pinned functions of ``oracle.compressor`` / ``oracle.quant``; the
 projections are torch float32 matmuls; the top-k uses ``attention.topk_indices``'s lowest-
@@ -51,15 +52,41 @@ def _t(a) -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(a, F32))
 
 
-def rope_tables(positions, rope_dim: int, theta: float) -> tuple[np.ndarray, np.ndarray]:
-    """``DeepseekV41RotaryEmbedding.forward`` (norm_rope.py:108-124) for the default RoPE:
-    ``inv_freq = 1 / theta^(arange(0, rd, 2) / rd)`` (dsv4 modeling_deepseek_v41.py:127-137,
-    ``dim = int(head_dim * partial_rotary_factor)`` = qk_rope_head_dim), then
-    ``(inv_freq @ positions).T`` cos / sin in float32 -> [..., rd/2]."""
-    inv = 1.0 / (theta ** (torch.arange(0, rope_dim, 2, dtype=torch.float) / rope_dim))
+def rope_tables(positions, rope_dim: int, theta: float, yarn: dict | None = None) -> tuple[np.ndarray, np.ndarray]:
+    """``DeepseekV41RotaryEmbedding.forward`` (norm_rope.py:108-124): ``inv_freq = 1 /
+    theta^(arange(0, rd, 2) / rd)`` for the default RoPE (dsv4 modeling_deepseek_v41.py:127-137,
+    ``dim = int(head_dim * partial_rotary_factor)`` = qk_rope_head_dim), or, with ``yarn`` (the
+    compress rope's YaRN settings, owlet1/config.py:419-434), the frequencies and attention
+    factor of the library routine the reference calls for it (transformers'
+    ``ROPE_INIT_FUNCTIONS["yarn"]``, norm_rope.py:70-73); then ``(inv_freq @ positions).T``
+    cos / sin in float32, times the attention factor -> [..., rd/2]."""
+    scale = 1.0
+    if yarn is None:
+        inv = 1.0 / (theta ** (torch.arange(0, rope_dim, 2, dtype=torch.float) / rope_dim))
+    else:
+        inv, scale = _yarn_library(theta, rope_dim, yarn)
     pos = torch.as_tensor(np.array(positions, np.float32))
     freqs = (inv.view(-1, 1) @ pos.reshape(1, -1)).T.reshape(*pos.shape, -1)
-    return freqs.cos().numpy(), freqs.sin().numpy()
+    return (freqs.cos() * scale).numpy(), (freqs.sin() * scale).numpy()
+
+
+def _yarn_library(theta: float, rope_dim: int, yarn: dict):
+    """transformers' YaRN frequencies for a rope of ``rope_dim`` channels (a config whose
+    head_dim is rope_dim, partial factor 1); ``yarn`` holds the rope_parameters sub-dict keys
+    (factor, original_max_position_embeddings, beta_fast, beta_slow, attention_factor, mscale,
+    mscale_all_dim) and optionally ``truncate`` (top level of rope_parameters, where the library
+    reads it) and ``max_position_embeddings``."""
+    from transformers import PretrainedConfig
+    from transformers.modeling_rope_utils import ROPE_INIT_FUNCTIONS
+    sub = {k: v for k, v in yarn.items() if k not in ("truncate", "max_position_embeddings")}
+    sub.update(rope_type="yarn", rope_theta=theta, partial_rotary_factor=1.0)
+    rp = {"compress": sub}
+    if "truncate" in yarn:
+        rp["truncate"] = yarn["truncate"]
+    c = PretrainedConfig(head_dim=rope_dim, hidden_size=rope_dim, num_attention_heads=1,
+                         max_position_embeddings=yarn.get("max_position_embeddings", 1 << 20), rope_parameters=rp)
+    inv, scale = ROPE_INIT_FUNCTIONS["yarn"](c, None, layer_type="compress")
+    return inv.float(), float(scale)
 
 
 def rms_norm(x, weight, eps) -> np.ndarray:
@@ -132,7 +159,7 @@ def indexer(params, cfg, x, q_residual, latent, fgp, positions, state, shared, s
             k = rms_norm(linear(latent, params["indexer.wk.weight"]), params["indexer.k_norm.weight"],
                          cfg["rms_norm_eps"])
             gpos = fgp + r * np.arange(latent.shape[1])
-            cos, sin = rope_tables(np.broadcast_to(gpos, (b, len(gpos))), rd, theta)
+            cos, sin = rope_tables(np.broadcast_to(gpos, (b, len(gpos))), rd, theta, cfg.get("compress_yarn"))
             k = C.rope(k, cos, sin)
             k = Q.fake_quant_fp4_block(k, 32)
             if state is not None:
@@ -145,7 +172,7 @@ def indexer(params, cfg, x, q_residual, latent, fgp, positions, state, shared, s
     g = 0 if index_k is None else index_k.shape[1]
     if g == 0:
         return
-    cos_q, sin_q = rope_tables(positions, rd, theta)                  # indexer.py:124-126
+    cos_q, sin_q = rope_tables(positions, rd, theta, cfg.get("compress_yarn"))  # indexer.py:124-126
     q = linear(q_residual, params["indexer.wq_b.weight"]).reshape(b, s, hi, di)
     q = C.rope(q, cos_q[:, :, None], sin_q[:, :, None])
     q = Q.fake_quant_fp4_block(q, 32)
@@ -203,7 +230,7 @@ def attention_layer(params, cfg, i: int, x, positions, state: LayerState | None,
     eps = cfg["rms_norm_eps"]
     lcfg = dict(cfg, compress_ratio=r)
     theta = cfg["compress_rope_theta"] if r else cfg.get("rope_theta", 10000.0)   # attention.py:100, :143
-    cos, sin = rope_tables(positions, rd, theta)
+    cos, sin = rope_tables(positions, rd, theta, cfg.get("compress_yarn") if r else None)
 
     q_res = rms_norm(linear(x, params["wq_a.weight"]), params["q_norm.weight"], eps)
     q = linear(q_res, params["wq_b.weight"]).reshape(b, s, h, d)
@@ -236,7 +263,8 @@ def attention_layer(params, cfg, i: int, x, positions, state: LayerState | None,
         sel = shared.get("selection")
         if latent is not None:                                         # attention.py:173-192
             gpos = fgp + r * np.arange(latent.shape[1])
-            cc, ss = rope_tables(np.broadcast_to(gpos, (b, len(gpos))), rd, cfg["compress_rope_theta"])
+            cc, ss = rope_tables(np.broadcast_to(gpos, (b, len(gpos))), rd, cfg["compress_rope_theta"],
+                                 cfg.get("compress_yarn"))
             rot = Q.fake_quant_fp4_block(C.rope(latent, cc, ss), 16, e4m3_scales=True)
             if state is not None:
                 state.compressed = rot if state.compressed is None else np.concatenate([state.compressed, rot], 1)

@@ -270,3 +270,34 @@ def test_attention_interface_matches_eager(dev):
     assert weights is None and got.shape == (b, s, h, d)
     ref, _ = OA._attend(q, kv, kv, mask, mod.attn_sink.detach().cpu())
     _assert_attn(got.cpu(), ref, "attention interface")
+
+
+def test_layer_with_yarn(dev):
+    """The compress RoPE extended with YaRN (owlet1/config.py:419-434: the reference's
+    rope_parameters layout, YaRN on the compressed branch only): the drop-in layer against the
+    oracle composition, whose YaRN tables come from the library routine the reference calls.
+    The original context is short enough that YaRN changes most pairs' frequencies at these
+    positions, so the default-RoPE composition misses the bar."""
+    c = spec.CONFIGS["small"]
+    yarn = dict(factor=8.0, original_max_position_embeddings=64, attention_factor=1.0)
+    params, x, pos = spec.make_params_and_inputs(c)
+    cfg = _config(c)
+    partial = c["qk_rope_head_dim"] / c["head_dim"]
+    cfg.rope_parameters = {
+        "main": {"rope_type": "default", "rope_theta": spec.ROPE_THETA, "partial_rotary_factor": partial},
+        "compress": dict(yarn, rope_type="yarn", rope_theta=spec.COMPRESS_ROPE_THETA, partial_rotary_factor=partial)}
+    mod = MO.DeepseekV41Attention(cfg, 0)
+    res = mod.load_state_dict(params, strict=True)
+    assert not res.missing_keys and not res.unexpected_keys
+    mod = mod.to(dev).eval()
+    out, shared = _forward(mod, x, pos, None, dev)
+    torch.cuda.synchronize()
+    b, s, g = c["batch"], c["seq"], c["seq"] // c["compress_ratio"]
+    sel = _selection(shared, b, s, g)
+    ref, oshared = OM.layer_forward(params, dict(_ocfg(c), compress_yarn=yarn), x, pos, select=sel)
+    _assert_attn(out.cpu(), ref, "small layer with YaRN vs oracle")
+    gk = shared["index_k"][:, 0].float().cpu().numpy()
+    assert np.mean(gk == oshared["index_k"]) > 0.999, "published indexer keys (YaRN)"
+    plain, _ = OM.layer_forward(params, _ocfg(c), x, pos, select=sel)
+    assert cosine(torch.from_numpy(plain).flatten(), out.cpu().float().flatten()) < ATTN_COS_MIN, \
+        "YaRN made no difference at these positions"
