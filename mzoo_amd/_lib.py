@@ -9,12 +9,14 @@ call raises.
 from __future__ import annotations
 
 import ctypes
+import os
 import pathlib
 import re
 
 import torch
 
-LIB_PATH = pathlib.Path(__file__).resolve().parent / "_mzk.so"
+# MZOO_AMD_LIB names another build of the library (the sanitizer build of the host code)
+LIB_PATH = pathlib.Path(os.environ.get("MZOO_AMD_LIB") or pathlib.Path(__file__).resolve().parent / "_mzk.so")
 HEADER = pathlib.Path(__file__).resolve().parent.parent / "include" / "mzk.h"
 
 MZK_F32, MZK_BF16, MZK_F16 = 0, 1, 2

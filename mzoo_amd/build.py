@@ -38,33 +38,43 @@ COMMON = [
 ]
 
 
-def _compile(src: pathlib.Path) -> pathlib.Path:
-    obj = OBJ / (src.name + ".o")
-    cmd = [HIPCC, *COMMON, "-c", str(src), "-o", str(obj)]
+# The AddressSanitizer variant (``build(asan=True)``): the host code -- argument checks,
+# dispatch, the error text -- instrumented, the device code as in the product.  It loads into
+# a process that preloads the sanitizer runtime (tests/test_asan_host.py).
+ASAN_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer"]
+ASAN_OUT = OBJ / "asan" / "_mzk_asan.so"
+
+
+def _compile(src: pathlib.Path, obj_dir: pathlib.Path = OBJ, extra: tuple = ()) -> pathlib.Path:
+    obj = obj_dir / (src.name + ".o")
+    cmd = [HIPCC, *COMMON, *extra, "-c", str(src), "-o", str(obj)]
     if src.suffix == ".cpp":
-        cmd = [HIPCC, *[f for f in COMMON if f not in ("--offload-arch=gfx950",)], "-x", "c++", "-c", str(src),
-               "-o", str(obj)]
+        cmd = [HIPCC, *[f for f in COMMON if f not in ("--offload-arch=gfx950",)], *extra, "-x", "c++", "-c",
+               str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
     return obj
 
 
-def build(verbose: bool = True) -> pathlib.Path:
-    OBJ.mkdir(exist_ok=True)
+def build(verbose: bool = True, asan: bool = False) -> pathlib.Path:
+    out = ASAN_OUT if asan else OUT
+    obj_dir = out.parent if asan else OBJ
+    obj_dir.mkdir(parents=True, exist_ok=True)
+    extra = tuple(ASAN_FLAGS) if asan else ()
     sources = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
     jobs = min(len(sources), max(1, min(8, os.cpu_count() or 1)))
     with cf.ThreadPoolExecutor(jobs) as ex:
-        objs = list(ex.map(_compile, sources))
-    tmp = OUT.with_suffix(".so.tmp")
-    cmd = [HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", *map(str, objs), "-o", str(tmp)]
+        objs = list(ex.map(lambda f: _compile(f, obj_dir, extra), sources))
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", *extra, *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, OUT)
+    os.replace(tmp, out)
     if verbose:
-        print(f"built {OUT} from {len(sources)} sources")
-    return OUT
+        print(f"built {out} from {len(sources)} sources")
+    return out
 
 
 def clean() -> None:
@@ -75,4 +85,4 @@ def clean() -> None:
 if __name__ == "__main__":
     if "--clean" in sys.argv:
         clean()
-    build()
+    build(asan="--asan" in sys.argv)
