@@ -487,6 +487,24 @@ int mzk_sparse_mqa_rope(const void* q, int64_t B, int64_t S, int H, int D, int f
                         float* workspace, int64_t workspace_bytes, void* out, float* lse,
                         const void* rope_cos, const void* rope_sin, int rope_dim, void* stream);
 
+/* mzk_sparse_mqa_rope (rope_cos / rope_sin may be NULL: then mzk_sparse_mqa) for one decode
+ * step (S = 1, out and lse given) that also advances the positions it reads: positions[b] +=
+ * 1 for every row once the call's launches have read them -- in the split merge's launch,
+ * which reads no position (nsplit > 1 with the merge kernel), else in a launch of its own
+ * after the attention.  Saves a decode step its separate `positions += 1` launch (1.5-2.5 us
+ * inside a HIP graph on MI355X).  A caller whose later launches of the same step read the
+ * same positions advances them once, on the last call.  No counterpart in the reference:
+ * its decoder derives each step's position_ids on the host from the tokens the cache has
+ * seen (owlet1/decoder.py:285-288); this build keeps positions on the device so that graph
+ * replays decode consecutive tokens. */
+int mzk_sparse_mqa_advance(const void* q, int64_t B, int64_t S, int H, int D, int fmt, int nope,
+                           int64_t* positions, const void* win, int64_t win_batch_entries, int win_cap,
+                           int window, const void* dense, int64_t dense_batch_entries, int dense_cap,
+                           int dense_ratio, const void* main_kv, int64_t main_batch_entries, int64_t G,
+                           const int32_t* idx, int64_t idx_row_stride, int topk, const float* sinks, int nsplit,
+                           float* workspace, int64_t workspace_bytes, void* out, float* lse, const void* rope_cos,
+                           const void* rope_sin, int rope_dim, void* stream);
+
 /* The split partials of part of a row's entry list, for launches that share one workspace:
  * splits split_base .. split_base + nsplit - 1 of a workspace holding split_total splits
  * per row (rows*split_total*H*(2*D+8) bytes, laid out as for mzk_sparse_mqa), over the

@@ -70,6 +70,8 @@ _SIGS = {
     "mzk_sparse_mqa_set_merge": [_I32],
     "mzk_sparse_mqa_rope": [_P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _I64, _I32, _I32, _P, _I64, _I32, _I32,
                             _P, _I64, _I64, _P, _I64, _I32, _P, _I32, _P, _I64, _P, _P, _P, _P, _I32, _P],
+    "mzk_sparse_mqa_advance": [_P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _I64, _I32, _I32, _P, _I64, _I32,
+                               _I32, _P, _I64, _I64, _P, _I64, _I32, _P, _I32, _P, _I64, _P, _P, _P, _P, _I32, _P],
     "mzk_sparse_mqa_part": [_P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _I64, _I32, _I32, _P, _I64, _I32, _I32,
                             _P, _I64, _I64, _P, _I64, _I32, _I32, _I32, _I32, _P, _I64, _P, _P, _I32, _P],
     "mzk_sparse_mqa_combine_rope": [_P, _I64, _I64, _I32, _I32, _I32, _P, _P, _P, _I32, _P, _P, _P],

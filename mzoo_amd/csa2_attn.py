@@ -108,7 +108,7 @@ def sparse_mqa_decode(q: torch.Tensor, positions: torch.Tensor, win_cache: torch
                       dense_cache: torch.Tensor | None = None, dense_ratio: int = 1,
                       sinks: torch.Tensor | None = None, nsplit: int = 1, nope: int = 512,
                       workspace: torch.Tensor | None = None, out: torch.Tensor | None = None,
-                      lse: torch.Tensor | None = None, rope: tuple | None = None):
+                      lse: torch.Tensor | None = None, rope: tuple | None = None, advance: bool = False):
     """One decode token per batch row over FP8-b128 caches.
 
     q bf16 [B,H,D]; positions int64 [B] (absolute position of the new token, whose own
@@ -119,7 +119,11 @@ def sparse_mqa_decode(q: torch.Tensor, positions: torch.Tensor, win_cache: torch
 
     ``rope=(cos, sin)`` (bf16 [B, (D-nope)/2], the row's ``position_embeddings``): q arrives
     unrotated and the kernels apply ``apply_rotary_pos_emb`` to it on load and the inverse
-    rotation to the output (``owlet1/attention.py:147`` and ``:226`` fused in)."""
+    rotation to the output (``owlet1/attention.py:147`` and ``:226`` fused in).
+
+    ``advance=True`` also adds 1 to ``positions`` once the call's launches have read them, in
+    the split merge's launch (no launch of its own for a decode step's ``positions += 1``;
+    ``mzk_sparse_mqa_advance``)."""
     b, h, d = q.shape
     _lib.require_gpu(q, positions, win_cache)
     # the kernels read these buffers through raw pointers with the layouts below: a wrong
@@ -159,7 +163,10 @@ def sparse_mqa_decode(q: torch.Tensor, positions: torch.Tensor, win_cache: torch
             _lib.ptr(main_cache), 0 if main_cache is None else main_cache.shape[1], groups,
             _lib.ptr(indices), topk, topk, _lib.ptr(sinks), nsplit, _lib.ptr(workspace), need,
             out.data_ptr(), lse.data_ptr())
-    if rope is None:
+    if advance:
+        _lib.call("mzk_sparse_mqa_advance", *args, _lib.ptr(rc), _lib.ptr(rs), 0 if rope is None else d - nope,
+                  _lib.stream_of(q))
+    elif rope is None:
         _lib.call("mzk_sparse_mqa", *args, _lib.stream_of(q))
     else:
         _lib.call("mzk_sparse_mqa_rope", *args, rc.data_ptr(), rs.data_ptr(), d - nope, _lib.stream_of(q))

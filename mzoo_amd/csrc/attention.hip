@@ -1407,6 +1407,12 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
   }
 }
 
+// positions[i] += 1 for the rows of a call whose last launch does not merge splits.
+__global__ void __launch_bounds__(256) advance_kernel(int64_t* __restrict__ positions, int64_t rows) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < rows) positions[i] += 1;
+}
+
 // The merge launch: the split partials merged with the sink (merge_pieces).  One thread per
 // 8 * NP channels of a (row, head), NP 16-byte pieces of every split in flight per memory
 // round trip.  A wave takes 16 heads x 4 runs of 8 * NP channels (lane % 16 the head, lane /
@@ -1418,8 +1424,15 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
                                                       int64_t rows, const float* __restrict__ sinks,
                                                       uint16_t* __restrict__ out, float* __restrict__ lse,
                                                       const uint16_t* __restrict__ rope_cos,
-                                                      const uint16_t* __restrict__ rope_sin, int rope_dim) {
+                                                      const uint16_t* __restrict__ rope_sin, int rope_dim,
+                                                      int64_t* __restrict__ advance) {
   static_assert(D % 16 == 0 && (NP == 1 || NP == 2), "16-channel groups, one or two pieces per thread");
+  // a decode step's position advance: this launch reads no position and the attention launch
+  // before it has read them all; thread i of the grid (at least `rows` threads) owns row i
+  if (advance != nullptr) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i < rows) advance[i] += 1;
+  }
   constexpr int CPW = 4 * 8 * NP;             // channels per wave
   constexpr int NWB = (D + CPW - 1) / CPW;    // waves per 16 heads of a row
   const int nhb = (H + 15) / 16;
@@ -1549,7 +1562,7 @@ int dispatch(int fmt, int D, int nope, const AttnParams& p, int64_t rows, hipStr
 template <int D>
 void launch_combine(const uint16_t* po, const float* pml, int nsplit, int H, int64_t S, const float* sinks,
                     uint16_t* out, float* lse, int64_t rows, const uint16_t* rope_cos, const uint16_t* rope_sin,
-                    int rope_dim, hipStream_t s) {
+                    int rope_dim, int64_t* advance, hipStream_t s) {
   // two 16-byte pieces per thread for a few splits, where a thread's channels cannot straddle
   // the rope slice (config 2, 4 splits: 7.4 vs 7.9 us); with more splits, whose chunk of 8
   // then holds 16 pieces in flight per thread, one is faster (configs 4 / 5, 16 / 32 splits:
@@ -1559,11 +1572,13 @@ void launch_combine(const uint16_t* po, const float* pml, int nsplit, int H, int
   if (nsplit <= 4 && (rope_cos == nullptr || (D - rope_dim) % 16 == 0)) {
     const int64_t n = threads(2);
     combine_kernel<D, 2><<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(po, pml, nsplit, H, S, rows, sinks,
-                                                                                out, lse, rope_cos, rope_sin, rope_dim);
+                                                                                out, lse, rope_cos, rope_sin, rope_dim,
+                                                                                advance);
   } else {
     const int64_t n = threads(1);
     combine_kernel<D, 1><<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(po, pml, nsplit, H, S, rows, sinks,
-                                                                                out, lse, rope_cos, rope_sin, rope_dim);
+                                                                                out, lse, rope_cos, rope_sin, rope_dim,
+                                                                                advance);
   }
 }
 
@@ -1574,7 +1589,8 @@ using namespace mzk;
 
 namespace {
 int combine_impl(const float* workspace, int64_t B, int64_t S, int H, int D, int nsplit, const float* sinks,
-                 const void* rope_cos, const void* rope_sin, int rope_dim, void* out, float* lse, void* stream);
+                 const void* rope_cos, const void* rope_sin, int rope_dim, void* out, float* lse, int64_t* advance,
+                 void* stream);
 
 // Where the split merge runs: 0: the merge launch (the default); 1: inside the attention
 // launch where it applies; 2: inside, every workgroup on the release / acquire path (a test
@@ -1611,7 +1627,7 @@ int sparse_mqa_impl(const void* q, int64_t B, int64_t S, int H, int D, int fmt, 
                     int64_t main_batch_entries, int64_t G, const int32_t* idx, int64_t idx_row_stride, int topk,
                     const float* sinks, int nsplit, float* workspace, int64_t workspace_bytes, void* out, float* lse,
                     const void* rope_cos, const void* rope_sin, int rope_dim, int split_base, int split_total,
-                    void* stream) {
+                    void* stream, int64_t* advance = nullptr) {
   const bool part_only = split_total >= 1;
   MZK_CHECK_ARG(B >= 0 && S >= 0 && H >= 1 && D > 0, "sparse_mqa: bad sizes");
   if (rope_cos || rope_sin) {
@@ -1720,12 +1736,17 @@ int sparse_mqa_impl(const void* q, int64_t B, int64_t S, int H, int D, int fmt, 
   if (rc) return rc;
   MZK_LAUNCH_CHECK("sparse_mqa");
   if (!part_only && nsplit > 1 && out != nullptr && !merged)
-    return combine_impl(workspace, B, S, H, D, nsplit, sinks, rope_cos, rope_sin, rope_dim, out, lse, stream);
+    return combine_impl(workspace, B, S, H, D, nsplit, sinks, rope_cos, rope_sin, rope_dim, out, lse, advance, stream);
+  if (advance != nullptr) {  // no merge launch follows: one of its own
+    advance_kernel<<<static_cast<unsigned>((rows + 255) / 256), 256, 0, s>>>(advance, rows);
+    MZK_LAUNCH_CHECK("sparse_mqa_advance");
+  }
   return MZK_OK;
 }
 
 int combine_impl(const float* workspace, int64_t B, int64_t S, int H, int D, int nsplit, const float* sinks,
-                 const void* rope_cos, const void* rope_sin, int rope_dim, void* out, float* lse, void* stream) {
+                 const void* rope_cos, const void* rope_sin, int rope_dim, void* out, float* lse, int64_t* advance,
+                 void* stream) {
   MZK_CHECK_ARG(B >= 0 && S >= 0 && H >= 1 && nsplit >= 1, "sparse_mqa_combine: bad sizes");
   if (rope_cos || rope_sin) {
     MZK_CHECK_ARG(rope_cos && rope_sin, "sparse_mqa_combine_rope: cos and sin go together");
@@ -1745,12 +1766,12 @@ int combine_impl(const float* workspace, int64_t B, int64_t S, int H, int D, int
   const uint16_t* rs_ = static_cast<const uint16_t*>(rope_sin);
   hipStream_t s = as_stream(stream);
   switch (D) {
-    case 64: launch_combine<64>(po, pml, nsplit, H, S, sinks, o, lse, rows, rc_, rs_, rope_dim, s); break;
-    case 96: launch_combine<96>(po, pml, nsplit, H, S, sinks, o, lse, rows, rc_, rs_, rope_dim, s); break;
-    case 128: launch_combine<128>(po, pml, nsplit, H, S, sinks, o, lse, rows, rc_, rs_, rope_dim, s); break;
-    case 160: launch_combine<160>(po, pml, nsplit, H, S, sinks, o, lse, rows, rc_, rs_, rope_dim, s); break;
-    case 256: launch_combine<256>(po, pml, nsplit, H, S, sinks, o, lse, rows, rc_, rs_, rope_dim, s); break;
-    case 576: launch_combine<576>(po, pml, nsplit, H, S, sinks, o, lse, rows, rc_, rs_, rope_dim, s); break;
+    case 64: launch_combine<64>(po, pml, nsplit, H, S, sinks, o, lse, rows, rc_, rs_, rope_dim, advance, s); break;
+    case 96: launch_combine<96>(po, pml, nsplit, H, S, sinks, o, lse, rows, rc_, rs_, rope_dim, advance, s); break;
+    case 128: launch_combine<128>(po, pml, nsplit, H, S, sinks, o, lse, rows, rc_, rs_, rope_dim, advance, s); break;
+    case 160: launch_combine<160>(po, pml, nsplit, H, S, sinks, o, lse, rows, rc_, rs_, rope_dim, advance, s); break;
+    case 256: launch_combine<256>(po, pml, nsplit, H, S, sinks, o, lse, rows, rc_, rs_, rope_dim, advance, s); break;
+    case 576: launch_combine<576>(po, pml, nsplit, H, S, sinks, o, lse, rows, rc_, rs_, rope_dim, advance, s); break;
     default: set_last_error("sparse_mqa_combine: unsupported head dim %d", D); return MZK_EUNSUPPORTED;
   }
   MZK_LAUNCH_CHECK("sparse_mqa_combine");
@@ -1782,6 +1803,21 @@ extern "C" int mzk_sparse_mqa_rope(const void* q, int64_t B, int64_t S, int H, i
                          dense_batch_entries, dense_cap, dense_ratio, main_kv, main_batch_entries, G, idx,
                          idx_row_stride, topk, sinks, nsplit, workspace, workspace_bytes, out, lse, rope_cos, rope_sin,
                          rope_dim, 0, -1, stream);
+}
+
+extern "C" int mzk_sparse_mqa_advance(const void* q, int64_t B, int64_t S, int H, int D, int fmt, int nope,
+                                      int64_t* positions, const void* win, int64_t win_batch_entries, int win_cap,
+                                      int window, const void* dense, int64_t dense_batch_entries, int dense_cap,
+                                      int dense_ratio, const void* main_kv, int64_t main_batch_entries, int64_t G,
+                                      const int32_t* idx, int64_t idx_row_stride, int topk, const float* sinks,
+                                      int nsplit, float* workspace, int64_t workspace_bytes, void* out, float* lse,
+                                      const void* rope_cos, const void* rope_sin, int rope_dim, void* stream) {
+  MZK_CHECK_ARG(S == 1, "sparse_mqa_advance: one query per row (a decode step), got S = %lld", (long long)S);
+  MZK_CHECK_ARG(out != nullptr && lse != nullptr, "sparse_mqa_advance: out and lse are required");
+  return sparse_mqa_impl(q, B, S, H, D, fmt, nope, positions, win, win_batch_entries, win_cap, window, dense,
+                         dense_batch_entries, dense_cap, dense_ratio, main_kv, main_batch_entries, G, idx,
+                         idx_row_stride, topk, sinks, nsplit, workspace, workspace_bytes, out, lse, rope_cos, rope_sin,
+                         rope_dim, 0, -1, stream, positions);
 }
 
 extern "C" int mzk_sparse_mqa_part(const void* q, int64_t B, int64_t S, int H, int D, int fmt, int nope,
@@ -1875,12 +1911,12 @@ extern "C" int mzk_sparse_mqa_set_merge(int mode) {
 
 extern "C" int mzk_sparse_mqa_combine(const float* workspace, int64_t B, int64_t S, int H, int D, int nsplit,
                                       const float* sinks, void* out, float* lse, void* stream) {
-  return combine_impl(workspace, B, S, H, D, nsplit, sinks, nullptr, nullptr, 0, out, lse, stream);
+  return combine_impl(workspace, B, S, H, D, nsplit, sinks, nullptr, nullptr, 0, out, lse, nullptr, stream);
 }
 
 extern "C" int mzk_sparse_mqa_combine_rope(const float* workspace, int64_t B, int64_t S, int H, int D, int nsplit,
                                            const float* sinks, const void* rope_cos, const void* rope_sin,
                                            int rope_dim, void* out, float* lse, void* stream) {
   MZK_CHECK_ARG(rope_cos && rope_sin, "sparse_mqa_combine_rope: cos and sin are required");
-  return combine_impl(workspace, B, S, H, D, nsplit, sinks, rope_cos, rope_sin, rope_dim, out, lse, stream);
+  return combine_impl(workspace, B, S, H, D, nsplit, sinks, rope_cos, rope_sin, rope_dim, out, lse, nullptr, stream);
 }

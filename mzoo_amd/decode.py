@@ -25,7 +25,7 @@ preallocated on the device so the whole step records into one HIP graph:
      append + quantization launch, then the scores launch,
   4. top-k (lowest index wins ties),
   5. sparse MQA over window + [coarse] + top-k entries with the sink, split-KV + merge,
-  6. ``positions += 1`` when ``advance``.
+  6. ``positions += 1`` when ``advance`` (by the merge launch of step 5, no launch of its own).
 
 Group emission -- the compressor, the cache append and the indexer's key publication, one
 entry per ``ratio`` tokens (``owlet1/cache.py:96-124``, ``:159-172``, ``owlet1/indexer.py:96-117``,
@@ -419,9 +419,7 @@ class SparseDecodeLayer:
                 raise ValueError("step(rope='table'): needs the kv projection and the layer's kv_norm_weight")
             if self._merged_emit:
                 self._emit_scores(compress, kvc, q_idx.contiguous(), w)
-                self._select_and_attend(q, (self.step_cos, self.step_sin))
-                if advance:
-                    self.positions.add_(1)
+                self._select_and_attend(q, (self.step_cos, self.step_sin), advance)
                 return self.out if self.out_proj is None else self.out_proj(self.out)
             self._emit(compress, True, prologue=(kvc, q_idx.contiguous()))
             pos = self.positions.view(b, 1)
@@ -431,9 +429,7 @@ class SparseDecodeLayer:
             else:
                 indexer.scores_mxfp4(self.q_codes, self.q_e8m0, w.view(b, 1, -1), self.k_packed, self.k_e8m0,
                                      compress_ratio=cfg.ratio, positions=pos, out=self.scores)
-            self._select_and_attend(q, (self.step_cos, self.step_sin))
-            if advance:
-                self.positions.add_(1)
+            self._select_and_attend(q, (self.step_cos, self.step_sin), advance)
             return self.out if self.out_proj is None else self.out_proj(self.out)
         if compress is not None:
             self._emit(compress, from_table)
@@ -461,9 +457,7 @@ class SparseDecodeLayer:
                       cfg.index_dim, 1, self.q_codes.data_ptr(), None, self.q_e8m0.data_ptr(), _lib.stream_of(qc))
             indexer.scores_mxfp4(self.q_codes, self.q_e8m0, w.view(b, 1, -1), self.k_packed, self.k_e8m0,
                                  compress_ratio=cfg.ratio, positions=pos, out=self.scores)
-        self._select_and_attend(q, None)
-        if advance:
-            self.positions.add_(1)
+        self._select_and_attend(q, None, advance)
         return self.out
 
     def _step_fused(self, q, kv, q_idx, w, advance, rope):
@@ -480,13 +474,12 @@ class SparseDecodeLayer:
                              positions=self.positions.view(b, 1), q_rope=(icos, isin), kv=kv,
                              kv_weight=self.kv_norm_weight, kv_eps=self.kv_norm_eps, kv_rope=(cos, sin),
                              win_cache=self.win, out=self.scores, nope=cfg.nope, rope=cfg.rope)
-        self._select_and_attend(q, (cos, sin))
-        if advance:
-            self.positions.add_(1)
+        self._select_and_attend(q, (cos, sin), advance)
         return self.out if self.out_proj is None else self.out_proj(self.out)
 
-    def _select_and_attend(self, q, rope):
-        """Top-k, then the attention over [window ; dense ; top-k entries] with the sink.  With
+    def _select_and_attend(self, q, rope, advance=False):
+        """Top-k, then the attention over [window ; dense ; top-k entries] with the sink, and
+        with ``advance`` the positions' ``+= 1`` (in the merge launch).  With
         ``branch_overlap`` the window and dense branches run on the side stream while the
         top-k runs, each launch writing its own splits of the shared workspace, and one merge
         takes them all (the same softmax over the concatenated entries)."""
@@ -498,7 +491,7 @@ class SparseDecodeLayer:
                                         groups=cfg.max_groups, indices=self.idx, dense_cache=self.coarse,
                                         dense_ratio=max(cfg.coarse_ratio, 1), sinks=self.sinks, nsplit=cfg.nsplit,
                                         nope=cfg.nope, workspace=self.workspace, out=self.out, lse=self.lse,
-                                        rope=rope)
+                                        rope=rope, advance=advance)
             return
         # the side stream reads q and the RoPE tables while the main stream runs on: they
         # must be the caller's own tensors, not temporaries the caching allocator could hand
@@ -538,6 +531,8 @@ class SparseDecodeLayer:
             _lib.call("mzk_sparse_mqa_combine_rope", ws.data_ptr(), b, 1, cfg.heads, cfg.dim, total,
                       _lib.ptr(self.sinks), rc.data_ptr(), rs.data_ptr(), cfg.rope, self.out.data_ptr(),
                       self.lse.data_ptr(), main.cuda_stream)
+        if advance:
+            self.positions.add_(1)
 
     def capture(self, q, kv, q_idx, w, advance: bool = False, warmup: int = 2,
                 rope: tuple | str | None = None, compress: tuple | None = None,

@@ -98,6 +98,32 @@ def test_topk_long_rows_split_over_workgroups(dev, rows, g, k, kind):
     assert np.array_equal(single.cpu().numpy(), want)
 
 
+def test_topk_long_rows_reuse_one_workspace(dev):
+    """One workspace serves calls of different row counts, lengths, data and k in a row,
+    never cleared: every launch writes the state the next one reads (chunk histograms,
+    counts, the per-row selection, the candidates it reads back), so no call depends on
+    what an earlier call left.  The workspace starts filled with garbage to show it needs
+    no initialization."""
+    shapes = [(4, 131072, 2048, "distinct"), (8, 65537, 512, "ties"), (2, 262144, 4096, "three_values"),
+              (4, 131072, 2048, "distinct"), (1, 524288, 16384, "negative"), (8, 40000, 2048, "ties")]
+    size = max(MI.topk_workspace_bytes(r, g) for r, g, _, _ in shapes)
+    assert size > 0
+    ws = torch.randint(-2**31, 2**31 - 1, ((size + 15) // 16 * 4,), dtype=torch.int32, device=dev)
+    for i, (rows, g, k, kind) in enumerate(shapes):
+        gen = torch.Generator().manual_seed(1000 + i)
+        if kind == "distinct":
+            sc = torch.randn(rows, g, generator=gen)
+        elif kind == "ties":
+            sc = torch.round(torch.randn(rows, g, generator=gen) * 8) / 8
+            sc[:, 3::7] = float("-inf")
+        elif kind == "three_values":
+            sc = torch.randint(0, 3, (rows, g), generator=gen).float()
+        else:
+            sc = -torch.rand(rows, g, generator=gen) - 1.0
+        got = MI.topk(sc.to(dev), k, workspace=ws).cpu().numpy()
+        assert np.array_equal(got, OA.topk_indices(sc.numpy(), k)), (i, rows, g, k, kind)
+
+
 @pytest.mark.parametrize("case", ["distinct", "near_lowest_float", "mixed_sign_few_exponents"])
 def test_topk_exact_distinct_and_extreme(dev, case):
     """Distinct scores (the radix search usually stops once the k-th key's bin is taken
