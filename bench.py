@@ -11,8 +11,10 @@ ring; every 4th token the group's pooling + norm, its rotated FP8-b128 cache ent
 index key; the token's RoPE tables from the position table), the new token's kv RMSNorm +
 RoPE + window append, the indexer query's RoPE + quantization and the indexer scores (one
 launch), top-k, sparse MQA with the query's RoPE on load (split-KV), and the split merge with
-the output's inverse RoPE -- the per-token work of ``DeepseekV41Attention.forward`` between
-the projections.  Every replay advances the positions, so the replays decode consecutive
+the output's inverse RoPE and the positions' advance -- the per-token work of
+``DeepseekV41Attention.forward`` between the projections.  At config 2 (8192 keys) the top-k
+runs inside the attention launch (every attention workgroup of a row selects the row's list
+from the scores itself); longer rows keep the top-k launch.  Every replay advances the positions, so the replays decode consecutive
 tokens ending at position ctx-1 and emit a group every 4th step, as a decode loop does
 (``--prologue rotated`` takes already-rotated q / q_idx / latent at a fixed position instead,
 without emission, as the kernels' reference signatures do).  Distinct layers keep one layer's working set
@@ -357,6 +359,19 @@ def stage_fns(torch, layer, inputs):
         else:
             _lib.call("mzk_sparse_mqa", *args, st())
     fns["sparse_mqa"] = attn
+    if layer.selects_in_attention:
+        # the step's attention launch: the row's top-k selected inside it from the scores (the
+        # "topk" and "sparse_mqa" stages above are the two launches it replaces)
+        def attn_select():
+            _lib.call("mzk_sparse_mqa_select", q.data_ptr(), b, cfg.heads, cfg.dim, 1, cfg.nope,
+                      layer.positions.data_ptr(), 0, layer.win.data_ptr(), cfg.window, cfg.window, cfg.window,
+                      None if coarse is None else coarse.data_ptr(), cfg.coarse_groups, cfg.coarse_groups,
+                      max(cfg.coarse_ratio, 1), layer.main.data_ptr(), cfg.max_groups, cfg.max_groups,
+                      layer.scores.data_ptr(), cfg.max_groups, cfg.topk, layer.idx.data_ptr(), cfg.topk,
+                      layer.sinks.data_ptr(), cfg.nsplit, ws.data_ptr(), ws.numel() * ws.element_size(),
+                      *((layer.out.data_ptr(), layer.lse.data_ptr()) if inline else (None, None)),
+                      *((rope[0].data_ptr(), rope[1].data_ptr(), cfg.rope) if rope else (None, None, 0)), st())
+        fns["sparse_mqa_select"] = attn_select
     if inline:
         pass
     elif rope:
@@ -513,11 +528,18 @@ def run_decode(torch, dev, args):
     idx_flops = rows * 2.0 * cfg.index_heads * cfg.index_dim * cfg.max_groups
     idx_stage = next(k for k in ("indexer_emit_fp8", "indexer_emit_mxfp4", "indexer_scores_fp8",
                                  "indexer_scores_mxfp4", "indexer_decode_fp8", "indexer_decode_mxfp4") if k in stages)
-    # the dominant single kernel: rows longer than 32768 keys run the top-k as three launches
-    # (a latency stage, not one kernel), so it is a candidate only as one launch
-    cands = ("sparse_mqa", idx_stage) + (("topk",) if cfg.max_groups <= 32768 else ())
+    # the dominant single kernel among the step's launches: with the top-k inside the
+    # attention launch that launch (it also reads the scores and writes the list); else the
+    # attention and the top-k launch -- rows longer than 32768 keys run the top-k as three
+    # launches (a latency stage, not one kernel), so it is a candidate only as one launch
+    if "sparse_mqa_select" in stages:
+        cands = ("sparse_mqa_select", idx_stage)
+    else:
+        cands = ("sparse_mqa", idx_stage) + (("topk",) if cfg.max_groups <= 32768 else ())
     dominant = max(cands, key=lambda k: stages[k])
-    if dominant == "sparse_mqa":
+    if dominant == "sparse_mqa_select":
+        roof = roofline(None, attn_flops, attn_bytes + rows * (cfg.max_groups + cfg.topk) * 4, stages[dominant])
+    elif dominant == "sparse_mqa":
         roof = roofline(None, attn_flops, attn_bytes, stages[dominant])
     elif dominant == idx_stage:
         roof = roofline("hbm", idx_flops, idx_bytes, stages[dominant])
@@ -552,6 +574,7 @@ def run_decode(torch, dev, args):
                    "split_merge": "merge kernel" if "sparse_mqa_combine" in stages else "inside the attention launch",
                    "emission": ("inside the indexer launch" if layer._merged_emit else "launch of its own")
                    if fused else None,
+                   "topk": "inside the attention launch" if layer.selects_in_attention else "launch of its own",
                    "step": "per attention layer, inside a graph replay of graph_layers layers",
                    "prologue": ("fused: in-step group emission (carry ring, pooling + norm, cache entry and "
                                 "index key every 4th token; RoPE tables from the position table), kv RMSNorm + "

@@ -505,6 +505,29 @@ int mzk_sparse_mqa_advance(const void* q, int64_t B, int64_t S, int H, int D, in
                            float* workspace, int64_t workspace_bytes, void* out, float* lse, const void* rope_cos,
                            const void* rope_sin, int rope_dim, void* stream);
 
+/* One decode step's selection and attention in one launch (S = 1): the top-topk of the
+ * indexer scores [B, score_stride] fp32 over G keys (owlet1/indexer.py:158-165 as
+ * mzk_topk_rows: -inf never taken, lower index first among equal scores, ascending, then
+ * -1) becomes the sparse list of mzk_sparse_mqa_rope over main_kv -- every attention
+ * workgroup of a row selects the row's list itself, so the step has no top-k launch -- and
+ * the list is also written to idx_out [B, idx_out_stride] int32.  With advance != 0 the
+ * positions then advance as in mzk_sparse_mqa_advance.  In one launch for the FP8 latent
+ * rows (fmt 1, D 576, nope 512) with G <= 8192 and topk <= 2048, both multiples of 4,
+ * score_stride and idx_out_stride multiples of 4, scores / idx_out 16-byte aligned, and
+ * splits of at most 1024 - 96 entries ((window + dense_cap + topk) / nsplit, the decode
+ * kernel's entry tables); otherwise mzk_topk_rows and then the attention, same results.
+ * out and lse NULL (nsplit > 1, advance 0): the split partials only, as mzk_sparse_mqa.  Other arguments
+ * as mzk_sparse_mqa_rope (rope_cos / rope_sin may be NULL).  No counterpart in the
+ * reference as one call: it is the reference's index_scores.topk followed by its sparse
+ * attention (owlet1/attention.py:217-229). */
+int mzk_sparse_mqa_select(const void* q, int64_t B, int H, int D, int fmt, int nope, int64_t* positions,
+                          int advance, const void* win, int64_t win_batch_entries, int win_cap, int window,
+                          const void* dense, int64_t dense_batch_entries, int dense_cap, int dense_ratio,
+                          const void* main_kv, int64_t main_batch_entries, int64_t G, const float* scores,
+                          int64_t score_stride, int topk, int32_t* idx_out, int64_t idx_out_stride,
+                          const float* sinks, int nsplit, float* workspace, int64_t workspace_bytes, void* out,
+                          float* lse, const void* rope_cos, const void* rope_sin, int rope_dim, void* stream);
+
 /* The split partials of part of a row's entry list, for launches that share one workspace:
  * splits split_base .. split_base + nsplit - 1 of a workspace holding split_total splits
  * per row (rows*split_total*H*(2*D+8) bytes, laid out as for mzk_sparse_mqa), over the

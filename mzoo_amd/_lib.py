@@ -72,6 +72,8 @@ _SIGS = {
                             _P, _I64, _I64, _P, _I64, _I32, _P, _I32, _P, _I64, _P, _P, _P, _P, _I32, _P],
     "mzk_sparse_mqa_advance": [_P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _I64, _I32, _I32, _P, _I64, _I32,
                                _I32, _P, _I64, _I64, _P, _I64, _I32, _P, _I32, _P, _I64, _P, _P, _P, _P, _I32, _P],
+    "mzk_sparse_mqa_select": [_P, _I64, _I32, _I32, _I32, _I32, _P, _I32, _P, _I64, _I32, _I32, _P, _I64, _I32, _I32,
+                              _P, _I64, _I64, _P, _I64, _I32, _P, _I64, _P, _I32, _P, _I64, _P, _P, _P, _P, _I32, _P],
     "mzk_sparse_mqa_part": [_P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _I64, _I32, _I32, _P, _I64, _I32, _I32,
                             _P, _I64, _I64, _P, _I64, _I32, _I32, _I32, _I32, _P, _I64, _P, _P, _I32, _P],
     "mzk_sparse_mqa_combine_rope": [_P, _I64, _I64, _I32, _I32, _I32, _P, _P, _P, _I32, _P, _P, _P],

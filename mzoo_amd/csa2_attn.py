@@ -61,6 +61,55 @@ def merge_status(workspace: torch.Tensor, rows: int, heads: int, dim: int, nspli
     return int(w[0]), int(w[1])
 
 
+def sparse_mqa_decode_select(q: torch.Tensor, positions: torch.Tensor, win_cache: torch.Tensor, window: int, *,
+                             main_cache: torch.Tensor, scores: torch.Tensor, topk: int,
+                             idx_out: torch.Tensor | None = None, dense_cache: torch.Tensor | None = None,
+                             dense_ratio: int = 1, sinks: torch.Tensor | None = None, nsplit: int = 1,
+                             nope: int = 512, workspace: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                             lse: torch.Tensor | None = None, rope: tuple | None = None, advance: bool = False):
+    """``sparse_mqa_decode`` over the top-``topk`` of the indexer ``scores`` (fp32 [B, G], the
+    keys of ``main_cache``'s first G entries) -- the reference's ``index_scores.topk``
+    (``owlet1/indexer.py:158-165``, lowest index first among equal scores) feeding its
+    sparse attention -- with the selection inside the attention launch where it fits
+    (``mzk_sparse_mqa_select``).  Returns (o, lse, idx int32 [B, topk]: the list the attention
+    read, ascending picks then -1)."""
+    b, h, d = q.shape
+    _lib.require_gpu(q, positions, win_cache, main_cache, scores)
+    if scores.dtype != torch.float32 or scores.dim() != 2 or scores.shape[0] != b or scores.stride(1) != 1:
+        raise ValueError(f"sparse_mqa_decode_select: scores must be fp32 [{b}, G] with unit column stride")
+    for name, t, dt, shape in (("q", q, torch.bfloat16, (b, h, d)), ("positions", positions, torch.int64, (b,)),
+                               ("win_cache", win_cache, torch.uint8, None), ("main_cache", main_cache, torch.uint8, None),
+                               ("dense_cache", dense_cache, torch.uint8, None), ("sinks", sinks, torch.float32, (h,)),
+                               ("out", out, torch.bfloat16, (b, h, d)), ("lse", lse, torch.float32, (b, h)),
+                               ("idx_out", idx_out, torch.int32, (b, topk))):
+        if t is None:
+            continue
+        if t.dtype != dt or not t.is_contiguous() or (shape is not None and tuple(t.shape) != shape):
+            raise ValueError(f"sparse_mqa_decode_select: {name} must be a contiguous {dt} tensor"
+                             + (f" of shape {list(shape)}" if shape is not None else ""))
+    rc = rs = None
+    if rope is not None:
+        rc, rs = (t.contiguous() for t in rope)
+        if rc.dtype != torch.bfloat16 or rs.dtype != torch.bfloat16 or rc.shape != (b, (d - nope) // 2) \
+                or rs.shape != rc.shape:
+            raise ValueError(f"sparse_mqa_decode_select: rope cos/sin must be bf16 [B, {(d - nope) // 2}]")
+    out = torch.empty_like(q) if out is None else out
+    lse = torch.empty(b, h, dtype=torch.float32, device=q.device) if lse is None else lse
+    idx_out = torch.empty(b, topk, dtype=torch.int32, device=q.device) if idx_out is None else idx_out
+    need = workspace_bytes(b, h, d, nsplit)
+    if nsplit > 1 and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = new_workspace(b, h, d, nsplit, q.device)
+    g = scores.shape[1]
+    _lib.call("mzk_sparse_mqa_select", q.data_ptr(), b, h, d, FMT_FP8, nope, positions.data_ptr(), int(advance),
+              win_cache.data_ptr(), win_cache.shape[1], win_cache.shape[1], window,
+              _lib.ptr(dense_cache), 0 if dense_cache is None else dense_cache.shape[1],
+              0 if dense_cache is None else dense_cache.shape[1], dense_ratio, main_cache.data_ptr(),
+              main_cache.shape[1], g, scores.data_ptr(), scores.stride(0), topk, idx_out.data_ptr(), topk,
+              _lib.ptr(sinks), nsplit, _lib.ptr(workspace), need, out.data_ptr(), lse.data_ptr(), _lib.ptr(rc),
+              _lib.ptr(rs), 0 if rope is None else d - nope, _lib.stream_of(q))
+    return out, lse, idx_out
+
+
 def fwd(q: torch.Tensor, kv: torch.Tensor, main_kv: torch.Tensor, indices: torch.Tensor, *, window: int,
         compress_ratio: int, causal: bool = True, sinks: torch.Tensor | None = None):
     """Sliding-window + top-k gathered compressed shared-latent MQA forward."""

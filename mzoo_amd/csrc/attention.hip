@@ -34,6 +34,7 @@
 #include <mutex>
 
 #include "common.h"
+#include "topk_core.h"
 
 namespace mzk {
 namespace {
@@ -101,6 +102,14 @@ struct AttnParams {
   uint32_t* merge_rec;
   uint32_t* merge_err;
   int merge_fence;  // every workgroup takes the release / acquire path (a test mode)
+  // The sparse list selected in the launch (decode, the SEL kernel instance; idx unused):
+  // the top-topk of the row's sel_scores [rows, sel_stride] fp32 over G keys, in the top-k
+  // launch's form (ascending picks, then -1), which the row's first workgroup also writes to
+  // sel_out [rows, sel_out_stride] int32.
+  const float* sel_scores;
+  int64_t sel_stride;
+  int32_t* sel_out;
+  int64_t sel_out_stride;
 };
 
 template <int FMT, int D, int NOPE>
@@ -978,7 +987,11 @@ struct SplitSmem {
 // (its longest possible split does), so the ring of tables and its index reads (which may
 // go to global memory, and whose waits would then also drain the tile loads in flight) are
 // compiled out.
-template <int FMT, int D, int NOPE, bool ALLTAB>
+// SEL (with ALLTAB): the workgroup selects its row's sparse list itself from the indexer
+// scores (topk_core.h's row selection, 16 scores per thread: G <= 8192, topk <= 2048, both
+// multiples of 4), in the LDS the tiles take later -- every workgroup of the row computes
+// the same list, so no workgroup waits for another and the top-k launch goes away.
+template <int FMT, int D, int NOPE, bool ALLTAB, bool SEL = false>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 sparse_mqa_dsplit_kernel(const AttnParams p) {
   using M = SplitSmem<FMT, D, NOPE>;
@@ -1020,10 +1033,27 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
   rp.tab_ptr = tab_ptr;
   rp.tab_mask = tab_mask;
   rp.template locate<ALLTAB>(p, HG * 32);
-  // The row's index list, its position and this lane's query fragment are requested
-  // together: one memory round trip at the start instead of three dependent ones.
+  // The row's index list (SEL: its scores), its position and this lane's query fragment are
+  // requested together: one memory round trip at the start instead of three dependent ones.
   v4i pre;
-  const bool pre_ok = rp.prefetch_indices(p, tid, pre);
+  bool pre_ok;
+  constexpr int SKPT = 16;  // SEL: scores per thread
+  static_assert(!SEL || (ALLTAB && SKPT * NT == 8192), "the selecting instance: decode, 8192 scores per row");
+  float4 sc4[SEL ? SKPT / 4 : 1];
+  if constexpr (SEL) {
+    // branch-free: G is a multiple of 4, so a thread's last aligned float4 at or past the
+    // row's end is re-read from G - 4 (and its keys are padding below)
+    const float* srow = p.sel_scores + rp.row * p.sel_stride;
+    const int G4 = static_cast<int>(p.G) - 4;
+#pragma unroll
+    for (int m = 0; m < SKPT / 4; ++m) {
+      const int o = SKPT * tid + 4 * m;
+      sc4[m] = *reinterpret_cast<const float4*>(srow + (o <= G4 ? o : G4));
+    }
+    pre_ok = true;
+  } else {
+    pre_ok = rp.prefetch_indices(p, tid, pre);
+  }
   const int64_t row_pos = p.positions[rp.row];
 
   const int hl = hg * 32 + (lane & 31);  // head within the workgroup
@@ -1077,9 +1107,59 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
     }
   }
   __shared__ int wred[2 * 8];
-  rp.plan(p, row_pos, pre_ok ? rp.valid_prefix(p, tid, pre, wred) : -1);
-  if (pre_ok) rp.stage_prefetched(sidx, kSplitIdxCap, tid, pre);
-  else rp.stage_indices(p, sidx, kSplitIdxCap, tid);
+  if constexpr (SEL) {
+    // the row's selection in the tile region of LDS (first written by the tile loop, after
+    // the barriers below): three histograms and the scan scratch
+    int* const h1 = reinterpret_cast<int*>(smem);
+    int* const h2 = h1 + kBins * kSub1;
+    int* const h3 = h2 + kBins;
+    int* const sw = h3 + kBins / 2;
+    static_assert((kBins * kSub1 + kBins + kBins / 2 + 16) * 4 <= M::NKT * M::KT, "selection LDS");
+    const RowSelLds lds{h1, h2, h3, sw, sw + 8, sw + 12};
+    const int G = static_cast<int>(p.G), k = p.topk;
+    const bool search = G > k;
+    if (search) {
+      row_sel_clear<NT>(lds, tid);
+      __syncthreads();
+    }
+    const int i0 = SKPT * tid;
+    uint32_t key[SKPT];
+#pragma unroll
+    for (int m = 0; m < SKPT / 4; ++m) {
+      const float v[4] = {sc4[m].x, sc4[m].y, sc4[m].z, sc4[m].w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) key[4 * m + c] = order_key(v[c]) & key_mask(i0 + 4 * m + c, G);
+    }
+
+    uint32_t T;
+    int need_eq;
+    row_sel_threshold<SKPT, NT>(key, search, k, lds, T, need_eq);
+    const RowTake tk = row_sel_take<SKPT, NT>(key, T, need_eq, sw);
+    // the list is in the top-k launch's form (ascending picks, then -1) by construction, so
+    // the split is planned over its `written` valid entries directly, and every thread puts
+    // its picks of this split's slice straight into the staged indices (a slice holds at most
+    // kAllTabCap - 96 < kSplitIdxCap entries); the row's first workgroup also writes the list
+    rp.plan(p, row_pos, tk.written);
+    const int sp_end = rp.v_end > rp.nwd ? rp.v_end - rp.nwd : 0;
+    const bool first = p.sel_out != nullptr && rp.split == 0 && rp.hgrp == 0;
+    int32_t* const orow = first ? p.sel_out + rp.row * p.sel_out_stride : nullptr;
+    uint32_t sel = tk.sel;
+    for (int at = tk.pos; sel != 0u; ++at) {
+      const int g = i0 + __builtin_ctz(sel);
+      if (at >= rp.sp_begin && at < sp_end) sidx[at - rp.sp_begin] = g;
+      if (first && at < k) orow[at] = g;
+      sel &= sel - 1u;
+    }
+    if (first)
+      for (int i = tk.written + tid; i < k; i += NT) orow[i] = -1;
+    rp.sidx = (const __attribute__((address_space(3))) int32_t*)(sidx);
+    rp.sidx_cap = kSplitIdxCap;
+    rp.idx_row = nullptr;  // never read: the slice fits the staged indices
+  } else {
+    rp.plan(p, row_pos, pre_ok ? rp.valid_prefix(p, tid, pre, wred) : -1);
+    if (pre_ok) rp.stage_prefetched(sidx, kSplitIdxCap, tid, pre);
+    else rp.stage_indices(p, sidx, kSplitIdxCap, tid);
+  }
   __syncthreads();
   // Splits of at most kAllTabCap entries (every decode configuration) get all their entry
   // tables here, so the tile loop builds none (a table build costs the building wave an
@@ -1492,6 +1572,16 @@ int launch_kernel(K kern, size_t dyn_lds, int threads, int heads_per_wg, const A
   return MZK_OK;
 }
 
+// Whether the longest split any workgroup of a D-split launch can plan (RowPlan::plan with
+// every source full) keeps all its entry tables (RowPlan::table_tiles): the decode kernel
+// instances (ALLTAB), which the in-launch merge and the in-launch selection need.
+bool dsplit_all_tables(int window, const void* dense, int dense_cap, const void* main_kv, int topk, int nsplit) {
+  const int64_t total_max = static_cast<int64_t>(window) + (dense ? dense_cap : 0) + (main_kv ? topk : 0);
+  const int64_t chunk_max = ((total_max + nsplit - 1) / nsplit + kTile - 1) / kTile * kTile;
+  const int64_t tables_max = chunk_max / kTile + 3 > 4 ? chunk_max / kTile + 3 : 4;
+  return tables_max * kTile <= kAllTabCap;
+}
+
 // `merged` is set when the launch merges its splits itself (p.merge_rec given and the
 // launch takes the kernel instance that carries the merge).
 template <int FMT, int D, int NOPE>
@@ -1508,6 +1598,7 @@ int dispatch_heads(const AttnParams& p_in, int64_t rows, hipStream_t s, bool* me
     static_assert(M::LDS + 8 * kAllTabCap + 4 * (kAllTabCap / kTile) + 128 <= 160 * 1024, "LDS budget");
     auto kern_all = sparse_mqa_dsplit_kernel<FMT, D, NOPE, true>;
     auto kern_ring = sparse_mqa_dsplit_kernel<FMT, D, NOPE, false>;
+    auto kern_sel = sparse_mqa_dsplit_kernel<FMT, D, NOPE, true, true>;
     // the dynamic-LDS limit is a per-device function attribute: set once per device
     static std::atomic<bool> attr_set[kMaxDevices] = {};  // setting it twice is harmless
     int dev = 0;
@@ -1516,7 +1607,8 @@ int dispatch_heads(const AttnParams& p_in, int64_t rows, hipStream_t s, bool* me
       return MZK_ELAUNCH;
     }
     if (!attr_set[dev].load(std::memory_order_acquire)) {
-      for (const void* k : {reinterpret_cast<const void*>(kern_all), reinterpret_cast<const void*>(kern_ring)}) {
+      for (const void* k : {reinterpret_cast<const void*>(kern_all), reinterpret_cast<const void*>(kern_ring),
+                            reinterpret_cast<const void*>(kern_sel)}) {
         if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, M::LDS) != hipSuccess) {
           set_last_error("sparse_mqa: cannot raise the kernel's LDS limit to %d bytes", M::LDS);
           return MZK_ELAUNCH;
@@ -1524,13 +1616,16 @@ int dispatch_heads(const AttnParams& p_in, int64_t rows, hipStream_t s, bool* me
       }
       attr_set[dev].store(true, std::memory_order_release);
     }
-    // the longest split any workgroup can plan (RowPlan::plan with every source full) and
-    // the entry tables it needs (RowPlan::table_tiles)
-    const int64_t total_max = static_cast<int64_t>(p.window) + (p.dense ? p.dense_cap : 0) + (p.main ? p.topk : 0);
-    const int64_t chunk_max = ((total_max + p.nsplit - 1) / p.nsplit + kTile - 1) / kTile * kTile;
-    const int64_t tables_max = chunk_max / kTile + 3 > 4 ? chunk_max / kTile + 3 : 4;
-    const bool all_tables = tables_max * kTile <= kAllTabCap;
+    const bool all_tables = dsplit_all_tables(p.window, p.dense, p.dense_cap, p.main, p.topk, p.nsplit);
     if (!all_tables) p.merge_rec = nullptr;  // only the decode instance carries the in-launch merge
+    if (p.sel_scores != nullptr) {  // the host checked the selecting instance's limits
+      if (!all_tables) {
+        set_last_error("sparse_mqa_select: the splits exceed the decode kernel's entry tables");
+        return MZK_EUNSUPPORTED;
+      }
+      *merged = p.merge_rec != nullptr;
+      return launch_kernel(kern_sel, M::LDS, 512, 64, p, rows, s);
+    }
     *merged = p.merge_rec != nullptr;
     return launch_kernel(all_tables ? kern_all : kern_ring, M::LDS, 512, 64, p, rows, s);
   } else {
@@ -1627,7 +1722,8 @@ int sparse_mqa_impl(const void* q, int64_t B, int64_t S, int H, int D, int fmt, 
                     int64_t main_batch_entries, int64_t G, const int32_t* idx, int64_t idx_row_stride, int topk,
                     const float* sinks, int nsplit, float* workspace, int64_t workspace_bytes, void* out, float* lse,
                     const void* rope_cos, const void* rope_sin, int rope_dim, int split_base, int split_total,
-                    void* stream, int64_t* advance = nullptr) {
+                    void* stream, int64_t* advance = nullptr, const float* sel_scores = nullptr,
+                    int64_t sel_stride = 0, int32_t* sel_out = nullptr, int64_t sel_out_stride = 0) {
   const bool part_only = split_total >= 1;
   MZK_CHECK_ARG(B >= 0 && S >= 0 && H >= 1 && D > 0, "sparse_mqa: bad sizes");
   if (rope_cos || rope_sin) {
@@ -1654,7 +1750,8 @@ int sparse_mqa_impl(const void* q, int64_t B, int64_t S, int H, int D, int fmt, 
   }
   MZK_CHECK_ARG(win_cap == 0 || win_cap >= window, "sparse_mqa: ring capacity smaller than the window");
   MZK_CHECK_ARG(!dense || (dense_ratio >= 1 && dense_cap >= 0), "sparse_mqa: dense source needs ratio >= 1");
-  MZK_CHECK_ARG(!main_kv || (idx && topk >= 0 && G >= 0 && idx_row_stride >= topk && main_batch_entries >= G),
+  MZK_CHECK_ARG(!main_kv || ((idx || sel_scores) && topk >= 0 && G >= 0 && idx_row_stride >= topk &&
+                              main_batch_entries >= G),
                 "sparse_mqa: sparse source needs idx [rows, >= topk] and main_batch_entries >= G");
   const int64_t rows = B * S;
   if (rows == 0) return MZK_OK;
@@ -1712,6 +1809,11 @@ int sparse_mqa_impl(const void* q, int64_t B, int64_t S, int H, int D, int fmt, 
   }
   p.rope_cos = static_cast<const uint16_t*>(rope_cos);
   p.rope_sin = static_cast<const uint16_t*>(rope_sin);
+  p.sel_scores = sel_scores;
+  p.sel_stride = sel_stride;
+  p.sel_out = sel_out;
+  p.sel_out_stride = sel_out_stride;
+  if (sel_scores) p.idx = nullptr;
   // The split merge inside the attention launch: a full call of the D-split kernel with
   // nsplit dividing 64, rows or rows * (64-head groups) a multiple of 8 (the mappings that put
   // a group's splits on one XCD), a workspace that holds the merge records, and a grid of at
@@ -1818,6 +1920,43 @@ extern "C" int mzk_sparse_mqa_advance(const void* q, int64_t B, int64_t S, int H
                          dense_batch_entries, dense_cap, dense_ratio, main_kv, main_batch_entries, G, idx,
                          idx_row_stride, topk, sinks, nsplit, workspace, workspace_bytes, out, lse, rope_cos, rope_sin,
                          rope_dim, 0, -1, stream, positions);
+}
+
+extern "C" int mzk_sparse_mqa_select(const void* q, int64_t B, int H, int D, int fmt, int nope, int64_t* positions,
+                                     int advance, const void* win, int64_t win_batch_entries, int win_cap, int window,
+                                     const void* dense, int64_t dense_batch_entries, int dense_cap, int dense_ratio,
+                                     const void* main_kv, int64_t main_batch_entries, int64_t G, const float* scores,
+                                     int64_t score_stride, int topk, int32_t* idx_out, int64_t idx_out_stride,
+                                     const float* sinks, int nsplit, float* workspace, int64_t workspace_bytes,
+                                     void* out, float* lse, const void* rope_cos, const void* rope_sin, int rope_dim,
+                                     void* stream) {
+  MZK_CHECK_ARG(B >= 0 && G >= 0 && topk >= 0, "sparse_mqa_select: negative size");
+  MZK_CHECK_ARG(idx_out != nullptr && scores != nullptr && main_kv != nullptr,
+                "sparse_mqa_select: needs scores, the main cache and idx_out");
+  MZK_CHECK_ARG((out != nullptr && lse != nullptr) || (out == nullptr && lse == nullptr && nsplit > 1 && !advance),
+                "sparse_mqa_select: out and lse, or neither (split partials only: nsplit > 1, no advance)");
+  MZK_CHECK_ARG(score_stride >= G && idx_out_stride >= topk, "sparse_mqa_select: strides smaller than the row");
+  if (B == 0) return MZK_OK;
+  // the selecting kernel instance: the FP8 latent decode kernel, 16 scores per thread of its
+  // 512, whole float4 / int4 groups
+  const bool in_launch = fmt == 1 && D == 576 && nope == 512 && G >= 4 && G <= 8192 && G % 4 == 0 &&
+                         score_stride % 4 == 0 && aligned16(scores) && topk >= 4 && topk <= 2048 && topk % 4 == 0 &&
+                         idx_out_stride % 4 == 0 && aligned16(idx_out) && nsplit >= 1 && nsplit <= 65535 &&
+                         window >= 0 && dense_cap >= 0 &&
+                         dsplit_all_tables(window, dense, dense_cap, main_kv, topk, nsplit);
+  int64_t* adv = advance ? positions : nullptr;
+  if (!in_launch) {  // the top-k launch, then the attention over its list
+    int rc = mzk_topk_rows(scores, B, G, score_stride, topk, idx_out, idx_out_stride, stream);
+    if (rc) return rc;
+    return sparse_mqa_impl(q, B, 1, H, D, fmt, nope, positions, win, win_batch_entries, win_cap, window, dense,
+                           dense_batch_entries, dense_cap, dense_ratio, main_kv, main_batch_entries, G, idx_out,
+                           idx_out_stride, topk, sinks, nsplit, workspace, workspace_bytes, out, lse, rope_cos,
+                           rope_sin, rope_dim, 0, -1, stream, adv);
+  }
+  return sparse_mqa_impl(q, B, 1, H, D, fmt, nope, positions, win, win_batch_entries, win_cap, window, dense,
+                         dense_batch_entries, dense_cap, dense_ratio, main_kv, main_batch_entries, G, nullptr, topk,
+                         topk, sinks, nsplit, workspace, workspace_bytes, out, lse, rope_cos, rope_sin, rope_dim, 0, -1,
+                         stream, adv, scores, score_stride, idx_out, idx_out_stride);
 }
 
 extern "C" int mzk_sparse_mqa_part(const void* q, int64_t B, int64_t S, int H, int D, int fmt, int nope,

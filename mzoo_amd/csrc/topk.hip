@@ -20,7 +20,7 @@
 // row); longer rows without a workspace stream the row through 8-bit digit passes
 // (topk_rows_kernel).  mzk_topk_rows_ws splits rows of 32769 .. 64 x 8192 keys over chunk
 // workgroups (three launches, see below).
-#include "common.h"
+#include "topk_core.h"
 
 namespace mzk {
 namespace {
@@ -28,12 +28,6 @@ namespace {
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
 constexpr int kLdsKeys = 16384;            // 64 KiB of keys
-constexpr uint32_t kNegInfKey = 0x007fffffu;
-
-__device__ __forceinline__ uint32_t order_key(float f) {
-  const uint32_t u = __float_as_uint(f);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
 
 __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
 #pragma unroll
@@ -197,92 +191,11 @@ __global__ void __launch_bounds__(kThreads) topk_rows_kernel(const float* __rest
 
 // ---- rows of G <= KPT * kThreads, keys held in registers -----------------------------
 
-// Inclusive prefix sum over the 64 lanes with DPP: Kogge-Stone inside each row of 16
-// lanes (row_shr 1, 2, 4, 8), then row_bcast:15 adds row r's total to row r+1 (rows 1, 3)
-// and row_bcast:31 adds the total of rows 0-1 to rows 2-3.  Lanes a DPP source does not
-// reach, and rows the row mask leaves out, add 0.
-__device__ __forceinline__ int wave_incl_scan_dpp(int v) {
-  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);  // row_shr:1
-  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);  // row_shr:2
-  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);  // row_shr:4
-  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);  // row_shr:8
-  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false); // row_bcast:15
-  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false); // row_bcast:31
-  return v;
-}
 
 // ---- rows of G <= KPT * NT, one workgroup per row, keys held in registers -------------
 //
-// Three levels of bins, each a histogram in LDS over the keys still open: the top 11 bits of
-// the key (sign, exponent and two mantissa bits of the score: four bins per octave; finite
-// keys lie in bins >= 4, -inf is key 0x007fffff in bin 3, the padding key 0 in bin 0), then
-// bits 20..10 and bits 9..0 of the keys in the bin holding the k-th largest.  A level stops
-// the search when that bin is taken whole (its keys are all among the k largest), which for
-// distinct scores happens after the first or the second.  The three histograms are cleared
-// up front, so a level costs one barrier for its histogram and two for its bin search:
-// workgroup barriers, not arithmetic, are what a level costs here.  Compaction: the output
-// slot of an entry is (#key > T before it) + min(#key == T before it, need_eq), from one
-// scan of the packed pair (n_gt << 16 | n_eq).
-constexpr int kBinBits = 11;
-constexpr int kBins = 1 << kBinBits;           // 2048 first-level bins
-constexpr int kLowBits = 32 - kBinBits;        // 21 bits below a first-level bin
-constexpr int kSub1 = 4;                       // first-level sub-counters per bin (lane % kSub1)
-static_assert(kSub1 % 4 == 0, "a bin's sub-counters are read as whole int4s");
-
-// Inclusive scan over the NT threads of one int each (one barrier); `total` is the sum.
-// wsum [NT/64] may be written again after the caller's next barrier.
-template <int NT>
-__device__ __forceinline__ int block_incl_scan(int v, int* wsum, int& total) {
-  constexpr int NW = NT / 64;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int incl = wave_incl_scan_dpp(v);
-  if (lane == 63) wsum[wave] = incl;
-  __syncthreads();
-  int before = 0, tot = 0;
-#pragma unroll
-  for (int w = 0; w < NW; ++w) {
-    const int x = wsum[w];
-    before += w < wave ? x : 0;
-    tot += x;
-  }
-  total = tot;
-  return incl + before;
-}
-
-// The bin holding the rem-th largest entry of an NB-bin histogram: thread t holds the counts
-// c[j] of bins NB-1-(BPT*t+j) (descending), so the block scan counts the entries above each
-// thread's bins.  Every thread returns the same (bin = rem = count = 0 when rem exceeds the
-// total).  Two barriers; sh [3] may be written again after the caller's next barrier.
-struct BinHit {
-  int bin, rem, count, total;  // the bin, the rank left inside it, its count, the histogram total
-};
-template <int NT, int NB>
-__device__ __forceinline__ BinHit find_bin(const int (&c)[NB / NT], int rem, int* wsum, int* sh) {
-  constexpr int BPT = NB / NT;
-  const int tid = threadIdx.x;
-  if (tid == 0) {
-    sh[0] = 0;
-    sh[1] = 0;
-    sh[2] = 0;
-  }
-  int s = 0;
-#pragma unroll
-  for (int j = 0; j < BPT; ++j) s += c[j];
-  int total;
-  const int incl = block_incl_scan<NT>(s, wsum, total);
-  int above = incl - s;
-#pragma unroll
-  for (int j = 0; j < BPT; ++j) {
-    if (above < rem && rem <= above + c[j]) {  // exactly one (thread, j) when rem <= total
-      sh[0] = NB - 1 - (BPT * tid + j);
-      sh[1] = rem - above;
-      sh[2] = c[j];
-    }
-    above += c[j];
-  }
-  __syncthreads();
-  return BinHit{sh[0], sh[1], sh[2], total};
-}
+// The row selection of topk_core.h (three levels of bins, then the compaction in index
+// order) over the row's scores, KPT keys per thread.
 
 // MAP: the row is a candidate axis of blocks of kMapBs slots (slot j = key
 // cand[row][j / kMapBs] * kMapBs + j % kMapBs, the level-two scores); the index list is
@@ -300,18 +213,17 @@ __global__ void __launch_bounds__(NT) topk_row_kernel(const float* __restrict__ 
                                                       int k, int32_t* __restrict__ out, int64_t out_stride,
                                                       SlotMap sm = SlotMap{}) {
   constexpr int NW = NT / 64;
-  static_assert(KPT * NT <= 32768, "packed counts: at most 2^15 keys per row");
   __shared__ __align__(16) int hist1[kBins * kSub1];
-  __shared__ __align__(16) int hist2[kBins];       // bits 20..10 of the keys in the first level's bin
-  __shared__ __align__(16) int hist3[kBins / 2];   // bits 9..0 of the keys in the second level's bin
+  __shared__ __align__(16) int hist2[kBins];
+  __shared__ __align__(16) int hist3[kBins / 2];
   __shared__ int wsum[NW];
-  __shared__ int sh[2][3];  // bin searches alternate between the two
+  __shared__ int sh[2][3];
+  const RowSelLds lds{hist1, hist2, hist3, wsum, sh[0], sh[1]};
 
   const int64_t row = blockIdx.x;
   const float* src = scores + row * row_stride;
   int32_t* dst = out + row * out_stride;
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
   const int i0 = tid * KPT;
 
   float x[KPT];
@@ -338,99 +250,20 @@ __global__ void __launch_bounds__(NT) topk_row_kernel(const float* __restrict__ 
   // G <= k (workgroup-uniform): every finite key is taken, no search
   const bool search = G > k;
   if (search) {
-    int4* h4 = reinterpret_cast<int4*>(hist1);
-    for (int i = tid; i < kBins * kSub1 / 4; i += NT) h4[i] = int4{0, 0, 0, 0};
-    for (int i = tid; i < kBins / 4; i += NT) reinterpret_cast<int4*>(hist2)[i] = int4{0, 0, 0, 0};
-    for (int i = tid; i < kBins / 8; i += NT) reinterpret_cast<int4*>(hist3)[i] = int4{0, 0, 0, 0};
+    row_sel_clear<NT>(lds, tid);
     __syncthreads();  // histograms cleared (while the scores are in flight)
   }
-
   uint32_t key[KPT];
 #pragma unroll
-  for (int j = 0; j < KPT; ++j) key[j] = (i0 + j < G) ? order_key(x[j]) : 0u;  // 0 sorts below -inf: never taken
-  BinHit h1{0, 0, 0, 0};
-  if (search) {
-    int* hl = hist1 + (lane & (kSub1 - 1));
-#pragma unroll
-    for (int j = 0; j < KPT; ++j)
-      if (key[j] > kNegInfKey) atomicAdd(hl + (key[j] >> kLowBits) * kSub1, 1);
-    __syncthreads();
-    int c1[kBins / NT];
-#pragma unroll
-    for (int j = 0; j < kBins / NT; ++j) {
-      const int4* hb = reinterpret_cast<const int4*>(hist1) + (kBins - 1 - ((kBins / NT) * tid + j)) * (kSub1 / 4);
-      int s = 0;
-#pragma unroll
-      for (int q = 0; q < kSub1 / 4; ++q) {
-        const int4 v = hb[q];
-        s += (v.x + v.y) + (v.z + v.w);
-      }
-      c1[j] = s;
-    }
-    h1 = find_bin<NT, kBins>(c1, k, wsum, sh[0]);
-  }
-
-  uint32_t T = kNegInfKey;  // at most k finite keys: take them all
-  int need_eq = 0;
-  if (search && h1.total > k) {
-    const uint32_t b1 = static_cast<uint32_t>(h1.bin);  // >= 4
-    if (h1.count == h1.rem) {
-      T = (b1 << kLowBits) - 1u;
-    } else {
-#pragma unroll
-      for (int j = 0; j < KPT; ++j)
-        if ((key[j] >> kLowBits) == b1) atomicAdd(&hist2[(key[j] >> 10) & (kBins - 1)], 1);
-      __syncthreads();
-      int c2[kBins / NT];
-#pragma unroll
-      for (int j = 0; j < kBins / NT; ++j) c2[j] = hist2[kBins - 1 - ((kBins / NT) * tid + j)];
-      const BinHit h2 = find_bin<NT, kBins>(c2, h1.rem, wsum, sh[1]);
-      const uint32_t p2 = (b1 << kLowBits) | (static_cast<uint32_t>(h2.bin) << 10);
-      if (h2.count == h2.rem) {
-        T = p2 - 1u;
-      } else {
-#pragma unroll
-        for (int j = 0; j < KPT; ++j)
-          if ((key[j] >> 10) == (p2 >> 10)) atomicAdd(&hist3[key[j] & 1023u], 1);
-        __syncthreads();
-        constexpr int B3 = kBins / 2;
-        int c3[B3 / NT];
-#pragma unroll
-        for (int j = 0; j < B3 / NT; ++j) c3[j] = hist3[B3 - 1 - ((B3 / NT) * tid + j)];
-        const BinHit h3 = find_bin<NT, B3>(c3, h2.rem, wsum, sh[0]);
-        T = p2 | static_cast<uint32_t>(h3.bin);  // the k-th largest key itself
-        need_eq = h3.rem;
-      }
-    }
-  }
-
-  // compaction in index order: a key is taken when it lies above T, or equals T with fewer
-  // than need_eq keys equal to T before it; its output slot is the number of taken keys
-  // before it
-  static_assert(KPT <= 32, "one bit per key of a thread");
-  uint32_t gt_mask = 0u, eq_mask = 0u;
-#pragma unroll
-  for (int j = 0; j < KPT; ++j) {
-    gt_mask |= static_cast<uint32_t>(key[j] > T) << j;
-    eq_mask |= static_cast<uint32_t>((key[j] == T) && (T != kNegInfKey)) << j;
-  }
-  const int n_gt = __builtin_popcount(gt_mask), n_eq = __builtin_popcount(eq_mask);
-  // packed as unsigned: n_gt <= G <= 32768 fills bit 31 at most, n_eq stays below 2^16
-  const int packed = (n_gt << 16) | n_eq;
-  int tot_p;
-  const int incl = block_incl_scan<NT>(packed, wsum, tot_p);
-  const uint32_t before = static_cast<uint32_t>(incl - packed), tot = static_cast<uint32_t>(tot_p);
-  const int gt_before = static_cast<int>(before >> 16), eq_before = static_cast<int>(before & 0xffffu);
-  const int written = static_cast<int>(tot >> 16) + min(static_cast<int>(tot & 0xffffu), need_eq);
-  uint32_t sel = gt_mask;  // this thread's taken keys
-  for (int m = need_eq - eq_before; m > 0 && eq_mask != 0u; --m) {
-    const uint32_t low = eq_mask & (0u - eq_mask);  // its lowest-indexed keys equal to T first
-    sel |= low;
-    eq_mask ^= low;
-  }
+  for (int j = 0; j < KPT; ++j) key[j] = order_key(x[j]) & key_mask(i0 + j, G);  // 0 sorts below -inf: never taken
+  uint32_t T;
+  int need_eq;
+  row_sel_threshold<KPT, NT>(key, search, k, lds, T, need_eq);
+  const RowTake tk = row_sel_take<KPT, NT>(key, T, need_eq, wsum);
+  uint32_t sel = tk.sel;
+  int pos = tk.pos;
   // Written in rounds, one taken key per thread (lowest index first), so a wave issues as
   // many store instructions as its busiest thread has taken keys rather than KPT.
-  int pos = gt_before + min(eq_before, need_eq);
   while (__any(sel != 0u)) {
     if (sel != 0u) {
       const int j = __builtin_ctz(sel);
@@ -449,7 +282,7 @@ __global__ void __launch_bounds__(NT) topk_row_kernel(const float* __restrict__ 
       sel &= sel - 1u;
     }
   }
-  for (int i = written + tid; i < k; i += NT) dst[i] = -1;
+  for (int i = tk.written + tid; i < k; i += NT) dst[i] = -1;
 }
 
 // ---- long rows, few of them: the row split over chunk workgroups ---------------------

@@ -138,6 +138,10 @@ class DecodeConfig:
     # indexer launch (one workgroup per row emits the group and scores the new key, nine pool
     # a coarse group) -- one launch less per step; False keeps the emission launch of its own
     merged_emit: bool = True
+    # the top-k inside the attention launch (every attention workgroup of a row selects the
+    # row's list from the scores itself: no top-k launch) where the attention kernel takes it
+    # -- at most 8192 keys and a top-2048, multiples of 4; False keeps the top-k launch
+    select_in_attention: bool = True
 
     @property
     def dim(self) -> int:
@@ -477,6 +481,14 @@ class SparseDecodeLayer:
         self._select_and_attend(q, (cos, sin), advance)
         return self.out if self.out_proj is None else self.out_proj(self.out)
 
+    @property
+    def selects_in_attention(self) -> bool:
+        """Whether the step's top-k runs inside the attention launch (``select_in_attention``,
+        no branch overlap, at most 8192 keys and a top-2048, multiples of 4)."""
+        cfg = self.cfg
+        return (cfg.select_in_attention and not cfg.branch_overlap and cfg.max_groups <= 8192 and cfg.topk <= 2048
+                and cfg.max_groups % 4 == 0 and cfg.topk % 4 == 0)
+
     def _select_and_attend(self, q, rope, advance=False):
         """Top-k, then the attention over [window ; dense ; top-k entries] with the sink, and
         with ``advance`` the positions' ``+= 1`` (in the merge launch).  With
@@ -485,6 +497,14 @@ class SparseDecodeLayer:
         takes them all (the same softmax over the concatenated entries)."""
         cfg = self.cfg
         b = cfg.batch
+        if self.selects_in_attention:
+            csa2_attn.sparse_mqa_decode_select(q, self.positions, self.win, cfg.window, main_cache=self.main,
+                                               scores=self.scores.view(b, cfg.max_groups), topk=cfg.topk,
+                                               idx_out=self.idx, dense_cache=self.coarse,
+                                               dense_ratio=max(cfg.coarse_ratio, 1), sinks=self.sinks,
+                                               nsplit=cfg.nsplit, nope=cfg.nope, workspace=self.workspace,
+                                               out=self.out, lse=self.lse, rope=rope, advance=advance)
+            return
         if not cfg.branch_overlap:
             indexer.topk(self.scores.view(b, cfg.max_groups), cfg.topk, out=self.idx, workspace=self.topk_ws)
             csa2_attn.sparse_mqa_decode(q, self.positions, self.win, cfg.window, main_cache=self.main,
