@@ -574,7 +574,7 @@ def run_decode(torch, dev, args):
                    "split_merge": "merge kernel" if "sparse_mqa_combine" in stages else "inside the attention launch",
                    "emission": ("inside the indexer launch" if layer._merged_emit else "launch of its own")
                    if fused else None,
-                   "topk": "inside the attention launch" if layer.selects_in_attention else "launch of its own",
+                   "selection": "inside the attention launch" if layer.selects_in_attention else "top-k launch",
                    "step": "per attention layer, inside a graph replay of graph_layers layers",
                    "prologue": ("fused: in-step group emission (carry ring, pooling + norm, cache entry and "
                                 "index key every 4th token; RoPE tables from the position table), kv RMSNorm + "
