@@ -289,6 +289,35 @@ struct RowPlan {
     g_lim = p.G < 0x7fffffff ? p.G : 0x7fffffff;
   }
 
+  // plan() in two parts, for the selecting kernel: the row's (plan_row, given its position;
+  // its divisions run while the scores are in flight) and the split's (plan_split, given the
+  // sparse list's valid length once it is selected).  The same results as plan().
+  __device__ void plan_row(const AttnParams& p, int64_t row_pos) {
+    pos = row_pos < -1 ? -1 : row_pos;
+    nw = static_cast<int>(pos + 1 < p.window ? pos + 1 : p.window);
+    int nd = 0;
+    if (p.dense) {
+      const int64_t n = (pos + 1) / p.dense_ratio;
+      nd = static_cast<int>(n < p.dense_cap ? n : p.dense_cap);
+    }
+    nwd = nw + nd;
+    win_b = p.win + b * p.win_batch_entries * L::kEntryBytes;
+    dense_b = p.dense ? p.dense + b * p.dense_batch_entries * L::kEntryBytes : nullptr;
+    main_b = p.main ? p.main + b * p.main_batch_entries * L::kEntryBytes : nullptr;
+    win_first = static_cast<int>(p.win_cap ? (pos - nw + 1) % p.win_cap : pos - nw + 1);
+    g_lim = p.G < 0x7fffffff ? p.G : 0x7fffffff;
+  }
+  __device__ void plan_split(const AttnParams& p, int ns_used) {
+    const int ns = p.main ? ns_used : 0;
+    const int total = nwd + ns;
+    int chunk = (total + p.nsplit - 1) / p.nsplit;
+    chunk = (chunk + kTile - 1) / kTile * kTile;
+    v_begin = split * chunk;
+    v_end = v_begin + chunk < total ? v_begin + chunk : total;
+    ntiles = v_end > v_begin ? (v_end - v_begin + kTile - 1) / kTile : 0;
+    sp_begin = v_begin > nwd ? v_begin - nwd : 0;
+  }
+
   // Stage up to `cap` indices of this split's slice of the sparse list in LDS, so the tile
   // loop reads them from there; positions beyond the cap are read from global memory.
   // The caller synchronises before the slice is read.
@@ -1108,6 +1137,7 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
   }
   __shared__ int wred[2 * 8];
   if constexpr (SEL) {
+    rp.plan_row(p, row_pos);
     // the row's selection in the tile region of LDS (first written by the tile loop, after
     // the barriers below): three histograms and the scan scratch
     int* const h1 = reinterpret_cast<int*>(smem);
@@ -1139,16 +1169,21 @@ sparse_mqa_dsplit_kernel(const AttnParams p) {
     // the split is planned over its `written` valid entries directly, and every thread puts
     // its picks of this split's slice straight into the staged indices (a slice holds at most
     // kAllTabCap - 96 < kSplitIdxCap entries); the row's first workgroup also writes the list
-    rp.plan(p, row_pos, tk.written);
+    rp.plan_split(p, tk.written);
     const int sp_end = rp.v_end > rp.nwd ? rp.v_end - rp.nwd : 0;
     const bool first = p.sel_out != nullptr && rp.split == 0 && rp.hgrp == 0;
     int32_t* const orow = first ? p.sel_out + rp.row * p.sel_out_stride : nullptr;
+    // a thread's picks take list positions pos .. pos + popcount - 1, ascending with the
+    // thread, so only the threads around this split's slice (and in the row's first
+    // workgroup, every thread) walk them
     uint32_t sel = tk.sel;
-    for (int at = tk.pos; sel != 0u; ++at) {
-      const int g = i0 + __builtin_ctz(sel);
-      if (at >= rp.sp_begin && at < sp_end) sidx[at - rp.sp_begin] = g;
-      if (first && at < k) orow[at] = g;
-      sel &= sel - 1u;
+    if (first || (tk.pos < sp_end && tk.pos + __builtin_popcount(sel) > rp.sp_begin)) {
+      for (int at = tk.pos; sel != 0u; ++at) {
+        const int g = i0 + __builtin_ctz(sel);
+        if (at >= rp.sp_begin && at < sp_end) sidx[at - rp.sp_begin] = g;
+        if (first && at < k) orow[at] = g;
+        sel &= sel - 1u;
+      }
     }
     if (first)
       for (int i = tk.written + tid; i < k; i += NT) orow[i] = -1;
