@@ -7,8 +7,8 @@ top-k launch followed by the attention over that list (``indexer.topk`` +
 finite scores than topk and rows with none, the fused RoPE, a dense branch, one to sixteen
 splits, the merge inside the attention launch, the position advance, graph replays, and the
 form that falls back to the two launches (a key count that is not a multiple of 4, or more
-than 8192 keys).  The list also equals the oracle's top-k, and the output meets the
-attention bar against the oracle.
+than 8192 keys: config 4's 32768 among them).  The list also equals the oracle's top-k, and
+the output meets the attention bar against the oracle.
 """
 
 import numpy as np
@@ -67,7 +67,8 @@ def _rope(b, dev, seed):
 @pytest.mark.parametrize("b,g,topk,nsplit,kind,use_rope,dense", [
     (32, 8192, 2048, 4, "normal", True, 0), (8, 8192, 2048, 4, "ties", True, 0), (8, 8192, 2048, 1, "normal", True, 0),
     (8, 8192, 2048, 16, "ties", False, 0), (4, 4096, 512, 4, "normal", True, 256), (6, 1000, 128, 2, "ties", False, 0),
-    (5, 8190, 2048, 4, "normal", True, 0), (4, 16384, 2048, 8, "normal", True, 0)])
+    (5, 8190, 2048, 4, "normal", True, 0), (8, 32768, 2048, 16, "normal", True, 0), (8, 32768, 2048, 16, "ties", True, 0),
+    (4, 16384, 2048, 8, "normal", False, 0), (3, 20000, 512, 4, "ties", True, 128), (2, 40000, 2048, 8, "normal", True, 0)])
 def test_select_equals_topk_then_attention(dev, b, g, topk, nsplit, kind, use_rope, dense):
     pos = 4 * g + 3 if kind != "ties" else 3 * g  # ties: a quarter of the groups still invisible
     q, win_c, main_c, dense_c, sc, sinks = _case(dev, b, g, pos, seed=b + g + nsplit, kind=kind, dense=dense)
