@@ -158,6 +158,10 @@ struct IdxParams {
   int64_t cand_stride;
   int cand_nb, cand_bs;
   int64_t cand_keys;  // keys per batch row (the slots' key range)
+  // EMIT: the grid is one-dimensional, rows x scoring workgroups per row, then (lead_last)
+  // the rows' lead workgroups, or the lead workgroups first
+  int64_t rows;
+  int lead_last;
 };
 
 constexpr int kFuseNope = 512, kFuseRope = 64, kFuseChunks = (kFuseNope + kFuseRope) / 64;
@@ -509,11 +513,13 @@ __device__ __forceinline__ void emit_and_score(const IdxParams& p, const EmitPar
 // runs the kv prologue (FusedKv): loads before the keys', the work after the query's
 // quantization.
 // EMIT (with FUSE; one query row per batch row, ratio 4): the step's group emission joins
-// the launch.  Per row, workgroup 0 runs the emission (emit_row: carry slot, step tables,
-// and on a group step the group's entry and index key) and then scores the new key itself
-// (emit_and_score), workgroup 1 writes the token's window entry (kv_prologue), and the
-// scoring workgroups start at 2; they take the query's RoPE tables from row `pos` of the
-// position table and leave the new key's score to workgroup 0.
+// the launch.  Per row, lead workgroup 0 runs the emission (emit_row: carry slot, step
+// tables, and on a group step the group's entry and index key) and then scores the new key
+// itself (emit_and_score), lead workgroup 1 writes the token's window entry (kv_prologue),
+// and the scoring workgroups take the query's RoPE tables from row `pos` of the position
+// table and leave the new key's score to lead workgroup 0.  The grid is one-dimensional:
+// rows x scoring workgroups, then rows x lead workgroups (or the lead workgroups first, see
+// IdxParams::lead_last); xw below is the workgroup's place in its row, leads first.
 template <int FMT, int DI, int MB, bool QRAW, bool APPEND, bool FUSE = false, bool GATHER = false, bool EMIT = false,
           int NKB = kNkb, bool COARSE = false>
 __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxParams p, const EmitSet es) {
@@ -532,7 +538,23 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int hi = lane >> 5;
-  const int64_t row = blockIdx.y;
+  // the row and the workgroup's place in it: xw < kLead a lead workgroup (EMIT), else the
+  // scoring workgroup xw - kLead of the row
+  int64_t row = blockIdx.y;
+  int64_t xw = blockIdx.x;
+  if constexpr (EMIT) {
+    const int64_t nsw = (p.G + kWaves * NKB * 32 - 1) / (kWaves * NKB * 32);
+    const int64_t l = blockIdx.x;
+    const int64_t lead0 = p.lead_last ? p.rows * nsw : 0;  // the first lead workgroup
+    const int64_t sc0 = p.lead_last ? 0 : p.rows * kLead;  // the first scoring workgroup
+    if (l >= lead0 && l < lead0 + p.rows * kLead) {
+      row = (l - lead0) / kLead;
+      xw = (l - lead0) % kLead;
+    } else {
+      row = (l - sc0) / nsw;
+      xw = kLead + (l - sc0) % nsw;
+    }
+  }
   const int64_t b = row / p.S;
   const int Hi = p.Hi;
   const int64_t G = p.G;
@@ -544,22 +566,22 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
   float* out = p.scores + row * p.sstride;
 
   if constexpr (EMIT) {
-    if (blockIdx.x == 0) {  // uniform: the row's emission
+    if (xw == 0) {  // uniform: the row's emission
       emit_and_score<FMT, MB>(p, e, row);
       return;
     }
-    if (blockIdx.x == 1) {  // uniform: the token's window entry and its carry slot
+    if (xw == 1) {  // uniform: the token's window entry and its carry slot
       if (tid < 64) kv_prologue(e, row, tid);
       else carry_slot<kWaves * 64 - 64>(e, row, tid - 64);
       return;
     }
-    if (COARSE && blockIdx.x < kLead) {  // uniform: a part of the coarse branch's group step
-      coarse_body(es.coarse, row * kCoarseParts + (blockIdx.x - 2));
+    if (COARSE && xw < kLead) {  // uniform: a part of the coarse branch's group step
+      coarse_body(es.coarse, row * kCoarseParts + (xw - 2));
       return;
     }
   }
   const int64_t wave_key0 =
-      (static_cast<int64_t>(blockIdx.x) - kLead) * (kWaves * NKB * 32) + wave * (NKB * 32);
+      (xw - kLead) * (kWaves * NKB * 32) + wave * (NKB * 32);
   // Load order.  Vector-memory loads complete in issue order, so the small operands every
   // tile needs -- the query (fragments, or the bf16 rows to quantize) and the head
   // weights -- go first; then all key fragments of the wave's tiles, so tile 0's MFMAs
@@ -607,10 +629,16 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
   // the whole workgroup) and before the keys (which the score loop waits for)
   FusedKv fkv;
   if constexpr (FUSE && !EMIT) {
-    if (blockIdx.x == 0 && tid < 64) fkv.load(p, row, tid);
+    if (xw == 0 && tid < 64) fkv.load(p, row, tid);
   }
-  Frag bf[NKB][NST];
-  float ksv[NKB];  // FP8: the per-key scales
+  // Key fragments: up to five tiles per wave are all requested here; more (a wave of 8 or 16
+  // tiles, EMIT's long-row forms) stream through a ring of NBUF tile slots, tile t + NBUF
+  // requested into tile t's slot once tile t is scored, so NBUF tiles stay in flight.  Every
+  // request is unconditional (rows clamped), which keeps the in-order wait counts exact.
+  constexpr int NBUF = NKB > 5 ? 4 : NKB;
+  static_assert(NBUF == NKB || (EMIT && !GATHER), "the tile ring serves the merged emission's scorer");
+  Frag bf[NBUF][NST];
+  float ksv[NBUF];  // FP8: the per-key scales
   int32_t cblk[NKB];  // GATHER: the candidate block of each tile's slot, all loaded first
   if constexpr (GATHER) {
     // (loads complete in order: list entries issued between key loads would make each
@@ -622,8 +650,7 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
       cblk[t] = p.cand[row * p.cand_stride + gc / p.cand_bs];
     }
   }
-#pragma unroll
-  for (int t = 0; t < NKB; ++t) {
+  auto issue = [&](int t) __attribute__((always_inline)) {
     // keys at or beyond G read row G-1 instead: their score columns are never written
     const int64_t g = wave_key0 + t * 32 + (lane & 31);
     int64_t gc = g < G ? g : G - 1;
@@ -635,9 +662,11 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
     const uint8_t* krow = kb_base + gc * RB;
     const uint8_t* kerow = FMT == kMxfp4 ? ke_base + gc * (DI / 32) : nullptr;
 #pragma unroll
-    for (int st = 0; st < NST; ++st) bf[t][st] = load_frag<FMT, DI>(krow, kerow, st, hi);
-    ksv[t] = FMT == kFp8 ? ks_base[gc] : 1.0f;
-  }
+    for (int st = 0; st < NST; ++st) bf[t % NBUF][st] = load_frag<FMT, DI>(krow, kerow, st, hi);
+    ksv[t % NBUF] = FMT == kFp8 ? ks_base[gc] : 1.0f;
+  };
+#pragma unroll
+  for (int t = 0; t < NBUF; ++t) issue(t);
   // APPEND: thread t's share of the new latent (nope channels 4t..4t+3, rope channel t),
   // loaded by every workgroup (clamped), packed by workgroup 0 at the end
   uint2 kv_nope = uint2{0u, 0u};
@@ -671,7 +700,7 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
     // the step's RoPE tables (row pos of the position table, which the later launches of
     // the step read) from the row's first scoring workgroup, which holds the row already
     // (emit_row<R, true> leaves them to it): cos in words 0..15 of tw, sin in 16..31
-    if (blockIdx.x == kLead && tid == 0 && e.step_cos && epos >= 0 && epos < e.tab_rows) {
+    if (xw == kLead && tid == 0 && e.step_cos && epos >= 0 && epos < e.tab_rows) {
       uint4* dc = reinterpret_cast<uint4*>(e.step_cos + row * kRopePairs);
       uint4* ds = reinterpret_cast<uint4*>(e.step_sin + row * kRopePairs);
 #pragma unroll
@@ -708,7 +737,7 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
   if constexpr (FUSE && !EMIT) {
     // the row's kv prologue, while the key loads are still in flight (its registers are
     // free again before the score loop)
-    if (blockIdx.x == 0 && tid < 64) fkv.append(p, b, pos, tid);
+    if (xw == 0 && tid < 64) fkv.append(p, b, pos, tid);
   }
   const float cwq = cw * cq;
   float coef[MB][16];
@@ -717,28 +746,27 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
 #pragma unroll
     for (int j = 0; j < 16; ++j) coef[mb][j] = __shfl(cwq, mb * 32 + acc_row(j, lane), 64);
 
-#pragma unroll
-  for (int t = 0; t < NKB; ++t) {
+  // the scores of tile t (a tile that starts below G)
+  auto score = [&](int t) __attribute__((always_inline)) {
     const int64_t g0 = wave_key0 + t * 32;
     const int64_t g = g0 + (lane & 31);
-    if (g0 >= G) break;
     if (!GATHER && g0 >= vis) {  // nothing in this tile is visible to the row
       if (lane < 32 && g < G) out[g] = -__builtin_huge_valf();
-      continue;
+      return;
     }
     float part = 0.0f;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
       v16f acc = {};
 #pragma unroll
-      for (int st = 0; st < NST; ++st) acc = mma<FMT>(a[mb][st], bf[t][st], acc);
+      for (int st = 0; st < NST; ++st) acc = mma<FMT>(a[mb][st], bf[t % NBUF][st], acc);
 #pragma unroll
       for (int j = 0; j < 16; ++j) part = relu_fma(coef[mb][j], acc[j], part);
     }
     const float total = part + __shfl_xor(part, 32, 64);
     if (lane < 32 && g < G && (!EMIT || g != g_own)) {
       float s = total * inv_sqrt_di;
-      if constexpr (FMT == kFp8) s = s * ksv[t];
+      if constexpr (FMT == kFp8) s = s * ksv[t % NBUF];
       int64_t kpos = g;
       if constexpr (GATHER) {  // g < G here, so cblk[t] is slot g's block
         kpos = static_cast<int64_t>(cblk[t]) * p.cand_bs + g % p.cand_bs;
@@ -746,10 +774,25 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
       }
       out[g] = (kpos >= 0 && kpos < vis) ? s : -__builtin_huge_valf();
     }
+  };
+  if constexpr (NBUF == NKB) {
+#pragma unroll
+    for (int t = 0; t < NKB; ++t) {
+      if (wave_key0 + t * 32 >= G) break;
+      score(t);
+    }
+  } else {
+    // the ring: the next request into this tile's slot follows its scores, whether or not the
+    // tile lies inside the row (so every wave issues the same requests)
+#pragma unroll
+    for (int t = 0; t < NKB; ++t) {
+      if (wave_key0 + t * 32 < G) score(t);
+      if (t + NBUF < NKB) issue(t + NBUF);
+    }
   }
 
   if constexpr (QRAW) {
-    if (blockIdx.x == 0) {
+    if (xw == 0) {
       // the quantized query, for callers that keep it (the codes are still in LDS)
       if constexpr (FMT == kFp8) {
         if (p.q_codes_out && qh < Hi) {
@@ -1400,19 +1443,34 @@ extern "C" int mzk_decode_emit_scores(const int64_t* positions, int64_t B, const
                             positions, ratio, scores, score_stride);
   p.q_raw = static_cast<const uint16_t*>(q_idx);
   p.q_rope_dim = 2 * kRopePairs;
-  // four key tiles per wave (512 keys per workgroup) when the grid, with the workgroups before
-  // the scoring ones, fits one round of resident workgroups (two per compute unit); else five
-  // (640 keys), which keeps it within one round where four would overflow it (config 2:
-  // 32 rows x (2 + 16) = 576 > 512, x (2 + 13) = 480 with five)
+  // Key tiles per wave: the fewest of 4, 8 and 16 (512, 1024, 2048 keys per workgroup) that
+  // leave at most one scoring workgroup per compute unit.  The key stream is what a compute
+  // unit's time goes to, so the scoring workgroups carry equal shares, one per unit; the lead
+  // workgroups (emission, window entry, coarse parts; light on a carry-only step) come last
+  // in the grid and share units with scoring workgroups, when the whole grid fits one round
+  // of resident workgroups (two per unit); otherwise they come first.  (Config 2: 32 rows x 8
+  // scoring workgroups of 1024 keys on the 256 units, then the 64 lead workgroups.)
   const int lead = 2 + (coarse ? kCoarseParts : 0);
-  const bool five = B * (lead + (G + kKeysPerWg - 1) / kKeysPerWg) > resident_workgroups(2);
-  const int keys_per_wg = kWaves * (five ? 5 : 4) * 32;
-  dim3 grid(static_cast<unsigned>(lead + (G + keys_per_wg - 1) / keys_per_wg), static_cast<unsigned>(B));
+  const int64_t cus = resident_workgroups(1);
+  int nkb = 16;
+  for (int c : {4, 8}) {
+    if (B * ((G + kWaves * 32 * c - 1) / (kWaves * 32 * c)) <= cus) {
+      nkb = c;
+      break;
+    }
+  }
+  const int64_t nsw = (G + kWaves * 32 * nkb - 1) / (kWaves * 32 * nkb);
+  const int64_t nwg = B * (nsw + lead);
+  MZK_CHECK_ARG(nwg <= 0x7fffffff, "decode_emit_scores: %lld workgroups exceed the grid limit", (long long)nwg);
+  p.rows = B;
+  p.lead_last = nwg <= resident_workgroups(2) ? 1 : 0;
+  dim3 grid(static_cast<unsigned>(nwg));
   hipStream_t s = as_stream(stream);
-#define MZK_EMIT_LAUNCH(F, M, C)                                                                                      \
-  do {                                                                                                               \
-    if (five) indexer_scores_kernel<F, kDi, M, true, false, true, false, true, 5, C><<<grid, kWaves * 64, 0, s>>>(p, es); \
-    else indexer_scores_kernel<F, kDi, M, true, false, true, false, true, 4, C><<<grid, kWaves * 64, 0, s>>>(p, es);      \
+#define MZK_EMIT_LAUNCH(F, M, C)                                                                                       \
+  do {                                                                                                                \
+    if (nkb == 4) indexer_scores_kernel<F, kDi, M, true, false, true, false, true, 4, C><<<grid, kWaves * 64, 0, s>>>(p, es);  \
+    else if (nkb == 8) indexer_scores_kernel<F, kDi, M, true, false, true, false, true, 8, C><<<grid, kWaves * 64, 0, s>>>(p, es); \
+    else indexer_scores_kernel<F, kDi, M, true, false, true, false, true, 16, C><<<grid, kWaves * 64, 0, s>>>(p, es);  \
   } while (0)
   if (fp8) {
     if (coarse) {

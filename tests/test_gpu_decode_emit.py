@@ -327,10 +327,13 @@ def test_emission_pair_equals_two_launches(dev):
     assert pair["main"].any() and pair["coarse"].any() and pair["kc"].any()
 
 
-@pytest.mark.parametrize("fmt,hi,cratio,cap", [("fp8", 64, 0, 1100), ("mxfp4", 64, 0, 1100), ("fp8", 32, 0, 1100),
-                                               ("mxfp4", 20, 0, 1100), ("mxfp4", 64, 8, 1100), ("fp8", 64, 40, 1100),
-                                               ("fp8", 64, 0, 60000), ("mxfp4", 64, 8, 60000)])
-def test_emit_scores_equals_two_launches(dev, fmt, hi, cratio, cap):
+@pytest.mark.parametrize("fmt,hi,cratio,cap,b", [("fp8", 64, 0, 1100, 5), ("mxfp4", 64, 0, 1100, 5),
+                                                 ("fp8", 32, 0, 1100, 5), ("mxfp4", 20, 0, 1100, 5),
+                                                 ("mxfp4", 64, 8, 1100, 5), ("fp8", 64, 40, 1100, 5),
+                                                 ("fp8", 64, 0, 30000, 5), ("mxfp4", 64, 8, 30000, 5),
+                                                 ("fp8", 64, 0, 60000, 5), ("mxfp4", 64, 8, 60000, 5),
+                                                 ("fp8", 64, 0, 720, 300), ("mxfp4", 32, 8, 720, 300)])
+def test_emit_scores_equals_two_launches(dev, fmt, hi, cratio, cap, b):
     """``mzk_decode_emit_scores`` (the emission, the window entry, the indexer query's RoPE +
     quantization and the scores in one launch, the new key scored by its emission workgroup;
     with ``cratio`` a keyless coarse branch too) writes what the emission launch followed by
@@ -338,10 +341,12 @@ def test_emit_scores_equals_two_launches(dev, fmt, hi, cratio, cap):
     on the step's tables) writes, bit for bit -- carries, main and coarse caches, keys, window
     ring, step tables and every score -- over steps that complete groups and steps that only
     carry, with an inactive row (position -1) and a key axis of several scoring workgroups
-    with a partial last one.  ``cap`` 60000 takes the five-tile scoring workgroups (the grid
-    with four would not fit one round of resident workgroups), 1100 the four-tile ones."""
+    with a partial last one.  The key axis takes each form of the scoring workgroups: four
+    tiles per wave (``cap`` 1100), eight (30000) and sixteen (60000: the 16-tile ring), with
+    the lead workgroups after the scoring ones in the grid; 300 rows make the grid larger
+    than one round of resident workgroups, which puts the lead workgroups first."""
     from mzoo_amd import _lib
-    b, ratio, wcap, ccap = 5, 4, 16, 120
+    ratio, wcap, ccap = 4, 16, 120
     rows_tab = 4 * cap + 8
     steps = max(2 * ratio, cratio) + 1
     rng = np.random.default_rng(5 + hi + cratio)
@@ -370,7 +375,10 @@ def test_emit_scores_equals_two_launches(dev, fmt, hi, cratio, cap):
         return s
 
     one, two = state(), state()
+    # five phases of the group (an inactive row first), repeated with shifts for more rows
     start = np.array([-1, 0, 5, 13, 4 * 700 + 2], dtype=np.int64)
+    if b > 5:
+        start = np.array([start[i % 5] + (i // 5) % 4 if i % 5 else -1 for i in range(b)], dtype=np.int64)
     for step in range(steps):
         print(f"emit+scores ({fmt}, Hi={hi}, coarse ratio {cratio}, G={cap}): step {step}", flush=True)
         pos_d = dv(start + step)
