@@ -158,10 +158,8 @@ struct IdxParams {
   int64_t cand_stride;
   int cand_nb, cand_bs;
   int64_t cand_keys;  // keys per batch row (the slots' key range)
-  // EMIT: the grid is one-dimensional, rows x scoring workgroups per row, then (lead_last)
-  // the rows' lead workgroups, or the lead workgroups first
+  // EMIT: the grid is one-dimensional, rows x lead workgroups, then rows x scoring workgroups
   int64_t rows;
-  int lead_last;
 };
 
 constexpr int kFuseNope = 512, kFuseRope = 64, kFuseChunks = (kFuseNope + kFuseRope) / 64;
@@ -518,8 +516,8 @@ __device__ __forceinline__ void emit_and_score(const IdxParams& p, const EmitPar
 // itself (emit_and_score), lead workgroup 1 writes the token's window entry (kv_prologue),
 // and the scoring workgroups take the query's RoPE tables from row `pos` of the position
 // table and leave the new key's score to lead workgroup 0.  The grid is one-dimensional:
-// rows x scoring workgroups, then rows x lead workgroups (or the lead workgroups first, see
-// IdxParams::lead_last); xw below is the workgroup's place in its row, leads first.
+// rows x lead workgroups, then rows x scoring workgroups; xw below is the workgroup's place
+// in its row, leads first.
 template <int FMT, int DI, int MB, bool QRAW, bool APPEND, bool FUSE = false, bool GATHER = false, bool EMIT = false,
           int NKB = kNkb, bool COARSE = false>
 __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxParams p, const EmitSet es) {
@@ -545,14 +543,12 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
   if constexpr (EMIT) {
     const int64_t nsw = (p.G + kWaves * NKB * 32 - 1) / (kWaves * NKB * 32);
     const int64_t l = blockIdx.x;
-    const int64_t lead0 = p.lead_last ? p.rows * nsw : 0;  // the first lead workgroup
-    const int64_t sc0 = p.lead_last ? 0 : p.rows * kLead;  // the first scoring workgroup
-    if (l >= lead0 && l < lead0 + p.rows * kLead) {
-      row = (l - lead0) / kLead;
-      xw = (l - lead0) % kLead;
+    if (l < p.rows * kLead) {
+      row = l / kLead;
+      xw = l % kLead;
     } else {
-      row = (l - sc0) / nsw;
-      xw = kLead + (l - sc0) % nsw;
+      row = (l - p.rows * kLead) / nsw;
+      xw = kLead + (l - p.rows * kLead) % nsw;
     }
   }
   const int64_t b = row / p.S;
@@ -567,7 +563,10 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
 
   if constexpr (EMIT) {
     if (xw == 0) {  // uniform: the row's emission
-      emit_and_score<FMT, MB>(p, e, row);
+      // a step that completes no group has nothing here (its carry slot is lead workgroup
+      // 1's): leave before requesting anything, so the compute unit's key stream is not
+      // queued behind this workgroup's loads
+      if (emitted_group(e, *(const_i64_ptr)(e.positions + row)) >= 0) emit_and_score<FMT, MB>(p, e, row);
       return;
     }
     if (xw == 1) {  // uniform: the token's window entry and its carry slot
@@ -1445,11 +1444,11 @@ extern "C" int mzk_decode_emit_scores(const int64_t* positions, int64_t B, const
   p.q_rope_dim = 2 * kRopePairs;
   // Key tiles per wave: the fewest of 4, 8 and 16 (512, 1024, 2048 keys per workgroup) that
   // leave at most one scoring workgroup per compute unit.  The key stream is what a compute
-  // unit's time goes to, so the scoring workgroups carry equal shares, one per unit; the lead
-  // workgroups (emission, window entry, coarse parts; light on a carry-only step) come last
-  // in the grid and share units with scoring workgroups, when the whole grid fits one round
-  // of resident workgroups (two per unit); otherwise they come first.  (Config 2: 32 rows x 8
-  // scoring workgroups of 1024 keys on the 256 units, then the 64 lead workgroups.)
+  // unit's time goes to, so the scoring workgroups carry equal shares, one per unit.  The lead
+  // workgroups (emission, window entry, coarse parts) come first in the grid: they share
+  // units with scoring workgroups, and a group step's emission, dispatched first, has its
+  // loads (the key weights) served ahead of its neighbour's key stream.  (Config 2: the 64
+  // lead workgroups, then 32 rows x 8 scoring workgroups of 1024 keys on the 256 units.)
   const int lead = 2 + (coarse ? kCoarseParts : 0);
   const int64_t cus = resident_workgroups(1);
   int nkb = 16;
@@ -1463,7 +1462,6 @@ extern "C" int mzk_decode_emit_scores(const int64_t* positions, int64_t B, const
   const int64_t nwg = B * (nsw + lead);
   MZK_CHECK_ARG(nwg <= 0x7fffffff, "decode_emit_scores: %lld workgroups exceed the grid limit", (long long)nwg);
   p.rows = B;
-  p.lead_last = nwg <= resident_workgroups(2) ? 1 : 0;
   dim3 grid(static_cast<unsigned>(nwg));
   hipStream_t s = as_stream(stream);
 #define MZK_EMIT_LAUNCH(F, M, C)                                                                                       \

@@ -342,9 +342,8 @@ def test_emit_scores_equals_two_launches(dev, fmt, hi, cratio, cap, b):
     ring, step tables and every score -- over steps that complete groups and steps that only
     carry, with an inactive row (position -1) and a key axis of several scoring workgroups
     with a partial last one.  The key axis takes each form of the scoring workgroups: four
-    tiles per wave (``cap`` 1100), eight (30000) and sixteen (60000: the 16-tile ring), with
-    the lead workgroups after the scoring ones in the grid; 300 rows make the grid larger
-    than one round of resident workgroups, which puts the lead workgroups first."""
+    tiles per wave (``cap`` 1100), eight (30000) and sixteen (60000: the 16-tile ring); 300
+    rows make the grid larger than one round of resident workgroups."""
     from mzoo_amd import _lib
     ratio, wcap, ccap = 4, 16, 120
     rows_tab = 4 * cap + 8
