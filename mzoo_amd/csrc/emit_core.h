@@ -304,7 +304,12 @@ __device__ __forceinline__ bool emit_row(const EmitParams& p, int64_t b, uint8_t
       }
     }
   }
-  const int64_t pos = p.positions[b];
+  // MERGED: the position through the scalar cache (no vector-memory write in the launch
+  // touches it), so it arrives within one round trip instead of behind the operands above
+  // (a vector load completes after every load issued before it: 4 us into a config-2 group
+  // step, which held back the key weights' requests below)
+  typedef const __attribute__((address_space(4))) int64_t* scalar_i64_ptr;
+  const int64_t pos = MERGED ? *(scalar_i64_ptr)(p.positions + b) : p.positions[b];
   if (pos < 0) return false;  // an inactive row: nothing to carry or emit
   const int r = R > 0 ? R : br.ratio;
   const int slot = static_cast<int>(pos % r);
@@ -322,7 +327,7 @@ __device__ __forceinline__ bool emit_row(const EmitParams& p, int64_t b, uint8_t
   const int lane = t & 63, wv = t >> 6;
   const int j8 = lane & (kLanesPerOut - 1);
   uint4 wreg[4][kChunksPerLane];
-  if (key) {
+  auto load_wk = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int ps = 0; ps < 4; ++ps) {
       const int o = 32 * wv + 8 * ps + (lane >> 3);
@@ -330,6 +335,9 @@ __device__ __forceinline__ bool emit_row(const EmitParams& p, int64_t b, uint8_t
 #pragma unroll
       for (int c = 0; c < kChunksPerLane; ++c) wreg[ps][c] = wrow[j8 + kLanesPerOut * c];
     }
+  };
+  if constexpr (!MERGED) {
+    if (key) load_wk();
   }
   const uint16_t knr = (key ? br.kn_w : br.norm_w)[t & (kDi - 1)];
   // the group's RoPE pair (t & 31): threads 128..159 rotate the latent, 0..31 the key
@@ -340,6 +348,12 @@ __device__ __forceinline__ bool emit_row(const EmitParams& p, int64_t b, uint8_t
   const uint16_t* trow = p.tab + min(pos, last_row) * 2 * kRopePairs;
   const bool step_tab = p.step_cos && pos < p.tab_rows;  // uniform
   const uint16_t stab = trow[t & 63];
+  // MERGED (whose launch always has the key weights, and here a step that emits): the 147 KB
+  // of key weights are requested last and outside any branch, so the pooling and the entry
+  // wait only for their own operands (loads complete in order, and a load inside a branch
+  // would make the waits after it count as if every later load were outstanding: the
+  // pooling then waited for the weights, 8.4 us into a config-2 group step)
+  if constexpr (MERGED) load_wk();
 
   // ---- the token into its carry slot; the step's RoPE tables --------------------------
   if constexpr (!MERGED) {

@@ -266,7 +266,41 @@ constexpr int q_pitch() { return FMT == kFp8 ? 128 + 16 : 64 + 16; }
 typedef unsigned short mzk_u16x2v __attribute__((ext_vector_type(2)));
 typedef __bf16 mzk_bf16x2v __attribute__((ext_vector_type(2)));
 
+// The MFMA A fragments of the query codes quantize_query left in LDS, and (FP8) the lane's
+// head scale.
 template <int FMT, int DI, int MB>
+__device__ __forceinline__ void query_frags(int lane, int hi, int hl, const uint8_t* q_lds, const float* qs_lds,
+                                            const uint8_t* qe_lds, Frag (&a)[MB][DI / Step<FMT>::K], float& cq) {
+  constexpr int QP = q_pitch<FMT>();
+  constexpr int NST = DI / Step<FMT>::K;
+  if constexpr (FMT == kMxfp4) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int h = mb * 32 + (lane & 31);
+#pragma unroll
+      for (int st = 0; st < NST; ++st) {
+        const uint4 u = *reinterpret_cast<const uint4*>(q_lds + h * QP + st * 32 + hi * 16);
+        a[mb][st].v = v8i{(int)u.x, (int)u.y, (int)u.z, (int)u.w, 0, 0, 0, 0};
+        a[mb][st].scale = qe_lds[h * 4 + st * 2 + hi];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const uint4* src = reinterpret_cast<const uint4*>(q_lds + (mb * 32 + (lane & 31)) * QP);
+#pragma unroll
+      for (int st = 0; st < NST; ++st) {
+        const uint4 u = src[4 * st + 2 * hi], v = src[4 * st + 2 * hi + 1];
+        a[mb][st].v = v8i{(int)u.x, (int)u.y, (int)u.z, (int)u.w, (int)v.x, (int)v.y, (int)v.z, (int)v.w};
+        a[mb][st].scale = 127;
+      }
+    }
+    cq = qs_lds[hl];
+  }
+}
+
+// READ false: the codes (and scales) into LDS and the barrier only; query_frags reads them.
+template <int FMT, int DI, int MB, bool READ = true>
 __device__ __forceinline__ void quantize_query(const uint4 (&qr)[4], int qh, int qc, int Hi, int lane, int hi, int hl,
                                                uint8_t* q_lds, float* qs_lds, uint8_t* qe_lds,
                                                Frag (&a)[MB][DI / Step<FMT>::K], float& cq) {
@@ -323,16 +357,7 @@ __device__ __forceinline__ void quantize_query(const uint4 (&qr)[4], int qh, int
     *reinterpret_cast<uint4*>(q_lds + qh * QP + 16 * qc) = uint4{wd[0], wd[1], wd[2], wd[3]};
     qe_lds[qh * 4 + qc] = static_cast<uint8_t>(__float_as_uint(sc) >> 23);
     __syncthreads();
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const int h = mb * 32 + (lane & 31);
-#pragma unroll
-      for (int st = 0; st < NST; ++st) {
-        const uint4 u = *reinterpret_cast<const uint4*>(q_lds + h * QP + st * 32 + hi * 16);
-        a[mb][st].v = v8i{(int)u.x, (int)u.y, (int)u.z, (int)u.w, 0, 0, 0, 0};
-        a[mb][st].scale = qe_lds[h * 4 + st * 2 + hi];
-      }
-    }
+    if constexpr (READ) query_frags<FMT, DI, MB>(lane, hi, hl, q_lds, qs_lds, qe_lds, a, cq);
   } else {
     amax = group_max(amax, 4);  // the 4 threads of a head are consecutive lanes
     const float sc = fp8_scale_from_amax(amax);
@@ -369,17 +394,7 @@ __device__ __forceinline__ void quantize_query(const uint4 (&qr)[4], int qh, int
     dst[1] = uint4{wd[4], wd[5], wd[6], wd[7]};
     if (qc == 0) qs_lds[qh] = sc;
     __syncthreads();
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const uint4* src = reinterpret_cast<const uint4*>(q_lds + (mb * 32 + (lane & 31)) * QP);
-#pragma unroll
-      for (int st = 0; st < NST; ++st) {
-        const uint4 u = src[4 * st + 2 * hi], v = src[4 * st + 2 * hi + 1];
-        a[mb][st].v = v8i{(int)u.x, (int)u.y, (int)u.z, (int)u.w, (int)v.x, (int)v.y, (int)v.z, (int)v.w};
-        a[mb][st].scale = 127;
-      }
-    }
-    cq = qs_lds[hl];
+    if constexpr (READ) query_frags<FMT, DI, MB>(lane, hi, hl, q_lds, qs_lds, qe_lds, a, cq);
   }
 }
 
@@ -464,15 +479,19 @@ __device__ __forceinline__ void emit_and_score(const IdxParams& p, const EmitPar
   float cw = p.w[row * Hi + hl];
   uint32_t tw[kRopePairs];
   load_table_row(e, pos, tw);
-  if (!emit_row<kEmitRatio, true>(e, row, key_lds)) return;  // uniform
-  const int64_t g = (pos + 1) / kEmitRatio - 1;
-  if (g >= p.G) return;
+  // the query is rotated and quantized into LDS first, while the emission's operands (the
+  // key weights last) are still arriving; its fragments are read after the emission
   cw = lane < Hi ? cw : 0.0f;
   rope_query_table(qr, qc, tw);
   Frag a[MB][NST];
   float cq = 1.0f;
-  quantize_query<FMT, kDi, MB>(qr, qh, qc, Hi, lane, hi, hl, q_lds, qs_lds, qe_lds, a, cq);
-  if (tid >= 64) return;  // one wave scores the key (the key bytes were stored before the barrier above)
+  quantize_query<FMT, kDi, MB, false>(qr, qh, qc, Hi, lane, hi, hl, q_lds, qs_lds, qe_lds, a, cq);
+  if (!emit_row<kEmitRatio, true>(e, row, key_lds)) return;  // uniform
+  const int64_t g = (pos + 1) / kEmitRatio - 1;
+  if (g >= p.G) return;  // uniform
+  __syncthreads();  // the key bytes in key_lds
+  if (tid >= 64) return;  // one wave scores the key
+  query_frags<FMT, kDi, MB>(lane, hi, hl, q_lds, qs_lds, qe_lds, a, cq);
   const float cwq = cw * cq;
   float coef[MB][16];
 #pragma unroll
