@@ -179,7 +179,8 @@ int mzk_decode_emit_pair(const int64_t* positions, int64_t B, const float* kv, c
  * With c_kv non-NULL a keyless coarse branch joins the launch, as mzk_decode_emit_pair's
  * (c_* arguments; c_ratio 2 .. 128, B <= 1024).  Per row one workgroup emits the fine group
  * (and scores the new key itself), one writes the window entry, 9 pool the coarse group, and
- * ceil(G / 640) score.  ratio must be 4 (MZK_EINVAL otherwise). */
+ * ceil(G / K) score, K = 512, 1024 or 2048 keys: the least that leaves at most one scoring
+ * workgroup per compute unit.  ratio must be 4 (MZK_EINVAL otherwise). */
 int mzk_decode_emit_scores(const int64_t* positions, int64_t B, const float* kv, const float* gate, float* carry_kv,
                            float* carry_gate, int ratio, const void* norm_weight, float eps, uint8_t* cache,
                            int64_t cache_batch_entries, int64_t cache_cap, const void* wk, const void* k_norm_weight,
