@@ -651,9 +651,11 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
   }
   // Key fragments: up to five tiles per wave are all requested here; more (a wave of 8 or 16
   // tiles, EMIT's long-row forms) stream through a ring of NBUF tile slots, tile t + NBUF
-  // requested into tile t's slot once tile t is scored, so NBUF tiles stay in flight.  Every
-  // request is unconditional (rows clamped), which keeps the in-order wait counts exact.
-  constexpr int NBUF = NKB > 5 ? 4 : NKB;
+  // requested into tile t's slot once tile t is scored, so NBUF tiles stay in flight: 8 KB of
+  // keys per wave, two FP8 tiles or four MXFP4 ones (measured best of 2 .. 7 slots for both:
+  // more in flight was slower).  Every request is unconditional (rows clamped), which keeps
+  // the in-order wait counts exact.
+  constexpr int NBUF = NKB > 5 ? (FMT == kFp8 ? 2 : 4) : NKB;
   static_assert(NBUF == NKB || (EMIT && !GATHER), "the tile ring serves the merged emission's scorer");
   Frag bf[NBUF][NST];
   float ksv[NBUF];  // FP8: the per-key scales
