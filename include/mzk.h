@@ -180,7 +180,12 @@ int mzk_decode_emit_pair(const int64_t* positions, int64_t B, const float* kv, c
  * (c_* arguments; c_ratio 2 .. 128, B <= 1024).  Per row one workgroup emits the fine group
  * (and scores the new key itself), one writes the window entry, 9 pool the coarse group, and
  * ceil(G / K) score, K = 512, 1024 or 2048 keys: the least that leaves at most one scoring
- * workgroup per compute unit.  ratio must be 4 (MZK_EINVAL otherwise). */
+ * workgroup per compute unit.  On a group step the window workgroup computes half of the
+ * key projection and hands it to the emission workgroup through key_half, int64 [B, 40]
+ * (16-byte aligned, zero before the first call; the launch keeps a per-row count of group
+ * steps there, and word 33 of a row turns nonzero, and stays, if the emission workgroup gave
+ * up waiting).  Calls that overlap on one key_half race.  ratio must be 4 (MZK_EINVAL
+ * otherwise). */
 int mzk_decode_emit_scores(const int64_t* positions, int64_t B, const float* kv, const float* gate, float* carry_kv,
                            float* carry_gate, int ratio, const void* norm_weight, float eps, uint8_t* cache,
                            int64_t cache_batch_entries, int64_t cache_cap, const void* wk, const void* k_norm_weight,
@@ -190,7 +195,8 @@ int mzk_decode_emit_scores(const int64_t* positions, int64_t B, const float* kv,
                            int64_t win_batch_entries, int win_cap, const void* q_idx, const float* w, int Hi,
                            int64_t G, float* scores, int64_t score_stride, const float* c_kv, const float* c_gate,
                            float* c_carry_kv, float* c_carry_gate, int c_ratio, const void* c_norm_weight, float c_eps,
-                           uint8_t* c_cache, int64_t c_cache_batch_entries, int64_t c_cache_cap, void* stream);
+                           uint8_t* c_cache, int64_t c_cache_batch_entries, int64_t c_cache_cap, void* key_half,
+                           void* stream);
 
 /* ---------------------------------------------------------------------------------
  * Piece 2: KV compressor and RoPE

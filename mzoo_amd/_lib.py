@@ -84,7 +84,7 @@ _SIGS = {
                         _I64, _P, _P, _P, _P, _F32, _P, _I64, _I32, _P, _I32, _P, _P, _P],
     "mzk_decode_emit_scores": [_P, _I64, _P, _P, _P, _P, _I32, _P, _F32, _P, _I64, _I64, _P, _P, _F32, _I32, _P, _P, _I64,
                                _P, _I64, _P, _P, _P, _P, _F32, _P, _I64, _I32, _P, _P, _I32, _I64, _P, _I64,
-                               _P, _P, _P, _P, _I32, _P, _F32, _P, _I64, _I64, _P],
+                               _P, _P, _P, _P, _I32, _P, _F32, _P, _I64, _I64, _P, _P],
     "mzk_decode_emit_pair": [_P, _I64, _P, _P, _P, _P, _I32, _P, _F32, _P, _I64, _I64, _P, _P, _F32, _I32, _P, _P, _I64, _P, _I64, _P, _P, _P, _P, _F32, _P, _I64, _I32, _P, _I32, _P, _P, _P, _P, _P, _P, _I32, _P, _F32, _P, _I64, _I64, _P],
     "mzk_sparse_mqa_noalloc": [_P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _I64, _I32, _I32, _P, _I64, _I32, _I32,
                                _P, _I64, _I64, _P, _I64, _I32, _P, _I32, _P, _P, _P, _P, _I32, _P],

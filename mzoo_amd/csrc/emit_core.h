@@ -73,12 +73,26 @@ struct EmitParams {
   uint8_t* win;              // window ring of FP8-b128 entries, slot b * win_batch + pos % win_cap
   int64_t win_batch;
   int win_cap;
+  // MERGED: [B, kKeyHalfWords] the key projection's handoff between the row's two lead
+  // workgroups (zero before the first launch); null elsewhere
+  uint64_t* key_half;
   const uint16_t* q_idx;     // [B, 64, 128] bf16: the unrotated indexer query (null: none)
   int q_fmt;                 // 0: FP8 b128 -> q_codes [B, 64, 128] + fp32 [B, 64]; 1: MXFP4 -> [B, 64, 64] + e8m0 [B, 64, 4]
   uint8_t* q_codes;
   void* q_scales;
   int64_t B;                 // rows; the workgroups from B on run the prologue
 };
+
+// The merged launch splits a group step's key projection (k = latent . wk^T, 128 outputs)
+// between the row's emission workgroup (outputs 0..63, then the rest of the key) and its
+// window workgroup (outputs 64..127, which it recomputes the pooled latent for): each reads
+// half of the 147 KB of key weights.  Handoff record of a row (kKeyHalfWords 64-bit words):
+// word 0 the row's epoch (group steps handed over so far), words 1..32 the helper's 64
+// outputs as bf16 pairs under the epoch + 1 in the high half, word 33 a flag (nonzero: the
+// emission workgroup gave up waiting; it stays set).  Every word is written and read with
+// device-scope atomics, so the record needs no fence on any placement of the two.
+constexpr int kKeyHalfWords = 40;
+constexpr int kKeyHalfSpinLimit = 1 << 20;
 
 constexpr int kQHeads = 64;   // indexer heads
 constexpr int kQBlocks = 4;   // query workgroups per row: 16 heads each, 16 threads x 8 channels a head
@@ -255,10 +269,15 @@ __device__ __forceinline__ void carry_slot(const EmitParams& p, int64_t b, int t
 // MERGED (the merged emission + scores launch, R > 1): the token's carry slot and the step's
 // RoPE tables are written by other workgroups of that launch (carry_slot, the row's first
 // scoring workgroup), so a step that completes no group ends as soon as the position is
-// known.
-template <int R, bool MERGED = false>
+// known.  ROLE (MERGED): 1 the emission workgroup (key outputs 0..63, the rest from the
+// handoff), 2 the window workgroup's half (the pooled latent, key outputs 64..127 to the
+// handoff; no entry, no key; returns false).
+template <int R, bool MERGED = false, int ROLE = 0>
 __device__ __forceinline__ bool emit_row(const EmitParams& p, int64_t b, uint8_t* key_out) {
   static_assert(!MERGED || R > 1, "the merged form keeps the group in registers");
+  static_assert(ROLE == 0 || MERGED, "the key split is the merged launch's");
+  constexpr int NPS = ROLE ? 2 : 4;         // key-output passes of 8 per wave
+  constexpr int OBASE = ROLE == 2 ? 64 : 0;  // this workgroup's first key output
   __shared__ float lat[kD];
   __shared__ float kvec[kDi];
   __shared__ float inv_s[2];
@@ -321,16 +340,27 @@ __device__ __forceinline__ bool emit_row(const EmitParams& p, int64_t b, uint8_t
   float* ckv = br.carry_kv + b * static_cast<int64_t>(r) * kD;
   float* cgt = br.carry_gate + b * static_cast<int64_t>(r) * kD;
   if (MERGED && !emit) return false;  // uniform: the carry slot is another workgroup's
+  // ROLE: the row's handoff record and the epoch this step hands over under
+  uint64_t* kh = ROLE ? p.key_half + b * kKeyHalfWords : nullptr;
+  uint32_t epoch = 0;
+  if constexpr (ROLE != 0) {
+    if (t == 0) inv_s[1] = __uint_as_float(static_cast<uint32_t>(
+                    __hip_atomic_load(kh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) + 1u);
+  }
   // key weights: lane j of each 8-lane group reads chunks j, j+8, ... of its output's row,
   // so one load instruction covers 8 rows x 128 contiguous bytes; a wave serves 8 outputs
   // per pass, 4 passes (outputs 32 w + 8 pass + lane / 8)
   const int lane = t & 63, wv = t >> 6;
   const int j8 = lane & (kLanesPerOut - 1);
-  uint4 wreg[4][kChunksPerLane];
+  // key output of pass ps of this lane (8 lanes per output)
+  auto out_of = [&](int ps) __attribute__((always_inline)) {
+    return OBASE + (ROLE ? 16 : 32) * wv + 8 * ps + (lane >> 3);
+  };
+  uint4 wreg[NPS][kChunksPerLane];
   auto load_wk = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int ps = 0; ps < 4; ++ps) {
-      const int o = 32 * wv + 8 * ps + (lane >> 3);
+    for (int ps = 0; ps < NPS; ++ps) {
+      const int o = out_of(ps);
       const uint4* wrow = reinterpret_cast<const uint4*>(br.wk + static_cast<int64_t>(o) * kD);
 #pragma unroll
       for (int c = 0; c < kChunksPerLane; ++c) wreg[ps][c] = wrow[j8 + kLanesPerOut * c];
@@ -469,10 +499,13 @@ __device__ __forceinline__ bool emit_row(const EmitParams& p, int64_t b, uint8_t
     }
   }
   __syncthreads();
+  if constexpr (ROLE != 0) epoch = __float_as_uint(inv_s[1]);  // written before the barriers above
 
   // ---- the main cache entry: FP8-b128 nope blocks + rotated bf16 rope channels
   uint8_t* ent = br.cache + (b * br.cache_batch + g) * kEntryBytes;
-  if (t < kNope / 4) {
+  if (ROLE == 2) {
+    // the window workgroup's half: no entry
+  } else if (t < kNope / 4) {
     float v[4] = {lat[4 * t], lat[4 * t + 1], lat[4 * t + 2], lat[4 * t + 3]};
     float amax = abs_max4(v);
     amax = wave_max_group(amax, 32);
@@ -494,7 +527,7 @@ __device__ __forceinline__ bool emit_row(const EmitParams& p, int64_t b, uint8_t
 
   // ---- the index key: k = bf16(latent . wk^T), pinned 8-lane order
 #pragma unroll
-  for (int ps = 0; ps < 4; ++ps) {
+  for (int ps = 0; ps < NPS; ++ps) {
     float acc = 0.0f;
 #pragma unroll
     for (int c = 0; c < kChunksPerLane; ++c) {
@@ -512,9 +545,50 @@ __device__ __forceinline__ bool emit_row(const EmitParams& p, int64_t b, uint8_t
     acc = acc + lane_xor<4>(acc);
     acc = acc + lane_xor<2>(acc);
     acc = acc + lane_xor<1>(acc);
-    if (j8 == 0) kvec[32 * wv + 8 * ps + (lane >> 3)] = bf(acc);
+    if (j8 == 0) kvec[out_of(ps)] = bf(acc);
   }
   __syncthreads();
+  if constexpr (ROLE == 2) {
+    // outputs 64..127 to the handoff: lane l of wave 0 sends outputs 64 + 2l, 65 + 2l
+    if (t < 32) {
+      const uint32_t pair = static_cast<uint32_t>(f32_to_bf16(kvec[64 + 2 * t])) |
+                            (static_cast<uint32_t>(f32_to_bf16(kvec[65 + 2 * t])) << 16);
+      __hip_atomic_store(kh + 1 + t, (static_cast<uint64_t>(epoch) << 32) | pair, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return false;
+  }
+  if constexpr (ROLE == 1) {
+    // outputs 64..127 from the window workgroup: lane l of wave 0 polls its pair's word
+    // until it carries this step's epoch (bounded: after kKeyHalfSpinLimit polls the flag
+    // is set and the key is written from zeros)
+    if (t < 64) {
+      uint64_t w = 0;
+      bool have = true;
+      if (t < 32) {
+        w = __hip_atomic_load(kh + 1 + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        have = static_cast<uint32_t>(w >> 32) == epoch;
+      }
+      for (int it = 0; !__all(have) && it < kKeyHalfSpinLimit; ++it) {
+        __builtin_amdgcn_s_sleep(1);
+        if (!have) {
+          w = __hip_atomic_load(kh + 1 + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          have = static_cast<uint32_t>(w >> 32) == epoch;
+        }
+      }
+      const bool all = __all(have);
+      if (t < 32) {
+        const uint32_t pair = all ? static_cast<uint32_t>(w) : 0u;
+        kvec[64 + 2 * t] = bf16_to_f32(static_cast<uint16_t>(pair & 0xffffu));
+        kvec[65 + 2 * t] = bf16_to_f32(static_cast<uint16_t>(pair >> 16));
+      }
+      if (t == 0) {
+        __hip_atomic_store(kh, static_cast<uint64_t>(epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (!all) __hip_atomic_store(kh + 33, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    __syncthreads();
+  }
   if (t < 64) {  // k_norm: lane l sums channels l, l + 64
     float ss = 0.0f;
     ss = ss + kvec[t] * kvec[t];

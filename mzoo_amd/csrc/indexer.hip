@@ -486,7 +486,7 @@ __device__ __forceinline__ void emit_and_score(const IdxParams& p, const EmitPar
   Frag a[MB][NST];
   float cq = 1.0f;
   quantize_query<FMT, kDi, MB, false>(qr, qh, qc, Hi, lane, hi, hl, q_lds, qs_lds, qe_lds, a, cq);
-  if (!emit_row<kEmitRatio, true>(e, row, key_lds)) return;  // uniform
+  if (!emit_row<kEmitRatio, true, 1>(e, row, key_lds)) return;  // uniform
   const int64_t g = (pos + 1) / kEmitRatio - 1;
   if (g >= p.G) return;  // uniform
   __syncthreads();  // the key bytes in key_lds
@@ -591,6 +591,9 @@ __global__ void __launch_bounds__(kWaves * 64) indexer_scores_kernel(const IdxPa
     if (xw == 1) {  // uniform: the token's window entry and its carry slot
       if (tid < 64) kv_prologue(e, row, tid);
       else carry_slot<kWaves * 64 - 64>(e, row, tid - 64);
+      // on a group step then the key projection's second half, which the emission workgroup
+      // waits for
+      if (emitted_group(e, *(const_i64_ptr)(e.positions + row)) >= 0) emit_row<kEmitRatio, true, 2>(e, row, nullptr);
       return;
     }
     if (COARSE && xw < kLead) {  // uniform: a part of the coarse branch's group step
@@ -1430,16 +1433,20 @@ extern "C" int mzk_decode_emit_scores(const int64_t* positions, int64_t B, const
                                       int64_t score_stride, const float* c_kv, const float* c_gate, float* c_carry_kv,
                                       float* c_carry_gate, int c_ratio, const void* c_norm_weight, float c_eps,
                                       uint8_t* c_cache, int64_t c_cache_batch_entries, int64_t c_cache_cap,
-                                      void* stream) {
+                                      void* key_half, void* stream) {
   MZK_CHECK_ARG(ratio == kEmitRatio, "decode_emit_scores: the merged launch takes compress ratio 4 (got %d)", ratio);
   MZK_CHECK_ARG(wk && kv_proj && q_idx && w && scores,
                 "decode_emit_scores: needs the index key weights, the kv prologue, q_idx, w and scores");
+  MZK_CHECK_ARG(key_half != nullptr && aligned16(key_half),
+                "decode_emit_scores: key_half (a zeroed, 16-byte aligned [B, %d] int64 buffer) is required",
+                kKeyHalfWords);
   EmitSet es;
   int rc = build_emit(positions, B, kv, gate, carry_kv, carry_gate, ratio, norm_weight, eps, cache,
                       cache_batch_entries, cache_cap, wk, k_norm_weight, k_eps, key_format, k_codes, k_scales,
                       key_batch_entries, rope_table, table_rows, step_cos, step_sin, kv_proj, kv_weight, kv_eps,
                       win_cache, win_batch_entries, win_cap, nullptr, 0, nullptr, nullptr, es.fine);
   if (rc) return rc;
+  es.fine.key_half = static_cast<uint64_t*>(key_half);
   const bool coarse = c_kv != nullptr;
   if (coarse) {
     rc = build_emit(positions, B, c_kv, c_gate, c_carry_kv, c_carry_gate, c_ratio, c_norm_weight, c_eps, c_cache,

@@ -234,6 +234,9 @@ class SparseDecodeLayer:
         # the emission inside the indexer launch (coarse branches of ratio <= 128, up to 1024 rows)
         self._merged_emit = (self._emit_prologue and cfg.merged_emit and cfg.ratio == 4
                              and (not cfg.coarse_ratio or (2 <= cfg.coarse_ratio <= 128 and b <= 1024)))
+        # the merged launch's key-projection handoff between a row's two lead workgroups
+        # (zero before the first step; the launch keeps its per-row count there)
+        self.key_half = torch.zeros(b, 40, dtype=torch.int64, device=dev) if self._merged_emit else None
         if self._emit_prologue and cfg.index_format == "fp8":
             self.q_codes = torch.empty(b, 1, cfg.index_heads, cfg.index_dim, dtype=torch.uint8, device=dev)
             self.q_scales = torch.empty(b, 1, cfg.index_heads, dtype=torch.float32, device=dev)
@@ -378,7 +381,8 @@ class SparseDecodeLayer:
                   self.rope_table.data_ptr(), self.rope_table.shape[0], self.step_cos.data_ptr(),
                   self.step_sin.data_ptr(), kv.data_ptr(), self.kv_norm_weight.data_ptr(), self.kv_norm_eps,
                   self.win.data_ptr(), cfg.window, cfg.window, q_idx.data_ptr(), wc.data_ptr(), cfg.index_heads,
-                  cfg.max_groups, self.scores.data_ptr(), cfg.max_groups, *coarse, _lib.stream_of(self.positions))
+                  cfg.max_groups, self.scores.data_ptr(), cfg.max_groups, *coarse, self.key_half.data_ptr(),
+                  _lib.stream_of(self.positions))
 
     def fill_coarse(self, latents: torch.Tensor) -> None:
         """latents [B, n, D] -> coarse entries 0..n-1 of every row."""

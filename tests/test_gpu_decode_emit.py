@@ -374,6 +374,7 @@ def test_emit_scores_equals_two_launches(dev, fmt, hi, cratio, cap, b):
         return s
 
     one, two = state(), state()
+    key_half = torch.zeros(b, 40, dtype=torch.int64, device=dev)  # the merged launch's handoff
     # five phases of the group (an inactive row first), repeated with shifts for more rows
     start = np.array([-1, 0, 5, 13, 4 * 700 + 2], dtype=np.int64)
     if b > 5:
@@ -398,7 +399,7 @@ def test_emit_scores_equals_two_launches(dev, fmt, hi, cratio, cap, b):
             if merged:
                 _lib.call("mzk_decode_emit_scores", *emit, kvp.data_ptr(), kvw_d.data_ptr(), 1e-6,
                           s["win"].data_ptr(), wcap, wcap, q_idx.data_ptr(), w.data_ptr(), hi, cap,
-                          s["scores"].data_ptr(), cap, *coarse, st)
+                          s["scores"].data_ptr(), cap, *coarse, key_half.data_ptr(), st)
             else:
                 no_pro = (None, None, 0.0, None, 0, 0, None, 0, None, None)
                 if cratio:
@@ -424,3 +425,8 @@ def test_emit_scores_equals_two_launches(dev, fmt, hi, cratio, cap, b):
     last = start + steps - 1
     finite = torch.isfinite(one["scores"]).sum(1).cpu().numpy()
     assert np.array_equal(finite, np.minimum(cap, (last + 1) // ratio)), finite
+    # the handoff: one count per group step that emits a key, no wait given up
+    kh = key_half.cpu().numpy()
+    groups = [sum((q + 1) % ratio == 0 and q >= 0 and (q + 1) // ratio - 1 < cap and (q + 1) // ratio * ratio - ratio
+                  < rows_tab for q in range(s0, s0 + steps)) for s0 in start]
+    assert np.array_equal(kh[:, 0], np.array(groups)) and not kh[:, 33].any(), (kh[:, 0], groups)
