@@ -349,7 +349,8 @@ __device__ __forceinline__ bool emit_row(const EmitParams& p, int64_t b, uint8_t
   }
   // key weights: lane j of each 8-lane group reads chunks j, j+8, ... of its output's row,
   // so one load instruction covers 8 rows x 128 contiguous bytes; a wave serves 8 outputs
-  // per pass, 4 passes (outputs 32 w + 8 pass + lane / 8)
+  // per pass, 4 passes (outputs 32 w + 8 pass + lane / 8), or with ROLE 2 passes over the
+  // workgroup's half (OBASE + 16 w + 8 pass + lane / 8)
   const int lane = t & 63, wv = t >> 6;
   const int j8 = lane & (kLanesPerOut - 1);
   // key output of pass ps of this lane (8 lanes per output)
