@@ -65,7 +65,7 @@ DECODE = {
     2: dict(batch=32, ctx=32768, groups=8192, index_format="fp8", coarse_ratio=0, coarse_groups=0, nsplit=4, seed=1,
             text="config2: decode B=32 ctx=32768, 128 heads x (512+64) FP8-b128 latent cache, FP8 indexer 64x128 "
                  "over 8192 groups (ratio 4), top-2048, window 128, sink"),
-    4: dict(batch=8, ctx=131072, groups=32768, index_format="mxfp4", coarse_ratio=0, coarse_groups=0, nsplit=12,
+    4: dict(batch=8, ctx=131072, groups=32768, index_format="mxfp4", coarse_ratio=0, coarse_groups=0, nsplit=14,
             seed=2, text="config4: decode B=8 ctx=131072, 128 heads x (512+64) FP8-b128 latent cache, MXFP4 indexer "
                          "64x128 over 32768 groups (ratio 4), top-2048, window 128, sink"),
     5: dict(batch=4, ctx=524288, groups=131072, index_format="mxfp4", coarse_ratio=128, coarse_groups=4096, nsplit=32,

@@ -30,7 +30,7 @@ pytestmark = pytest.mark.gpu
 DECODE = {
     # name: (batch, position, groups, index format, coarse ratio, coarse groups, nsplit)
     "config2": (32, 32767, 8192, "fp8", 0, 0, 4),
-    "config4": (8, 131071, 32768, "mxfp4", 0, 0, 16),
+    "config4": (8, 131071, 32768, "mxfp4", 0, 0, 14),
     "config5": (4, 524287, 131072, "mxfp4", 128, 4096, 32),
 }
 
